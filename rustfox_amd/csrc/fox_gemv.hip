@@ -1,0 +1,914 @@
+// fox_gemv.hip -- activation quantisation and the quantised GEMVs on gfx950.
+//
+// Exactness contract (RustFox src/gemv.c, src/ternary.c, src/kernels.c):
+//   * int8 activations are bit-identical to fox_quantize_activations_i8
+//     (gemv.c:11-42) / quantize_activations_k (kernels.c:722-754): this file
+//     is built with -ffp-contract=off, 127/amax and amax/127 are correctly
+//     rounded (computed in double, which rounds innocuously for a float
+//     quotient), v +/- 0.5f is rounded once and truncated;
+//   * per-block integer sums are exact (integer MFMA);
+//   * every output row combines its per-block terms in block order into a
+//     float accumulator starting at 0.0f with one rounding per operation, as
+//     the reference's row loop does (ternary.c:370-390, kernels.c:571-661),
+//     so outputs equal the reference built without FMA contraction.
+//
+// Work split: one workgroup (4 waves) per 16-row tile and segment; waves take
+// 256-element blocks round-robin; each block is one 16 x 256 slab reduced by
+// four v_mfma_i32_16x16x64_i8, the token dimension (M <= 8) riding in the
+// MFMA's 16 columns.  Per-block float terms go to LDS and 16*M lanes add them
+// in block order.
+//
+// TQ1_0 decode.  With F_l = floor(b * 3^l / 256), the reference's trit
+// t_l = ((uint8)(b*3^l) * 3) >> 8 equals F_{l+1} - 3 F_l, so for a byte with
+// L levels and activations a_0..a_{L-1}:
+//     sum_l t_l a_l = sum_{l=1..L} F_l a_{l-1} - 3 sum_{l=1..L-1} F_l a_l.
+// F_l is the high byte of the 16-bit product b * 3^l (no wrap for l <= 5),
+// so two packed u16 multiplies and one byte permute give four F_l bytes; the
+// MFMA takes F_l as the A operand and (a_{l-1}, a_l) as two B columns.
+// F_5 (<= 242) enters as F_5 - 128 (sign bit flipped) and 128 * sum(a_4) is
+// added back; the -1 of every trit is the block sum of activations.
+#include "fox_internal.h"
+
+#include <cstring>
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
+
+#define WAVES 4
+#define WG (WAVES * 64)
+#define MAX_SEGS 4
+
+enum { FMT_TQ1 = 0, FMT_TQ2 = 1, FMT_Q4K = 2, FMT_Q6K = 3 };
+
+static int fmt_of(int type)
+{
+    switch (type) {
+    case FOX_GPU_TQ1_0: return FMT_TQ1;
+    case FOX_GPU_TQ2_0: return FMT_TQ2;
+    case FOX_GPU_Q4_K: return FMT_Q4K;
+    case FOX_GPU_Q6_K: return FMT_Q6K;
+    default: return -1;
+    }
+}
+
+// float terms per block and row in the ordered combine
+__host__ __device__ constexpr int terms_per_block(int fmt)
+{
+    return fmt == FMT_Q4K ? 8 : fmt == FMT_Q6K ? 4 : 1;
+}
+
+// B-operand bytes per block and token, aux int32 per block and token
+__host__ __device__ constexpr int b_bytes_per_block_tok(int fmt)
+{
+    return (fmt == FMT_TQ1 || fmt == FMT_Q4K) ? 512 : 256;
+}
+
+__host__ __device__ constexpr int aux_per_block_tok(int fmt)
+{
+    return fmt == FMT_Q4K ? 8 : fmt == FMT_Q6K ? 16 : 1;
+}
+
+__device__ __forceinline__ float half_bits_to_float(unsigned h)
+{
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)h);
+}
+
+// ---------------------------------------------------------------- reduce
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float w = __shfl_xor(v, o);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+__device__ __forceinline__ int wave_sum_i(int v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// ---------------------------------------------------- activation prep
+
+// src/gemv.c:31-38 and src/kernels.c:744-751 for one element
+__device__ __forceinline__ int8_t quant_one(float x, float inv)
+{
+    float v = x * inv;
+    float t = v < 0.0f ? v - 0.5f : v + 0.5f;
+    int r = (int)t;
+    r = r > 127 ? 127 : r;
+    r = r < -127 ? -127 : r;
+    return (int8_t)r;
+}
+
+// Element index (within a 256-block) behind byte p of slot s of lane group g,
+// B column c (0: a_{l-1}, 1: a_l); -1 for a zero byte.  Must mirror the A
+// slots built in gemv_blocks<FMT_TQ1>.
+__device__ __forceinline__ int tq1_elem(int s, int g, int p, int c)
+{
+    if (s < 15) {
+        int sec = s / 5, l = s % 5 + 1;
+        if (c == 1 && l == 5) return -1;
+        int lev = c == 0 ? l - 1 : l;
+        if (sec < 2) return lev * 32 + 8 * g + 4 * sec + p;
+        return 160 + lev * 16 + 4 * g + p;
+    }
+    int l = p + 1;
+    if (c == 1 && l == 4) return -1;
+    int lev = c == 0 ? l - 1 : l;
+    return 240 + lev * 4 + g;
+}
+
+// One workgroup per token: quantise (or copy a given q), then lay the int8
+// values out as the MFMA B operand of format FMT plus per-block integer sums.
+template <int FMT>
+__global__ __launch_bounds__(512) void act_prep(const float *__restrict__ x, int x_stride,
+                                               int K, int M, const int8_t *__restrict__ q_in,
+                                               const float *__restrict__ scale_in,
+                                               int8_t *__restrict__ q_out,
+                                               float *__restrict__ scale_out,
+                                               uint8_t *__restrict__ B,
+                                               int32_t *__restrict__ aux)
+{
+    extern __shared__ int8_t qbuf[];
+    __shared__ float red[16];
+    const int t = blockIdx.x, tid = threadIdx.x, nthr = blockDim.x;
+    const int lane = tid & 63, wave = tid >> 6, nwaves = nthr >> 6;
+    const int nb = K >> 8;
+    const bool per_block = (FMT == FMT_Q4K || FMT == FMT_Q6K);
+
+    if (q_in) {
+        for (int i = tid; i < K; i += nthr) qbuf[i] = q_in[(size_t)t * K + i];
+        if (scale_in && per_block) {
+            for (int b = tid; b < nb; b += nthr) scale_out[(size_t)t * nb + b] = scale_in[(size_t)t * nb + b];
+        } else if (scale_in && tid == 0) {
+            scale_out[t] = scale_in[t];
+        }
+    } else if (!per_block) {
+        const float *xt = x + (size_t)t * x_stride;
+        float m = 0.0f;
+        for (int i = tid; i < K; i += nthr) {
+            float a = fabsf(xt[i]);
+            if (a > m) m = a;
+        }
+        m = wave_max(m);
+        if (lane == 0) red[wave] = m;
+        __syncthreads();
+        if (tid == 0) {
+            float a = 0.0f;
+            for (int w = 0; w < nwaves; w++) if (red[w] > a) a = red[w];
+            red[15] = a;
+        }
+        __syncthreads();
+        float amax = red[15];
+        if (!(amax > 0.0f)) {
+            for (int i = tid; i < K; i += nthr) qbuf[i] = 0;
+            if (tid == 0) scale_out[t] = 0.0f;
+        } else {
+            float inv = (float)(127.0 / (double)amax);
+            for (int i = tid; i < K; i += nthr) qbuf[i] = quant_one(xt[i], inv);
+            if (tid == 0) scale_out[t] = (float)((double)amax / 127.0);
+        }
+    } else {
+        const float *xt = x + (size_t)t * x_stride;
+        for (int b = wave; b < nb; b += nwaves) {
+            float v[4], m = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                v[e] = xt[b * 256 + e * 64 + lane];
+                float a = fabsf(v[e]);
+                if (a > m) m = a;
+            }
+            m = wave_max(m);
+            if (!(m > 0.0f)) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) qbuf[b * 256 + e * 64 + lane] = 0;
+                if (lane == 0) scale_out[(size_t)t * nb + b] = 0.0f;
+            } else {
+                float inv = (float)(127.0 / (double)m);
+#pragma unroll
+                for (int e = 0; e < 4; e++) qbuf[b * 256 + e * 64 + lane] = quant_one(v[e], inv);
+                if (lane == 0) scale_out[(size_t)t * nb + b] = (float)((double)m / 127.0);
+            }
+        }
+    }
+    __syncthreads();
+    if (q_out && !q_in)
+        for (int i = tid; i < K; i += nthr) q_out[(size_t)t * K + i] = qbuf[i];
+
+    // ---- B operand
+    if (FMT == FMT_TQ1) {
+        const int items = nb * 32;  // (b, u, g, c)
+        for (int it = tid; it < items; it += nthr) {
+            int c = it & 1, g = (it >> 1) & 3, u = (it >> 3) & 3, b = it >> 5;
+            uint32_t w4[4];
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                uint32_t d = 0;
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    int e = tq1_elem(4 * u + w, g, p, c);
+                    uint32_t byte = e >= 0 ? (uint8_t)qbuf[b * 256 + e] : 0u;
+                    d |= byte << (8 * p);
+                }
+                w4[w] = d;
+            }
+            size_t off = ((((size_t)b * 4 + u) * 4 + g) * (2 * M) + 2 * t + c) * 16;
+            *(uint4 *)(B + off) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
+        // corr = 128 * sum(level-4 activations of qs bytes) - sum(block)
+        for (int b = wave; b < nb; b += nwaves) {
+            const int8_t *qb = qbuf + b * 256;
+            int a = qb[lane] + qb[lane + 64] + qb[lane + 128] + qb[lane + 192];
+            int i4 = lane < 32 ? 128 + lane : lane < 48 ? 224 + (lane - 32) : -1;
+            int a4 = i4 >= 0 ? qb[i4] : 0;
+            a = wave_sum_i(a);
+            a4 = wave_sum_i(a4);
+            if (lane == 0) aux[(size_t)b * M + t] = 128 * a4 - a;
+        }
+    } else if (FMT == FMT_TQ2) {
+        const int items = nb * 16;  // (b, u, g)
+        for (int it = tid; it < items; it += nthr) {
+            int g = it & 3, u = (it >> 2) & 3, b = it >> 4;
+            uint32_t w4[4];
+#pragma unroll
+            for (int l = 0; l < 4; l++) {
+                uint32_t d = 0;
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    int m = 16 * g + 4 * u + p;
+                    int e = (m >> 5) * 128 + l * 32 + (m & 31);
+                    d |= (uint32_t)(uint8_t)qbuf[b * 256 + e] << (8 * p);
+                }
+                w4[l] = d;
+            }
+            size_t off = ((((size_t)b * 4 + u) * 4 + g) * M + t) * 16;
+            *(uint4 *)(B + off) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
+        for (int b = wave; b < nb; b += nwaves) {
+            const int8_t *qb = qbuf + b * 256;
+            int a = wave_sum_i(qb[lane] + qb[lane + 64] + qb[lane + 128] + qb[lane + 192]);
+            if (lane == 0) aux[(size_t)b * M + t] = -a;
+        }
+    } else if (FMT == FMT_Q4K) {
+        const int items = nb * 32;  // (b, p, g, c)
+        for (int it = tid; it < items; it += nthr) {
+            int c = it & 1, g = (it >> 1) & 3, p = (it >> 3) & 3, b = it >> 5;
+            const int8_t *src = qbuf + b * 256 + 64 * p + 32 * c + 8 * g;
+            uint32_t lo0 = 0, lo1 = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                lo0 |= (uint32_t)(uint8_t)src[e] << (8 * e);
+                lo1 |= (uint32_t)(uint8_t)src[4 + e] << (8 * e);
+            }
+            uint4 v = c == 0 ? make_uint4(lo0, lo1, 0u, 0u) : make_uint4(0u, 0u, lo0, lo1);
+            size_t off = ((((size_t)b * 4 + p) * 4 + g) * (2 * M) + 2 * t + c) * 16;
+            *(uint4 *)(B + off) = v;
+        }
+        for (int it = wave; it < nb * 8; it += nwaves) {
+            int b = it >> 3, j = it & 7;
+            int a = lane < 32 ? qbuf[b * 256 + 32 * j + lane] : 0;
+            a = wave_sum_i(a);
+            if (lane == 0) aux[((size_t)b * 8 + j) * M + t] = a;
+        }
+    } else {  // FMT_Q6K: diagonal blocks only
+        const int items = nb * 16;  // (b, v, g)
+        for (int it = tid; it < items; it += nthr) {
+            int g = it & 3, v = (it >> 2) & 3, b = it >> 4;
+            int h = v >> 1, s = v & 1;
+            const int8_t *src = qbuf + b * 256 + 128 * h + 32 * g + 16 * s;
+            uint32_t w4[4];
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                uint32_t d = 0;
+#pragma unroll
+                for (int p = 0; p < 4; p++) d |= (uint32_t)(uint8_t)src[4 * w + p] << (8 * p);
+                w4[w] = d;
+            }
+            size_t off = ((((size_t)b * 4 + v) * 4 + g) * M + t) * 16;
+            *(uint4 *)(B + off) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
+        for (int it = wave; it < nb * 16; it += nwaves) {
+            int b = it >> 4, v = (it >> 2) & 3, g = it & 3;
+            int h = v >> 1, s = v & 1;
+            int a = lane < 16 ? qbuf[b * 256 + 128 * h + 32 * g + 16 * s + lane] : 0;
+            a = wave_sum_i(a);
+            if (lane == 0) aux[((((size_t)b * 4 + v) * 4) + g) * M + t] = a;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ GEMV
+
+struct Segs {
+    const uint8_t *w[MAX_SEGS];
+    float *out[MAX_SEGS];
+    int out_stride[MAX_SEGS];
+    int n_rows[MAX_SEGS];
+    int tile_start[MAX_SEGS + 1];
+    int n;
+};
+
+// four F_l bytes of the bytes of dword d at level l (multiplier m = 3^l)
+__device__ __forceinline__ uint32_t tq1_level(uint32_t e, uint32_t o, unsigned short m)
+{
+    v2u16 mm = {m, m};
+    uint32_t ye = __builtin_bit_cast(uint32_t, (v2u16)(__builtin_bit_cast(v2u16, e) * mm));
+    uint32_t yo = __builtin_bit_cast(uint32_t, (v2u16)(__builtin_bit_cast(v2u16, o) * mm));
+    return __builtin_amdgcn_perm(yo, ye, 0x07030501u);
+}
+
+__device__ __forceinline__ void tq1_slots(uint32_t d, uint32_t *a)
+{
+    uint32_t e = __builtin_amdgcn_perm(0u, d, 0x0c020c00u);  // b0, b2 as u16
+    uint32_t o = __builtin_amdgcn_perm(0u, d, 0x0c030c01u);  // b1, b3 as u16
+    a[0] = tq1_level(e, o, 3);
+    a[1] = tq1_level(e, o, 9);
+    a[2] = tq1_level(e, o, 27);
+    a[3] = tq1_level(e, o, 81);
+    a[4] = tq1_level(e, o, 243) ^ 0x80808080u;
+}
+
+__device__ __forceinline__ uint32_t tq1_qh_slot(uint32_t b)
+{
+    uint32_t e = __builtin_amdgcn_perm(0u, b, 0x0c000c00u);  // b, b as u16
+    v2u16 m1 = {3, 9}, m2 = {27, 81};
+    uint32_t ya = __builtin_bit_cast(uint32_t, (v2u16)(__builtin_bit_cast(v2u16, e) * m1));
+    uint32_t yb = __builtin_bit_cast(uint32_t, (v2u16)(__builtin_bit_cast(v2u16, e) * m2));
+    return __builtin_amdgcn_perm(yb, ya, 0x07050301u);  // F1 F2 F3 F4
+}
+
+__device__ __forceinline__ v4i mfma(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3,
+                                    v4i b, v4i c)
+{
+    v4i a = {(int)a0, (int)a1, (int)a2, (int)a3};
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ v4i load_b(const uint8_t *p, bool ok)
+{
+    v4i z = {0, 0, 0, 0};
+    return ok ? *(const v4i *)p : z;
+}
+
+// Process block b of the tile at `ch` (its chunk) for one wave; writes the
+// block's float terms (or integer sums) of rows 4g+r.
+template <int FMT>
+__device__ __forceinline__ void gemv_block(const uint8_t *__restrict__ ch, int b, int nb,
+                                           int M, int lane, const uint8_t *__restrict__ B,
+                                           const int32_t *__restrict__ aux,
+                                           const float *__restrict__ scale,
+                                           float *__restrict__ terms /* [T][16][M] */,
+                                           int32_t *__restrict__ sums, int row0, int n_rows)
+{
+    const int g = lane >> 4, j = lane & 15;
+    const v4i zero = {0, 0, 0, 0};
+
+    if (FMT == FMT_TQ1) {
+        const uint32_t *qs = (const uint32_t *)(ch + 12 * lane);
+        uint32_t d0 = qs[0], d1 = qs[1], d2 = qs[2];
+        uint32_t qh = ch[768 + lane];
+        uint2 dd = *(const uint2 *)(ch + 832 + 8 * g);
+        const bool bok = j < 2 * M;
+        v4i bv[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            bv[u] = load_b(B + ((((size_t)b * 4 + u) * 4 + g) * (2 * M) + j) * 16, bok);
+        uint32_t a[16];
+        tq1_slots(d0, a);
+        tq1_slots(d1, a + 5);
+        tq1_slots(d2, a + 10);
+        a[15] = tq1_qh_slot(qh);
+        v4i acc = zero;
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            acc = mfma(a[4 * u], a[4 * u + 1], a[4 * u + 2], a[4 * u + 3], bv[u], acc);
+        int oth[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) oth[r] = __shfl_xor(acc[r], 1);
+        if (bok && !(j & 1)) {
+            int t = j >> 1;
+            int corr = aux[(size_t)b * M + t];
+            uint32_t hw[2] = {dd.x, dd.y};
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                int S = acc[r] - 3 * oth[r] + corr;
+                int row = 4 * g + r;
+                if (sums) {
+                    if (row0 + row < n_rows) sums[((size_t)t * n_rows + row0 + row) * nb + b] = S;
+                } else {
+                    float d = half_bits_to_float((hw[r >> 1] >> (16 * (r & 1))) & 0xFFFFu);
+                    terms[row * M + t] = d * (float)S;
+                }
+            }
+        }
+    } else if (FMT == FMT_TQ2) {
+        uint4 qs = *(const uint4 *)(ch + 16 * lane);
+        uint2 dd = *(const uint2 *)(ch + 1024 + 8 * g);
+        const bool bok = j < M;
+        uint32_t dw[4] = {qs.x, qs.y, qs.z, qs.w};
+        v4i acc = zero;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            v4i bv = load_b(B + ((((size_t)b * 4 + u) * 4 + g) * M + j) * 16, bok);
+            uint32_t d = dw[u];
+            acc = mfma(d & 0x03030303u, (d >> 2) & 0x03030303u, (d >> 4) & 0x03030303u,
+                       (d >> 6) & 0x03030303u, bv, acc);
+        }
+        if (bok) {
+            int t = j;
+            int corr = aux[(size_t)b * M + t];
+            uint32_t hw[2] = {dd.x, dd.y};
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                int S = acc[r] + corr;
+                int row = 4 * g + r;
+                if (sums) {
+                    if (row0 + row < n_rows) sums[((size_t)t * n_rows + row0 + row) * nb + b] = S;
+                } else {
+                    float d = half_bits_to_float((hw[r >> 1] >> (16 * (r & 1))) & 0xFFFFu);
+                    terms[row * M + t] = d * (float)S;
+                }
+            }
+        }
+    } else if (FMT == FMT_Q4K) {
+        const uint4 *qp = (const uint4 *)(ch + 32 * lane);
+        uint4 q0 = qp[0], q1 = qp[1];
+        uint32_t dw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        const bool bok = j < 2 * M;
+        v4i acc[4];
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            v4i bv = load_b(B + ((((size_t)b * 4 + p) * 4 + g) * (2 * M) + j) * 16, bok);
+            uint32_t a0 = dw[2 * p], a1 = dw[2 * p + 1];
+            acc[p] = mfma(a0 & 0x0F0F0F0Fu, a1 & 0x0F0F0F0Fu, (a0 >> 4) & 0x0F0F0F0Fu,
+                          (a1 >> 4) & 0x0F0F0F0Fu, bv, zero);
+        }
+        if (bok) {
+            const int t = j >> 1, c = j & 1;
+            const float as = sums ? 0.0f : scale[(size_t)t * nb + b];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int row = 4 * g + r;
+                const uint8_t *hd = ch + 2048 + 16 * row;
+                uint4 h4 = *(const uint4 *)hd;
+                uint32_t hb[4] = {h4.x, h4.y, h4.z, h4.w};
+                const uint8_t *sb = (const uint8_t *)hb + 4;  // scales[12]
+                float d = half_bits_to_float(hb[0] & 0xFFFFu);
+                float dmin = half_bits_to_float(hb[0] >> 16);
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    const int sj = 2 * p + c;  // src/kernels.c:246-255
+                    int sc, mn;
+                    if (sj < 4) {
+                        sc = sb[sj] & 63;
+                        mn = sb[sj + 4] & 63;
+                    } else {
+                        sc = (sb[sj + 4] & 0x0F) | ((sb[sj - 4] >> 6) << 4);
+                        mn = (sb[sj + 4] >> 4) | ((sb[sj] >> 6) << 4);
+                    }
+                    int D = acc[p][r];
+                    if (sums) {
+                        if (row0 + row < n_rows)
+                            sums[(((size_t)t * n_rows + row0 + row) * nb + b) * 8 + sj] = D;
+                    } else {
+                        int sq = aux[((size_t)b * 8 + sj) * M + t];
+                        float tv = d * (float)sc * (float)D - dmin * (float)mn * (float)sq;
+                        terms[(sj * 16 + row) * M + t] = as * tv;
+                    }
+                }
+            }
+        }
+    } else {  // FMT_Q6K
+        const int i = lane & 15;
+        const uint8_t *ql = ch + 128 * i;
+        const uint8_t *qh = ch + 2048 + 64 * i;
+        uint32_t a[4][4];
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int h = v >> 1, s = v & 1;
+            uint4 L4 = *(const uint4 *)(ql + 64 * h + 32 * (g & 1) + 16 * s);
+            uint4 H4 = *(const uint4 *)(qh + 32 * h + 16 * s);
+            uint32_t Lw[4] = {L4.x, L4.y, L4.z, L4.w}, Hw[4] = {H4.x, H4.y, H4.z, H4.w};
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                uint32_t nib = (g < 2 ? Lw[w] : Lw[w] >> 4) & 0x0F0F0F0Fu;
+                uint32_t hi = ((Hw[w] >> (2 * g)) & 0x03030303u) << 4;
+                a[v][w] = nib | hi;
+            }
+        }
+        for (int t0 = 0; t0 < M; t0 += 4) {
+            const int c = j & 3, t = t0 + (j >> 2);
+            const bool bok = t < M && c == g;
+            v4i acc[4];
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                v4i bv = load_b(B + ((((size_t)b * 4 + v) * 4 + g) * M + t) * 16, bok);
+                acc[v] = mfma(a[v][0], a[v][1], a[v][2], a[v][3], bv, zero);
+            }
+            const bool tok = t < M;
+            const float as = (!tok || sums) ? 0.0f : scale[(size_t)t * nb + b];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int row = 4 * g + r;
+                uint4 s4 = *(const uint4 *)(ch + 3072 + 16 * row);
+                uint32_t sw[4] = {s4.x, s4.y, s4.z, s4.w};
+                const int8_t *sc = (const int8_t *)sw;
+                float d = half_bits_to_float(*(const unsigned short *)(ch + 3328 + 2 * row));
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int h = v >> 1, s = v & 1;
+                    int part = 0;
+                    if (tok) {
+                        int as16 = aux[((((size_t)b * 4 + v) * 4) + c) * M + t];
+                        part = (int)sc[8 * h + s + 2 * c] * (acc[v][r] - 32 * as16);
+                    }
+                    part += __shfl_xor(part, 1);
+                    part += __shfl_xor(part, 2);
+                    if (tok && c == 0) {
+                        if (sums) {
+                            if (row0 + row < n_rows)
+                                sums[(((size_t)t * n_rows + row0 + row) * nb + b) * 4 + v] = part;
+                        } else {
+                            terms[(v * 16 + row) * M + t] = as * d * (float)part;
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(WG) void gemv_blocks(Segs segs, int nb, int M, int chunk_blocks,
+                                                 const uint8_t *__restrict__ B,
+                                                 const int32_t *__restrict__ aux,
+                                                 const float *__restrict__ scale,
+                                                 unsigned flags, int32_t *__restrict__ sums)
+{
+    extern __shared__ float terms[];  // [chunk_blocks][T][16][M]
+    constexpr int T = terms_per_block(FMT);
+    constexpr int CHUNK = FMT == FMT_TQ1 ? TQ1_CHUNK : FMT == FMT_TQ2 ? TQ2_CHUNK
+                        : FMT == FMT_Q4K ? Q4K_CHUNK : Q6K_CHUNK;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    int s = 0;
+    while (s + 1 < segs.n && (int)blockIdx.x >= segs.tile_start[s + 1]) s++;
+    const int tile = blockIdx.x - segs.tile_start[s];
+    const int n_rows = segs.n_rows[s];
+    const uint8_t *wt = segs.w[s] + (size_t)tile * nb * CHUNK;
+
+    const bool combiner = tid < 16 * M;
+    const int crow = tid & 15, ct = tid >> 4;
+    float acc = 0.0f;
+
+    for (int c0 = 0; c0 < nb; c0 += chunk_blocks) {
+        const int c1 = c0 + chunk_blocks < nb ? c0 + chunk_blocks : nb;
+        for (int b = c0 + wave; b < c1; b += WAVES)
+            gemv_block<FMT>(wt + (size_t)b * CHUNK, b, nb, M, lane, B, aux, scale,
+                            terms + (size_t)(b - c0) * T * 16 * M, sums, tile * 16, n_rows);
+        if (sums) continue;
+        __syncthreads();
+        if (combiner) {
+            for (int b = c0; b < c1; b++) {
+                const float *tb = terms + (size_t)(b - c0) * T * 16 * M;
+#pragma unroll
+                for (int k = 0; k < T; k++) acc = acc + tb[(k * 16 + crow) * M + ct];
+            }
+        }
+        __syncthreads();
+    }
+    if (sums || !combiner) return;
+    const int row = tile * 16 + crow;
+    if (row >= n_rows) return;
+    float y = (FMT == FMT_TQ1 || FMT == FMT_TQ2) ? acc * scale[ct] : acc;  // src/gemv.c:70
+    float *o = segs.out[s] + (size_t)ct * segs.out_stride[s] + row;
+    *o = (flags & FOX_GPU_GEMV_ACCUMULATE) ? *o + y : y;
+}
+
+// -------------------------------------------------------- float weights
+
+// F16 / F32 rows (src/kernels.c:81-96): each lane owns one row and adds
+// w[k] * x[k] sequentially in k, exactly the reference's order; weights are
+// staged through LDS with coalesced loads.
+template <typename WT>
+__global__ __launch_bounds__(256) void gemv_float(const WT *__restrict__ W, int K, int N,
+                                                 const float *__restrict__ x, int x_stride,
+                                                 int M, float *__restrict__ out,
+                                                 int out_stride, unsigned flags)
+{
+    constexpr int FCH = 128 / sizeof(WT);        // elements per 128-byte chunk
+    constexpr int EPD = 4 / sizeof(WT);          // elements per dword
+    constexpr int RSTR = FCH / EPD + 1;          // padded row stride in dwords
+    __shared__ uint32_t wl[256 * RSTR];
+    __shared__ float xs[FOX_GPU_MAX_TOKENS * 64];
+    const int tid = threadIdx.x;
+    const int r0 = blockIdx.x * 256;
+    const bool vec = (K % (16 / (int)sizeof(WT))) == 0;
+    float acc[FOX_GPU_MAX_TOKENS];
+#pragma unroll
+    for (int t = 0; t < FOX_GPU_MAX_TOKENS; t++) acc[t] = 0.0f;
+
+    for (int k0 = 0; k0 < K; k0 += FCH) {
+        const int kn = K - k0 < FCH ? K - k0 : FCH;
+        // 256 rows x FCH elements; 16-byte pieces of FCH*sizeof(WT)/16 per row
+        constexpr int PPR = FCH * sizeof(WT) / 16;
+        constexpr int EPP = 16 / sizeof(WT);
+        for (int pc = tid; pc < 256 * PPR; pc += 256) {
+            const int r = pc / PPR, part = pc % PPR;
+            const int row = r0 + r, kk = part * EPP;
+            uint32_t v[4] = {0u, 0u, 0u, 0u};
+            if (row < N && kk < kn) {
+                const WT *src = W + (size_t)row * K + k0 + kk;
+                if (vec && kk + EPP <= kn) {
+                    uint4 u = *(const uint4 *)src;
+                    v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+                } else {
+                    WT tmp[EPP];
+                    for (int e = 0; e < EPP; e++) tmp[e] = kk + e < kn ? src[e] : (WT)0;
+                    memcpy(v, tmp, 16);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) wl[r * RSTR + part * 4 + e] = v[e];
+        }
+        for (int i = tid; i < M * FCH; i += 256) {
+            const int t = i / FCH, kk = i % FCH;
+            xs[i] = kk < kn ? x[(size_t)t * x_stride + k0 + kk] : 0.0f;
+        }
+        __syncthreads();
+        const uint32_t *myw = wl + tid * RSTR;
+        for (int kk = 0; kk < kn; kk++) {
+            const uint32_t dword = myw[kk / EPD];
+            float w;
+            if (sizeof(WT) == 2)
+                w = half_bits_to_float((dword >> (16 * (kk % EPD))) & 0xFFFFu);
+            else
+                w = __builtin_bit_cast(float, dword);
+#pragma unroll
+            for (int t = 0; t < FOX_GPU_MAX_TOKENS; t++)
+                if (t < M) acc[t] = acc[t] + w * xs[t * FCH + kk];
+        }
+        __syncthreads();
+    }
+    const int row = r0 + tid;
+    if (row >= N) return;
+    for (int t = 0; t < M; t++) {
+        float *o = out + (size_t)t * out_stride + row;
+        *o = (flags & FOX_GPU_GEMV_ACCUMULATE) ? *o + acc[t] : acc[t];
+    }
+}
+
+// ----------------------------------------------------------------- host
+
+static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+struct Ws {
+    int8_t *q;
+    float *scale;
+    uint8_t *B;
+    int32_t *aux;
+};
+
+static fox_gpu_status carve(fox_gpu_ctx *ctx, int fmt, size_t K, size_t M, Ws *w)
+{
+    const size_t nb = K / 256;
+    size_t off = 0, oq, os, ob, oa;
+    oq = off; off = align_up(off + M * K, 256);
+    os = off; off = align_up(off + M * nb * 4, 256);
+    ob = off; off = align_up(off + nb * M * (size_t)b_bytes_per_block_tok(fmt), 256);
+    oa = off; off = align_up(off + nb * M * (size_t)aux_per_block_tok(fmt) * 4, 256);
+    fox_gpu_status st = fox_ws_reserve(ctx, off);
+    if (st) return st;
+    w->q = (int8_t *)(ctx->ws + oq);
+    w->scale = (float *)(ctx->ws + os);
+    w->B = ctx->ws + ob;
+    w->aux = (int32_t *)(ctx->ws + oa);
+    return FOX_GPU_OK;
+}
+
+static fox_gpu_status launch_prep(fox_gpu_ctx *ctx, int fmt, const float *x, size_t x_stride,
+                                  const int8_t *q_in, const float *scale_in, size_t K,
+                                  size_t M, const Ws &w, int8_t *q_out, float *scale_out)
+{
+    dim3 grid((unsigned)M), block(512);
+    size_t lds = align_up(K, 16);
+    if (lds > 65536 - 256)
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "gemv: K = %zu exceeds the 65536 "
+                        "activation values one workgroup stages", K);
+    switch (fmt) {
+    case FMT_TQ1:
+        hipLaunchKernelGGL(act_prep<FMT_TQ1>, grid, block, lds, ctx->stream, x, (int)x_stride,
+                           (int)K, (int)M, q_in, scale_in, q_out, scale_out, w.B, w.aux);
+        break;
+    case FMT_TQ2:
+        hipLaunchKernelGGL(act_prep<FMT_TQ2>, grid, block, lds, ctx->stream, x, (int)x_stride,
+                           (int)K, (int)M, q_in, scale_in, q_out, scale_out, w.B, w.aux);
+        break;
+    case FMT_Q4K:
+        hipLaunchKernelGGL(act_prep<FMT_Q4K>, grid, block, lds, ctx->stream, x, (int)x_stride,
+                           (int)K, (int)M, q_in, scale_in, q_out, scale_out, w.B, w.aux);
+        break;
+    default:
+        hipLaunchKernelGGL(act_prep<FMT_Q6K>, grid, block, lds, ctx->stream, x, (int)x_stride,
+                           (int)K, (int)M, q_in, scale_in, q_out, scale_out, w.B, w.aux);
+        break;
+    }
+    FOX_LAUNCHED("act_prep");
+    return FOX_GPU_OK;
+}
+
+static fox_gpu_status check_common(size_t n, const fox_gpu_tensor *const *ws, size_t M,
+                                   int *type, size_t *K)
+{
+    if (!ws || n == 0 || n > MAX_SEGS)
+        return fox_fail(FOX_GPU_ERR_ARG, "gemv: 1 to %d matrices per call", MAX_SEGS);
+    if (M == 0 || M > FOX_GPU_MAX_TOKENS)
+        return fox_fail(FOX_GPU_ERR_ARG, "gemv: %zu tokens; 1 to %d per call", M,
+                        FOX_GPU_MAX_TOKENS);
+    for (size_t i = 0; i < n; i++) {
+        if (!ws[i]) return fox_fail(FOX_GPU_ERR_ARG, "gemv: null tensor");
+        if (i && (ws[i]->type != ws[0]->type || ws[i]->ne0 != ws[0]->ne0))
+            return fox_fail(FOX_GPU_ERR_ARG,
+                            "gemv: matrices of one call must share type and width");
+    }
+    *type = ws[0]->type;
+    *K = (size_t)ws[0]->ne0;
+    if (*K > (1u << 20) || ws[0]->ne1 > (1u << 30))
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "gemv: matrix too large");
+    return FOX_GPU_OK;
+}
+
+fox_gpu_status fox_gemv_launch(fox_gpu_ctx *ctx, size_t n, const fox_gpu_tensor *const *ws,
+                               const float *x, size_t x_stride, const int8_t *q,
+                               const float *scale, size_t M, float *const *outs,
+                               const size_t *out_strides, unsigned flags, int32_t *sums)
+{
+    int type;
+    size_t K;
+    fox_gpu_status st;
+
+    if (!ctx) return fox_fail(FOX_GPU_ERR_ARG, "gemv: null context");
+    if ((st = check_common(n, ws, M, &type, &K))) return st;
+    if (!x && !q) return fox_fail(FOX_GPU_ERR_ARG, "gemv: null activations");
+    if (!sums) {
+        if (!outs || !out_strides) return fox_fail(FOX_GPU_ERR_ARG, "gemv: null output");
+        for (size_t i = 0; i < n; i++) {
+            if (!outs[i]) return fox_fail(FOX_GPU_ERR_ARG, "gemv: null output");
+            if (M > 1 && out_strides[i] < ws[i]->ne1)
+                return fox_fail(FOX_GPU_ERR_ARG, "gemv: output stride %zu < %llu rows",
+                                out_strides[i], (unsigned long long)ws[i]->ne1);
+        }
+    }
+    if (x && M > 1 && x_stride < K)
+        return fox_fail(FOX_GPU_ERR_ARG, "gemv: input stride %zu < K = %zu", x_stride, K);
+
+    if (type == FOX_GPU_F16 || type == FOX_GPU_F32) {
+        if (!x || sums)
+            return fox_fail(FOX_GPU_ERR_UNSUPPORTED,
+                            "gemv: %s weights take float activations", fox_type_name(type));
+        for (size_t i = 0; i < n; i++) {
+            const int N = (int)ws[i]->ne1;
+            dim3 grid((unsigned)((N + 255) / 256)), block(256);
+            if (type == FOX_GPU_F16)
+                hipLaunchKernelGGL(gemv_float<_Float16>, grid, block, 0, ctx->stream,
+                                   (const _Float16 *)ws[i]->d, (int)K, N, x, (int)x_stride,
+                                   (int)M, outs[i], (int)out_strides[i], flags);
+            else
+                hipLaunchKernelGGL(gemv_float<float>, grid, block, 0, ctx->stream,
+                                   (const float *)ws[i]->d, (int)K, N, x, (int)x_stride,
+                                   (int)M, outs[i], (int)out_strides[i], flags);
+            FOX_LAUNCHED("gemv_float");
+        }
+        return FOX_GPU_OK;
+    }
+
+    const int fmt = fmt_of(type);
+    if (fmt < 0)
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "gemv: no kernel for %s", fox_type_name(type));
+    if (K % 256)
+        return fox_fail(FOX_GPU_ERR_ARG,
+                        "gemv: %zu columns is not a multiple of the 256-element block", K);
+    Ws w;
+    if ((st = carve(ctx, fmt, K, M, &w))) return st;
+    if ((st = launch_prep(ctx, fmt, x, x_stride, q, scale, K, M, w, w.q, w.scale))) return st;
+
+    Segs sg;
+    memset(&sg, 0, sizeof(sg));
+    sg.n = (int)n;
+    int tiles = 0;
+    for (size_t i = 0; i < n; i++) {
+        sg.w[i] = ws[i]->d;
+        sg.out[i] = outs ? outs[i] : nullptr;
+        sg.out_stride[i] = out_strides ? (int)out_strides[i] : 0;
+        sg.n_rows[i] = (int)ws[i]->ne1;
+        sg.tile_start[i] = tiles;
+        tiles += (int)ws[i]->n_tiles;
+    }
+    sg.tile_start[n] = tiles;
+
+    const int nb = (int)(K / 256);
+    const int T = terms_per_block(fmt);
+    int chunk_blocks = (int)(65536 / ((size_t)T * 16 * M * 4));
+    chunk_blocks = chunk_blocks / WAVES * WAVES;
+    if (chunk_blocks < WAVES) chunk_blocks = WAVES;
+    if (chunk_blocks > nb) chunk_blocks = nb;
+    size_t lds = sums ? 0 : (size_t)chunk_blocks * T * 16 * M * 4;
+    dim3 grid((unsigned)tiles), block(WG);
+    switch (fmt) {
+    case FMT_TQ1:
+        hipLaunchKernelGGL(gemv_blocks<FMT_TQ1>, grid, block, lds, ctx->stream, sg, nb, (int)M,
+                           chunk_blocks, w.B, w.aux, w.scale, flags, sums);
+        break;
+    case FMT_TQ2:
+        hipLaunchKernelGGL(gemv_blocks<FMT_TQ2>, grid, block, lds, ctx->stream, sg, nb, (int)M,
+                           chunk_blocks, w.B, w.aux, w.scale, flags, sums);
+        break;
+    case FMT_Q4K:
+        hipLaunchKernelGGL(gemv_blocks<FMT_Q4K>, grid, block, lds, ctx->stream, sg, nb, (int)M,
+                           chunk_blocks, w.B, w.aux, w.scale, flags, sums);
+        break;
+    default:
+        hipLaunchKernelGGL(gemv_blocks<FMT_Q6K>, grid, block, lds, ctx->stream, sg, nb, (int)M,
+                           chunk_blocks, w.B, w.aux, w.scale, flags, sums);
+        break;
+    }
+    FOX_LAUNCHED("gemv_blocks");
+    return FOX_GPU_OK;
+}
+
+// ----------------------------------------------------------- C entries
+
+extern "C" fox_gpu_status fox_gpu_quantize(fox_gpu_ctx *ctx, int mode, const float *x, size_t K,
+                                           size_t M, size_t x_stride, int8_t *q, float *scale)
+{
+    if (!ctx || !x || !q || !scale || K == 0 || M == 0)
+        return fox_fail(FOX_GPU_ERR_ARG, "quantize: bad argument");
+    if (M > FOX_GPU_MAX_TOKENS)
+        return fox_fail(FOX_GPU_ERR_ARG, "quantize: %zu rows; at most %d", M, FOX_GPU_MAX_TOKENS);
+    if (M > 1 && x_stride < K) return fox_fail(FOX_GPU_ERR_ARG, "quantize: stride < K");
+    if (mode != FOX_GPU_ACT_PER_VECTOR && mode != FOX_GPU_ACT_PER_BLOCK)
+        return fox_fail(FOX_GPU_ERR_ARG, "quantize: unknown mode %d", mode);
+    if (mode == FOX_GPU_ACT_PER_BLOCK && K % 256)
+        return fox_fail(FOX_GPU_ERR_ARG, "quantize: %zu values is not a whole number of "
+                        "256-element blocks", K);
+    const int fmt = mode == FOX_GPU_ACT_PER_BLOCK ? FMT_Q4K : FMT_TQ1;
+    Ws w;
+    fox_gpu_status st;
+    // the B operand is laid out for whole blocks only; a ragged tail is
+    // quantised with the rest but has no block to go into
+    size_t Kb = K / 256 * 256;
+    if ((st = carve(ctx, fmt, Kb ? Kb : 256, M, &w))) return st;
+    return launch_prep(ctx, fmt, x, M > 1 ? x_stride : K, nullptr, nullptr, K, M, w, q, scale);
+}
+
+extern "C" fox_gpu_status fox_gpu_gemv(fox_gpu_ctx *ctx, const fox_gpu_tensor *w, const float *x,
+                                       size_t x_stride, size_t M, float *out, size_t out_stride,
+                                       unsigned flags)
+{
+    if (!x || !out) return fox_fail(FOX_GPU_ERR_ARG, "gemv: null pointer");
+    const fox_gpu_tensor *ws[1] = {w};
+    float *outs[1] = {out};
+    size_t strides[1] = {M > 1 ? out_stride : (w ? (size_t)w->ne1 : 0)};
+    return fox_gemv_launch(ctx, 1, ws, x, M > 1 ? x_stride : (w ? (size_t)w->ne0 : 0), nullptr,
+                           nullptr, M, outs, strides, flags, nullptr);
+}
+
+extern "C" fox_gpu_status fox_gpu_gemv_multi(fox_gpu_ctx *ctx, size_t n,
+                                             const fox_gpu_tensor *const *ws, const float *x,
+                                             size_t x_stride, size_t M, float *const *outs,
+                                             const size_t *out_strides, unsigned flags)
+{
+    if (!x || !outs || !out_strides) return fox_fail(FOX_GPU_ERR_ARG, "gemv_multi: null pointer");
+    return fox_gemv_launch(ctx, n, ws, x, x_stride, nullptr, nullptr, M, outs, out_strides,
+                           flags, nullptr);
+}
+
+extern "C" fox_gpu_status fox_gpu_gemv_i8(fox_gpu_ctx *ctx, const fox_gpu_tensor *w,
+                                          const int8_t *q, const float *scale, size_t M,
+                                          float *out, size_t out_stride)
+{
+    if (!q || !scale || !out) return fox_fail(FOX_GPU_ERR_ARG, "gemv_i8: null pointer");
+    if (w && !fox_is_block_type(w->type))
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "gemv_i8: %s weights have no int8 path",
+                        fox_type_name(w->type));
+    const fox_gpu_tensor *ws[1] = {w};
+    float *outs[1] = {out};
+    size_t strides[1] = {M > 1 ? out_stride : (w ? (size_t)w->ne1 : 0)};
+    return fox_gemv_launch(ctx, 1, ws, nullptr, 0, q, scale, M, outs, strides, 0, nullptr);
+}
+
+extern "C" fox_gpu_status fox_gpu_block_sums(fox_gpu_ctx *ctx, const fox_gpu_tensor *w,
+                                             const int8_t *q, size_t M, int32_t *sums)
+{
+    if (!q || !sums) return fox_fail(FOX_GPU_ERR_ARG, "block_sums: null pointer");
+    if (w && !fox_is_block_type(w->type))
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "block_sums: %s has no integer blocks",
+                        fox_type_name(w->type));
+    const fox_gpu_tensor *ws[1] = {w};
+    return fox_gemv_launch(ctx, 1, ws, nullptr, 0, q, nullptr, M, nullptr, nullptr, 0, sums);
+}

@@ -1,0 +1,492 @@
+// fox_gpu.hip -- context, errors, memory, weight upload/repack, graphs, events.
+#include "fox_internal.h"
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+
+// ------------------------------------------------------------------ errors
+
+static thread_local char g_err[512];
+
+fox_gpu_status fox_fail(fox_gpu_status st, const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return st;
+}
+
+fox_gpu_status fox_hip_fail(hipError_t e, const char *what)
+{
+    return fox_fail(e == hipErrorOutOfMemory ? FOX_GPU_ERR_NOMEM : FOX_GPU_ERR_INTERNAL,
+                    "hip: %s failed: %s", what, hipGetErrorString(e));
+}
+
+extern "C" const char *fox_gpu_last_error(void) { return g_err; }
+
+extern "C" const char *fox_gpu_status_str(fox_gpu_status s)
+{
+    switch (s) {
+    case FOX_GPU_OK: return "ok";
+    case FOX_GPU_ERR_ARG: return "invalid argument";
+    case FOX_GPU_ERR_IO: return "i/o error";
+    case FOX_GPU_ERR_NOMEM: return "out of memory";
+    case FOX_GPU_ERR_FORMAT: return "bad format";
+    case FOX_GPU_ERR_UNSUPPORTED: return "unsupported";
+    case FOX_GPU_ERR_NOTFOUND: return "not found";
+    case FOX_GPU_ERR_INTERNAL: return "internal error";
+    }
+    return "unknown status";
+}
+
+// ---------------------------------------------------------------- context
+
+static fox_gpu_status set_device(fox_gpu_ctx *ctx)
+{
+    FOX_HIP(hipSetDevice(ctx->device));
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_init(int device, fox_gpu_ctx **out)
+{
+    int count = 0;
+    hipDeviceProp_t prop;
+    fox_gpu_ctx *ctx;
+
+    if (!out) return fox_fail(FOX_GPU_ERR_ARG, "init: null output");
+    *out = nullptr;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0)
+        return fox_fail(FOX_GPU_ERR_NOTFOUND, "init: no HIP device is visible");
+    if (device < 0 || device >= count)
+        return fox_fail(FOX_GPU_ERR_ARG, "init: device %d of %d", device, count);
+    FOX_HIP(hipSetDevice(device));
+    FOX_HIP(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED,
+                        "init: device %d is %s; this library is built for gfx950 (MI355X)",
+                        device, prop.gcnArchName);
+    ctx = new (std::nothrow) fox_gpu_ctx();
+    if (!ctx) return fox_fail(FOX_GPU_ERR_NOMEM, "init: context");
+    ctx->device = device;
+    ctx->n_cu = prop.multiProcessorCount;
+    ctx->hbm_bytes = prop.totalGlobalMem;
+    snprintf(ctx->name, sizeof(ctx->name), "%s (%s)", prop.name, prop.gcnArchName);
+    if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete ctx;
+        return fox_fail(FOX_GPU_ERR_INTERNAL, "init: stream creation failed");
+    }
+    fox_gpu_status st = fox_ws_reserve(ctx, 8u << 20);
+    if (st != FOX_GPU_OK) {
+        fox_gpu_shutdown(ctx);
+        return st;
+    }
+    *out = ctx;
+    return FOX_GPU_OK;
+}
+
+extern "C" void fox_gpu_shutdown(fox_gpu_ctx *ctx)
+{
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) {
+        (void)hipStreamSynchronize(ctx->stream);
+        (void)hipStreamDestroy(ctx->stream);
+    }
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    delete ctx;
+}
+
+extern "C" fox_gpu_status fox_gpu_device_info(fox_gpu_ctx *ctx, char *name, size_t cap,
+                                              int *compute_units, uint64_t *hbm_bytes)
+{
+    if (!ctx) return fox_fail(FOX_GPU_ERR_ARG, "device_info: null context");
+    if (name && cap) snprintf(name, cap, "%s", ctx->name);
+    if (compute_units) *compute_units = ctx->n_cu;
+    if (hbm_bytes) *hbm_bytes = ctx->hbm_bytes;
+    return FOX_GPU_OK;
+}
+
+fox_gpu_status fox_ws_reserve(fox_gpu_ctx *ctx, size_t bytes)
+{
+    if (bytes <= ctx->ws_cap) return FOX_GPU_OK;
+    if (ctx->capturing)
+        return fox_fail(FOX_GPU_ERR_NOMEM,
+                        "workspace: %zu bytes needed but only %zu are reserved, and "
+                        "memory cannot be allocated during graph capture; run the same "
+                        "calls once before capturing",
+                        bytes, ctx->ws_cap);
+    size_t cap = ctx->ws_cap ? ctx->ws_cap : (1u << 20);
+    while (cap < bytes) cap *= 2;
+    if (ctx->ws) {
+        FOX_HIP(hipStreamSynchronize(ctx->stream));
+        FOX_HIP(hipFree(ctx->ws));
+        ctx->ws = nullptr;
+        ctx->ws_cap = 0;
+    }
+    FOX_HIP(hipMalloc(&ctx->ws, cap));
+    ctx->ws_cap = cap;
+    return FOX_GPU_OK;
+}
+
+// ----------------------------------------------------------------- memory
+
+extern "C" fox_gpu_status fox_gpu_malloc(fox_gpu_ctx *ctx, size_t bytes, void **out)
+{
+    if (!ctx || !out || bytes == 0) return fox_fail(FOX_GPU_ERR_ARG, "malloc: bad argument");
+    fox_gpu_status st = set_device(ctx);
+    if (st) return st;
+    hipError_t e = hipMalloc(out, bytes);
+    if (e != hipSuccess) {
+        *out = nullptr;
+        return fox_fail(FOX_GPU_ERR_NOMEM, "malloc: %zu bytes: %s", bytes, hipGetErrorString(e));
+    }
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_free(fox_gpu_ctx *ctx, void *ptr)
+{
+    if (!ctx) return fox_fail(FOX_GPU_ERR_ARG, "free: null context");
+    if (!ptr) return FOX_GPU_OK;
+    FOX_HIP(hipFree(ptr));
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_memcpy_h2d(fox_gpu_ctx *ctx, void *dst, const void *src, size_t n)
+{
+    if (!ctx || (!dst && n) || (!src && n)) return fox_fail(FOX_GPU_ERR_ARG, "memcpy_h2d: null pointer");
+    if (!n) return FOX_GPU_OK;
+    FOX_HIP(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, ctx->stream));
+    FOX_HIP(hipStreamSynchronize(ctx->stream));
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_memcpy_d2h(fox_gpu_ctx *ctx, void *dst, const void *src, size_t n)
+{
+    if (!ctx || (!dst && n) || (!src && n)) return fox_fail(FOX_GPU_ERR_ARG, "memcpy_d2h: null pointer");
+    if (!n) return FOX_GPU_OK;
+    FOX_HIP(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, ctx->stream));
+    FOX_HIP(hipStreamSynchronize(ctx->stream));
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_memcpy_d2d(fox_gpu_ctx *ctx, void *dst, const void *src, size_t n)
+{
+    if (!ctx || (!dst && n) || (!src && n)) return fox_fail(FOX_GPU_ERR_ARG, "memcpy_d2d: null pointer");
+    if (!n) return FOX_GPU_OK;
+    FOX_HIP(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, ctx->stream));
+    return FOX_GPU_OK;
+}
+
+__global__ void fill_bytes(uint8_t *dst, uint8_t v, size_t n)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t step = (size_t)gridDim.x * blockDim.x;
+    for (; i < n; i += step) dst[i] = v;
+}
+
+extern "C" fox_gpu_status fox_gpu_memset(fox_gpu_ctx *ctx, void *dst, int value, size_t n)
+{
+    if (!ctx || (!dst && n)) return fox_fail(FOX_GPU_ERR_ARG, "memset: null pointer");
+    if (!n) return FOX_GPU_OK;
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(fill_bytes, dim3((unsigned)blocks), dim3(256), 0, ctx->stream,
+                       (uint8_t *)dst, (uint8_t)value, n);
+    FOX_LAUNCHED("memset");
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_sync(fox_gpu_ctx *ctx)
+{
+    if (!ctx) return fox_fail(FOX_GPU_ERR_ARG, "sync: null context");
+    FOX_HIP(hipStreamSynchronize(ctx->stream));
+    return FOX_GPU_OK;
+}
+
+// ------------------------------------------------------- weight repacking
+
+// Position of byte `o` of a device chunk in the GGUF block of tile row i:
+// returns the byte offset k inside that row's block and sets *row.
+__device__ __forceinline__ int chunk_source(int type, int o, int *row)
+{
+    int L, e, g;
+    switch (type) {
+    case FOX_GPU_TQ1_0:
+        if (o < 768) {
+            L = o / 12; e = o % 12; g = L >> 4; *row = L & 15;
+            return e < 8 ? 8 * g + e : 32 + 4 * g + (e - 8);
+        }
+        if (o < 832) { L = o - 768; *row = L & 15; return 48 + (L >> 4); }
+        *row = (o - 832) >> 1;
+        return 52 + ((o - 832) & 1);
+    case FOX_GPU_TQ2_0:
+        if (o < 1024) { L = o >> 4; e = o & 15; *row = L & 15; return 16 * (L >> 4) + e; }
+        *row = (o - 1024) >> 1;
+        return 64 + ((o - 1024) & 1);
+    case FOX_GPU_Q4_K:
+        if (o < 2048) {
+            L = o >> 5; e = o & 31; *row = L & 15;
+            return 16 + 32 * (e >> 3) + 8 * (L >> 4) + (e & 7);
+        }
+        *row = (o - 2048) >> 4;
+        return (o - 2048) & 15;
+    case FOX_GPU_Q6_K:
+        if (o < 2048) { *row = o >> 7; return o & 127; }
+        if (o < 3072) { *row = (o - 2048) >> 6; return 128 + ((o - 2048) & 63); }
+        if (o < 3328) { *row = (o - 3072) >> 4; return 192 + ((o - 3072) & 15); }
+        *row = (o - 3328) >> 1;
+        return 208 + ((o - 3328) & 1);
+    }
+    *row = 0;
+    return 0;
+}
+
+// dir 0: GGUF bytes (src) -> device layout (dst); dir 1: the inverse.
+__global__ void repack_blocks(int type, int dir, const uint8_t *src, uint8_t *dst,
+                              uint64_t n_rows, uint64_t nb, uint64_t chunk,
+                              uint64_t blk_bytes, uint64_t total)
+{
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint64_t step = (uint64_t)gridDim.x * blockDim.x;
+    for (; i < total; i += step) {
+        uint64_t c = i / chunk;
+        int o = (int)(i - c * chunk);
+        uint64_t tile = c / nb, b = c - tile * nb;
+        int r;
+        int k = chunk_source(type, o, &r);
+        uint64_t row = tile * FOX_TILE + (uint64_t)r;
+        uint64_t g = (row * nb + b) * blk_bytes + (uint64_t)k;
+        if (dir == 0) {
+            dst[i] = row < n_rows ? src[g] : 0;
+        } else if (row < n_rows) {
+            dst[g] = src[i];
+        }
+    }
+}
+
+static unsigned grid_for(uint64_t n, unsigned block)
+{
+    uint64_t g = (n + block - 1) / block;
+    return (unsigned)(g > 65536 ? 65536 : g);
+}
+
+extern "C" fox_gpu_status fox_gpu_tensor_upload(fox_gpu_ctx *ctx, int type, uint64_t ne0,
+                                                uint64_t ne1, const void *host, uint64_t bytes,
+                                                fox_gpu_tensor **out)
+{
+    size_t be = fox_block_elems(type), bb = fox_block_bytes(type);
+    uint64_t rows = ne1 ? ne1 : 1, want;
+    fox_gpu_tensor *t;
+    fox_gpu_status st;
+
+    if (!ctx || !host || !out || ne0 == 0)
+        return fox_fail(FOX_GPU_ERR_ARG, "tensor_upload: bad argument");
+    *out = nullptr;
+    if (!be)
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED,
+                        "tensor_upload: no device layout for ggml type %d; the device "
+                        "path handles F32, F16, Q4_K, Q6_K, TQ1_0 and TQ2_0", type);
+    if (ne0 % be)
+        return fox_fail(FOX_GPU_ERR_ARG,
+                        "tensor_upload: %llu columns is not a whole number of %s blocks",
+                        (unsigned long long)ne0, fox_type_name(type));
+    want = rows * (ne0 / be) * bb;
+    if (bytes != want)
+        return fox_fail(FOX_GPU_ERR_ARG,
+                        "tensor_upload: %s %llux%llu is %llu bytes, %llu were given",
+                        fox_type_name(type), (unsigned long long)ne0, (unsigned long long)rows,
+                        (unsigned long long)want, (unsigned long long)bytes);
+    if ((st = set_device(ctx))) return st;
+
+    t = new (std::nothrow) fox_gpu_tensor();
+    if (!t) return fox_fail(FOX_GPU_ERR_NOMEM, "tensor_upload: handle");
+    t->type = type;
+    t->ne0 = ne0;
+    t->ne1 = rows;
+    t->gguf_bytes = bytes;
+
+    if (!fox_is_block_type(type)) {
+        t->dev_bytes = bytes;
+        if (hipMalloc(&t->d, bytes) != hipSuccess) {
+            delete t;
+            return fox_fail(FOX_GPU_ERR_NOMEM, "tensor_upload: %llu bytes of HBM",
+                            (unsigned long long)bytes);
+        }
+        if ((st = fox_gpu_memcpy_h2d(ctx, t->d, host, bytes))) {
+            fox_gpu_tensor_free(ctx, t);
+            return st;
+        }
+        *out = t;
+        return FOX_GPU_OK;
+    }
+
+    uint64_t nb = ne0 / 256, chunk = fox_chunk_bytes(type);
+    t->n_tiles = (rows + FOX_TILE - 1) / FOX_TILE;
+    t->dev_bytes = t->n_tiles * nb * chunk;
+    uint8_t *stage = nullptr;
+    if (hipMalloc(&t->d, t->dev_bytes) != hipSuccess) {
+        delete t;
+        return fox_fail(FOX_GPU_ERR_NOMEM, "tensor_upload: %llu bytes of HBM",
+                        (unsigned long long)t->dev_bytes);
+    }
+    if (hipMalloc(&stage, bytes) != hipSuccess) {
+        fox_gpu_tensor_free(ctx, t);
+        return fox_fail(FOX_GPU_ERR_NOMEM, "tensor_upload: %llu bytes of staging",
+                        (unsigned long long)bytes);
+    }
+    st = fox_gpu_memcpy_h2d(ctx, stage, host, bytes);
+    if (!st) {
+        hipLaunchKernelGGL(repack_blocks, dim3(grid_for(t->dev_bytes, 256)), dim3(256), 0,
+                           ctx->stream, type, 0, stage, t->d, rows, nb, chunk,
+                           (uint64_t)bb, t->dev_bytes);
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) st = fox_hip_fail(e, "tensor_upload: repack");
+    }
+    (void)hipFree(stage);
+    if (st) {
+        fox_gpu_tensor_free(ctx, t);
+        return st;
+    }
+    *out = t;
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_tensor_info(const fox_gpu_tensor *t, int *type, uint64_t *ne0,
+                                              uint64_t *ne1, uint64_t *gguf_bytes,
+                                              uint64_t *device_bytes)
+{
+    if (!t) return fox_fail(FOX_GPU_ERR_ARG, "tensor_info: null tensor");
+    if (type) *type = t->type;
+    if (ne0) *ne0 = t->ne0;
+    if (ne1) *ne1 = t->ne1;
+    if (gguf_bytes) *gguf_bytes = t->gguf_bytes;
+    if (device_bytes) *device_bytes = t->dev_bytes;
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_tensor_download(fox_gpu_ctx *ctx, const fox_gpu_tensor *t,
+                                                  void *host, uint64_t bytes)
+{
+    fox_gpu_status st;
+    if (!ctx || !t || !host) return fox_fail(FOX_GPU_ERR_ARG, "tensor_download: bad argument");
+    if (bytes != t->gguf_bytes)
+        return fox_fail(FOX_GPU_ERR_ARG, "tensor_download: tensor holds %llu bytes, %llu asked",
+                        (unsigned long long)t->gguf_bytes, (unsigned long long)bytes);
+    if ((st = set_device(ctx))) return st;
+    if (!fox_is_block_type(t->type)) return fox_gpu_memcpy_d2h(ctx, host, t->d, bytes);
+
+    uint8_t *stage = nullptr;
+    if (hipMalloc(&stage, bytes) != hipSuccess)
+        return fox_fail(FOX_GPU_ERR_NOMEM, "tensor_download: staging");
+    uint64_t nb = t->ne0 / 256;
+    hipLaunchKernelGGL(repack_blocks, dim3(grid_for(t->dev_bytes, 256)), dim3(256), 0,
+                       ctx->stream, t->type, 1, t->d, stage, t->ne1, nb,
+                       (uint64_t)fox_chunk_bytes(t->type), (uint64_t)fox_block_bytes(t->type),
+                       t->dev_bytes);
+    hipError_t e = hipGetLastError();
+    st = e == hipSuccess ? fox_gpu_memcpy_d2h(ctx, host, stage, bytes)
+                         : fox_hip_fail(e, "tensor_download: unpack");
+    (void)hipFree(stage);
+    return st;
+}
+
+extern "C" void fox_gpu_tensor_free(fox_gpu_ctx *ctx, fox_gpu_tensor *t)
+{
+    if (!t) return;
+    if (ctx) (void)hipSetDevice(ctx->device);
+    if (t->d) (void)hipFree(t->d);
+    delete t;
+}
+
+// ----------------------------------------------------------------- graphs
+
+extern "C" fox_gpu_status fox_gpu_graph_begin(fox_gpu_ctx *ctx)
+{
+    if (!ctx) return fox_fail(FOX_GPU_ERR_ARG, "graph_begin: null context");
+    if (ctx->capturing) return fox_fail(FOX_GPU_ERR_ARG, "graph_begin: already capturing");
+    FOX_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->capturing = 1;
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_graph_end(fox_gpu_ctx *ctx, fox_gpu_graph **out)
+{
+    hipGraph_t graph = nullptr;
+    if (!ctx || !out) return fox_fail(FOX_GPU_ERR_ARG, "graph_end: bad argument");
+    if (!ctx->capturing) return fox_fail(FOX_GPU_ERR_ARG, "graph_end: not capturing");
+    ctx->capturing = 0;
+    FOX_HIP(hipStreamEndCapture(ctx->stream, &graph));
+    fox_gpu_graph *g = new (std::nothrow) fox_gpu_graph();
+    if (!g) {
+        (void)hipGraphDestroy(graph);
+        return fox_fail(FOX_GPU_ERR_NOMEM, "graph_end: handle");
+    }
+    g->graph = graph;
+    hipError_t e = hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        delete g;
+        return fox_hip_fail(e, "graph_end: instantiate");
+    }
+    *out = g;
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_graph_launch(fox_gpu_ctx *ctx, fox_gpu_graph *g)
+{
+    if (!ctx || !g) return fox_fail(FOX_GPU_ERR_ARG, "graph_launch: bad argument");
+    FOX_HIP(hipGraphLaunch(g->exec, ctx->stream));
+    return FOX_GPU_OK;
+}
+
+extern "C" void fox_gpu_graph_free(fox_gpu_graph *g)
+{
+    if (!g) return;
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
+}
+
+// ----------------------------------------------------------------- events
+
+extern "C" fox_gpu_status fox_gpu_event_create(fox_gpu_ctx *ctx, fox_gpu_event **out)
+{
+    if (!ctx || !out) return fox_fail(FOX_GPU_ERR_ARG, "event_create: bad argument");
+    fox_gpu_event *e = new (std::nothrow) fox_gpu_event();
+    if (!e) return fox_fail(FOX_GPU_ERR_NOMEM, "event_create: handle");
+    hipError_t r = hipEventCreate(&e->ev);
+    if (r != hipSuccess) {
+        delete e;
+        return fox_hip_fail(r, "event_create");
+    }
+    *out = e;
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_event_record(fox_gpu_ctx *ctx, fox_gpu_event *e)
+{
+    if (!ctx || !e) return fox_fail(FOX_GPU_ERR_ARG, "event_record: bad argument");
+    FOX_HIP(hipEventRecord(e->ev, ctx->stream));
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_event_elapsed(fox_gpu_event *start, fox_gpu_event *stop,
+                                                float *ms)
+{
+    if (!start || !stop || !ms) return fox_fail(FOX_GPU_ERR_ARG, "event_elapsed: bad argument");
+    FOX_HIP(hipEventSynchronize(stop->ev));
+    FOX_HIP(hipEventElapsedTime(ms, start->ev, stop->ev));
+    return FOX_GPU_OK;
+}
+
+extern "C" void fox_gpu_event_destroy(fox_gpu_event *e)
+{
+    if (!e) return;
+    (void)hipEventDestroy(e->ev);
+    delete e;
+}

@@ -1,0 +1,141 @@
+// fox_internal.h -- shared definitions of the gfx950 decode library.
+//
+// Device weight layouts.  Rows are grouped in tiles of 16 (the M dimension of
+// a 16x16xK MFMA); the rows of a tensor are padded with zero rows up to a
+// multiple of 16.  For every (tile, 256-element block) one contiguous chunk
+// holds the 16 rows' bytes of that block, arranged so that lane
+// L = i + 16 g (row i of the tile, k-group g) of a wave reads only its own
+// bytes with aligned 4..16-byte loads.  Byte counts per chunk equal 16 GGUF
+// blocks (no expansion):
+//
+//   TQ1_0  864 B = QS[64 lanes][12]  lane (i,g): qs[8g..8g+7] ++ qs[32+4g..32+4g+3]
+//                  QH[64 lanes][1]   lane (i,g): qh[g]
+//                  D [16 rows][f16]
+//   TQ2_0 1056 B = QS[64 lanes][16]  lane (i,g): qs[16g..16g+15]
+//                  D [16 rows][f16]
+//   Q4_K  2304 B = QS[64 lanes][32]  lane (i,g): for p<4: qs[32p+8g..32p+8g+7]
+//                  HD[16 rows][16]   d, dmin, scales[12]
+//   Q6_K  3360 B = QL[16 rows][128]  QH[16 rows][64]  SC[16 rows][16]  D[16 rows][f16]
+//
+// F16 / F32 tensors stay row-major as in GGUF.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/fox_gpu.h"
+
+#define FOX_TILE 16
+#define TQ1_CHUNK 864
+#define TQ2_CHUNK 1056
+#define Q4K_CHUNK 2304
+#define Q6K_CHUNK 3360
+
+struct fox_gpu_ctx {
+    int device;
+    hipStream_t stream;
+    int n_cu;
+    uint64_t hbm_bytes;
+    char name[128];
+    // activation workspace (quantised values, B operands, corrections)
+    uint8_t *ws;
+    size_t ws_cap;
+    int capturing;
+};
+
+struct fox_gpu_tensor {
+    int type;
+    uint64_t ne0, ne1;        // K, N
+    uint64_t gguf_bytes;
+    uint64_t dev_bytes;
+    uint64_t n_tiles;         // block types: ceil(N / 16)
+    uint8_t *d;
+};
+
+struct fox_gpu_graph {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+struct fox_gpu_event {
+    hipEvent_t ev;
+};
+
+// ---- errors (implemented in fox_gpu.hip)
+fox_gpu_status fox_fail(fox_gpu_status st, const char *fmt, ...)
+    __attribute__((format(printf, 2, 3)));
+fox_gpu_status fox_hip_fail(hipError_t e, const char *what);
+
+#define FOX_HIP(call)                                                    \
+    do {                                                                 \
+        hipError_t fox_e_ = (call);                                      \
+        if (fox_e_ != hipSuccess) return fox_hip_fail(fox_e_, #call);    \
+    } while (0)
+
+#define FOX_LAUNCHED(what)                                               \
+    do {                                                                 \
+        hipError_t fox_e_ = hipGetLastError();                           \
+        if (fox_e_ != hipSuccess) return fox_hip_fail(fox_e_, what);     \
+    } while (0)
+
+// ---- workspace (fox_gpu.hip)
+fox_gpu_status fox_ws_reserve(fox_gpu_ctx *ctx, size_t bytes);
+
+// ---- type helpers
+static inline size_t fox_block_bytes(int type)
+{
+    switch (type) {
+    case FOX_GPU_F32: return 4;
+    case FOX_GPU_F16: return 2;
+    case FOX_GPU_Q4_K: return 144;
+    case FOX_GPU_Q6_K: return 210;
+    case FOX_GPU_TQ1_0: return 54;
+    case FOX_GPU_TQ2_0: return 66;
+    default: return 0;
+    }
+}
+
+static inline size_t fox_block_elems(int type)
+{
+    switch (type) {
+    case FOX_GPU_F32: case FOX_GPU_F16: return 1;
+    case FOX_GPU_Q4_K: case FOX_GPU_Q6_K: case FOX_GPU_TQ1_0: case FOX_GPU_TQ2_0:
+        return 256;
+    default: return 0;
+    }
+}
+
+static inline bool fox_is_block_type(int type) { return fox_block_elems(type) == 256; }
+
+static inline size_t fox_chunk_bytes(int type)
+{
+    switch (type) {
+    case FOX_GPU_Q4_K: return Q4K_CHUNK;
+    case FOX_GPU_Q6_K: return Q6K_CHUNK;
+    case FOX_GPU_TQ1_0: return TQ1_CHUNK;
+    case FOX_GPU_TQ2_0: return TQ2_CHUNK;
+    default: return 0;
+    }
+}
+
+static inline const char *fox_type_name(int type)
+{
+    switch (type) {
+    case FOX_GPU_F32: return "F32";
+    case FOX_GPU_F16: return "F16";
+    case FOX_GPU_Q4_K: return "Q4_K";
+    case FOX_GPU_Q6_K: return "Q6_K";
+    case FOX_GPU_TQ1_0: return "TQ1_0";
+    case FOX_GPU_TQ2_0: return "TQ2_0";
+    default: return "unknown";
+    }
+}
+
+// ---- gemv internals shared by fox_gemv.hip and fox_gpu.hip
+fox_gpu_status fox_gemv_launch(fox_gpu_ctx *ctx, size_t n, const fox_gpu_tensor *const *ws,
+                               const float *x, size_t x_stride, const int8_t *q,
+                               const float *scale, size_t M, float *const *outs,
+                               const size_t *out_strides, unsigned flags,
+                               int32_t *sums);

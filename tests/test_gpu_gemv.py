@@ -1,0 +1,212 @@
+"""GPU parity of the quantised GEMVs against the oracle (bit-exact).
+
+Per-block integer sums, int8 activations and GEMV outputs must equal the
+oracle's (the reference's arithmetic, src/gemv.c, src/ternary.c,
+src/kernels.c, without FMA contraction) bit for bit.
+"""
+import numpy as np
+import pytest
+
+import rustfox_amd as rf
+from rustfox_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+TYPES = {"TQ1_0": 34, "TQ2_0": 35, "Q4_K": 12, "Q6_K": 14, "F16": 1, "F32": 0}
+
+
+def weights(rng, gtype, N, K, raw_bytes=True):
+    """Weights of N rows x K columns.  Block types use arbitrary bytes (every
+    byte value a decoder can meet) with a valid f16 scale, as the reference's
+    own tests do (tests/test_ternary.c:138-144)."""
+    if gtype == 34:
+        w = rng.integers(0, 256, size=(N * K // 256, 54), dtype=np.uint8) if raw_bytes \
+            else synth.tq1_random(rng, N * K // 256)
+        w[:, 52:54] = rng.uniform(0.01, 0.05, size=w.shape[0]).astype(np.float16).view(
+            np.uint8).reshape(-1, 2)
+        return w.reshape(-1)
+    if gtype == 35:
+        w = rng.integers(0, 256, size=(N * K // 256, 66), dtype=np.uint8)
+        w[:, 64:66] = rng.uniform(0.01, 0.05, size=w.shape[0]).astype(np.float16).view(
+            np.uint8).reshape(-1, 2)
+        return w.reshape(-1)
+    if gtype == 12:
+        return synth.q4k_quantize(rng.standard_normal((N, K)).astype(np.float32) * 0.02).reshape(-1)
+    if gtype == 14:
+        return synth.q6k_quantize(rng.standard_normal((N, K)).astype(np.float32) * 0.02).reshape(-1)
+    if gtype == 1:
+        return (rng.standard_normal((N, K)) * 0.02).astype(np.float16).view(np.uint8).reshape(-1)
+    return (rng.standard_normal((N, K)) * 0.02).astype(np.float32).view(np.uint8).reshape(-1)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def oracle_gemv(oracle, gtype, x, w, N, K):
+    return np.stack([oracle.gemv(gtype, x[t], w, N, K) for t in range(x.shape[0])])
+
+
+CASES = [
+    # (type, N, K, M)
+    ("TQ1_0", 16, 256, 1), ("TQ1_0", 37, 512, 1), ("TQ1_0", 100, 2560, 3),
+    ("TQ1_0", 4096, 4096, 1), ("TQ1_0", 1024, 9728, 8), ("TQ1_0", 333, 768, 5),
+    ("TQ2_0", 37, 512, 1), ("TQ2_0", 4096, 4096, 1), ("TQ2_0", 130, 1280, 8),
+    ("Q4_K", 33, 768, 1), ("Q4_K", 512, 4096, 2), ("Q4_K", 64, 2048, 8),
+    ("Q6_K", 29, 512, 1), ("Q6_K", 300, 4096, 3), ("Q6_K", 48, 1024, 8),
+    ("F16", 50, 288, 1), ("F16", 1000, 2560, 2), ("F16", 7, 8, 1), ("F16", 257, 1000, 8),
+    ("F32", 9, 64, 1), ("F32", 300, 288, 4),
+]
+
+
+@pytest.mark.parametrize("tname,N,K,M", CASES)
+def test_gemv_bit_exact(gpu, oracle, tname, N, K, M):
+    print(f"case gemv {tname} N={N} K={K} M={M}", flush=True)
+    gtype = TYPES[tname]
+    rng = np.random.default_rng([N, K, M, gtype])
+    w = weights(rng, gtype, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    want = oracle_gemv(oracle, gtype, x, w, N, K)
+    t = gpu.tensor(gtype, K, N, w)
+    dx = gpu.array(x)
+    out = gpu.empty((M, N), np.float32)
+    gpu.gemv(t, dx, M, out)
+    got = out.numpy()
+    mism = np.flatnonzero(bits(got) != bits(want))
+    assert mism.size == 0, (f"{mism.size} of {got.size} outputs differ; first "
+                            f"{mism[:5]} got {got.reshape(-1)[mism[:5]]} "
+                            f"want {want.reshape(-1)[mism[:5]]}")
+
+
+@pytest.mark.parametrize("tname,N,K,M", [c for c in CASES if c[0] in ("TQ1_0", "TQ2_0", "Q4_K", "Q6_K")])
+def test_block_sums_exact(gpu, oracle, tname, N, K, M):
+    print(f"case block_sums {tname} N={N} K={K} M={M}", flush=True)
+    gtype = TYPES[tname]
+    rng = np.random.default_rng([N, K, M, gtype, 1])
+    w = weights(rng, gtype, N, K)
+    q = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    per = {34: 1, 35: 1, 12: 8, 14: 4}[gtype]
+    want = np.stack([oracle.block_sums(gtype, q[t], w, N, K).reshape(N, K // 256, per)
+                     for t in range(M)])
+    t = gpu.tensor(gtype, K, N, w)
+    sums = gpu.empty((M, N, K // 256, per), np.int32)
+    gpu.block_sums(t, gpu.array(q), M, sums)
+    got = sums.numpy()
+    assert np.array_equal(got, want), f"{np.count_nonzero(got != want)} sums differ"
+
+
+def test_tq1_closed_forms(gpu):
+    """tests/test_ternary.c:100-136: byte 255 / qh 253 decode to all +1 and
+    byte 0 to all -1, so with all-one activations and d = 1 a block sums to
+    +256 / -256."""
+    blk_p = np.zeros(54, np.uint8)
+    blk_p[:48] = 255
+    blk_p[48:52] = 253
+    blk_p[52:54] = [0x00, 0x3C]
+    blk_m = np.zeros(54, np.uint8)
+    blk_m[52:54] = [0x00, 0x3C]
+    w = np.concatenate([np.tile(blk_p, 3), np.tile(blk_m, 3)])
+    t = gpu.tensor(34, 768, 2, w)
+    q = gpu.array(np.ones((1, 768), np.int8))
+    sums = gpu.empty((1, 2, 3, 1), np.int32)
+    gpu.block_sums(t, q, 1, sums)
+    assert np.array_equal(sums.numpy().reshape(2, 3), [[256] * 3, [-256] * 3])
+
+
+@pytest.mark.parametrize("K,M,mode", [(512, 1, 0), (4096, 3, 0), (288, 1, 0), (9728, 8, 0),
+                                      (4096, 2, 1), (768, 8, 1)])
+def test_quantize_exact(gpu, oracle, K, M, mode):
+    print(f"case quantize K={K} M={M} mode={mode}", flush=True)
+    rng = np.random.default_rng([K, M, mode])
+    x = (rng.standard_normal((M, K)) * rng.uniform(0.01, 100)).astype(np.float32)
+    x[0, : min(K, 16)] = 0.0
+    if M > 1:
+        x[1] = 0.0  # an all-zero token gets q = 0 and scale 0 (tests/test_gemv.c:254-257)
+    nsc = M if mode == 0 else M * (K // 256)
+    dq, ds = gpu.empty((M, K), np.int8), gpu.empty(nsc, np.float32)
+    gpu.quantize(mode, gpu.array(x), K, M, K, dq, ds)
+    q, s = dq.numpy(), ds.numpy()
+    for t in range(M):
+        if mode == 0:
+            wq, ws = oracle.quantize(x[t])
+            assert np.array_equal(q[t], wq)
+            assert bits(s[t]) == bits(np.float32(ws))
+        else:
+            wq, ws = oracle.quantize_k(x[t])
+            assert np.array_equal(q[t], wq)
+            assert np.array_equal(bits(s.reshape(M, -1)[t]), bits(ws))
+
+
+@pytest.mark.parametrize("tname", ["TQ1_0", "TQ2_0", "Q4_K", "Q6_K"])
+def test_i8_entry_equals_float_entry(gpu, oracle, tname):
+    """f32 entry == pre-quantised entry exactly (tests/test_gemv.c:318-325)."""
+    gtype = TYPES[tname]
+    N, K, M = 70, 1024, 2
+    rng = np.random.default_rng([7, gtype])
+    w = weights(rng, gtype, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    t = gpu.tensor(gtype, K, N, w)
+    mode = 1 if gtype in (12, 14) else 0
+    dq = gpu.empty((M, K), np.int8)
+    ds = gpu.empty(M * (K // 256) if mode else M, np.float32)
+    dx = gpu.array(x)
+    gpu.quantize(mode, dx, K, M, K, dq, ds)
+    a, b = gpu.empty((M, N), np.float32), gpu.empty((M, N), np.float32)
+    gpu.gemv(t, dx, M, a)
+    gpu.gemv_i8(t, dq, ds, M, b)
+    assert np.array_equal(bits(a.numpy()), bits(b.numpy()))
+    want = oracle_gemv(oracle, gtype, x, w, N, K)
+    assert np.array_equal(bits(a.numpy()), bits(want))
+
+
+def test_gemv_multi_and_accumulate(gpu, oracle):
+    """q/k/v in one call share the quantised input; ACCUMULATE adds into out
+    exactly as fox_add would (src/ops.c:50-54)."""
+    rng = np.random.default_rng(11)
+    K = 2560
+    shapes = [4096, 1024, 1024]
+    ws = [weights(rng, 34, n, K) for n in shapes]
+    x = rng.standard_normal((2, K)).astype(np.float32)
+    ts = [gpu.tensor(34, K, n, w) for n, w in zip(shapes, ws)]
+    outs = [gpu.empty((2, n), np.float32) for n in shapes]
+    gpu.gemv_multi(ts, gpu.array(x), 2, outs)
+    for n, w, o in zip(shapes, ws, outs):
+        assert np.array_equal(bits(o.numpy()), bits(oracle_gemv(oracle, 34, x, w, n, K)))
+    base = rng.standard_normal((2, 4096)).astype(np.float32)
+    acc = gpu.array(base)
+    gpu.gemv(ts[0], gpu.array(x), 2, acc, flags=rf.GEMV_ACCUMULATE)
+    want = base + oracle_gemv(oracle, 34, x, ws[0], 4096, K)
+    assert np.array_equal(bits(acc.numpy()), bits(want))
+
+
+@pytest.mark.parametrize("tname,N,K", [("TQ1_0", 37, 512), ("TQ2_0", 20, 256),
+                                       ("Q4_K", 17, 512), ("Q6_K", 33, 256), ("F16", 5, 288)])
+def test_tensor_bytes_round_trip(gpu, tname, N, K):
+    """The device backend holds the GGUF bytes exactly: repack then unpack
+    gives them back (the resident == streamed byte check of
+    tests/test_weights.c:142-175, for HBM)."""
+    gtype = TYPES[tname]
+    rng = np.random.default_rng(3)
+    w = rng.integers(0, 256, size=N * synth.row_bytes(gtype, K), dtype=np.uint8)
+    t = gpu.tensor(gtype, K, N, w)
+    assert np.array_equal(t.download(), w)
+    info = t.info()
+    assert info["gguf_bytes"] == w.nbytes
+    assert info["device_bytes"] >= w.nbytes
+
+
+def test_errors_follow_the_reference(gpu):
+    """Ragged K, bad sizes and unknown types fail with the reference's
+    status codes (src/gemv.c:80-85, src/kernels.c:852-857)."""
+    with pytest.raises(rf.FoxError) as e:
+        gpu.tensor(34, 255, 4, np.zeros(54 * 4, np.uint8))
+    assert e.value.status == 1
+    with pytest.raises(rf.FoxError) as e:
+        gpu.tensor(10, 256, 1, np.zeros(84, np.uint8))   # Q2_K: no kernel
+    assert e.value.status == 5
+    t = gpu.tensor(34, 256, 16, np.zeros(54 * 16, np.uint8))
+    x = gpu.array(np.zeros((9, 256), np.float32))
+    out = gpu.empty((9, 16), np.float32)
+    with pytest.raises(rf.FoxError) as e:
+        gpu.gemv(t, x, 9, out)                           # more than 8 tokens
+    assert e.value.status == 1
