@@ -178,13 +178,18 @@ fox_gpu_status fox_gpu_rope_store(fox_gpu_ctx *ctx, float *q, size_t q_stride,
                                   float *k_cache, float *v_cache);
 
 /* Causal GQA attention of M tokens at positions pos[0] + t over cache rows
- * 0 .. pos[0] + t: softmax(q.k / sqrt(hd)) v (src/forward.c:303-338),
- * computed split over positions and merged (flash-decoding). */
+ * 0 .. pos[0] + t: softmax(q.k / sqrt(hd)) v (src/forward.c:303-338).
+ * FOX_GPU_ATTN_EXACT computes every sum in the reference's order (scores in
+ * head-dimension order, softmax and value sums in position order) and
+ * reproduces it bit for bit; FOX_GPU_ATTN_SPLIT splits positions over
+ * workgroups and merges the partial softmaxes (flash-decoding), equal to it
+ * within float rounding. */
+enum { FOX_GPU_ATTN_SPLIT = 0, FOX_GPU_ATTN_EXACT = 1 };
 fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t out_stride,
                                  const float *q, size_t q_stride,
                                  const float *k_cache, const float *v_cache,
                                  size_t n_head, size_t n_head_kv, size_t head_dim,
-                                 size_t M, const uint32_t *pos, size_t n_ctx);
+                                 size_t M, const uint32_t *pos, size_t n_ctx, int mode);
 
 /* gate = silu(gate) * up (src/ops.c:41-48) and dst += src (src/ops.c:50-54)
  * on M rows of n. */
@@ -193,11 +198,13 @@ fox_gpu_status fox_gpu_silu_mul(fox_gpu_ctx *ctx, float *gate, const float *up,
 fox_gpu_status fox_gpu_add(fox_gpu_ctx *ctx, float *dst, const float *src,
                            size_t n, size_t M, size_t stride);
 
-/* first index of the maximum (src/sample.c:147-153) -> *idx (device uint32);
- * with pos != NULL the device position is advanced by `advance` in the same
- * launch (the decode loop's bookkeeping, kept on the device). */
+/* first index of the maximum (src/sample.c:147-153) -> *idx (device uint32).
+ * With pos != NULL the device position is advanced by `advance` in the same
+ * launch, and with history != NULL history[pos before the advance] = *idx:
+ * the bookkeeping of a decode loop kept on the device. */
 fox_gpu_status fox_gpu_argmax(fox_gpu_ctx *ctx, const float *logits, size_t n,
-                              uint32_t *idx, uint32_t *pos, uint32_t advance);
+                              uint32_t *idx, uint32_t *pos, uint32_t advance,
+                              uint32_t *history);
 
 /* ------------------------------------------------------------- graphs */
 

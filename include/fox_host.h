@@ -1,0 +1,190 @@
+/*
+ * fox_host.h -- the RustFox host API, kept, over the gfx950 device path.
+ *
+ * libfox.so exports the RustFox entry points a decode loop uses, with the
+ * same names, argument meaning, status codes and ownership rules as
+ * include/fox/fox.h of RustFox, so a caller of the reference switches by
+ * opening the model with FOX_WEIGHTS_DEVICE.  Compute runs on the GPU through
+ * include/fox_gpu.h; there are no CPU kernels in this library.
+ *
+ * Declarations below cite the RustFox interface each one keeps
+ * (include/fox/fox.h:line).  Entries marked EXTENSION have no RustFox
+ * counterpart.
+ */
+#ifndef FOX_HOST_H
+#define FOX_HOST_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* include/fox/fox.h:17-30 */
+typedef enum {
+    FOX_OK = 0,
+    FOX_ERR_ARG,
+    FOX_ERR_IO,
+    FOX_ERR_NOMEM,
+    FOX_ERR_FORMAT,
+    FOX_ERR_UNSUPPORTED,
+    FOX_ERR_NOTFOUND,
+    FOX_ERR_INTERNAL
+} fox_status;
+
+const char *fox_version(void);
+const char *fox_status_str(fox_status s);
+const char *fox_last_error(void);
+
+#define FOX_NAME_MAX 128
+
+/* include/fox/fox.h:213-224 (the ids this build reads) */
+typedef enum {
+    FOX_GGML_F32 = 0, FOX_GGML_F16 = 1, FOX_GGML_Q4_K = 12, FOX_GGML_Q6_K = 14,
+    FOX_GGML_TQ1_0 = 34, FOX_GGML_TQ2_0 = 35
+} fox_ggml_type;
+
+const char *fox_ggml_type_name(fox_ggml_type type);
+uint32_t    fox_ggml_type_block_size(fox_ggml_type type);
+uint32_t    fox_ggml_type_block_bytes(fox_ggml_type type);
+/* include/fox/fox.h:360-361: a type the device path has kernels for */
+int         fox_gemv_supports(fox_ggml_type type);
+size_t      fox_row_bytes(fox_ggml_type type, size_t n_cols);
+
+/* ------------------------------------------------------------- weights */
+
+/* include/fox/fox.h:370-403, plus the HBM-resident mode */
+#define FOX_WEIGHTS_MAX_LIVE_LEASES 8
+
+typedef enum {
+    FOX_WEIGHTS_RESIDENT = 0,   /* host memory, loaded on first touch        */
+    FOX_WEIGHTS_STREAM   = 1,   /* not provided by this build                */
+    FOX_WEIGHTS_DEVICE   = 2    /* HBM of the GPU, loaded once per tensor    */
+} fox_weights_mode;
+
+typedef struct fox_weights fox_weights;
+
+/* For FOX_WEIGHTS_DEVICE, data is an opaque device tensor handle
+ * (const fox_gpu_tensor *, include/fox_gpu.h) and bytes the GGUF size. */
+typedef struct {
+    const void *data;
+    uint64_t    bytes;
+    size_t      tensor_index;
+    void       *slot;
+} fox_weights_lease;
+
+fox_status fox_weights_open(const char *gguf_path, fox_weights_mode mode,
+                            uint64_t budget_bytes, fox_weights **out);
+void       fox_weights_close(fox_weights *w);
+fox_weights_mode fox_weights_get_mode(const fox_weights *w);
+size_t     fox_weights_tensor_count(const fox_weights *w);             /* EXTENSION */
+size_t     fox_weights_tensor_find(const fox_weights *w, const char *name); /* EXTENSION */
+fox_status fox_weights_acquire(fox_weights *w, size_t tensor_index,
+                               fox_weights_lease *lease);
+void       fox_weights_release(fox_weights *w, fox_weights_lease *lease);
+fox_status fox_weights_prefetch(fox_weights *w, size_t tensor_index);
+fox_status fox_weights_prefetch_async(fox_weights *w, size_t tensor_index);
+fox_status fox_weights_prefetch_wait(fox_weights *w, size_t tensor_index);
+size_t     fox_weights_live_leases(const fox_weights *w);
+uint64_t   fox_weights_resident_bytes(const fox_weights *w);
+uint64_t   fox_weights_reads(const fox_weights *w);
+uint64_t   fox_weights_evictions(const fox_weights *w);
+
+/* -------------------------------------------------------- model / eval */
+
+/* include/fox/fox.h:405-420 */
+typedef struct {
+    char     arch[32];
+    char     name[FOX_NAME_MAX];
+    uint32_t n_layer;
+    uint32_t n_embd;
+    uint32_t n_head;
+    uint32_t n_head_kv;
+    uint32_t n_ff;
+    uint32_t head_dim;
+    uint32_t n_vocab;
+    uint32_t n_ctx_train;
+    float    rms_eps;
+    float    rope_freq_base;
+    uint64_t weight_bytes;
+    int      tied_output;
+} fox_model_info;
+
+typedef struct fox_model   fox_model;
+typedef struct fox_context fox_context;
+
+/* include/fox/fox.h:425-431.  The GPU is HIP device FOX_DEVICE (environment,
+ * default 0). */
+fox_status fox_model_open(const char *gguf_path, fox_weights_mode mode,
+                          uint64_t budget_bytes, fox_model **out);
+void       fox_model_close(fox_model *m);
+const fox_model_info *fox_model_get_info(const fox_model *m);
+fox_weights          *fox_model_weights(fox_model *m);
+
+/* include/fox/fox.h:433-451 */
+typedef struct {
+    uint32_t n_ctx;
+    uint32_t n_batch;
+    int      n_threads;   /* kept for the ABI; the GPU path ignores it */
+} fox_context_config;
+
+void       fox_context_config_default(fox_context_config *cfg, const fox_model *m);
+fox_status fox_context_create(fox_model *m, const fox_context_config *cfg,
+                              fox_context **out);
+void       fox_context_destroy(fox_context *ctx);
+void       fox_context_reset(fox_context *ctx);
+/* logits of the last token, host memory owned by ctx, valid until the next
+ * eval or destroy (src/forward.c:492-519) */
+fox_status fox_eval(fox_context *ctx, const uint32_t *tokens, size_t n_tokens,
+                    float **logits_out);
+uint32_t   fox_context_position(const fox_context *ctx);
+double     fox_context_last_eval_seconds(const fox_context *ctx);
+uint64_t   fox_context_weight_reads(const fox_context *ctx);
+
+/* EXTENSION.  Greedy decode kept on the device: feed `token` at the current
+ * position, then n_steps times take the first argmax of the logits
+ * (src/sample.c:147-153, repeat penalty 1.0) as the next input.  out_ids
+ * receives the n_steps chosen ids.  The step is one captured HIP graph, so
+ * no logits cross PCIe.  Equivalent to fox_eval + argmax per step. */
+fox_status fox_decode_greedy(fox_context *ctx, uint32_t token, size_t n_steps,
+                             uint32_t *out_ids);
+
+/* EXTENSION.  Write rows [p0, p0+n) of one layer's K and V cache (n_head_kv *
+ * head_dim floats per row, host memory) and set the position: a pre-filled
+ * cache without a prefill pass.  RustFox keeps its cache private. */
+fox_status fox_context_set_kv(fox_context *ctx, uint32_t layer, uint32_t p0, uint32_t n,
+                              const float *k, const float *v);
+fox_status fox_context_set_position(fox_context *ctx, uint32_t pos);
+
+/* EXTENSION.  Attention summation order.  exact != 0 (the default) sums in
+ * the reference's order and reproduces its logits bit for bit; exact == 0
+ * splits positions over workgroups (flash-decoding), logits equal within
+ * float rounding.  The environment variable FOX_ATTENTION=split sets the
+ * default of new contexts. */
+fox_status fox_context_set_attention(fox_context *ctx, int exact);
+
+/* ------------------------------------------------------------- sampler */
+
+/* include/fox/fox.h:453-469 */
+typedef struct {
+    float    temperature;
+    int      top_k;
+    float    top_p;
+    float    repeat_penalty;
+    uint32_t repeat_last_n;
+    uint64_t seed;
+} fox_sampler_config;
+
+typedef struct fox_sampler fox_sampler;
+
+void         fox_sampler_config_default(fox_sampler_config *cfg);
+fox_sampler *fox_sampler_create(const fox_sampler_config *cfg, size_t n_vocab);
+void         fox_sampler_destroy(fox_sampler *s);
+void         fox_sampler_accept(fox_sampler *s, uint32_t token);
+fox_status   fox_sampler_pick(fox_sampler *s, const float *logits, uint32_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

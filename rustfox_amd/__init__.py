@@ -23,6 +23,7 @@ HOST_LIB = os.path.join(HERE, "lib", "libfox.so")
 F32, F16, Q4_K, Q6_K, TQ1_0, TQ2_0 = 0, 1, 12, 14, 34, 35
 ACT_PER_VECTOR, ACT_PER_BLOCK = 0, 1
 GEMV_ACCUMULATE = 1
+ATTN_SPLIT, ATTN_EXACT = 0, 1
 MAX_TOKENS = 8
 
 STATUS = ["OK", "ERR_ARG", "ERR_IO", "ERR_NOMEM", "ERR_FORMAT", "ERR_UNSUPPORTED",
@@ -76,10 +77,10 @@ def gpu_lib() -> C.CDLL:
         "fox_gpu_rmsnorm": [vp, vp, sz, vp, sz, vp, sz, sz, C.c_float],
         "fox_gpu_rope_store": [vp, vp, sz, vp, sz, vp, sz, sz, sz, sz, sz, vp, vp, vp, sz,
                                vp, vp],
-        "fox_gpu_attention": [vp, vp, sz, vp, sz, vp, vp, sz, sz, sz, sz, vp, sz],
+        "fox_gpu_attention": [vp, vp, sz, vp, sz, vp, vp, sz, sz, sz, sz, vp, sz, C.c_int],
         "fox_gpu_silu_mul": [vp, vp, vp, sz, sz, sz],
         "fox_gpu_add": [vp, vp, vp, sz, sz, sz],
-        "fox_gpu_argmax": [vp, vp, sz, vp, vp, C.c_uint32],
+        "fox_gpu_argmax": [vp, vp, sz, vp, vp, C.c_uint32, vp],
         "fox_gpu_graph_begin": [vp],
         "fox_gpu_graph_end": [vp, C.POINTER(vp)],
         "fox_gpu_graph_launch": [vp, vp],
@@ -269,5 +270,224 @@ class Gpu:
     def __del__(self):
         try:
             self.close()
+        except Exception:
+            pass
+
+
+# ----------------------------------------------------------------- host API
+
+WEIGHTS_RESIDENT, WEIGHTS_STREAM, WEIGHTS_DEVICE = 0, 1, 2
+_host = None
+
+
+class ModelInfo(C.Structure):
+    """fox_model_info (include/fox_host.h)."""
+    _fields_ = [("arch", C.c_char * 32), ("name", C.c_char * 128), ("n_layer", C.c_uint32),
+                ("n_embd", C.c_uint32), ("n_head", C.c_uint32), ("n_head_kv", C.c_uint32),
+                ("n_ff", C.c_uint32), ("head_dim", C.c_uint32), ("n_vocab", C.c_uint32),
+                ("n_ctx_train", C.c_uint32), ("rms_eps", C.c_float),
+                ("rope_freq_base", C.c_float), ("weight_bytes", C.c_uint64),
+                ("tied_output", C.c_int)]
+
+
+class ContextConfig(C.Structure):
+    _fields_ = [("n_ctx", C.c_uint32), ("n_batch", C.c_uint32), ("n_threads", C.c_int)]
+
+
+class SamplerConfig(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_int), ("top_p", C.c_float),
+                ("repeat_penalty", C.c_float), ("repeat_last_n", C.c_uint32),
+                ("seed", C.c_uint64)]
+
+
+class Lease(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("bytes", C.c_uint64), ("tensor_index", C.c_size_t),
+                ("slot", C.c_void_p)]
+
+
+def host_lib() -> C.CDLL:
+    """Load libfox.so (the RustFox host API over the GPU path)."""
+    global _host
+    if _host is not None:
+        return _host
+    if not os.path.exists(HOST_LIB):
+        raise FileNotFoundError(f"{HOST_LIB} is missing: build it with `make -C rustfox_amd`")
+    L = C.CDLL(HOST_LIB)
+    vp, sz, u32 = C.c_void_p, C.c_size_t, C.c_uint32
+    u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
+    f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+    sigs = {
+        "fox_model_open": ([C.c_char_p, C.c_int, C.c_uint64, C.POINTER(vp)], C.c_int),
+        "fox_model_close": ([vp], None),
+        "fox_model_get_info": ([vp], C.POINTER(ModelInfo)),
+        "fox_model_weights": ([vp], vp),
+        "fox_context_config_default": ([C.POINTER(ContextConfig), vp], None),
+        "fox_context_create": ([vp, C.POINTER(ContextConfig), C.POINTER(vp)], C.c_int),
+        "fox_context_destroy": ([vp], None),
+        "fox_context_reset": ([vp], None),
+        "fox_eval": ([vp, u32p, sz, C.POINTER(C.POINTER(C.c_float))], C.c_int),
+        "fox_decode_greedy": ([vp, u32, sz, u32p], C.c_int),
+        "fox_context_position": ([vp], u32),
+        "fox_context_last_eval_seconds": ([vp], C.c_double),
+        "fox_context_weight_reads": ([vp], C.c_uint64),
+        "fox_context_set_kv": ([vp, u32, u32, u32, f32p, f32p], C.c_int),
+        "fox_context_set_position": ([vp, u32], C.c_int),
+        "fox_context_set_attention": ([vp, C.c_int], C.c_int),
+        "fox_weights_open": ([C.c_char_p, C.c_int, C.c_uint64, C.POINTER(vp)], C.c_int),
+        "fox_weights_close": ([vp], None),
+        "fox_weights_get_mode": ([vp], C.c_int),
+        "fox_weights_tensor_count": ([vp], sz),
+        "fox_weights_tensor_find": ([vp, C.c_char_p], sz),
+        "fox_weights_acquire": ([vp, sz, C.POINTER(Lease)], C.c_int),
+        "fox_weights_release": ([vp, C.POINTER(Lease)], None),
+        "fox_weights_prefetch": ([vp, sz], C.c_int),
+        "fox_weights_prefetch_async": ([vp, sz], C.c_int),
+        "fox_weights_prefetch_wait": ([vp, sz], C.c_int),
+        "fox_weights_live_leases": ([vp], sz),
+        "fox_weights_resident_bytes": ([vp], C.c_uint64),
+        "fox_weights_reads": ([vp], C.c_uint64),
+        "fox_weights_evictions": ([vp], C.c_uint64),
+        "fox_sampler_config_default": ([C.POINTER(SamplerConfig)], None),
+        "fox_sampler_create": ([C.POINTER(SamplerConfig), sz], vp),
+        "fox_sampler_destroy": ([vp], None),
+        "fox_sampler_accept": ([vp, u32], None),
+        "fox_sampler_pick": ([vp, f32p, C.POINTER(u32)], C.c_int),
+        "fox_gemv_supports": ([C.c_int], C.c_int),
+        "fox_row_bytes": ([C.c_int, sz], sz),
+        "fox_last_error": ([], C.c_char_p),
+        "fox_version": ([], C.c_char_p),
+    }
+    for name, (args, res) in sigs.items():
+        f = getattr(L, name)
+        f.argtypes = args
+        f.restype = res
+    _host = L
+    return L
+
+
+def _hcheck(st: int):
+    if st != 0:
+        msg = host_lib().fox_last_error()
+        raise FoxError(st, msg.decode() if msg else "")
+
+
+class Model:
+    """fox_model_open(path, mode): the RustFox model API on the GPU build."""
+
+    def __init__(self, path: str, mode: int = WEIGHTS_DEVICE, budget: int = 0):
+        self.lib = host_lib()
+        m = C.c_void_p()
+        _hcheck(self.lib.fox_model_open(path.encode(), mode, budget, C.byref(m)))
+        self.m = m.value
+        self.info = self.lib.fox_model_get_info(self.m).contents
+
+    def context(self, n_ctx: int = 0, n_batch: int = 32) -> "Context":
+        return Context(self, n_ctx, n_batch)
+
+    def weights(self):
+        return self.lib.fox_model_weights(self.m)
+
+    def close(self):
+        if self.m:
+            self.lib.fox_model_close(self.m)
+            self.m = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Context:
+    def __init__(self, model: Model, n_ctx: int = 0, n_batch: int = 32):
+        self.model, self.lib = model, model.lib
+        cfg = ContextConfig()
+        self.lib.fox_context_config_default(C.byref(cfg), model.m)
+        if n_ctx:
+            cfg.n_ctx = n_ctx
+        cfg.n_batch = n_batch
+        ctx = C.c_void_p()
+        _hcheck(self.lib.fox_context_create(model.m, C.byref(cfg), C.byref(ctx)))
+        self.ctx = ctx.value
+
+    def eval(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(np.atleast_1d(tokens), dtype=np.uint32)
+        lp = C.POINTER(C.c_float)()
+        _hcheck(self.lib.fox_eval(self.ctx, t, t.size, C.byref(lp)))
+        return np.ctypeslib.as_array(lp, shape=(self.model.info.n_vocab,)).copy()
+
+    def decode_greedy(self, token: int, n_steps: int) -> np.ndarray:
+        out = np.zeros(n_steps, np.uint32)
+        _hcheck(self.lib.fox_decode_greedy(self.ctx, int(token), n_steps, out))
+        return out
+
+    def set_kv(self, layer, p0, k, v):
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        _hcheck(self.lib.fox_context_set_kv(self.ctx, layer, p0, k.shape[0], k, v))
+
+    def set_position(self, pos):
+        _hcheck(self.lib.fox_context_set_position(self.ctx, pos))
+
+    def set_attention(self, exact: bool):
+        _hcheck(self.lib.fox_context_set_attention(self.ctx, 1 if exact else 0))
+
+    @property
+    def position(self) -> int:
+        return self.lib.fox_context_position(self.ctx)
+
+    @property
+    def last_seconds(self) -> float:
+        return self.lib.fox_context_last_eval_seconds(self.ctx)
+
+    def reset(self):
+        self.lib.fox_context_reset(self.ctx)
+
+    def close(self):
+        if self.ctx:
+            self.lib.fox_context_destroy(self.ctx)
+            self.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Sampler:
+    def __init__(self, n_vocab: int, temperature=None, **kw):
+        self.lib = host_lib()
+        cfg = SamplerConfig()
+        self.lib.fox_sampler_config_default(C.byref(cfg))
+        if temperature is not None:
+            cfg.temperature = temperature
+        for k, v in kw.items():
+            setattr(cfg, k, v)
+        self.s = self.lib.fox_sampler_create(C.byref(cfg), n_vocab)
+        if not self.s:
+            raise FoxError(1, host_lib().fox_last_error().decode())
+
+    def accept(self, tok):
+        self.lib.fox_sampler_accept(self.s, int(tok))
+
+    def pick(self, logits) -> int:
+        out = C.c_uint32()
+        _hcheck(self.lib.fox_sampler_pick(self.s, np.ascontiguousarray(logits, np.float32),
+                                          C.byref(out)))
+        return out.value
+
+    def __del__(self):
+        try:
+            if self.s:
+                self.lib.fox_sampler_destroy(self.s)
+                self.s = None
         except Exception:
             pass

@@ -97,6 +97,7 @@ extern "C" void fox_gpu_shutdown(fox_gpu_ctx *ctx)
         (void)hipStreamDestroy(ctx->stream);
     }
     if (ctx->ws) (void)hipFree(ctx->ws);
+    for (int i = 0; i < ctx->n_retired; i++) (void)hipFree(ctx->retired[i]);
     delete ctx;
 }
 
@@ -121,13 +122,16 @@ fox_gpu_status fox_ws_reserve(fox_gpu_ctx *ctx, size_t bytes)
                         bytes, ctx->ws_cap);
     size_t cap = ctx->ws_cap ? ctx->ws_cap : (1u << 20);
     while (cap < bytes) cap *= 2;
+    uint8_t *fresh = nullptr;
+    FOX_HIP(hipMalloc(&fresh, cap));
     if (ctx->ws) {
-        FOX_HIP(hipStreamSynchronize(ctx->stream));
-        FOX_HIP(hipFree(ctx->ws));
-        ctx->ws = nullptr;
-        ctx->ws_cap = 0;
+        if (ctx->n_retired == (int)(sizeof(ctx->retired) / sizeof(ctx->retired[0]))) {
+            (void)hipFree(fresh);
+            return fox_fail(FOX_GPU_ERR_NOMEM, "workspace: grown too many times");
+        }
+        ctx->retired[ctx->n_retired++] = ctx->ws;
     }
-    FOX_HIP(hipMalloc(&ctx->ws, cap));
+    ctx->ws = fresh;
     ctx->ws_cap = cap;
     return FOX_GPU_OK;
 }

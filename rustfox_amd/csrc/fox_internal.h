@@ -43,6 +43,10 @@ struct fox_gpu_ctx {
     uint8_t *ws;
     size_t ws_cap;
     int capturing;
+    // earlier, smaller workspaces: a captured graph may still address them,
+    // so they are freed only at shutdown
+    uint8_t *retired[32];
+    int n_retired;
 };
 
 struct fox_gpu_tensor {

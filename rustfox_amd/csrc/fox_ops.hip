@@ -3,6 +3,7 @@
 // Built with -ffp-contract=off like the rest of the library: every float op
 // rounds once, in the reference's order where the reference fixes an order.
 #include "fox_internal.h"
+#include "fox_math.h"
 
 #include <cmath>
 
@@ -58,9 +59,19 @@ __device__ __forceinline__ double wave_sum_d(double v)
     return v;
 }
 
-// src/ops.c:7-22: squares summed in double (here as a tree; every term is
-// exact in double, the float scale below rounds away the order), then
-// out = x * scale * w with two float roundings.
+// src/ops.c:7-22: scale = (float)(1 / sqrt(sum x^2 / n + eps)) with the
+// squares (exact in double) summed in double in index order, then
+// out = x * scale * w, two float roundings.  The in-order double sum is
+// replaced by a tree sum S_t; the in-order sum lies within
+// (n + 64) * 2^-52 * S_t of it, so if both ends of that interval give the
+// same float scale (double operations widened by a few ulps), that float is
+// the reference's.  Otherwise (about one call in 10^5) one lane redoes the
+// sum in index order.
+__device__ __forceinline__ double rms_scale_d(double ss, int n, float eps)
+{
+    return 1.0 / __builtin_sqrt(ss / (double)n + (double)eps);
+}
+
 __global__ __launch_bounds__(256) void rmsnorm_k(float *__restrict__ out, size_t out_stride,
                                                  const float *__restrict__ x, size_t x_stride,
                                                  const float *__restrict__ w, int n, float eps)
@@ -75,8 +86,18 @@ __global__ __launch_bounds__(256) void rmsnorm_k(float *__restrict__ out, size_t
     if ((tid & 63) == 0) red[tid >> 6] = s;
     __syncthreads();
     if (tid == 0) {
-        double tot = (red[0] + red[1]) + (red[2] + red[3]);
-        sc = (float)(1.0 / sqrt(tot / (double)n + (double)eps));
+        const double tot = (red[0] + red[1]) + (red[2] + red[3]);
+        const double rel = (double)(n + 64) * 0x1p-52;
+        const double y_hi = rms_scale_d(tot * (1.0 - rel), n, eps) * (1.0 + 0x1p-50);
+        const double y_lo = rms_scale_d(tot * (1.0 + rel), n, eps) * (1.0 - 0x1p-50);
+        float f_hi = (float)y_hi, f_lo = (float)y_lo;
+        if (f_hi == f_lo) {
+            sc = f_hi;
+        } else {
+            double seq = 0.0;
+            for (int i = 0; i < n; i++) seq += (double)xt[i] * (double)xt[i];
+            sc = (float)rms_scale_d(seq, n, eps);
+        }
     }
     __syncthreads();
     const float scale = sc;
@@ -200,7 +221,7 @@ __global__ __launch_bounds__(256) void attn_partial(const float *__restrict__ q,
         }
         return;
     }
-    const float scale = 1.0f / sqrtf((float)hd);
+    const float scale = fox_div(1.0f, fox_sqrtf((float)hd));
     for (int i = tid; i < gqa * hd; i += 256)
         qs[i] = q[(size_t)t * q_stride + (size_t)kvh * gqa * hd + i];
     __syncthreads();
@@ -232,7 +253,7 @@ __global__ __launch_bounds__(256) void attn_partial(const float *__restrict__ q,
         float m = v;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-        float e = lane < pn ? expf(v - m) : 0.0f;
+        float e = lane < pn ? fox_expf(v - m) : 0.0f;
         if (lane < pn) sc[g * ATT_SPLIT + lane] = e;
         float l = wave_sum_f(e);
         if (lane == 0) {
@@ -269,23 +290,139 @@ __global__ void attn_merge(const float *__restrict__ part, int n_head, int hd, i
     float L = 0.0f;
     for (int s = 0; s < n_splits; s++) {
         float m = base[s * rec];
-        if (m > -INFINITY) L += base[s * rec + 1] * expf(m - mx);
+        if (m > -INFINITY) L += base[s * rec + 1] * fox_expf(m - mx);
     }
     for (int d = threadIdx.x; d < hd; d += blockDim.x) {
         float o = 0.0f;
         for (int s = 0; s < n_splits; s++) {
             float m = base[s * rec];
-            if (m > -INFINITY) o += base[s * rec + 2 + d] * expf(m - mx);
+            if (m > -INFINITY) o += base[s * rec + 2 + d] * fox_expf(m - mx);
         }
         out[(size_t)t * out_stride + (size_t)h * hd + d] = o / L;
     }
+}
+
+
+// ---- attention in the reference's order (src/forward.c:303-338,
+// src/ops.c:24-39, 75-81), bit for bit:
+//   score_j = (sum_d q_d k_jd, summed in d order) * (1 / sqrtf(hd));
+//   softmax: max, e_j = expf(score_j - max), sum in j order, e_j * (1/sum);
+//   out_d = sum in j order of a_j v_jd.
+// Each in-order sum is one lane's chain; work is spread over lanes by
+// position (scores), head (softmax) and head x dimension (values).
+
+#define EX_TILE 32
+
+__global__ __launch_bounds__(256) void attn_scores_exact(const float *__restrict__ q,
+                                                         size_t q_stride,
+                                                         const float *__restrict__ kc,
+                                                         int n_head, int n_head_kv, int hd,
+                                                         const uint32_t *__restrict__ pos,
+                                                         int n_ctx, float *__restrict__ att)
+{
+    __shared__ float ks[EX_TILE * (ATT_MAXHD + 1)];
+    __shared__ float qs[ATT_MAXG * ATT_MAXHD];
+    const int p0 = blockIdx.x * EX_TILE, kvh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
+    const int gqa = n_head / n_head_kv, kvd = n_head_kv * hd, ks_stride = hd + 1;
+    const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
+    if (p0 >= upto) return;
+    const int pn = upto - p0 < EX_TILE ? upto - p0 : EX_TILE;
+    for (int i = tid; i < pn * hd; i += 256) {
+        const int j = i / hd, d = i % hd;
+        ks[j * ks_stride + d] = kc[(size_t)(p0 + j) * kvd + (size_t)kvh * hd + d];
+    }
+    for (int i = tid; i < gqa * hd; i += 256)
+        qs[i] = q[(size_t)t * q_stride + (size_t)kvh * gqa * hd + i];
+    __syncthreads();
+    const float scale = fox_div(1.0f, fox_sqrtf((float)hd));
+    for (int i = tid; i < gqa * EX_TILE; i += 256) {
+        const int g = i / EX_TILE, j = i % EX_TILE;
+        if (j >= pn) continue;
+        const float *qr = qs + g * hd, *kr = ks + j * ks_stride;
+        float a = 0.0f;
+        for (int d = 0; d < hd; d++) a = a + qr[d] * kr[d];
+        att[((size_t)t * n_head + (size_t)kvh * gqa + g) * n_ctx + p0 + j] = a * scale;
+    }
+}
+
+__global__ __launch_bounds__(256) void attn_softmax_exact(float *__restrict__ att, int n_head,
+                                                          const uint32_t *__restrict__ pos,
+                                                          int n_ctx)
+{
+    extern __shared__ float e[];
+    __shared__ float red[4];
+    __shared__ float inv_s;
+    __shared__ int norm;
+    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
+    float *row = att + ((size_t)t * n_head + h) * n_ctx;
+    float m = -INFINITY;
+    for (int j = tid; j < upto; j += 256) m = fmaxf(m, row[j]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    // src/ops.c:26-30: the maximum in index order from x[0]; with no NaN
+    // this is the plain maximum
+    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int j = tid; j < upto; j += 256) e[j] = fox_expf(row[j] - mx);
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.0f;
+        int j = 0;
+        for (; j + 8 <= upto; j += 8) {
+            sum = sum + e[j];
+            sum = sum + e[j + 1];
+            sum = sum + e[j + 2];
+            sum = sum + e[j + 3];
+            sum = sum + e[j + 4];
+            sum = sum + e[j + 5];
+            sum = sum + e[j + 6];
+            sum = sum + e[j + 7];
+        }
+        for (; j < upto; j++) sum = sum + e[j];
+        norm = sum > 0.0f;
+        inv_s = norm ? fox_div(1.0f, sum) : 1.0f;
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    for (int j = tid; j < upto; j += 256) row[j] = norm ? e[j] * inv : e[j];
+}
+
+__global__ __launch_bounds__(64) void attn_values_exact(const float *__restrict__ att,
+                                                        const float *__restrict__ vc,
+                                                        int n_head, int n_head_kv, int hd,
+                                                        const uint32_t *__restrict__ pos,
+                                                        int n_ctx, float *__restrict__ out,
+                                                        size_t out_stride)
+{
+    const int h = blockIdx.x, t = blockIdx.y, d = blockIdx.z * 64 + threadIdx.x;
+    if (d >= hd) return;
+    const int gqa = n_head / n_head_kv, kvh = h / gqa, kvd = n_head_kv * hd;
+    const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
+    const float *a = att + ((size_t)t * n_head + h) * n_ctx;
+    const float *v = vc + (size_t)kvh * hd + d;
+    float acc = 0.0f;
+    int j = 0;
+    for (; j + 8 <= upto; j += 8) {
+        float vv[8], aa[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            vv[u] = v[(size_t)(j + u) * kvd];
+            aa[u] = a[j + u];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc = acc + aa[u] * vv[u];
+    }
+    for (; j < upto; j++) acc = acc + a[j] * v[(size_t)j * kvd];
+    out[(size_t)t * out_stride + (size_t)h * hd + d] = acc;
 }
 
 extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t out_stride,
                                             const float *q, size_t q_stride, const float *k_cache,
                                             const float *v_cache, size_t n_head, size_t n_head_kv,
                                             size_t head_dim, size_t M, const uint32_t *pos,
-                                            size_t n_ctx)
+                                            size_t n_ctx, int mode)
 {
     if (!ctx || !out || !q || !k_cache || !v_cache || !pos || n_head == 0 || n_head_kv == 0 ||
         head_dim == 0 || M == 0 || n_ctx == 0)
@@ -298,6 +435,33 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
                         "attention: at most %d query heads per kv head and head_dim %d",
                         ATT_MAXG, ATT_MAXHD);
     if (M > FOX_GPU_MAX_TOKENS) return fox_fail(FOX_GPU_ERR_ARG, "attention: too many tokens");
+    if (mode == FOX_GPU_ATTN_EXACT) {
+        const size_t bytes = M * n_head * n_ctx * sizeof(float);
+        if (n_ctx * sizeof(float) > 60 * 1024)
+            return fox_fail(FOX_GPU_ERR_UNSUPPORTED,
+                            "attention: exact mode keeps a head's %zu scores in LDS; at most "
+                            "15360 positions", n_ctx);
+        fox_gpu_status st = fox_ws_reserve(ctx, bytes);
+        if (st) return st;
+        float *att = (float *)ctx->ws;
+        const size_t qs = M > 1 ? q_stride : n_head * head_dim;
+        hipLaunchKernelGGL(attn_scores_exact,
+                           dim3((unsigned)((n_ctx + EX_TILE - 1) / EX_TILE), (unsigned)n_head_kv,
+                                (unsigned)M), dim3(256), 0, ctx->stream, q, qs, k_cache,
+                           (int)n_head, (int)n_head_kv, (int)head_dim, pos, (int)n_ctx, att);
+        FOX_LAUNCHED("attention scores");
+        hipLaunchKernelGGL(attn_softmax_exact, dim3((unsigned)n_head, (unsigned)M), dim3(256),
+                           n_ctx * sizeof(float), ctx->stream, att, (int)n_head, pos, (int)n_ctx);
+        FOX_LAUNCHED("attention softmax");
+        hipLaunchKernelGGL(attn_values_exact,
+                           dim3((unsigned)n_head, (unsigned)M, (unsigned)((head_dim + 63) / 64)),
+                           dim3(64), 0, ctx->stream, att, v_cache, (int)n_head, (int)n_head_kv,
+                           (int)head_dim, pos, (int)n_ctx, out,
+                           M > 1 ? out_stride : n_head * head_dim);
+        FOX_LAUNCHED("attention values");
+        return FOX_GPU_OK;
+    }
+    if (mode != FOX_GPU_ATTN_SPLIT) return fox_fail(FOX_GPU_ERR_ARG, "attention: unknown mode %d", mode);
     const int n_splits = (int)((n_ctx + ATT_SPLIT - 1) / ATT_SPLIT);
     const size_t bytes = M * n_head * (size_t)n_splits * (2 + head_dim) * sizeof(float);
     fox_gpu_status st = fox_ws_reserve(ctx, bytes);
@@ -323,7 +487,7 @@ __global__ void silu_mul_k(float *__restrict__ g, const float *__restrict__ u, i
     const int t = blockIdx.y;
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
         float x = g[(size_t)t * stride + i];
-        g[(size_t)t * stride + i] = x / (1.0f + expf(-x)) * u[(size_t)t * stride + i];
+        g[(size_t)t * stride + i] = fox_div(x, 1.0f + fox_expf(-x)) * u[(size_t)t * stride + i];
     }
 }
 
@@ -368,7 +532,8 @@ extern "C" fox_gpu_status fox_gpu_add(fox_gpu_ctx *ctx, float *dst, const float 
 // best starts at 0 and moves only on a strict '>'; a NaN at index 0 stays).
 __global__ __launch_bounds__(1024) void argmax_k(const float *__restrict__ x, int n,
                                                  uint32_t *__restrict__ idx,
-                                                 uint32_t *__restrict__ pos, uint32_t advance)
+                                                 uint32_t *__restrict__ pos, uint32_t advance,
+                                                 uint32_t *__restrict__ history)
 {
     __shared__ float bv[16];
     __shared__ int bi[16];
@@ -394,17 +559,21 @@ __global__ __launch_bounds__(1024) void argmax_k(const float *__restrict__ x, in
         float x0 = x[0];
         uint32_t r = (x0 != x0 || !(best > x0)) ? 0u : (uint32_t)bidx;
         *idx = r;
-        if (pos) *pos += advance;
+        if (pos) {
+            if (history) history[*pos] = r;
+            *pos += advance;
+        }
     }
 }
 
 extern "C" fox_gpu_status fox_gpu_argmax(fox_gpu_ctx *ctx, const float *logits, size_t n,
-                                         uint32_t *idx, uint32_t *pos, uint32_t advance)
+                                         uint32_t *idx, uint32_t *pos, uint32_t advance,
+                                         uint32_t *history)
 {
     if (!ctx || !logits || !idx || n == 0 || n > 0x7fffffff)
         return fox_fail(FOX_GPU_ERR_ARG, "argmax: bad argument");
     hipLaunchKernelGGL(argmax_k, dim3(1), dim3(1024), 0, ctx->stream, logits, (int)n, idx, pos,
-                       advance);
+                       advance, history);
     FOX_LAUNCHED("argmax");
     return FOX_GPU_OK;
 }
