@@ -1,0 +1,261 @@
+#!/usr/bin/env python3
+"""Decode throughput of the 4B-class TQ1_0 model on one MI355X.
+
+Prints one JSON line:
+  value      greedy decode tok/s of the 4B-class dense decoder (36 layers,
+             d_model 2560, 32/8 heads x 128, SwiGLU 9728, vocab 151936, TQ1_0
+             linear weights, f16 embedding and output), fully HBM-resident,
+             batch 1, KV cache pre-filled with 2048 positions of f16 N(0,1)
+             values; exact attention (logits bit-identical to RustFox's).
+  roofline   the TQ1_0 GEMV kernel (gemv_blocks, 14336 x 4096, one token):
+             algorithmic bytes per launch / its mean launch time from HIP
+             events on the stream it runs on, against 8 TB/s.
+  cpu_baseline  RustFox's own threadpool CPU path (compiled from its sources
+             into oracle/_ref) decoding the same model file on this host.
+
+A step is one token through all 36 layers, the output head and the greedy
+pick.  Inputs are resident in HBM before the timed region starts.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import rustfox_amd as rf  # noqa: E402
+from rustfox_amd import synth  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+PREFILL = 2048
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ decode
+
+def prefill_cache(ctx, spec, seed=11):
+    rng = np.random.default_rng([seed, 0xCAC4E])
+    kvd = spec.n_head_kv * spec.head_dim
+    for layer in range(spec.n_layer):
+        k = rng.standard_normal((PREFILL, kvd), dtype=np.float32).astype(np.float16)
+        v = rng.standard_normal((PREFILL, kvd), dtype=np.float32).astype(np.float16)
+        ctx.set_kv(layer, 0, k.astype(np.float32), v.astype(np.float32))
+    ctx.set_position(PREFILL)
+
+
+def time_decode(ctx, steps, warmup, exact):
+    ctx.set_attention(exact)
+    ctx.set_position(PREFILL)
+    tok = 1
+    if warmup:
+        tok = int(ctx.decode_greedy(tok, warmup)[-1])
+    t0 = time.perf_counter()
+    ids = ctx.decode_greedy(tok, steps)
+    dt = time.perf_counter() - t0
+    return dt, ids
+
+
+# --------------------------------------------------------------- GEMV bench
+
+def gemv_bytes(gtype, N, K, M):
+    """Algorithmic bytes of one launch: packed weights + int8 activations +
+    their scale(s) + f32 outputs."""
+    wb = N * synth.row_bytes(gtype, K)
+    return wb + M * K + 4 * M + 4 * M * N
+
+
+def gemv_case(gpu, gtype, N, K, M, rotate_bytes=1 << 30, min_launches=400):
+    rng = np.random.default_rng([N, K, gtype])
+    if gtype == rf.TQ1_0:
+        w = synth.tq1_random(rng, N * K // 256).reshape(-1)
+    else:
+        w = synth.tq2_random(rng, N * K // 256).reshape(-1)
+    n_copies = max(2, -(-rotate_bytes // w.nbytes))
+    ts = [gpu.tensor(gtype, K, N, w) for _ in range(n_copies)]
+    x = gpu.array(rng.standard_normal((M, K)).astype(np.float32))
+    out = gpu.empty((M, N), np.float32)
+    act = gpu.act_prepare(gtype, x, K, M)
+    for i in range(min(n_copies, 32)):
+        gpu.gemv_act(ts[i], act, out)
+    gpu.sync()
+    launches = max(min_launches, 2 * n_copies)
+    e0, e1 = gpu.event(), gpu.event()
+    gpu.record(e0)
+    for i in range(launches):
+        gpu.gemv_act(ts[i % n_copies], act, out)
+    gpu.record(e1)
+    ms = gpu.elapsed_ms(e0, e1)
+    gpu.act_free(act)
+    for t in ts:
+        t.free()
+    us = ms * 1e3 / launches
+    b = gemv_bytes(gtype, N, K, M)
+    return dict(type=synth.TYPE_NAMES[gtype], rows=N, cols=K, tokens=M, us_per_launch=round(us, 3),
+                bytes_per_launch=b, gbs=round(b / us / 1e3, 1),
+                frac_of_hbm=round(b / us / 1e3 / HBM_PEAK_GBS, 4), weight_copies=n_copies)
+
+
+# ------------------------------------------------------------ CPU baseline
+
+def cpu_threads():
+    n = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS")
+    if cap and cap.isdigit():
+        n = min(n, int(cap))
+    return max(1, min(n, 256))
+
+
+def cpu_baseline(path, spec, budget_s):
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from checkers import REF_FAST_SO, Ref  # test infrastructure: the reference
+    threads = cpu_threads()
+    if not os.path.exists(REF_FAST_SO):
+        return None
+    ref = Ref(REF_FAST_SO)
+    m = ref.open_model(path)
+    ctx = m.context(64, n_batch=32, n_threads=threads)
+    t0 = time.perf_counter()
+    ctx.eval(np.array([1], np.uint32))        # first touch loads the weights
+    load_s = time.perf_counter() - t0
+    times = []
+    tok = 2
+    t_start = time.perf_counter()
+    while len(times) < 16 and (time.perf_counter() - t_start) < budget_s:
+        lg = ctx.eval(np.array([tok], np.uint32))
+        times.append(ctx.last_seconds())
+        tok = int(np.argmax(lg))
+    ctx.close()
+    m.close()
+    med = statistics.median(times)
+    return {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": threads,
+            "kind": "reference",
+            "sample": (f"RustFox fox_eval (built from its sources, -O3 -march=x86-64-v3, "
+                       f"threadpool of {threads}) on the same 4B TQ1_0 GGUF, single-token "
+                       f"decode at positions 1..{len(times)} (its cache cannot be pre-filled, "
+                       f"so attention reads <= {len(times) + 1} rows instead of 2048+), median "
+                       f"of {len(times)} tokens; weight load {load_s:.1f} s excluded")}
+
+
+# --------------------------------------------------------------------- main
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-gemv", action="store_true")
+    ap.add_argument("--workdir", default=None)
+    a = ap.parse_args()
+
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported "
+              "(the sharded design is described in DESIGN.md, not built)", file=sys.stderr)
+        sys.exit(2)
+
+    spec = synth.spec("4b", n_ctx=PREFILL + a.warmup + a.steps)
+    workdir = a.workdir or tempfile.mkdtemp(prefix="foxbench-", dir="/tmp")
+    path = synth.path_in(workdir, spec)
+    t0 = time.perf_counter()
+    if not os.path.exists(path):
+        synth.write_gguf(path, spec)
+    log(f"bench: model file {path} ({os.path.getsize(path) / 1e9:.2f} GB) "
+        f"in {time.perf_counter() - t0:.1f} s")
+
+    t0 = time.perf_counter()
+    model = rf.Model(path, mode=rf.WEIGHTS_DEVICE)
+    ctx = model.context(spec.n_ctx, n_batch=8)
+    prefill_cache(ctx, spec)
+    log(f"bench: HBM load + cache prefill {time.perf_counter() - t0:.1f} s")
+
+    dt, ids = time_decode(ctx, a.steps, a.warmup, exact=True)
+    tok_s = a.steps / dt
+    log(f"bench: exact attention  {tok_s:.1f} tok/s ({dt * 1e3 / a.steps:.3f} ms/token)")
+    dt_split, ids_split = time_decode(ctx, a.steps, a.warmup, exact=False)
+    log(f"bench: split attention  {a.steps / dt_split:.1f} tok/s")
+    ctx.close()
+    model.close()
+
+    gemv = []
+    roof = None
+    if not a.no_gemv:
+        gpu = rf.Gpu(0)
+        for gtype in (rf.TQ1_0, rf.TQ2_0):
+            for (N, K) in ((4096, 4096), (14336, 4096)):
+                for M in (1, 8):
+                    r = gemv_case(gpu, gtype, N, K, M)
+                    gemv.append(r)
+                    log(f"bench: gemv {r['type']} {N}x{K} M={M}: {r['us_per_launch']} us, "
+                        f"{r['gbs']} GB/s ({100 * r['frac_of_hbm']:.1f}% of 8 TB/s)")
+        gpu.close()
+        main_case = [g for g in gemv if g["type"] == "TQ1_0" and g["rows"] == 14336
+                     and g["tokens"] == 1][0]
+        roof = {"bound": "hbm", "achieved": main_case["gbs"], "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(main_case["gbs"] / HBM_PEAK_GBS, 4),
+                "traffic": None,
+                "kernel": "gemv_blocks<TQ1_0>, 14336x4096, 1 token",
+                "bytes_per_launch": main_case["bytes_per_launch"],
+                "us_per_launch": main_case["us_per_launch"]}
+
+    cpu = None
+    if not a.no_cpu:
+        try:
+            cpu = cpu_baseline(path, spec, a.cpu_seconds)
+            if cpu:
+                log(f"bench: cpu reference {cpu['value']} tok/s on {cpu['cores']} threads")
+        except Exception as e:  # the GPU number stands without it
+            log(f"bench: cpu baseline failed: {e}")
+
+    if not a.workdir:
+        try:
+            os.remove(path)
+            os.rmdir(workdir)
+        except OSError:
+            pass
+
+    per_token_bytes = (766_402_560 + 777_912_320 + 747_520
+                       + 2 * spec.n_layer * (PREFILL + a.warmup + a.steps // 2)
+                       * spec.n_head_kv * spec.head_dim * 4)
+    line = {
+        "metric": "decode tok/s on 1 MI355X; quantized-GEMV HBM GB/s as % of peak",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(dt * 1e3 / a.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 x ternary (int32 block sums), f32 combine",
+        "data": "synthetic (seeded ternary weights, f16 N(0,0.02) embeddings, f16 N(0,1) cache)",
+        "config": {"workload": "4B-class dense decoder, TQ1_0, HBM-resident, batch 1, "
+                               "greedy decode after a 2048-position pre-filled cache",
+                   "layers": spec.n_layer, "d_model": spec.n_embd, "heads": spec.n_head,
+                   "kv_heads": spec.n_head_kv, "head_dim": spec.head_dim, "ffn": spec.n_ff,
+                   "vocab": spec.n_vocab, "kv_context": PREFILL, "kv_dtype": "f32",
+                   "attention": "exact (reference summation order)"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "split_attention_tok_s": round(a.steps / dt_split, 2),
+        "decode_hbm_gbs": round(per_token_bytes * tok_s / 1e9, 1),
+        "gemv": gemv,
+        "greedy_ids_head": [int(i) for i in ids[:8]],
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -148,6 +148,18 @@ fox_gpu_status fox_gpu_gemv_i8(fox_gpu_ctx *ctx, const fox_gpu_tensor *w,
 fox_gpu_status fox_gpu_block_sums(fox_gpu_ctx *ctx, const fox_gpu_tensor *w,
                                   const int8_t *q, size_t M, int32_t *sums);
 
+/* Prepared activations: x quantised once for one weight type and width, in
+ * its own device buffer, then applied to any number of matrices of that
+ * type and width with one kernel launch each (fox_gpu_gemv_act).  Block
+ * types only; F16/F32 matrices read float activations directly. */
+typedef struct fox_gpu_act fox_gpu_act;
+fox_gpu_status fox_gpu_act_prepare(fox_gpu_ctx *ctx, int type, const float *x, size_t K,
+                                   size_t M, size_t x_stride, fox_gpu_act **out);
+fox_gpu_status fox_gpu_gemv_act(fox_gpu_ctx *ctx, const fox_gpu_tensor *w,
+                                const fox_gpu_act *act, float *out, size_t out_stride,
+                                unsigned flags);
+void           fox_gpu_act_free(fox_gpu_ctx *ctx, fox_gpu_act *act);
+
 /* ---------------------------------------------------------------- ops */
 
 /* Rows of a tensor as f32 (fox_dequant_row, include/fox/fox.h:367-368):

@@ -73,6 +73,9 @@ def gpu_lib() -> C.CDLL:
                                C.POINTER(sz), C.c_uint],
         "fox_gpu_gemv_i8": [vp, vp, vp, vp, sz, vp, sz],
         "fox_gpu_block_sums": [vp, vp, vp, sz, vp],
+        "fox_gpu_act_prepare": [vp, C.c_int, vp, sz, sz, sz, C.POINTER(vp)],
+        "fox_gpu_gemv_act": [vp, vp, vp, vp, sz, C.c_uint],
+        "fox_gpu_act_free": [vp, vp],
         "fox_gpu_get_rows": [vp, vp, vp, sz, vp, sz, vp],
         "fox_gpu_rmsnorm": [vp, vp, sz, vp, sz, vp, sz, sz, C.c_float],
         "fox_gpu_rope_store": [vp, vp, sz, vp, sz, vp, sz, sz, sz, sz, sz, vp, vp, vp, sz,
@@ -93,7 +96,7 @@ def gpu_lib() -> C.CDLL:
     for name, args in sigs.items():
         f = getattr(L, name)
         f.argtypes = args
-        f.restype = None if name in ("fox_gpu_shutdown", "fox_gpu_tensor_free",
+        f.restype = None if name in ("fox_gpu_shutdown", "fox_gpu_tensor_free", "fox_gpu_act_free",
                                      "fox_gpu_graph_free", "fox_gpu_event_destroy") else C.c_int
     L.fox_gpu_last_error.restype = C.c_char_p
     L.fox_gpu_last_error.argtypes = []
@@ -250,6 +253,18 @@ class Gpu:
                 out_stride=None):
         _check(self.lib.fox_gpu_gemv_i8(self.ctx, w.h, q.ptr, scale.ptr, M, out.ptr,
                                         out_stride or w.ne1))
+
+    def act_prepare(self, gtype, x: DeviceArray, K, M, x_stride=None):
+        a = C.c_void_p()
+        _check(self.lib.fox_gpu_act_prepare(self.ctx, gtype, x.ptr, K, M, x_stride or K,
+                                            C.byref(a)))
+        return a.value
+
+    def gemv_act(self, w: Tensor, act, out: DeviceArray, out_stride=None, flags=0):
+        _check(self.lib.fox_gpu_gemv_act(self.ctx, w.h, act, out.ptr, out_stride or w.ne1, flags))
+
+    def act_free(self, act):
+        self.lib.fox_gpu_act_free(self.ctx, act)
 
     def block_sums(self, w: Tensor, q: DeviceArray, M, sums: DeviceArray):
         _check(self.lib.fox_gpu_block_sums(self.ctx, w.h, q.ptr, M, sums.ptr))

@@ -30,6 +30,7 @@
 #include "fox_internal.h"
 
 #include <cstring>
+#include <new>
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
@@ -674,20 +675,29 @@ struct Ws {
     int32_t *aux;
 };
 
-static fox_gpu_status carve(fox_gpu_ctx *ctx, int fmt, size_t K, size_t M, Ws *w)
+// layout of the activation buffers of one format; returns the byte count
+static size_t act_layout(int fmt, size_t K, size_t M, uint8_t *base, Ws *w)
 {
     const size_t nb = K / 256;
     size_t off = 0, oq, os, ob, oa;
     oq = off; off = align_up(off + M * K, 256);
-    os = off; off = align_up(off + M * nb * 4, 256);
+    os = off; off = align_up(off + M * (nb ? nb : 1) * 4, 256);
     ob = off; off = align_up(off + nb * M * (size_t)b_bytes_per_block_tok(fmt), 256);
     oa = off; off = align_up(off + nb * M * (size_t)aux_per_block_tok(fmt) * 4, 256);
-    fox_gpu_status st = fox_ws_reserve(ctx, off);
+    if (w) {
+        w->q = (int8_t *)(base + oq);
+        w->scale = (float *)(base + os);
+        w->B = base + ob;
+        w->aux = (int32_t *)(base + oa);
+    }
+    return off;
+}
+
+static fox_gpu_status carve(fox_gpu_ctx *ctx, int fmt, size_t K, size_t M, Ws *w)
+{
+    fox_gpu_status st = fox_ws_reserve(ctx, act_layout(fmt, K, M, nullptr, nullptr));
     if (st) return st;
-    w->q = (int8_t *)(ctx->ws + oq);
-    w->scale = (float *)(ctx->ws + os);
-    w->B = ctx->ws + ob;
-    w->aux = (int32_t *)(ctx->ws + oa);
+    act_layout(fmt, K, M, ctx->ws, w);
     return FOX_GPU_OK;
 }
 
@@ -719,6 +729,38 @@ static fox_gpu_status launch_prep(fox_gpu_ctx *ctx, int fmt, const float *x, siz
         break;
     }
     FOX_LAUNCHED("act_prep");
+    return FOX_GPU_OK;
+}
+
+static fox_gpu_status launch_blocks(fox_gpu_ctx *ctx, int fmt, const Segs &sg, int tiles,
+                                    int nb, int M, const Ws &w, unsigned flags, int32_t *sums)
+{
+    const int T = terms_per_block(fmt);
+    int chunk_blocks = (int)(65536 / ((size_t)T * 16 * M * 4));
+    chunk_blocks = chunk_blocks / WAVES * WAVES;
+    if (chunk_blocks < WAVES) chunk_blocks = WAVES;
+    if (chunk_blocks > nb) chunk_blocks = nb;
+    size_t lds = sums ? 0 : (size_t)chunk_blocks * T * 16 * M * 4;
+    dim3 grid((unsigned)tiles), block(WG);
+    switch (fmt) {
+    case FMT_TQ1:
+        hipLaunchKernelGGL(gemv_blocks<FMT_TQ1>, grid, block, lds, ctx->stream, sg, nb, M,
+                           chunk_blocks, w.B, w.aux, w.scale, flags, sums);
+        break;
+    case FMT_TQ2:
+        hipLaunchKernelGGL(gemv_blocks<FMT_TQ2>, grid, block, lds, ctx->stream, sg, nb, M,
+                           chunk_blocks, w.B, w.aux, w.scale, flags, sums);
+        break;
+    case FMT_Q4K:
+        hipLaunchKernelGGL(gemv_blocks<FMT_Q4K>, grid, block, lds, ctx->stream, sg, nb, M,
+                           chunk_blocks, w.B, w.aux, w.scale, flags, sums);
+        break;
+    default:
+        hipLaunchKernelGGL(gemv_blocks<FMT_Q6K>, grid, block, lds, ctx->stream, sg, nb, M,
+                           chunk_blocks, w.B, w.aux, w.scale, flags, sums);
+        break;
+    }
+    FOX_LAUNCHED("gemv_blocks");
     return FOX_GPU_OK;
 }
 
@@ -810,35 +852,7 @@ fox_gpu_status fox_gemv_launch(fox_gpu_ctx *ctx, size_t n, const fox_gpu_tensor 
         tiles += (int)ws[i]->n_tiles;
     }
     sg.tile_start[n] = tiles;
-
-    const int nb = (int)(K / 256);
-    const int T = terms_per_block(fmt);
-    int chunk_blocks = (int)(65536 / ((size_t)T * 16 * M * 4));
-    chunk_blocks = chunk_blocks / WAVES * WAVES;
-    if (chunk_blocks < WAVES) chunk_blocks = WAVES;
-    if (chunk_blocks > nb) chunk_blocks = nb;
-    size_t lds = sums ? 0 : (size_t)chunk_blocks * T * 16 * M * 4;
-    dim3 grid((unsigned)tiles), block(WG);
-    switch (fmt) {
-    case FMT_TQ1:
-        hipLaunchKernelGGL(gemv_blocks<FMT_TQ1>, grid, block, lds, ctx->stream, sg, nb, (int)M,
-                           chunk_blocks, w.B, w.aux, w.scale, flags, sums);
-        break;
-    case FMT_TQ2:
-        hipLaunchKernelGGL(gemv_blocks<FMT_TQ2>, grid, block, lds, ctx->stream, sg, nb, (int)M,
-                           chunk_blocks, w.B, w.aux, w.scale, flags, sums);
-        break;
-    case FMT_Q4K:
-        hipLaunchKernelGGL(gemv_blocks<FMT_Q4K>, grid, block, lds, ctx->stream, sg, nb, (int)M,
-                           chunk_blocks, w.B, w.aux, w.scale, flags, sums);
-        break;
-    default:
-        hipLaunchKernelGGL(gemv_blocks<FMT_Q6K>, grid, block, lds, ctx->stream, sg, nb, (int)M,
-                           chunk_blocks, w.B, w.aux, w.scale, flags, sums);
-        break;
-    }
-    FOX_LAUNCHED("gemv_blocks");
-    return FOX_GPU_OK;
+    return launch_blocks(ctx, fmt, sg, tiles, (int)(K / 256), (int)M, w, flags, sums);
 }
 
 // ----------------------------------------------------------- C entries
@@ -911,4 +925,80 @@ extern "C" fox_gpu_status fox_gpu_block_sums(fox_gpu_ctx *ctx, const fox_gpu_ten
                         fox_type_name(w->type));
     const fox_gpu_tensor *ws[1] = {w};
     return fox_gemv_launch(ctx, 1, ws, nullptr, 0, q, nullptr, M, nullptr, nullptr, 0, sums);
+}
+
+// ------------------------------------------------------ prepared activations
+
+struct fox_gpu_act {
+    int fmt, type;
+    size_t K, M;
+    uint8_t *buf;
+    Ws w;
+};
+
+extern "C" fox_gpu_status fox_gpu_act_prepare(fox_gpu_ctx *ctx, int type, const float *x,
+                                              size_t K, size_t M, size_t x_stride,
+                                              fox_gpu_act **out)
+{
+    if (!ctx || !x || !out || K == 0 || M == 0)
+        return fox_fail(FOX_GPU_ERR_ARG, "act_prepare: bad argument");
+    *out = nullptr;
+    const int fmt = fmt_of(type);
+    if (fmt < 0)
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "act_prepare: %s weights read float "
+                        "activations directly", fox_type_name(type));
+    if (K % 256) return fox_fail(FOX_GPU_ERR_ARG, "act_prepare: K %% 256 != 0");
+    if (M > FOX_GPU_MAX_TOKENS) return fox_fail(FOX_GPU_ERR_ARG, "act_prepare: too many tokens");
+    if (M > 1 && x_stride < K) return fox_fail(FOX_GPU_ERR_ARG, "act_prepare: stride < K");
+    fox_gpu_act *a = new (std::nothrow) fox_gpu_act();
+    if (!a) return fox_fail(FOX_GPU_ERR_NOMEM, "act_prepare: handle");
+    a->fmt = fmt;
+    a->type = type;
+    a->K = K;
+    a->M = M;
+    hipError_t e = hipMalloc(&a->buf, act_layout(fmt, K, M, nullptr, nullptr));
+    if (e != hipSuccess) {
+        delete a;
+        return fox_hip_fail(e, "act_prepare: buffer");
+    }
+    act_layout(fmt, K, M, a->buf, &a->w);
+    fox_gpu_status st = launch_prep(ctx, fmt, x, M > 1 ? x_stride : K, nullptr, nullptr, K, M,
+                                    a->w, a->w.q, a->w.scale);
+    if (st) {
+        fox_gpu_act_free(ctx, a);
+        return st;
+    }
+    *out = a;
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_gemv_act(fox_gpu_ctx *ctx, const fox_gpu_tensor *w,
+                                           const fox_gpu_act *act, float *out,
+                                           size_t out_stride, unsigned flags)
+{
+    if (!ctx || !w || !act || !out) return fox_fail(FOX_GPU_ERR_ARG, "gemv_act: bad argument");
+    if (w->type != act->type || w->ne0 != act->K)
+        return fox_fail(FOX_GPU_ERR_ARG, "gemv_act: activations were prepared for %s K=%zu, "
+                        "the matrix is %s K=%llu", fox_type_name(act->type), act->K,
+                        fox_type_name(w->type), (unsigned long long)w->ne0);
+    if (act->M > 1 && out_stride < w->ne1)
+        return fox_fail(FOX_GPU_ERR_ARG, "gemv_act: output stride < rows");
+    Segs sg;
+    memset(&sg, 0, sizeof(sg));
+    sg.n = 1;
+    sg.w[0] = w->d;
+    sg.out[0] = out;
+    sg.out_stride[0] = act->M > 1 ? (int)out_stride : (int)w->ne1;
+    sg.n_rows[0] = (int)w->ne1;
+    sg.tile_start[1] = (int)w->n_tiles;
+    return launch_blocks(ctx, act->fmt, sg, (int)w->n_tiles, (int)(act->K / 256), (int)act->M,
+                         act->w, flags, nullptr);
+}
+
+extern "C" void fox_gpu_act_free(fox_gpu_ctx *ctx, fox_gpu_act *a)
+{
+    if (!a) return;
+    if (ctx) (void)hipSetDevice(ctx->device);
+    if (a->buf) (void)hipFree(a->buf);
+    delete a;
 }

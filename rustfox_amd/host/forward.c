@@ -41,6 +41,7 @@ struct fox_context {
     float *x, *xb, *q, *k, *v, *hb, *hb2, *dlogits;
     float *kc, *vc, *rc, *rs;
     uint32_t *dtok, *dpos, *dhist, *dzero;
+    float *norms;                  /* all norm vectors, n_embd floats each */
     float *logits;                 /* host */
     double last_seconds;
     uint64_t reads_at_start;
@@ -104,13 +105,11 @@ void fox_context_destroy(fox_context *c)
     free(c);
 }
 
-/* device f32 copy of a norm vector (src/forward.c:248-267 dequantises it per
- * use; it never changes, so it is dequantised once) */
-static fox_status norm_vector(fox_context *c, size_t idx, float **out)
+/* device f32 copy of a norm vector into `dst` (src/forward.c:248-267
+ * dequantises it per use; it never changes, so it is dequantised once) */
+static fox_status norm_vector(fox_context *c, size_t idx, float *dst)
 {
-    fox_status st = dalloc(c, c->d * sizeof(float), (void **)out);
-    if (st != FOX_OK) return st;
-    GPU(fox_gpu_get_rows(c->gpu, dev_tensor(c->m, idx), c->dzero, 1, *out, c->d, NULL),
+    GPU(fox_gpu_get_rows(c->gpu, dev_tensor(c->m, idx), c->dzero, 1, dst, c->d, NULL),
         "context: norm weights");
     return FOX_OK;
 }
@@ -180,6 +179,7 @@ fox_status fox_context_create(fox_model *m, const fox_context_config *cfg, fox_c
     ALLOC(c->dpos, 4)
     ALLOC(c->dhist, (size_t)k.n_ctx * 4)
     ALLOC(c->dzero, 4)
+    ALLOC(c->norms, (2 * (size_t)mi->n_layer + 1) * c->d * 4)
 #undef ALLOC
     if (fox_gpu_memcpy_h2d(c->gpu, c->dzero, &zero, 4) != FOX_GPU_OK ||
         fox_gpu_memset(c->gpu, c->kc, 0, (size_t)mi->n_layer * k.n_ctx * c->nkv * 4) != FOX_GPU_OK ||
@@ -225,13 +225,16 @@ fox_status fox_context_create(fox_model *m, const fox_context_config *cfg, fox_c
         D->ffn_gate = dev_tensor(m, t->ffn_gate);
         D->ffn_up = dev_tensor(m, t->ffn_up);
         D->ffn_down = dev_tensor(m, t->ffn_down);
-        if ((st = norm_vector(c, t->attn_norm, &D->attn_norm)) != FOX_OK ||
-            (st = norm_vector(c, t->ffn_norm, &D->ffn_norm)) != FOX_OK) {
+        D->attn_norm = c->norms + (2 * (size_t)l) * c->d;
+        D->ffn_norm = c->norms + (2 * (size_t)l + 1) * c->d;
+        if ((st = norm_vector(c, t->attn_norm, D->attn_norm)) != FOX_OK ||
+            (st = norm_vector(c, t->ffn_norm, D->ffn_norm)) != FOX_OK) {
             fox_context_destroy(c);
             return st;
         }
     }
-    if ((st = norm_vector(c, m->output_norm, &c->out_norm)) != FOX_OK) {
+    c->out_norm = c->norms + 2 * (size_t)mi->n_layer * c->d;
+    if ((st = norm_vector(c, m->output_norm, c->out_norm)) != FOX_OK) {
         fox_context_destroy(c);
         return st;
     }
@@ -397,8 +400,20 @@ fox_status fox_decode_greedy(fox_context *c, uint32_t token, size_t n_steps, uin
     GPU(fox_gpu_memcpy_h2d(c->gpu, c->dtok, &token, 4), "decode: token");
     GPU(fox_gpu_memcpy_h2d(c->gpu, c->dpos, &c->pos, 4), "decode: position");
     /* the first step runs eagerly (it also sizes every workspace), the rest
-     * replay one captured graph */
+     * replay one captured graph; FOX_GRAPHS=0 keeps every step eager (for
+     * profilers that cannot follow graph launches) */
     if ((st = greedy_step(c)) != FOX_OK) return st;
+    {
+        const char *e = getenv("FOX_GRAPHS");
+        if (e && strcmp(e, "0") == 0) {
+            for (s = 1; s < n_steps; s++)
+                if ((st = greedy_step(c)) != FOX_OK) return st;
+            GPU(fox_gpu_memcpy_d2h(c->gpu, out_ids, c->dhist + c->pos, n_steps * 4), "decode: ids");
+            c->pos += (uint32_t)n_steps;
+            c->last_seconds = now_s() - t0;
+            return FOX_OK;
+        }
+    }
     if (n_steps > 1 && !c->greedy) {
         GPU(fox_gpu_graph_begin(c->gpu), "decode: capture");
         st = greedy_step(c);

@@ -66,6 +66,10 @@ class Oracle:
         L.or_tq1_block_sum.restype = C.c_int32
         L.or_tq2_block_sum.argtypes = [_i8p, _u8p]
         L.or_tq2_block_sum.restype = C.c_int32
+        L.or_q4k_block_sums.argtypes = [_i8p, _u8p, C.c_void_p, C.c_void_p]
+        L.or_q4k_block_sums.restype = None
+        L.or_q6k_block_sums.argtypes = [_i8p, _u8p, C.c_void_p]
+        L.or_q6k_block_sums.restype = None
         L.or_block_sums.argtypes = [C.c_int, _i8p, _u8p, C.c_size_t, C.c_size_t, _i32p]
         L.or_gemv_tq_i8.argtypes = [C.c_int, _i8p, C.c_float, _u8p, C.c_size_t,
                                     C.c_size_t, _f32p]
