@@ -179,8 +179,14 @@ fox_gpu_status fox_gpu_rmsnorm(fox_gpu_ctx *ctx, float *out, size_t out_stride,
 /* RoPE on q (n_head heads) and k (n_head_kv heads) of M tokens at positions
  * pos[0] + t, adjacent pairs (src/ops.c:56-73) with the host-built tables
  * (src/forward.c:104-118), then k and v rows stored into the layer's cache
- * rows pos[0] + t (src/forward.c:427-443).  Caches are f32 [n_ctx][kv_dim];
- * a token whose position is not below n_ctx is neither rotated nor stored. */
+ * rows pos[0] + t (src/forward.c:427-443).  A token whose position is not
+ * below n_ctx is neither rotated nor stored.
+ *
+ * Cache layout: k_cache is f32 [n_ctx][kv_dim] (the reference's); v_cache is
+ * position-quad interleaved, element (p, c) at ((p/4)*kv_dim + c)*4 + p%4,
+ * and holds FOX_GPU_V_CACHE_FLOATS(n_ctx, kv_dim) floats.  Four consecutive
+ * positions of a column are one 16-byte load for the value sums. */
+#define FOX_GPU_V_CACHE_FLOATS(n_ctx, kv_dim) ((((size_t)(n_ctx) + 3) / 4) * 4 * (size_t)(kv_dim))
 fox_gpu_status fox_gpu_rope_store(fox_gpu_ctx *ctx, float *q, size_t q_stride,
                                   float *k, size_t k_stride,
                                   const float *v, size_t v_stride,
@@ -188,6 +194,13 @@ fox_gpu_status fox_gpu_rope_store(fox_gpu_ctx *ctx, float *q, size_t q_stride,
                                   size_t M, const float *cos_t, const float *sin_t,
                                   const uint32_t *pos, size_t n_ctx,
                                   float *k_cache, float *v_cache);
+
+/* Rows p0 .. p0+n-1 of a layer's caches from device row-major k, v
+ * [n][kv_dim] (pre-filling a cache; src/forward.c:427-443 stores rows one
+ * token at a time). */
+fox_gpu_status fox_gpu_kv_write(fox_gpu_ctx *ctx, float *k_cache, float *v_cache,
+                                size_t kv_dim, size_t n_ctx, size_t p0, size_t n,
+                                const float *k, const float *v);
 
 /* Causal GQA attention of M tokens at positions pos[0] + t over cache rows
  * 0 .. pos[0] + t: softmax(q.k / sqrt(hd)) v (src/forward.c:303-338).

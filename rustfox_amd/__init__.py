@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import weakref
 
 import numpy as np
 
@@ -81,6 +82,7 @@ def gpu_lib() -> C.CDLL:
         "fox_gpu_rope_store": [vp, vp, sz, vp, sz, vp, sz, sz, sz, sz, sz, vp, vp, vp, sz,
                                vp, vp],
         "fox_gpu_attention": [vp, vp, sz, vp, sz, vp, vp, sz, sz, sz, sz, vp, sz, C.c_int],
+        "fox_gpu_kv_write": [vp, vp, vp, sz, sz, sz, sz, vp, vp],
         "fox_gpu_silu_mul": [vp, vp, vp, sz, sz, sz],
         "fox_gpu_add": [vp, vp, vp, sz, sz, sz],
         "fox_gpu_argmax": [vp, vp, sz, vp, vp, C.c_uint32, vp],
@@ -269,6 +271,19 @@ class Gpu:
     def block_sums(self, w: Tensor, q: DeviceArray, M, sums: DeviceArray):
         _check(self.lib.fox_gpu_block_sums(self.ctx, w.h, q.ptr, M, sums.ptr))
 
+    def kv_write(self, kc: DeviceArray, vc: DeviceArray, kv_dim, n_ctx, p0, k: DeviceArray,
+                 v: DeviceArray, n):
+        _check(self.lib.fox_gpu_kv_write(self.ctx, kc.ptr, vc.ptr, kv_dim, n_ctx, p0, n, k.ptr,
+                                         v.ptr))
+
+    def attention(self, out: DeviceArray, q: DeviceArray, kc: DeviceArray, vc: DeviceArray,
+                  n_head, n_head_kv, head_dim, M, pos: DeviceArray, n_ctx, mode,
+                  q_stride=None, out_stride=None):
+        w = n_head * head_dim
+        _check(self.lib.fox_gpu_attention(self.ctx, out.ptr, out_stride or w, q.ptr,
+                                          q_stride or w, kc.ptr, vc.ptr, n_head, n_head_kv,
+                                          head_dim, M, pos.ptr, n_ctx, mode))
+
     def event(self):
         e = C.c_void_p()
         _check(self.lib.fox_gpu_event_create(self.ctx, C.byref(e)))
@@ -395,14 +410,22 @@ class Model:
         _hcheck(self.lib.fox_model_open(path.encode(), mode, budget, C.byref(m)))
         self.m = m.value
         self.info = self.lib.fox_model_get_info(self.m).contents
+        self._contexts = weakref.WeakSet()
 
     def context(self, n_ctx: int = 0, n_batch: int = 32) -> "Context":
-        return Context(self, n_ctx, n_batch)
+        c = Context(self, n_ctx, n_batch)
+        self._contexts.add(c)
+        return c
 
     def weights(self):
         return self.lib.fox_model_weights(self.m)
 
     def close(self):
+        """Destroys the model's live contexts first: a context uses the
+        model's device and weights (fox_context_destroy after fox_model_close
+        would touch freed memory)."""
+        for c in list(self._contexts):
+            c.close()
         if self.m:
             self.lib.fox_model_close(self.m)
             self.m = None

@@ -124,6 +124,15 @@ extern "C" fox_gpu_status fox_gpu_rmsnorm(fox_gpu_ctx *ctx, float *out, size_t o
 
 // ------------------------------------------------------------ rope+store
 
+// Cache layout.  K rows are f32 [n_ctx][kv_dim] as in the reference.  V is
+// position-quad interleaved: element (p, c) at ((p / 4) * kv_dim + c) * 4 +
+// p % 4, so four consecutive positions of one column are one 16-byte load
+// (the value sums walk positions in order, one column per lane).
+__device__ __forceinline__ size_t vq_index(size_t p, size_t c, size_t kvd)
+{
+    return ((p >> 2) * kvd + c) * 4 + (p & 3);
+}
+
 // src/ops.c:56-73 on q and k of token t at position pos[0]+t, then the
 // src/forward.c:427-443 copies of k and v into cache row pos[0]+t.
 __global__ void rope_store_k(float *__restrict__ q, size_t q_stride, float *__restrict__ k,
@@ -153,7 +162,7 @@ __global__ void rope_store_k(float *__restrict__ q, size_t q_stride, float *__re
     const int kvd = n_head_kv * hd;
     for (int i = threadIdx.x; i < kvd; i += blockDim.x) {
         kc[p * kvd + i] = kt[i];
-        vc[p * kvd + i] = vt[i];
+        vc[vq_index(p, (size_t)i, (size_t)kvd)] = vt[i];
     }
 }
 
@@ -176,8 +185,34 @@ extern "C" fox_gpu_status fox_gpu_rope_store(fox_gpu_ctx *ctx, float *q, size_t 
     return FOX_GPU_OK;
 }
 
-// -------------------------------------------------------------- attention
+// rows p0 .. p0+n-1 of both caches from row-major [n][kv_dim] k and v
+__global__ void kv_write_k(float *__restrict__ kc, float *__restrict__ vc, int kvd, size_t p0,
+                           const float *__restrict__ k, const float *__restrict__ v)
+{
+    const size_t i = blockIdx.x, p = p0 + i;
+    for (int c = threadIdx.x; c < kvd; c += blockDim.x) {
+        kc[p * kvd + c] = k[i * kvd + c];
+        vc[vq_index(p, (size_t)c, (size_t)kvd)] = v[i * kvd + c];
+    }
+}
 
+extern "C" fox_gpu_status fox_gpu_kv_write(fox_gpu_ctx *ctx, float *k_cache, float *v_cache,
+                                           size_t kv_dim, size_t n_ctx, size_t p0, size_t n,
+                                           const float *k, const float *v)
+{
+    if (!ctx || !k_cache || !v_cache || !k || !v || kv_dim == 0 || n == 0)
+        return fox_fail(FOX_GPU_ERR_ARG, "kv_write: bad argument");
+    if (p0 + n > n_ctx || n > 0x7fffffff)
+        return fox_fail(FOX_GPU_ERR_ARG, "kv_write: rows %zu..%zu outside the %zu-row cache", p0,
+                        p0 + n, n_ctx);
+    hipLaunchKernelGGL(kv_write_k, dim3((unsigned)n), dim3(256), 0, ctx->stream, k_cache, v_cache,
+                       (int)kv_dim, p0, k, v);
+    FOX_LAUNCHED("kv_write");
+    return FOX_GPU_OK;
+}
+
+// -------------------------------------------------------------- attention
+//
 #define ATT_SPLIT 32   // cache rows per workgroup
 #define ATT_MAXG 8     // query heads per kv head handled by one workgroup
 #define ATT_MAXHD 256
@@ -262,12 +297,13 @@ __global__ __launch_bounds__(256) void attn_partial(const float *__restrict__ q,
         }
     }
     __syncthreads();
-    // o = sum_p e_p v_p, one (head, dim) per thread, rows read coalesced in d
+    // o = sum_p e_p v_p, one (head, dim) per thread
     for (int i = tid; i < gqa * hd; i += 256) {
         const int g = i / hd, d = i % hd;
+        const size_t c = (size_t)kvh * hd + d;
         float o = 0.0f;
         for (int pp = 0; pp < pn; pp++)
-            o += sc[g * ATT_SPLIT + pp] * vc[(size_t)(p0 + pp) * kvd + (size_t)kvh * hd + d];
+            o += sc[g * ATT_SPLIT + pp] * vc[vq_index((size_t)(p0 + pp), c, (size_t)kvd)];
         float *r = base + (size_t)g * n_splits * rec;
         if (d == 0) {
             r[0] = st_m[g];
@@ -302,83 +338,121 @@ __global__ void attn_merge(const float *__restrict__ part, int n_head, int hd, i
     }
 }
 
-
-// ---- attention in the reference's order (src/forward.c:303-338,
-// src/ops.c:24-39, 75-81), bit for bit:
+// ---- attention in the reference's order (src/forward.c:222-257,
+// src/ops.c:24-39), bit for bit:
 //   score_j = (sum_d q_d k_jd, summed in d order) * (1 / sqrtf(hd));
 //   softmax: max, e_j = expf(score_j - max), sum in j order, e_j * (1/sum);
 //   out_d = sum in j order of a_j v_jd.
-// Each in-order sum is one lane's chain; work is spread over lanes by
-// position (scores), head (softmax) and head x dimension (values).
+// Each in-order sum is one lane's chain.  Three kernels: scores (a lane per
+// position, K tile in LDS) with per-tile maxima; softmax (one lane runs the
+// position-order sum from LDS); values (a lane per output column, walking
+// the interleaved V and the weights four positions per load).
 
-#define EX_TILE 32
+#define SC_TILE 64
 
-__global__ __launch_bounds__(256) void attn_scores_exact(const float *__restrict__ q,
-                                                         size_t q_stride,
-                                                         const float *__restrict__ kc,
-                                                         int n_head, int n_head_kv, int hd,
-                                                         const uint32_t *__restrict__ pos,
-                                                         int n_ctx, float *__restrict__ att)
+__global__ __launch_bounds__(256) void attn_scores_x(const float *__restrict__ q,
+                                                     size_t q_stride,
+                                                     const float *__restrict__ kc, int n_head,
+                                                     int n_head_kv, int hd,
+                                                     const uint32_t *__restrict__ pos,
+                                                     int n_ctx, size_t att_stride,
+                                                     float *__restrict__ att,
+                                                     float *__restrict__ tmax, int n_tiles)
 {
-    __shared__ float ks[EX_TILE * (ATT_MAXHD + 1)];
-    __shared__ float qs[ATT_MAXG * ATT_MAXHD];
-    const int p0 = blockIdx.x * EX_TILE, kvh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
-    const int gqa = n_head / n_head_kv, kvd = n_head_kv * hd, ks_stride = hd + 1;
+    extern __shared__ float4 lds4[];
+    float *ks = (float *)lds4;                      // [SC_TILE][hd + 4]
+    const int ks_str = hd + 4;
+    float *qs = ks + SC_TILE * ks_str;              // [gqa][hd]
+    const int tile = blockIdx.x, p0 = tile * SC_TILE, kvh = blockIdx.y, t = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int gqa = n_head / n_head_kv, kvd = n_head_kv * hd, nv = hd >> 2;
     const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
     if (p0 >= upto) return;
-    const int pn = upto - p0 < EX_TILE ? upto - p0 : EX_TILE;
-    for (int i = tid; i < pn * hd; i += 256) {
-        const int j = i / hd, d = i % hd;
-        ks[j * ks_stride + d] = kc[(size_t)(p0 + j) * kvd + (size_t)kvh * hd + d];
+    const int pn = upto - p0 < SC_TILE ? upto - p0 : SC_TILE;
+    for (int i = tid; i < pn * nv; i += 256) {
+        const int j = i / nv, c = i - j * nv;
+        const float4 v = *(const float4 *)(kc + (size_t)(p0 + j) * kvd + (size_t)kvh * hd + 4 * c);
+        *(float4 *)(ks + j * ks_str + 4 * c) = v;
     }
-    for (int i = tid; i < gqa * hd; i += 256)
-        qs[i] = q[(size_t)t * q_stride + (size_t)kvh * gqa * hd + i];
+    for (int i = tid; i < gqa * nv; i += 256)
+        *(float4 *)(qs + 4 * i) =
+            *(const float4 *)(q + (size_t)t * q_stride + (size_t)kvh * gqa * hd + 4 * i);
     __syncthreads();
     const float scale = fox_div(1.0f, fox_sqrtf((float)hd));
-    for (int i = tid; i < gqa * EX_TILE; i += 256) {
-        const int g = i / EX_TILE, j = i % EX_TILE;
-        if (j >= pn) continue;
-        const float *qr = qs + g * hd, *kr = ks + j * ks_stride;
+    const bool ok = lane < pn;
+    const float *kr = ks + (ok ? lane : 0) * ks_str;
+    for (int g = wave; g < gqa; g += 4) {
+        const float *qr = qs + g * hd;
         float a = 0.0f;
-        for (int d = 0; d < hd; d++) a = a + qr[d] * kr[d];
-        att[((size_t)t * n_head + (size_t)kvh * gqa + g) * n_ctx + p0 + j] = a * scale;
+        for (int d = 0; d < hd; d += 4) {
+            const float4 qv = *(const float4 *)(qr + d);
+            const float4 kv = *(const float4 *)(kr + d);
+            a = a + qv.x * kv.x;
+            a = a + qv.y * kv.y;
+            a = a + qv.z * kv.z;
+            a = a + qv.w * kv.w;
+        }
+        const float s = a * scale;
+        const int h = kvh * gqa + g;
+        if (ok) att[((size_t)t * n_head + h) * att_stride + p0 + lane] = s;
+        // tile maximum, NaN never taken
+        float m = (ok && s == s) ? s : -INFINITY;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float w = __shfl_xor(m, o);
+            m = w > m ? w : m;
+        }
+        if (lane == 0) tmax[((size_t)t * n_head + h) * n_tiles + tile] = m;
     }
 }
 
-__global__ __launch_bounds__(256) void attn_softmax_exact(float *__restrict__ att, int n_head,
-                                                          const uint32_t *__restrict__ pos,
-                                                          int n_ctx)
+__global__ __launch_bounds__(256) void attn_softmax_x(float *__restrict__ att,
+                                                      size_t att_stride,
+                                                      const float *__restrict__ tmax,
+                                                      int n_tiles, int n_head,
+                                                      const uint32_t *__restrict__ pos,
+                                                      int n_ctx)
 {
-    extern __shared__ float e[];
+    extern __shared__ float4 e4[];
+    float *e = (float *)e4;
     __shared__ float red[4];
     __shared__ float inv_s;
     __shared__ int norm;
     const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
     const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
-    float *row = att + ((size_t)t * n_head + h) * n_ctx;
+    const int used = (upto + SC_TILE - 1) / SC_TILE;
+    float *row = att + ((size_t)t * n_head + h) * att_stride;
+    const float *tm = tmax + ((size_t)t * n_head + h) * n_tiles;
     float m = -INFINITY;
-    for (int j = tid; j < upto; j += 256) m = fmaxf(m, row[j]);
+    for (int i = tid; i < used; i += 256) {
+        const float v = tm[i];
+        m = v > m ? v : m;
+    }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    for (int o = 32; o > 0; o >>= 1) {
+        const float w = __shfl_xor(m, o);
+        m = w > m ? w : m;
+    }
     if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
-    // src/ops.c:26-30: the maximum in index order from x[0]; with no NaN
-    // this is the plain maximum
-    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // src/ops.c:26-30: max starts at x[0] and moves on a strict '>', so a
+    // NaN first score stays the maximum; otherwise NaNs are skipped
+    float mx = red[0];
+    for (int w = 1; w < 4; w++) mx = red[w] > mx ? red[w] : mx;
+    const float s0 = row[0];
+    if (s0 != s0) mx = s0;
     for (int j = tid; j < upto; j += 256) e[j] = fox_expf(row[j] - mx);
     __syncthreads();
     if (tid == 0) {
         float sum = 0.0f;
         int j = 0;
-        for (; j + 8 <= upto; j += 8) {
-            sum = sum + e[j];
-            sum = sum + e[j + 1];
-            sum = sum + e[j + 2];
-            sum = sum + e[j + 3];
-            sum = sum + e[j + 4];
-            sum = sum + e[j + 5];
-            sum = sum + e[j + 6];
-            sum = sum + e[j + 7];
+        for (; j + 16 <= upto; j += 16) {
+            const float4 a = *(const float4 *)(e + j), b = *(const float4 *)(e + j + 4);
+            const float4 c = *(const float4 *)(e + j + 8), d = *(const float4 *)(e + j + 12);
+            sum = sum + a.x; sum = sum + a.y; sum = sum + a.z; sum = sum + a.w;
+            sum = sum + b.x; sum = sum + b.y; sum = sum + b.z; sum = sum + b.w;
+            sum = sum + c.x; sum = sum + c.y; sum = sum + c.z; sum = sum + c.w;
+            sum = sum + d.x; sum = sum + d.y; sum = sum + d.z; sum = sum + d.w;
         }
         for (; j < upto; j++) sum = sum + e[j];
         norm = sum > 0.0f;
@@ -386,36 +460,290 @@ __global__ __launch_bounds__(256) void attn_softmax_exact(float *__restrict__ at
     }
     __syncthreads();
     const float inv = inv_s;
-    for (int j = tid; j < upto; j += 256) row[j] = norm ? e[j] * inv : e[j];
+    const int nrm = norm;
+    for (int j = tid; j < upto; j += 256) row[j] = nrm ? e[j] * inv : e[j];
 }
 
-__global__ __launch_bounds__(64) void attn_values_exact(const float *__restrict__ att,
-                                                        const float *__restrict__ vc,
-                                                        int n_head, int n_head_kv, int hd,
-                                                        const uint32_t *__restrict__ pos,
-                                                        int n_ctx, float *__restrict__ out,
-                                                        size_t out_stride)
+// One wave per (kv head, column slice, token).  Lane = (query head g of the
+// kv head's group, column d); the wave covers gqa heads x (64 / gqa) columns.
+#define VX_U 8
+
+__device__ __forceinline__ float vx_quad(float acc, float4 a, float4 v)
 {
-    const int h = blockIdx.x, t = blockIdx.y, d = blockIdx.z * 64 + threadIdx.x;
-    if (d >= hd) return;
-    const int gqa = n_head / n_head_kv, kvh = h / gqa, kvd = n_head_kv * hd;
+    acc = acc + a.x * v.x;
+    acc = acc + a.y * v.y;
+    acc = acc + a.z * v.z;
+    acc = acc + a.w * v.w;
+    return acc;
+}
+
+__global__ __launch_bounds__(64) void attn_values_x(const float *__restrict__ att,
+                                                    size_t att_stride,
+                                                    const float *__restrict__ vc, int n_head,
+                                                    int n_head_kv, int hd, int ds,
+                                                    const uint32_t *__restrict__ pos,
+                                                    int n_ctx, float *__restrict__ out,
+                                                    size_t out_stride)
+{
+    const int lane = threadIdx.x, t = blockIdx.y;
+    const int gqa = n_head / n_head_kv, kvd = n_head_kv * hd;
+    const int n_sl = (hd + ds - 1) / ds;
+    const int kvh = blockIdx.x / n_sl, sl = blockIdx.x - kvh * n_sl;
+    const int g = lane / ds, d = sl * ds + (lane - g * ds);
+    if (g >= gqa || d >= hd) return;
+    const int h = kvh * gqa + g;
     const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
-    const float *a = att + ((size_t)t * n_head + h) * n_ctx;
-    const float *v = vc + (size_t)kvh * hd + d;
+    const int nq = upto >> 2;
+    const float4 *ap = (const float4 *)(att + ((size_t)t * n_head + h) * att_stride);
+    const float4 *vp = (const float4 *)vc + (size_t)kvh * hd + d;   // quad jq at vp[jq * kvd]
     float acc = 0.0f;
-    int j = 0;
-    for (; j + 8 <= upto; j += 8) {
-        float vv[8], aa[8];
+    int jq = 0;
+    if (nq >= 2 * VX_U) {
+        float4 va[VX_U], aa[VX_U], vb[VX_U], ab[VX_U];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            vv[u] = v[(size_t)(j + u) * kvd];
-            aa[u] = a[j + u];
+        for (int u = 0; u < VX_U; u++) {
+            va[u] = vp[(size_t)u * kvd];
+            aa[u] = ap[u];
+        }
+        for (; jq + 2 * VX_U <= nq; jq += 2 * VX_U) {
+#pragma unroll
+            for (int u = 0; u < VX_U; u++) {
+                vb[u] = vp[(size_t)(jq + VX_U + u) * kvd];
+                ab[u] = ap[jq + VX_U + u];
+            }
+#pragma unroll
+            for (int u = 0; u < VX_U; u++) acc = vx_quad(acc, aa[u], va[u]);
+#pragma unroll
+            for (int u = 0; u < VX_U; u++) {
+                // the next pair's first half, clamped inside the visible rows
+                const int k = jq + 2 * VX_U + u < nq ? jq + 2 * VX_U + u : nq - 1;
+                va[u] = vp[(size_t)k * kvd];
+                aa[u] = ap[k];
+            }
+#pragma unroll
+            for (int u = 0; u < VX_U; u++) acc = vx_quad(acc, ab[u], vb[u]);
+        }
+    }
+    for (; jq < nq; jq++) acc = vx_quad(acc, ap[jq], vp[(size_t)jq * kvd]);
+    const float *as = (const float *)(ap + nq);
+    const float *vs = (const float *)(vp + (size_t)nq * kvd);
+    for (int r = 0; r < (upto & 3); r++) acc = acc + as[r] * vs[r];
+    out[(size_t)t * out_stride + (size_t)h * hd + d] = acc;
+}
+
+// ---- fused softmax + values (exact order), one workgroup per (kv head,
+// column slice, token), 16 waves; the kv head's G query heads x 64/G columns
+// make the 64 lanes of wave 0:
+//   all waves: head maxima from the per-tile maxima, e_j = expf(s_j - max)
+//     into LDS for the G heads;
+//   wave 0: one lane per head runs the position-order sum, then the wave
+//     scales e_j by 1/sum in place (a_j);
+//   loader waves: stream the slice's V columns (each 16-byte quad loaded once,
+//     two 64-position tiles in flight per wave from the start of the kernel),
+//     multiply by the G heads' a_j and hand the products to wave 0 through a
+//     ring of LDS stages;
+//   wave 0: one lane per (head, column) adds the products in position order.
+// Stages are handed over with workgroup-scope release/acquire flags in LDS;
+// every wait is bounded (a wave that times out writes NaN and leaves).
+#define SV_WAVES 16
+#define SV_QT 16                    // quads (4 positions) per stage
+#define SV_NP 4                     // product stages
+#define SV_LOADERS 12               // waves 1-3, 5-7, 9-11, 13-15
+#define SV_E_MAX (80 * 1024)        // LDS bytes for the weights of the group
+#define SV_SPIN (1 << 22)
+
+__device__ __forceinline__ bool sv_wait_ge(int *flag, int v)
+{
+    for (int n = 0; n < SV_SPIN; n++) {
+        if (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= v)
+            return true;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return false;
+}
+
+__device__ __forceinline__ void sv_signal(int *flag, int v)
+{
+    __hip_atomic_store(flag, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+template <int G>
+__global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
+    const float *__restrict__ att, size_t att_stride, const float *__restrict__ tmax, int n_tiles,
+    const float *__restrict__ vc, int n_head, int n_head_kv, int hd,
+    const uint32_t *__restrict__ pos, int n_ctx, float *__restrict__ out, size_t out_stride)
+{
+    constexpr int DS = 64 / G;               // columns per slice
+    constexpr int NLD = SV_QT / G;           // 16-byte loads per lane per tile
+    constexpr bool DB = G > 1;               // second tile in flight
+    extern __shared__ float4 sv_lds[];
+    float4 *ring = sv_lds;                                  // [SV_NP][SV_QT][64]
+    float *e = (float *)(sv_lds + SV_NP * SV_QT * 64);      // [G][att_stride]
+    __shared__ float mx_s[G];
+    __shared__ int ready[SV_NP], consumed, a_ready;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kvd = n_head_kv * hd;
+    const int n_sl = (hd + DS - 1) / DS;
+    const int kvh = blockIdx.x / n_sl, sl = blockIdx.x - kvh * n_sl, t = blockIdx.y;
+    const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
+    const int nq = upto >> 2, rem = upto & 3, nq_all = (upto + 3) >> 2;
+    const int ntile = (nq_all + SV_QT - 1) / SV_QT;
+    const int estr = (int)att_stride;
+    const float *srow = att + ((size_t)t * n_head + (size_t)kvh * G) * att_stride;
+
+    // loaders: lane -> (quad lq of each group of G quads, column ld)
+    const int lq = lane / DS, ld = sl * DS + (lane - lq * DS);
+    const float4 *v4 = (const float4 *)vc + kvh * hd + (ld < hd ? ld : sl * DS);
+    const bool loader = (wave & 3) != 0;     // waves on SIMD 0 do not load
+    const int li = wave - 1 - (wave >> 2);
+    float4 vcur[NLD], vnext[DB ? NLD : 1];
+    if (loader && li < ntile) {
+#pragma unroll
+        for (int k = 0; k < NLD; k++) {
+            const int jq = min(li * SV_QT + k * G + lq, nq_all - 1);
+            vcur[k] = v4[(size_t)jq * kvd];
+        }
+    }
+
+    // ---- head maxima (src/ops.c:26-30: a NaN first score stays the max)
+    if (wave < G) {
+        const float *tm = tmax + ((size_t)t * n_head + (size_t)kvh * G + wave) * n_tiles;
+        const int used = (upto + SC_TILE - 1) / SC_TILE;
+        float m = -INFINITY;
+        for (int i = lane; i < used; i += 64) {
+            const float v = tm[i];
+            m = v > m ? v : m;
         }
 #pragma unroll
-        for (int u = 0; u < 8; u++) acc = acc + aa[u] * vv[u];
+        for (int o = 32; o > 0; o >>= 1) {
+            const float w = __shfl_xor(m, o);
+            m = w > m ? w : m;
+        }
+        const float s0 = srow[(size_t)wave * att_stride];
+        if (lane == 0) mx_s[wave] = s0 != s0 ? s0 : m;
     }
-    for (; j < upto; j++) acc = acc + a[j] * v[(size_t)j * kvd];
-    out[(size_t)t * out_stride + (size_t)h * hd + d] = acc;
+    if (tid < SV_NP) ready[tid] = -1;
+    if (tid == 0) {
+        consumed = 0;
+        a_ready = 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int gg = 0; gg < G; gg++) {
+        const float mx = mx_s[gg];
+        const float *sr = srow + (size_t)gg * att_stride;
+        for (int j = tid; j < upto; j += SV_WAVES * 64) e[gg * estr + j] = fox_expf(sr[j] - mx);
+    }
+    __syncthreads();
+
+    if (wave == 0) {
+        // ---- softmax sums, one lane per head, position order
+        float sum = 0.0f;
+        if (lane < G) {
+            const float *er = e + lane * estr;
+            int j = 0;
+            for (; j + 8 <= upto; j += 8) {
+                const float4 a = *(const float4 *)(er + j), b = *(const float4 *)(er + j + 4);
+                sum = sum + a.x; sum = sum + a.y; sum = sum + a.z; sum = sum + a.w;
+                sum = sum + b.x; sum = sum + b.y; sum = sum + b.z; sum = sum + b.w;
+            }
+            for (; j < upto; j++) sum = sum + er[j];
+        }
+        const int nrm = sum > 0.0f;
+        const float inv = nrm ? fox_div(1.0f, sum) : 1.0f;
+#pragma unroll
+        for (int gg = 0; gg < G; gg++) {
+            const float ig = __shfl(inv, gg);
+            if (!__shfl(nrm, gg)) continue;
+            float4 *er = (float4 *)(e + gg * estr);
+            for (int q4 = lane; q4 < nq_all; q4 += 64) {
+                float4 v = er[q4];
+                v.x = v.x * ig; v.y = v.y * ig; v.z = v.z * ig; v.w = v.w * ig;
+                er[q4] = v;
+            }
+        }
+        sv_signal(&a_ready, 1);
+
+        // ---- value sums: lane (head g, column d) adds its products in order
+        const int g = lane / DS, d = sl * DS + (lane - g * DS);
+        float acc = 0.0f;
+        bool ok = true;
+        for (int i = 0; i < ntile; i++) {
+            const int s = i % SV_NP;
+            if (!sv_wait_ge(&ready[s], i)) {
+                ok = false;
+                break;
+            }
+            const float4 *P = ring + s * SV_QT * 64 + lane;
+            const int q0 = i * SV_QT;
+            const int nfull = min(max(nq - q0, 0), SV_QT);
+            int qi = 0;
+            for (; qi + 2 <= nfull; qi += 2) {
+                const float4 p = P[qi * 64], r = P[(qi + 1) * 64];
+                acc = acc + p.x; acc = acc + p.y; acc = acc + p.z; acc = acc + p.w;
+                acc = acc + r.x; acc = acc + r.y; acc = acc + r.z; acc = acc + r.w;
+            }
+            for (; qi < nfull; qi++) {
+                const float4 p = P[qi * 64];
+                acc = acc + p.x; acc = acc + p.y; acc = acc + p.z; acc = acc + p.w;
+            }
+            if (rem && q0 + nfull == nq && nfull < SV_QT) {
+                const float4 p = P[nfull * 64];
+                acc = acc + p.x;
+                if (rem > 1) acc = acc + p.y;
+                if (rem > 2) acc = acc + p.z;
+            }
+            sv_signal(&consumed, i + 1);
+        }
+        if (!ok) {
+            sv_signal(&consumed, 1 << 30);
+            acc = __builtin_nanf("");
+        }
+        if (g < G && d < hd) out[(size_t)t * out_stride + (size_t)(kvh * G + g) * hd + d] = acc;
+        return;
+    }
+    if (!loader) return;
+
+    // ---- loaders: tile i = li, li + SV_LOADERS, ...
+    if (!sv_wait_ge(&a_ready, 1)) return;
+    for (int i = li; i < ntile; i += SV_LOADERS) {
+        const int inext = i + SV_LOADERS;
+        if (DB && inext < ntile) {
+#pragma unroll
+            for (int k = 0; k < NLD; k++) {
+                const int jq = min(inext * SV_QT + k * G + lq, nq_all - 1);
+                vnext[DB ? k : 0] = v4[(size_t)jq * kvd];
+            }
+        }
+        const int s = i % SV_NP;
+        if (i >= SV_NP && !sv_wait_ge(&consumed, i - SV_NP + 1)) return;
+        float4 *P = ring + s * SV_QT * 64;
+#pragma unroll
+        for (int k = 0; k < NLD; k++) {
+            const int qi = k * G + lq;                       // quad within the tile
+            const int jq = min(i * SV_QT + qi, nq_all - 1);
+            const float4 v = vcur[k];
+#pragma unroll
+            for (int gg = 0; gg < G; gg++) {
+                const float4 a = ((const float4 *)(e + gg * estr))[jq];
+                float4 p;
+                p.x = a.x * v.x; p.y = a.y * v.y; p.z = a.z * v.z; p.w = a.w * v.w;
+                P[qi * 64 + gg * DS + (lane - lq * DS)] = p;
+            }
+        }
+        sv_signal(&ready[s], i);
+        if (DB) {
+#pragma unroll
+            for (int k = 0; k < NLD; k++) vcur[k] = vnext[DB ? k : 0];
+        } else if (i + SV_LOADERS < ntile) {
+#pragma unroll
+            for (int k = 0; k < NLD; k++) {
+                const int jq = min((i + SV_LOADERS) * SV_QT + k * G + lq, nq_all - 1);
+                vcur[k] = v4[(size_t)jq * kvd];
+            }
+        }
+    }
 }
 
 extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t out_stride,
@@ -430,34 +758,74 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
     if (n_head % n_head_kv)
         return fox_fail(FOX_GPU_ERR_ARG, "attention: %zu heads over %zu kv heads", n_head,
                         n_head_kv);
-    if (n_head / n_head_kv > ATT_MAXG || head_dim > ATT_MAXHD)
+    if (n_head / n_head_kv > ATT_MAXG || head_dim > ATT_MAXHD || head_dim % 4)
         return fox_fail(FOX_GPU_ERR_UNSUPPORTED,
-                        "attention: at most %d query heads per kv head and head_dim %d",
-                        ATT_MAXG, ATT_MAXHD);
+                        "attention: at most %d query heads per kv head, head_dim a multiple of "
+                        "4 up to %d", ATT_MAXG, ATT_MAXHD);
     if (M > FOX_GPU_MAX_TOKENS) return fox_fail(FOX_GPU_ERR_ARG, "attention: too many tokens");
+    if (n_ctx > (1u << 30)) return fox_fail(FOX_GPU_ERR_ARG, "attention: n_ctx too large");
+    const size_t qs = M > 1 ? q_stride : n_head * head_dim;
+    const size_t os = M > 1 ? out_stride : n_head * head_dim;
+    if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 || qs % 4)
+        return fox_fail(FOX_GPU_ERR_ARG, "attention: q and the caches must be 16-byte aligned "
+                        "and the q stride a multiple of 4");
     if (mode == FOX_GPU_ATTN_EXACT) {
-        const size_t bytes = M * n_head * n_ctx * sizeof(float);
         if (n_ctx * sizeof(float) > 60 * 1024)
             return fox_fail(FOX_GPU_ERR_UNSUPPORTED,
-                            "attention: exact mode keeps a head's %zu scores in LDS; at most "
+                            "attention: exact mode keeps a head's %zu weights in LDS; at most "
                             "15360 positions", n_ctx);
+        const size_t att_stride = (n_ctx + 3) & ~(size_t)3;
+        const int n_tiles = (int)((n_ctx + SC_TILE - 1) / SC_TILE);
+        const size_t att_bytes = M * n_head * att_stride * sizeof(float);
+        const size_t bytes = att_bytes + M * n_head * (size_t)n_tiles * sizeof(float);
         fox_gpu_status st = fox_ws_reserve(ctx, bytes);
         if (st) return st;
         float *att = (float *)ctx->ws;
-        const size_t qs = M > 1 ? q_stride : n_head * head_dim;
-        hipLaunchKernelGGL(attn_scores_exact,
-                           dim3((unsigned)((n_ctx + EX_TILE - 1) / EX_TILE), (unsigned)n_head_kv,
-                                (unsigned)M), dim3(256), 0, ctx->stream, q, qs, k_cache,
-                           (int)n_head, (int)n_head_kv, (int)head_dim, pos, (int)n_ctx, att);
+        float *tmax = (float *)(ctx->ws + att_bytes);
+        const size_t gqa = n_head / n_head_kv;
+        const size_t lds = (SC_TILE * (head_dim + 4) + gqa * head_dim) * sizeof(float);
+        if (lds > 64 * 1024) {
+            hipError_t e = hipFuncSetAttribute((const void *)attn_scores_x,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)lds);
+            if (e != hipSuccess) return fox_hip_fail(e, "attention: LDS size");
+        }
+        hipLaunchKernelGGL(attn_scores_x, dim3((unsigned)n_tiles, (unsigned)n_head_kv, (unsigned)M),
+                           dim3(256), lds, ctx->stream, q, qs, k_cache, (int)n_head,
+                           (int)n_head_kv, (int)head_dim, pos, (int)n_ctx, att_stride, att, tmax,
+                           n_tiles);
         FOX_LAUNCHED("attention scores");
-        hipLaunchKernelGGL(attn_softmax_exact, dim3((unsigned)n_head, (unsigned)M), dim3(256),
-                           n_ctx * sizeof(float), ctx->stream, att, (int)n_head, pos, (int)n_ctx);
+        const int ds = (int)(64 / gqa);
+        const int n_sl = (int)((head_dim + ds - 1) / ds);
+        const size_t e_bytes = gqa * att_stride * sizeof(float);
+        const int ih = (int)n_head, ikv = (int)n_head_kv, ihd = (int)head_dim, ictx = (int)n_ctx;
+        const void *sv = gqa == 1 ? (const void *)attn_sv_x<1>
+                       : gqa == 2 ? (const void *)attn_sv_x<2>
+                       : gqa == 4 ? (const void *)attn_sv_x<4>
+                       : gqa == 8 ? (const void *)attn_sv_x<8> : nullptr;
+        if (sv && e_bytes <= SV_E_MAX) {
+            const size_t sv_lds = (size_t)SV_NP * SV_QT * 64 * 16 + e_bytes;
+            hipError_t e = hipFuncSetAttribute(sv, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)sv_lds);
+            if (e != hipSuccess) return fox_hip_fail(e, "attention: LDS size");
+            const int sv_ds = (int)(64 / gqa);
+            const unsigned nsl = (unsigned)((head_dim + sv_ds - 1) / sv_ds);
+            void *args[] = {(void *)&att, (void *)&att_stride, (void *)&tmax, (void *)&n_tiles,
+                            (void *)&v_cache, (void *)&ih, (void *)&ikv, (void *)&ihd,
+                            (void *)&pos, (void *)&ictx, (void *)&out, (void *)&os};
+            e = hipLaunchKernel(sv, dim3((unsigned)n_head_kv * nsl, (unsigned)M),
+                                dim3(SV_WAVES * 64), args, sv_lds, ctx->stream);
+            if (e != hipSuccess) return fox_hip_fail(e, "attention softmax+values");
+            FOX_LAUNCHED("attention softmax+values");
+            return FOX_GPU_OK;
+        }
+        hipLaunchKernelGGL(attn_softmax_x, dim3((unsigned)n_head, (unsigned)M), dim3(256),
+                           att_stride * sizeof(float), ctx->stream, att, att_stride, tmax,
+                           n_tiles, (int)n_head, pos, (int)n_ctx);
         FOX_LAUNCHED("attention softmax");
-        hipLaunchKernelGGL(attn_values_exact,
-                           dim3((unsigned)n_head, (unsigned)M, (unsigned)((head_dim + 63) / 64)),
-                           dim3(64), 0, ctx->stream, att, v_cache, (int)n_head, (int)n_head_kv,
-                           (int)head_dim, pos, (int)n_ctx, out,
-                           M > 1 ? out_stride : n_head * head_dim);
+        hipLaunchKernelGGL(attn_values_x, dim3((unsigned)(n_head_kv * n_sl), (unsigned)M),
+                           dim3(64), 0, ctx->stream, att, att_stride, v_cache, (int)n_head,
+                           (int)n_head_kv, (int)head_dim, ds, pos, (int)n_ctx, out, os);
         FOX_LAUNCHED("attention values");
         return FOX_GPU_OK;
     }
@@ -468,13 +836,11 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
     if (st) return st;
     float *part = (float *)ctx->ws;
     hipLaunchKernelGGL(attn_partial, dim3((unsigned)n_splits, (unsigned)n_head_kv, (unsigned)M),
-                       dim3(256), 0, ctx->stream, q, M > 1 ? q_stride : n_head * head_dim,
-                       k_cache, v_cache, (int)n_head, (int)n_head_kv, (int)head_dim, pos,
-                       (int)n_ctx, n_splits, part);
+                       dim3(256), 0, ctx->stream, q, qs, k_cache, v_cache, (int)n_head,
+                       (int)n_head_kv, (int)head_dim, pos, (int)n_ctx, n_splits, part);
     FOX_LAUNCHED("attention partial");
     hipLaunchKernelGGL(attn_merge, dim3((unsigned)n_head, (unsigned)M), dim3(128), 0, ctx->stream,
-                       part, (int)n_head, (int)head_dim, n_splits, out,
-                       M > 1 ? out_stride : n_head * head_dim);
+                       part, (int)n_head, (int)head_dim, n_splits, out, os);
     FOX_LAUNCHED("attention merge");
     return FOX_GPU_OK;
 }

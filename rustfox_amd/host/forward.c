@@ -8,8 +8,9 @@
  *   hb = silu(hb) * hb2; x += W_down hb.
  * then xb = rmsnorm(x_last, output_norm) and logits = W_out xb.
  *
- * The cache is f32 [n_layer][n_ctx][n_head_kv * head_dim] as in the
- * reference; the RoPE tables are built on the host in double exactly as
+ * The K cache is f32 [n_layer][n_ctx][n_head_kv * head_dim] as in the
+ * reference, the V cache the device's position-quad interleaved layout
+ * (fox_gpu.h) per layer; the RoPE tables are built on the host in double exactly as
  * src/forward.c:188-199 and uploaded.  A pass takes at most
  * FOX_GPU_MAX_TOKENS tokens; fox_eval cuts its input into such passes, which
  * gives the same result as the reference's n_batch chunks because a token
@@ -172,7 +173,7 @@ fox_status fox_context_create(fox_model *m, const fox_context_config *cfg, fox_c
     ALLOC(c->hb2, nb * c->ff * 4)
     ALLOC(c->dlogits, c->vocab * 4)
     ALLOC(c->kc, (size_t)mi->n_layer * k.n_ctx * c->nkv * 4)
-    ALLOC(c->vc, (size_t)mi->n_layer * k.n_ctx * c->nkv * 4)
+    ALLOC(c->vc, (size_t)mi->n_layer * FOX_GPU_V_CACHE_FLOATS(k.n_ctx, c->nkv) * 4)
     ALLOC(c->rc, (size_t)k.n_ctx * (c->hd / 2) * 4)
     ALLOC(c->rs, (size_t)k.n_ctx * (c->hd / 2) * 4)
     ALLOC(c->dtok, nb * 4)
@@ -183,7 +184,9 @@ fox_status fox_context_create(fox_model *m, const fox_context_config *cfg, fox_c
 #undef ALLOC
     if (fox_gpu_memcpy_h2d(c->gpu, c->dzero, &zero, 4) != FOX_GPU_OK ||
         fox_gpu_memset(c->gpu, c->kc, 0, (size_t)mi->n_layer * k.n_ctx * c->nkv * 4) != FOX_GPU_OK ||
-        fox_gpu_memset(c->gpu, c->vc, 0, (size_t)mi->n_layer * k.n_ctx * c->nkv * 4) != FOX_GPU_OK) {
+        fox_gpu_memset(c->gpu, c->vc, 0,
+                       (size_t)mi->n_layer * FOX_GPU_V_CACHE_FLOATS(k.n_ctx, c->nkv) * 4) !=
+            FOX_GPU_OK) {
         st = fox_gpu_failed(FOX_GPU_ERR_INTERNAL, "context: initialise buffers");
         fox_context_destroy(c);
         return st;
@@ -291,6 +294,7 @@ static fox_status forward_pass(fox_context *c, size_t M, int want_logits)
 {
     const fox_model_info *mi = &c->m->info;
     const size_t kvl = (size_t)c->cfg.n_ctx * c->nkv;
+    const size_t vl = FOX_GPU_V_CACHE_FLOATS(c->cfg.n_ctx, c->nkv);
     uint32_t l;
     fox_status st;
 
@@ -310,9 +314,9 @@ static fox_status forward_pass(fox_context *c, size_t M, int want_logits)
             return st;
         GPU(fox_gpu_rope_store(c->gpu, c->q, c->nq, c->k, c->nkv, c->v, c->nkv, mi->n_head,
                                mi->n_head_kv, c->hd, M, c->rc, c->rs, c->dpos, c->cfg.n_ctx,
-                               c->kc + l * kvl, c->vc + l * kvl), "forward: rope");
+                               c->kc + l * kvl, c->vc + l * vl), "forward: rope");
         GPU(fox_gpu_attention(c->gpu, c->xb, c->wide, c->q, c->nq, c->kc + l * kvl,
-                              c->vc + l * kvl, mi->n_head, mi->n_head_kv, c->hd, M, c->dpos,
+                              c->vc + l * vl, mi->n_head, mi->n_head_kv, c->hd, M, c->dpos,
                               c->cfg.n_ctx, c->attn_mode), "forward: attention");
         GPU(fox_gpu_gemv(c->gpu, D->attn_out, c->xb, c->wide, M, c->x, c->d,
                          FOX_GPU_GEMV_ACCUMULATE), "forward: attn_output");
@@ -433,14 +437,25 @@ fox_status fox_decode_greedy(fox_context *c, uint32_t token, size_t n_steps, uin
 fox_status fox_context_set_kv(fox_context *c, uint32_t layer, uint32_t p0, uint32_t n,
                               const float *k, const float *v)
 {
-    size_t off;
+    size_t bytes;
+    float *tmp;
+    fox_gpu_status gs;
     if (!c || !k || !v) return fox_fail(FOX_ERR_ARG, "set_kv: null argument");
     if (layer >= c->m->info.n_layer || (size_t)p0 + n > c->cfg.n_ctx)
         return fox_fail(FOX_ERR_ARG, "set_kv: rows %u..%u of layer %u are outside the cache",
                         p0, p0 + n, layer);
-    off = ((size_t)layer * c->cfg.n_ctx + p0) * c->nkv;
-    GPU(fox_gpu_memcpy_h2d(c->gpu, c->kc + off, k, (size_t)n * c->nkv * 4), "set_kv: k");
-    GPU(fox_gpu_memcpy_h2d(c->gpu, c->vc + off, v, (size_t)n * c->nkv * 4), "set_kv: v");
+    if (n == 0) return FOX_OK;
+    bytes = (size_t)n * c->nkv * 4;
+    GPU(fox_gpu_malloc(c->gpu, 2 * bytes, (void **)&tmp), "set_kv: staging");
+    gs = fox_gpu_memcpy_h2d(c->gpu, tmp, k, bytes);
+    if (gs == FOX_GPU_OK) gs = fox_gpu_memcpy_h2d(c->gpu, tmp + (size_t)n * c->nkv, v, bytes);
+    if (gs == FOX_GPU_OK)
+        gs = fox_gpu_kv_write(c->gpu, c->kc + (size_t)layer * c->cfg.n_ctx * c->nkv,
+                              c->vc + (size_t)layer * FOX_GPU_V_CACHE_FLOATS(c->cfg.n_ctx, c->nkv),
+                              c->nkv, c->cfg.n_ctx, p0, n, tmp, tmp + (size_t)n * c->nkv);
+    if (gs == FOX_GPU_OK) gs = fox_gpu_sync(c->gpu);
+    fox_gpu_free(c->gpu, tmp);
+    if (gs != FOX_GPU_OK) return fox_gpu_failed(gs, "set_kv");
     return FOX_OK;
 }
 

@@ -136,6 +136,11 @@ class Oracle:
                                       rows, cols, out) == 0
         return out
 
+    def softmax(self, x):
+        x = np.array(x, dtype=np.float32)
+        self.lib.or_softmax(x, x.size)
+        return x
+
     def dequant(self, gtype, row, n):
         out = np.empty(n, np.float32)
         assert self.lib.or_dequant_row(gtype, np.ascontiguousarray(row, np.uint8), n, out) == 0

@@ -1,0 +1,104 @@
+"""Attention on the GPU against the reference's order of operations
+(src/forward.c:222-257, src/ops.c:24-39) restated with float32 numpy steps
+(each numpy float32 operation rounds once, no contraction) and the oracle's
+softmax (glibc expf).  Exact mode must be bit-identical; split mode within
+float rounding.  Caches are written through fox_gpu_kv_write, so the
+interleaved V layout is exercised as the decode path uses it."""
+import numpy as np
+import pytest
+
+import rustfox_amd as rf
+
+pytestmark = pytest.mark.gpu
+
+
+def reference_attention(oracle, q, K, V, n_head, n_kv, hd, pos, M, n_ctx):
+    """q [M][n_head*hd]; K, V [n_ctx][n_kv*hd] row-major."""
+    gqa = n_head // n_kv
+    out = np.zeros((M, n_head * hd), np.float32)
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    for t in range(M):
+        upto = min(pos + t + 1, n_ctx)
+        for h in range(n_head):
+            kvh = h // gqa
+            qh = q[t, h * hd:(h + 1) * hd]
+            Kh = K[:upto, kvh * hd:(kvh + 1) * hd]
+            a = np.zeros(upto, np.float32)
+            for d in range(hd):                    # fox_dot_f32 in d order
+                a = a + qh[d] * Kh[:, d]
+            att = oracle.softmax(a * scale)
+            Vh = V[:upto, kvh * hd:(kvh + 1) * hd]
+            acc = np.zeros(hd, np.float32)
+            for j in range(upto):                  # dst[d] += a * vj[d], j order
+                acc = acc + att[j] * Vh[j]
+            out[t, h * hd:(h + 1) * hd] = acc
+    return out
+
+
+def run_gpu(gpu, q, K, V, n_head, n_kv, hd, pos, M, n_ctx, mode):
+    kvd = n_kv * hd
+    kc = gpu.empty(n_ctx * kvd, np.float32)
+    vc = gpu.empty((n_ctx + 3) // 4 * 4 * kvd, np.float32)
+    dk = gpu.array(K.astype(np.float32))
+    dv = gpu.array(V.astype(np.float32))
+    gpu.kv_write(kc, vc, kvd, n_ctx, 0, dk, dv, n_ctx)
+    dq = gpu.array(q)
+    dpos = gpu.array(np.array([pos], np.uint32))
+    out = gpu.empty(M * n_head * hd, np.float32)
+    gpu.attention(out, dq, kc, vc, n_head, n_kv, hd, M, dpos, n_ctx, mode)
+    gpu.sync()
+    return out.numpy().reshape(M, n_head * hd)
+
+
+CASES = [  # n_head, n_kv, hd, n_ctx, pos, M
+    (32, 8, 128, 700, 650, 1),     # 4B/8B head shape, long chain with a ragged tail
+    (32, 16, 128, 300, 299, 1),    # 27B head shape, last row of the cache
+    (8, 8, 64, 130, 100, 4),       # no GQA, 4 tokens at consecutive positions
+    (6, 6, 48, 77, 70, 1),         # tiny-288 heads
+    (4, 1, 128, 64, 0, 1),         # a single visible row
+    (16, 2, 128, 257, 200, 8),     # 8 tokens (verify batch), gqa 8
+    (12, 4, 64, 100, 99, 1),       # gqa 3: the three-kernel path
+    (8, 2, 64, 6000, 5990, 2),     # weights beyond the fused kernel's LDS: three-kernel path
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "h%d_kv%d_d%d_ctx%d_p%d_m%d" % c)
+def test_attention_exact_is_bit_identical(gpu, oracle, case):
+    n_head, n_kv, hd, n_ctx, pos, M = case
+    rng = np.random.default_rng(sum(case))
+    q = (rng.standard_normal((M, n_head * hd)) * 0.3).astype(np.float32)
+    K = rng.standard_normal((n_ctx, n_kv * hd)).astype(np.float32)
+    V = rng.standard_normal((n_ctx, n_kv * hd)).astype(np.float32)
+    got = run_gpu(gpu, q, K, V, n_head, n_kv, hd, pos, M, n_ctx, rf.ATTN_EXACT)
+    want = reference_attention(oracle, q, K, V, n_head, n_kv, hd, pos, M, n_ctx)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
+        f"max abs diff {np.abs(got - want).max()}"
+
+
+@pytest.mark.parametrize("case", CASES[:3], ids=lambda c: "h%d_kv%d_d%d_ctx%d_p%d_m%d" % c)
+def test_attention_split_within_rounding(gpu, oracle, case):
+    n_head, n_kv, hd, n_ctx, pos, M = case
+    rng = np.random.default_rng(7 + sum(case))
+    q = (rng.standard_normal((M, n_head * hd)) * 0.3).astype(np.float32)
+    K = rng.standard_normal((n_ctx, n_kv * hd)).astype(np.float32)
+    V = rng.standard_normal((n_ctx, n_kv * hd)).astype(np.float32)
+    got = run_gpu(gpu, q, K, V, n_head, n_kv, hd, pos, M, n_ctx, rf.ATTN_SPLIT)
+    want = reference_attention(oracle, q, K, V, n_head, n_kv, hd, pos, M, n_ctx)
+    err = np.linalg.norm(got - want) / np.linalg.norm(want)
+    assert err < 1e-5, err
+
+
+def test_nan_first_score_follows_the_reference(gpu, oracle):
+    """src/ops.c:26-30: a NaN score at position 0 stays the maximum, so every
+    weight of that head is NaN and the sum is not normalised; a NaN later in
+    the row is skipped by the maximum.  Other heads are unaffected."""
+    n_head, n_kv, hd, n_ctx, pos, M = 4, 2, 64, 40, 39, 1
+    rng = np.random.default_rng(5)
+    q = (rng.standard_normal((M, n_head * hd)) * 0.3).astype(np.float32)
+    K = rng.standard_normal((n_ctx, n_kv * hd)).astype(np.float32)
+    V = rng.standard_normal((n_ctx, n_kv * hd)).astype(np.float32)
+    K[0, 0] = np.nan            # kv head 0: heads 0, 1 get a NaN first score
+    got = run_gpu(gpu, q, K, V, n_head, n_kv, hd, pos, M, n_ctx, rf.ATTN_EXACT)
+    want = reference_attention(oracle, q, K, V, n_head, n_kv, hd, pos, M, n_ctx)
+    assert np.isnan(want[0, :2 * hd]).all() and np.isnan(got[0, :2 * hd]).all()
+    assert np.array_equal(got[0, 2 * hd:].view(np.uint32), want[0, 2 * hd:].view(np.uint32))
