@@ -30,7 +30,9 @@ __device__ __constant__ const uint64_t fox_exp2_tab[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-__device__ __forceinline__ float fox_expf(float x)
+// fox_expf with the 2^(i/32) table read from `tab` (a copy of fox_exp2_tab,
+// e.g. in LDS, so that a wave's scattered lookups avoid a memory round trip)
+__device__ __forceinline__ float fox_expf_t(float x, const uint64_t *tab)
 {
     const double inv_ln2_32 = 0x1.71547652b82fep+0 * 32.0;
     const double shift = 0x1.8p+52;
@@ -39,20 +41,25 @@ __device__ __forceinline__ float fox_expf(float x)
     const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
 
     if (x != x) return x + x;
-    if (x > 0x1.62e42ep6f) return __builtin_inff();     // past log(2^128)
-    if (x < -0x1.9fe368p6f) return 0.0f;                // below log(2^-150)
+    if (x > 0x1.62e42ep6f) return __builtin_inff();
+    if (x < -0x1.9fe368p6f) return 0.0f;
     const double xd = (double)x;
     double kd = __builtin_fma(inv_ln2_32, xd, shift);
     const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
     kd -= shift;
     const double r = __builtin_fma(inv_ln2_32, xd, -kd);
-    const uint64_t t = fox_exp2_tab[ki & 31] + (ki << 47);
+    const uint64_t t = tab[ki & 31] + (ki << 47);
     const double s = __builtin_bit_cast(double, t);
     const double z = __builtin_fma(c0, r, c1);
     const double r2 = r * r;
     double y = __builtin_fma(c2, r, 1.0);
     y = __builtin_fma(z, r2, y);
     return (float)(y * s);
+}
+
+__device__ __forceinline__ float fox_expf(float x)
+{
+    return fox_expf_t(x, fox_exp2_tab);
 }
 
 __device__ __forceinline__ float fox_div(float a, float b)

@@ -369,6 +369,7 @@ __global__ __launch_bounds__(256) void attn_scores_x(const float *__restrict__ q
     const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
     if (p0 >= upto) return;
     const int pn = upto - p0 < SC_TILE ? upto - p0 : SC_TILE;
+#pragma unroll 8
     for (int i = tid; i < pn * nv; i += 256) {
         const int j = i / nv, c = i - j * nv;
         const float4 v = *(const float4 *)(kc + (size_t)(p0 + j) * kvd + (size_t)kvh * hd + 4 * c);
@@ -384,6 +385,7 @@ __global__ __launch_bounds__(256) void attn_scores_x(const float *__restrict__ q
     for (int g = wave; g < gqa; g += 4) {
         const float *qr = qs + g * hd;
         float a = 0.0f;
+#pragma unroll 8
         for (int d = 0; d < hd; d += 4) {
             const float4 qv = *(const float4 *)(qr + d);
             const float4 kv = *(const float4 *)(kr + d);
@@ -552,11 +554,34 @@ __global__ __launch_bounds__(64) void attn_values_x(const float *__restrict__ at
 #define SV_E_MAX (80 * 1024)        // LDS bytes for the weights of the group
 #define SV_SPIN (1 << 22)
 
+// v of lane (quad base + sel) for each lane, sel from a quad_perm control
+// word known at compile time (DPP, no LDS traffic)
+__device__ __forceinline__ float dpp_bcast(float v, int ctl)
+{
+    switch (ctl) {
+    case 0x00: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x00, 0xF, 0xF, false));
+    case 0x55: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x55, 0xF, 0xF, false));
+    case 0xAA: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xAA, 0xF, 0xF, false));
+    case 0xFF: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xFF, 0xF, 0xF, false));
+    case 0xA0: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xA0, 0xF, 0xF, false));
+    default:   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xF5, 0xF, 0xF, false));
+    }
+}
+
+// Hand-over flags live in LDS and guard LDS data only, so the fences order
+// LDS accesses only: global loads a wave has in flight stay in flight.
+__device__ __forceinline__ int sv_peek(int *flag)
+{
+    return __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 __device__ __forceinline__ bool sv_wait_ge(int *flag, int v)
 {
     for (int n = 0; n < SV_SPIN; n++) {
-        if (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= v)
+        if (sv_peek(flag) >= v) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
             return true;
+        }
         __builtin_amdgcn_s_sleep(1);
     }
     return false;
@@ -564,7 +589,47 @@ __device__ __forceinline__ bool sv_wait_ge(int *flag, int v)
 
 __device__ __forceinline__ void sv_signal(int *flag, int v)
 {
-    __hip_atomic_store(flag, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __hip_atomic_store(flag, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// acc + x_0 + x_1 + ... over 4 * nq floats of LDS, in index order; the reads
+// of the next eight quads are in flight while the current eight are added
+__device__ __forceinline__ float chain_add_lds(float acc, const float4 *p, int nq)
+{
+    int q = 0;
+    if (nq >= 16) {
+        float4 A[8], B[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) A[u] = p[u];
+        for (; q + 24 <= nq; q += 16) {
+#pragma unroll
+            for (int u = 0; u < 8; u++) B[u] = p[q + 8 + u];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                acc = acc + A[u].x; acc = acc + A[u].y; acc = acc + A[u].z; acc = acc + A[u].w;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) A[u] = p[q + 16 + u];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                acc = acc + B[u].x; acc = acc + B[u].y; acc = acc + B[u].z; acc = acc + B[u].w;
+            }
+        }
+        // A holds quads q .. q+7
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            acc = acc + A[u].x; acc = acc + A[u].y; acc = acc + A[u].z; acc = acc + A[u].w;
+        }
+        q += 8;
+    }
+    for (; q < nq; q++) {
+        const float4 v = p[q];
+        acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
+    }
+    return acc;
 }
 
 template <int G>
@@ -578,8 +643,10 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
     constexpr bool DB = G > 1;               // second tile in flight
     extern __shared__ float4 sv_lds[];
     float4 *ring = sv_lds;                                  // [SV_NP][SV_QT][64]
-    float *e = (float *)(sv_lds + SV_NP * SV_QT * 64);      // [G][att_stride]
-    __shared__ float mx_s[G];
+    float *e = (float *)(sv_lds + SV_NP * SV_QT * 64);      // [G][att_stride + 4]
+    __shared__ float mx_s[G], inv_s[G];
+    __shared__ int nrm_s[G];
+    __shared__ uint64_t tab[32];
     __shared__ int ready[SV_NP], consumed, a_ready;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -589,7 +656,7 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
     const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
     const int nq = upto >> 2, rem = upto & 3, nq_all = (upto + 3) >> 2;
     const int ntile = (nq_all + SV_QT - 1) / SV_QT;
-    const int estr = (int)att_stride;
+    const int estr = (int)att_stride + 4;        // padded: heads in different banks
     const float *srow = att + ((size_t)t * n_head + (size_t)kvh * G) * att_stride;
 
     // loaders: lane -> (quad lq of each group of G quads, column ld)
@@ -624,16 +691,29 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
         if (lane == 0) mx_s[wave] = s0 != s0 ? s0 : m;
     }
     if (tid < SV_NP) ready[tid] = -1;
+    if (tid < 32) tab[tid] = fox_exp2_tab[tid];
     if (tid == 0) {
         consumed = 0;
         a_ready = 0;
     }
     __syncthreads();
+    // e_j = expf(s_j - max): a thread's scores are loaded before any is used
+    for (int j0 = 0; j0 < upto; j0 += 4 * SV_WAVES * 64) {
+        float sc[G][4];
 #pragma unroll
-    for (int gg = 0; gg < G; gg++) {
-        const float mx = mx_s[gg];
-        const float *sr = srow + (size_t)gg * att_stride;
-        for (int j = tid; j < upto; j += SV_WAVES * 64) e[gg * estr + j] = fox_expf(sr[j] - mx);
+        for (int gg = 0; gg < G; gg++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int j = j0 + r * SV_WAVES * 64 + tid;
+                sc[gg][r] = j < upto ? srow[(size_t)gg * att_stride + j] : 0.0f;
+            }
+#pragma unroll
+        for (int gg = 0; gg < G; gg++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int j = j0 + r * SV_WAVES * 64 + tid;
+                if (j < upto) e[gg * estr + j] = fox_expf_t(sc[gg][r] - mx_s[gg], tab);
+            }
     }
     __syncthreads();
 
@@ -642,57 +722,81 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
         float sum = 0.0f;
         if (lane < G) {
             const float *er = e + lane * estr;
-            int j = 0;
-            for (; j + 8 <= upto; j += 8) {
-                const float4 a = *(const float4 *)(er + j), b = *(const float4 *)(er + j + 4);
-                sum = sum + a.x; sum = sum + a.y; sum = sum + a.z; sum = sum + a.w;
-                sum = sum + b.x; sum = sum + b.y; sum = sum + b.z; sum = sum + b.w;
-            }
-            for (; j < upto; j++) sum = sum + er[j];
+            sum = chain_add_lds(0.0f, (const float4 *)er, nq);
+            for (int j = 4 * nq; j < upto; j++) sum = sum + er[j];
         }
-        const int nrm = sum > 0.0f;
-        const float inv = nrm ? fox_div(1.0f, sum) : 1.0f;
-#pragma unroll
-        for (int gg = 0; gg < G; gg++) {
-            const float ig = __shfl(inv, gg);
-            if (!__shfl(nrm, gg)) continue;
-            float4 *er = (float4 *)(e + gg * estr);
-            for (int q4 = lane; q4 < nq_all; q4 += 64) {
-                float4 v = er[q4];
-                v.x = v.x * ig; v.y = v.y * ig; v.z = v.z * ig; v.w = v.w * ig;
-                er[q4] = v;
-            }
+        // a_j = e_j * (1/sum) is formed by the loaders (src/ops.c:35-38)
+        if (lane < G) {
+            nrm_s[lane] = sum > 0.0f;
+            inv_s[lane] = sum > 0.0f ? fox_div(1.0f, sum) : 1.0f;
         }
         sv_signal(&a_ready, 1);
 
-        // ---- value sums: lane (head g, column d) adds its products in order
+        // ---- value sums: lane (head g, column d) adds its products in order.
+        // A tile is read as two halves of eight quads: the second half is in
+        // flight while the first is added, the next tile's first half while
+        // the second is added.
         const int g = lane / DS, d = sl * DS + (lane - g * DS);
         float acc = 0.0f;
-        bool ok = true;
-        for (int i = 0; i < ntile; i++) {
-            const int s = i % SV_NP;
-            if (!sv_wait_ge(&ready[s], i)) {
+        bool ok = sv_wait_ge(&ready[0], 0);
+        float4 X[8], Y[8];
+        // ring slots are XOR-swizzled by (quad & 3) so that the loaders' four
+        // quads per store fall in different banks
+        int sw[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) sw[c] = lane ^ (c << 2);
+        if (ok) {
+#pragma unroll
+            for (int u = 0; u < 8; u++) X[u] = ring[u * 64 + sw[u & 3]];
+        }
+        // whole tiles: one basic block per tile.  The next tile's flag is read
+        // before the first half is added and tested after it (through a
+        // zero that depends on the sum, so the test cannot move up).
+        const int nwhole = nq / SV_QT;
+        int i = 0;
+        for (; i < nwhole; i++) {
+            const float4 *P = ring + (i % SV_NP) * SV_QT * 64;
+            const float4 *Pn = ring + ((i + 1) % SV_NP) * SV_QT * 64;
+#pragma unroll
+            for (int u = 0; u < 8; u++) Y[u] = P[(8 + u) * 64 + sw[u & 3]];
+            const int nf = sv_peek(&ready[(i + 1) % SV_NP]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                acc = acc + X[u].x; acc = acc + X[u].y; acc = acc + X[u].z; acc = acc + X[u].w;
+            }
+            int z;
+            asm volatile("v_mov_b32 %0, 0" : "=v"(z) : "v"(acc));
+            if (nf + z < i + 1 && i + 1 < ntile && !sv_wait_ge(&ready[(i + 1) % SV_NP], i + 1)) {
                 ok = false;
                 break;
             }
-            const float4 *P = ring + s * SV_QT * 64 + lane;
-            const int q0 = i * SV_QT;
-            const int nfull = min(max(nq - q0, 0), SV_QT);
-            int qi = 0;
-            for (; qi + 2 <= nfull; qi += 2) {
-                const float4 p = P[qi * 64], r = P[(qi + 1) * 64];
-                acc = acc + p.x; acc = acc + p.y; acc = acc + p.z; acc = acc + p.w;
-                acc = acc + r.x; acc = acc + r.y; acc = acc + r.z; acc = acc + r.w;
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+#pragma unroll
+            for (int u = 0; u < 8; u++) X[u] = Pn[u * 64 + sw[u & 3]];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                acc = acc + Y[u].x; acc = acc + Y[u].y; acc = acc + Y[u].z; acc = acc + Y[u].w;
             }
-            for (; qi < nfull; qi++) {
-                const float4 p = P[qi * 64];
-                acc = acc + p.x; acc = acc + p.y; acc = acc + p.z; acc = acc + p.w;
-            }
-            if (rem && q0 + nfull == nq && nfull < SV_QT) {
-                const float4 p = P[nfull * 64];
-                acc = acc + p.x;
-                if (rem > 1) acc = acc + p.y;
-                if (rem > 2) acc = acc + p.z;
+            sv_signal(&consumed, i + 1);
+        }
+        // the last tile, partly filled: nfull whole quads, then rem positions
+        if (ok && i < ntile) {
+            const float4 *P = ring + (i % SV_NP) * SV_QT * 64;
+#pragma unroll
+            for (int u = 0; u < 8; u++) Y[u] = P[(8 + u) * 64 + sw[u & 3]];
+            const int nfull = nq - i * SV_QT;
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                const float4 v = u < 8 ? X[u & 7] : Y[u & 7];
+                if (u < nfull) {
+                    acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
+                } else if (u == nfull && rem) {
+                    acc = acc + v.x;
+                    if (rem > 1) acc = acc + v.y;
+                    if (rem > 2) acc = acc + v.z;
+                }
             }
             sv_signal(&consumed, i + 1);
         }
@@ -707,6 +811,13 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
 
     // ---- loaders: tile i = li, li + SV_LOADERS, ...
     if (!sv_wait_ge(&a_ready, 1)) return;
+    float inv[G];
+    int nrm[G];
+#pragma unroll
+    for (int gg = 0; gg < G; gg++) {
+        inv[gg] = inv_s[gg];
+        nrm[gg] = nrm_s[gg];
+    }
     for (int i = li; i < ntile; i += SV_LOADERS) {
         const int inext = i + SV_LOADERS;
         if (DB && inext < ntile) {
@@ -724,12 +835,36 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
             const int qi = k * G + lq;                       // quad within the tile
             const int jq = min(i * SV_QT + qi, nq_all - 1);
             const float4 v = vcur[k];
+            // weights of head `mine` for this quad, normalised; with G = 2 or 4
+            // the lanes of a DPP quad hold the G heads and exchange them
+            const int mine = (lane - lq * DS) % G;
+            float4 am = ((const float4 *)(e + mine * estr))[jq];
+            if (nrm[mine]) {
+                const float iv = inv[mine];
+                am.x = am.x * iv; am.y = am.y * iv; am.z = am.z * iv; am.w = am.w * iv;
+            }
 #pragma unroll
             for (int gg = 0; gg < G; gg++) {
-                const float4 a = ((const float4 *)(e + gg * estr))[jq];
+                float4 a;
+                if (G == 2 || G == 4) {
+                    // quad_perm: every lane of a quad takes lane (quad base + gg)
+                    constexpr int c0 = 0;
+                    const int ctl = G == 4 ? gg * 0x55 : (gg ? 0xF5 : 0xA0);
+                    (void)c0;
+                    a.x = dpp_bcast(am.x, ctl);
+                    a.y = dpp_bcast(am.y, ctl);
+                    a.z = dpp_bcast(am.z, ctl);
+                    a.w = dpp_bcast(am.w, ctl);
+                } else {
+                    a = ((const float4 *)(e + gg * estr))[jq];
+                    if (nrm[gg]) {
+                        a.x = a.x * inv[gg]; a.y = a.y * inv[gg];
+                        a.z = a.z * inv[gg]; a.w = a.w * inv[gg];
+                    }
+                }
                 float4 p;
                 p.x = a.x * v.x; p.y = a.y * v.y; p.z = a.z * v.z; p.w = a.w * v.w;
-                P[qi * 64 + gg * DS + (lane - lq * DS)] = p;
+                P[qi * 64 + ((gg * DS + (lane - lq * DS)) ^ ((qi & 3) << 2))] = p;
             }
         }
         sv_signal(&ready[s], i);
@@ -797,7 +932,7 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
         FOX_LAUNCHED("attention scores");
         const int ds = (int)(64 / gqa);
         const int n_sl = (int)((head_dim + ds - 1) / ds);
-        const size_t e_bytes = gqa * att_stride * sizeof(float);
+        const size_t e_bytes = gqa * (att_stride + 4) * sizeof(float);
         const int ih = (int)n_head, ikv = (int)n_head_kv, ihd = (int)head_dim, ictx = (int)n_ctx;
         const void *sv = gqa == 1 ? (const void *)attn_sv_x<1>
                        : gqa == 2 ? (const void *)attn_sv_x<2>
