@@ -148,6 +148,36 @@ fox_gpu_status fox_gpu_gemv_i8(fox_gpu_ctx *ctx, const fox_gpu_tensor *w,
 fox_gpu_status fox_gpu_block_sums(fox_gpu_ctx *ctx, const fox_gpu_tensor *w,
                                   const int8_t *q, size_t M, int32_t *sums);
 
+/* One-launch stages of a decode layer (src/forward.c:399-478) for TQ1_0 and
+ * TQ2_0 weights: the input stage (RMSNorm, int8 quantisation) runs inside
+ * the GEMV's workgroups, results bit-identical to the separate calls.
+ * Other weight types return FOX_GPU_ERR_UNSUPPORTED (use the separate
+ * calls); so do activations too large for one workgroup's LDS.
+ *
+ * y_i = W_i rmsnorm(x, norm_w) for up to 4 matrices of one type and width
+ * (flags as fox_gpu_gemv; the attn_norm / ffn_norm + project steps). */
+fox_gpu_status fox_gpu_gemv_rmsnorm(fox_gpu_ctx *ctx, size_t n,
+                                    const fox_gpu_tensor *const *ws, const float *x,
+                                    size_t x_stride, size_t M, const float *norm_w,
+                                    float eps, float *const *outs,
+                                    const size_t *out_strides, unsigned flags);
+
+/* xb = rmsnorm(x, norm_w); q, k, v = W xb; RoPE on q and k at pos[0] + t;
+ * q -> q_out, k and v -> the layer's caches (layouts as fox_gpu_rope_store). */
+fox_gpu_status fox_gpu_qkv_rope(fox_gpu_ctx *ctx, const fox_gpu_tensor *wq,
+                                const fox_gpu_tensor *wk, const fox_gpu_tensor *wv,
+                                const float *x, size_t x_stride, size_t M,
+                                const float *norm_w, float eps, float *q_out,
+                                size_t q_stride, const float *cos_t, const float *sin_t,
+                                const uint32_t *pos, size_t n_ctx, float *k_cache,
+                                float *v_cache, size_t head_dim);
+
+/* xb = rmsnorm(x, norm_w); h = silu(W_gate xb) * (W_up xb). */
+fox_gpu_status fox_gpu_gate_up_silu(fox_gpu_ctx *ctx, const fox_gpu_tensor *w_gate,
+                                    const fox_gpu_tensor *w_up, const float *x,
+                                    size_t x_stride, size_t M, const float *norm_w,
+                                    float eps, float *h_out, size_t h_stride);
+
 /* Prepared activations: x quantised once for one weight type and width, in
  * its own device buffer, then applied to any number of matrices of that
  * type and width with one kernel launch each (fox_gpu_gemv_act).  Block

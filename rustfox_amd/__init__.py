@@ -83,6 +83,11 @@ def gpu_lib() -> C.CDLL:
                                vp, vp],
         "fox_gpu_attention": [vp, vp, sz, vp, sz, vp, vp, sz, sz, sz, sz, vp, sz, C.c_int],
         "fox_gpu_kv_write": [vp, vp, vp, sz, sz, sz, sz, vp, vp],
+        "fox_gpu_gemv_rmsnorm": [vp, sz, C.POINTER(vp), vp, sz, sz, vp, C.c_float,
+                                 C.POINTER(vp), C.POINTER(sz), C.c_uint],
+        "fox_gpu_qkv_rope": [vp, vp, vp, vp, vp, sz, sz, vp, C.c_float, vp, sz, vp, vp, vp, sz,
+                             vp, vp, sz],
+        "fox_gpu_gate_up_silu": [vp, vp, vp, vp, sz, sz, vp, C.c_float, vp, sz],
         "fox_gpu_silu_mul": [vp, vp, vp, sz, sz, sz],
         "fox_gpu_add": [vp, vp, vp, sz, sz, sz],
         "fox_gpu_argmax": [vp, vp, sz, vp, vp, C.c_uint32, vp],
@@ -270,6 +275,28 @@ class Gpu:
 
     def block_sums(self, w: Tensor, q: DeviceArray, M, sums: DeviceArray):
         _check(self.lib.fox_gpu_block_sums(self.ctx, w.h, q.ptr, M, sums.ptr))
+
+    def gemv_rmsnorm(self, ws, x: DeviceArray, M, norm: DeviceArray, eps, outs, flags=0):
+        n = len(ws)
+        wa = (C.c_void_p * n)(*[w.h for w in ws])
+        oa = (C.c_void_p * n)(*[o.ptr for o in outs])
+        sa = (C.c_size_t * n)(*[w.info()["ne1"] for w in ws])
+        K = ws[0].info()["ne0"]
+        _check(self.lib.fox_gpu_gemv_rmsnorm(self.ctx, n, wa, x.ptr, K, M, norm.ptr, eps, oa, sa,
+                                             flags))
+
+    def qkv_rope(self, wq, wk, wv, x: DeviceArray, M, norm: DeviceArray, eps, q_out: DeviceArray,
+                 cos_t: DeviceArray, sin_t: DeviceArray, pos: DeviceArray, n_ctx, kc: DeviceArray,
+                 vc: DeviceArray, head_dim):
+        K, nq = wq.info()["ne0"], wq.info()["ne1"]
+        _check(self.lib.fox_gpu_qkv_rope(self.ctx, wq.h, wk.h, wv.h, x.ptr, K, M, norm.ptr, eps,
+                                         q_out.ptr, nq, cos_t.ptr, sin_t.ptr, pos.ptr, n_ctx,
+                                         kc.ptr, vc.ptr, head_dim))
+
+    def gate_up_silu(self, wg, wu, x: DeviceArray, M, norm: DeviceArray, eps, h: DeviceArray):
+        K, ff = wg.info()["ne0"], wg.info()["ne1"]
+        _check(self.lib.fox_gpu_gate_up_silu(self.ctx, wg.h, wu.h, x.ptr, K, M, norm.ptr, eps,
+                                             h.ptr, ff))
 
     def kv_write(self, kc: DeviceArray, vc: DeviceArray, kv_dim, n_ctx, p0, k: DeviceArray,
                  v: DeviceArray, n):

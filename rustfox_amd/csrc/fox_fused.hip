@@ -1,0 +1,644 @@
+// fox_fused.hip -- one-launch GEMV stages of a decode layer for the ternary
+// formats (TQ1_0, TQ2_0): the activation input stage runs inside the GEMV.
+//
+// Every workgroup takes the f32 input (optionally RMS-normalised first),
+// quantises it to int8 exactly as src/gemv.c:11-42 does, and lays it out in
+// LDS as the MFMA B operand; the weight loads of its waves are already in
+// flight while it does so.  The per-block integer sums, the block-order
+// float combine and the final activation-scale multiply are those of
+// gemv_blocks (fox_gemv.hip), so results are bit-identical to it and to the
+// reference.  Epilogues:
+//   STORE  y (or out + y with FOX_GPU_GEMV_ACCUMULATE: the residual add of
+//          src/forward.c:374-377, 393-396);
+//   ROPE   segments q, k, v of one projection: RoPE on q and k
+//          (src/ops.c:56-73) at position pos[0] + t, q to its buffer, k and
+//          v into the layer's caches (src/forward.c:399-443);
+//   SILU   segments gate and up, one tile of each per workgroup:
+//          h = silu(gate) * up (src/ops.c:41-48);
+//   SUMS   per-block integer sums only (fox_gpu_block_sums).
+#include "fox_gemv_dev.h"
+#include "fox_math.h"
+
+#include <cstring>
+
+#define FW 8                    // waves per workgroup
+#define FWG (FW * 64)
+#define PF 4                    // weight blocks in flight per wave
+#define FUSED_LDS_MAX (96 * 1024)
+
+enum { IN_Q = 0, IN_F32 = 1, IN_NORM = 2 };
+enum { EPI_STORE = 0, EPI_ROPE = 1, EPI_SILU = 2, EPI_SUMS = 3 };
+
+struct FusedArgs {
+    const uint8_t *w[MAX_SEGS];
+    float *out[MAX_SEGS];
+    int out_stride[MAX_SEGS];
+    int n_rows[MAX_SEGS];
+    int tile_start[MAX_SEGS + 1];
+    int nseg, nb, M;
+    unsigned flags;
+    const float *x;
+    int x_stride;
+    const float *norm_w;
+    float eps;
+    const int8_t *q_in;
+    const float *scale_in;
+    int32_t *sums;
+    const float *rope_cos, *rope_sin;
+    const uint32_t *pos;
+    int head_dim, kv_dim, n_ctx;
+    float *k_cache, *v_cache;
+};
+
+// LDS carve-up (bytes), identical on host and device
+struct FusedLds {
+    int q, B, aux, terms, y, total;
+};
+
+__host__ __device__ inline FusedLds fused_lds(int fmt, int K, int M, int nslab)
+{
+    const int nb = K / 256;
+    FusedLds L;
+    int off = 0;
+    L.q = off;     off += (M * K + 15) & ~15;
+    L.B = off;     off += nb * M * b_bytes_per_block_tok(fmt);
+    L.aux = off;   off += ((nb * M * aux_per_block_tok(fmt) * 4) + 15) & ~15;
+    L.terms = off; off += nslab * nb * terms_per_block(fmt) * 16 * M * 4;
+    L.y = off;     off += nslab * 16 * M * 4;
+    L.total = off;
+    return L;
+}
+
+// ------------------------------------------------------------ input stage
+
+__device__ __forceinline__ double wave_sum_dd(double v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// src/ops.c:7-22 scale of one row, summed as a tree and certified (or
+// redone in index order by one thread); every thread returns it
+__device__ float rms_scale_wg(const float *__restrict__ xt, int n, float eps, double *dred,
+                              float *fred)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    double s = 0.0;
+    for (int i = tid; i < n; i += FWG) s += (double)xt[i] * (double)xt[i];
+    s = wave_sum_dd(s);
+    if (lane == 0) dred[wave] = s;
+    __syncthreads();
+    if (tid == 0) {
+        double tot = 0.0;
+        for (int w = 0; w < FW; w++) tot += dred[w];
+        const double rel = (double)(n + 64) * 0x1p-52;
+        const double y_hi = 1.0 / __builtin_sqrt(tot * (1.0 - rel) / (double)n + (double)eps) *
+                            (1.0 + 0x1p-50);
+        const double y_lo = 1.0 / __builtin_sqrt(tot * (1.0 + rel) / (double)n + (double)eps) *
+                            (1.0 - 0x1p-50);
+        const float f_hi = (float)y_hi, f_lo = (float)y_lo;
+        if (f_hi == f_lo) {
+            fred[0] = f_hi;
+        } else {
+            double seq = 0.0;
+            for (int i = 0; i < n; i++) seq += (double)xt[i] * (double)xt[i];
+            fred[0] = (float)(1.0 / __builtin_sqrt(seq / (double)n + (double)eps));
+        }
+    }
+    __syncthreads();
+    const float r = fred[0];
+    __syncthreads();
+    return r;
+}
+
+// Token t of the input, quantised per vector (src/gemv.c:11-42) into
+// q (LDS, K bytes); returns the activation scale amax / 127.
+template <int IN>
+__device__ float quantise_vector(const FusedArgs &a, int t, int K, int8_t *q, double *dred,
+                                 float *fred)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (IN == IN_Q) {
+        // block sums come without a scale (scale_in is NULL)
+        for (int i = tid; i < K; i += FWG) q[i] = a.q_in[(size_t)t * K + i];
+        return a.scale_in ? a.scale_in[t] : 0.0f;
+    }
+    const float *xt = a.x + (size_t)t * a.x_stride;
+    float rs = 1.0f;
+    if (IN == IN_NORM) rs = rms_scale_wg(xt, K, a.eps, dred, fred);
+    float m = 0.0f;
+    for (int i = tid; i < K; i += FWG) {
+        float v = xt[i];
+        if (IN == IN_NORM) v = v * rs * a.norm_w[i];      // src/ops.c:17: x * scale * w
+        const float av = fabsf(v);
+        if (av > m) m = av;
+    }
+    m = wave_max(m);
+    if (lane == 0) fred[1 + wave] = m;
+    __syncthreads();
+    float amax = 0.0f;
+    for (int w = 0; w < FW; w++) if (fred[1 + w] > amax) amax = fred[1 + w];
+    if (!(amax > 0.0f)) {
+        for (int i = tid; i < K; i += FWG) q[i] = 0;
+        __syncthreads();
+        return 0.0f;
+    }
+    const float inv = (float)(127.0 / (double)amax);
+    for (int i = tid; i < K; i += FWG) {
+        float v = xt[i];
+        if (IN == IN_NORM) v = v * rs * a.norm_w[i];
+        q[i] = quant_one(v, inv);
+    }
+    __syncthreads();
+    return (float)((double)amax / 127.0);
+}
+
+// B operand and per-block corrections of token t from q (LDS -> LDS), in the
+// layouts gemv_block reads (the act_prep layouts of fox_gemv.hip)
+template <int FMT>
+__device__ void build_b(const int8_t *__restrict__ qb0, int t, int M, int nb, uint8_t *B,
+                        int32_t *aux)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (FMT == FMT_TQ1) {
+        for (int it = tid; it < nb * 32; it += FWG) {
+            const int c = it & 1, g = (it >> 1) & 3, u = (it >> 3) & 3, b = it >> 5;
+            uint32_t w4[4];
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                uint32_t d = 0;
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    const int e = tq1_elem(4 * u + w, g, p, c);
+                    const uint32_t byte = e >= 0 ? (uint8_t)qb0[b * 256 + e] : 0u;
+                    d |= byte << (8 * p);
+                }
+                w4[w] = d;
+            }
+            const int off = ((((b * 4 + u) * 4 + g) * (2 * M) + 2 * t + c)) * 16;
+            *(uint4 *)(B + off) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
+        for (int b = wave; b < nb; b += FW) {
+            const int8_t *qb = qb0 + b * 256;
+            int s = qb[lane] + qb[lane + 64] + qb[lane + 128] + qb[lane + 192];
+            const int i4 = lane < 32 ? 128 + lane : lane < 48 ? 224 + (lane - 32) : -1;
+            int s4 = i4 >= 0 ? qb[i4] : 0;
+            s = wave_sum_i(s);
+            s4 = wave_sum_i(s4);
+            if (lane == 0) aux[b * M + t] = 128 * s4 - s;
+        }
+    } else {  // FMT_TQ2
+        for (int it = tid; it < nb * 16; it += FWG) {
+            const int g = it & 3, u = (it >> 2) & 3, b = it >> 4;
+            uint32_t w4[4];
+#pragma unroll
+            for (int l = 0; l < 4; l++) {
+                uint32_t d = 0;
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    const int m = 16 * g + 4 * u + p;
+                    const int e = (m >> 5) * 128 + l * 32 + (m & 31);
+                    d |= (uint32_t)(uint8_t)qb0[b * 256 + e] << (8 * p);
+                }
+                w4[l] = d;
+            }
+            const int off = (((b * 4 + u) * 4 + g) * M + t) * 16;
+            *(uint4 *)(B + off) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
+        for (int b = wave; b < nb; b += FW) {
+            const int8_t *qb = qb0 + b * 256;
+            const int s = wave_sum_i(qb[lane] + qb[lane + 64] + qb[lane + 128] + qb[lane + 192]);
+            if (lane == 0) aux[b * M + t] = -s;
+        }
+    }
+}
+
+// ------------------------------------------------------------ weights
+
+// one lane's bytes of one (tile, block) chunk
+struct RawBlk {
+    uint32_t d0, d1, d2, d3;   // TQ1: qs dwords d0..d2, qh byte in d3; TQ2: qs uint4
+    uint2 dd;                  // f16 scales of rows 4g .. 4g+3
+};
+
+template <int FMT>
+__device__ __forceinline__ RawBlk load_raw(const uint8_t *__restrict__ ch, int lane)
+{
+    RawBlk r;
+    const int g = lane >> 4;
+    if (FMT == FMT_TQ1) {
+        const uint32_t *qs = (const uint32_t *)(ch + 12 * lane);
+        r.d0 = qs[0];
+        r.d1 = qs[1];
+        r.d2 = qs[2];
+        r.d3 = ch[768 + lane];
+        r.dd = *(const uint2 *)(ch + 832 + 8 * g);
+    } else {
+        const uint4 v = *(const uint4 *)(ch + 16 * lane);
+        r.d0 = v.x;
+        r.d1 = v.y;
+        r.d2 = v.z;
+        r.d3 = v.w;
+        r.dd = *(const uint2 *)(ch + 1024 + 8 * g);
+    }
+    return r;
+}
+
+// integer block sums of rows 4g .. 4g+3 for the lane's B column; returns
+// S in acc[r] for lanes with j < ncol (ncol = 2M for TQ1, M for TQ2)
+template <int FMT>
+__device__ __forceinline__ void block_mfma(const RawBlk &r, const uint8_t *__restrict__ Bb,
+                                           int M, int lane, int corr, int S[4])
+{
+    const int g = lane >> 4, j = lane & 15;
+    const v4i zero = {0, 0, 0, 0};
+    v4i acc = zero;
+    if (FMT == FMT_TQ1) {
+        const bool bok = j < 2 * M;
+        v4i bv[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            bv[u] = bok ? *(const v4i *)(Bb + (((u * 4 + g) * (2 * M)) + j) * 16) : zero;
+        uint32_t av[16];
+        tq1_slots(r.d0, av);
+        tq1_slots(r.d1, av + 5);
+        tq1_slots(r.d2, av + 10);
+        av[15] = tq1_qh_slot(r.d3);
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            acc = mfma(av[4 * u], av[4 * u + 1], av[4 * u + 2], av[4 * u + 3], bv[u], acc);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int oth = __shfl_xor(acc[q], 1);
+            S[q] = acc[q] - 3 * oth + corr;
+        }
+    } else {
+        const bool bok = j < M;
+        const uint32_t dw[4] = {r.d0, r.d1, r.d2, r.d3};
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const v4i bv = bok ? *(const v4i *)(Bb + (((u * 4 + g) * M) + j) * 16) : zero;
+            const uint32_t d = dw[u];
+            acc = mfma(d & 0x03030303u, (d >> 2) & 0x03030303u, (d >> 4) & 0x03030303u,
+                       (d >> 6) & 0x03030303u, bv, acc);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) S[q] = acc[q] + corr;
+    }
+}
+
+// ------------------------------------------------------------ kernel
+
+template <int FMT, int IN, int EPI>
+__global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
+{
+    extern __shared__ uint4 fused_lds4[];
+    uint8_t *lds = (uint8_t *)fused_lds4;
+    __shared__ double dred[FW];
+    __shared__ float fred[1 + FW];
+    __shared__ float ascale[FOX_GPU_MAX_TOKENS];
+
+    constexpr int CHUNK = FMT == FMT_TQ1 ? TQ1_CHUNK : TQ2_CHUNK;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nb = a.nb, M = a.M, K = nb * 256;
+    const int nslab = EPI == EPI_SILU ? 2 : 1;
+    const FusedLds L = fused_lds(FMT, K, M, nslab);
+    int8_t *q = (int8_t *)(lds + L.q);
+    uint8_t *B = lds + L.B;
+    int32_t *aux = (int32_t *)(lds + L.aux);
+    float *terms = (float *)(lds + L.terms);
+    float *ybuf = (float *)(lds + L.y);
+
+    // ---- this workgroup's slabs (segment, tile)
+    int seg[2], tile[2];
+    if (EPI == EPI_SILU) {
+        seg[0] = 0;
+        seg[1] = 1;
+        tile[0] = tile[1] = blockIdx.x;
+    } else {
+        int s = 0;
+        while (s + 1 < a.nseg && (int)blockIdx.x >= a.tile_start[s + 1]) s++;
+        seg[0] = seg[1] = s;
+        tile[0] = tile[1] = blockIdx.x - a.tile_start[s];
+    }
+    const uint8_t *wt0 = a.w[seg[0]] + (size_t)tile[0] * nb * CHUNK;
+    const uint8_t *wt1 = a.w[seg[1]] + (size_t)tile[1] * nb * CHUNK;
+
+    // ---- issue the weight loads of this wave's first PF units (unit u =
+    // slab * nb + block; wave w takes w, w + FW, ...)
+    const int nunits = nslab * nb;
+    RawBlk raw[PF];
+#pragma unroll
+    for (int k = 0; k < PF; k++) {
+        const int u = wave + k * FW;
+        if (u < nunits) {
+            const int sl = u >= nb, b = u - sl * nb;
+            raw[k] = load_raw<FMT>((sl ? wt1 : wt0) + (size_t)b * CHUNK, lane);
+        }
+    }
+
+    // ---- input stage: int8 activations and the B operand in LDS
+    for (int t = 0; t < M; t++) {
+        const float s = quantise_vector<IN>(a, t, K, q + t * K, dred, fred);
+        if (tid == 0) ascale[t] = s;
+    }
+    __syncthreads();
+    for (int t = 0; t < M; t++) build_b<FMT>(q + t * K, t, M, nb, B, aux);
+    __syncthreads();
+
+    // ---- blocks: integer sums, then one float term per row and token
+    const int g = lane >> 4, j = lane & 15;
+    const int ncol = FMT == FMT_TQ1 ? 2 * M : M;
+    const int bbytes = b_bytes_per_block_tok(FMT) * M;
+    for (int k0 = 0; k0 * FW + wave < nunits; k0 += PF) {
+#pragma unroll
+        for (int k = 0; k < PF; k++) {
+            const int u = wave + (k0 + k) * FW;
+            if (u >= nunits) break;
+            const int sl = u >= nb, b = u - sl * nb;
+            const bool lead = FMT == FMT_TQ1 ? (j < ncol && !(j & 1)) : j < ncol;
+            const int tok = FMT == FMT_TQ1 ? j >> 1 : j;
+            const int corr = lead ? aux[b * M + tok] : 0;
+            int S[4];
+            block_mfma<FMT>(raw[k], B + b * bbytes, M, lane, corr, S);
+            const RawBlk rk = raw[k];
+            const int un = u + PF * FW;
+            if (un < nunits) {
+                const int sln = un >= nb, bn = un - sln * nb;
+                raw[k] = load_raw<FMT>((sln ? wt1 : wt0) + (size_t)bn * CHUNK, lane);
+            }
+            if (lead) {
+                const uint32_t hw[2] = {rk.dd.x, rk.dd.y};
+                const int nrows = a.n_rows[seg[sl]];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int row = 4 * g + r;
+                    if (EPI == EPI_SUMS) {
+                        const int grow = tile[sl] * 16 + row;
+                        if (grow < nrows) a.sums[((size_t)tok * nrows + grow) * nb + b] = S[r];
+                    } else {
+                        const float d = half_bits_to_float((hw[r >> 1] >> (16 * (r & 1))) & 0xFFFFu);
+                        terms[((sl * nb + b) * 16 + row) * M + tok] = d * (float)S[r];
+                    }
+                }
+            }
+        }
+    }
+    if (EPI == EPI_SUMS) return;
+    __syncthreads();
+
+    // ---- combine in block order, activation scale, epilogue
+    const int nthr = nslab * 16 * M;
+    const bool comb = tid < nthr;
+    const int sl = tid / (16 * M), rem = tid - sl * 16 * M;
+    const int ct = rem >> 4, crow = rem & 15;
+    float y = 0.0f;
+    if (comb) {
+        float acc = 0.0f;
+        for (int b = 0; b < nb; b++) acc = acc + terms[((sl * nb + b) * 16 + crow) * M + ct];
+        y = acc * ascale[ct];                               // src/gemv.c:70
+    }
+    const int s = seg[sl];
+    const int row = tile[sl] * 16 + crow;
+    if (EPI == EPI_STORE) {
+        if (comb && row < a.n_rows[s]) {
+            float *o = a.out[s] + (size_t)ct * a.out_stride[s] + row;
+            *o = (a.flags & FOX_GPU_GEMV_ACCUMULATE) ? *o + y : y;
+        }
+    } else if (EPI == EPI_SILU) {
+        if (comb) ybuf[tid] = y;
+        __syncthreads();
+        if (comb && sl == 0 && row < a.n_rows[0]) {
+            const float gt = y, up = ybuf[16 * M + rem];
+            a.out[0][(size_t)ct * a.out_stride[0] + row] =
+                fox_div(gt, 1.0f + fox_expf(-gt)) * up;     // src/ops.c:45-46
+        }
+    } else {  // EPI_ROPE: segment 0 q, 1 k, 2 v
+        const float partner = __shfl_xor(y, 1);
+        if (comb && row < a.n_rows[s]) {
+            const size_t p = (size_t)a.pos[0] + (size_t)ct;
+            const bool inside = p < (size_t)a.n_ctx;
+            float v = y;
+            if (s < 2 && inside) {
+                const int half = a.head_dim / 2;
+                const int i = (row % a.head_dim) >> 1;
+                const float c = a.rope_cos[p * half + i], sn = a.rope_sin[p * half + i];
+                // src/ops.c:64-69 on the pair (row & ~1, row | 1)
+                v = (row & 1) ? partner * sn + y * c : y * c - partner * sn;
+            }
+            if (s == 0) {
+                a.out[0][(size_t)ct * a.out_stride[0] + row] = v;
+            } else if (inside) {
+                const size_t kvd = (size_t)a.kv_dim;
+                if (s == 1) a.k_cache[p * kvd + row] = v;
+                else a.v_cache[((p >> 2) * kvd + row) * 4 + (p & 3)] = v;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------ host
+
+static fox_gpu_status fused_check(int type, size_t K, size_t M, int nslab, int *fmt)
+{
+    *fmt = fmt_of(type);
+    if (*fmt != FMT_TQ1 && *fmt != FMT_TQ2)
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "fused gemv: %s weights use the unfused path",
+                        fox_type_name(type));
+    if (K % 256 || K == 0) return fox_fail(FOX_GPU_ERR_ARG, "fused gemv: K %% 256 != 0");
+    if (M == 0 || M > FOX_GPU_MAX_TOKENS)
+        return fox_fail(FOX_GPU_ERR_ARG, "fused gemv: 1 to %d tokens", FOX_GPU_MAX_TOKENS);
+    if (fused_lds(*fmt, (int)K, (int)M, nslab).total > FUSED_LDS_MAX)
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "fused gemv: %zu x %zu activations exceed the "
+                        "workgroup's LDS", M, K);
+    return FOX_GPU_OK;
+}
+
+template <int FMT, int IN, int EPI>
+static fox_gpu_status fused_go(fox_gpu_ctx *ctx, const FusedArgs &a, int grid)
+{
+    const size_t lds = fused_lds(FMT, a.nb * 256, a.M, EPI == EPI_SILU ? 2 : 1).total;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute((const void *)gemv_fused<FMT, IN, EPI>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return fox_hip_fail(e, "fused gemv: LDS size");
+    }
+    hipLaunchKernelGGL((gemv_fused<FMT, IN, EPI>), dim3((unsigned)grid), dim3(FWG), lds,
+                       ctx->stream, a);
+    FOX_LAUNCHED("gemv_fused");
+    return FOX_GPU_OK;
+}
+
+template <int IN, int EPI>
+static fox_gpu_status fused_dispatch(fox_gpu_ctx *ctx, int fmt, const FusedArgs &a, int grid)
+{
+    return fmt == FMT_TQ1 ? fused_go<FMT_TQ1, IN, EPI>(ctx, a, grid)
+                          : fused_go<FMT_TQ2, IN, EPI>(ctx, a, grid);
+}
+
+static void fused_segments(FusedArgs &a, size_t n, const fox_gpu_tensor *const *ws,
+                           float *const *outs, const size_t *strides, size_t M, int *tiles)
+{
+    int t = 0;
+    for (size_t i = 0; i < n; i++) {
+        a.w[i] = ws[i]->d;
+        a.out[i] = outs ? outs[i] : nullptr;
+        a.out_stride[i] = strides ? (int)(M > 1 ? strides[i] : ws[i]->ne1) : 0;
+        a.n_rows[i] = (int)ws[i]->ne1;
+        a.tile_start[i] = t;
+        t += (int)ws[i]->n_tiles;
+    }
+    a.tile_start[n] = t;
+    a.nseg = (int)n;
+    *tiles = t;
+}
+
+// The fused entry for y_i = W_i x of the existing gemv calls (x f32 or int8);
+// returns FOX_GPU_ERR_UNSUPPORTED when the unfused path must run instead.
+fox_gpu_status fox_fused_gemv(fox_gpu_ctx *ctx, size_t n, const fox_gpu_tensor *const *ws,
+                              const float *x, size_t x_stride, const int8_t *q,
+                              const float *scale, size_t M, float *const *outs,
+                              const size_t *out_strides, unsigned flags, int32_t *sums)
+{
+    int fmt;
+    const size_t K = (size_t)ws[0]->ne0;
+    if (fmt_of(ws[0]->type) != FMT_TQ1 && fmt_of(ws[0]->type) != FMT_TQ2)
+        return FOX_GPU_ERR_UNSUPPORTED;
+    if (fused_lds(fmt_of(ws[0]->type), (int)K, (int)M, 1).total > FUSED_LDS_MAX)
+        return FOX_GPU_ERR_UNSUPPORTED;
+    fox_gpu_status st = fused_check(ws[0]->type, K, M, 1, &fmt);
+    if (st) return st;
+    FusedArgs a;
+    memset(&a, 0, sizeof(a));
+    int tiles;
+    fused_segments(a, n, ws, outs, out_strides, M, &tiles);
+    a.nb = (int)(K / 256);
+    a.M = (int)M;
+    a.flags = flags;
+    a.x = x;
+    a.x_stride = (int)(M > 1 ? x_stride : K);
+    a.q_in = q;
+    a.scale_in = scale;
+    a.sums = sums;
+    if ((!x && !q) || (!sums && (!outs || (q && !scale))))
+        return fox_fail(FOX_GPU_ERR_ARG, "fused gemv: missing activations, scale or output");
+    if (sums) return fused_dispatch<IN_Q, EPI_SUMS>(ctx, fmt, a, tiles);
+    if (q) return fused_dispatch<IN_Q, EPI_STORE>(ctx, fmt, a, tiles);
+    return fused_dispatch<IN_F32, EPI_STORE>(ctx, fmt, a, tiles);
+}
+
+extern "C" fox_gpu_status fox_gpu_gemv_rmsnorm(fox_gpu_ctx *ctx, size_t n,
+                                               const fox_gpu_tensor *const *ws, const float *x,
+                                               size_t x_stride, size_t M, const float *norm_w,
+                                               float eps, float *const *outs,
+                                               const size_t *out_strides, unsigned flags)
+{
+    if (!ctx || !ws || !x || !norm_w || !outs || !out_strides || n == 0 || n > MAX_SEGS)
+        return fox_fail(FOX_GPU_ERR_ARG, "gemv_rmsnorm: bad argument");
+    for (size_t i = 0; i < n; i++) {
+        if (!ws[i] || !outs[i]) return fox_fail(FOX_GPU_ERR_ARG, "gemv_rmsnorm: null tensor");
+        if (ws[i]->type != ws[0]->type || ws[i]->ne0 != ws[0]->ne0)
+            return fox_fail(FOX_GPU_ERR_ARG, "gemv_rmsnorm: matrices must share type and width");
+        if (M > 1 && out_strides[i] < ws[i]->ne1)
+            return fox_fail(FOX_GPU_ERR_ARG, "gemv_rmsnorm: output stride < rows");
+    }
+    const size_t K = (size_t)ws[0]->ne0;
+    if (M > 1 && x_stride < K) return fox_fail(FOX_GPU_ERR_ARG, "gemv_rmsnorm: input stride < K");
+    int fmt;
+    fox_gpu_status st = fused_check(ws[0]->type, K, M, 1, &fmt);
+    if (st) return st;
+    FusedArgs a;
+    memset(&a, 0, sizeof(a));
+    int tiles;
+    fused_segments(a, n, ws, outs, out_strides, M, &tiles);
+    a.nb = (int)(K / 256);
+    a.M = (int)M;
+    a.flags = flags;
+    a.x = x;
+    a.x_stride = (int)(M > 1 ? x_stride : K);
+    a.norm_w = norm_w;
+    a.eps = eps;
+    return fused_dispatch<IN_NORM, EPI_STORE>(ctx, fmt, a, tiles);
+}
+
+extern "C" fox_gpu_status fox_gpu_qkv_rope(fox_gpu_ctx *ctx, const fox_gpu_tensor *wq,
+                                           const fox_gpu_tensor *wk, const fox_gpu_tensor *wv,
+                                           const float *x, size_t x_stride, size_t M,
+                                           const float *norm_w, float eps, float *q_out,
+                                           size_t q_stride, const float *cos_t,
+                                           const float *sin_t, const uint32_t *pos,
+                                           size_t n_ctx, float *k_cache, float *v_cache,
+                                           size_t head_dim)
+{
+    if (!ctx || !wq || !wk || !wv || !x || !norm_w || !q_out || !cos_t || !sin_t || !pos ||
+        !k_cache || !v_cache || head_dim == 0 || n_ctx == 0)
+        return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: bad argument");
+    if (wq->type != wk->type || wk->type != wv->type || wq->ne0 != wk->ne0 ||
+        wk->ne0 != wv->ne0 || wk->ne1 != wv->ne1)
+        return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: q, k, v must share type and width, k and v "
+                        "their rows");
+    if (head_dim % 2 || wq->ne1 % head_dim || wk->ne1 % head_dim)
+        return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: rows are not whole heads of even size");
+    const size_t K = (size_t)wq->ne0;
+    if (M > 1 && (x_stride < K || q_stride < wq->ne1))
+        return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: stride too small");
+    if (n_ctx > 0x7fffffff) return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: n_ctx too large");
+    int fmt;
+    fox_gpu_status st = fused_check(wq->type, K, M, 1, &fmt);
+    if (st) return st;
+    const fox_gpu_tensor *ws[3] = {wq, wk, wv};
+    float *outs[3] = {q_out, nullptr, nullptr};
+    size_t strides[3] = {q_stride, 0, 0};
+    FusedArgs a;
+    memset(&a, 0, sizeof(a));
+    int tiles;
+    fused_segments(a, 3, ws, outs, strides, M, &tiles);
+    a.out_stride[0] = (int)(M > 1 ? q_stride : wq->ne1);
+    a.nb = (int)(K / 256);
+    a.M = (int)M;
+    a.x = x;
+    a.x_stride = (int)(M > 1 ? x_stride : K);
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.rope_cos = cos_t;
+    a.rope_sin = sin_t;
+    a.pos = pos;
+    a.head_dim = (int)head_dim;
+    a.kv_dim = (int)wk->ne1;
+    a.n_ctx = (int)n_ctx;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    return fused_dispatch<IN_NORM, EPI_ROPE>(ctx, fmt, a, tiles);
+}
+
+extern "C" fox_gpu_status fox_gpu_gate_up_silu(fox_gpu_ctx *ctx, const fox_gpu_tensor *wg,
+                                               const fox_gpu_tensor *wu, const float *x,
+                                               size_t x_stride, size_t M, const float *norm_w,
+                                               float eps, float *h_out, size_t h_stride)
+{
+    if (!ctx || !wg || !wu || !x || !norm_w || !h_out)
+        return fox_fail(FOX_GPU_ERR_ARG, "gate_up_silu: bad argument");
+    if (wg->type != wu->type || wg->ne0 != wu->ne0 || wg->ne1 != wu->ne1)
+        return fox_fail(FOX_GPU_ERR_ARG, "gate_up_silu: gate and up must have one shape and type");
+    const size_t K = (size_t)wg->ne0;
+    if (M > 1 && (x_stride < K || h_stride < wg->ne1))
+        return fox_fail(FOX_GPU_ERR_ARG, "gate_up_silu: stride too small");
+    int fmt;
+    fox_gpu_status st = fused_check(wg->type, K, M, 2, &fmt);
+    if (st) return st;
+    const fox_gpu_tensor *ws[2] = {wg, wu};
+    float *outs[2] = {h_out, nullptr};
+    size_t strides[2] = {h_stride, h_stride};
+    FusedArgs a;
+    memset(&a, 0, sizeof(a));
+    int tiles;
+    fused_segments(a, 2, ws, outs, strides, M, &tiles);
+    a.nb = (int)(K / 256);
+    a.M = (int)M;
+    a.x = x;
+    a.x_stride = (int)(M > 1 ? x_stride : K);
+    a.norm_w = norm_w;
+    a.eps = eps;
+    return fused_dispatch<IN_NORM, EPI_SILU>(ctx, fmt, a, (int)wg->n_tiles);
+}

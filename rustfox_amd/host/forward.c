@@ -1,11 +1,11 @@
 /* forward.c -- fox_eval on the GPU (RustFox src/forward.c:137-519 semantics).
  *
  * One decode pass, per layer (src/forward.c:399-478):
- *   xb = rmsnorm(x, attn_norm); q, k, v = W xb (one launch, one quantisation);
- *   rope(q, k) at pos + t and store k, v in the layer's cache;
+ *   xb = rmsnorm(x, attn_norm); q, k, v = W xb; rope(q, k) at pos + t and
+ *   store k, v in the layer's cache (one launch for ternary weights);
  *   xb = attention; x += W_o xb (residual fused into the gemv);
- *   xb = rmsnorm(x, ffn_norm); hb, hb2 = W_gate xb, W_up xb (one launch);
- *   hb = silu(hb) * hb2; x += W_down hb.
+ *   xb = rmsnorm(x, ffn_norm); hb = silu(W_gate xb) * (W_up xb) (one launch
+ *   for ternary weights); x += W_down hb.
  * then xb = rmsnorm(x_last, output_norm) and logits = W_out xb.
  *
  * The K cache is f32 [n_layer][n_ctx][n_head_kv * head_dim] as in the
@@ -297,6 +297,7 @@ static fox_status forward_pass(fox_context *c, size_t M, int want_logits)
     const size_t vl = FOX_GPU_V_CACHE_FLOATS(c->cfg.n_ctx, c->nkv);
     uint32_t l;
     fox_status st;
+    fox_gpu_status gs;
 
     GPU(fox_gpu_get_rows(c->gpu, c->embd, c->dtok, M, c->x, c->d, NULL), "forward: embed");
     for (l = 0; l < mi->n_layer; l++) {
@@ -308,23 +309,39 @@ static fox_status forward_pass(fox_context *c, size_t M, int want_logits)
         float *gu_out[2] = { c->hb, c->hb2 };
         size_t gu_str[2] = { c->ff, c->ff };
 
-        GPU(fox_gpu_rmsnorm(c->gpu, c->xb, c->wide, c->x, c->d, D->attn_norm, c->d, M,
-                            mi->rms_eps), "forward: attn_norm");
-        if ((st = project_group(c, 3, qkv, c->xb, c->wide, M, qkv_out, qkv_str)) != FOX_OK)
-            return st;
-        GPU(fox_gpu_rope_store(c->gpu, c->q, c->nq, c->k, c->nkv, c->v, c->nkv, mi->n_head,
-                               mi->n_head_kv, c->hd, M, c->rc, c->rs, c->dpos, c->cfg.n_ctx,
-                               c->kc + l * kvl, c->vc + l * vl), "forward: rope");
+        /* ternary layers: norm, quantisation, q/k/v and RoPE + cache store in
+         * one launch; other types (or activations too wide for one
+         * workgroup) take the separate steps */
+        gs = fox_gpu_qkv_rope(c->gpu, D->attn_q, D->attn_k, D->attn_v, c->x, c->d, M,
+                              D->attn_norm, mi->rms_eps, c->q, c->nq, c->rc, c->rs, c->dpos,
+                              c->cfg.n_ctx, c->kc + l * kvl, c->vc + l * vl, c->hd);
+        if (gs == FOX_GPU_ERR_UNSUPPORTED) {
+            GPU(fox_gpu_rmsnorm(c->gpu, c->xb, c->wide, c->x, c->d, D->attn_norm, c->d, M,
+                                mi->rms_eps), "forward: attn_norm");
+            if ((st = project_group(c, 3, qkv, c->xb, c->wide, M, qkv_out, qkv_str)) != FOX_OK)
+                return st;
+            GPU(fox_gpu_rope_store(c->gpu, c->q, c->nq, c->k, c->nkv, c->v, c->nkv, mi->n_head,
+                                   mi->n_head_kv, c->hd, M, c->rc, c->rs, c->dpos, c->cfg.n_ctx,
+                                   c->kc + l * kvl, c->vc + l * vl), "forward: rope");
+        } else if (gs != FOX_GPU_OK) {
+            return fox_gpu_failed(gs, "forward: q/k/v");
+        }
         GPU(fox_gpu_attention(c->gpu, c->xb, c->wide, c->q, c->nq, c->kc + l * kvl,
                               c->vc + l * vl, mi->n_head, mi->n_head_kv, c->hd, M, c->dpos,
                               c->cfg.n_ctx, c->attn_mode), "forward: attention");
         GPU(fox_gpu_gemv(c->gpu, D->attn_out, c->xb, c->wide, M, c->x, c->d,
                          FOX_GPU_GEMV_ACCUMULATE), "forward: attn_output");
-        GPU(fox_gpu_rmsnorm(c->gpu, c->xb, c->wide, c->x, c->d, D->ffn_norm, c->d, M,
-                            mi->rms_eps), "forward: ffn_norm");
-        if ((st = project_group(c, 2, gu, c->xb, c->wide, M, gu_out, gu_str)) != FOX_OK)
-            return st;
-        GPU(fox_gpu_silu_mul(c->gpu, c->hb, c->hb2, c->ff, M, c->ff), "forward: swiglu");
+        gs = fox_gpu_gate_up_silu(c->gpu, D->ffn_gate, D->ffn_up, c->x, c->d, M, D->ffn_norm,
+                                  mi->rms_eps, c->hb, c->ff);
+        if (gs == FOX_GPU_ERR_UNSUPPORTED) {
+            GPU(fox_gpu_rmsnorm(c->gpu, c->xb, c->wide, c->x, c->d, D->ffn_norm, c->d, M,
+                                mi->rms_eps), "forward: ffn_norm");
+            if ((st = project_group(c, 2, gu, c->xb, c->wide, M, gu_out, gu_str)) != FOX_OK)
+                return st;
+            GPU(fox_gpu_silu_mul(c->gpu, c->hb, c->hb2, c->ff, M, c->ff), "forward: swiglu");
+        } else if (gs != FOX_GPU_OK) {
+            return fox_gpu_failed(gs, "forward: gate/up");
+        }
         GPU(fox_gpu_gemv(c->gpu, D->ffn_down, c->hb, c->ff, M, c->x, c->d,
                          FOX_GPU_GEMV_ACCUMULATE), "forward: ffn_down");
     }

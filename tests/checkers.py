@@ -136,6 +136,23 @@ class Oracle:
                                       rows, cols, out) == 0
         return out
 
+    def rmsnorm(self, x, w, eps):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty_like(x)
+        self.lib.or_rmsnorm(out, x, np.ascontiguousarray(w, np.float32), x.size, eps)
+        return out
+
+    def rope(self, vec, n_heads, head_dim, cos_row, sin_row):
+        v = np.array(vec, dtype=np.float32)
+        self.lib.or_rope(v, n_heads, head_dim, np.ascontiguousarray(cos_row, np.float32),
+                         np.ascontiguousarray(sin_row, np.float32))
+        return v
+
+    def silu_mul(self, gate, up):
+        g = np.array(gate, dtype=np.float32)
+        self.lib.or_silu_mul(g, np.ascontiguousarray(up, np.float32), g.size)
+        return g
+
     def softmax(self, x):
         x = np.array(x, dtype=np.float32)
         self.lib.or_softmax(x, x.size)

@@ -1,0 +1,122 @@
+"""One-launch decode-layer stages (fox_gpu_gemv_rmsnorm, fox_gpu_qkv_rope,
+fox_gpu_gate_up_silu) against the oracle's separate steps: RMSNorm
+(src/ops.c:7-22), the quantised GEMV (src/gemv.c), RoPE (src/ops.c:56-73),
+the cache store (src/forward.c:427-443) and SwiGLU (src/ops.c:41-48).
+Outputs must be bit-identical."""
+import numpy as np
+import pytest
+
+import rustfox_amd as rf
+from test_gpu_gemv import weights, bits
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-5
+
+
+def ref_norm_gemv(oracle, gtype, x, nw, W, N, K):
+    return np.stack([oracle.gemv(gtype, oracle.rmsnorm(x[t], nw, EPS), W, N, K)
+                     for t in range(x.shape[0])])
+
+
+@pytest.mark.parametrize("tname,gtype", [("TQ1_0", 34), ("TQ2_0", 35)])
+@pytest.mark.parametrize("K,M,accumulate", [(2560, 1, False), (4096, 1, True), (768, 3, False),
+                                            (512, 8, True)])
+def test_gemv_rmsnorm_bit_exact(gpu, oracle, tname, gtype, K, M, accumulate):
+    rng = np.random.default_rng(K * 10 + M)
+    Ns = [48, 37]
+    Ws = [weights(rng, gtype, N, K) for N in Ns]
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    ts = [gpu.tensor(gtype, K, N, w) for N, w in zip(Ns, Ws)]
+    init = [rng.standard_normal((M, N)).astype(np.float32) for N in Ns]
+    outs = [gpu.array(i if accumulate else np.zeros_like(i)) for i in init]
+    gpu.gemv_rmsnorm(ts, gpu.array(x), M, gpu.array(nw), EPS, outs,
+                     rf.GEMV_ACCUMULATE if accumulate else 0)
+    gpu.sync()
+    for N, W, o, i in zip(Ns, Ws, outs, init):
+        want = ref_norm_gemv(oracle, gtype, x, nw, W, N, K)
+        if accumulate:
+            want = i + want
+        assert np.array_equal(bits(o.numpy()), bits(want)), tname
+
+
+@pytest.mark.parametrize("gtype", [34, 35])
+@pytest.mark.parametrize("M,pos", [(1, 5), (3, 36), (2, 39)])
+def test_qkv_rope_bit_exact(gpu, oracle, gtype, M, pos):
+    """q, k, v projections of rmsnorm(x), RoPE at pos + t, k and v rows into
+    the caches; a token at or past n_ctx is neither rotated nor stored."""
+    K, n_head, n_kv, hd, n_ctx = 768, 4, 2, 64, 40
+    rng = np.random.default_rng(100 + M + pos + gtype)
+    Wq, Wk, Wv = (weights(rng, gtype, n, K) for n in (n_head * hd, n_kv * hd, n_kv * hd))
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    cos_t, sin_t = oracle.rope_tables(n_ctx, hd, 10000.0)
+    kvd = n_kv * hd
+    q_out = gpu.empty(M * n_head * hd, np.float32)
+    kc = gpu.array(np.zeros(n_ctx * kvd, np.float32))
+    vc = gpu.array(np.zeros((n_ctx + 3) // 4 * 4 * kvd, np.float32))
+    gpu.qkv_rope(gpu.tensor(gtype, K, n_head * hd, Wq), gpu.tensor(gtype, K, kvd, Wk),
+                 gpu.tensor(gtype, K, kvd, Wv), gpu.array(x), M, gpu.array(nw), EPS, q_out,
+                 gpu.array(cos_t), gpu.array(sin_t), gpu.array(np.array([pos], np.uint32)),
+                 n_ctx, kc, vc, hd)
+    gpu.sync()
+    got_q = q_out.numpy().reshape(M, -1)
+    got_k = kc.numpy().reshape(n_ctx, kvd)
+    vq = vc.numpy().reshape(-1, kvd, 4)
+    got_v = np.stack([vq[p // 4, :, p % 4] for p in range(n_ctx)])
+    want_k = np.zeros((n_ctx, kvd), np.float32)
+    want_v = np.zeros((n_ctx, kvd), np.float32)
+    half = hd // 2
+    for t in range(M):
+        xb = oracle.rmsnorm(x[t], nw, EPS)
+        q = oracle.gemv(gtype, xb, Wq, n_head * hd, K)
+        k = oracle.gemv(gtype, xb, Wk, kvd, K)
+        v = oracle.gemv(gtype, xb, Wv, kvd, K)
+        p = pos + t
+        if p < n_ctx:
+            cr, sr = cos_t[p * half:(p + 1) * half], sin_t[p * half:(p + 1) * half]
+            q = oracle.rope(q, n_head, hd, cr, sr)
+            want_k[p] = oracle.rope(k, n_kv, hd, cr, sr)
+            want_v[p] = v
+        assert np.array_equal(bits(got_q[t]), bits(q)), f"q of token {t}"
+    assert np.array_equal(bits(got_k), bits(want_k))
+    assert np.array_equal(bits(got_v), bits(want_v))
+
+
+@pytest.mark.parametrize("gtype", [34, 35])
+@pytest.mark.parametrize("K,ff,M", [(2560, 700, 1), (768, 1040, 2), (512, 96, 8)])
+def test_gate_up_silu_bit_exact(gpu, oracle, gtype, K, ff, M):
+    rng = np.random.default_rng(K + ff + M + gtype)
+    Wg, Wu = weights(rng, gtype, ff, K), weights(rng, gtype, ff, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    h = gpu.empty(M * ff, np.float32)
+    gpu.gate_up_silu(gpu.tensor(gtype, K, ff, Wg), gpu.tensor(gtype, K, ff, Wu), gpu.array(x), M,
+                     gpu.array(nw), EPS, h)
+    gpu.sync()
+    got = h.numpy().reshape(M, ff)
+    for t in range(M):
+        xb = oracle.rmsnorm(x[t], nw, EPS)
+        want = oracle.silu_mul(oracle.gemv(gtype, xb, Wg, ff, K), oracle.gemv(gtype, xb, Wu, ff, K))
+        assert np.array_equal(bits(got[t]), bits(want)), f"token {t}"
+
+
+def test_unsupported_cases_say_so(gpu):
+    """K-quants, and activations too wide for one workgroup, are refused with
+    FOX_GPU_ERR_UNSUPPORTED (the host then runs the separate steps)."""
+    rng = np.random.default_rng(3)
+    q4 = gpu.tensor(12, 512, 16, weights(rng, 12, 16, 512))
+    x = gpu.array(rng.standard_normal(512).astype(np.float32))
+    nw = gpu.array(np.ones(512, np.float32))
+    out = gpu.empty(16, np.float32)
+    with pytest.raises(rf.FoxError) as e:
+        gpu.gemv_rmsnorm([q4], x, 1, nw, EPS, [out])
+    assert e.value.status == 5
+    K = 9728
+    t = gpu.tensor(34, K, 16, weights(rng, 34, 16, K))
+    xw = gpu.array(rng.standard_normal((8, K)).astype(np.float32))
+    with pytest.raises(rf.FoxError) as e:
+        gpu.gemv_rmsnorm([t], xw, 8, gpu.array(np.ones(K, np.float32)), EPS,
+                         [gpu.empty(8 * 16, np.float32)])
+    assert e.value.status == 5
