@@ -60,7 +60,7 @@ __host__ __device__ inline FusedLds fused_lds(int fmt, int K, int M, int nslab)
     const int nb = K / 256;
     FusedLds L;
     int off = 0;
-    L.q = off;     off += (M * K + 15) & ~15;
+    L.q = off;
     L.B = off;     off += nb * M * b_bytes_per_block_tok(fmt);
     L.aux = off;   off += ((nb * M * aux_per_block_tok(fmt) * 4) + 15) & ~15;
     L.terms = off; off += nslab * nb * terms_per_block(fmt) * 16 * M * 4;
@@ -78,140 +78,192 @@ __device__ __forceinline__ double wave_sum_dd(double v)
     return v;
 }
 
-// src/ops.c:7-22 scale of one row, summed as a tree and certified (or
-// redone in index order by one thread); every thread returns it
-__device__ float rms_scale_wg(const float *__restrict__ xt, int n, float eps, double *dred,
-                              float *fred)
+#define R4_LIMIT 8              // input dwords per thread: K <= 4 * R4_LIMIT * FWG
+
+__device__ __forceinline__ uint32_t pack_q4(float4 v, float inv)
 {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    double s = 0.0;
-    for (int i = tid; i < n; i += FWG) s += (double)xt[i] * (double)xt[i];
-    s = wave_sum_dd(s);
-    if (lane == 0) dred[wave] = s;
-    __syncthreads();
-    if (tid == 0) {
-        double tot = 0.0;
-        for (int w = 0; w < FW; w++) tot += dred[w];
-        const double rel = (double)(n + 64) * 0x1p-52;
-        const double y_hi = 1.0 / __builtin_sqrt(tot * (1.0 - rel) / (double)n + (double)eps) *
-                            (1.0 + 0x1p-50);
-        const double y_lo = 1.0 / __builtin_sqrt(tot * (1.0 + rel) / (double)n + (double)eps) *
-                            (1.0 - 0x1p-50);
-        const float f_hi = (float)y_hi, f_lo = (float)y_lo;
-        if (f_hi == f_lo) {
-            fred[0] = f_hi;
-        } else {
-            double seq = 0.0;
-            for (int i = 0; i < n; i++) seq += (double)xt[i] * (double)xt[i];
-            fred[0] = (float)(1.0 / __builtin_sqrt(seq / (double)n + (double)eps));
-        }
-    }
-    __syncthreads();
-    const float r = fred[0];
-    __syncthreads();
-    return r;
+    return (uint32_t)(uint8_t)quant_one(v.x, inv) | (uint32_t)(uint8_t)quant_one(v.y, inv) << 8 |
+           (uint32_t)(uint8_t)quant_one(v.z, inv) << 16 |
+           (uint32_t)(uint8_t)quant_one(v.w, inv) << 24;
 }
 
-// Token t of the input, quantised per vector (src/gemv.c:11-42) into
-// q (LDS, K bytes); returns the activation scale amax / 127.
-template <int IN>
-__device__ float quantise_vector(const FusedArgs &a, int t, int K, int8_t *q, double *dred,
-                                 float *fred)
+__device__ __forceinline__ int sum_q4(uint32_t d)
 {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (IN == IN_Q) {
-        // block sums come without a scale (scale_in is NULL)
-        for (int i = tid; i < K; i += FWG) q[i] = a.q_in[(size_t)t * K + i];
-        return a.scale_in ? a.scale_in[t] : 0.0f;
-    }
-    const float *xt = a.x + (size_t)t * a.x_stride;
-    float rs = 1.0f;
-    if (IN == IN_NORM) rs = rms_scale_wg(xt, K, a.eps, dred, fred);
-    float m = 0.0f;
-    for (int i = tid; i < K; i += FWG) {
-        float v = xt[i];
-        if (IN == IN_NORM) v = v * rs * a.norm_w[i];      // src/ops.c:17: x * scale * w
-        const float av = fabsf(v);
-        if (av > m) m = av;
-    }
-    m = wave_max(m);
-    if (lane == 0) fred[1 + wave] = m;
-    __syncthreads();
-    float amax = 0.0f;
-    for (int w = 0; w < FW; w++) if (fred[1 + w] > amax) amax = fred[1 + w];
-    if (!(amax > 0.0f)) {
-        for (int i = tid; i < K; i += FWG) q[i] = 0;
-        __syncthreads();
-        return 0.0f;
-    }
-    const float inv = (float)(127.0 / (double)amax);
-    for (int i = tid; i < K; i += FWG) {
-        float v = xt[i];
-        if (IN == IN_NORM) v = v * rs * a.norm_w[i];
-        q[i] = quant_one(v, inv);
-    }
-    __syncthreads();
-    return (float)((double)amax / 127.0);
+    return (int)(int8_t)d + (int)(int8_t)(d >> 8) + (int)(int8_t)(d >> 16) + (int)(int8_t)(d >> 24);
 }
 
-// B operand and per-block corrections of token t from q (LDS -> LDS), in the
-// layouts gemv_block reads (the act_prep layouts of fox_gemv.hip)
+// Place the int8 dword of block-local dword index dl (elements 4dl..4dl+3)
+// of block b, token t, into the B operand: the layouts of act_prep
+// (fox_gemv.hip), which mirror the A slots of the block decode.
 template <int FMT>
-__device__ void build_b(const int8_t *__restrict__ qb0, int t, int M, int nb, uint8_t *B,
-                        int32_t *aux)
+__device__ __forceinline__ void put_b(uint8_t *B, int M, int b, int t, int dl, uint32_t d)
+{
+    if (FMT == FMT_TQ1) {
+        // B entry (b, u, g, column 2t + c) is 16 bytes; dword w is slot s = 4u + w
+        auto at = [&](int s, int g, int c) -> uint8_t * {
+            return B + ((((b * 4 + (s >> 2)) * 4 + g) * (2 * M) + 2 * t + c) * 16) + (s & 3) * 4;
+        };
+        if (dl < 60) {
+            int lev, g, sec;
+            if (dl < 40) {
+                lev = dl >> 3;
+                g = (dl & 7) >> 1;
+                sec = dl & 1;
+            } else {
+                lev = (dl - 40) >> 2;
+                g = (dl - 40) & 3;
+                sec = 2;
+            }
+            // column 0 pairs level lev with slot level lev + 1, column 1 with lev
+            *(uint32_t *)at(5 * sec + lev, g, 0) = d;
+            if (lev >= 1) *(uint32_t *)at(5 * sec + lev - 1, g, 1) = d;
+            if (lev == 4) *(uint32_t *)at(5 * sec + 4, g, 1) = 0u;
+        } else {
+            // qh elements 240 + 4 lev + g: byte g of dword lev; slot 15 byte lev
+            // (column 0) and byte lev - 1 (column 1; byte 3 of column 1 is 0)
+            const int lev = dl - 60;
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const uint8_t v = (uint8_t)(d >> (8 * g));
+                at(15, g, 0)[lev] = v;
+                if (lev >= 1) at(15, g, 1)[lev - 1] = v;
+                if (lev == 3) at(15, g, 1)[3] = 0;
+            }
+        }
+    } else {  // FMT_TQ2: elements e0 = 4 dl .. : half (g >> 1), level l, offset 16 (g & 1) + 4 u
+        const int e0 = 4 * dl;
+        const int half = e0 >> 7, l = (e0 >> 5) & 3, off = e0 & 31;
+        const int g = 2 * half + (off >> 4), u = (off & 15) >> 2;
+        *(uint32_t *)(B + (((b * 4 + u) * 4 + g) * M + t) * 16 + l * 4) = d;
+    }
+}
+
+// Token t of the input: optional RMSNorm (src/ops.c:7-22), per-vector int8
+// quantisation (src/gemv.c:11-42) and the B operand and per-block
+// corrections in LDS, in one pass over the input.  Thread tid owns input
+// dwords m = tid + FWG r; dword m lies in block m / 64, so a wave owns the
+// 64 dwords of a block and block sums are wave sums.  Returns amax / 127.
+template <int FMT, int IN, int R4MAX>
+__device__ float quantise_to_b(const FusedArgs &a, int t, int K, uint8_t *B, int32_t *aux,
+                               double *dred, float *fred)
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (FMT == FMT_TQ1) {
-        for (int it = tid; it < nb * 32; it += FWG) {
-            const int c = it & 1, g = (it >> 1) & 3, u = (it >> 3) & 3, b = it >> 5;
-            uint32_t w4[4];
+    const int M = a.M, nd = K >> 2;
+    uint32_t qd[R4MAX];
+    float act = 0.0f;
+    if (IN == IN_Q) {
+        const uint32_t *q4 = (const uint32_t *)(a.q_in + (size_t)t * K);
 #pragma unroll
-            for (int w = 0; w < 4; w++) {
-                uint32_t d = 0;
-#pragma unroll
-                for (int p = 0; p < 4; p++) {
-                    const int e = tq1_elem(4 * u + w, g, p, c);
-                    const uint32_t byte = e >= 0 ? (uint8_t)qb0[b * 256 + e] : 0u;
-                    d |= byte << (8 * p);
-                }
-                w4[w] = d;
-            }
-            const int off = ((((b * 4 + u) * 4 + g) * (2 * M) + 2 * t + c)) * 16;
-            *(uint4 *)(B + off) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        for (int r = 0; r < R4MAX; r++) {
+            const int m = tid + r * FWG;
+            qd[r] = m < nd ? q4[m] : 0u;
         }
-        for (int b = wave; b < nb; b += FW) {
-            const int8_t *qb = qb0 + b * 256;
-            int s = qb[lane] + qb[lane + 64] + qb[lane + 128] + qb[lane + 192];
-            const int i4 = lane < 32 ? 128 + lane : lane < 48 ? 224 + (lane - 32) : -1;
-            int s4 = i4 >= 0 ? qb[i4] : 0;
+        act = a.scale_in ? a.scale_in[t] : 0.0f;    // block sums come without a scale
+    } else {
+        const float4 *x4 = (const float4 *)(a.x + (size_t)t * a.x_stride);
+        const float4 *w4 = (const float4 *)a.norm_w;
+        float4 xv[R4MAX];
+        const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int r = 0; r < R4MAX; r++) {
+            const int m = tid + r * FWG;
+            xv[r] = m < nd ? x4[m] : z4;
+        }
+        if (IN == IN_NORM) {
+            float4 wv[R4MAX];
+#pragma unroll
+            for (int r = 0; r < R4MAX; r++) {
+                const int m = tid + r * FWG;
+                wv[r] = m < nd ? w4[m] : z4;
+            }
+            double ss = 0.0;
+#pragma unroll
+            for (int r = 0; r < R4MAX; r++) {
+                ss += (double)xv[r].x * (double)xv[r].x;
+                ss += (double)xv[r].y * (double)xv[r].y;
+                ss += (double)xv[r].z * (double)xv[r].z;
+                ss += (double)xv[r].w * (double)xv[r].w;
+            }
+            ss = wave_sum_dd(ss);
+            if (lane == 0) dred[wave] = ss;
+            __syncthreads();
+            if (tid == 0) {
+                double tot = 0.0;
+                for (int w = 0; w < FW; w++) tot += dred[w];
+                // the tree sum certifies the float scale of the reference's
+                // index-order double sum (it lies within (K + 64) 2^-52 tot),
+                // else one thread redoes that sum
+                const double rel = (double)(K + 64) * 0x1p-52;
+                const double y_hi = 1.0 / __builtin_sqrt(tot * (1.0 - rel) / (double)K +
+                                                         (double)a.eps) * (1.0 + 0x1p-50);
+                const double y_lo = 1.0 / __builtin_sqrt(tot * (1.0 + rel) / (double)K +
+                                                         (double)a.eps) * (1.0 - 0x1p-50);
+                const float f_hi = (float)y_hi, f_lo = (float)y_lo;
+                if (f_hi == f_lo) {
+                    fred[0] = f_hi;
+                } else {
+                    const float *xt = a.x + (size_t)t * a.x_stride;
+                    double seq = 0.0;
+                    for (int i = 0; i < K; i++) seq += (double)xt[i] * (double)xt[i];
+                    fred[0] = (float)(1.0 / __builtin_sqrt(seq / (double)K + (double)a.eps));
+                }
+            }
+            __syncthreads();
+            const float rs = fred[0];
+#pragma unroll
+            for (int r = 0; r < R4MAX; r++) {           // src/ops.c:17: x * scale * w
+                xv[r].x = xv[r].x * rs * wv[r].x;
+                xv[r].y = xv[r].y * rs * wv[r].y;
+                xv[r].z = xv[r].z * rs * wv[r].z;
+                xv[r].w = xv[r].w * rs * wv[r].w;
+            }
+        }
+        float m = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R4MAX; r++) {
+            const float v4[4] = {xv[r].x, xv[r].y, xv[r].z, xv[r].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float av = fabsf(v4[e]);
+                if (av > m) m = av;
+            }
+        }
+        m = wave_max(m);
+        if (lane == 0) fred[1 + wave] = m;
+        __syncthreads();
+        float amax = 0.0f;
+        for (int w = 0; w < FW; w++) if (fred[1 + w] > amax) amax = fred[1 + w];
+        if (amax > 0.0f) {
+            const float inv = (float)(127.0 / (double)amax);
+#pragma unroll
+            for (int r = 0; r < R4MAX; r++) qd[r] = pack_q4(xv[r], inv);
+            act = (float)((double)amax / 127.0);
+        } else {
+#pragma unroll
+            for (int r = 0; r < R4MAX; r++) qd[r] = 0u;
+        }
+    }
+    // B operand and per-block corrections
+#pragma unroll
+    for (int r = 0; r < R4MAX; r++) {
+        const int m = tid + r * FWG;
+        if (r * FWG >= nd) break;                      // uniform: no block left
+        const int b = m >> 6, dl = lane;               // m & 63 == lane
+        if (m < nd) put_b<FMT>(B, M, b, t, dl, qd[r]);
+        int s = m < nd ? sum_q4(qd[r]) : 0;
+        if (FMT == FMT_TQ1) {
+            // corr = 128 * (sum of elements 128..159 and 224..239) - block sum
+            int s4 = ((dl >= 32 && dl < 40) || (dl >= 56 && dl < 60)) ? s : 0;
             s = wave_sum_i(s);
             s4 = wave_sum_i(s4);
-            if (lane == 0) aux[b * M + t] = 128 * s4 - s;
-        }
-    } else {  // FMT_TQ2
-        for (int it = tid; it < nb * 16; it += FWG) {
-            const int g = it & 3, u = (it >> 2) & 3, b = it >> 4;
-            uint32_t w4[4];
-#pragma unroll
-            for (int l = 0; l < 4; l++) {
-                uint32_t d = 0;
-#pragma unroll
-                for (int p = 0; p < 4; p++) {
-                    const int m = 16 * g + 4 * u + p;
-                    const int e = (m >> 5) * 128 + l * 32 + (m & 31);
-                    d |= (uint32_t)(uint8_t)qb0[b * 256 + e] << (8 * p);
-                }
-                w4[l] = d;
-            }
-            const int off = (((b * 4 + u) * 4 + g) * M + t) * 16;
-            *(uint4 *)(B + off) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-        }
-        for (int b = wave; b < nb; b += FW) {
-            const int8_t *qb = qb0 + b * 256;
-            const int s = wave_sum_i(qb[lane] + qb[lane + 64] + qb[lane + 128] + qb[lane + 192]);
-            if (lane == 0) aux[b * M + t] = -s;
+            if (lane == 0 && m < nd) aux[b * M + t] = 128 * s4 - s;
+        } else {
+            s = wave_sum_i(s);
+            if (lane == 0 && m < nd) aux[b * M + t] = -s;
         }
     }
+    __syncthreads();
+    return act;
 }
 
 // ------------------------------------------------------------ weights
@@ -290,7 +342,7 @@ __device__ __forceinline__ void block_mfma(const RawBlk &r, const uint8_t *__res
 
 // ------------------------------------------------------------ kernel
 
-template <int FMT, int IN, int EPI>
+template <int FMT, int IN, int EPI, int R4>
 __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
 {
     extern __shared__ uint4 fused_lds4[];
@@ -304,7 +356,6 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     const int nb = a.nb, M = a.M, K = nb * 256;
     const int nslab = EPI == EPI_SILU ? 2 : 1;
     const FusedLds L = fused_lds(FMT, K, M, nslab);
-    int8_t *q = (int8_t *)(lds + L.q);
     uint8_t *B = lds + L.B;
     int32_t *aux = (int32_t *)(lds + L.aux);
     float *terms = (float *)(lds + L.terms);
@@ -338,13 +389,11 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
         }
     }
 
-    // ---- input stage: int8 activations and the B operand in LDS
+    // ---- input stage: int8 activations straight into the B operand in LDS
     for (int t = 0; t < M; t++) {
-        const float s = quantise_vector<IN>(a, t, K, q + t * K, dred, fred);
+        const float s = quantise_to_b<FMT, IN, R4>(a, t, K, B, aux, dred, fred);
         if (tid == 0) ascale[t] = s;
     }
-    __syncthreads();
-    for (int t = 0; t < M; t++) build_b<FMT>(q + t * K, t, M, nb, B, aux);
     __syncthreads();
 
     // ---- blocks: integer sums, then one float term per row and token
@@ -440,6 +489,12 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
 
 // ------------------------------------------------------------ host
 
+// the input stage reads x (and the norm weights) as float4, q as int32
+static bool fused_aligned(const void *x, size_t x_stride, size_t M, const void *w)
+{
+    return !((uintptr_t)x % 16) && !((uintptr_t)w % 16) && (M == 1 || x_stride % 4 == 0);
+}
+
 static fox_gpu_status fused_check(int type, size_t K, size_t M, int nslab, int *fmt)
 {
     *fmt = fmt_of(type);
@@ -447,6 +502,9 @@ static fox_gpu_status fused_check(int type, size_t K, size_t M, int nslab, int *
         return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "fused gemv: %s weights use the unfused path",
                         fox_type_name(type));
     if (K % 256 || K == 0) return fox_fail(FOX_GPU_ERR_ARG, "fused gemv: K %% 256 != 0");
+    if (K > 4 * R4_LIMIT * FWG)
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "fused gemv: K = %zu exceeds the %d values "
+                        "one workgroup holds", K, 4 * R4_LIMIT * FWG);
     if (M == 0 || M > FOX_GPU_MAX_TOKENS)
         return fox_fail(FOX_GPU_ERR_ARG, "fused gemv: 1 to %d tokens", FOX_GPU_MAX_TOKENS);
     if (fused_lds(*fmt, (int)K, (int)M, nslab).total > FUSED_LDS_MAX)
@@ -455,19 +513,30 @@ static fox_gpu_status fused_check(int type, size_t K, size_t M, int nslab, int *
     return FOX_GPU_OK;
 }
 
-template <int FMT, int IN, int EPI>
-static fox_gpu_status fused_go(fox_gpu_ctx *ctx, const FusedArgs &a, int grid)
+template <int FMT, int IN, int EPI, int R4>
+static fox_gpu_status fused_go_r(fox_gpu_ctx *ctx, const FusedArgs &a, int grid)
 {
     const size_t lds = fused_lds(FMT, a.nb * 256, a.M, EPI == EPI_SILU ? 2 : 1).total;
     if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute((const void *)gemv_fused<FMT, IN, EPI>,
+        hipError_t e = hipFuncSetAttribute((const void *)gemv_fused<FMT, IN, EPI, R4>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return fox_hip_fail(e, "fused gemv: LDS size");
     }
-    hipLaunchKernelGGL((gemv_fused<FMT, IN, EPI>), dim3((unsigned)grid), dim3(FWG), lds,
+    hipLaunchKernelGGL((gemv_fused<FMT, IN, EPI, R4>), dim3((unsigned)grid), dim3(FWG), lds,
                        ctx->stream, a);
     FOX_LAUNCHED("gemv_fused");
     return FOX_GPU_OK;
+}
+
+// the input registers per thread fit K: 2, 3, 5 or 8 dwords
+template <int FMT, int IN, int EPI>
+static fox_gpu_status fused_go(fox_gpu_ctx *ctx, const FusedArgs &a, int grid)
+{
+    const int per = (a.nb * 64 + FWG - 1) / FWG;
+    if (per <= 2) return fused_go_r<FMT, IN, EPI, 2>(ctx, a, grid);
+    if (per <= 3) return fused_go_r<FMT, IN, EPI, 3>(ctx, a, grid);
+    if (per <= 5) return fused_go_r<FMT, IN, EPI, 5>(ctx, a, grid);
+    return fused_go_r<FMT, IN, EPI, 8>(ctx, a, grid);
 }
 
 template <int IN, int EPI>
@@ -505,7 +574,9 @@ fox_gpu_status fox_fused_gemv(fox_gpu_ctx *ctx, size_t n, const fox_gpu_tensor *
     const size_t K = (size_t)ws[0]->ne0;
     if (fmt_of(ws[0]->type) != FMT_TQ1 && fmt_of(ws[0]->type) != FMT_TQ2)
         return FOX_GPU_ERR_UNSUPPORTED;
-    if (fused_lds(fmt_of(ws[0]->type), (int)K, (int)M, 1).total > FUSED_LDS_MAX)
+    if (fused_lds(fmt_of(ws[0]->type), (int)K, (int)M, 1).total > FUSED_LDS_MAX ||
+        K > 4 * R4_LIMIT * FWG || !fused_aligned(x ? (const void *)x : (const void *)q,
+                                             x ? x_stride : K, M, nullptr))
         return FOX_GPU_ERR_UNSUPPORTED;
     fox_gpu_status st = fused_check(ws[0]->type, K, M, 1, &fmt);
     if (st) return st;
@@ -548,6 +619,9 @@ extern "C" fox_gpu_status fox_gpu_gemv_rmsnorm(fox_gpu_ctx *ctx, size_t n,
     int fmt;
     fox_gpu_status st = fused_check(ws[0]->type, K, M, 1, &fmt);
     if (st) return st;
+    if (!fused_aligned(x, x_stride, M, norm_w))
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "gemv_rmsnorm: x and norm_w must be 16-byte "
+                        "aligned, the stride a multiple of 4");
     FusedArgs a;
     memset(&a, 0, sizeof(a));
     int tiles;
@@ -587,6 +661,9 @@ extern "C" fox_gpu_status fox_gpu_qkv_rope(fox_gpu_ctx *ctx, const fox_gpu_tenso
     int fmt;
     fox_gpu_status st = fused_check(wq->type, K, M, 1, &fmt);
     if (st) return st;
+    if (!fused_aligned(x, x_stride, M, norm_w))
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "qkv_rope: x and norm_w must be 16-byte "
+                        "aligned, the stride a multiple of 4");
     const fox_gpu_tensor *ws[3] = {wq, wk, wv};
     float *outs[3] = {q_out, nullptr, nullptr};
     size_t strides[3] = {q_stride, 0, 0};
@@ -627,6 +704,9 @@ extern "C" fox_gpu_status fox_gpu_gate_up_silu(fox_gpu_ctx *ctx, const fox_gpu_t
     int fmt;
     fox_gpu_status st = fused_check(wg->type, K, M, 2, &fmt);
     if (st) return st;
+    if (!fused_aligned(x, x_stride, M, norm_w))
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "gate_up_silu: x and norm_w must be 16-byte "
+                        "aligned, the stride a multiple of 4");
     const fox_gpu_tensor *ws[2] = {wg, wu};
     float *outs[2] = {h_out, nullptr};
     size_t strides[2] = {h_stride, h_stride};
