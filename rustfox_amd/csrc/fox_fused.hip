@@ -35,7 +35,7 @@ struct FusedArgs {
     int out_stride[MAX_SEGS];
     int n_rows[MAX_SEGS];
     int tile_start[MAX_SEGS + 1];
-    int nseg, nb, M;
+    int nseg, nb, M, n_work;
     unsigned flags;
     const float *x;
     int x_stride;
@@ -63,7 +63,7 @@ __host__ __device__ inline FusedLds fused_lds(int fmt, int K, int M, int nslab)
     L.q = off;
     L.B = off;     off += nb * M * b_bytes_per_block_tok(fmt);
     L.aux = off;   off += ((nb * M * aux_per_block_tok(fmt) * 4) + 15) & ~15;
-    L.terms = off; off += nslab * nb * terms_per_block(fmt) * 16 * M * 4;
+    L.terms = off; off += 2 * nslab * nb * terms_per_block(fmt) * 16 * M * 4;
     L.y = off;     off += nslab * 16 * M * 4;
     L.total = off;
     return L;
@@ -143,39 +143,61 @@ __device__ __forceinline__ void put_b(uint8_t *B, int M, int b, int t, int dl, u
 // corrections in LDS, in one pass over the input.  Thread tid owns input
 // dwords m = tid + FWG r; dword m lies in block m / 64, so a wave owns the
 // 64 dwords of a block and block sums are wave sums.  Returns amax / 127.
-template <int FMT, int IN, int R4MAX>
-__device__ float quantise_to_b(const FusedArgs &a, int t, int K, uint8_t *B, int32_t *aux,
-                               double *dred, float *fred)
-{
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int M = a.M, nd = K >> 2;
+// a thread's input dwords of one token, loaded before anything else
+template <int R4MAX>
+struct InRegs {
+    float4 xv[R4MAX], wv[R4MAX];
     uint32_t qd[R4MAX];
-    float act = 0.0f;
+};
+
+template <int IN, int R4MAX>
+__device__ __forceinline__ void load_input(const FusedArgs &a, int t, int K, InRegs<R4MAX> &in)
+{
+    const int tid = threadIdx.x, nd = K >> 2;
+    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (IN == IN_Q) {
         const uint32_t *q4 = (const uint32_t *)(a.q_in + (size_t)t * K);
 #pragma unroll
         for (int r = 0; r < R4MAX; r++) {
             const int m = tid + r * FWG;
-            qd[r] = m < nd ? q4[m] : 0u;
+            in.qd[r] = m < nd ? q4[m] : 0u;
         }
-        act = a.scale_in ? a.scale_in[t] : 0.0f;    // block sums come without a scale
-    } else {
-        const float4 *x4 = (const float4 *)(a.x + (size_t)t * a.x_stride);
+        return;
+    }
+    // (an if, not a select with a zero vector: the select becomes a load
+    // through a generic pointer, in 8-byte pieces)
+    const float4 *x4 = (const float4 *)(a.x + (size_t)t * a.x_stride);
+#pragma unroll
+    for (int r = 0; r < R4MAX; r++) {
+        const int m = tid + r * FWG;
+        in.xv[r] = z4;
+        if (m < nd) in.xv[r] = x4[m];
+    }
+    if (IN == IN_NORM) {
         const float4 *w4 = (const float4 *)a.norm_w;
-        float4 xv[R4MAX];
-        const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
         for (int r = 0; r < R4MAX; r++) {
             const int m = tid + r * FWG;
-            xv[r] = m < nd ? x4[m] : z4;
+            in.wv[r] = z4;
+            if (m < nd) in.wv[r] = w4[m];
         }
+    }
+}
+
+template <int FMT, int IN, int R4MAX>
+__device__ float quantise_to_b(const FusedArgs &a, int t, int K, uint8_t *B, int32_t *aux,
+                               double *dred, float *fred, InRegs<R4MAX> &in)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int M = a.M, nd = K >> 2;
+    uint32_t *qd = in.qd;
+    float act = 0.0f;
+    if (IN == IN_Q) {
+        act = a.scale_in ? a.scale_in[t] : 0.0f;    // block sums come without a scale
+    } else {
+        float4 *xv = in.xv;
         if (IN == IN_NORM) {
-            float4 wv[R4MAX];
-#pragma unroll
-            for (int r = 0; r < R4MAX; r++) {
-                const int m = tid + r * FWG;
-                wv[r] = m < nd ? w4[m] : z4;
-            }
+            const float4 *wv = in.wv;
             double ss = 0.0;
 #pragma unroll
             for (int r = 0; r < R4MAX; r++) {
@@ -187,19 +209,20 @@ __device__ float quantise_to_b(const FusedArgs &a, int t, int K, uint8_t *B, int
             ss = wave_sum_dd(ss);
             if (lane == 0) dred[wave] = ss;
             __syncthreads();
-            if (tid == 0) {
+            if (tid < 2) {
                 double tot = 0.0;
                 for (int w = 0; w < FW; w++) tot += dred[w];
                 // the tree sum certifies the float scale of the reference's
-                // index-order double sum (it lies within (K + 64) 2^-52 tot),
-                // else one thread redoes that sum
+                // index-order double sum (it lies within (K + 64) 2^-52 tot):
+                // lanes 0 and 1 evaluate the two ends of that interval
                 const double rel = (double)(K + 64) * 0x1p-52;
-                const double y_hi = 1.0 / __builtin_sqrt(tot * (1.0 - rel) / (double)K +
-                                                         (double)a.eps) * (1.0 + 0x1p-50);
-                const double y_lo = 1.0 / __builtin_sqrt(tot * (1.0 + rel) / (double)K +
-                                                         (double)a.eps) * (1.0 - 0x1p-50);
-                const float f_hi = (float)y_hi, f_lo = (float)y_lo;
-                if (f_hi == f_lo) {
+                const double sgn = lane == 0 ? -1.0 : 1.0;
+                const double y = 1.0 / __builtin_sqrt(tot * (1.0 + sgn * rel) / (double)K +
+                                                      (double)a.eps) * (1.0 - sgn * 0x1p-50);
+                const float f = (float)y;
+                const float f_hi = __shfl(f, 0), f_lo = __shfl(f, 1);
+                if (lane != 0) {
+                } else if (f_hi == f_lo) {
                     fred[0] = f_hi;
                 } else {
                     const float *xt = a.x + (size_t)t * a.x_stride;
@@ -342,6 +365,14 @@ __device__ __forceinline__ void block_mfma(const RawBlk &r, const uint8_t *__res
 
 // ------------------------------------------------------------ kernel
 
+// v[s] of a kernel-argument array, read with constant indices
+template <typename T>
+__device__ __forceinline__ T pick4(const T *v, int s)
+{
+    const T v0 = v[0], v1 = v[1], v2 = v[2], v3 = v[3];
+    return s == 0 ? v0 : s == 1 ? v1 : s == 2 ? v2 : v3;
+}
+
 template <int FMT, int IN, int EPI, int R4>
 __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
 {
@@ -358,136 +389,207 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     const FusedLds L = fused_lds(FMT, K, M, nslab);
     uint8_t *B = lds + L.B;
     int32_t *aux = (int32_t *)(lds + L.aux);
-    float *terms = (float *)(lds + L.terms);
+    float *terms = (float *)(lds + L.terms);               // [2][nslab][nb][16][M]
     float *ybuf = (float *)(lds + L.y);
+    const int tstride = nslab * nb * 16 * M;               // floats per terms buffer
 
-    // ---- this workgroup's slabs (segment, tile)
-    int seg[2], tile[2];
-    if (EPI == EPI_SILU) {
-        seg[0] = 0;
-        seg[1] = 1;
-        tile[0] = tile[1] = blockIdx.x;
-    } else {
-        int s = 0;
-        while (s + 1 < a.nseg && (int)blockIdx.x >= a.tile_start[s + 1]) s++;
-        seg[0] = seg[1] = s;
-        tile[0] = tile[1] = blockIdx.x - a.tile_start[s];
-    }
-    const uint8_t *wt0 = a.w[seg[0]] + (size_t)tile[0] * nb * CHUNK;
-    const uint8_t *wt1 = a.w[seg[1]] + (size_t)tile[1] * nb * CHUNK;
-
-    // ---- issue the weight loads of this wave's first PF units (unit u =
-    // slab * nb + block; wave w takes w, w + FW, ...)
+    // ---- work: items bx, bx + gridDim.x, ... (a 16-row tile of one segment,
+    // or with SILU a tile of gate and the same tile of up).  Arguments are
+    // read with constant indices only, so that they arrive in one batch of
+    // scalar loads (an argument indexed at run time is a chain of loads).
+    const int bx = blockIdx.x, nwg = gridDim.x;
+    const int ntl = bx < a.n_work ? (a.n_work - 1 - bx) / nwg + 1 : 0;
+    const int ts1 = a.tile_start[1], ts2 = a.tile_start[2], ts3 = a.tile_start[3];
+    const int nseg = a.nseg;
+    auto item = [&](int ti, int sl, int &sg, int &tl) {
+        const int w = bx + ti * nwg;
+        if (EPI == EPI_SILU) {
+            sg = sl;
+            tl = w;
+        } else {
+            sg = (nseg > 1 && w >= ts1) + (nseg > 2 && w >= ts2) + (nseg > 3 && w >= ts3);
+            tl = w - (sg == 0 ? 0 : sg == 1 ? ts1 : sg == 2 ? ts2 : ts3);
+        }
+    };
     const int nunits = nslab * nb;
+    const int nu = wave < nunits ? (nunits - 1 - wave) / FW + 1 : 0;   // units per item
+    const int total = nu * ntl;
+    auto unit_ptr = [&](int n) -> const uint8_t * {
+        const int ti = n / nu, r = n - ti * nu;
+        const int u = wave + FW * r, sl = u >= nb, b = u - sl * nb;
+        int sg, tl;
+        item(ti, sl, sg, tl);
+        return pick4(a.w, sg) + ((size_t)tl * nb + b) * CHUNK;
+    };
+
+    // ---- loads in the order they are used (they complete in order): the
+    // input of token 0, the first weight blocks, the epilogue's operands
+    InRegs<R4> in;
+    load_input<IN, R4>(a, 0, K, in);
     RawBlk raw[PF];
 #pragma unroll
-    for (int k = 0; k < PF; k++) {
-        const int u = wave + k * FW;
-        if (u < nunits) {
-            const int sl = u >= nb, b = u - sl * nb;
-            raw[k] = load_raw<FMT>((sl ? wt1 : wt0) + (size_t)b * CHUNK, lane);
+    for (int k = 0; k < PF; k++)
+        if (k < total) raw[k] = load_raw<FMT>(unit_ptr(k), lane);
+
+    // combiner threads: (slab, token, row) of an item's outputs
+    const int nthr = nslab * 16 * M;
+    const bool comb = tid < nthr;
+    const int csl = tid / (16 * M), crem = tid - csl * 16 * M;
+    const int ct = crem >> 4, crow = crem & 15;
+    // the position through the scalar cache: its wait does not wait for the
+    // vector loads above
+    size_t rp = 0;
+    if (EPI == EPI_ROPE)
+        rp = (size_t)*(const __attribute__((address_space(4))) uint32_t *)a.pos + (size_t)ct;
+    // epilogue operands of item ti for this thread (old output, RoPE table)
+    auto epi_load = [&](int ti, float &p0, float &p1) {
+        if (!comb || ti >= ntl) return;
+        int sg, tl;
+        item(ti, csl, sg, tl);
+        const int orow = tl * 16 + crow;
+        if (orow >= pick4(a.n_rows, sg)) return;
+        if (EPI == EPI_STORE && (a.flags & FOX_GPU_GEMV_ACCUMULATE))
+            p0 = pick4(a.out, sg)[(size_t)ct * pick4(a.out_stride, sg) + orow];
+        if (EPI == EPI_ROPE && sg < 2 && rp < (size_t)a.n_ctx) {
+            const int half = a.head_dim / 2, i = (orow % a.head_dim) >> 1;
+            p0 = a.rope_cos[rp * half + i];
+            p1 = a.rope_sin[rp * half + i];
         }
-    }
+    };
+    float pre0 = 0.0f, pre1 = 0.0f;
+    if (EPI == EPI_STORE) epi_load(0, pre0, pre1);
 
     // ---- input stage: int8 activations straight into the B operand in LDS
     for (int t = 0; t < M; t++) {
-        const float s = quantise_to_b<FMT, IN, R4>(a, t, K, B, aux, dred, fred);
+        if (t > 0) load_input<IN, R4>(a, t, K, in);
+        const float s = quantise_to_b<FMT, IN, R4>(a, t, K, B, aux, dred, fred, in);
         if (tid == 0) ascale[t] = s;
     }
+    if (EPI == EPI_ROPE) epi_load(0, pre0, pre1);
     __syncthreads();
 
-    // ---- blocks: integer sums, then one float term per row and token
+    // ---- end of item ti: ordered combine, activation scale, epilogue
+    auto item_end = [&](int ti) {
+        if (EPI == EPI_SUMS) return;
+        __syncthreads();
+        float n0 = 0.0f, n1 = 0.0f;
+        epi_load(ti + 1, n0, n1);                           // the next item's, in flight
+        int sg = 0, tl = 0;
+        item(ti, csl, sg, tl);
+        const int orow = tl * 16 + crow;
+        const bool owns = comb && orow < pick4(a.n_rows, sg);
+        float y = 0.0f;
+        if (comb) {
+            const float *tb = terms + (ti & 1) * tstride + (csl * nb * 16 + crow) * M + ct;
+            float acc = 0.0f;
+            int b = 0;
+            for (; b + 4 <= nb; b += 4) {
+                const float t0 = tb[(b + 0) * 16 * M], t1 = tb[(b + 1) * 16 * M];
+                const float t2 = tb[(b + 2) * 16 * M], t3 = tb[(b + 3) * 16 * M];
+                acc = acc + t0;
+                acc = acc + t1;
+                acc = acc + t2;
+                acc = acc + t3;
+            }
+            for (; b < nb; b++) acc = acc + tb[b * 16 * M];
+            y = acc * ascale[ct];                           // src/gemv.c:70
+        }
+        if (EPI == EPI_STORE) {
+            if (owns) {
+                float *o = pick4(a.out, sg) + (size_t)ct * pick4(a.out_stride, sg) + orow;
+                *o = (a.flags & FOX_GPU_GEMV_ACCUMULATE) ? pre0 + y : y;
+            }
+        } else if (EPI == EPI_SILU) {
+            if (comb) ybuf[tid] = y;
+            __syncthreads();
+            if (owns && csl == 0) {
+                const float gt = y, up = ybuf[16 * M + crem];
+                a.out[0][(size_t)ct * a.out_stride[0] + orow] =
+                    fox_div(gt, 1.0f + fox_expf(-gt)) * up; // src/ops.c:45-46
+            }
+        } else {  // EPI_ROPE: segment 0 q, 1 k, 2 v
+            const float partner = __shfl_xor(y, 1);
+            if (owns) {
+                const bool inside = rp < (size_t)a.n_ctx;
+                float v = y;
+                if (sg < 2 && inside) {
+                    // src/ops.c:64-69 on the pair (row & ~1, row | 1)
+                    v = (orow & 1) ? partner * pre1 + y * pre0 : y * pre0 - partner * pre1;
+                }
+                if (sg == 0) {
+                    a.out[0][(size_t)ct * a.out_stride[0] + orow] = v;
+                } else if (inside) {
+                    const size_t kvd = (size_t)a.kv_dim;
+                    if (sg == 1) a.k_cache[rp * kvd + orow] = v;
+                    else a.v_cache[((rp >> 2) * kvd + orow) * 4 + (rp & 3)] = v;
+                }
+            }
+        }
+        pre0 = n0;
+        pre1 = n1;
+    };
+
+    // ---- blocks: integer sums, then one float term per row and token.  A
+    // wave's units run through all its items; PF blocks stay in flight.
     const int g = lane >> 4, j = lane & 15;
     const int ncol = FMT == FMT_TQ1 ? 2 * M : M;
     const int bbytes = b_bytes_per_block_tok(FMT) * M;
-    for (int k0 = 0; k0 * FW + wave < nunits; k0 += PF) {
+    const bool lead = FMT == FMT_TQ1 ? (j < ncol && !(j & 1)) : j < ncol;
+    const int tok = FMT == FMT_TQ1 ? j >> 1 : j;
+    if (nu == 0) {
+        for (int ti = 0; ti < ntl; ti++) item_end(ti);
+        return;
+    }
+    for (int n0 = 0; n0 < total; n0 += PF) {
 #pragma unroll
         for (int k = 0; k < PF; k++) {
-            const int u = wave + (k0 + k) * FW;
-            if (u >= nunits) break;
-            const int sl = u >= nb, b = u - sl * nb;
-            const bool lead = FMT == FMT_TQ1 ? (j < ncol && !(j & 1)) : j < ncol;
-            const int tok = FMT == FMT_TQ1 ? j >> 1 : j;
+            const int n = n0 + k;
+            if (n >= total) break;
+            const int ti = n / nu, r = n - ti * nu;
+            const int u = wave + FW * r, sl = u >= nb, b = u - sl * nb;
             const int corr = lead ? aux[b * M + tok] : 0;
             int S[4];
             block_mfma<FMT>(raw[k], B + b * bbytes, M, lane, corr, S);
             const RawBlk rk = raw[k];
-            const int un = u + PF * FW;
-            if (un < nunits) {
-                const int sln = un >= nb, bn = un - sln * nb;
-                raw[k] = load_raw<FMT>((sln ? wt1 : wt0) + (size_t)bn * CHUNK, lane);
-            }
+            if (n + PF < total) raw[k] = load_raw<FMT>(unit_ptr(n + PF), lane);
             if (lead) {
                 const uint32_t hw[2] = {rk.dd.x, rk.dd.y};
-                const int nrows = a.n_rows[seg[sl]];
+                int sg, tl;
+                item(ti, sl, sg, tl);
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int row = 4 * g + r;
+                for (int q = 0; q < 4; q++) {
+                    const int row = 4 * g + q;
                     if (EPI == EPI_SUMS) {
-                        const int grow = tile[sl] * 16 + row;
-                        if (grow < nrows) a.sums[((size_t)tok * nrows + grow) * nb + b] = S[r];
+                        const int nrows = pick4(a.n_rows, sg), grow = tl * 16 + row;
+                        if (grow < nrows) a.sums[((size_t)tok * nrows + grow) * nb + b] = S[q];
                     } else {
-                        const float d = half_bits_to_float((hw[r >> 1] >> (16 * (r & 1))) & 0xFFFFu);
-                        terms[((sl * nb + b) * 16 + row) * M + tok] = d * (float)S[r];
+                        const float d = half_bits_to_float((hw[q >> 1] >> (16 * (q & 1))) & 0xFFFFu);
+                        terms[(ti & 1) * tstride + ((sl * nb + b) * 16 + row) * M + tok] =
+                            d * (float)S[q];
                     }
                 }
             }
-        }
-    }
-    if (EPI == EPI_SUMS) return;
-    __syncthreads();
-
-    // ---- combine in block order, activation scale, epilogue
-    const int nthr = nslab * 16 * M;
-    const bool comb = tid < nthr;
-    const int sl = tid / (16 * M), rem = tid - sl * 16 * M;
-    const int ct = rem >> 4, crow = rem & 15;
-    float y = 0.0f;
-    if (comb) {
-        float acc = 0.0f;
-        for (int b = 0; b < nb; b++) acc = acc + terms[((sl * nb + b) * 16 + crow) * M + ct];
-        y = acc * ascale[ct];                               // src/gemv.c:70
-    }
-    const int s = seg[sl];
-    const int row = tile[sl] * 16 + crow;
-    if (EPI == EPI_STORE) {
-        if (comb && row < a.n_rows[s]) {
-            float *o = a.out[s] + (size_t)ct * a.out_stride[s] + row;
-            *o = (a.flags & FOX_GPU_GEMV_ACCUMULATE) ? *o + y : y;
-        }
-    } else if (EPI == EPI_SILU) {
-        if (comb) ybuf[tid] = y;
-        __syncthreads();
-        if (comb && sl == 0 && row < a.n_rows[0]) {
-            const float gt = y, up = ybuf[16 * M + rem];
-            a.out[0][(size_t)ct * a.out_stride[0] + row] =
-                fox_div(gt, 1.0f + fox_expf(-gt)) * up;     // src/ops.c:45-46
-        }
-    } else {  // EPI_ROPE: segment 0 q, 1 k, 2 v
-        const float partner = __shfl_xor(y, 1);
-        if (comb && row < a.n_rows[s]) {
-            const size_t p = (size_t)a.pos[0] + (size_t)ct;
-            const bool inside = p < (size_t)a.n_ctx;
-            float v = y;
-            if (s < 2 && inside) {
-                const int half = a.head_dim / 2;
-                const int i = (row % a.head_dim) >> 1;
-                const float c = a.rope_cos[p * half + i], sn = a.rope_sin[p * half + i];
-                // src/ops.c:64-69 on the pair (row & ~1, row | 1)
-                v = (row & 1) ? partner * sn + y * c : y * c - partner * sn;
-            }
-            if (s == 0) {
-                a.out[0][(size_t)ct * a.out_stride[0] + row] = v;
-            } else if (inside) {
-                const size_t kvd = (size_t)a.kv_dim;
-                if (s == 1) a.k_cache[p * kvd + row] = v;
-                else a.v_cache[((p >> 2) * kvd + row) * 4 + (p & 3)] = v;
-            }
+            if (r == nu - 1) item_end(ti);
         }
     }
 }
 
 // ------------------------------------------------------------ host
+
+// Workgroups write output rows while others still read the input, so an
+// output must not overlap the input (the unfused path has no such limit).
+static bool out_overlaps(const void *in, size_t in_bytes, size_t n, float *const *outs,
+                         const size_t *rows, const size_t *strides, size_t M)
+{
+    const uintptr_t i0 = (uintptr_t)in, i1 = i0 + in_bytes;
+    for (size_t k = 0; k < n; k++) {
+        if (!outs[k]) continue;
+        const uintptr_t o0 = (uintptr_t)outs[k];
+        const uintptr_t o1 = o0 + ((M - 1) * (M > 1 ? strides[k] : 0) + rows[k]) * sizeof(float);
+        if (o0 < i1 && i0 < o1) return true;
+    }
+    return false;
+}
 
 // the input stage reads x (and the norm weights) as float4, q as int32
 static bool fused_aligned(const void *x, size_t x_stride, size_t M, const void *w)
@@ -513,9 +615,14 @@ static fox_gpu_status fused_check(int type, size_t K, size_t M, int nslab, int *
     return FOX_GPU_OK;
 }
 
+// n_work items (tiles, or gate/up tile pairs) over at most two persistent
+// workgroups per compute unit
 template <int FMT, int IN, int EPI, int R4>
-static fox_gpu_status fused_go_r(fox_gpu_ctx *ctx, const FusedArgs &a, int grid)
+static fox_gpu_status fused_go_r(fox_gpu_ctx *ctx, FusedArgs a, int n_work)
 {
+    a.n_work = n_work;
+    const int cap = 2 * (ctx->n_cu > 0 ? ctx->n_cu : 1);
+    const int grid = n_work < cap ? n_work : cap;
     const size_t lds = fused_lds(FMT, a.nb * 256, a.M, EPI == EPI_SILU ? 2 : 1).total;
     if (lds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute((const void *)gemv_fused<FMT, IN, EPI, R4>,
@@ -580,6 +687,14 @@ fox_gpu_status fox_fused_gemv(fox_gpu_ctx *ctx, size_t n, const fox_gpu_tensor *
         return FOX_GPU_ERR_UNSUPPORTED;
     fox_gpu_status st = fused_check(ws[0]->type, K, M, 1, &fmt);
     if (st) return st;
+    if (outs) {
+        size_t rows[MAX_SEGS];
+        for (size_t i = 0; i < n; i++) rows[i] = (size_t)ws[i]->ne1;
+        const size_t in_bytes = x ? ((M - 1) * (M > 1 ? x_stride : 0) + K) * sizeof(float) : M * K;
+        if (out_overlaps(x ? (const void *)x : (const void *)q, in_bytes, n, outs, rows,
+                         out_strides, M))
+            return FOX_GPU_ERR_UNSUPPORTED;
+    }
     FusedArgs a;
     memset(&a, 0, sizeof(a));
     int tiles;
@@ -622,6 +737,13 @@ extern "C" fox_gpu_status fox_gpu_gemv_rmsnorm(fox_gpu_ctx *ctx, size_t n,
     if (!fused_aligned(x, x_stride, M, norm_w))
         return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "gemv_rmsnorm: x and norm_w must be 16-byte "
                         "aligned, the stride a multiple of 4");
+    {
+        size_t rows[MAX_SEGS];
+        for (size_t i = 0; i < n; i++) rows[i] = (size_t)ws[i]->ne1;
+        if (out_overlaps(x, ((M - 1) * (M > 1 ? x_stride : 0) + K) * sizeof(float), n, outs, rows,
+                         out_strides, M))
+            return fox_fail(FOX_GPU_ERR_ARG, "gemv_rmsnorm: an output overlaps the input");
+    }
     FusedArgs a;
     memset(&a, 0, sizeof(a));
     int tiles;
@@ -664,6 +786,13 @@ extern "C" fox_gpu_status fox_gpu_qkv_rope(fox_gpu_ctx *ctx, const fox_gpu_tenso
     if (!fused_aligned(x, x_stride, M, norm_w))
         return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "qkv_rope: x and norm_w must be 16-byte "
                         "aligned, the stride a multiple of 4");
+    {
+        float *o[1] = {q_out};
+        size_t rows[1] = {(size_t)wq->ne1}, str[1] = {q_stride};
+        if (out_overlaps(x, ((M - 1) * (M > 1 ? x_stride : 0) + K) * sizeof(float), 1, o, rows,
+                         str, M))
+            return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: q_out overlaps the input");
+    }
     const fox_gpu_tensor *ws[3] = {wq, wk, wv};
     float *outs[3] = {q_out, nullptr, nullptr};
     size_t strides[3] = {q_stride, 0, 0};
@@ -707,6 +836,13 @@ extern "C" fox_gpu_status fox_gpu_gate_up_silu(fox_gpu_ctx *ctx, const fox_gpu_t
     if (!fused_aligned(x, x_stride, M, norm_w))
         return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "gate_up_silu: x and norm_w must be 16-byte "
                         "aligned, the stride a multiple of 4");
+    {
+        float *o[1] = {h_out};
+        size_t rows[1] = {(size_t)wg->ne1}, str[1] = {h_stride};
+        if (out_overlaps(x, ((M - 1) * (M > 1 ? x_stride : 0) + K) * sizeof(float), 1, o, rows,
+                         str, M))
+            return fox_fail(FOX_GPU_ERR_ARG, "gate_up_silu: h_out overlaps the input");
+    }
     const fox_gpu_tensor *ws[2] = {wg, wu};
     float *outs[2] = {h_out, nullptr};
     size_t strides[2] = {h_stride, h_stride};

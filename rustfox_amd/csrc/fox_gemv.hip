@@ -465,71 +465,121 @@ __global__ __launch_bounds__(WG) void gemv_blocks(Segs segs, int nb, int M, int 
 // -------------------------------------------------------- float weights
 
 // F16 / F32 rows (src/kernels.c:81-96): each lane owns one row and adds
-// w[k] * x[k] sequentially in k, exactly the reference's order; weights are
-// staged through LDS with coalesced loads.
-template <typename WT>
-__global__ __launch_bounds__(256) void gemv_float(const WT *__restrict__ W, int K, int N,
+// w[k] * x[k] sequentially in k, exactly the reference's order.  A
+// workgroup owns one 256-row tile of the tiled float layout; its chunks
+// (128 bytes of every row, 32 KB contiguous) stream through LDS (rows padded
+// by a dword against bank conflicts), double buffered: the next chunk's
+// loads are in flight while a chunk is summed.  The activations of a chunk
+// ride along in the same buffers.
+#define FR 256      // rows per workgroup
+
+template <typename WT, int MT>
+__global__ __launch_bounds__(FR) void gemv_float(const WT *__restrict__ W, int K, int N,
                                                  const float *__restrict__ x, int x_stride,
                                                  int M, float *__restrict__ out,
                                                  int out_stride, unsigned flags)
 {
-    constexpr int FCH = 128 / sizeof(WT);        // elements per 128-byte chunk
-    constexpr int EPD = 4 / sizeof(WT);          // elements per dword
-    constexpr int RSTR = FCH / EPD + 1;          // padded row stride in dwords
-    __shared__ uint32_t wl[256 * RSTR];
-    __shared__ float xs[FOX_GPU_MAX_TOKENS * 64];
+    constexpr int FK = 128 / sizeof(WT);               // elements of a 128-byte row chunk
+    constexpr int RDW = FK * sizeof(WT) / 4;           // dwords of a row chunk
+    constexpr int RSTR = RDW + 1;                       // padded row stride
+    constexpr int PPR = RDW / 4;                        // 16-byte pieces per row chunk
+    constexpr int NP = FR * PPR / FR;                   // pieces per thread
+    __shared__ uint32_t wl[2][FR * RSTR];
+    __shared__ float xs[2][MT * FK];
+    if (MT == 1) M = 1;
     const int tid = threadIdx.x;
-    const int r0 = blockIdx.x * 256;
-    const bool vec = (K % (16 / (int)sizeof(WT))) == 0;
-    float acc[FOX_GPU_MAX_TOKENS];
-#pragma unroll
-    for (int t = 0; t < FOX_GPU_MAX_TOKENS; t++) acc[t] = 0.0f;
+    const int r0 = blockIdx.x * FR;
+    const int nchunk = (K + FK - 1) / FK;
+    // this tile's chunks, 32 KB each (rows and columns zero-padded)
+    const uint4 *tw = (const uint4 *)W + (size_t)blockIdx.x * nchunk * (FR * PPR);
 
-    for (int k0 = 0; k0 < K; k0 += FCH) {
-        const int kn = K - k0 < FCH ? K - k0 : FCH;
-        // 256 rows x FCH elements; 16-byte pieces of FCH*sizeof(WT)/16 per row
-        constexpr int PPR = FCH * sizeof(WT) / 16;
-        constexpr int EPP = 16 / sizeof(WT);
-        for (int pc = tid; pc < 256 * PPR; pc += 256) {
-            const int r = pc / PPR, part = pc % PPR;
-            const int row = r0 + r, kk = part * EPP;
-            uint32_t v[4] = {0u, 0u, 0u, 0u};
-            if (row < N && kk < kn) {
-                const WT *src = W + (size_t)row * K + k0 + kk;
-                if (vec && kk + EPP <= kn) {
-                    uint4 u = *(const uint4 *)src;
-                    v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
-                } else {
-                    WT tmp[EPP];
-                    for (int e = 0; e < EPP; e++) tmp[e] = kk + e < kn ? src[e] : (WT)0;
-                    memcpy(v, tmp, 16);
-                }
+    constexpr int XPT = (MT * FK + FR - 1) / FR;        // activations staged per thread
+    uint4 R[NP];
+    float xr[XPT];
+    // global -> registers for chunk c (rows past N and columns past K read 0)
+    auto fetch = [&](int c) {
+        const int k0 = c * FK, kn = K - k0 < FK ? K - k0 : FK;
+        const uint4 *cw = tw + (size_t)c * (FR * PPR);
+#pragma unroll
+        for (int i = 0; i < NP; i++) R[i] = cw[tid + i * FR];
+#pragma unroll
+        for (int v = 0; v < XPT; v++) {
+            const int e = tid + v * FR;
+            xr[v] = 0.0f;
+            if (e < M * FK) {
+                const int t = e / FK, kk = e - t * FK;
+                if (kk < kn) xr[v] = x[(size_t)t * x_stride + k0 + kk];
             }
-#pragma unroll
-            for (int e = 0; e < 4; e++) wl[r * RSTR + part * 4 + e] = v[e];
         }
-        for (int i = tid; i < M * FCH; i += 256) {
-            const int t = i / FCH, kk = i % FCH;
-            xs[i] = kk < kn ? x[(size_t)t * x_stride + k0 + kk] : 0.0f;
-        }
-        __syncthreads();
-        const uint32_t *myw = wl + tid * RSTR;
-        for (int kk = 0; kk < kn; kk++) {
-            const uint32_t dword = myw[kk / EPD];
-            float w;
-            if (sizeof(WT) == 2)
-                w = half_bits_to_float((dword >> (16 * (kk % EPD))) & 0xFFFFu);
-            else
-                w = __builtin_bit_cast(float, dword);
+    };
+    auto stash = [&](int buf) {
 #pragma unroll
-            for (int t = 0; t < FOX_GPU_MAX_TOKENS; t++)
-                if (t < M) acc[t] = acc[t] + w * xs[t * FCH + kk];
+        for (int i = 0; i < NP; i++) {
+            const int pc = tid + i * FR, r = pc / PPR, part = pc - r * PPR;
+            uint32_t *d = &wl[buf][r * RSTR + part * 4];
+            d[0] = R[i].x;
+            d[1] = R[i].y;
+            d[2] = R[i].z;
+            d[3] = R[i].w;
+        }
+#pragma unroll
+        for (int v = 0; v < XPT; v++) {
+            const int e = tid + v * FR;
+            if (e < M * FK) xs[buf][e] = xr[v];
+        }
+    };
+
+    float acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) acc[t] = 0.0f;
+
+    fetch(0);
+    stash(0);
+    if (nchunk > 1) fetch(1);
+    __syncthreads();
+    for (int c = 0; c < nchunk; c++) {
+        const int buf = c & 1;
+        const int kn = K - c * FK < FK ? K - c * FK : FK;
+        const uint32_t *myw = &wl[buf][tid * RSTR];
+        const float *xb = xs[buf];
+        if (kn == FK) {
+#pragma unroll 8
+            for (int kk = 0; kk < FK; kk++) {
+                const uint32_t dword = myw[kk / (4 / (int)sizeof(WT))];
+                float w;
+                if (sizeof(WT) == 2)
+                    w = half_bits_to_float((dword >> (16 * (kk & 1))) & 0xFFFFu);
+                else
+                    w = __builtin_bit_cast(float, dword);
+#pragma unroll
+                for (int t = 0; t < MT; t++)
+                    if (t < M) acc[t] = acc[t] + w * xb[t * FK + kk];
+            }
+        } else {
+            for (int kk = 0; kk < kn; kk++) {
+                const uint32_t dword = myw[kk / (4 / (int)sizeof(WT))];
+                float w;
+                if (sizeof(WT) == 2)
+                    w = half_bits_to_float((dword >> (16 * (kk & 1))) & 0xFFFFu);
+                else
+                    w = __builtin_bit_cast(float, dword);
+#pragma unroll
+                for (int t = 0; t < MT; t++)
+                    if (t < M) acc[t] = acc[t] + w * xb[t * FK + kk];
+            }
+        }
+        if (c + 1 < nchunk) {
+            // the other buffer was last read before the previous barrier
+            stash(buf ^ 1);
+            if (c + 2 < nchunk) fetch(c + 2);
         }
         __syncthreads();
     }
     const int row = r0 + tid;
     if (row >= N) return;
-    for (int t = 0; t < M; t++) {
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        if (t >= M) break;
         float *o = out + (size_t)t * out_stride + row;
         *o = (flags & FOX_GPU_GEMV_ACCUMULATE) ? *o + acc[t] : acc[t];
     }
@@ -686,15 +736,25 @@ fox_gpu_status fox_gemv_launch(fox_gpu_ctx *ctx, size_t n, const fox_gpu_tensor 
                             "gemv: %s weights take float activations", fox_type_name(type));
         for (size_t i = 0; i < n; i++) {
             const int N = (int)ws[i]->ne1;
-            dim3 grid((unsigned)((N + 255) / 256)), block(256);
-            if (type == FOX_GPU_F16)
-                hipLaunchKernelGGL(gemv_float<_Float16>, grid, block, 0, ctx->stream,
-                                   (const _Float16 *)ws[i]->d, (int)K, N, x, (int)x_stride,
-                                   (int)M, outs[i], (int)out_strides[i], flags);
+            dim3 grid((unsigned)((N + FR - 1) / FR)), block(FR);
+            const _Float16 *wh = (const _Float16 *)ws[i]->d;
+            const float *wf = (const float *)ws[i]->d;
+            if (type == FOX_GPU_F16 && M == 1)
+                hipLaunchKernelGGL((gemv_float<_Float16, 1>), grid, block, 0, ctx->stream, wh,
+                                   (int)K, N, x, (int)x_stride, (int)M, outs[i],
+                                   (int)out_strides[i], flags);
+            else if (type == FOX_GPU_F16)
+                hipLaunchKernelGGL((gemv_float<_Float16, FOX_GPU_MAX_TOKENS>), grid, block, 0,
+                                   ctx->stream, wh, (int)K, N, x, (int)x_stride, (int)M, outs[i],
+                                   (int)out_strides[i], flags);
+            else if (M == 1)
+                hipLaunchKernelGGL((gemv_float<float, 1>), grid, block, 0, ctx->stream, wf,
+                                   (int)K, N, x, (int)x_stride, (int)M, outs[i],
+                                   (int)out_strides[i], flags);
             else
-                hipLaunchKernelGGL(gemv_float<float>, grid, block, 0, ctx->stream,
-                                   (const float *)ws[i]->d, (int)K, N, x, (int)x_stride,
-                                   (int)M, outs[i], (int)out_strides[i], flags);
+                hipLaunchKernelGGL((gemv_float<float, FOX_GPU_MAX_TOKENS>), grid, block, 0,
+                                   ctx->stream, wf, (int)K, N, x, (int)x_stride, (int)M, outs[i],
+                                   (int)out_strides[i], flags);
             FOX_LAUNCHED("gemv_float");
         }
         return FOX_GPU_OK;

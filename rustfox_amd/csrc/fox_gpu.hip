@@ -272,6 +272,31 @@ __global__ void repack_blocks(int type, int dir, const uint8_t *src, uint8_t *ds
     }
 }
 
+// float tensors, one element per step. dir 0: row-major (src) -> tiles (dst),
+// padding zero; dir 1: tiles (src) -> row-major (dst).
+template <typename T>
+__global__ void repack_float(int dir, const T *src, T *dst, uint64_t n_rows, uint64_t K,
+                             uint64_t total)
+{
+    const uint64_t per = FOX_FCHUNK / sizeof(T), nchunk = (K + per - 1) / per;
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
+    for (; i < total; i += step) {
+        if (dir == 0) {
+            // i: element of the tiled layout
+            const uint64_t e = i % per, rest = i / per;
+            const uint64_t ri = rest % FOX_FTILE, rest2 = rest / FOX_FTILE;
+            const uint64_t c = rest2 % nchunk, tile = rest2 / nchunk;
+            const uint64_t r = tile * FOX_FTILE + ri, k = c * per + e;
+            dst[i] = (r < n_rows && k < K) ? src[r * K + k] : (T)0;
+        } else {
+            // i: element of the row-major layout
+            const uint64_t r = i / K, k = i % K;
+            dst[i] = src[fox_float_offset(r, k, K, sizeof(T)) / sizeof(T)];
+        }
+    }
+}
+
 static unsigned grid_for(uint64_t n, unsigned block)
 {
     uint64_t g = (n + block - 1) / block;
@@ -314,13 +339,37 @@ extern "C" fox_gpu_status fox_gpu_tensor_upload(fox_gpu_ctx *ctx, int type, uint
     t->gguf_bytes = bytes;
 
     if (!fox_is_block_type(type)) {
-        t->dev_bytes = bytes;
-        if (hipMalloc(&t->d, bytes) != hipSuccess) {
+        const uint64_t es = bb, per = FOX_FCHUNK / es, nchunk = (ne0 + per - 1) / per;
+        t->n_tiles = (rows + FOX_FTILE - 1) / FOX_FTILE;
+        t->dev_bytes = t->n_tiles * nchunk * FOX_FTILE * FOX_FCHUNK;
+        uint8_t *stage = nullptr;
+        if (hipMalloc(&t->d, t->dev_bytes) != hipSuccess) {
             delete t;
             return fox_fail(FOX_GPU_ERR_NOMEM, "tensor_upload: %llu bytes of HBM",
+                            (unsigned long long)t->dev_bytes);
+        }
+        if (hipMalloc(&stage, bytes) != hipSuccess) {
+            fox_gpu_tensor_free(ctx, t);
+            return fox_fail(FOX_GPU_ERR_NOMEM, "tensor_upload: %llu bytes of staging",
                             (unsigned long long)bytes);
         }
-        if ((st = fox_gpu_memcpy_h2d(ctx, t->d, host, bytes))) {
+        st = fox_gpu_memcpy_h2d(ctx, stage, host, bytes);
+        if (!st) {
+            const uint64_t n = t->dev_bytes / es;
+            if (es == 2)
+                hipLaunchKernelGGL(repack_float<uint16_t>, dim3(grid_for(n, 256)), dim3(256), 0,
+                                   ctx->stream, 0, (const uint16_t *)stage, (uint16_t *)t->d,
+                                   rows, ne0, n);
+            else
+                hipLaunchKernelGGL(repack_float<uint32_t>, dim3(grid_for(n, 256)), dim3(256), 0,
+                                   ctx->stream, 0, (const uint32_t *)stage, (uint32_t *)t->d,
+                                   rows, ne0, n);
+            hipError_t e = hipGetLastError();
+            if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+            if (e != hipSuccess) st = fox_hip_fail(e, "tensor_upload: repack");
+        }
+        (void)hipFree(stage);
+        if (st) {
             fox_gpu_tensor_free(ctx, t);
             return st;
         }
@@ -382,11 +431,25 @@ extern "C" fox_gpu_status fox_gpu_tensor_download(fox_gpu_ctx *ctx, const fox_gp
         return fox_fail(FOX_GPU_ERR_ARG, "tensor_download: tensor holds %llu bytes, %llu asked",
                         (unsigned long long)t->gguf_bytes, (unsigned long long)bytes);
     if ((st = set_device(ctx))) return st;
-    if (!fox_is_block_type(t->type)) return fox_gpu_memcpy_d2h(ctx, host, t->d, bytes);
-
     uint8_t *stage = nullptr;
     if (hipMalloc(&stage, bytes) != hipSuccess)
         return fox_fail(FOX_GPU_ERR_NOMEM, "tensor_download: staging");
+    if (!fox_is_block_type(t->type)) {
+        const uint64_t es = fox_block_bytes(t->type), n = bytes / es;
+        if (es == 2)
+            hipLaunchKernelGGL(repack_float<uint16_t>, dim3(grid_for(n, 256)), dim3(256), 0,
+                               ctx->stream, 1, (const uint16_t *)t->d, (uint16_t *)stage, t->ne1,
+                               t->ne0, n);
+        else
+            hipLaunchKernelGGL(repack_float<uint32_t>, dim3(grid_for(n, 256)), dim3(256), 0,
+                               ctx->stream, 1, (const uint32_t *)t->d, (uint32_t *)stage, t->ne1,
+                               t->ne0, n);
+        hipError_t e = hipGetLastError();
+        st = e == hipSuccess ? fox_gpu_memcpy_d2h(ctx, host, stage, bytes)
+                             : fox_hip_fail(e, "tensor_download: unpack");
+        (void)hipFree(stage);
+        return st;
+    }
     uint64_t nb = t->ne0 / 256;
     hipLaunchKernelGGL(repack_blocks, dim3(grid_for(t->dev_bytes, 256)), dim3(256), 0,
                        ctx->stream, t->type, 1, t->d, stage, t->ne1, nb,

@@ -17,7 +17,11 @@
 //                  HD[16 rows][16]   d, dmin, scales[12]
 //   Q6_K  3360 B = QL[16 rows][128]  QH[16 rows][64]  SC[16 rows][16]  D[16 rows][f16]
 //
-// F16 / F32 tensors stay row-major as in GGUF.
+// F16 / F32 tensors are stored in tiles of 256 rows, chunk by chunk: the
+// 128-byte pieces (64 halves or 32 floats) of the tile's rows for columns
+// c*E .. c*E+E-1 are one contiguous 32 KB block, rows and columns padded
+// with zeros.  A GEMV workgroup (one lane per row) then reads each chunk
+// as one contiguous run.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -28,6 +32,17 @@
 #include "../../include/fox_gpu.h"
 
 #define FOX_TILE 16
+#define FOX_FTILE 256            // rows per tile of a float tensor
+#define FOX_FCHUNK 128           // bytes per row in one chunk of a float tensor
+
+// byte offset of element (r, k) of a float tensor with K columns
+__host__ __device__ inline uint64_t fox_float_offset(uint64_t r, uint64_t k, uint64_t K,
+                                                     uint64_t esize)
+{
+    const uint64_t per = FOX_FCHUNK / esize, nchunk = (K + per - 1) / per;
+    return (((r / FOX_FTILE) * nchunk + k / per) * FOX_FTILE + r % FOX_FTILE) * FOX_FCHUNK +
+           (k % per) * esize;
+}
 #define TQ1_CHUNK 864
 #define TQ2_CHUNK 1056
 #define Q4K_CHUNK 2304

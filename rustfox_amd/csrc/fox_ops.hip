@@ -20,10 +20,10 @@ __global__ void get_rows_k(const WT *__restrict__ src, uint64_t K, uint64_t N,
         if (bad && blockIdx.x == 0 && threadIdx.x == 0) *bad = 1u;
         return;
     }
-    const WT *row = src + (size_t)r * K;
     for (uint64_t k = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; k < K;
          k += (uint64_t)gridDim.x * blockDim.x)
-        out[(size_t)i * out_stride + k] = (float)row[k];
+        out[(size_t)i * out_stride + k] =
+            (float)src[fox_float_offset(r, k, K, sizeof(WT)) / sizeof(WT)];
 }
 
 extern "C" fox_gpu_status fox_gpu_get_rows(fox_gpu_ctx *ctx, const fox_gpu_tensor *t,
