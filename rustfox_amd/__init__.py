@@ -298,6 +298,11 @@ class Gpu:
         _check(self.lib.fox_gpu_gate_up_silu(self.ctx, wg.h, wu.h, x.ptr, K, M, norm.ptr, eps,
                                              h.ptr, ff))
 
+    def argmax(self, logits: DeviceArray, n, idx: DeviceArray, pos: DeviceArray = None,
+               advance=0, history: DeviceArray = None):
+        _check(self.lib.fox_gpu_argmax(self.ctx, logits.ptr, n, idx.ptr, pos.ptr if pos else None,
+                                       advance, history.ptr if history else None))
+
     def kv_write(self, kc: DeviceArray, vc: DeviceArray, kv_dim, n_ctx, p0, k: DeviceArray,
                  v: DeviceArray, n):
         _check(self.lib.fox_gpu_kv_write(self.ctx, kc.ptr, vc.ptr, kv_dim, n_ctx, p0, n, k.ptr,

@@ -84,6 +84,11 @@ extern "C" fox_gpu_status fox_gpu_init(int device, fox_gpu_ctx **out)
         fox_gpu_shutdown(ctx);
         return st;
     }
+    if (hipMalloc(&ctx->small, FOX_SMALL_BYTES) != hipSuccess ||
+        hipMemset(ctx->small, 0, FOX_SMALL_BYTES) != hipSuccess) {
+        fox_gpu_shutdown(ctx);
+        return fox_fail(FOX_GPU_ERR_NOMEM, "init: small buffer");
+    }
     *out = ctx;
     return FOX_GPU_OK;
 }
@@ -97,6 +102,7 @@ extern "C" void fox_gpu_shutdown(fox_gpu_ctx *ctx)
         (void)hipStreamDestroy(ctx->stream);
     }
     if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->small) (void)hipFree(ctx->small);
     for (int i = 0; i < ctx->n_retired; i++) (void)hipFree(ctx->retired[i]);
     delete ctx;
 }

@@ -62,7 +62,11 @@ struct fox_gpu_ctx {
     // so they are freed only at shutdown
     uint8_t *retired[32];
     int n_retired;
+    // small fixed buffer (counters, cross-workgroup partials) zeroed at init;
+    // its address never changes, so captured graphs may use it
+    uint8_t *small;
 };
+#define FOX_SMALL_BYTES (64 * 1024)
 
 struct fox_gpu_tensor {
     int type;

@@ -1031,39 +1031,84 @@ extern "C" fox_gpu_status fox_gpu_add(fox_gpu_ctx *ctx, float *dst, const float 
 
 // First index of the maximum, NaN never winning (src/sample.c:147-153:
 // best starts at 0 and moves only on a strict '>'; a NaN at index 0 stays).
-__global__ __launch_bounds__(1024) void argmax_k(const float *__restrict__ x, int n,
-                                                 uint32_t *__restrict__ idx,
-                                                 uint32_t *__restrict__ pos, uint32_t advance,
-                                                 uint32_t *__restrict__ history)
+// Workgroups reduce contiguous ranges to (max, first index) partials; the
+// last workgroup to finish (a device-scope counter) merges them in index
+// order, applies the index-0 rule, writes the result and, for a decode loop,
+// the history entry and the advanced position, and resets the counter.
+#define AM_THREADS 256
+#define AM_MAX_WG 256
+
+__device__ __forceinline__ void am_merge(float &best, int &bidx, float ov, int oi)
 {
-    __shared__ float bv[16];
-    __shared__ int bi[16];
+    if (ov > best || (ov == best && oi < bidx)) {
+        best = ov;
+        bidx = oi;
+    }
+}
+
+__global__ __launch_bounds__(AM_THREADS) void argmax_k(const float *__restrict__ x, int n,
+                                                       int per, float *pv, int *pi,
+                                                       unsigned *counter,
+                                                       uint32_t *__restrict__ idx,
+                                                       uint32_t *__restrict__ pos,
+                                                       uint32_t advance,
+                                                       uint32_t *__restrict__ history)
+{
+    __shared__ float bv[AM_THREADS / 64];
+    __shared__ int bi[AM_THREADS / 64];
+    __shared__ int last;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int i0 = blockIdx.x * per, i1 = min(n, i0 + per);
     float best = -INFINITY;
     int bidx = 0x7fffffff;
-    for (int i = tid; i < n; i += 1024) {
-        float v = x[i];
-        if (v > best) { best = v; bidx = i; }
+    for (int i = i0 + tid; i < i1; i += AM_THREADS) {
+        const float v = x[i];
+        if (v > best) {
+            best = v;
+            bidx = i;
+        }
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        float ov = __shfl_xor(best, o);
-        int oi = __shfl_xor(bidx, o);
-        if (ov > best || (ov == best && oi < bidx)) { best = ov; bidx = oi; }
+    for (int o = 32; o > 0; o >>= 1) am_merge(best, bidx, __shfl_xor(best, o), __shfl_xor(bidx, o));
+    if (lane == 0) {
+        bv[wave] = best;
+        bi[wave] = bidx;
     }
-    if (lane == 0) { bv[wave] = best; bi[wave] = bidx; }
     __syncthreads();
     if (tid == 0) {
-        for (int w = 1; w < 16; w++)
-            if (bv[w] > best || (bv[w] == best && bi[w] < bidx)) { best = bv[w]; bidx = bi[w]; }
+        for (int w = 1; w < AM_THREADS / 64; w++) am_merge(best, bidx, bv[w], bi[w]);
+        __hip_atomic_store(&pv[blockIdx.x], best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&pi[blockIdx.x], bidx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned done = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        last = done == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    best = -INFINITY;
+    bidx = 0x7fffffff;
+    for (int b = tid; b < (int)gridDim.x; b += AM_THREADS)
+        am_merge(best, bidx,
+                 __hip_atomic_load(&pv[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                 __hip_atomic_load(&pi[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) am_merge(best, bidx, __shfl_xor(best, o), __shfl_xor(bidx, o));
+    if (lane == 0) {
+        bv[wave] = best;
+        bi[wave] = bidx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < AM_THREADS / 64; w++) am_merge(best, bidx, bv[w], bi[w]);
         // index 0 wins unless something is strictly greater than x[0]
-        float x0 = x[0];
-        uint32_t r = (x0 != x0 || !(best > x0)) ? 0u : (uint32_t)bidx;
+        const float x0 = x[0];
+        const uint32_t r = (x0 != x0 || !(best > x0)) ? 0u : (uint32_t)bidx;
         *idx = r;
         if (pos) {
             if (history) history[*pos] = r;
             *pos += advance;
         }
+        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -1073,8 +1118,16 @@ extern "C" fox_gpu_status fox_gpu_argmax(fox_gpu_ctx *ctx, const float *logits, 
 {
     if (!ctx || !logits || !idx || n == 0 || n > 0x7fffffff)
         return fox_fail(FOX_GPU_ERR_ARG, "argmax: bad argument");
-    hipLaunchKernelGGL(argmax_k, dim3(1), dim3(1024), 0, ctx->stream, logits, (int)n, idx, pos,
-                       advance, history);
+    // partials and the counter live in the context's fixed small buffer
+    unsigned *counter = (unsigned *)ctx->small;
+    float *pv = (float *)(ctx->small + 256);
+    int *pi = (int *)(ctx->small + 256 + 4 * AM_MAX_WG);
+    size_t nwg = (n + 2047) / 2048;
+    if (nwg > AM_MAX_WG) nwg = AM_MAX_WG;
+    const size_t per = (n + nwg - 1) / nwg;
+    nwg = (n + per - 1) / per;
+    hipLaunchKernelGGL(argmax_k, dim3((unsigned)nwg), dim3(AM_THREADS), 0, ctx->stream, logits,
+                       (int)n, (int)per, pv, pi, counter, idx, pos, advance, history);
     FOX_LAUNCHED("argmax");
     return FOX_GPU_OK;
 }

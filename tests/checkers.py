@@ -153,6 +153,9 @@ class Oracle:
         self.lib.or_silu_mul(g, np.ascontiguousarray(up, np.float32), g.size)
         return g
 
+    def argmax(self, x):
+        return int(self.lib.or_argmax(np.ascontiguousarray(x, np.float32), len(x)))
+
     def softmax(self, x):
         x = np.array(x, dtype=np.float32)
         self.lib.or_softmax(x, x.size)
