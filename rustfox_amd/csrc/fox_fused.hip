@@ -73,9 +73,7 @@ __host__ __device__ inline FusedLds fused_lds(int fmt, int K, int M, int nslab)
 
 __device__ __forceinline__ double wave_sum_dd(double v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    return wave_reduce(v, 0.0, [](double x, double y) { return x + y; });
 }
 
 #define R4_LIMIT 8              // input dwords per thread: K <= 4 * R4_LIMIT * FWG
@@ -154,42 +152,66 @@ template <int IN, int R4MAX>
 __device__ __forceinline__ void load_input(const FusedArgs &a, int t, int K, InRegs<R4MAX> &in)
 {
     const int tid = threadIdx.x, nd = K >> 2;
-    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    // Every lane loads (past the end it re-reads dword nd - 1; in_mask drops
+    // the value at its first use): a load under a condition leaves the
+    // compiler unsure how many loads follow this one, and a register
+    // overwritten here waits for its load, so either would make the weight
+    // blocks issued next wait for the input.
     if (IN == IN_Q) {
         const uint32_t *q4 = (const uint32_t *)(a.q_in + (size_t)t * K);
 #pragma unroll
         for (int r = 0; r < R4MAX; r++) {
             const int m = tid + r * FWG;
-            in.qd[r] = m < nd ? q4[m] : 0u;
+            in.qd[r] = q4[m < nd ? m : nd - 1];
         }
         return;
     }
-    // (an if, not a select with a zero vector: the select becomes a load
-    // through a generic pointer, in 8-byte pieces)
     const float4 *x4 = (const float4 *)(a.x + (size_t)t * a.x_stride);
 #pragma unroll
     for (int r = 0; r < R4MAX; r++) {
         const int m = tid + r * FWG;
-        in.xv[r] = z4;
-        if (m < nd) in.xv[r] = x4[m];
+        in.xv[r] = x4[m < nd ? m : nd - 1];
     }
     if (IN == IN_NORM) {
         const float4 *w4 = (const float4 *)a.norm_w;
 #pragma unroll
         for (int r = 0; r < R4MAX; r++) {
             const int m = tid + r * FWG;
-            in.wv[r] = z4;
-            if (m < nd) in.wv[r] = w4[m];
+            in.wv[r] = w4[m < nd ? m : nd - 1];
+        }
+    }
+}
+
+// zero the input dwords past the end (at their first use; selects on the
+// values: a select between two float4 objects would put them in memory)
+__device__ __forceinline__ float4 keep4(bool ok, float4 v)
+{
+    return make_float4(ok ? v.x : 0.0f, ok ? v.y : 0.0f, ok ? v.z : 0.0f, ok ? v.w : 0.0f);
+}
+
+template <int IN, int R4MAX>
+__device__ __forceinline__ void in_mask(int K, InRegs<R4MAX> &in)
+{
+    const int tid = threadIdx.x, nd = K >> 2;
+#pragma unroll
+    for (int r = 0; r < R4MAX; r++) {
+        const bool ok = tid + r * FWG < nd;
+        if (IN == IN_Q) {
+            in.qd[r] = ok ? in.qd[r] : 0u;
+        } else {
+            in.xv[r] = keep4(ok, in.xv[r]);
+            if (IN == IN_NORM) in.wv[r] = keep4(ok, in.wv[r]);
         }
     }
 }
 
 template <int FMT, int IN, int R4MAX>
-__device__ float quantise_to_b(const FusedArgs &a, int t, int K, uint8_t *B, int32_t *aux,
+__device__ __forceinline__ float quantise_to_b(const FusedArgs &a, int t, int K, uint8_t *B, int32_t *aux,
                                double *dred, float *fred, InRegs<R4MAX> &in)
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int M = a.M, nd = K >> 2;
+    in_mask<IN, R4MAX>(K, in);
     uint32_t *qd = in.qd;
     float act = 0.0f;
     if (IN == IN_Q) {
@@ -209,30 +231,26 @@ __device__ float quantise_to_b(const FusedArgs &a, int t, int K, uint8_t *B, int
             ss = wave_sum_dd(ss);
             if (lane == 0) dred[wave] = ss;
             __syncthreads();
-            if (tid < 2) {
-                double tot = 0.0;
-                for (int w = 0; w < FW; w++) tot += dred[w];
-                // the tree sum certifies the float scale of the reference's
-                // index-order double sum (it lies within (K + 64) 2^-52 tot):
-                // lanes 0 and 1 evaluate the two ends of that interval
-                const double rel = (double)(K + 64) * 0x1p-52;
-                const double sgn = lane == 0 ? -1.0 : 1.0;
-                const double y = 1.0 / __builtin_sqrt(tot * (1.0 + sgn * rel) / (double)K +
-                                                      (double)a.eps) * (1.0 - sgn * 0x1p-50);
-                const float f = (float)y;
-                const float f_hi = __shfl(f, 0), f_lo = __shfl(f, 1);
-                if (lane != 0) {
-                } else if (f_hi == f_lo) {
-                    fred[0] = f_hi;
-                } else {
-                    const float *xt = a.x + (size_t)t * a.x_stride;
-                    double seq = 0.0;
-                    for (int i = 0; i < K; i++) seq += (double)xt[i] * (double)xt[i];
-                    fred[0] = (float)(1.0 / __builtin_sqrt(seq / (double)K + (double)a.eps));
-                }
+            // Every wave derives the scale itself (no second barrier).  The
+            // tree sum certifies the float scale of the reference's
+            // index-order double sum (it lies within (K + 64) 2^-52 tot):
+            // even lanes evaluate the low end of that interval, odd lanes the
+            // high end; equal floats are the reference's.
+            double tot = 0.0;
+            for (int w = 0; w < FW; w++) tot += dred[w];
+            const double rel = (double)(K + 64) * 0x1p-52;
+            const double sgn = (lane & 1) ? 1.0 : -1.0;
+            const double y = 1.0 / __builtin_sqrt(tot * (1.0 + sgn * rel) / (double)K +
+                                                  (double)a.eps) * (1.0 - sgn * 0x1p-50);
+            const float f = (float)y;
+            float rs = read_lane(f, 0);
+            if (rs != read_lane(f, 1)) {
+                // undecided: the sequential sum, by every lane (wave-uniform)
+                const float *xt = a.x + (size_t)t * a.x_stride;
+                double seq = 0.0;
+                for (int i = 0; i < K; i++) seq += (double)xt[i] * (double)xt[i];
+                rs = (float)(1.0 / __builtin_sqrt(seq / (double)K + (double)a.eps));
             }
-            __syncthreads();
-            const float rs = fred[0];
 #pragma unroll
             for (int r = 0; r < R4MAX; r++) {           // src/ops.c:17: x * scale * w
                 xv[r].x = xv[r].x * rs * wv[r].x;
@@ -345,7 +363,7 @@ __device__ __forceinline__ void block_mfma(const RawBlk &r, const uint8_t *__res
             acc = mfma(av[4 * u], av[4 * u + 1], av[4 * u + 2], av[4 * u + 3], bv[u], acc);
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const int oth = __shfl_xor(acc[q], 1);
+            const int oth = lane_xor1(acc[q]);
             S[q] = acc[q] - 3 * oth + corr;
         }
     } else {
@@ -399,6 +417,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     // scalar loads (an argument indexed at run time is a chain of loads).
     const int bx = blockIdx.x, nwg = gridDim.x;
     const int ntl = bx < a.n_work ? (a.n_work - 1 - bx) / nwg + 1 : 0;
+    if (ntl == 0) return;                                  // (the host launches none such)
     const int ts1 = a.tile_start[1], ts2 = a.tile_start[2], ts3 = a.tile_start[3];
     const int nseg = a.nseg;
     auto item = [&](int ti, int sl, int &sg, int &tl) {
@@ -426,10 +445,12 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     // input of token 0, the first weight blocks, the epilogue's operands
     InRegs<R4> in;
     load_input<IN, R4>(a, 0, K, in);
+    // (every wave issues PF block loads, past its last unit re-reading that
+    // one, so that the input's first use waits for the input only)
     RawBlk raw[PF];
 #pragma unroll
     for (int k = 0; k < PF; k++)
-        if (k < total) raw[k] = load_raw<FMT>(unit_ptr(k), lane);
+        raw[k] = load_raw<FMT>(total > 0 ? unit_ptr(k < total ? k : total - 1) : a.w[0], lane);
 
     // combiner threads: (slab, token, row) of an item's outputs
     const int nthr = nslab * 16 * M;
@@ -442,26 +463,36 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     if (EPI == EPI_ROPE)
         rp = (size_t)*(const __attribute__((address_space(4))) uint32_t *)a.pos + (size_t)ct;
     // epilogue operands of item ti for this thread (old output, RoPE table)
+    // (loads at clamped in-range addresses, values dropped where unused: a
+    // fixed number of loads keeps the compiler's waits exact)
     auto epi_load = [&](int ti, float &p0, float &p1) {
-        if (!comb || ti >= ntl) return;
         int sg, tl;
-        item(ti, csl, sg, tl);
-        const int orow = tl * 16 + crow;
-        if (orow >= pick4(a.n_rows, sg)) return;
-        if (EPI == EPI_STORE && (a.flags & FOX_GPU_GEMV_ACCUMULATE))
+        item(ti < ntl ? ti : ntl - 1, csl < nslab ? csl : 0, sg, tl);
+        const int nr = pick4(a.n_rows, sg);
+        int orow = tl * 16 + crow;
+        orow = orow < nr ? orow : nr - 1;
+        if (EPI == EPI_STORE)                               // used with ACCUMULATE only
             p0 = pick4(a.out, sg)[(size_t)ct * pick4(a.out_stride, sg) + orow];
-        if (EPI == EPI_ROPE && sg < 2 && rp < (size_t)a.n_ctx) {
+        if (EPI == EPI_ROPE) {
             const int half = a.head_dim / 2, i = (orow % a.head_dim) >> 1;
-            p0 = a.rope_cos[rp * half + i];
-            p1 = a.rope_sin[rp * half + i];
+            const size_t rc = rp < (size_t)a.n_ctx ? rp : (size_t)a.n_ctx - 1;
+            p0 = a.rope_cos[rc * half + i];
+            p1 = a.rope_sin[rc * half + i];
         }
     };
     float pre0 = 0.0f, pre1 = 0.0f;
     if (EPI == EPI_STORE) epi_load(0, pre0, pre1);
+    // (nothing that uses the input may be scheduled above the weight loads)
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- input stage: int8 activations straight into the B operand in LDS
-    for (int t = 0; t < M; t++) {
-        if (t > 0) load_input<IN, R4>(a, t, K, in);
+    // (token 0 outside the loop: its waits then count the loads above)
+    {
+        const float s = quantise_to_b<FMT, IN, R4>(a, 0, K, B, aux, dred, fred, in);
+        if (tid == 0) ascale[0] = s;
+    }
+    for (int t = 1; t < M; t++) {
+        load_input<IN, R4>(a, t, K, in);
         const float s = quantise_to_b<FMT, IN, R4>(a, t, K, B, aux, dred, fred, in);
         if (tid == 0) ascale[t] = s;
     }
@@ -508,7 +539,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
                     fox_div(gt, 1.0f + fox_expf(-gt)) * up; // src/ops.c:45-46
             }
         } else {  // EPI_ROPE: segment 0 q, 1 k, 2 v
-            const float partner = __shfl_xor(y, 1);
+            const float partner = lane_xor1(y);
             if (owns) {
                 const bool inside = rp < (size_t)a.n_ctx;
                 float v = y;

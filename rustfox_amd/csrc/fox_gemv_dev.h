@@ -47,21 +47,67 @@ __device__ __forceinline__ float half_bits_to_float(unsigned h)
 
 // ---------------------------------------------------------------- reduce
 
+// Lane movement through DPP (a VALU operand modifier, no LDS round trip).
+// CTL: 0xB1 quad_perm [1,0,3,2] (lane ^ 1), 0x4E quad_perm [2,3,0,1]
+// (lane ^ 2), 0x141 row_half_mirror (lane 7 - i within 8), 0x140 row_mirror
+// (lane 15 - i within 16), 0x142 row_bcast:15 (lane 15 of row r to row r + 1),
+// 0x143 row_bcast:31 (lane 31 to rows 2 and 3).  Rows outside RM keep `old`.
+template <int CTL, int RM, typename T>
+__device__ __forceinline__ T dpp_t(T old, T v)
+{
+    static_assert(sizeof(T) % 4 == 0, "32-bit words");
+    constexpr int N = sizeof(T) / 4;
+    struct W { int w[N]; };
+    const W o = __builtin_bit_cast(W, old), s = __builtin_bit_cast(W, v);
+    W r;
+#pragma unroll
+    for (int i = 0; i < N; i++) r.w[i] = __builtin_amdgcn_update_dpp(o.w[i], s.w[i], CTL, RM, 0xF, false);
+    return __builtin_bit_cast(T, r);
+}
+
+template <typename T>
+__device__ __forceinline__ T read_lane(T v, int l)
+{
+    constexpr int N = sizeof(T) / 4;
+    struct W { int w[N]; };
+    const W s = __builtin_bit_cast(W, v);
+    W r;
+#pragma unroll
+    for (int i = 0; i < N; i++) r.w[i] = __builtin_amdgcn_readlane(s.w[i], l);
+    return __builtin_bit_cast(T, r);
+}
+
+// v of lane ^ 1
+template <typename T>
+__device__ __forceinline__ T lane_xor1(T v)
+{
+    return dpp_t<0xB1, 0xF>(v, v);
+}
+
+// op over the 64 lanes (op associative and commutative, id its identity):
+// quads, 8 lanes, rows, then rows 0+1 into row 1 and 0..3 into row 3; the
+// result, read from lane 63, is wave-uniform
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_reduce(T v, T id, Op op)
+{
+    v = op(v, dpp_t<0xB1, 0xF>(id, v));
+    v = op(v, dpp_t<0x4E, 0xF>(id, v));
+    v = op(v, dpp_t<0x141, 0xF>(id, v));
+    v = op(v, dpp_t<0x140, 0xF>(id, v));
+    v = op(v, dpp_t<0x142, 0xA>(id, v));
+    v = op(v, dpp_t<0x143, 0xC>(id, v));
+    return read_lane(v, 63);
+}
+
+// max over the wave of values that are >= 0 and not NaN
 __device__ __forceinline__ float wave_max(float v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        float w = __shfl_xor(v, o);
-        v = w > v ? w : v;
-    }
-    return v;
+    return wave_reduce(v, 0.0f, [](float x, float y) { return y > x ? y : x; });
 }
 
 __device__ __forceinline__ int wave_sum_i(int v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    return wave_reduce(v, 0, [](int x, int y) { return x + y; });
 }
 
 // src/gemv.c:31-38 and src/kernels.c:744-751 for one element

@@ -536,10 +536,12 @@ __global__ __launch_bounds__(64) void attn_values_x(const float *__restrict__ at
 // ---- fused softmax + values (exact order), one workgroup per (kv head,
 // column slice, token), 16 waves; the kv head's G query heads x 64/G columns
 // make the 64 lanes of wave 0:
-//   all waves: head maxima from the per-tile maxima, e_j = expf(s_j - max)
-//     into LDS for the G heads;
-//   wave 0: one lane per head runs the position-order sum, then the wave
-//     scales e_j by 1/sum in place (a_j);
+//   waves 0-3: head maxima from the per-tile maxima (the scores themselves
+//     are already on their way to the loader waves);
+//   loader waves: e_j = expf(s_j - max) into LDS for the G heads, in rounds of
+//     SV_EXR positions, each round counted when a wave completes it;
+//   wave 0: one lane per head runs the position-order sum, round by round as
+//     the rounds complete, then 1/sum;
 //   loader waves: stream the slice's V columns (each 16-byte quad loaded once,
 //     two 64-position tiles in flight per wave from the start of the kernel),
 //     multiply by the G heads' a_j and hand the products to wave 0 through a
@@ -549,9 +551,13 @@ __global__ __launch_bounds__(64) void attn_values_x(const float *__restrict__ at
 // every wait is bounded (a wave that times out writes NaN and leaves).
 #define SV_WAVES 16
 #define SV_QT 16                    // quads (4 positions) per stage
-#define SV_NP 4                     // product stages
+#define SV_NP_MAX 8                 // product stages: as many as fit beside the weights
+#define SV_NP_MIN 3
 #define SV_LOADERS 12               // waves 1-3, 5-7, 9-11, 13-15
-#define SV_E_MAX (80 * 1024)        // LDS bytes for the weights of the group
+#define SV_LDS_MAX (159 * 1024)     // dynamic LDS of the kernel (160 KB less its static part)
+#define SV_STAGE (SV_QT * 64 * 16)  // bytes per product stage
+#define SV_EXR (SV_LOADERS * 64)    // positions per exp round
+#define SV_EXP_PF 3                 // exp rounds whose scores are loaded up front
 #define SV_SPIN (1 << 22)
 
 // v of lane (quad base + sel) for each lane, sel from a quad_perm control
@@ -636,18 +642,19 @@ template <int G>
 __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
     const float *__restrict__ att, size_t att_stride, const float *__restrict__ tmax, int n_tiles,
     const float *__restrict__ vc, int n_head, int n_head_kv, int hd,
-    const uint32_t *__restrict__ pos, int n_ctx, float *__restrict__ out, size_t out_stride)
+    const uint32_t *__restrict__ pos, int n_ctx, float *__restrict__ out, size_t out_stride,
+    int np)
 {
     constexpr int DS = 64 / G;               // columns per slice
     constexpr int NLD = SV_QT / G;           // 16-byte loads per lane per tile
     constexpr bool DB = G > 1;               // second tile in flight
     extern __shared__ float4 sv_lds[];
-    float4 *ring = sv_lds;                                  // [SV_NP][SV_QT][64]
-    float *e = (float *)(sv_lds + SV_NP * SV_QT * 64);      // [G][att_stride + 4]
+    float4 *ring = sv_lds;                                  // [np][SV_QT][64]
+    float *e = (float *)(sv_lds + np * SV_QT * 64);         // [G][att_stride + 4]
     __shared__ float mx_s[G], inv_s[G];
     __shared__ int nrm_s[G];
     __shared__ uint64_t tab[32];
-    __shared__ int ready[SV_NP], consumed, a_ready;
+    __shared__ int ready[SV_NP_MAX], consumed, a_ready, e_done;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kvd = n_head_kv * hd;
@@ -673,6 +680,20 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
         }
     }
 
+    // scores of the first SV_EXP_PF exp rounds, loaded now: their latency
+    // overlaps the head maxima
+    const int ex0 = li * 64 + lane;                 // loader's position in a round
+    float sc[SV_EXP_PF][G];
+    if (loader) {
+#pragma unroll
+        for (int k = 0; k < SV_EXP_PF; k++) {
+            const int p = k * SV_EXR + ex0;
+#pragma unroll
+            for (int gg = 0; gg < G; gg++)
+                sc[k][gg] = srow[(size_t)gg * att_stride + (p < upto ? p : 0)];
+        }
+    }
+
     // ---- head maxima (src/ops.c:26-30: a NaN first score stays the max)
     if (wave < G) {
         const float *tm = tmax + ((size_t)t * n_head + (size_t)kvh * G + wave) * n_tiles;
@@ -690,41 +711,62 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
         const float s0 = srow[(size_t)wave * att_stride];
         if (lane == 0) mx_s[wave] = s0 != s0 ? s0 : m;
     }
-    if (tid < SV_NP) ready[tid] = -1;
+    if (tid < SV_NP_MAX) ready[tid] = -1;
     if (tid < 32) tab[tid] = fox_exp2_tab[tid];
     if (tid == 0) {
         consumed = 0;
         a_ready = 0;
+        e_done = 0;
     }
     __syncthreads();
-    // e_j = expf(s_j - max): a thread's scores are loaded before any is used
-    for (int j0 = 0; j0 < upto; j0 += 4 * SV_WAVES * 64) {
-        float sc[G][4];
+    if (!loader && wave != 0) return;                // (SIMD 0 stays with wave 0)
+
+    if (loader) {
+        // ---- e_j = expf(s_j - max) (src/ops.c:31-34) in rounds of SV_EXR
+        // positions; a wave counts each round it completes
+        float mx[G];
 #pragma unroll
-        for (int gg = 0; gg < G; gg++)
+        for (int gg = 0; gg < G; gg++) mx[gg] = mx_s[gg];
+        auto exp_round = [&](int k, const float *scr) {
+            const int p = k * SV_EXR + ex0;
+            if (p < upto) {
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int j = j0 + r * SV_WAVES * 64 + tid;
-                sc[gg][r] = j < upto ? srow[(size_t)gg * att_stride + j] : 0.0f;
+                for (int gg = 0; gg < G; gg++) e[gg * estr + p] = fox_expf_t(scr[gg] - mx[gg], tab);
             }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            if (lane == 0) __hip_atomic_fetch_add(&e_done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        };
 #pragma unroll
-        for (int gg = 0; gg < G; gg++)
+        for (int k = 0; k < SV_EXP_PF; k++)
+            if (k * SV_EXR < upto) exp_round(k, sc[k]);
+        for (int k = SV_EXP_PF; k * SV_EXR < upto; k++) {
+            const int p = k * SV_EXR + ex0;
+            float s2[G];
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int j = j0 + r * SV_WAVES * 64 + tid;
-                if (j < upto) e[gg * estr + j] = fox_expf_t(sc[gg][r] - mx_s[gg], tab);
-            }
+            for (int gg = 0; gg < G; gg++) s2[gg] = srow[(size_t)gg * att_stride + (p < upto ? p : 0)];
+            exp_round(k, s2);
+        }
     }
-    __syncthreads();
 
     if (wave == 0) {
-        // ---- softmax sums, one lane per head, position order
+        // ---- softmax sums, one lane per head, position order; round k is
+        // added once every loader wave has counted it
         float sum = 0.0f;
-        if (lane < G) {
-            const float *er = e + lane * estr;
-            sum = chain_add_lds(0.0f, (const float4 *)er, nq);
-            for (int j = 4 * nq; j < upto; j++) sum = sum + er[j];
+        bool eok = true;
+        for (int k = 0; k * SV_EXR < upto; k++) {
+            if (!sv_wait_ge(&e_done, SV_LOADERS * (k + 1))) {
+                eok = false;
+                break;
+            }
+            const int p0 = k * SV_EXR, p1 = min(upto, p0 + SV_EXR);
+            if (lane < G) {
+                const float *er = e + lane * estr;
+                const int nqk = (p1 - p0) >> 2;
+                sum = chain_add_lds(sum, (const float4 *)(er + p0), nqk);
+                for (int j = p0 + 4 * nqk; j < p1; j++) sum = sum + er[j];
+            }
         }
+        if (!eok) sum = __builtin_nanf("");
         // a_j = e_j * (1/sum) is formed by the loaders (src/ops.c:35-38)
         if (lane < G) {
             nrm_s[lane] = sum > 0.0f;
@@ -738,7 +780,7 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
         // the second is added.
         const int g = lane / DS, d = sl * DS + (lane - g * DS);
         float acc = 0.0f;
-        bool ok = sv_wait_ge(&ready[0], 0);
+        bool ok = eok && sv_wait_ge(&ready[0], 0);
         float4 X[8], Y[8];
         // ring slots are XOR-swizzled by (quad & 3) so that the loaders' four
         // quads per store fall in different banks
@@ -752,14 +794,16 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
         // whole tiles: one basic block per tile.  The next tile's flag is read
         // before the first half is added and tested after it (through a
         // zero that depends on the sum, so the test cannot move up).
+        // (stage of tile i: i mod np, kept as a running index)
         const int nwhole = nq / SV_QT;
-        int i = 0;
+        int i = 0, st = 0;
         for (; i < nwhole; i++) {
-            const float4 *P = ring + (i % SV_NP) * SV_QT * 64;
-            const float4 *Pn = ring + ((i + 1) % SV_NP) * SV_QT * 64;
+            const int stn = st + 1 == np ? 0 : st + 1;
+            const float4 *P = ring + st * SV_QT * 64;
+            const float4 *Pn = ring + stn * SV_QT * 64;
 #pragma unroll
             for (int u = 0; u < 8; u++) Y[u] = P[(8 + u) * 64 + sw[u & 3]];
-            const int nf = sv_peek(&ready[(i + 1) % SV_NP]);
+            const int nf = sv_peek(&ready[stn]);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int u = 0; u < 8; u++) {
@@ -767,7 +811,7 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
             }
             int z;
             asm volatile("v_mov_b32 %0, 0" : "=v"(z) : "v"(acc));
-            if (nf + z < i + 1 && i + 1 < ntile && !sv_wait_ge(&ready[(i + 1) % SV_NP], i + 1)) {
+            if (nf + z < i + 1 && i + 1 < ntile && !sv_wait_ge(&ready[stn], i + 1)) {
                 ok = false;
                 break;
             }
@@ -780,10 +824,11 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
                 acc = acc + Y[u].x; acc = acc + Y[u].y; acc = acc + Y[u].z; acc = acc + Y[u].w;
             }
             sv_signal(&consumed, i + 1);
+            st = stn;
         }
         // the last tile, partly filled: nfull whole quads, then rem positions
         if (ok && i < ntile) {
-            const float4 *P = ring + (i % SV_NP) * SV_QT * 64;
+            const float4 *P = ring + st * SV_QT * 64;
 #pragma unroll
             for (int u = 0; u < 8; u++) Y[u] = P[(8 + u) * 64 + sw[u & 3]];
             const int nfull = nq - i * SV_QT;
@@ -818,6 +863,9 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
         inv[gg] = inv_s[gg];
         nrm[gg] = nrm_s[gg];
     }
+    // (stage of tile i: i mod np, kept as a running index)
+    const int st_step = SV_LOADERS % np;
+    int s = li % np;
     for (int i = li; i < ntile; i += SV_LOADERS) {
         const int inext = i + SV_LOADERS;
         if (DB && inext < ntile) {
@@ -827,8 +875,7 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
                 vnext[DB ? k : 0] = v4[(size_t)jq * kvd];
             }
         }
-        const int s = i % SV_NP;
-        if (i >= SV_NP && !sv_wait_ge(&consumed, i - SV_NP + 1)) return;
+        if (i >= np && !sv_wait_ge(&consumed, i - np + 1)) return;
         float4 *P = ring + s * SV_QT * 64;
 #pragma unroll
         for (int k = 0; k < NLD; k++) {
@@ -868,6 +915,8 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
             }
         }
         sv_signal(&ready[s], i);
+        s += st_step;
+        if (s >= np) s -= np;
         if (DB) {
 #pragma unroll
             for (int k = 0; k < NLD; k++) vcur[k] = vnext[DB ? k : 0];
@@ -938,8 +987,11 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
                        : gqa == 2 ? (const void *)attn_sv_x<2>
                        : gqa == 4 ? (const void *)attn_sv_x<4>
                        : gqa == 8 ? (const void *)attn_sv_x<8> : nullptr;
-        if (sv && e_bytes <= SV_E_MAX) {
-            const size_t sv_lds = (size_t)SV_NP * SV_QT * 64 * 16 + e_bytes;
+        // product stages: as many as fit beside the weights (at least SV_NP_MIN)
+        const size_t np_fit = e_bytes < SV_LDS_MAX ? (SV_LDS_MAX - e_bytes) / SV_STAGE : 0;
+        const int np = (int)(np_fit < SV_NP_MAX ? np_fit : SV_NP_MAX);
+        if (sv && np >= SV_NP_MIN) {
+            const size_t sv_lds = (size_t)np * SV_STAGE + e_bytes;
             hipError_t e = hipFuncSetAttribute(sv, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                (int)sv_lds);
             if (e != hipSuccess) return fox_hip_fail(e, "attention: LDS size");
@@ -947,7 +999,8 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
             const unsigned nsl = (unsigned)((head_dim + sv_ds - 1) / sv_ds);
             void *args[] = {(void *)&att, (void *)&att_stride, (void *)&tmax, (void *)&n_tiles,
                             (void *)&v_cache, (void *)&ih, (void *)&ikv, (void *)&ihd,
-                            (void *)&pos, (void *)&ictx, (void *)&out, (void *)&os};
+                            (void *)&pos, (void *)&ictx, (void *)&out, (void *)&os,
+                            (void *)&np};
             e = hipLaunchKernel(sv, dim3((unsigned)n_head_kv * nsl, (unsigned)M),
                                 dim3(SV_WAVES * 64), args, sv_lds, ctx->stream);
             if (e != hipSuccess) return fox_hip_fail(e, "attention softmax+values");

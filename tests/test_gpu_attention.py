@@ -58,7 +58,8 @@ CASES = [  # n_head, n_kv, hd, n_ctx, pos, M
     (4, 1, 128, 64, 0, 1),         # a single visible row
     (16, 2, 128, 257, 200, 8),     # 8 tokens (verify batch), gqa 8
     (12, 4, 64, 100, 99, 1),       # gqa 3: the three-kernel path
-    (8, 2, 64, 6000, 5990, 2),     # weights beyond the fused kernel's LDS: three-kernel path
+    (8, 2, 64, 6000, 5990, 2),     # weights leave room for few product stages (4)
+    (8, 2, 64, 9000, 8990, 2),     # weights beyond the fused kernel's LDS: three-kernel path
 ]
 
 
