@@ -78,62 +78,77 @@ __device__ __forceinline__ double wave_sum_dd(double v)
 
 #define R4_LIMIT 8              // input dwords per thread: K <= 4 * R4_LIMIT * FWG
 
-__device__ __forceinline__ uint32_t pack_q4(float4 v, float inv)
-{
-    return (uint32_t)(uint8_t)quant_one(v.x, inv) | (uint32_t)(uint8_t)quant_one(v.y, inv) << 8 |
-           (uint32_t)(uint8_t)quant_one(v.z, inv) << 16 |
-           (uint32_t)(uint8_t)quant_one(v.w, inv) << 24;
-}
+// Where lane dl's int8 dword (block-local elements 4 dl .. 4 dl + 3) goes in
+// a block's B operand for one token: the layouts of act_prep (fox_gemv.hip),
+// which mirror the A slots of the block decode, as byte offsets from the
+// block's token-t base.  TQ1: dword A at slot lev of section sec, column 0;
+// dword B at slot lev - 1, column 1 (lev >= 1); a zero at slot 4 of the
+// section, column 1 (lev == 4); lanes 60..63 (the qh elements 240..255) hold
+// slot 15 of group dl - 60 instead, byte-transposed (qh_dwords).  TQ2: one
+// dword.
+struct BLane {
+    int offA, offB, offC;
+    bool hasB, hasC;
+};
 
-__device__ __forceinline__ int sum_q4(uint32_t d)
-{
-    return (int)(int8_t)d + (int)(int8_t)(d >> 8) + (int)(int8_t)(d >> 16) + (int)(int8_t)(d >> 24);
-}
-
-// Place the int8 dword of block-local dword index dl (elements 4dl..4dl+3)
-// of block b, token t, into the B operand: the layouts of act_prep
-// (fox_gemv.hip), which mirror the A slots of the block decode.
 template <int FMT>
-__device__ __forceinline__ void put_b(uint8_t *B, int M, int b, int t, int dl, uint32_t d)
+__device__ __forceinline__ BLane b_lane(int dl, int M)
 {
+    BLane L;
     if (FMT == FMT_TQ1) {
-        // B entry (b, u, g, column 2t + c) is 16 bytes; dword w is slot s = 4u + w
-        auto at = [&](int s, int g, int c) -> uint8_t * {
-            return B + ((((b * 4 + (s >> 2)) * 4 + g) * (2 * M) + 2 * t + c) * 16) + (s & 3) * 4;
-        };
-        if (dl < 60) {
-            int lev, g, sec;
-            if (dl < 40) {
-                lev = dl >> 3;
-                g = (dl & 7) >> 1;
-                sec = dl & 1;
-            } else {
-                lev = (dl - 40) >> 2;
-                g = (dl - 40) & 3;
-                sec = 2;
-            }
-            // column 0 pairs level lev with slot level lev + 1, column 1 with lev
-            *(uint32_t *)at(5 * sec + lev, g, 0) = d;
-            if (lev >= 1) *(uint32_t *)at(5 * sec + lev - 1, g, 1) = d;
-            if (lev == 4) *(uint32_t *)at(5 * sec + 4, g, 1) = 0u;
+        // byte offset of slot s, group g, column c: B entry (u = s / 4, g,
+        // column 2t + c) is 16 bytes, dword s % 4 of it
+        auto off = [&](int s, int g, int c) { return ((s >> 2) * 4 + g) * 32 * M + 16 * c + (s & 3) * 4; };
+        int lev, g, sec;
+        if (dl < 40) {
+            lev = dl >> 3;
+            g = (dl & 7) >> 1;
+            sec = dl & 1;
         } else {
-            // qh elements 240 + 4 lev + g: byte g of dword lev; slot 15 byte lev
-            // (column 0) and byte lev - 1 (column 1; byte 3 of column 1 is 0)
-            const int lev = dl - 60;
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const uint8_t v = (uint8_t)(d >> (8 * g));
-                at(15, g, 0)[lev] = v;
-                if (lev >= 1) at(15, g, 1)[lev - 1] = v;
-                if (lev == 3) at(15, g, 1)[3] = 0;
-            }
+            lev = (dl - 40) >> 2;
+            g = (dl - 40) & 3;
+            sec = 2;
         }
-    } else {  // FMT_TQ2: elements e0 = 4 dl .. : half (g >> 1), level l, offset 16 (g & 1) + 4 u
+        if (dl < 60) {
+            L.offA = off(5 * sec + lev, g, 0);
+            L.offB = off(5 * sec + (lev >= 1 ? lev - 1 : 0), g, 1);
+            L.offC = off(5 * sec + 4, g, 1);
+            L.hasB = lev >= 1;
+            L.hasC = lev == 4;
+        } else {
+            L.offA = off(15, dl - 60, 0);
+            L.offB = off(15, dl - 60, 1);
+            L.offC = 0;
+            L.hasB = true;
+            L.hasC = false;
+        }
+    } else {  // elements e0 = 4 dl ..: half (g >> 1), level l, offset 16 (g & 1) + 4 u
         const int e0 = 4 * dl;
-        const int half = e0 >> 7, l = (e0 >> 5) & 3, off = e0 & 31;
-        const int g = 2 * half + (off >> 4), u = (off & 15) >> 2;
-        *(uint32_t *)(B + (((b * 4 + u) * 4 + g) * M + t) * 16 + l * 4) = d;
+        const int half = e0 >> 7, l = (e0 >> 5) & 3, o = e0 & 31;
+        const int g = 2 * half + (o >> 4), u = (o & 15) >> 2;
+        L.offA = ((u * 4 + g) * M) * 16 + l * 4;
+        L.offB = L.offC = 0;
+        L.hasB = L.hasC = false;
     }
+    return L;
+}
+
+// TQ1 slot 15 for the lane's quad of lanes (lanes 60..63 hold the qh
+// dwords d_0..d_3 of elements 240 + 4 lev + g, byte g of d_lev): lane
+// 60 + g gets column 0 = (d_0, d_1, d_2, d_3 byte g) and column 1 =
+// (d_1, d_2, d_3 byte g, 0); other lanes compute values they do not use
+__device__ __forceinline__ void qh_dwords(uint32_t d, int g, uint32_t &c0, uint32_t &c1)
+{
+    const uint32_t d0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)d, 0x00, 0xF, 0xF, false);
+    const uint32_t d1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)d, 0x55, 0xF, 0xF, false);
+    const uint32_t d2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)d, 0xAA, 0xF, 0xF, false);
+    const uint32_t d3 = (uint32_t)__builtin_amdgcn_mov_dpp((int)d, 0xFF, 0xF, 0xF, false);
+    const uint32_t ug = (uint32_t)g;
+    const uint32_t lo = ug | (ug + 4) << 8 | 0x0c0c0000u;     // bytes 0, 1 from (S1, S0) byte g
+    const uint32_t hi = 0x0c0cu | ug << 16 | (ug + 4) << 24;  // bytes 2, 3 from (S1, S0) byte g
+    const uint32_t b2 = 0x0c000c0cu | ug << 16;               // byte 2 from S1 byte g
+    c0 = __builtin_amdgcn_perm(d1, d0, lo) | __builtin_amdgcn_perm(d3, d2, hi);
+    c1 = __builtin_amdgcn_perm(d2, d1, lo) | __builtin_amdgcn_perm(0u, d3, b2);
 }
 
 // Token t of the input: optional RMSNorm (src/ops.c:7-22), per-vector int8
@@ -207,35 +222,36 @@ __device__ __forceinline__ void in_mask(int K, InRegs<R4MAX> &in)
 
 template <int FMT, int IN, int R4MAX>
 __device__ __forceinline__ float quantise_to_b(const FusedArgs &a, int t, int K, uint8_t *B, int32_t *aux,
-                               double *dred, float *fred, InRegs<R4MAX> &in)
+                                               double *dred, uint32_t *ured, InRegs<R4MAX> &in)
 {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int M = a.M, nd = K >> 2;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int M = a.M, nb = K >> 8;
     in_mask<IN, R4MAX>(K, in);
     uint32_t *qd = in.qd;
     float act = 0.0f;
-    if (IN == IN_Q) {
-        act = a.scale_in ? a.scale_in[t] : 0.0f;    // block sums come without a scale
-    } else {
+    if (IN != IN_Q) {
         float4 *xv = in.xv;
         if (IN == IN_NORM) {
             const float4 *wv = in.wv;
             double ss = 0.0;
 #pragma unroll
             for (int r = 0; r < R4MAX; r++) {
-                ss += (double)xv[r].x * (double)xv[r].x;
-                ss += (double)xv[r].y * (double)xv[r].y;
-                ss += (double)xv[r].z * (double)xv[r].z;
-                ss += (double)xv[r].w * (double)xv[r].w;
+                const double x0 = xv[r].x, x1 = xv[r].y, x2 = xv[r].z, x3 = xv[r].w;
+                ss = __builtin_fma(x0, x0, ss);
+                ss = __builtin_fma(x1, x1, ss);
+                ss = __builtin_fma(x2, x2, ss);
+                ss = __builtin_fma(x3, x3, ss);
             }
             ss = wave_sum_dd(ss);
             if (lane == 0) dred[wave] = ss;
             __syncthreads();
             // Every wave derives the scale itself (no second barrier).  The
             // tree sum certifies the float scale of the reference's
-            // index-order double sum (it lies within (K + 64) 2^-52 tot):
-            // even lanes evaluate the low end of that interval, odd lanes the
-            // high end; equal floats are the reference's.
+            // index-order double sum (it lies within (K + 64) 2^-52 tot, and
+            // the scale is monotone in the sum): even lanes evaluate the low
+            // end of that interval, odd lanes the high end; equal floats are
+            // the reference's.
             double tot = 0.0;
             for (int w = 0; w < FW; w++) tot += dred[w];
             const double rel = (double)(K + 64) * 0x1p-52;
@@ -259,50 +275,102 @@ __device__ __forceinline__ float quantise_to_b(const FusedArgs &a, int t, int K,
                 xv[r].w = xv[r].w * rs * wv[r].w;
             }
         }
-        float m = 0.0f;
+        // amax (src/gemv.c:20-23) as the largest |x| bit pattern: for x >= 0
+        // the integer order is the float order, and NaN lies above inf
+        uint32_t mb = 0;
 #pragma unroll
         for (int r = 0; r < R4MAX; r++) {
-            const float v4[4] = {xv[r].x, xv[r].y, xv[r].z, xv[r].w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const float av = fabsf(v4[e]);
-                if (av > m) m = av;
-            }
+            mb = max(mb, __float_as_uint(xv[r].x) & 0x7fffffffu);
+            mb = max(mb, __float_as_uint(xv[r].y) & 0x7fffffffu);
+            mb = max(mb, __float_as_uint(xv[r].z) & 0x7fffffffu);
+            mb = max(mb, __float_as_uint(xv[r].w) & 0x7fffffffu);
         }
-        m = wave_max(m);
-        if (lane == 0) fred[1 + wave] = m;
+        mb = wave_reduce(mb, 0u, [](uint32_t x, uint32_t y) { return x > y ? x : y; });
+        if (lane == 0) ured[wave] = mb;
         __syncthreads();
-        float amax = 0.0f;
-        for (int w = 0; w < FW; w++) if (fred[1 + w] > amax) amax = fred[1 + w];
-        if (amax > 0.0f) {
-            const float inv = (float)(127.0 / (double)amax);
+        uint32_t am = 0;
+        for (int w = 0; w < FW; w++) am = max(am, ured[w]);
+        if (am >= 0x03800000u && am < 0x7f800000u) {
+            // amax in [2^-120, inf), no NaN: quant_fast applies
+            const float amax = __uint_as_float(am);
+            const float inv = fox_div(127.0f, amax);
 #pragma unroll
-            for (int r = 0; r < R4MAX; r++) qd[r] = pack_q4(xv[r], inv);
-            act = (float)((double)amax / 127.0);
-        } else {
+            for (int r = 0; r < R4MAX; r++)
+                qd[r] = pack_lo_bytes(quant_fast(xv[r].x, inv), quant_fast(xv[r].y, inv),
+                                      quant_fast(xv[r].z, inv), quant_fast(xv[r].w, inv));
+            act = fox_div(amax, 127.0f);
+        } else if (am == 0) {
 #pragma unroll
             for (int r = 0; r < R4MAX; r++) qd[r] = 0u;
+        } else {
+            // NaN, inf or a tiny amax (wave-uniform): the float amax of the
+            // non-NaN values (src/gemv.c:20-23), then the exact quantiser
+            float m = 0.0f;
+#pragma unroll
+            for (int r = 0; r < R4MAX; r++) {
+                const float v4[4] = {xv[r].x, xv[r].y, xv[r].z, xv[r].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float av = fabsf(v4[e]);
+                    if (av > m) m = av;
+                }
+            }
+            m = wave_max(m);
+            __syncthreads();
+            if (lane == 0) ured[wave] = __float_as_uint(m);
+            __syncthreads();
+            float amax = 0.0f;
+            for (int w = 0; w < FW; w++) amax = max(amax, __uint_as_float(ured[w]));
+            if (amax > 0.0f) {
+                const float inv = fox_div(127.0f, amax);
+#pragma unroll
+                for (int r = 0; r < R4MAX; r++)
+                    qd[r] = pack_lo_bytes(quant_one(xv[r].x, inv), quant_one(xv[r].y, inv),
+                                          quant_one(xv[r].z, inv), quant_one(xv[r].w, inv));
+                act = fox_div(amax, 127.0f);
+            } else {
+#pragma unroll
+                for (int r = 0; r < R4MAX; r++) qd[r] = 0u;
+            }
         }
     }
-    // B operand and per-block corrections
+    // B operand and per-block corrections; a wave's 64 lanes are one block
+    const BLane bl = b_lane<FMT>(lane, M);
+    const int bbytes = b_bytes_per_block_tok(FMT) * M;
+    const int tbytes = FMT == FMT_TQ1 ? 32 : 16;
+    // TQ1: corr = 128 * (sum of elements 128..159 and 224..239) - block sum
+    const bool in4 = (lane >= 32 && lane < 40) || (lane >= 56 && lane < 60);
 #pragma unroll
     for (int r = 0; r < R4MAX; r++) {
-        const int m = tid + r * FWG;
-        if (r * FWG >= nd) break;                      // uniform: no block left
-        const int b = m >> 6, dl = lane;               // m & 63 == lane
-        if (m < nd) put_b<FMT>(B, M, b, t, dl, qd[r]);
-        int s = m < nd ? sum_q4(qd[r]) : 0;
+        const int b = wave + FW * r;
+        if (b >= nb) break;                            // uniform: no block left
+        uint8_t *Bb = B + b * bbytes + t * tbytes;
+        const uint32_t d = qd[r];
+        uint32_t dA = d, dB = d;
         if (FMT == FMT_TQ1) {
-            // corr = 128 * (sum of elements 128..159 and 224..239) - block sum
-            int s4 = ((dl >= 32 && dl < 40) || (dl >= 56 && dl < 60)) ? s : 0;
-            s = wave_sum_i(s);
-            s4 = wave_sum_i(s4);
-            if (lane == 0 && m < nd) aux[b * M + t] = 128 * s4 - s;
+            uint32_t c0, c1;
+            qh_dwords(d, lane & 3, c0, c1);
+            if (lane >= 60) {
+                dA = c0;
+                dB = c1;
+            }
+        }
+        *(uint32_t *)(Bb + bl.offA) = dA;
+        if (bl.hasB) *(uint32_t *)(Bb + bl.offB) = dB;
+        if (bl.hasC) *(uint32_t *)(Bb + bl.offC) = 0u;
+        const int sd = __builtin_amdgcn_sdot4((int)d, 0x01010101, 0, false);
+        if (FMT == FMT_TQ1) {
+            // block sum s and partial sum s4 in one reduction: |s| < 2^15
+            const int tot = wave_sum_i(sd + (in4 ? sd : 0) * 65536);
+            const int s = (int)(short)(tot & 0xffff);
+            const int s4 = (tot - s) / 65536;
+            if (lane == 0) aux[b * M + t] = 128 * s4 - s;
         } else {
-            s = wave_sum_i(s);
-            if (lane == 0 && m < nd) aux[b * M + t] = -s;
+            const int s = wave_sum_i(sd);
+            if (lane == 0) aux[b * M + t] = -s;
         }
     }
+    if (IN == IN_Q) act = a.scale_in ? a.scale_in[t] : 0.0f;   // block sums come without a scale
     __syncthreads();
     return act;
 }
@@ -397,7 +465,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     extern __shared__ uint4 fused_lds4[];
     uint8_t *lds = (uint8_t *)fused_lds4;
     __shared__ double dred[FW];
-    __shared__ float fred[1 + FW];
+    __shared__ uint32_t ured[FW];
     __shared__ float ascale[FOX_GPU_MAX_TOKENS];
 
     constexpr int CHUNK = FMT == FMT_TQ1 ? TQ1_CHUNK : TQ2_CHUNK;
@@ -488,12 +556,12 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     // ---- input stage: int8 activations straight into the B operand in LDS
     // (token 0 outside the loop: its waits then count the loads above)
     {
-        const float s = quantise_to_b<FMT, IN, R4>(a, 0, K, B, aux, dred, fred, in);
+        const float s = quantise_to_b<FMT, IN, R4>(a, 0, K, B, aux, dred, ured, in);
         if (tid == 0) ascale[0] = s;
     }
     for (int t = 1; t < M; t++) {
         load_input<IN, R4>(a, t, K, in);
-        const float s = quantise_to_b<FMT, IN, R4>(a, t, K, B, aux, dred, fred, in);
+        const float s = quantise_to_b<FMT, IN, R4>(a, t, K, B, aux, dred, ured, in);
         if (tid == 0) ascale[t] = s;
     }
     if (EPI == EPI_ROPE) epi_load(0, pre0, pre1);

@@ -110,15 +110,36 @@ __device__ __forceinline__ int wave_sum_i(int v)
     return wave_reduce(v, 0, [](int x, int y) { return x + y; });
 }
 
-// src/gemv.c:31-38 and src/kernels.c:744-751 for one element
+// src/gemv.c:31-38 and src/kernels.c:744-751 for one element.  The (int)
+// conversion of the reference's x86 build (cvttss2si) gives INT_MIN for NaN
+// and for values outside int range, which the clamp turns into -127; the
+// GPU conversion would give 0 or a saturated value, so those cases are
+// mapped explicitly.
 __device__ __forceinline__ int8_t quant_one(float x, float inv)
 {
     float v = x * inv;
     float t = v < 0.0f ? v - 0.5f : v + 0.5f;
-    int r = (int)t;
+    int r = (t >= -2147483648.0f && t < 2147483648.0f) ? (int)t : (int)0x80000000u;
     r = r > 127 ? 127 : r;
     r = r < -127 ? -127 : r;
     return (int8_t)r;
+}
+
+// quant_one when |x| <= amax with amax in [2^-120, inf) and inv = 127 / amax:
+// inv is finite, |x * inv| < 127.5 so no clamp applies, and v +/- 0.5 is
+// v + copysign(0.5, v) (for v = -0.0 both truncate to 0)
+__device__ __forceinline__ int quant_fast(float x, float inv)
+{
+    const float v = x * inv;
+    return (int)(v + __builtin_copysignf(0.5f, v));
+}
+
+// the low bytes of r0..r3 as one dword, byte k from r_k
+__device__ __forceinline__ uint32_t pack_lo_bytes(int r0, int r1, int r2, int r3)
+{
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)r1, (uint32_t)r0, 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)r3, (uint32_t)r2, 0x04000c0cu);
+    return lo | hi;
 }
 
 // Element index (within a 256-block) behind byte p of slot s of lane group g,

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import rustfox_amd as rf
-from test_gpu_gemv import weights, bits
+from test_gpu_gemv import weights, bits, nonfinite_rows, same_or_both_nan
 
 pytestmark = pytest.mark.gpu
 
@@ -100,6 +100,30 @@ def test_gate_up_silu_bit_exact(gpu, oracle, gtype, K, ff, M):
         xb = oracle.rmsnorm(x[t], nw, EPS)
         want = oracle.silu_mul(oracle.gemv(gtype, xb, Wg, ff, K), oracle.gemv(gtype, xb, Wu, ff, K))
         assert np.array_equal(bits(got[t]), bits(want)), f"token {t}"
+
+
+@pytest.mark.parametrize("gtype", [34, 35])
+def test_gemv_rmsnorm_nonfinite_follows_the_reference(gpu, oracle, gtype):
+    """RMSNorm then quantisation on rows with NaN, inf and tiny values, and
+    on a normal row scaled by norm weights that hold a NaN and an inf: the
+    exact path of the in-workgroup quantiser (NaN outputs compared as NaN)."""
+    rng = np.random.default_rng(31 + gtype)
+    K, N = 512, 40
+    W = weights(rng, gtype, N, K)
+    t = gpu.tensor(gtype, K, N, W)
+    rows = list(nonfinite_rows(rng, K))
+    nws = [rng.uniform(0.5, 1.5, K).astype(np.float32) for _ in rows]
+    x = rng.standard_normal(K).astype(np.float32)
+    for bad in (np.nan, np.inf):
+        nw = rng.uniform(0.5, 1.5, K).astype(np.float32)
+        nw[7] = bad
+        rows.append(x)
+        nws.append(nw)
+    for r, (xr, nw) in enumerate(zip(rows, nws)):
+        out = gpu.array(np.zeros((1, N), np.float32))
+        gpu.gemv_rmsnorm([t], gpu.array(xr[None, :]), 1, gpu.array(nw), EPS, [out], 0)
+        want = oracle.gemv(gtype, oracle.rmsnorm(xr, nw, EPS), W, N, K)
+        assert same_or_both_nan(out.numpy()[0], want), r
 
 
 def test_unsupported_cases_say_so(gpu):

@@ -137,6 +137,72 @@ def test_quantize_exact(gpu, oracle, K, M, mode):
             assert np.array_equal(bits(s.reshape(M, -1)[t]), bits(ws))
 
 
+def nonfinite_rows(rng, K):
+    """Activation rows the fast quantiser must hand to its exact path: a NaN
+    (amax skips it, its q is the x86 conversion of NaN: -127), +inf and -inf
+    (amax = inf, inv = 0), a subnormal amax (inv = inf) and an amax just
+    above 2^-120 (the fast path's limit)."""
+    rows = []
+    for kind in ("nan", "inf", "-inf", "tiny", "edge"):
+        x = rng.standard_normal(K).astype(np.float32)
+        if kind == "nan":
+            x[rng.integers(0, K, 3)] = np.nan
+        elif kind == "inf":
+            x[K // 3] = np.inf
+        elif kind == "-inf":
+            x[K // 2] = -np.inf
+        elif kind == "tiny":
+            x = (x * np.float32(1e-40)).astype(np.float32)
+        else:
+            x = (x / np.abs(x).max() * np.float32(2.0 ** -120)).astype(np.float32)
+        rows.append(x)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_quantize_nonfinite_follows_the_reference(gpu, oracle, mode):
+    """src/gemv.c:20-38 on NaN, inf and tiny inputs as the reference's x86 build
+    runs it: (int) of NaN or of an out-of-range value is INT_MIN, clamped to
+    -127."""
+    rng = np.random.default_rng(11 + mode)
+    K = 512
+    x = nonfinite_rows(rng, K)
+    M = x.shape[0]
+    nsc = M if mode == 0 else M * (K // 256)
+    dq, ds = gpu.empty((M, K), np.int8), gpu.empty(nsc, np.float32)
+    gpu.quantize(mode, gpu.array(x), K, M, K, dq, ds)
+    q, s = dq.numpy(), ds.numpy()
+    for t in range(M):
+        wq, ws = oracle.quantize(x[t]) if mode == 0 else oracle.quantize_k(x[t])
+        assert np.array_equal(q[t], wq), t
+        got_s = s[t:t + 1] if mode == 0 else s.reshape(M, -1)[t]
+        assert np.array_equal(bits(got_s), bits(np.atleast_1d(np.float32(ws)) if mode == 0
+                                                 else ws)), t
+
+
+def same_or_both_nan(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    nan = np.isnan(a)
+    return np.array_equal(nan, np.isnan(b)) and np.array_equal(bits(a[~nan]), bits(b[~nan]))
+
+
+@pytest.mark.parametrize("tname", ["TQ1_0", "TQ2_0"])
+def test_fused_gemv_nonfinite_follows_the_reference(gpu, oracle, tname):
+    """The fused GEMV's in-workgroup quantiser on the same rows (NaN outputs
+    compared as NaN)."""
+    gtype = TYPES[tname]
+    rng = np.random.default_rng(21 + gtype)
+    K, N = 512, 48
+    w = weights(rng, gtype, N, K)
+    x = nonfinite_rows(rng, K)
+    M = x.shape[0]
+    t = gpu.tensor(gtype, K, N, w)
+    for r in range(M):
+        out = gpu.empty((1, N), np.float32)
+        gpu.gemv(t, gpu.array(x[r:r + 1]), 1, out)
+        assert same_or_both_nan(out.numpy()[0], oracle.gemv(gtype, x[r], w, N, K)), r
+
+
 @pytest.mark.parametrize("tname", ["TQ1_0", "TQ2_0", "Q4_K", "Q6_K"])
 def test_i8_entry_equals_float_entry(gpu, oracle, tname):
     """f32 entry == pre-quantised entry exactly (tests/test_gemv.c:318-325)."""
