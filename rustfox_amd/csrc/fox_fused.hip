@@ -23,7 +23,13 @@
 
 #define FW 8                    // waves per workgroup
 #define FWG (FW * 64)
-#define PF 4                    // weight blocks in flight per wave
+// weight blocks in flight per wave: one item's units (R4 blocks, 2 R4 for
+// gate/up pairs), at least 4 and at most 8 (more would take the registers
+// that let two workgroups share a compute unit)
+__host__ __device__ constexpr int pf_of(int R4, int epi2)
+{
+    return epi2 * R4 < 4 ? 4 : epi2 * R4 > 8 ? 8 : epi2 * R4;
+}
 #define FUSED_LDS_MAX (96 * 1024)
 
 enum { IN_Q = 0, IN_F32 = 1, IN_NORM = 2 };
@@ -513,6 +519,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     // input of token 0, the first weight blocks, the epilogue's operands
     InRegs<R4> in;
     load_input<IN, R4>(a, 0, K, in);
+    constexpr int PF = pf_of(R4, EPI == EPI_SILU ? 2 : 1);
     // (every wave issues PF block loads, past its last unit re-reading that
     // one, so that the input's first use waits for the input only)
     RawBlk raw[PF];

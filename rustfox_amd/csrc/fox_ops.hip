@@ -576,11 +576,21 @@ __device__ __forceinline__ float dpp_bcast(float v, int ctl)
 
 // Hand-over flags live in LDS and guard LDS data only, so the fences order
 // LDS accesses only: global loads a wave has in flight stay in flight.
-__device__ __forceinline__ int sv_peek(int *flag)
+__device__ __forceinline__ int sv_load(int *flag)
 {
     return __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+// (read as a wave-uniform value: tests on it are then scalar branches and
+// the loops around them stay uniform)
+__device__ __forceinline__ int sv_peek(int *flag)
+{
+    return __builtin_amdgcn_readfirstlane(sv_load(flag));
+}
+
+// (a tight loop: waves that poll with s_sleep 1 between reads slow the
+// dependent adds of a wave on another SIMD by about a tenth; polling
+// without a sleep does not)
 __device__ __forceinline__ bool sv_wait_ge(int *flag, int v)
 {
     for (int n = 0; n < SV_SPIN; n++) {
@@ -588,7 +598,6 @@ __device__ __forceinline__ bool sv_wait_ge(int *flag, int v)
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
             return true;
         }
-        __builtin_amdgcn_s_sleep(1);
     }
     return false;
 }
@@ -791,27 +800,29 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
 #pragma unroll
             for (int u = 0; u < 8; u++) X[u] = ring[u * 64 + sw[u & 3]];
         }
-        // whole tiles: one basic block per tile.  The next tile's flag is read
-        // before the first half is added and tested after it (through a
-        // zero that depends on the sum, so the test cannot move up).
+        // whole tiles.  Tile i + 2's flag is read while tile i's first half
+        // is added and becomes a scalar only at the end of tile i, so no
+        // instruction waits for that read; the test for tile i + 1 uses the
+        // value read during tile i - 1 (a tile not yet marked then is waited
+        // for, which is rare with the stages ahead).
         // (stage of tile i: i mod np, kept as a running index)
         const int nwhole = nq / SV_QT;
         int i = 0, st = 0;
+        int f1 = np > 1 ? sv_peek(&ready[1]) : -1;       // tile 1's flag
         for (; i < nwhole; i++) {
             const int stn = st + 1 == np ? 0 : st + 1;
+            const int st2 = stn + 1 == np ? 0 : stn + 1;
             const float4 *P = ring + st * SV_QT * 64;
             const float4 *Pn = ring + stn * SV_QT * 64;
 #pragma unroll
             for (int u = 0; u < 8; u++) Y[u] = P[(8 + u) * 64 + sw[u & 3]];
-            const int nf = sv_peek(&ready[stn]);
+            const int p2 = sv_load(&ready[st2]);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 acc = acc + X[u].x; acc = acc + X[u].y; acc = acc + X[u].z; acc = acc + X[u].w;
             }
-            int z;
-            asm volatile("v_mov_b32 %0, 0" : "=v"(z) : "v"(acc));
-            if (nf + z < i + 1 && i + 1 < ntile && !sv_wait_ge(&ready[stn], i + 1)) {
+            if (f1 < i + 1 && i + 1 < ntile && !sv_wait_ge(&ready[stn], i + 1)) {
                 ok = false;
                 break;
             }
@@ -823,7 +834,9 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
             for (int u = 0; u < 8; u++) {
                 acc = acc + Y[u].x; acc = acc + Y[u].y; acc = acc + Y[u].z; acc = acc + Y[u].w;
             }
+            __builtin_amdgcn_sched_barrier(0);
             sv_signal(&consumed, i + 1);
+            f1 = __builtin_amdgcn_readfirstlane(p2);
             st = stn;
         }
         // the last tile, partly filled: nfull whole quads, then rem positions
