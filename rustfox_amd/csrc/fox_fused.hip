@@ -24,8 +24,7 @@
 #define FW 8                    // waves per workgroup
 #define FWG (FW * 64)
 // weight blocks in flight per wave: one item's units (R4 blocks, 2 R4 for
-// gate/up pairs), at least 4 and at most 8 (more would take the registers
-// that let two workgroups share a compute unit)
+// gate/up pairs), at least 4 and at most 8
 __host__ __device__ constexpr int pf_of(int R4, int epi2)
 {
     return epi2 * R4 < 4 ? 4 : epi2 * R4 > 8 ? 8 : epi2 * R4;
@@ -475,7 +474,10 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     __shared__ float ascale[FOX_GPU_MAX_TOKENS];
 
     constexpr int CHUNK = FMT == FMT_TQ1 ? TQ1_CHUNK : TQ2_CHUNK;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // (the wave index as a wave-uniform value: everything per wave below,
+    // the units, items and weight addresses, is then scalar work)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nb = a.nb, M = a.M, K = nb * 256;
     const int nslab = EPI == EPI_SILU ? 2 : 1;
     const FusedLds L = fused_lds(FMT, K, M, nslab);
@@ -507,12 +509,19 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     const int nunits = nslab * nb;
     const int nu = wave < nunits ? (nunits - 1 - wave) / FW + 1 : 0;   // units per item
     const int total = nu * ntl;
-    auto unit_ptr = [&](int n) -> const uint8_t * {
-        const int ti = n / nu, r = n - ti * nu;
+    // unit r (of nu) of item ti: block u = wave + FW r of the item's units
+    auto unit_ptr = [&](int ti, int r) -> const uint8_t * {
         const int u = wave + FW * r, sl = u >= nb, b = u - sl * nb;
         int sg, tl;
         item(ti, sl, sg, tl);
         return pick4(a.w, sg) + ((size_t)tl * nb + b) * CHUNK;
+    };
+    // (item, unit) counters stepped one unit at a time (no divisions)
+    auto step = [&](int &ti, int &r) {
+        if (++r == nu) {
+            r = 0;
+            ti++;
+        }
     };
 
     // ---- loads in the order they are used (they complete in order): the
@@ -523,9 +532,13 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     // (every wave issues PF block loads, past its last unit re-reading that
     // one, so that the input's first use waits for the input only)
     RawBlk raw[PF];
+    int fti = 0, fr = 0;                                   // unit k (then PF) of the wave
 #pragma unroll
-    for (int k = 0; k < PF; k++)
-        raw[k] = load_raw<FMT>(total > 0 ? unit_ptr(k < total ? k : total - 1) : a.w[0], lane);
+    for (int k = 0; k < PF; k++) {
+        raw[k] = load_raw<FMT>(total > 0 ? unit_ptr(fti, fr) : a.w[0], lane);
+        if (k + 1 < total) step(fti, fr);
+    }
+    if (PF < total) step(fti, fr);                         // unit PF: the first refill
 
     // combiner threads: (slab, token, row) of an item's outputs
     const int nthr = nslab * 16 * M;
@@ -646,18 +659,21 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
         for (int ti = 0; ti < ntl; ti++) item_end(ti);
         return;
     }
+    int ti = 0, r = 0;                                     // unit n of the wave
     for (int n0 = 0; n0 < total; n0 += PF) {
 #pragma unroll
         for (int k = 0; k < PF; k++) {
             const int n = n0 + k;
             if (n >= total) break;
-            const int ti = n / nu, r = n - ti * nu;
             const int u = wave + FW * r, sl = u >= nb, b = u - sl * nb;
             const int corr = lead ? aux[b * M + tok] : 0;
             int S[4];
             block_mfma<FMT>(raw[k], B + b * bbytes, M, lane, corr, S);
             const RawBlk rk = raw[k];
-            if (n + PF < total) raw[k] = load_raw<FMT>(unit_ptr(n + PF), lane);
+            if (n + PF < total) {
+                raw[k] = load_raw<FMT>(unit_ptr(fti, fr), lane);
+                step(fti, fr);
+            }
             if (lead) {
                 const uint32_t hw[2] = {rk.dd.x, rk.dd.y};
                 int sg, tl;
@@ -676,6 +692,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
                 }
             }
             if (r == nu - 1) item_end(ti);
+            step(ti, r);
         }
     }
 }
@@ -741,11 +758,12 @@ static fox_gpu_status fused_go_r(fox_gpu_ctx *ctx, FusedArgs a, int n_work)
     return FOX_GPU_OK;
 }
 
-// the input registers per thread fit K: 2, 3, 5 or 8 dwords
+// the input registers per thread fit K: 1, 2, 3, 5 or 8 dwords
 template <int FMT, int IN, int EPI>
 static fox_gpu_status fused_go(fox_gpu_ctx *ctx, const FusedArgs &a, int grid)
 {
     const int per = (a.nb * 64 + FWG - 1) / FWG;
+    if (per <= 1) return fused_go_r<FMT, IN, EPI, 1>(ctx, a, grid);
     if (per <= 2) return fused_go_r<FMT, IN, EPI, 2>(ctx, a, grid);
     if (per <= 3) return fused_go_r<FMT, IN, EPI, 3>(ctx, a, grid);
     if (per <= 5) return fused_go_r<FMT, IN, EPI, 5>(ctx, a, grid);
