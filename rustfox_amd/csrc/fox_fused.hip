@@ -41,6 +41,7 @@ struct FusedArgs {
     int n_rows[MAX_SEGS];
     int tile_start[MAX_SEGS + 1];
     int nseg, nb, M, n_work;
+    int n_per, n_rem;           // items per workgroup: n_per, plus one below n_rem
     unsigned flags;
     const float *x;
     int x_stride;
@@ -456,12 +457,16 @@ __device__ __forceinline__ void block_mfma(const RawBlk &r, const uint8_t *__res
 
 // ------------------------------------------------------------ kernel
 
-// v[s] of a kernel-argument array, read with constant indices
+// v[s] of a kernel-argument array, read with constant indices (flat
+// selects: a nested choice becomes branches)
 template <typename T>
 __device__ __forceinline__ T pick4(const T *v, int s)
 {
-    const T v0 = v[0], v1 = v[1], v2 = v[2], v3 = v[3];
-    return s == 0 ? v0 : s == 1 ? v1 : s == 2 ? v2 : v3;
+    T r = v[0];
+    r = s >= 1 ? v[1] : r;
+    r = s >= 2 ? v[2] : r;
+    r = s >= 3 ? v[3] : r;
+    return r;
 }
 
 template <int FMT, int IN, int EPI, int R4>
@@ -492,42 +497,50 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     // read with constant indices only, so that they arrive in one batch of
     // scalar loads (an argument indexed at run time is a chain of loads).
     const int bx = blockIdx.x, nwg = gridDim.x;
-    const int ntl = bx < a.n_work ? (a.n_work - 1 - bx) / nwg + 1 : 0;
-    if (ntl == 0) return;                                  // (the host launches none such)
+    // the input of token 0 first: nothing ahead of its loads but the
+    // argument reads they need
+    InRegs<R4> in;
+    load_input<IN, R4>(a, 0, K, in);
+    const int ntl = a.n_per + (bx < a.n_rem);              // items of this workgroup (>= 1)
     const int ts1 = a.tile_start[1], ts2 = a.tile_start[2], ts3 = a.tile_start[3];
-    const int nseg = a.nseg;
+    // (integer arithmetic only: comparisons turned into 0/1 values and
+    // branches would split the scalar work of the prologue into many small
+    // blocks; tile_start entries past the last segment are INT_MAX)
     auto item = [&](int ti, int sl, int &sg, int &tl) {
         const int w = bx + ti * nwg;
         if (EPI == EPI_SILU) {
             sg = sl;
             tl = w;
         } else {
-            sg = (nseg > 1 && w >= ts1) + (nseg > 2 && w >= ts2) + (nseg > 3 && w >= ts3);
-            tl = w - (sg == 0 ? 0 : sg == 1 ? ts1 : sg == 2 ? ts2 : ts3);
+            const int c1 = (int)((unsigned)(ts1 - 1 - w) >> 31);    // w >= ts1
+            const int c2 = (int)((unsigned)(ts2 - 1 - w) >> 31);
+            const int c3 = (int)((unsigned)(ts3 - 1 - w) >> 31);
+            sg = c1 + c2 + c3;
+            tl = w - (c1 * ts1 + c2 * (ts2 - ts1) + c3 * (ts3 - ts2));
         }
     };
     const int nunits = nslab * nb;
     const int nu = wave < nunits ? (nunits - 1 - wave) / FW + 1 : 0;   // units per item
     const int total = nu * ntl;
     // unit r (of nu) of item ti: block u = wave + FW r of the item's units
+    // (clamped to the item's last one: a wave without units reads that)
     auto unit_ptr = [&](int ti, int r) -> const uint8_t * {
-        const int u = wave + FW * r, sl = u >= nb, b = u - sl * nb;
+        const int u = min(wave + FW * r, nunits - 1), sl = u >= nb, b = u - sl * nb;
         int sg, tl;
         item(ti, sl, sg, tl);
         return pick4(a.w, sg) + ((size_t)tl * nb + b) * CHUNK;
     };
-    // (item, unit) counters stepped one unit at a time (no divisions)
+    // (item, unit) counters stepped one unit at a time (no divisions, no
+    // branches)
     auto step = [&](int &ti, int &r) {
-        if (++r == nu) {
-            r = 0;
-            ti++;
-        }
+        const int wrap = r + 1 == nu;
+        r = wrap ? 0 : r + 1;
+        ti += wrap;
     };
 
     // ---- loads in the order they are used (they complete in order): the
-    // input of token 0, the first weight blocks, the epilogue's operands
-    InRegs<R4> in;
-    load_input<IN, R4>(a, 0, K, in);
+    // input of token 0 (above), the first weight blocks, the epilogue's
+    // operands
     constexpr int PF = pf_of(R4, EPI == EPI_SILU ? 2 : 1);
     // (every wave issues PF block loads, past its last unit re-reading that
     // one, so that the input's first use waits for the input only)
@@ -535,8 +548,11 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     int fti = 0, fr = 0;                                   // unit k (then PF) of the wave
 #pragma unroll
     for (int k = 0; k < PF; k++) {
-        raw[k] = load_raw<FMT>(total > 0 ? unit_ptr(fti, fr) : a.w[0], lane);
-        if (k + 1 < total) step(fti, fr);
+        raw[k] = load_raw<FMT>(unit_ptr(fti, fr), lane);
+        int t2 = fti, r2 = fr;
+        step(t2, r2);
+        fti = k + 1 < total ? t2 : fti;                    // past the last unit: reload it
+        fr = k + 1 < total ? r2 : fr;
     }
     if (PF < total) step(fti, fr);                         // unit PF: the first refill
 
@@ -746,6 +762,8 @@ static fox_gpu_status fused_go_r(fox_gpu_ctx *ctx, FusedArgs a, int n_work)
     a.n_work = n_work;
     const int cap = 2 * (ctx->n_cu > 0 ? ctx->n_cu : 1);
     const int grid = n_work < cap ? n_work : cap;
+    a.n_per = n_work / grid;
+    a.n_rem = n_work - a.n_per * grid;
     const size_t lds = fused_lds(FMT, a.nb * 256, a.M, EPI == EPI_SILU ? 2 : 1).total;
     if (lds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute((const void *)gemv_fused<FMT, IN, EPI, R4>,
@@ -790,6 +808,7 @@ static void fused_segments(FusedArgs &a, size_t n, const fox_gpu_tensor *const *
         t += (int)ws[i]->n_tiles;
     }
     a.tile_start[n] = t;
+    for (size_t i = n + 1; i <= MAX_SEGS; i++) a.tile_start[i] = 0x7fffffff;
     a.nseg = (int)n;
     *tiles = t;
 }
