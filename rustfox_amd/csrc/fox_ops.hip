@@ -822,10 +822,9 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
             for (int u = 0; u < 8; u++) {
                 acc = acc + X[u].x; acc = acc + X[u].y; acc = acc + X[u].z; acc = acc + X[u].w;
             }
-            if (f1 < i + 1 && i + 1 < ntile && !sv_wait_ge(&ready[stn], i + 1)) {
-                ok = false;
-                break;
-            }
+            // (no early exit: after a timed-out wait the loop runs on without
+            // waiting and the sum is replaced by NaN below)
+            if (ok && f1 < i + 1 && i + 1 < ntile) ok = sv_wait_ge(&ready[stn], i + 1);
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 #pragma unroll
             for (int u = 0; u < 8; u++) X[u] = Pn[u * 64 + sw[u & 3]];
