@@ -84,9 +84,11 @@ fox_gpu_status fox_gpu_sync(fox_gpu_ctx *ctx);
 
 /* Upload one GGUF tensor (`bytes` = its GGUF size, host pointer) into HBM.
  * Block types are repacked into the device layout (same byte count plus
- * padding of the row count to 16); F16/F32 stay row-major.  Backs the
- * FOX_WEIGHTS_DEVICE mode of fox_weights_open (include/fox/fox.h:372-387),
- * loaded once per tensor like the resident backend (src/weights.c:461-496). */
+ * padding of the row count to 16); F16/F32 are laid out in 256-row tiles of
+ * 128-byte row chunks (fox_gpu_tensor_download gives row-major bytes back).
+ * Backs the FOX_WEIGHTS_DEVICE mode of fox_weights_open
+ * (include/fox/fox.h:372-387), loaded once per tensor like the resident
+ * backend (src/weights.c:461-496). */
 fox_gpu_status fox_gpu_tensor_upload(fox_gpu_ctx *ctx, int type, uint64_t ne0,
                                      uint64_t ne1, const void *host, uint64_t bytes,
                                      fox_gpu_tensor **out);
@@ -141,14 +143,14 @@ fox_gpu_status fox_gpu_gemv_i8(fox_gpu_ctx *ctx, const fox_gpu_tensor *w,
                                float *out, size_t out_stride);
 
 /* Integer block sums, the bit-exact part of the contract: for token t, row r,
- * block b: TQ1_0/TQ2_0 one int32 (src/ternary.c:217-237, 321-332), Q4_K the
+ * block b: TQ1_0/TQ2_0 one int32 (src/ternary.c:73-93, 177-188), Q4_K the
  * eight sub-block dots D_j (src/kernels.c:571-602), Q6_K the four scaled
  * group sums G (src/kernels.c:636-661).  sums is device memory of
  * M x N x K/256 x {1, 8, 4} int32. */
 fox_gpu_status fox_gpu_block_sums(fox_gpu_ctx *ctx, const fox_gpu_tensor *w,
                                   const int8_t *q, size_t M, int32_t *sums);
 
-/* One-launch stages of a decode layer (src/forward.c:399-478) for TQ1_0 and
+/* One-launch stages of a decode layer (src/forward.c:318-397) for TQ1_0 and
  * TQ2_0 weights: the input stage (RMSNorm, int8 quantisation) runs inside
  * the GEMV's workgroups, results bit-identical to the separate calls.
  * Other weight types return FOX_GPU_ERR_UNSUPPORTED (use the separate
@@ -196,7 +198,7 @@ void           fox_gpu_act_free(fox_gpu_ctx *ctx, fox_gpu_act *act);
  * out[i*out_stride ..] = row rows[i] for i < n; rows is device uint32.
  * A row index >= ne1 is not read: its output is left untouched and the
  * device flag *bad (if non-NULL) is set to 1.  Covers embed
- * (src/forward.c:340-374) and norm weights (src/forward.c:248-267). */
+ * (src/forward.c:259-293) and norm weights (src/forward.c:167-186). */
 fox_gpu_status fox_gpu_get_rows(fox_gpu_ctx *ctx, const fox_gpu_tensor *t,
                                 const uint32_t *rows, size_t n, float *out,
                                 size_t out_stride, uint32_t *bad);
@@ -209,7 +211,7 @@ fox_gpu_status fox_gpu_rmsnorm(fox_gpu_ctx *ctx, float *out, size_t out_stride,
 /* RoPE on q (n_head heads) and k (n_head_kv heads) of M tokens at positions
  * pos[0] + t, adjacent pairs (src/ops.c:56-73) with the host-built tables
  * (src/forward.c:104-118), then k and v rows stored into the layer's cache
- * rows pos[0] + t (src/forward.c:427-443).  A token whose position is not
+ * rows pos[0] + t (src/forward.c:346-362).  A token whose position is not
  * below n_ctx is neither rotated nor stored.
  *
  * Cache layout: k_cache is f32 [n_ctx][kv_dim] (the reference's); v_cache is
@@ -226,14 +228,14 @@ fox_gpu_status fox_gpu_rope_store(fox_gpu_ctx *ctx, float *q, size_t q_stride,
                                   float *k_cache, float *v_cache);
 
 /* Rows p0 .. p0+n-1 of a layer's caches from device row-major k, v
- * [n][kv_dim] (pre-filling a cache; src/forward.c:427-443 stores rows one
+ * [n][kv_dim] (pre-filling a cache; src/forward.c:346-362 stores rows one
  * token at a time). */
 fox_gpu_status fox_gpu_kv_write(fox_gpu_ctx *ctx, float *k_cache, float *v_cache,
                                 size_t kv_dim, size_t n_ctx, size_t p0, size_t n,
                                 const float *k, const float *v);
 
 /* Causal GQA attention of M tokens at positions pos[0] + t over cache rows
- * 0 .. pos[0] + t: softmax(q.k / sqrt(hd)) v (src/forward.c:303-338).
+ * 0 .. pos[0] + t: softmax(q.k / sqrt(hd)) v (src/forward.c:222-257).
  * FOX_GPU_ATTN_EXACT computes every sum in the reference's order (scores in
  * head-dimension order, softmax and value sums in position order) and
  * reproduces it bit for bit; FOX_GPU_ATTN_SPLIT splits positions over

@@ -135,7 +135,7 @@ fox_status fox_context_create(fox_model *m, const fox_context_config *cfg,
 void       fox_context_destroy(fox_context *ctx);
 void       fox_context_reset(fox_context *ctx);
 /* logits of the last token, host memory owned by ctx, valid until the next
- * eval or destroy (src/forward.c:492-519) */
+ * eval or destroy (src/forward.c:411-438) */
 fox_status fox_eval(fox_context *ctx, const uint32_t *tokens, size_t n_tokens,
                     float **logits_out);
 uint32_t   fox_context_position(const fox_context *ctx);

@@ -149,7 +149,7 @@ void or_quantize_act_k(const float *x, size_t n, int8_t *q, float *scales)
 
 /* ---------------------------------------------------------- block sums */
 
-/* src/ternary.c:203-207: trit at base-3 level l of a TQ1_0 byte */
+/* src/ternary.c:59-63: trit at base-3 level l of a TQ1_0 byte */
 static int tq1_trit(uint8_t code, int level)
 {
     static const uint8_t p3[5] = { 1, 3, 9, 27, 81 };
@@ -157,7 +157,7 @@ static int tq1_trit(uint8_t code, int level)
     return (int)(((unsigned)scaled * 3u) >> 8) - 1;
 }
 
-/* src/ternary.c:217-237 (element order; the SSE2 path in ternary.c:272-317
+/* src/ternary.c:73-93 (element order; the SSE2 path in ternary.c:97-173
  * computes the same integer) */
 int32_t or_tq1_block_sum(const int8_t *x, const uint8_t *blk)
 {
@@ -173,7 +173,7 @@ int32_t or_tq1_block_sum(const int8_t *x, const uint8_t *blk)
     return s;
 }
 
-/* src/ternary.c:321-332: code 3 decodes to +2 and is not clamped */
+/* src/ternary.c:177-188: code 3 decodes to +2 and is not clamped */
 int32_t or_tq2_block_sum(const int8_t *x, const uint8_t *blk)
 {
     int32_t s = 0;
@@ -280,7 +280,7 @@ int or_block_sums(int type, const int8_t *q, const void *w, size_t rows,
 
 /* ---------------------------------------------------------- row dots */
 
-/* src/ternary.c:370-390 / 447-469: acc starts at 0.0f and adds
+/* src/ternary.c:226-246 / 303-325 and src/gemv.c:62-70: acc starts at 0.0f and adds
  * f16(d) * (float)S block by block (two roundings per block) */
 static float tq_row(int type, const int8_t *q, const uint8_t *row, size_t cols)
 {
@@ -651,7 +651,7 @@ int or_context_create(const or_model *m, uint32_t n_ctx, uint32_t n_batch,
     if (!m || !out || !n_ctx) return OR_ERR_ARG;
     c = (or_context *)calloc(1, sizeof(*c));
     if (!c) return OR_ERR_NOMEM;
-    /* src/forward.c:57-66 */
+    /* src/forward.c:67-72 */
     if (n_batch == 0) n_batch = 32;
     if (n_batch > n_ctx) n_batch = n_ctx;
     c->m = m; c->n_ctx = n_ctx; c->n_batch = n_batch; c->n_threads = n_threads;
@@ -716,14 +716,14 @@ int or_context_set_pos(or_context *c, uint32_t pos)
     return OR_OK;
 }
 
-/* src/forward.c:248-267: a norm vector is the dequantised tensor */
+/* src/forward.c:167-186: a norm vector is the dequantised tensor */
 static const float *norm_vec(or_context *c, const or_tensor *t, size_t n)
 {
     or_dequant_row(t->type, t->data, n, c->norm);
     return c->norm;
 }
 
-/* src/forward.c:269-294: one gemv per token */
+/* src/forward.c:188-213: one gemv per token */
 static void project(or_context *c, const or_tensor *t, size_t rows, size_t cols,
                     size_t ntok, const float *in, size_t in_stride,
                     float *out, size_t out_stride)
@@ -734,7 +734,7 @@ static void project(or_context *c, const or_tensor *t, size_t rows, size_t cols,
                 out + i * out_stride, c->n_threads);
 }
 
-/* src/forward.c:303-338 for one head: scores, softmax, j-ordered V sum */
+/* src/forward.c:222-257 for one head: scores, softmax, j-ordered V sum */
 static void attend_head(or_context *c, size_t layer, size_t tok, size_t h,
                         uint32_t seq_pos)
 {
@@ -756,7 +756,7 @@ static void attend_head(or_context *c, size_t layer, size_t tok, size_t h,
     }
 }
 
-/* src/forward.c:376-490 */
+/* src/forward.c:295-409 */
 static int forward_batch(or_context *c, const uint32_t *tok, size_t n, int want_logits)
 {
     const or_model *m = c->m;
@@ -820,7 +820,7 @@ static int forward_batch(or_context *c, const uint32_t *tok, size_t n, int want_
     return OR_OK;
 }
 
-/* src/forward.c:492-519: chunks of n_batch tokens, logits for the last */
+/* src/forward.c:411-438: chunks of n_batch tokens, logits for the last */
 int or_eval(or_context *c, const uint32_t *tokens, size_t n, float **logits)
 {
     size_t done = 0;

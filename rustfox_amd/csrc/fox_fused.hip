@@ -12,7 +12,7 @@
 //          src/forward.c:374-377, 393-396);
 //   ROPE   segments q, k, v of one projection: RoPE on q and k
 //          (src/ops.c:56-73) at position pos[0] + t, q to its buffer, k and
-//          v into the layer's caches (src/forward.c:399-443);
+//          v into the layer's caches (src/forward.c:346-362);
 //   SILU   segments gate and up, one tile of each per workgroup:
 //          h = silu(gate) * up (src/ops.c:41-48);
 //   SUMS   per-block integer sums only (fox_gpu_block_sums).
@@ -274,7 +274,7 @@ __device__ __forceinline__ float quantise_to_b(const FusedArgs &a, int t, int K,
                 rs = (float)(1.0 / __builtin_sqrt(seq / (double)K + (double)a.eps));
             }
 #pragma unroll
-            for (int r = 0; r < R4MAX; r++) {           // src/ops.c:17: x * scale * w
+            for (int r = 0; r < R4MAX; r++) {           // src/ops.c:18: x * scale * w
                 xv[r].x = xv[r].x * rs * wv[r].x;
                 xv[r].y = xv[r].y * rs * wv[r].y;
                 xv[r].z = xv[r].z * rs * wv[r].z;

@@ -9,7 +9,7 @@
 //   * per-block integer sums are exact (integer MFMA);
 //   * every output row combines its per-block terms in block order into a
 //     float accumulator starting at 0.0f with one rounding per operation, as
-//     the reference's row loop does (ternary.c:370-390, kernels.c:571-661),
+//     the reference's row loop does (ternary.c:226-246, 303-325, kernels.c:571-661),
 //     so outputs equal the reference built without FMA contraction.
 //
 // Work split: one workgroup (4 waves) per 16-row tile and segment; waves take

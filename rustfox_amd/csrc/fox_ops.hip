@@ -134,7 +134,7 @@ __device__ __forceinline__ size_t vq_index(size_t p, size_t c, size_t kvd)
 }
 
 // src/ops.c:56-73 on q and k of token t at position pos[0]+t, then the
-// src/forward.c:427-443 copies of k and v into cache row pos[0]+t.
+// src/forward.c:357-361 copies of k and v into cache row pos[0]+t.
 __global__ void rope_store_k(float *__restrict__ q, size_t q_stride, float *__restrict__ k,
                              size_t k_stride, const float *__restrict__ v, size_t v_stride,
                              int n_head, int n_head_kv, int hd, const float *__restrict__ cos_t,

@@ -1,6 +1,6 @@
-/* forward.c -- fox_eval on the GPU (RustFox src/forward.c:137-519 semantics).
+/* forward.c -- fox_eval on the GPU (RustFox src/forward.c:56-132, 295-438 semantics).
  *
- * One decode pass, per layer (src/forward.c:399-478):
+ * One decode pass, per layer (src/forward.c:318-397):
  *   xb = rmsnorm(x, attn_norm); q, k, v = W xb; rope(q, k) at pos + t and
  *   store k, v in the layer's cache (one launch for ternary weights);
  *   xb = attention; x += W_o xb (residual fused into the gemv);
@@ -11,7 +11,7 @@
  * The K cache is f32 [n_layer][n_ctx][n_head_kv * head_dim] as in the
  * reference, the V cache the device's position-quad interleaved layout
  * (fox_gpu.h) per layer; the RoPE tables are built on the host in double exactly as
- * src/forward.c:188-199 and uploaded.  A pass takes at most
+ * src/forward.c:104-118 and uploaded.  A pass takes at most
  * FOX_GPU_MAX_TOKENS tokens; fox_eval cuts its input into such passes, which
  * gives the same result as the reference's n_batch chunks because a token
  * depends only on the cache rows before it (batched == stepped,
@@ -106,7 +106,7 @@ void fox_context_destroy(fox_context *c)
     free(c);
 }
 
-/* device f32 copy of a norm vector into `dst` (src/forward.c:248-267
+/* device f32 copy of a norm vector into `dst` (src/forward.c:167-186
  * dequantises it per use; it never changes, so it is dequantised once) */
 static fox_status norm_vector(fox_context *c, size_t idx, float *dst)
 {
@@ -192,7 +192,7 @@ fox_status fox_context_create(fox_model *m, const fox_context_config *cfg, fox_c
         return st;
     }
 
-    /* RoPE tables, src/forward.c:188-199 */
+    /* RoPE tables, src/forward.c:104-118 */
     half = c->hd / 2;
     tc = (float *)malloc((size_t)k.n_ctx * half * 4);
     ts = (float *)malloc((size_t)k.n_ctx * half * 4);

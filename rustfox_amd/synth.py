@@ -6,8 +6,8 @@ writers emit F32 test fixtures, tests/test_forward.c:129-186), so the
 synthetic models of the benchmark configurations are produced here.
 
 Block layouts follow the reference decoders:
-  TQ1_0  54 B / 256: qs[48] @0, qh[4] @48, f16 d @52   (src/ternary.c:203-237)
-  TQ2_0  66 B / 256: qs[64] @0, f16 d @64              (src/ternary.c:321-332)
+  TQ1_0  54 B / 256: qs[48] @0, qh[4] @48, f16 d @52   (src/ternary.c:17-21, 73-93)
+  TQ2_0  66 B / 256: qs[64] @0, f16 d @64              (src/ternary.c:17-21, 177-188)
   Q4_K  144 B / 256: f16 d, f16 dmin, scales[12], qs[128] (src/kernels.c:246-283)
   Q6_K  210 B / 256: ql[128], qh[64], int8 sc[16], f16 d (src/kernels.c:217-244)
 GGUF metadata keys are the llama.* keys read by src/model.c:188-237.

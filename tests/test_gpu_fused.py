@@ -1,7 +1,7 @@
 """One-launch decode-layer stages (fox_gpu_gemv_rmsnorm, fox_gpu_qkv_rope,
 fox_gpu_gate_up_silu) against the oracle's separate steps: RMSNorm
 (src/ops.c:7-22), the quantised GEMV (src/gemv.c), RoPE (src/ops.c:56-73),
-the cache store (src/forward.c:427-443) and SwiGLU (src/ops.c:41-48).
+the cache store (src/forward.c:346-362) and SwiGLU (src/ops.c:41-48).
 Outputs must be bit-identical."""
 import numpy as np
 import pytest

@@ -121,7 +121,7 @@ def test_quantize_exact(gpu, oracle, K, M, mode):
     x = (rng.standard_normal((M, K)) * rng.uniform(0.01, 100)).astype(np.float32)
     x[0, : min(K, 16)] = 0.0
     if M > 1:
-        x[1] = 0.0  # an all-zero token gets q = 0 and scale 0 (tests/test_gemv.c:254-257)
+        x[1] = 0.0  # an all-zero token gets q = 0 and scale 0 (tests/test_gemv.c:81-84)
     nsc = M if mode == 0 else M * (K // 256)
     dq, ds = gpu.empty((M, K), np.int8), gpu.empty(nsc, np.float32)
     gpu.quantize(mode, gpu.array(x), K, M, K, dq, ds)
@@ -205,7 +205,7 @@ def test_fused_gemv_nonfinite_follows_the_reference(gpu, oracle, tname):
 
 @pytest.mark.parametrize("tname", ["TQ1_0", "TQ2_0", "Q4_K", "Q6_K"])
 def test_i8_entry_equals_float_entry(gpu, oracle, tname):
-    """f32 entry == pre-quantised entry exactly (tests/test_gemv.c:318-325)."""
+    """f32 entry == pre-quantised entry exactly (tests/test_gemv.c:145-152)."""
     gtype = TYPES[tname]
     N, K, M = 70, 1024, 2
     rng = np.random.default_rng([7, gtype])

@@ -212,7 +212,7 @@ def test_f16_conversions(oracle):
 
 
 def test_quantizer_known_answers(oracle):
-    """tests/test_gemv.c:254-267: zero vector -> zero, ramp -> in range with
+    """tests/test_gemv.c:81-94: zero vector -> zero, ramp -> in range with
     the largest magnitude at +127; and q = round-half-away(x * 127/amax)."""
     q, s = oracle.quantize(np.zeros(512, np.float32))
     assert s == 0.0 and not q.any()
@@ -295,7 +295,7 @@ def test_gemv_vs_reference(oracle, ref, gtype, N, K):
         x = (rng.standard_normal(K) * rng.uniform(0.1, 50)).astype(np.float32)
         assert np.array_equal(bits(oracle.gemv(gtype, x, w, N, K)),
                               bits(ref.gemv(gtype, x, w, N, K, n_threads=1)))
-    # threaded == serial (tests/test_gemv.c:289-298)
+    # threaded == serial (tests/test_gemv.c:116-125)
     assert np.array_equal(bits(ref.gemv(gtype, x, w, N, K, n_threads=4)),
                           bits(oracle.gemv(gtype, x, w, N, K, n_threads=3)))
 
