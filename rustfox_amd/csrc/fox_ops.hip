@@ -9,6 +9,13 @@
 
 // ------------------------------------------------------------------ rows
 
+// the wave index as a wave-uniform (scalar) value: loops and tests on it
+// are then scalar branches, not masked vector code
+__device__ __forceinline__ int wave_index()
+{
+    return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+}
+
 template <typename WT>
 __global__ void get_rows_k(const WT *__restrict__ src, uint64_t K, uint64_t N,
                            const uint32_t *__restrict__ rows, int n, float *__restrict__ out,
@@ -239,7 +246,7 @@ __global__ __launch_bounds__(256) void attn_partial(const float *__restrict__ q,
     __shared__ float qs[ATT_MAXG * ATT_MAXHD];
     __shared__ float sc[ATT_MAXG * ATT_SPLIT];
     const int s = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
     const int gqa = n_head / n_head_kv, kvd = n_head_kv * hd;
     // rows 0 .. upto-1 are visible; never past the cache
     const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
@@ -364,7 +371,7 @@ __global__ __launch_bounds__(256) void attn_scores_x(const float *__restrict__ q
     const int ks_str = hd + 4;
     float *qs = ks + SC_TILE * ks_str;              // [gqa][hd]
     const int tile = blockIdx.x, p0 = tile * SC_TILE, kvh = blockIdx.y, t = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
     const int gqa = n_head / n_head_kv, kvd = n_head_kv * hd, nv = hd >> 2;
     const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
     if (p0 >= upto) return;
@@ -665,7 +672,7 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
     __shared__ uint64_t tab[32];
     __shared__ int ready[SV_NP_MAX], consumed, a_ready, e_done;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
     const int kvd = n_head_kv * hd;
     const int n_sl = (hd + DS - 1) / DS;
     const int kvh = blockIdx.x / n_sl, sl = blockIdx.x - kvh * n_sl, t = blockIdx.y;
@@ -868,13 +875,22 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
 
     // ---- loaders: tile i = li, li + SV_LOADERS, ...
     if (!sv_wait_ge(&a_ready, 1)) return;
-    float inv[G];
-    int nrm[G];
+    // a_j = e_j * (1/sum), or e_j where the sum is not positive
+    // (src/ops.c:35-38; e * 1 is e exactly): the scale per head, and that of
+    // the lane's own head for the DPP exchange below
+    float ivg[G];
 #pragma unroll
-    for (int gg = 0; gg < G; gg++) {
-        inv[gg] = inv_s[gg];
-        nrm[gg] = nrm_s[gg];
-    }
+    for (int gg = 0; gg < G; gg++) ivg[gg] = nrm_s[gg] ? inv_s[gg] : 1.0f;
+    constexpr bool DPPX = G == 2 || G == 4;  // the G heads exchanged within lane quads
+    const int mine = (lane - lq * DS) % G;
+    float ivm = ivg[0];
+#pragma unroll
+    for (int gg = 1; gg < G; gg++) ivm = mine == gg ? ivg[gg] : ivm;
+    // weight quads read per quad of V, and quads of V per batch of reads
+    // (all of a batch's reads are issued before the first is used)
+    constexpr int RK = DPPX ? 1 : G;
+    constexpr int KC = 8 / RK < NLD ? (8 / RK > 0 ? 8 / RK : 1) : NLD;
+    static_assert(NLD % KC == 0, "read batches cover the tile");
     // (stage of tile i: i mod np, kept as a running index)
     const int st_step = SV_LOADERS % np;
     int s = li % np;
@@ -890,40 +906,43 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
         if (i >= np && !sv_wait_ge(&consumed, i - np + 1)) return;
         float4 *P = ring + s * SV_QT * 64;
 #pragma unroll
-        for (int k = 0; k < NLD; k++) {
-            const int qi = k * G + lq;                       // quad within the tile
-            const int jq = min(i * SV_QT + qi, nq_all - 1);
-            const float4 v = vcur[k];
-            // weights of head `mine` for this quad, normalised; with G = 2 or 4
-            // the lanes of a DPP quad hold the G heads and exchange them
-            const int mine = (lane - lq * DS) % G;
-            float4 am = ((const float4 *)(e + mine * estr))[jq];
-            if (nrm[mine]) {
-                const float iv = inv[mine];
-                am.x = am.x * iv; am.y = am.y * iv; am.z = am.z * iv; am.w = am.w * iv;
+        for (int k0 = 0; k0 < NLD; k0 += KC) {
+            float4 wq[KC * RK];
+#pragma unroll
+            for (int kk = 0; kk < KC; kk++) {
+                const int jq = min(i * SV_QT + (k0 + kk) * G + lq, nq_all - 1);
+#pragma unroll
+                for (int r = 0; r < RK; r++)
+                    wq[kk * RK + r] = ((const float4 *)(e + (DPPX ? mine : r) * estr))[jq];
             }
 #pragma unroll
-            for (int gg = 0; gg < G; gg++) {
-                float4 a;
-                if (G == 2 || G == 4) {
-                    // quad_perm: every lane of a quad takes lane (quad base + gg)
-                    constexpr int c0 = 0;
-                    const int ctl = G == 4 ? gg * 0x55 : (gg ? 0xF5 : 0xA0);
-                    (void)c0;
-                    a.x = dpp_bcast(am.x, ctl);
-                    a.y = dpp_bcast(am.y, ctl);
-                    a.z = dpp_bcast(am.z, ctl);
-                    a.w = dpp_bcast(am.w, ctl);
-                } else {
-                    a = ((const float4 *)(e + gg * estr))[jq];
-                    if (nrm[gg]) {
-                        a.x = a.x * inv[gg]; a.y = a.y * inv[gg];
-                        a.z = a.z * inv[gg]; a.w = a.w * inv[gg];
-                    }
+            for (int kk = 0; kk < KC; kk++) {
+                const int k = k0 + kk;
+                const int qi = k * G + lq;                   // quad within the tile
+                const float4 v = vcur[k];
+                float4 am = wq[kk * RK];
+                if (DPPX) {
+                    am.x = am.x * ivm; am.y = am.y * ivm; am.z = am.z * ivm; am.w = am.w * ivm;
                 }
-                float4 p;
-                p.x = a.x * v.x; p.y = a.y * v.y; p.z = a.z * v.z; p.w = a.w * v.w;
-                P[qi * 64 + ((gg * DS + (lane - lq * DS)) ^ ((qi & 3) << 2))] = p;
+#pragma unroll
+                for (int gg = 0; gg < G; gg++) {
+                    float4 a;
+                    if (DPPX) {
+                        // quad_perm: every lane of a quad takes lane (quad base + gg)
+                        const int ctl = G == 4 ? gg * 0x55 : (gg ? 0xF5 : 0xA0);
+                        a.x = dpp_bcast(am.x, ctl);
+                        a.y = dpp_bcast(am.y, ctl);
+                        a.z = dpp_bcast(am.z, ctl);
+                        a.w = dpp_bcast(am.w, ctl);
+                    } else {
+                        a = wq[kk * RK + (DPPX ? 0 : gg)];
+                        a.x = a.x * ivg[gg]; a.y = a.y * ivg[gg];
+                        a.z = a.z * ivg[gg]; a.w = a.w * ivg[gg];
+                    }
+                    float4 p;
+                    p.x = a.x * v.x; p.y = a.y * v.y; p.z = a.z * v.z; p.w = a.w * v.w;
+                    P[qi * 64 + ((gg * DS + (lane - lq * DS)) ^ ((qi & 3) << 2))] = p;
+                }
             }
         }
         sv_signal(&ready[s], i);
@@ -1122,7 +1141,7 @@ __global__ __launch_bounds__(AM_THREADS) void argmax_k(const float *__restrict__
     __shared__ float bv[AM_THREADS / 64];
     __shared__ int bi[AM_THREADS / 64];
     __shared__ int last;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
     const int i0 = blockIdx.x * per, i1 = min(n, i0 + per);
     float best = -INFINITY;
     int bidx = 0x7fffffff;
