@@ -2,10 +2,12 @@
 // store, split-position GQA attention, SwiGLU, residual add, argmax.
 // Built with -ffp-contract=off like the rest of the library: every float op
 // rounds once, in the reference's order where the reference fixes an order.
+#include "fox_gemv_dev.h"
 #include "fox_internal.h"
 #include "fox_math.h"
 
 #include <cmath>
+#include <utility>
 
 // ------------------------------------------------------------------ rows
 
@@ -356,7 +358,49 @@ __global__ void attn_merge(const float *__restrict__ part, int n_head, int hd, i
 // the interleaved V and the weights four positions per load).
 
 #define SC_TILE 64
+#define SC_CQ 8                     // quads (4 dimensions) per chunk of a K row
 
+// vmcnt(n) alone (s_waitcnt fields of gfx9: vmcnt [3:0] and [15:14],
+// expcnt [6:4], lgkmcnt [11:8]; the others at their maximum)
+#define VMCNT_ONLY(n) ((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4) | (15 << 8))
+
+// s_waitcnt vmcnt(n) for n known once loops are unrolled (the instruction
+// takes an immediate)
+__device__ __forceinline__ void wait_vmcnt(int n)
+{
+    switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(0)); break;
+    case 1: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(1)); break;
+    case 2: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(2)); break;
+    case 3: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(3)); break;
+    case 4: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(4)); break;
+    case 5: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(5)); break;
+    case 6: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(6)); break;
+    case 7: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(7)); break;
+    case 8: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(8)); break;
+    case 10: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(10)); break;
+    case 12: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(12)); break;
+    case 14: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(14)); break;
+    default: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(0)); break;
+    }
+}
+
+// global -> LDS copy of 16 bytes per lane: lane l's bytes land at dst + 16 l
+// (dst wave-uniform), counted by vmcnt like a load
+__device__ __forceinline__ void copy_to_lds16(const void *src, void *dst)
+{
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+}
+
+// One workgroup per (64-position tile, kv head, token); wave w takes query
+// heads w, w + 4, ... of the kv head, one lane per position.  The tile's K
+// rows arrive in NCH chunks of 32 dimensions, copied straight into LDS: every
+// copy is issued at the start, and the dot products of chunk c run once that
+// chunk is in, while the later ones are still arriving (each sum stays in
+// head-dimension order, chunk after chunk).  A chunk holds 64 rows of 8
+// quads; quad j of row r sits in slot j ^ (r & 7), so that the 64 lanes'
+// reads of one quad fall in different banks.
+template <int NCH>
 __global__ __launch_bounds__(256) void attn_scores_x(const float *__restrict__ q,
                                                      size_t q_stride,
                                                      const float *__restrict__ kc, int n_head,
@@ -366,52 +410,99 @@ __global__ __launch_bounds__(256) void attn_scores_x(const float *__restrict__ q
                                                      float *__restrict__ att,
                                                      float *__restrict__ tmax, int n_tiles)
 {
-    extern __shared__ float4 lds4[];
-    float *ks = (float *)lds4;                      // [SC_TILE][hd + 4]
-    const int ks_str = hd + 4;
-    float *qs = ks + SC_TILE * ks_str;              // [gqa][hd]
+    // one array per chunk: separate objects, so that waiting for a chunk's
+    // copies does not wait for the later chunks' copies
+    __shared__ float4 kq0[SC_TILE * SC_CQ], kq1[NCH > 1 ? SC_TILE * SC_CQ : 1],
+        kq2[NCH > 2 ? SC_TILE * SC_CQ : 1], kq3[NCH > 3 ? SC_TILE * SC_CQ : 1],
+        kq4[NCH > 4 ? SC_TILE * SC_CQ : 1], kq5[NCH > 5 ? SC_TILE * SC_CQ : 1],
+        kq6[NCH > 6 ? SC_TILE * SC_CQ : 1], kq7[NCH > 7 ? SC_TILE * SC_CQ : 1];
+    __shared__ float4 qq[ATT_MAXG * ATT_MAXHD / 4];             // [gqa][hd / 4]
+    auto kq = [&](int c) -> float4 * {                          // chunk c: [64 rows][8 slots]
+        return c == 0 ? kq0 : c == 1 ? kq1 : c == 2 ? kq2 : c == 3 ? kq3
+             : c == 4 ? kq4 : c == 5 ? kq5 : c == 6 ? kq6 : kq7;
+    };
     const int tile = blockIdx.x, p0 = tile * SC_TILE, kvh = blockIdx.y, t = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
+    const int lane = threadIdx.x & 63, wave = wave_index();
     const int gqa = n_head / n_head_kv, kvd = n_head_kv * hd, nv = hd >> 2;
     const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
     if (p0 >= upto) return;
     const int pn = upto - p0 < SC_TILE ? upto - p0 : SC_TILE;
-#pragma unroll 8
-    for (int i = tid; i < pn * nv; i += 256) {
-        const int j = i / nv, c = i - j * nv;
-        const float4 v = *(const float4 *)(kc + (size_t)(p0 + j) * kvd + (size_t)kvh * hd + 4 * c);
-        *(float4 *)(ks + j * ks_str + 4 * c) = v;
-    }
-    for (int i = tid; i < gqa * nv; i += 256)
-        *(float4 *)(qs + 4 * i) =
-            *(const float4 *)(q + (size_t)t * q_stride + (size_t)kvh * gqa * hd + 4 * i);
-    __syncthreads();
-    const float scale = fox_div(1.0f, fox_sqrtf((float)hd));
-    const bool ok = lane < pn;
-    const float *kr = ks + (ok ? lane : 0) * ks_str;
-    for (int g = wave; g < gqa; g += 4) {
-        const float *qr = qs + g * hd;
-        float a = 0.0f;
-#pragma unroll 8
-        for (int d = 0; d < hd; d += 4) {
-            const float4 qv = *(const float4 *)(qr + d);
-            const float4 kv = *(const float4 *)(kr + d);
-            a = a + qv.x * kv.x;
-            a = a + qv.y * kv.y;
-            a = a + qv.z * kv.z;
-            a = a + qv.w * kv.w;
-        }
-        const float s = a * scale;
-        const int h = kvh * gqa + g;
-        if (ok) att[((size_t)t * n_head + h) * att_stride + p0 + lane] = s;
-        // tile maximum, NaN never taken
-        float m = (ok && s == s) ? s : -INFINITY;
+    // the query heads: blocks of 64 quads, wave w takes blocks w, w + 4
+    const int nqq = gqa * nv, nqb = (nqq + 63) >> 6;
+    const float *qbase = q + (size_t)t * q_stride + (size_t)kvh * gqa * hd;
+    constexpr int QB = ATT_MAXG * ATT_MAXHD / 4 / 64 / 4;   // blocks per wave at most
+    int nq_copies = 0;
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float w = __shfl_xor(m, o);
-            m = w > m ? w : m;
+    for (int k = 0; k < QB; k++) {
+        const int b = wave + 4 * k;
+        if (b < nqb) {
+            copy_to_lds16(qbase + 4 * min(64 * b + lane, nqq - 1), qq + 64 * b);
+            nq_copies++;
         }
-        if (lane == 0) tmax[((size_t)t * n_head + h) * n_tiles + tile] = m;
+    }
+    // K: chunk c is 8 blocks of 8 rows; wave w copies blocks 2w and 2w + 1
+    const float *kbase = kc + (size_t)p0 * kvd + (size_t)kvh * hd;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int b = 2 * wave + r, row = 8 * b + (lane >> 3);
+            const int j = (lane & 7) ^ (row & 7);
+            const int cq = min(SC_CQ * c + j, nv - 1);
+            copy_to_lds16(kbase + (size_t)min(row, pn - 1) * kvd + 4 * cq,
+                          kq(c) + 8 * b * SC_CQ);
+        }
+    }
+    const bool ok = lane < pn;
+    const int row = ok ? lane : 0, sw = row & 7;
+    constexpr int HW = ATT_MAXG / 4;                // heads per wave at most
+    float a[HW];
+#pragma unroll
+    for (int h = 0; h < HW; h++) a[h] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        // this wave's copies of chunk c (and the query heads) are in once at
+        // most 2 (NCH - 1 - c) copies are pending; the barrier covers the
+        // other waves' copies
+        wait_vmcnt(2 * (NCH - 1 - c));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        const float4 *kr = kq(c) + row * SC_CQ;
+#pragma unroll
+        for (int h = 0; h < HW; h++) {
+            const int g = wave + 4 * h;
+            if (g < gqa) {
+                const float4 *qr = qq + g * nv + SC_CQ * c;
+                float acc = a[h];
+#pragma unroll
+                for (int j = 0; j < SC_CQ; j++) {
+                    if (SC_CQ * c + j < nv) {
+                        const float4 qv = qr[j];
+                        const float4 kv = kr[j ^ sw];
+                        acc = acc + qv.x * kv.x;
+                        acc = acc + qv.y * kv.y;
+                        acc = acc + qv.z * kv.z;
+                        acc = acc + qv.w * kv.w;
+                    }
+                }
+                a[h] = acc;
+            }
+        }
+    }
+    (void)nq_copies;
+    const float scale = fox_div(1.0f, fox_sqrtf((float)hd));
+#pragma unroll
+    for (int h = 0; h < HW; h++) {
+        const int g = wave + 4 * h;
+        if (g < gqa) {
+            const float sc = a[h] * scale;
+            const int hh = kvh * gqa + g;
+            if (ok) att[((size_t)t * n_head + hh) * att_stride + p0 + lane] = sc;
+            // tile maximum, NaN never taken
+            const float m = wave_reduce((ok && sc == sc) ? sc : -INFINITY, -INFINITY,
+                                        [](float x, float y) { return y > x ? y : x; });
+            if (lane == 0) tmax[((size_t)t * n_head + hh) * n_tiles + tile] = m;
+        }
     }
 }
 
@@ -998,17 +1089,31 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
         float *att = (float *)ctx->ws;
         float *tmax = (float *)(ctx->ws + att_bytes);
         const size_t gqa = n_head / n_head_kv;
-        const size_t lds = (SC_TILE * (head_dim + 4) + gqa * head_dim) * sizeof(float);
+        const int nch = (int)((head_dim / 4 + SC_CQ - 1) / SC_CQ);
+        const size_t lds = 0;                                   // (static arrays)
+        const void *sk = nch == 1 ? (const void *)attn_scores_x<1>
+                       : nch == 2 ? (const void *)attn_scores_x<2>
+                       : nch == 3 ? (const void *)attn_scores_x<3>
+                       : nch == 4 ? (const void *)attn_scores_x<4>
+                       : nch == 5 ? (const void *)attn_scores_x<5>
+                       : nch == 6 ? (const void *)attn_scores_x<6>
+                       : nch == 7 ? (const void *)attn_scores_x<7>
+                                  : (const void *)attn_scores_x<8>;
         if (lds > 64 * 1024) {
-            hipError_t e = hipFuncSetAttribute((const void *)attn_scores_x,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+            hipError_t e = hipFuncSetAttribute(sk, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                (int)lds);
             if (e != hipSuccess) return fox_hip_fail(e, "attention: LDS size");
         }
-        hipLaunchKernelGGL(attn_scores_x, dim3((unsigned)n_tiles, (unsigned)n_head_kv, (unsigned)M),
-                           dim3(256), lds, ctx->stream, q, qs, k_cache, (int)n_head,
-                           (int)n_head_kv, (int)head_dim, pos, (int)n_ctx, att_stride, att, tmax,
-                           n_tiles);
+        {
+            const int ih = (int)n_head, ikv = (int)n_head_kv, ihd = (int)head_dim;
+            const int ictx = (int)n_ctx;
+            void *args[] = {(void *)&q, (void *)&qs, (void *)&k_cache, (void *)&ih, (void *)&ikv,
+                            (void *)&ihd, (void *)&pos, (void *)&ictx, (void *)&att_stride,
+                            (void *)&att, (void *)&tmax, (void *)&n_tiles};
+            hipError_t e = hipLaunchKernel(sk, dim3((unsigned)n_tiles, (unsigned)n_head_kv, (unsigned)M),
+                                           dim3(256), args, lds, ctx->stream);
+            if (e != hipSuccess) return fox_hip_fail(e, "attention scores");
+        }
         FOX_LAUNCHED("attention scores");
         const int ds = (int)(64 / gqa);
         const int n_sl = (int)((head_dim + ds - 1) / ds);
