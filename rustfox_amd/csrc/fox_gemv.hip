@@ -466,11 +466,15 @@ __global__ __launch_bounds__(WG) void gemv_blocks(Segs segs, int nb, int M, int 
 
 // F16 / F32 rows (src/kernels.c:81-96): each lane owns one row and adds
 // w[k] * x[k] sequentially in k, exactly the reference's order.  A
-// workgroup owns one 256-row tile of the tiled float layout; its chunks
-// (128 bytes of every row, 32 KB contiguous) stream through LDS (rows padded
-// by a dword against bank conflicts), double buffered: the next chunk's
-// loads are in flight while a chunk is summed.  The activations of a chunk
-// ride along in the same buffers.
+// workgroup owns one 256-row tile of the tiled float layout.  Its chunks
+// (128 bytes of every row, 32 KB contiguous) stream through LDS in halves
+// (64 bytes of every row per step; rows padded by a dword against bank
+// conflicts), double buffered: the next step's loads are in flight while a
+// step is summed.  The activations of a step ride along in the same
+// buffers.  (Half steps keep a workgroup's LDS near 35 KB, so that every
+// tile of a large head is resident at once: with whole chunks only two
+// workgroups fit a CU and the last tiles run in a second, mostly idle
+// round.)
 #define FR 256      // rows per workgroup
 
 template <typename WT, int MT>
@@ -479,19 +483,20 @@ __global__ __launch_bounds__(FR) void gemv_float(const WT *__restrict__ W, int K
                                                  int M, float *__restrict__ out,
                                                  int out_stride, unsigned flags)
 {
-    constexpr int FK = 128 / sizeof(WT);               // elements of a 128-byte row chunk
-    constexpr int RDW = FK * sizeof(WT) / 4;           // dwords of a row chunk
+    constexpr int FK = 64 / sizeof(WT);                // elements of a step (half a row chunk)
+    constexpr int RDW = FK * sizeof(WT) / 4;           // dwords of a row per step
     constexpr int RSTR = RDW + 1;                       // padded row stride
-    constexpr int PPR = RDW / 4;                        // 16-byte pieces per row chunk
+    constexpr int PPR = RDW / 4;                        // 16-byte pieces per row and step
     constexpr int NP = FR * PPR / FR;                   // pieces per thread
     __shared__ uint32_t wl[2][FR * RSTR];
     __shared__ float xs[2][MT * FK];
     if (MT == 1) M = 1;
     const int tid = threadIdx.x;
     const int r0 = blockIdx.x * FR;
-    const int nchunk = (K + FK - 1) / FK;
+    const int nchunk = (K + FK - 1) / FK;               // steps
+    const int nch128 = (K + 2 * FK - 1) / (2 * FK);     // 128-byte chunks of the layout
     // this tile's chunks, 32 KB each (rows and columns zero-padded)
-    const uint4 *tw = (const uint4 *)W + (size_t)blockIdx.x * nchunk * (FR * PPR);
+    const uint4 *tw = (const uint4 *)W + (size_t)blockIdx.x * nch128 * (FR * 2 * PPR);
 
     constexpr int XPT = (MT * FK + FR - 1) / FR;        // activations staged per thread
     uint4 R[NP];
@@ -499,9 +504,13 @@ __global__ __launch_bounds__(FR) void gemv_float(const WT *__restrict__ W, int K
     // global -> registers for chunk c (rows past N and columns past K read 0)
     auto fetch = [&](int c) {
         const int k0 = c * FK, kn = K - k0 < FK ? K - k0 : FK;
-        const uint4 *cw = tw + (size_t)c * (FR * PPR);
+        // half c & 1 of chunk c / 2: pieces (row, part) at row * 2 PPR + part
+        const uint4 *cw = tw + (size_t)(c >> 1) * (FR * 2 * PPR) + (c & 1) * PPR;
 #pragma unroll
-        for (int i = 0; i < NP; i++) R[i] = cw[tid + i * FR];
+        for (int i = 0; i < NP; i++) {
+            const int pc = tid + i * FR, r = pc / PPR, part = pc - r * PPR;
+            R[i] = cw[r * 2 * PPR + part];
+        }
 #pragma unroll
         for (int v = 0; v < XPT; v++) {
             const int e = tid + v * FR;
