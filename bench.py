@@ -7,9 +7,13 @@ Prints one JSON line:
              linear weights, f16 embedding and output), fully HBM-resident,
              batch 1, KV cache pre-filled with 2048 positions of f16 N(0,1)
              values; exact attention (logits bit-identical to RustFox's).
-  roofline   the TQ1_0 GEMV kernel (gemv_blocks, 14336 x 4096, one token):
-             algorithmic bytes per launch / its mean launch time from HIP
-             events on the stream it runs on, against 8 TB/s.
+  roofline   the fused TQ1_0 GEMV kernel (gemv_fused, 14336 x 4096, one
+             token): algorithmic bytes per launch / its mean launch time from
+             HIP events on the stream it runs on, against 8 TB/s.  traffic is
+             the HBM bytes per launch that rocprofv3 counts (FETCH_SIZE and
+             WRITE_SIZE, two runs of --gemv-only made before this process
+             touches the GPU), each counter scaled by its reading for a plain
+             256 MiB device copy.
   cpu_baseline  RustFox's own threadpool CPU path (compiled from its sources
              into oracle/_ref) decoding the same model file on this host.
 
@@ -19,9 +23,13 @@ pick.  Inputs are resident in HBM before the timed region starts.
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
+import shutil
 import statistics
+import subprocess
 import sys
 import tempfile
 import time
@@ -105,6 +113,74 @@ def gemv_case(gpu, gtype, N, K, M, rotate_bytes=1 << 30, min_launches=400):
                 frac_of_hbm=round(b / us / 1e3 / HBM_PEAK_GBS, 4), weight_copies=n_copies)
 
 
+COPY_BYTES = 256 << 20
+
+
+def gemv_only():
+    """The roofline case (TQ1_0 14336 x 4096, one token) and a plain device
+    copy of COPY_BYTES, whose counter readings scale the GEMV's."""
+    gpu = rf.Gpu(0)
+    r = gemv_case(gpu, rf.TQ1_0, 14336, 4096, 1, min_launches=100)
+    src = gpu.empty(COPY_BYTES, np.uint8)
+    dst = gpu.empty(COPY_BYTES, np.uint8)
+    gpu.copy(dst, src, COPY_BYTES)
+    gpu.sync()
+    gpu.copy(dst, src, COPY_BYTES)
+    gpu.sync()
+    src.free()
+    dst.free()
+    gpu.close()
+    log(f"bench: gemv-only {r['us_per_launch']} us per launch; copied {COPY_BYTES} bytes twice")
+
+
+def pmc_run(counter, timeout):
+    """Per-dispatch readings of one counter over a --gemv-only run:
+    (mean of the fused GEMV's, largest of the device copy's), in KiB."""
+    exe = shutil.which("rocprofv3")
+    if not exe:
+        return None
+    d = tempfile.mkdtemp(prefix="foxpmc-", dir="/tmp")
+    try:
+        cmd = [exe, "--pmc", counter, "--kernel-trace", "-d", d, "-o", "pmc", "-f", "csv",
+               "--", sys.executable, os.path.abspath(__file__), "--gemv-only"]
+        subprocess.run(cmd, timeout=timeout, stdout=subprocess.DEVNULL,
+                       stderr=subprocess.DEVNULL, check=True)
+        files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        gemv, copy = [], []
+        for r in csv.DictReader(open(files[0])):
+            if r["Counter_Name"] != counter:
+                continue
+            if "gemv_fused" in r["Kernel_Name"]:
+                gemv.append(float(r["Counter_Value"]))
+            elif "copyBuffer" in r["Kernel_Name"]:
+                copy.append(float(r["Counter_Value"]))
+        return statistics.mean(gemv), max(copy)
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
+def measure_traffic(timeout=180):
+    """HBM bytes per launch of the roofline GEMV: FETCH_SIZE + WRITE_SIZE,
+    each scaled so that the COPY_BYTES copy reads (or writes) COPY_BYTES."""
+    try:
+        total = 0.0
+        scales = {}
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            log(f"bench: rocprofv3 --pmc {counter} over the roofline GEMV and a copy")
+            r = pmc_run(counter, timeout)
+            if r is None:
+                return None
+            g, c = r
+            scales[counter] = COPY_BYTES / (c * 1024)
+            total += g * 1024 * scales[counter]
+        log(f"bench: counted traffic {total / 1e6:.3f} MB per launch (scales: fetch "
+            f"{scales['FETCH_SIZE']:.3f}, write {scales['WRITE_SIZE']:.3f})")
+        return int(round(total))
+    except Exception as e:  # the roofline stands without it
+        log(f"bench: traffic counters unavailable: {e}")
+        return None
+
+
 # ------------------------------------------------------------ CPU baseline
 
 def cpu_threads():
@@ -157,12 +233,23 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
     ap.add_argument("--workdir", default=None)
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 --pmc runs behind roofline.traffic")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="only the roofline GEMV case and a 256 MB device copy (the runs "
+                         "that rocprofv3 --pmc counts for the traffic figure)")
     a = ap.parse_args()
 
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported "
               "(the sharded design is described in DESIGN.md, not built)", file=sys.stderr)
         sys.exit(2)
+
+    if a.gemv_only:
+        gemv_only()
+        return
+    # (child processes: they run before this process initialises the GPU)
+    traffic = None if (a.no_traffic or a.no_gemv) else measure_traffic()
 
     spec = synth.spec("4b", n_ctx=PREFILL + a.warmup + a.steps)
     workdir = a.workdir or tempfile.mkdtemp(prefix="foxbench-", dir="/tmp")
@@ -203,7 +290,7 @@ def main():
                      and g["tokens"] == 1][0]
         roof = {"bound": "hbm", "achieved": main_case["gbs"], "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(main_case["gbs"] / HBM_PEAK_GBS, 4),
-                "traffic": None,
+                "traffic": traffic,
                 "kernel": "gemv_fused<TQ1_0, f32 in, store>, 14336x4096, 1 token",
                 "bytes_per_launch": main_case["bytes_per_launch"],
                 "us_per_launch": main_case["us_per_launch"]}

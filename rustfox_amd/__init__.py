@@ -239,6 +239,10 @@ class Gpu:
     def sync(self):
         _check(self.lib.fox_gpu_sync(self.ctx))
 
+    def copy(self, dst: DeviceArray, src: DeviceArray, nbytes: int):
+        """Device-to-device copy on the context's stream (fox_gpu_memcpy_d2d)."""
+        _check(self.lib.fox_gpu_memcpy_d2d(self.ctx, dst.ptr, src.ptr, nbytes))
+
     # -- compute (device arrays in, device arrays out)
     def quantize(self, mode, x: DeviceArray, K, M, x_stride, q: DeviceArray, scale: DeviceArray):
         _check(self.lib.fox_gpu_quantize(self.ctx, mode, x.ptr, K, M, x_stride, q.ptr, scale.ptr))
