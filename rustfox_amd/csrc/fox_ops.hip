@@ -706,36 +706,34 @@ __device__ __forceinline__ void sv_signal(int *flag, int v)
     __hip_atomic_store(flag, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// acc + x_0 + x_1 + ... over 4 * nq floats of LDS, in index order; the reads
-// of the next eight quads are in flight while the current eight are added
+// acc + x_0 + x_1 + ... over 4 * nq floats of LDS, in index order.  Eight
+// quad slots rotate: a slot is reloaded with the quad eight ahead right after
+// its four adds, so the read of a quad has seven quads of adds to complete
+// and no slot is copied (a pipelined pair of quad arrays compiles to a copy
+// of the array per step, which costs as much as the adds).
 __device__ __forceinline__ float chain_add_lds(float acc, const float4 *p, int nq)
 {
     int q = 0;
     if (nq >= 16) {
-        float4 A[8], B[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) A[u] = p[u];
-        for (; q + 24 <= nq; q += 16) {
-#pragma unroll
-            for (int u = 0; u < 8; u++) B[u] = p[q + 8 + u];
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                acc = acc + A[u].x; acc = acc + A[u].y; acc = acc + A[u].z; acc = acc + A[u].w;
-            }
-#pragma unroll
-            for (int u = 0; u < 8; u++) A[u] = p[q + 16 + u];
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                acc = acc + B[u].x; acc = acc + B[u].y; acc = acc + B[u].z; acc = acc + B[u].w;
-            }
+        float4 S0 = p[0], S1 = p[1], S2 = p[2], S3 = p[3];
+        float4 S4 = p[4], S5 = p[5], S6 = p[6], S7 = p[7];
+        auto add4 = [&](const float4 &v) {
+            acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
+        };
+        // (the scheduling barriers keep each reload after its slot's adds)
+        for (; q + 16 <= nq; q += 8) {
+            add4(S0); S0 = p[q + 8];  __builtin_amdgcn_sched_barrier(0);
+            add4(S1); S1 = p[q + 9];  __builtin_amdgcn_sched_barrier(0);
+            add4(S2); S2 = p[q + 10]; __builtin_amdgcn_sched_barrier(0);
+            add4(S3); S3 = p[q + 11]; __builtin_amdgcn_sched_barrier(0);
+            add4(S4); S4 = p[q + 12]; __builtin_amdgcn_sched_barrier(0);
+            add4(S5); S5 = p[q + 13]; __builtin_amdgcn_sched_barrier(0);
+            add4(S6); S6 = p[q + 14]; __builtin_amdgcn_sched_barrier(0);
+            add4(S7); S7 = p[q + 15]; __builtin_amdgcn_sched_barrier(0);
         }
-        // A holds quads q .. q+7
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            acc = acc + A[u].x; acc = acc + A[u].y; acc = acc + A[u].z; acc = acc + A[u].w;
-        }
+        // the slots hold quads q .. q + 7
+        add4(S0); add4(S1); add4(S2); add4(S3);
+        add4(S4); add4(S5); add4(S6); add4(S7);
         q += 8;
     }
     for (; q < nq; q++) {
