@@ -82,6 +82,27 @@ __device__ __forceinline__ double wave_sum_dd(double v)
     return wave_reduce(v, 0.0, [](double x, double y) { return x + y; });
 }
 
+// wave sums of N values at once (the steps of wave_reduce, interleaved);
+// every lane receives the sums
+template <int N>
+__device__ __forceinline__ void wave_sum_n(int (&v)[N])
+{
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_t<0xB1, 0xF>(0, v[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_t<0x4E, 0xF>(0, v[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_t<0x141, 0xF>(0, v[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_t<0x140, 0xF>(0, v[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_t<0x142, 0xA>(0, v[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] += dpp_t<0x143, 0xC>(0, v[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = read_lane(v[i], 63);
+}
+
 #define R4_LIMIT 8              // input dwords per thread: K <= 4 * R4_LIMIT * FWG
 
 // Where lane dl's int8 dword (block-local elements 4 dl .. 4 dl + 3) goes in
@@ -340,40 +361,51 @@ __device__ __forceinline__ float quantise_to_b(const FusedArgs &a, int t, int K,
             }
         }
     }
-    // B operand and per-block corrections; a wave's 64 lanes are one block
+    // B operand and per-block corrections; a wave's 64 lanes are one block.
+    // (No branches per lane: a lane without a B or C dword stores it into
+    // its slot of `sink`.  The block sums of all the wave's blocks reduce
+    // together, their steps interleaved.)
+    __shared__ uint32_t sink[64];
     const BLane bl = b_lane<FMT>(lane, M);
     const int bbytes = b_bytes_per_block_tok(FMT) * M;
     const int tbytes = FMT == FMT_TQ1 ? 32 : 16;
     // TQ1: corr = 128 * (sum of elements 128..159 and 224..239) - block sum
     const bool in4 = (lane >= 32 && lane < 40) || (lane >= 56 && lane < 60);
+    int part[R4MAX];
 #pragma unroll
     for (int r = 0; r < R4MAX; r++) {
         const int b = wave + FW * r;
-        if (b >= nb) break;                            // uniform: no block left
-        uint8_t *Bb = B + b * bbytes + t * tbytes;
         const uint32_t d = qd[r];
-        uint32_t dA = d, dB = d;
-        if (FMT == FMT_TQ1) {
-            uint32_t c0, c1;
-            qh_dwords(d, lane & 3, c0, c1);
-            if (lane >= 60) {
-                dA = c0;
-                dB = c1;
+        if (b < nb) {                                  // uniform
+            uint8_t *Bb = B + b * bbytes + t * tbytes;
+            if (FMT == FMT_TQ1) {
+                uint32_t c0, c1;
+                qh_dwords(d, lane & 3, c0, c1);
+                const bool qh = lane >= 60;
+                *(uint32_t *)(Bb + bl.offA) = qh ? c0 : d;
+                *(bl.hasB ? (uint32_t *)(Bb + bl.offB) : &sink[lane]) = qh ? c1 : d;
+                *(bl.hasC ? (uint32_t *)(Bb + bl.offC) : &sink[lane]) = 0u;
+            } else {
+                *(uint32_t *)(Bb + bl.offA) = d;
             }
         }
-        *(uint32_t *)(Bb + bl.offA) = dA;
-        if (bl.hasB) *(uint32_t *)(Bb + bl.offB) = dB;
-        if (bl.hasC) *(uint32_t *)(Bb + bl.offC) = 0u;
         const int sd = __builtin_amdgcn_sdot4((int)d, 0x01010101, 0, false);
-        if (FMT == FMT_TQ1) {
-            // block sum s and partial sum s4 in one reduction: |s| < 2^15
-            const int tot = wave_sum_i(sd + (in4 ? sd : 0) * 65536);
-            const int s = (int)(short)(tot & 0xffff);
-            const int s4 = (tot - s) / 65536;
-            if (lane == 0) aux[b * M + t] = 128 * s4 - s;
-        } else {
-            const int s = wave_sum_i(sd);
-            if (lane == 0) aux[b * M + t] = -s;
+        // TQ1: block sum s and partial sum s4 in one value: |s| < 2^15
+        part[r] = FMT == FMT_TQ1 ? sd + (in4 ? sd : 0) * 65536 : sd;
+    }
+    wave_sum_n<R4MAX>(part);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R4MAX; r++) {
+            const int b = wave + FW * r;
+            if (b >= nb) break;
+            if (FMT == FMT_TQ1) {
+                const int s = (int)(short)(part[r] & 0xffff);
+                const int s4 = (part[r] - s) / 65536;
+                aux[b * M + t] = 128 * s4 - s;
+            } else {
+                aux[b * M + t] = -part[r];
+            }
         }
     }
     if (IN == IN_Q) act = a.scale_in ? a.scale_in[t] : 0.0f;   // block sums come without a scale
@@ -457,15 +489,36 @@ __device__ __forceinline__ void block_mfma(const RawBlk &r, const uint8_t *__res
 
 // ------------------------------------------------------------ kernel
 
-// v[s] of a kernel-argument array, read with constant indices (flat
-// selects: a nested choice becomes branches)
+// a wave-uniform value pinned in scalar registers: the compiler may no longer
+// re-derive it from memory (pointers stay global-memory pointers, so that
+// loads through them remain global loads)
+template <typename T>
+__device__ __forceinline__ T in_sgpr(T v)
+{
+    asm volatile("" : "+s"(v));
+    return v;
+}
+
+template <typename T>
+__device__ __forceinline__ T *in_sgpr(T *p)
+{
+    auto g = (__attribute__((address_space(1))) T *)p;
+    asm volatile("" : "+s"(g));
+    return (T *)g;
+}
+
+// v[s] of a kernel-argument array: flat selects (a nested choice becomes
+// branches) among values pinned in registers (a select among the loads
+// themselves compiles to a load at a computed offset followed by a wait, at
+// every use: once per weight block)
 template <typename T>
 __device__ __forceinline__ T pick4(const T *v, int s)
 {
-    T r = v[0];
-    r = s >= 1 ? v[1] : r;
-    r = s >= 2 ? v[2] : r;
-    r = s >= 3 ? v[3] : r;
+    const T v0 = in_sgpr(v[0]), v1 = in_sgpr(v[1]), v2 = in_sgpr(v[2]), v3 = in_sgpr(v[3]);
+    T r = v0;
+    r = s >= 1 ? v1 : r;
+    r = s >= 2 ? v2 : r;
+    r = s >= 3 ? v3 : r;
     return r;
 }
 
@@ -616,17 +669,31 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
         float y = 0.0f;
         if (comb) {
             const float *tb = terms + (ti & 1) * tstride + (csl * nb * 16 + crow) * M + ct;
+            // terms in block order; eight slots rotate, each reloaded with
+            // the term eight ahead right after its add (the scheduling
+            // barriers keep that order), so that reads overlap the adds
+            const int ts = 16 * M;
             float acc = 0.0f;
             int b = 0;
-            for (; b + 4 <= nb; b += 4) {
-                const float t0 = tb[(b + 0) * 16 * M], t1 = tb[(b + 1) * 16 * M];
-                const float t2 = tb[(b + 2) * 16 * M], t3 = tb[(b + 3) * 16 * M];
-                acc = acc + t0;
-                acc = acc + t1;
-                acc = acc + t2;
-                acc = acc + t3;
+            if (nb >= 8) {
+                float T0 = tb[0], T1 = tb[ts], T2 = tb[2 * ts], T3 = tb[3 * ts];
+                float T4 = tb[4 * ts], T5 = tb[5 * ts], T6 = tb[6 * ts], T7 = tb[7 * ts];
+                for (; b + 16 <= nb; b += 8) {
+                    acc = acc + T0; T0 = tb[(b + 8) * ts];  __builtin_amdgcn_sched_barrier(0);
+                    acc = acc + T1; T1 = tb[(b + 9) * ts];  __builtin_amdgcn_sched_barrier(0);
+                    acc = acc + T2; T2 = tb[(b + 10) * ts]; __builtin_amdgcn_sched_barrier(0);
+                    acc = acc + T3; T3 = tb[(b + 11) * ts]; __builtin_amdgcn_sched_barrier(0);
+                    acc = acc + T4; T4 = tb[(b + 12) * ts]; __builtin_amdgcn_sched_barrier(0);
+                    acc = acc + T5; T5 = tb[(b + 13) * ts]; __builtin_amdgcn_sched_barrier(0);
+                    acc = acc + T6; T6 = tb[(b + 14) * ts]; __builtin_amdgcn_sched_barrier(0);
+                    acc = acc + T7; T7 = tb[(b + 15) * ts]; __builtin_amdgcn_sched_barrier(0);
+                }
+                // the slots hold terms b .. b + 7
+                acc = acc + T0; acc = acc + T1; acc = acc + T2; acc = acc + T3;
+                acc = acc + T4; acc = acc + T5; acc = acc + T6; acc = acc + T7;
+                b += 8;
             }
-            for (; b < nb; b++) acc = acc + tb[b * 16 * M];
+            for (; b < nb; b++) acc = acc + tb[b * ts];
             y = acc * ascale[ct];                           // src/gemv.c:70
         }
         if (EPI == EPI_STORE) {

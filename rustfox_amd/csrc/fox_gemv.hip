@@ -812,7 +812,7 @@ extern "C" fox_gpu_status fox_gpu_quantize(fox_gpu_ctx *ctx, int mode, const flo
     if (mode == FOX_GPU_ACT_PER_BLOCK && K % 256)
         return fox_fail(FOX_GPU_ERR_ARG, "quantize: %zu values is not a whole number of "
                         "256-element blocks", K);
-    const int fmt = mode == FOX_GPU_ACT_PER_BLOCK ? FMT_Q4K : FMT_TQ1;
+    const int fmt = mode == FOX_GPU_ACT_PER_BLOCK ? FMT_Q4K : FMT_TQ2;
     Ws w;
     fox_gpu_status st;
     // the B operand is laid out for whole blocks only; a ragged tail is

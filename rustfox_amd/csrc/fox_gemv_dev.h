@@ -12,10 +12,11 @@ typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 
 enum { FMT_TQ1 = 0, FMT_TQ2 = 1, FMT_Q4K = 2, FMT_Q6K = 3 };
 
+// the kernel format of a tensor of `type` (of its layout in HBM: TQ1_0
+// tensors are held as TQ2_0 blocks)
 static inline int fmt_of(int type)
 {
-    switch (type) {
-    case FOX_GPU_TQ1_0: return FMT_TQ1;
+    switch (fox_device_type(type)) {
     case FOX_GPU_TQ2_0: return FMT_TQ2;
     case FOX_GPU_Q4_K: return FMT_Q4K;
     case FOX_GPU_Q6_K: return FMT_Q6K;

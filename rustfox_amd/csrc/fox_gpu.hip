@@ -255,6 +255,98 @@ __device__ __forceinline__ int chunk_source(int type, int o, int *row)
     return 0;
 }
 
+// TQ1_0 <-> the TQ2_0 blocks TQ1_0 tensors are held as.  Element i of a
+// TQ1_0 block (src/ternary.c:73-93: bytes 0..31 carry elements l*32 + m at
+// level l, bytes 32..47 elements 160 + l*16 + m, the qh bytes 48..51
+// elements 240 + l*4 + m) has the trit ((uint8)(b * 3^l) * 3) >> 8
+// (src/ternary.c:59-63, before its - 1); element i of a TQ2_0 block
+// (src/ternary.c:177-188) is the 2-bit field 2 ((i % 128) / 32) of byte
+// (i / 128) * 32 + i % 32 (code - 1 likewise).  The f16 scale moves from
+// bytes 52..53 to 64..65.
+
+__device__ __forceinline__ int pow3(int l)
+{
+    int p = 1;
+    for (int k = 0; k < l; k++) p *= 3;
+    return p;
+}
+
+// the trit of element i of a TQ1_0 block
+__device__ __forceinline__ int tq1_trit(const uint8_t *blk, int i)
+{
+    int byte, level;
+    if (i < 160) {
+        byte = i & 31;
+        level = i >> 5;
+    } else if (i < 240) {
+        byte = 32 + ((i - 160) & 15);
+        level = (i - 160) >> 4;
+    } else {
+        byte = 48 + ((i - 240) & 3);
+        level = (i - 240) >> 2;
+    }
+    const uint8_t q = (uint8_t)(blk[byte] * pow3(level));
+    return (int)(((unsigned)q * 3u) >> 8);
+}
+
+// the code of element i of a TQ2_0 block
+__device__ __forceinline__ int tq2_code(const uint8_t *blk, int i)
+{
+    return (blk[(i >> 7) * 32 + (i & 31)] >> (2 * ((i & 127) >> 5))) & 3;
+}
+
+// total = blocks * 66: one output byte per step
+__global__ void tq1_to_tq2(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                           uint64_t total)
+{
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
+    for (; i < total; i += step) {
+        const uint64_t blk = i / 66;
+        const int j = (int)(i - blk * 66);
+        const uint8_t *s = src + blk * 54;
+        if (j < 64) {
+            const int h = j >> 5, m = j & 31;
+            int v = 0;
+            for (int l = 0; l < 4; l++) v |= tq1_trit(s, h * 128 + l * 32 + m) << (2 * l);
+            dst[i] = (uint8_t)v;
+        } else {
+            dst[i] = s[52 + (j - 64)];
+        }
+    }
+}
+
+// total = blocks * 54: one output byte per step.  A byte carrying the
+// digits q = sum_l t_l 3^(4 - l) is written as ceil(q * 256 / 243), the
+// encoding the reference's quantiser writes (a qh byte's four digits with a
+// fifth digit 0); any byte decoding to the same trits gives the same
+// results, this one is the canonical byte.
+__global__ void tq2_to_tq1(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                           uint64_t total)
+{
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
+    for (; i < total; i += step) {
+        const uint64_t blk = i / 54;
+        const int k = (int)(i - blk * 54);
+        const uint8_t *s = src + blk * 66;
+        if (k >= 52) {
+            dst[i] = s[64 + (k - 52)];
+            continue;
+        }
+        int q = 0;
+        if (k < 32) {
+            for (int l = 0; l < 5; l++) q = 3 * q + tq2_code(s, l * 32 + k);
+        } else if (k < 48) {
+            for (int l = 0; l < 5; l++) q = 3 * q + tq2_code(s, 160 + l * 16 + (k - 32));
+        } else {
+            for (int l = 0; l < 4; l++) q = 3 * q + tq2_code(s, 240 + l * 4 + (k - 48));
+            q *= 3;
+        }
+        dst[i] = (uint8_t)((q * 256 + 242) / 243);
+    }
+}
+
 // dir 0: GGUF bytes (src) -> device layout (dst); dir 1: the inverse.
 __global__ void repack_blocks(int type, int dir, const uint8_t *src, uint8_t *dst,
                               uint64_t n_rows, uint64_t nb, uint64_t chunk,
@@ -398,14 +490,32 @@ extern "C" fox_gpu_status fox_gpu_tensor_upload(fox_gpu_ctx *ctx, int type, uint
                         (unsigned long long)bytes);
     }
     st = fox_gpu_memcpy_h2d(ctx, stage, host, bytes);
+    const int dt = fox_device_type(type);
+    const uint8_t *src = stage;
+    uint64_t src_bb = bb;
+    uint8_t *stage2 = nullptr;
+    if (!st && dt != type) {
+        // TQ1_0: the same trits as TQ2_0 blocks first
+        src_bb = fox_block_bytes(dt);
+        const uint64_t n2 = rows * nb * src_bb;
+        if (hipMalloc(&stage2, n2) != hipSuccess) {
+            st = fox_fail(FOX_GPU_ERR_NOMEM, "tensor_upload: %llu bytes of staging",
+                          (unsigned long long)n2);
+        } else {
+            hipLaunchKernelGGL(tq1_to_tq2, dim3(grid_for(n2, 256)), dim3(256), 0, ctx->stream,
+                               stage, stage2, n2);
+            src = stage2;
+        }
+    }
     if (!st) {
         hipLaunchKernelGGL(repack_blocks, dim3(grid_for(t->dev_bytes, 256)), dim3(256), 0,
-                           ctx->stream, type, 0, stage, t->d, rows, nb, chunk,
-                           (uint64_t)bb, t->dev_bytes);
+                           ctx->stream, dt, 0, src, t->d, rows, nb, chunk, src_bb,
+                           t->dev_bytes);
         hipError_t e = hipGetLastError();
         if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
         if (e != hipSuccess) st = fox_hip_fail(e, "tensor_upload: repack");
     }
+    (void)hipFree(stage2);
     (void)hipFree(stage);
     if (st) {
         fox_gpu_tensor_free(ctx, t);
@@ -457,13 +567,23 @@ extern "C" fox_gpu_status fox_gpu_tensor_download(fox_gpu_ctx *ctx, const fox_gp
         return st;
     }
     uint64_t nb = t->ne0 / 256;
+    const int dt = fox_device_type(t->type);
+    const uint64_t dbb = fox_block_bytes(dt), n2 = t->ne1 * nb * dbb;
+    uint8_t *stage2 = nullptr;
+    if (dt != t->type && hipMalloc(&stage2, n2) != hipSuccess) {
+        (void)hipFree(stage);
+        return fox_fail(FOX_GPU_ERR_NOMEM, "tensor_download: staging");
+    }
     hipLaunchKernelGGL(repack_blocks, dim3(grid_for(t->dev_bytes, 256)), dim3(256), 0,
-                       ctx->stream, t->type, 1, t->d, stage, t->ne1, nb,
-                       (uint64_t)fox_chunk_bytes(t->type), (uint64_t)fox_block_bytes(t->type),
-                       t->dev_bytes);
+                       ctx->stream, dt, 1, t->d, stage2 ? stage2 : stage, t->ne1, nb,
+                       (uint64_t)fox_chunk_bytes(dt), dbb, t->dev_bytes);
+    if (stage2)   // TQ1_0: back from the TQ2_0 blocks it is held as
+        hipLaunchKernelGGL(tq2_to_tq1, dim3(grid_for(bytes, 256)), dim3(256), 0, ctx->stream,
+                           stage2, stage, (uint64_t)bytes);
     hipError_t e = hipGetLastError();
     st = e == hipSuccess ? fox_gpu_memcpy_d2h(ctx, host, stage, bytes)
                          : fox_hip_fail(e, "tensor_download: unpack");
+    (void)hipFree(stage2);
     (void)hipFree(stage);
     return st;
 }

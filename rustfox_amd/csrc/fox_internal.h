@@ -132,12 +132,22 @@ static inline size_t fox_block_elems(int type)
 
 static inline bool fox_is_block_type(int type) { return fox_block_elems(type) == 256; }
 
+// The block layout a tensor of `type` has in HBM.  TQ1_0 tensors are held
+// as TQ2_0 blocks: the upload re-encodes every trit (base-3 digit of a TQ1_0
+// byte) as the 2-bit code of the same element, so the GEMVs decode bit
+// fields instead of base-3 digits; integer block sums, and so every result,
+// are unchanged.
+static inline int fox_device_type(int type)
+{
+    return type == FOX_GPU_TQ1_0 ? FOX_GPU_TQ2_0 : type;
+}
+
+// bytes of one device chunk (16 rows x one block) of a tensor of `type`
 static inline size_t fox_chunk_bytes(int type)
 {
-    switch (type) {
+    switch (fox_device_type(type)) {
     case FOX_GPU_Q4_K: return Q4K_CHUNK;
     case FOX_GPU_Q6_K: return Q6K_CHUNK;
-    case FOX_GPU_TQ1_0: return TQ1_CHUNK;
     case FOX_GPU_TQ2_0: return TQ2_CHUNK;
     default: return 0;
     }

@@ -113,6 +113,43 @@ def test_tq1_closed_forms(gpu):
     assert np.array_equal(sums.numpy().reshape(2, 3), [[256] * 3, [-256] * 3])
 
 
+def tq1_trits(w):
+    """Trits (0..2, before the reference's - 1) of TQ1_0 blocks in element
+    order: src/ternary.c:59-63 on the bytes and levels of 73-93."""
+    b = w.reshape(-1, 54).astype(np.int64)
+    cols = []
+    for l in range(5):
+        cols.append(b[:, 0:32] * 3 ** l)
+    for l in range(5):
+        cols.append(b[:, 32:48] * 3 ** l)
+    for l in range(4):
+        cols.append(b[:, 48:52] * 3 ** l)
+    return ((np.concatenate(cols, axis=1) & 255) * 3) >> 8
+
+
+def test_tq1_noncanonical_download(gpu):
+    """TQ1_0 is held as 2-bit codes of its trits.  Bytes that are not the
+    canonical encoding of their trits (every byte decodes) come back as the
+    canonical byte, ceil(q * 256 / 243), of the same trits; scales exactly."""
+    rng = np.random.default_rng(11)
+    N, K = 24, 768
+    w = weights(rng, 34, N, K)
+    back = gpu.tensor(34, K, N, w).download()
+    assert np.array_equal(tq1_trits(back), tq1_trits(w))
+    t = tq1_trits(w)
+    q = np.zeros((t.shape[0], 52), np.int64)
+    for l in range(5):
+        q[:, 0:32] = 3 * q[:, 0:32] + t[:, 32 * l: 32 * l + 32]
+        q[:, 32:48] = 3 * q[:, 32:48] + t[:, 160 + 16 * l: 176 + 16 * l]
+    for l in range(4):
+        q[:, 48:52] = 3 * q[:, 48:52] + t[:, 240 + 4 * l: 244 + 4 * l]
+    q[:, 48:52] *= 3
+    b = back.reshape(-1, 54)
+    assert np.array_equal(b[:, :52], synth.tq1_pack_value(q))
+    assert np.array_equal(b[:, 52:], w.reshape(-1, 54)[:, 52:])
+    assert (b[:, :52] != w.reshape(-1, 54)[:, :52]).any()   # some bytes were not canonical
+
+
 @pytest.mark.parametrize("K,M,mode", [(512, 1, 0), (4096, 3, 0), (288, 1, 0), (9728, 8, 0),
                                       (4096, 2, 1), (768, 8, 1)])
 def test_quantize_exact(gpu, oracle, K, M, mode):
@@ -253,7 +290,13 @@ def test_tensor_bytes_round_trip(gpu, tname, N, K):
     tests/test_weights.c:142-175, for HBM)."""
     gtype = TYPES[tname]
     rng = np.random.default_rng(3)
-    w = rng.integers(0, 256, size=N * synth.row_bytes(gtype, K), dtype=np.uint8)
+    if tname == "TQ1_0":
+        # TQ1_0 is held as 2-bit codes: the bytes come back exactly when they
+        # are the canonical encoding of their trits, as the reference's
+        # quantiser writes them
+        w = synth.tq1_random(rng, N * K // 256).reshape(-1)
+    else:
+        w = rng.integers(0, 256, size=N * synth.row_bytes(gtype, K), dtype=np.uint8)
     t = gpu.tensor(gtype, K, N, w)
     assert np.array_equal(t.download(), w)
     info = t.info()
