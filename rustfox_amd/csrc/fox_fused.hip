@@ -1,5 +1,6 @@
 // fox_fused.hip -- one-launch GEMV stages of a decode layer for the ternary
-// formats (TQ1_0, TQ2_0): the activation input stage runs inside the GEMV.
+// formats (TQ1_0, TQ2_0; TQ1_0 tensors are held as TQ2_0 blocks of the same
+// trits): the activation input stage runs inside the GEMV.
 //
 // Every workgroup takes the f32 input (optionally RMS-normalised first),
 // quantises it to int8 exactly as src/gemv.c:11-42 does, and lays it out in
@@ -106,76 +107,16 @@ __device__ __forceinline__ void wave_sum_n(int (&v)[N])
 #define R4_LIMIT 8              // input dwords per thread: K <= 4 * R4_LIMIT * FWG
 
 // Where lane dl's int8 dword (block-local elements 4 dl .. 4 dl + 3) goes in
-// a block's B operand for one token: the layouts of act_prep (fox_gemv.hip),
-// which mirror the A slots of the block decode, as byte offsets from the
-// block's token-t base.  TQ1: dword A at slot lev of section sec, column 0;
-// dword B at slot lev - 1, column 1 (lev >= 1); a zero at slot 4 of the
-// section, column 1 (lev == 4); lanes 60..63 (the qh elements 240..255) hold
-// slot 15 of group dl - 60 instead, byte-transposed (qh_dwords).  TQ2: one
-// dword.
-struct BLane {
-    int offA, offB, offC;
-    bool hasB, hasC;
-};
-
-template <int FMT>
-__device__ __forceinline__ BLane b_lane(int dl, int M)
+// a block's B operand for one token, as a byte offset from the block's
+// token-t base: the TQ2_0 layout of act_prep (fox_gemv.hip), which mirrors
+// the A bytes of the block decode.  Elements e0 = 4 dl ..: half (g >> 1),
+// level l, offset 16 (g & 1) + 4 u.
+__device__ __forceinline__ int b_lane_off(int dl, int M)
 {
-    BLane L;
-    if (FMT == FMT_TQ1) {
-        // byte offset of slot s, group g, column c: B entry (u = s / 4, g,
-        // column 2t + c) is 16 bytes, dword s % 4 of it
-        auto off = [&](int s, int g, int c) { return ((s >> 2) * 4 + g) * 32 * M + 16 * c + (s & 3) * 4; };
-        int lev, g, sec;
-        if (dl < 40) {
-            lev = dl >> 3;
-            g = (dl & 7) >> 1;
-            sec = dl & 1;
-        } else {
-            lev = (dl - 40) >> 2;
-            g = (dl - 40) & 3;
-            sec = 2;
-        }
-        if (dl < 60) {
-            L.offA = off(5 * sec + lev, g, 0);
-            L.offB = off(5 * sec + (lev >= 1 ? lev - 1 : 0), g, 1);
-            L.offC = off(5 * sec + 4, g, 1);
-            L.hasB = lev >= 1;
-            L.hasC = lev == 4;
-        } else {
-            L.offA = off(15, dl - 60, 0);
-            L.offB = off(15, dl - 60, 1);
-            L.offC = 0;
-            L.hasB = true;
-            L.hasC = false;
-        }
-    } else {  // elements e0 = 4 dl ..: half (g >> 1), level l, offset 16 (g & 1) + 4 u
-        const int e0 = 4 * dl;
-        const int half = e0 >> 7, l = (e0 >> 5) & 3, o = e0 & 31;
-        const int g = 2 * half + (o >> 4), u = (o & 15) >> 2;
-        L.offA = ((u * 4 + g) * M) * 16 + l * 4;
-        L.offB = L.offC = 0;
-        L.hasB = L.hasC = false;
-    }
-    return L;
-}
-
-// TQ1 slot 15 for the lane's quad of lanes (lanes 60..63 hold the qh
-// dwords d_0..d_3 of elements 240 + 4 lev + g, byte g of d_lev): lane
-// 60 + g gets column 0 = (d_0, d_1, d_2, d_3 byte g) and column 1 =
-// (d_1, d_2, d_3 byte g, 0); other lanes compute values they do not use
-__device__ __forceinline__ void qh_dwords(uint32_t d, int g, uint32_t &c0, uint32_t &c1)
-{
-    const uint32_t d0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)d, 0x00, 0xF, 0xF, false);
-    const uint32_t d1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)d, 0x55, 0xF, 0xF, false);
-    const uint32_t d2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)d, 0xAA, 0xF, 0xF, false);
-    const uint32_t d3 = (uint32_t)__builtin_amdgcn_mov_dpp((int)d, 0xFF, 0xF, 0xF, false);
-    const uint32_t ug = (uint32_t)g;
-    const uint32_t lo = ug | (ug + 4) << 8 | 0x0c0c0000u;     // bytes 0, 1 from (S1, S0) byte g
-    const uint32_t hi = 0x0c0cu | ug << 16 | (ug + 4) << 24;  // bytes 2, 3 from (S1, S0) byte g
-    const uint32_t b2 = 0x0c000c0cu | ug << 16;               // byte 2 from S1 byte g
-    c0 = __builtin_amdgcn_perm(d1, d0, lo) | __builtin_amdgcn_perm(d3, d2, hi);
-    c1 = __builtin_amdgcn_perm(d2, d1, lo) | __builtin_amdgcn_perm(0u, d3, b2);
+    const int e0 = 4 * dl;
+    const int half = e0 >> 7, l = (e0 >> 5) & 3, o = e0 & 31;
+    const int g = 2 * half + (o >> 4), u = (o & 15) >> 2;
+    return ((u * 4 + g) * M) * 16 + l * 4;
 }
 
 // Token t of the input: optional RMSNorm (src/ops.c:7-22), per-vector int8
@@ -361,37 +302,17 @@ __device__ __forceinline__ float quantise_to_b(const FusedArgs &a, int t, int K,
             }
         }
     }
-    // B operand and per-block corrections; a wave's 64 lanes are one block.
-    // (No branches per lane: a lane without a B or C dword stores it into
-    // its slot of `sink`.  The block sums of all the wave's blocks reduce
-    // together, their steps interleaved.)
-    __shared__ uint32_t sink[64];
-    const BLane bl = b_lane<FMT>(lane, M);
+    // B operand and per-block corrections (-(block sum)); a wave's 64 lanes
+    // are one block.  The block sums of all the wave's blocks reduce
+    // together, their steps interleaved.
+    const int boff = b_lane_off(lane, M);
     const int bbytes = b_bytes_per_block_tok(FMT) * M;
-    const int tbytes = FMT == FMT_TQ1 ? 32 : 16;
-    // TQ1: corr = 128 * (sum of elements 128..159 and 224..239) - block sum
-    const bool in4 = (lane >= 32 && lane < 40) || (lane >= 56 && lane < 60);
     int part[R4MAX];
 #pragma unroll
     for (int r = 0; r < R4MAX; r++) {
         const int b = wave + FW * r;
-        const uint32_t d = qd[r];
-        if (b < nb) {                                  // uniform
-            uint8_t *Bb = B + b * bbytes + t * tbytes;
-            if (FMT == FMT_TQ1) {
-                uint32_t c0, c1;
-                qh_dwords(d, lane & 3, c0, c1);
-                const bool qh = lane >= 60;
-                *(uint32_t *)(Bb + bl.offA) = qh ? c0 : d;
-                *(bl.hasB ? (uint32_t *)(Bb + bl.offB) : &sink[lane]) = qh ? c1 : d;
-                *(bl.hasC ? (uint32_t *)(Bb + bl.offC) : &sink[lane]) = 0u;
-            } else {
-                *(uint32_t *)(Bb + bl.offA) = d;
-            }
-        }
-        const int sd = __builtin_amdgcn_sdot4((int)d, 0x01010101, 0, false);
-        // TQ1: block sum s and partial sum s4 in one value: |s| < 2^15
-        part[r] = FMT == FMT_TQ1 ? sd + (in4 ? sd : 0) * 65536 : sd;
+        if (b < nb) *(uint32_t *)(B + b * bbytes + t * 16 + boff) = qd[r];   // (uniform)
+        part[r] = __builtin_amdgcn_sdot4((int)qd[r], 0x01010101, 0, false);
     }
     wave_sum_n<R4MAX>(part);
     if (lane == 0) {
@@ -399,13 +320,7 @@ __device__ __forceinline__ float quantise_to_b(const FusedArgs &a, int t, int K,
         for (int r = 0; r < R4MAX; r++) {
             const int b = wave + FW * r;
             if (b >= nb) break;
-            if (FMT == FMT_TQ1) {
-                const int s = (int)(short)(part[r] & 0xffff);
-                const int s4 = (part[r] - s) / 65536;
-                aux[b * M + t] = 128 * s4 - s;
-            } else {
-                aux[b * M + t] = -part[r];
-            }
+            aux[b * M + t] = -part[r];
         }
     }
     if (IN == IN_Q) act = a.scale_in ? a.scale_in[t] : 0.0f;   // block sums come without a scale
@@ -417,7 +332,7 @@ __device__ __forceinline__ float quantise_to_b(const FusedArgs &a, int t, int K,
 
 // one lane's bytes of one (tile, block) chunk
 struct RawBlk {
-    uint32_t d0, d1, d2, d3;   // TQ1: qs dwords d0..d2, qh byte in d3; TQ2: qs uint4
+    uint32_t d0, d1, d2, d3;   // the lane's 16 bytes of 2-bit codes
     uint2 dd;                  // f16 scales of rows 4g .. 4g+3
 };
 
@@ -426,26 +341,18 @@ __device__ __forceinline__ RawBlk load_raw(const uint8_t *__restrict__ ch, int l
 {
     RawBlk r;
     const int g = lane >> 4;
-    if (FMT == FMT_TQ1) {
-        const uint32_t *qs = (const uint32_t *)(ch + 12 * lane);
-        r.d0 = qs[0];
-        r.d1 = qs[1];
-        r.d2 = qs[2];
-        r.d3 = ch[768 + lane];
-        r.dd = *(const uint2 *)(ch + 832 + 8 * g);
-    } else {
-        const uint4 v = *(const uint4 *)(ch + 16 * lane);
-        r.d0 = v.x;
-        r.d1 = v.y;
-        r.d2 = v.z;
-        r.d3 = v.w;
-        r.dd = *(const uint2 *)(ch + 1024 + 8 * g);
-    }
+    const uint4 v = *(const uint4 *)(ch + 16 * lane);
+    r.d0 = v.x;
+    r.d1 = v.y;
+    r.d2 = v.z;
+    r.d3 = v.w;
+    r.dd = *(const uint2 *)(ch + 1024 + 8 * g);
     return r;
 }
 
 // integer block sums of rows 4g .. 4g+3 for the lane's B column; returns
-// S in acc[r] for lanes with j < ncol (ncol = 2M for TQ1, M for TQ2)
+// S in acc[r] for lanes with j < M (each 2-bit code is one A byte; corr
+// carries the -1 of every code)
 template <int FMT>
 __device__ __forceinline__ void block_mfma(const RawBlk &r, const uint8_t *__restrict__ Bb,
                                            int M, int lane, int corr, int S[4])
@@ -453,38 +360,17 @@ __device__ __forceinline__ void block_mfma(const RawBlk &r, const uint8_t *__res
     const int g = lane >> 4, j = lane & 15;
     const v4i zero = {0, 0, 0, 0};
     v4i acc = zero;
-    if (FMT == FMT_TQ1) {
-        const bool bok = j < 2 * M;
-        v4i bv[4];
+    const bool bok = j < M;
+    const uint32_t dw[4] = {r.d0, r.d1, r.d2, r.d3};
 #pragma unroll
-        for (int u = 0; u < 4; u++)
-            bv[u] = bok ? *(const v4i *)(Bb + (((u * 4 + g) * (2 * M)) + j) * 16) : zero;
-        uint32_t av[16];
-        tq1_slots(r.d0, av);
-        tq1_slots(r.d1, av + 5);
-        tq1_slots(r.d2, av + 10);
-        av[15] = tq1_qh_slot(r.d3);
-#pragma unroll
-        for (int u = 0; u < 4; u++)
-            acc = mfma(av[4 * u], av[4 * u + 1], av[4 * u + 2], av[4 * u + 3], bv[u], acc);
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int oth = lane_xor1(acc[q]);
-            S[q] = acc[q] - 3 * oth + corr;
-        }
-    } else {
-        const bool bok = j < M;
-        const uint32_t dw[4] = {r.d0, r.d1, r.d2, r.d3};
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const v4i bv = bok ? *(const v4i *)(Bb + (((u * 4 + g) * M) + j) * 16) : zero;
-            const uint32_t d = dw[u];
-            acc = mfma(d & 0x03030303u, (d >> 2) & 0x03030303u, (d >> 4) & 0x03030303u,
-                       (d >> 6) & 0x03030303u, bv, acc);
-        }
-#pragma unroll
-        for (int q = 0; q < 4; q++) S[q] = acc[q] + corr;
+    for (int u = 0; u < 4; u++) {
+        const v4i bv = bok ? *(const v4i *)(Bb + (((u * 4 + g) * M) + j) * 16) : zero;
+        const uint32_t d = dw[u];
+        acc = mfma(d & 0x03030303u, (d >> 2) & 0x03030303u, (d >> 4) & 0x03030303u,
+                   (d >> 6) & 0x03030303u, bv, acc);
     }
+#pragma unroll
+    for (int q = 0; q < 4; q++) S[q] = acc[q] + corr;
 }
 
 // ------------------------------------------------------------ kernel
@@ -531,7 +417,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     __shared__ uint32_t ured[FW];
     __shared__ float ascale[FOX_GPU_MAX_TOKENS];
 
-    constexpr int CHUNK = FMT == FMT_TQ1 ? TQ1_CHUNK : TQ2_CHUNK;
+    constexpr int CHUNK = TQ2_CHUNK;
     // (the wave index as a wave-uniform value: everything per wave below,
     // the units, items and weight addresses, is then scalar work)
     const int tid = threadIdx.x, lane = tid & 63;
@@ -734,10 +620,10 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     // ---- blocks: integer sums, then one float term per row and token.  A
     // wave's units run through all its items; PF blocks stay in flight.
     const int g = lane >> 4, j = lane & 15;
-    const int ncol = FMT == FMT_TQ1 ? 2 * M : M;
+
     const int bbytes = b_bytes_per_block_tok(FMT) * M;
-    const bool lead = FMT == FMT_TQ1 ? (j < ncol && !(j & 1)) : j < ncol;
-    const int tok = FMT == FMT_TQ1 ? j >> 1 : j;
+    const bool lead = j < M;
+    const int tok = j;
     if (nu == 0) {
         for (int ti = 0; ti < ntl; ti++) item_end(ti);
         return;
@@ -806,7 +692,7 @@ static bool fused_aligned(const void *x, size_t x_stride, size_t M, const void *
 static fox_gpu_status fused_check(int type, size_t K, size_t M, int nslab, int *fmt)
 {
     *fmt = fmt_of(type);
-    if (*fmt != FMT_TQ1 && *fmt != FMT_TQ2)
+    if (*fmt != FMT_TQ2)
         return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "fused gemv: %s weights use the unfused path",
                         fox_type_name(type));
     if (K % 256 || K == 0) return fox_fail(FOX_GPU_ERR_ARG, "fused gemv: K %% 256 != 0");
@@ -858,8 +744,8 @@ static fox_gpu_status fused_go(fox_gpu_ctx *ctx, const FusedArgs &a, int grid)
 template <int IN, int EPI>
 static fox_gpu_status fused_dispatch(fox_gpu_ctx *ctx, int fmt, const FusedArgs &a, int grid)
 {
-    return fmt == FMT_TQ1 ? fused_go<FMT_TQ1, IN, EPI>(ctx, a, grid)
-                          : fused_go<FMT_TQ2, IN, EPI>(ctx, a, grid);
+    (void)fmt;   // fused_check admits the TQ2_0 layout only
+    return fused_go<FMT_TQ2, IN, EPI>(ctx, a, grid);
 }
 
 static void fused_segments(FusedArgs &a, size_t n, const fox_gpu_tensor *const *ws,
@@ -889,7 +775,7 @@ fox_gpu_status fox_fused_gemv(fox_gpu_ctx *ctx, size_t n, const fox_gpu_tensor *
 {
     int fmt;
     const size_t K = (size_t)ws[0]->ne0;
-    if (fmt_of(ws[0]->type) != FMT_TQ1 && fmt_of(ws[0]->type) != FMT_TQ2)
+    if (fmt_of(ws[0]->type) != FMT_TQ2)
         return FOX_GPU_ERR_UNSUPPORTED;
     if (fused_lds(fmt_of(ws[0]->type), (int)K, (int)M, 1).total > FUSED_LDS_MAX ||
         K > 4 * R4_LIMIT * FWG || !fused_aligned(x ? (const void *)x : (const void *)q,

@@ -18,15 +18,9 @@
 // MFMA's 16 columns.  Per-block float terms go to LDS and 16*M lanes add them
 // in block order.
 //
-// TQ1_0 decode.  With F_l = floor(b * 3^l / 256), the reference's trit
-// t_l = ((uint8)(b*3^l) * 3) >> 8 equals F_{l+1} - 3 F_l, so for a byte with
-// L levels and activations a_0..a_{L-1}:
-//     sum_l t_l a_l = sum_{l=1..L} F_l a_{l-1} - 3 sum_{l=1..L-1} F_l a_l.
-// F_l is the high byte of the 16-bit product b * 3^l (no wrap for l <= 5),
-// so two packed u16 multiplies and one byte permute give four F_l bytes; the
-// MFMA takes F_l as the A operand and (a_{l-1}, a_l) as two B columns.
-// F_5 (<= 242) enters as F_5 - 128 (sign bit flipped) and 128 * sum(a_4) is
-// added back; the -1 of every trit is the block sum of activations.
+// TQ1_0 tensors are held as TQ2_0 blocks of the same trits (the upload
+// converts them), so they run the TQ2_0 kernels: each 2-bit code is one
+// MFMA A byte, and the -1 of every trit is the block sum of activations.
 #include "fox_gemv_dev.h"
 
 #include <cstring>
@@ -115,36 +109,7 @@ __global__ __launch_bounds__(512) void act_prep(const float *__restrict__ x, int
         for (int i = tid; i < K; i += nthr) q_out[(size_t)t * K + i] = qbuf[i];
 
     // ---- B operand
-    if (FMT == FMT_TQ1) {
-        const int items = nb * 32;  // (b, u, g, c)
-        for (int it = tid; it < items; it += nthr) {
-            int c = it & 1, g = (it >> 1) & 3, u = (it >> 3) & 3, b = it >> 5;
-            uint32_t w4[4];
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-                uint32_t d = 0;
-#pragma unroll
-                for (int p = 0; p < 4; p++) {
-                    int e = tq1_elem(4 * u + w, g, p, c);
-                    uint32_t byte = e >= 0 ? (uint8_t)qbuf[b * 256 + e] : 0u;
-                    d |= byte << (8 * p);
-                }
-                w4[w] = d;
-            }
-            size_t off = ((((size_t)b * 4 + u) * 4 + g) * (2 * M) + 2 * t + c) * 16;
-            *(uint4 *)(B + off) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-        }
-        // corr = 128 * sum(level-4 activations of qs bytes) - sum(block)
-        for (int b = wave; b < nb; b += nwaves) {
-            const int8_t *qb = qbuf + b * 256;
-            int a = qb[lane] + qb[lane + 64] + qb[lane + 128] + qb[lane + 192];
-            int i4 = lane < 32 ? 128 + lane : lane < 48 ? 224 + (lane - 32) : -1;
-            int a4 = i4 >= 0 ? qb[i4] : 0;
-            a = wave_sum_i(a);
-            a4 = wave_sum_i(a4);
-            if (lane == 0) aux[(size_t)b * M + t] = 128 * a4 - a;
-        }
-    } else if (FMT == FMT_TQ2) {
+    if (FMT == FMT_TQ2) {
         const int items = nb * 16;  // (b, u, g)
         for (int it = tid; it < items; it += nthr) {
             int g = it & 3, u = (it >> 2) & 3, b = it >> 4;
@@ -240,45 +205,7 @@ __device__ __forceinline__ void gemv_block(const uint8_t *__restrict__ ch, int b
     const int g = lane >> 4, j = lane & 15;
     const v4i zero = {0, 0, 0, 0};
 
-    if (FMT == FMT_TQ1) {
-        const uint32_t *qs = (const uint32_t *)(ch + 12 * lane);
-        uint32_t d0 = qs[0], d1 = qs[1], d2 = qs[2];
-        uint32_t qh = ch[768 + lane];
-        uint2 dd = *(const uint2 *)(ch + 832 + 8 * g);
-        const bool bok = j < 2 * M;
-        v4i bv[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++)
-            bv[u] = load_b(B + ((((size_t)b * 4 + u) * 4 + g) * (2 * M) + j) * 16, bok);
-        uint32_t a[16];
-        tq1_slots(d0, a);
-        tq1_slots(d1, a + 5);
-        tq1_slots(d2, a + 10);
-        a[15] = tq1_qh_slot(qh);
-        v4i acc = zero;
-#pragma unroll
-        for (int u = 0; u < 4; u++)
-            acc = mfma(a[4 * u], a[4 * u + 1], a[4 * u + 2], a[4 * u + 3], bv[u], acc);
-        int oth[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) oth[r] = __shfl_xor(acc[r], 1);
-        if (bok && !(j & 1)) {
-            int t = j >> 1;
-            int corr = aux[(size_t)b * M + t];
-            uint32_t hw[2] = {dd.x, dd.y};
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                int S = acc[r] - 3 * oth[r] + corr;
-                int row = 4 * g + r;
-                if (sums) {
-                    if (row0 + row < n_rows) sums[((size_t)t * n_rows + row0 + row) * nb + b] = S;
-                } else {
-                    float d = half_bits_to_float((hw[r >> 1] >> (16 * (r & 1))) & 0xFFFFu);
-                    terms[row * M + t] = d * (float)S;
-                }
-            }
-        }
-    } else if (FMT == FMT_TQ2) {
+    if (FMT == FMT_TQ2) {
         uint4 qs = *(const uint4 *)(ch + 16 * lane);
         uint2 dd = *(const uint2 *)(ch + 1024 + 8 * g);
         const bool bok = j < M;
@@ -424,8 +351,7 @@ __global__ __launch_bounds__(WG) void gemv_blocks(Segs segs, int nb, int M, int 
 {
     extern __shared__ float terms[];  // [chunk_blocks][T][16][M]
     constexpr int T = terms_per_block(FMT);
-    constexpr int CHUNK = FMT == FMT_TQ1 ? TQ1_CHUNK : FMT == FMT_TQ2 ? TQ2_CHUNK
-                        : FMT == FMT_Q4K ? Q4K_CHUNK : Q6K_CHUNK;
+    constexpr int CHUNK = FMT == FMT_TQ2 ? TQ2_CHUNK : FMT == FMT_Q4K ? Q4K_CHUNK : Q6K_CHUNK;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
     int s = 0;
@@ -457,7 +383,7 @@ __global__ __launch_bounds__(WG) void gemv_blocks(Segs segs, int nb, int M, int 
     if (sums || !combiner) return;
     const int row = tile * 16 + crow;
     if (row >= n_rows) return;
-    float y = (FMT == FMT_TQ1 || FMT == FMT_TQ2) ? acc * scale[ct] : acc;  // src/gemv.c:70
+    float y = FMT == FMT_TQ2 ? acc * scale[ct] : acc;  // src/gemv.c:70
     float *o = segs.out[s] + (size_t)ct * segs.out_stride[s] + row;
     *o = (flags & FOX_GPU_GEMV_ACCUMULATE) ? *o + y : y;
 }
@@ -641,10 +567,6 @@ static fox_gpu_status launch_prep(fox_gpu_ctx *ctx, int fmt, const float *x, siz
         return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "gemv: K = %zu exceeds the 65536 "
                         "activation values one workgroup stages", K);
     switch (fmt) {
-    case FMT_TQ1:
-        hipLaunchKernelGGL(act_prep<FMT_TQ1>, grid, block, lds, ctx->stream, x, (int)x_stride,
-                           (int)K, (int)M, q_in, scale_in, q_out, scale_out, w.B, w.aux);
-        break;
     case FMT_TQ2:
         hipLaunchKernelGGL(act_prep<FMT_TQ2>, grid, block, lds, ctx->stream, x, (int)x_stride,
                            (int)K, (int)M, q_in, scale_in, q_out, scale_out, w.B, w.aux);
@@ -673,10 +595,6 @@ static fox_gpu_status launch_blocks(fox_gpu_ctx *ctx, int fmt, const Segs &sg, i
     size_t lds = sums ? 0 : (size_t)chunk_blocks * T * 16 * M * 4;
     dim3 grid((unsigned)tiles), block(WG);
     switch (fmt) {
-    case FMT_TQ1:
-        hipLaunchKernelGGL(gemv_blocks<FMT_TQ1>, grid, block, lds, ctx->stream, sg, nb, M,
-                           chunk_blocks, w.B, w.aux, w.scale, flags, sums);
-        break;
     case FMT_TQ2:
         hipLaunchKernelGGL(gemv_blocks<FMT_TQ2>, grid, block, lds, ctx->stream, sg, nb, M,
                            chunk_blocks, w.B, w.aux, w.scale, flags, sums);

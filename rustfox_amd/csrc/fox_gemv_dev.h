@@ -1,6 +1,6 @@
 // fox_gemv_dev.h -- device helpers shared by the GEMV kernels: the block
-// formats' MFMA operand layouts, the exact int8 activation quantiser and the
-// TQ1_0 level decode.  See fox_gemv.hip for the exactness contract.
+// formats' MFMA operand layouts, the exact int8 activation quantiser and
+// wave reductions.  See fox_gemv.hip for the exactness contract.
 #pragma once
 
 #include "fox_internal.h"
@@ -10,7 +10,7 @@
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 
-enum { FMT_TQ1 = 0, FMT_TQ2 = 1, FMT_Q4K = 2, FMT_Q6K = 3 };
+enum { FMT_TQ2 = 1, FMT_Q4K = 2, FMT_Q6K = 3 };
 
 // the kernel format of a tensor of `type` (of its layout in HBM: TQ1_0
 // tensors are held as TQ2_0 blocks)
@@ -33,7 +33,7 @@ __host__ __device__ constexpr int terms_per_block(int fmt)
 // B-operand bytes per block and token, aux int32 per block and token
 __host__ __device__ constexpr int b_bytes_per_block_tok(int fmt)
 {
-    return (fmt == FMT_TQ1 || fmt == FMT_Q4K) ? 512 : 256;
+    return fmt == FMT_Q4K ? 512 : 256;
 }
 
 __host__ __device__ constexpr int aux_per_block_tok(int fmt)
@@ -141,53 +141,6 @@ __device__ __forceinline__ uint32_t pack_lo_bytes(int r0, int r1, int r2, int r3
     const uint32_t lo = __builtin_amdgcn_perm((uint32_t)r1, (uint32_t)r0, 0x0c0c0400u);
     const uint32_t hi = __builtin_amdgcn_perm((uint32_t)r3, (uint32_t)r2, 0x04000c0cu);
     return lo | hi;
-}
-
-// Element index (within a 256-block) behind byte p of slot s of lane group g,
-// B column c (0: a_{l-1}, 1: a_l); -1 for a zero byte.  Must mirror the A
-// slots built in gemv_blocks<FMT_TQ1>.
-__device__ __forceinline__ int tq1_elem(int s, int g, int p, int c)
-{
-    if (s < 15) {
-        int sec = s / 5, l = s % 5 + 1;
-        if (c == 1 && l == 5) return -1;
-        int lev = c == 0 ? l - 1 : l;
-        if (sec < 2) return lev * 32 + 8 * g + 4 * sec + p;
-        return 160 + lev * 16 + 4 * g + p;
-    }
-    int l = p + 1;
-    if (c == 1 && l == 4) return -1;
-    int lev = c == 0 ? l - 1 : l;
-    return 240 + lev * 4 + g;
-}
-
-// four F_l bytes of the bytes of dword d at level l (multiplier m = 3^l)
-__device__ __forceinline__ uint32_t tq1_level(uint32_t e, uint32_t o, unsigned short m)
-{
-    v2u16 mm = {m, m};
-    uint32_t ye = __builtin_bit_cast(uint32_t, (v2u16)(__builtin_bit_cast(v2u16, e) * mm));
-    uint32_t yo = __builtin_bit_cast(uint32_t, (v2u16)(__builtin_bit_cast(v2u16, o) * mm));
-    return __builtin_amdgcn_perm(yo, ye, 0x07030501u);
-}
-
-__device__ __forceinline__ void tq1_slots(uint32_t d, uint32_t *a)
-{
-    uint32_t e = __builtin_amdgcn_perm(0u, d, 0x0c020c00u);  // b0, b2 as u16
-    uint32_t o = __builtin_amdgcn_perm(0u, d, 0x0c030c01u);  // b1, b3 as u16
-    a[0] = tq1_level(e, o, 3);
-    a[1] = tq1_level(e, o, 9);
-    a[2] = tq1_level(e, o, 27);
-    a[3] = tq1_level(e, o, 81);
-    a[4] = tq1_level(e, o, 243) ^ 0x80808080u;
-}
-
-__device__ __forceinline__ uint32_t tq1_qh_slot(uint32_t b)
-{
-    uint32_t e = __builtin_amdgcn_perm(0u, b, 0x0c000c00u);  // b, b as u16
-    v2u16 m1 = {3, 9}, m2 = {27, 81};
-    uint32_t ya = __builtin_bit_cast(uint32_t, (v2u16)(__builtin_bit_cast(v2u16, e) * m1));
-    uint32_t yb = __builtin_bit_cast(uint32_t, (v2u16)(__builtin_bit_cast(v2u16, e) * m2));
-    return __builtin_amdgcn_perm(yb, ya, 0x07050301u);  // F1 F2 F3 F4
 }
 
 __device__ __forceinline__ v4i mfma(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3,

@@ -223,16 +223,8 @@ extern "C" fox_gpu_status fox_gpu_sync(fox_gpu_ctx *ctx)
 // returns the byte offset k inside that row's block and sets *row.
 __device__ __forceinline__ int chunk_source(int type, int o, int *row)
 {
-    int L, e, g;
+    int L, e;
     switch (type) {
-    case FOX_GPU_TQ1_0:
-        if (o < 768) {
-            L = o / 12; e = o % 12; g = L >> 4; *row = L & 15;
-            return e < 8 ? 8 * g + e : 32 + 4 * g + (e - 8);
-        }
-        if (o < 832) { L = o - 768; *row = L & 15; return 48 + (L >> 4); }
-        *row = (o - 832) >> 1;
-        return 52 + ((o - 832) & 1);
     case FOX_GPU_TQ2_0:
         if (o < 1024) { L = o >> 4; e = o & 15; *row = L & 15; return 16 * (L >> 4) + e; }
         *row = (o - 1024) >> 1;

@@ -43,7 +43,6 @@ __host__ __device__ inline uint64_t fox_float_offset(uint64_t r, uint64_t k, uin
     return (((r / FOX_FTILE) * nchunk + k / per) * FOX_FTILE + r % FOX_FTILE) * FOX_FCHUNK +
            (k % per) * esize;
 }
-#define TQ1_CHUNK 864
 #define TQ2_CHUNK 1056
 #define Q4K_CHUNK 2304
 #define Q6K_CHUNK 3360
