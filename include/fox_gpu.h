@@ -84,8 +84,11 @@ fox_gpu_status fox_gpu_sync(fox_gpu_ctx *ctx);
 
 /* Upload one GGUF tensor (`bytes` = its GGUF size, host pointer) into HBM.
  * Block types are repacked into the device layout (same byte count plus
- * padding of the row count to 16); F16/F32 are laid out in 256-row tiles of
- * 128-byte row chunks (fox_gpu_tensor_download gives row-major bytes back).
+ * padding of the row count to 16), except TQ1_0, which is held as TQ2_0
+ * blocks of the same trits (66 B instead of 54 B per 256 weights: the GEMVs
+ * then decode 2-bit fields; results are unchanged).  F16/F32 are laid out in
+ * 256-row tiles of 128-byte row chunks (fox_gpu_tensor_download gives
+ * row-major bytes back).
  * Backs the FOX_WEIGHTS_DEVICE mode of fox_weights_open
  * (include/fox/fox.h:372-387), loaded once per tensor like the resident
  * backend (src/weights.c:461-496). */
@@ -95,7 +98,10 @@ fox_gpu_status fox_gpu_tensor_upload(fox_gpu_ctx *ctx, int type, uint64_t ne0,
 fox_gpu_status fox_gpu_tensor_info(const fox_gpu_tensor *t, int *type, uint64_t *ne0,
                                    uint64_t *ne1, uint64_t *gguf_bytes,
                                    uint64_t *device_bytes);
-/* Copy the tensor back in its GGUF byte layout (inverse repack). */
+/* Copy the tensor back in its GGUF byte layout (inverse repack).  TQ1_0
+ * bytes come back as the canonical encoding ceil(q * 256 / 243) of their
+ * trits, the byte the reference's quantiser writes; a byte that decodes to
+ * the same trits otherwise comes back as that canonical byte. */
 fox_gpu_status fox_gpu_tensor_download(fox_gpu_ctx *ctx, const fox_gpu_tensor *t,
                                        void *host, uint64_t bytes);
 void           fox_gpu_tensor_free(fox_gpu_ctx *ctx, fox_gpu_tensor *t);
