@@ -352,22 +352,24 @@ __device__ __forceinline__ RawBlk load_raw(const uint8_t *__restrict__ ch, int l
 
 // integer block sums of rows 4g .. 4g+3 for the lane's B column; returns
 // S in acc[r] for lanes with j < M (each 2-bit code is one A byte; corr
-// carries the -1 of every code)
+// carries the -1 of every code).  Lanes past the M tokens read the last
+// token's column (their MFMA columns are not used): with no lane-dependent
+// branch the four B reads issue together.
 template <int FMT>
 __device__ __forceinline__ void block_mfma(const RawBlk &r, const uint8_t *__restrict__ Bb,
                                            int M, int lane, int corr, int S[4])
 {
-    const int g = lane >> 4, j = lane & 15;
-    const v4i zero = {0, 0, 0, 0};
-    v4i acc = zero;
-    const bool bok = j < M;
+    const int g = lane >> 4, j = lane & 15, jc = j < M ? j : M - 1;
+    v4i bv[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) bv[u] = *(const v4i *)(Bb + (((u * 4 + g) * M) + jc) * 16);
+    v4i acc = {0, 0, 0, 0};
     const uint32_t dw[4] = {r.d0, r.d1, r.d2, r.d3};
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-        const v4i bv = bok ? *(const v4i *)(Bb + (((u * 4 + g) * M) + j) * 16) : zero;
         const uint32_t d = dw[u];
         acc = mfma(d & 0x03030303u, (d >> 2) & 0x03030303u, (d >> 4) & 0x03030303u,
-                   (d >> 6) & 0x03030303u, bv, acc);
+                   (d >> 6) & 0x03030303u, bv[u], acc);
     }
 #pragma unroll
     for (int q = 0; q < 4; q++) S[q] = acc[q] + corr;
@@ -635,7 +637,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
             const int n = n0 + k;
             if (n >= total) break;
             const int u = wave + FW * r, sl = u >= nb, b = u - sl * nb;
-            const int corr = lead ? aux[b * M + tok] : 0;
+            const int corr = aux[b * M + (lead ? tok : M - 1)];   // (used by lead lanes)
             int S[4];
             block_mfma<FMT>(raw[k], B + b * bbytes, M, lane, corr, S);
             const RawBlk rk = raw[k];
