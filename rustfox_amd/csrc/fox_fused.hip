@@ -70,7 +70,7 @@ __host__ __device__ inline FusedLds fused_lds(int fmt, int K, int M, int nslab)
     L.q = off;
     L.B = off;     off += nb * M * b_bytes_per_block_tok(fmt);
     L.aux = off;   off += ((nb * M * aux_per_block_tok(fmt) * 4) + 15) & ~15;
-    L.terms = off; off += 2 * nslab * nb * terms_per_block(fmt) * 16 * M * 4;
+    L.terms = off; off += 2 * nslab * 16 * M * ((nb + 3) & ~3) * terms_per_block(fmt) * 4;
     L.y = off;     off += nslab * 16 * M * 4;
     L.total = off;
     return L;
@@ -429,9 +429,13 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     const FusedLds L = fused_lds(FMT, K, M, nslab);
     uint8_t *B = lds + L.B;
     int32_t *aux = (int32_t *)(lds + L.aux);
-    float *terms = (float *)(lds + L.terms);               // [2][nslab][nb][16][M]
+    // block terms [2][nslab][16 rows][M][nbp]: a row's terms are contiguous,
+    // padded with zeros to nbp, a multiple of 4 (adding +0.0f changes no
+    // sum: the ordered sum starts at +0.0f and so is never -0.0f)
+    float *terms = (float *)(lds + L.terms);
     float *ybuf = (float *)(lds + L.y);
-    const int tstride = nslab * nb * 16 * M;               // floats per terms buffer
+    const int nbp = (nb + 3) & ~3;
+    const int tstride = nslab * 16 * M * nbp;              // floats per terms buffer
 
     // ---- work: items bx, bx + gridDim.x, ... (a 16-row tile of one segment,
     // or with SILU a tile of gate and the same tile of up).  Arguments are
@@ -529,6 +533,15 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     if (EPI == EPI_STORE) epi_load(0, pre0, pre1);
     // (nothing that uses the input may be scheduled above the weight loads)
     __builtin_amdgcn_sched_barrier(0);
+    // the zero padding of the term rows (read after the input stage's
+    // barriers)
+    if (nbp != nb) {
+        const int pad = nbp - nb;
+        for (int i = tid; i < 2 * nslab * 16 * M * pad; i += FWG) {
+            const int row = i / pad;
+            terms[row * nbp + nb + (i - row * pad)] = 0.0f;
+        }
+    }
 
     // ---- input stage: int8 activations straight into the B operand in LDS
     // (token 0 outside the loop: its waits then count the loads above)
@@ -556,32 +569,33 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
         const bool owns = comb && orow < pick4(a.n_rows, sg);
         float y = 0.0f;
         if (comb) {
-            const float *tb = terms + (ti & 1) * tstride + (csl * nb * 16 + crow) * M + ct;
-            // terms in block order; eight slots rotate, each reloaded with
-            // the term eight ahead right after its add (the scheduling
-            // barriers keep that order), so that reads overlap the adds
-            const int ts = 16 * M;
+            // The row's terms in block order, four at a time (chunk c holds
+            // terms 4c .. 4c + 3).  Four chunk slots rotate, each reloaded
+            // with the chunk four ahead right after its adds (the
+            // scheduling barriers keep that order), so that the reads
+            // overlap the adds; with up to four chunks all reads go out at
+            // once.
+            const float4 *tq = (const float4 *)(terms + (ti & 1) * tstride +
+                                                ((csl * 16 + crow) * M + ct) * nbp);
+            const int nq = nbp >> 2, last = nq - 1;
             float acc = 0.0f;
-            int b = 0;
-            if (nb >= 8) {
-                float T0 = tb[0], T1 = tb[ts], T2 = tb[2 * ts], T3 = tb[3 * ts];
-                float T4 = tb[4 * ts], T5 = tb[5 * ts], T6 = tb[6 * ts], T7 = tb[7 * ts];
-                for (; b + 16 <= nb; b += 8) {
-                    acc = acc + T0; T0 = tb[(b + 8) * ts];  __builtin_amdgcn_sched_barrier(0);
-                    acc = acc + T1; T1 = tb[(b + 9) * ts];  __builtin_amdgcn_sched_barrier(0);
-                    acc = acc + T2; T2 = tb[(b + 10) * ts]; __builtin_amdgcn_sched_barrier(0);
-                    acc = acc + T3; T3 = tb[(b + 11) * ts]; __builtin_amdgcn_sched_barrier(0);
-                    acc = acc + T4; T4 = tb[(b + 12) * ts]; __builtin_amdgcn_sched_barrier(0);
-                    acc = acc + T5; T5 = tb[(b + 13) * ts]; __builtin_amdgcn_sched_barrier(0);
-                    acc = acc + T6; T6 = tb[(b + 14) * ts]; __builtin_amdgcn_sched_barrier(0);
-                    acc = acc + T7; T7 = tb[(b + 15) * ts]; __builtin_amdgcn_sched_barrier(0);
-                }
-                // the slots hold terms b .. b + 7
-                acc = acc + T0; acc = acc + T1; acc = acc + T2; acc = acc + T3;
-                acc = acc + T4; acc = acc + T5; acc = acc + T6; acc = acc + T7;
-                b += 8;
+            auto add4 = [&](const float4 &v) {
+                acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
+            };
+            float4 S0 = tq[0], S1 = tq[min(1, last)], S2 = tq[min(2, last)], S3 = tq[min(3, last)];
+            int c = 0;
+            for (; c + 8 <= nq; c += 4) {
+                add4(S0); S0 = tq[c + 4]; __builtin_amdgcn_sched_barrier(0);
+                add4(S1); S1 = tq[c + 5]; __builtin_amdgcn_sched_barrier(0);
+                add4(S2); S2 = tq[c + 6]; __builtin_amdgcn_sched_barrier(0);
+                add4(S3); S3 = tq[c + 7]; __builtin_amdgcn_sched_barrier(0);
             }
-            for (; b < nb; b++) acc = acc + tb[b * ts];
+            // the slots hold chunks c .. c + 3 (those below nq)
+            add4(S0);
+            if (c + 1 < nq) add4(S1);
+            if (c + 2 < nq) add4(S2);
+            if (c + 3 < nq) add4(S3);
+            for (c += 4; c < nq; c++) add4(tq[c]);
             y = acc * ascale[ct];                           // src/gemv.c:70
         }
         if (EPI == EPI_STORE) {
@@ -657,7 +671,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
                         if (grow < nrows) a.sums[((size_t)tok * nrows + grow) * nb + b] = S[q];
                     } else {
                         const float d = half_bits_to_float((hw[q >> 1] >> (16 * (q & 1))) & 0xFFFFu);
-                        terms[(ti & 1) * tstride + ((sl * nb + b) * 16 + row) * M + tok] =
+                        terms[(ti & 1) * tstride + ((sl * 16 + row) * M + tok) * nbp + b] =
                             d * (float)S[q];
                     }
                 }
