@@ -482,6 +482,25 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
         r = wrap ? 0 : r + 1;
         ti += wrap;
     };
+    // The wave's weight cursor: unit r of item ti and its chunk.  The next
+    // unit of the same item and slab is FW chunks on; only a new item, or
+    // the step from the gate blocks to the up blocks, recomputes the
+    // address (the computation is scalar work every wave of the compute
+    // unit shares one scalar unit for).  Called only when a next unit
+    // exists.
+    struct Cur {
+        int ti, r;
+        const uint8_t *p;
+    };
+    auto cur_next = [&](Cur c) -> Cur {
+        const int u = wave + FW * c.r;
+        if (c.r + 1 == nu || (EPI == EPI_SILU && u < nb && u + FW >= nb)) {   // (uniform)
+            int ti = c.ti, r = c.r;
+            step(ti, r);
+            return Cur{ti, r, unit_ptr(ti, r)};
+        }
+        return Cur{c.ti, c.r + 1, c.p + FW * CHUNK};
+    };
 
     // ---- loads in the order they are used (they complete in order): the
     // input of token 0 (above), the first weight blocks, the epilogue's
@@ -490,16 +509,12 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     // (every wave issues PF block loads, past its last unit re-reading that
     // one, so that the input's first use waits for the input only)
     RawBlk raw[PF];
-    int fti = 0, fr = 0;                                   // unit k (then PF) of the wave
+    Cur fc{0, 0, unit_ptr(0, 0)};                          // unit k (then PF) of the wave
 #pragma unroll
     for (int k = 0; k < PF; k++) {
-        raw[k] = load_raw<FMT>(unit_ptr(fti, fr), lane);
-        int t2 = fti, r2 = fr;
-        step(t2, r2);
-        fti = k + 1 < total ? t2 : fti;                    // past the last unit: reload it
-        fr = k + 1 < total ? r2 : fr;
+        raw[k] = load_raw<FMT>(fc.p, lane);
+        if (k + 1 < total) fc = cur_next(fc);              // past the last unit: reload it
     }
-    if (PF < total) step(fti, fr);                         // unit PF: the first refill
 
     // combiner threads: (slab, token, row) of an item's outputs
     const int nthr = nslab * 16 * M;
@@ -656,8 +671,8 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
             block_mfma<FMT>(raw[k], B + b * bbytes, M, lane, corr, S);
             const RawBlk rk = raw[k];
             if (n + PF < total) {
-                raw[k] = load_raw<FMT>(unit_ptr(fti, fr), lane);
-                step(fti, fr);
+                raw[k] = load_raw<FMT>(fc.p, lane);
+                if (n + PF + 1 < total) fc = cur_next(fc);
             }
             if (lead) {
                 const uint32_t hw[2] = {rk.dd.x, rk.dd.y};
