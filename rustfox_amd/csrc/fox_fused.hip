@@ -545,7 +545,9 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
         }
     };
     float pre0 = 0.0f, pre1 = 0.0f;
-    if (EPI == EPI_STORE) epi_load(0, pre0, pre1);
+    // (the first item's old outputs or RoPE table entries: in flight during
+    // the input stage)
+    if (EPI == EPI_STORE || EPI == EPI_ROPE) epi_load(0, pre0, pre1);
     // (nothing that uses the input may be scheduled above the weight loads)
     __builtin_amdgcn_sched_barrier(0);
     // the zero padding of the term rows (read after the input stage's
@@ -569,7 +571,6 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
         const float s = quantise_to_b<FMT, IN, R4>(a, t, K, B, aux, dred, ured, in);
         if (tid == 0) ascale[t] = s;
     }
-    if (EPI == EPI_ROPE) epi_load(0, pre0, pre1);
     __syncthreads();
 
     // ---- end of item ti: ordered combine, activation scale, epilogue
