@@ -131,8 +131,12 @@ struct InRegs {
     uint32_t qd[R4MAX];
 };
 
+// (the pointers come in as separate kernel arguments, which the hardware
+// loads into scalar registers before the wave starts: the first input loads
+// need not wait for a kernel-argument read)
 template <int IN, int R4MAX>
-__device__ __forceinline__ void load_input(const FusedArgs &a, int t, int K, InRegs<R4MAX> &in)
+__device__ __forceinline__ void load_input(const float *x, const float *norm_w, const int8_t *q_in,
+                                           int x_stride, int t, int K, InRegs<R4MAX> &in)
 {
     const int tid = threadIdx.x, nd = K >> 2;
     // Every lane loads (past the end it re-reads dword nd - 1; in_mask drops
@@ -141,7 +145,7 @@ __device__ __forceinline__ void load_input(const FusedArgs &a, int t, int K, InR
     // overwritten here waits for its load, so either would make the weight
     // blocks issued next wait for the input.
     if (IN == IN_Q) {
-        const uint32_t *q4 = (const uint32_t *)(a.q_in + (size_t)t * K);
+        const uint32_t *q4 = (const uint32_t *)(q_in + (size_t)t * K);
 #pragma unroll
         for (int r = 0; r < R4MAX; r++) {
             const int m = tid + r * FWG;
@@ -149,14 +153,14 @@ __device__ __forceinline__ void load_input(const FusedArgs &a, int t, int K, InR
         }
         return;
     }
-    const float4 *x4 = (const float4 *)(a.x + (size_t)t * a.x_stride);
+    const float4 *x4 = (const float4 *)(x + (size_t)t * x_stride);
 #pragma unroll
     for (int r = 0; r < R4MAX; r++) {
         const int m = tid + r * FWG;
         in.xv[r] = x4[m < nd ? m : nd - 1];
     }
     if (IN == IN_NORM) {
-        const float4 *w4 = (const float4 *)a.norm_w;
+        const float4 *w4 = (const float4 *)norm_w;
 #pragma unroll
         for (int r = 0; r < R4MAX; r++) {
             const int m = tid + r * FWG;
@@ -411,7 +415,8 @@ __device__ __forceinline__ T pick4(const T *v, int s)
 }
 
 template <int FMT, int IN, int EPI, int R4>
-__global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
+__global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float *norm_in,
+                                                 const int8_t *q_in, int nb_in, FusedArgs a)
 {
     extern __shared__ uint4 fused_lds4[];
     uint8_t *lds = (uint8_t *)fused_lds4;
@@ -424,7 +429,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     // the units, items and weight addresses, is then scalar work)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int nb = a.nb, M = a.M, K = nb * 256;
+    const int nb = nb_in, M = a.M, K = nb * 256;
     const int nslab = EPI == EPI_SILU ? 2 : 1;
     const FusedLds L = fused_lds(FMT, K, M, nslab);
     uint8_t *B = lds + L.B;
@@ -445,7 +450,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
     // the input of token 0 first: nothing ahead of its loads but the
     // argument reads they need
     InRegs<R4> in;
-    load_input<IN, R4>(a, 0, K, in);
+    load_input<IN, R4>(x_in, norm_in, q_in, a.x_stride, 0, K, in);
     const int ntl = a.n_per + (bx < a.n_rem);              // items of this workgroup (>= 1)
     const int ts1 = a.tile_start[1], ts2 = a.tile_start[2], ts3 = a.tile_start[3];
     // (integer arithmetic only: comparisons turned into 0/1 values and
@@ -567,7 +572,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(FusedArgs a)
         if (tid == 0) ascale[0] = s;
     }
     for (int t = 1; t < M; t++) {
-        load_input<IN, R4>(a, t, K, in);
+        load_input<IN, R4>(x_in, norm_in, q_in, a.x_stride, t, K, in);
         const float s = quantise_to_b<FMT, IN, R4>(a, t, K, B, aux, dred, ured, in);
         if (tid == 0) ascale[t] = s;
     }
@@ -756,7 +761,7 @@ static fox_gpu_status fused_go_r(fox_gpu_ctx *ctx, FusedArgs a, int n_work)
         if (e != hipSuccess) return fox_hip_fail(e, "fused gemv: LDS size");
     }
     hipLaunchKernelGGL((gemv_fused<FMT, IN, EPI, R4>), dim3((unsigned)grid), dim3(FWG), lds,
-                       ctx->stream, a);
+                       ctx->stream, a.x, a.norm_w, a.q_in, a.nb, a);
     FOX_LAUNCHED("gemv_fused");
     return FOX_GPU_OK;
 }
