@@ -657,6 +657,7 @@ __global__ __launch_bounds__(64) void attn_values_x(const float *__restrict__ at
 #define SV_EXR (SV_LOADERS * 64)    // positions per exp round
 #define SV_EXP_PF 3                 // exp rounds whose scores are loaded up front
 #define SV_SPIN (1 << 22)
+#define SV_IDLE_SLEEP 4             // s_sleep units (64 clocks each) between idle polls
 
 // v of lane (quad base + sel) for each lane, sel from a quad_perm control
 // word known at compile time (DPP, no LDS traffic)
@@ -696,6 +697,21 @@ __device__ __forceinline__ bool sv_wait_ge(int *flag, int v)
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
             return true;
         }
+    }
+    return false;
+}
+
+// The same for waves that are not on the chains' critical path: a read every
+// few hundred cycles, so that their polling does not queue ahead of the
+// chain wave's LDS reads
+__device__ __forceinline__ bool sv_wait_ge_idle(int *flag, int v)
+{
+    for (int n = 0; n < SV_SPIN; n++) {
+        if (sv_peek(flag) >= v) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            return true;
+        }
+        __builtin_amdgcn_s_sleep(SV_IDLE_SLEEP);
     }
     return false;
 }
@@ -963,7 +979,7 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
     if (!loader) return;
 
     // ---- loaders: tile i = li, li + SV_LOADERS, ...
-    if (!sv_wait_ge(&a_ready, 1)) return;
+    if (!sv_wait_ge_idle(&a_ready, 1)) return;
     // a_j = e_j * (1/sum), or e_j where the sum is not positive
     // (src/ops.c:35-38; e * 1 is e exactly): the scale per head, and that of
     // the lane's own head for the DPP exchange below
@@ -992,7 +1008,7 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
                 vnext[DB ? k : 0] = v4[(size_t)jq * kvd];
             }
         }
-        if (i >= np && !sv_wait_ge(&consumed, i - np + 1)) return;
+        if (i >= np && !sv_wait_ge_idle(&consumed, i - np + 1)) return;
         float4 *P = ring + s * SV_QT * 64;
 #pragma unroll
         for (int k0 = 0; k0 < NLD; k0 += KC) {
