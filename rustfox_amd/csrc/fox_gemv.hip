@@ -209,11 +209,14 @@ __device__ __forceinline__ void gemv_block(const uint8_t *__restrict__ ch, int b
         uint4 qs = *(const uint4 *)(ch + 16 * lane);
         uint2 dd = *(const uint2 *)(ch + 1024 + 8 * g);
         const bool bok = j < M;
+        // (lanes past the M tokens read the last token's column, unused:
+        // with no lane-dependent branch the four B reads issue together)
+        const int jc = bok ? j : M - 1;
         uint32_t dw[4] = {qs.x, qs.y, qs.z, qs.w};
         v4i acc = zero;
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            v4i bv = load_b(B + ((((size_t)b * 4 + u) * 4 + g) * M + j) * 16, bok);
+            v4i bv = *(const v4i *)(B + ((((size_t)b * 4 + u) * 4 + g) * M + jc) * 16);
             uint32_t d = dw[u];
             acc = mfma(d & 0x03030303u, (d >> 2) & 0x03030303u, (d >> 4) & 0x03030303u,
                        (d >> 6) & 0x03030303u, bv, acc);
@@ -239,10 +242,11 @@ __device__ __forceinline__ void gemv_block(const uint8_t *__restrict__ ch, int b
         uint4 q0 = qp[0], q1 = qp[1];
         uint32_t dw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
         const bool bok = j < 2 * M;
+        const int jc = bok ? j : 2 * M - 1;                // (as for TQ2_0)
         v4i acc[4];
 #pragma unroll
         for (int p = 0; p < 4; p++) {
-            v4i bv = load_b(B + ((((size_t)b * 4 + p) * 4 + g) * (2 * M) + j) * 16, bok);
+            v4i bv = *(const v4i *)(B + ((((size_t)b * 4 + p) * 4 + g) * (2 * M) + jc) * 16);
             uint32_t a0 = dw[2 * p], a1 = dw[2 * p + 1];
             acc[p] = mfma(a0 & 0x0F0F0F0Fu, a1 & 0x0F0F0F0Fu, (a0 >> 4) & 0x0F0F0F0Fu,
                           (a1 >> 4) & 0x0F0F0F0Fu, bv, zero);
