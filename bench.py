@@ -193,7 +193,7 @@ def cpu_threads():
 
 def cpu_baseline(path, spec, budget_s):
     sys.path.insert(0, os.path.join(ROOT, "tests"))
-    from checkers import REF_FAST_SO, Ref  # test infrastructure: the reference
+    from oracle_libs import REF_FAST_SO, Ref  # test infrastructure: the reference
     threads = cpu_threads()
     if not os.path.exists(REF_FAST_SO):
         return None
@@ -241,8 +241,8 @@ def main():
     a = ap.parse_args()
 
     if a.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported "
-              "(the sharded design is described in DESIGN.md, not built)", file=sys.stderr)
+        print(f"bench.py: rustfox_amd runs on one GPU; --gpus {a.gpus} is not supported "
+              "(sharding is designed but not built)", file=sys.stderr)
         sys.exit(2)
 
     if a.gemv_only:

@@ -39,7 +39,7 @@ const char *fox_last_error(void);
 
 #define FOX_NAME_MAX 128
 
-/* include/fox/fox.h:213-224 (the ids this build reads) */
+/* include/fox/fox.h:213-224 (the ids rustfox_amd reads) */
 typedef enum {
     FOX_GGML_F32 = 0, FOX_GGML_F16 = 1, FOX_GGML_Q4_K = 12, FOX_GGML_Q6_K = 14,
     FOX_GGML_TQ1_0 = 34, FOX_GGML_TQ2_0 = 35
@@ -59,7 +59,7 @@ size_t      fox_row_bytes(fox_ggml_type type, size_t n_cols);
 
 typedef enum {
     FOX_WEIGHTS_RESIDENT = 0,   /* host memory, loaded on first touch        */
-    FOX_WEIGHTS_STREAM   = 1,   /* not provided by this build                */
+    FOX_WEIGHTS_STREAM   = 1,   /* not provided by rustfox_amd               */
     FOX_WEIGHTS_DEVICE   = 2    /* HBM of the GPU, loaded once per tensor    */
 } fox_weights_mode;
 

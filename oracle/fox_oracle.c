@@ -1,5 +1,5 @@
 /*
- * fox_oracle.c -- CPU restatement of RustFox's decode path (checker only).
+ * fox_oracle.c -- CPU restatement of RustFox's decode path (test oracle only).
  * See fox_oracle.h for scope, provenance and how each part is pinned.
  * Citations are file:line into the RustFox sources.
  */

@@ -1,7 +1,7 @@
 /*
  * fox_oracle.h -- CPU restatement of RustFox's per-token decode path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker: only tests/,
+ * TEST INFRASTRUCTURE ONLY.  This library is the oracle: only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, and
  * only to compute the expected answer.  Nothing in rustfox_amd/ links,
  * loads or calls it; the product path fails loudly when its HIP library is

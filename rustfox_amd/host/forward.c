@@ -129,7 +129,7 @@ fox_status fox_context_create(fox_model *m, const fox_context_config *cfg, fox_c
     *out = NULL;
     if (m->weights->mode != FOX_WEIGHTS_DEVICE)
         return fox_fail(FOX_ERR_UNSUPPORTED,
-                        "context: this build computes on the GPU; open the model with "
+                        "context: rustfox_amd computes on the GPU; open the model with "
                         "FOX_WEIGHTS_DEVICE");
     if (cfg) k = *cfg;
     else fox_context_config_default(&k, m);

@@ -222,7 +222,7 @@ fox_status fox_gguf_open(const char *path, fox_gguf **out)
         }
         if (!fox_type_layout((uint32_t)type, &block, &bytes)) {
             st = fox_fail(FOX_ERR_UNSUPPORTED, "gguf: tensor '%s' uses quantisation type %llu, "
-                          "which this build cannot lay out", t->name, (unsigned long long)type);
+                          "which rustfox_amd cannot lay out", t->name, (unsigned long long)type);
             goto fail;
         }
         if (elems % block) {

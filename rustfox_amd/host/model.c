@@ -175,7 +175,7 @@ fox_status fox_model_open(const char *gguf_path, fox_weights_mode mode,
 
     for (i = 0; i < g->n_tensors; i++) {
         if (!fox_gemv_supports((fox_ggml_type)g->tensors[i].type)) {
-            st = fox_fail(FOX_ERR_UNSUPPORTED, "model: tensor '%s' is %s and this build has no "
+            st = fox_fail(FOX_ERR_UNSUPPORTED, "model: tensor '%s' is %s and rustfox_amd has no "
                           "device kernel for it", g->tensors[i].name,
                           fox_ggml_type_name((fox_ggml_type)g->tensors[i].type));
             goto fail;

@@ -15,13 +15,13 @@ def pytest_configure(config):
 
 @pytest.fixture(scope="session")
 def oracle():
-    from checkers import Oracle
+    from oracle_libs import Oracle
     return Oracle()
 
 
 @pytest.fixture(scope="session")
 def ref():
-    from checkers import Ref, ref_available
+    from oracle_libs import Ref, ref_available
     if not ref_available():
         pytest.skip("oracle/_ref was not built (the reference sources were absent)")
     return Ref()

@@ -27,7 +27,7 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.dirname(HERE))
 
-from checkers import Ref  # noqa: E402
+from oracle_libs import Ref  # noqa: E402
 from rustfox_amd import synth  # noqa: E402
 
 TYPES = {"tq1_0": 34, "tq2_0": 35, "q4_k": 12, "q6_k": 14, "f16": 1}

@@ -1,4 +1,4 @@
-"""ctypes bindings of the two checkers used by the tests.
+"""ctypes bindings of the two oracle libraries used by the tests.
 
   Oracle  -- oracle/liboracle.so, this repository's C restatement of the
              RustFox decode path (oracle/fox_oracle.c).

@@ -3,7 +3,7 @@
 Checked against the reference compiled from its own sources (oracle/_ref)
 when it is present, else against the oracle (whose forward pass equals the
 reference's bit for bit, tests/test_oracle.py).  With exact attention (the
-default) logits must be bit-identical to the checker's (the 1e-3 relative L2
+default) logits must be bit-identical to the oracle's (the 1e-3 relative L2
 bound is met with zero error); split (flash-decoding) attention is checked
 only against gross error.  Greedy token sequences
 must be identical over 64 steps; batched == stepped and decode_greedy ==
@@ -34,9 +34,9 @@ def rel_l2(a, b):
     return float(np.linalg.norm(a.astype(np.float64) - b) / max(np.linalg.norm(b), 1e-30))
 
 
-def checker_run(oracle, spec, tensors, path, prompt, steps, n_ctx, kv=None):
-    """Prompt logits and greedy ids from the CPU checker."""
-    from checkers import Ref, ref_available
+def oracle_run(oracle, spec, tensors, path, prompt, steps, n_ctx, kv=None):
+    """Prompt logits and greedy ids from the CPU oracle."""
+    from oracle_libs import Ref, ref_available
     if ref_available() and kv is None:
         r = Ref()
         m = r.open_model(path)
@@ -88,7 +88,7 @@ def test_tiny_model_greedy_64(tiny_models, oracle, name, mode):
     s, t, p = tiny_models[name]
     print(f"case greedy64 {name} {mode}", flush=True)
     prompt = synth.prompt_ids(16, s.n_vocab)
-    want_first, want_ids = checker_run(oracle, s, t, p, prompt, 64, 96)
+    want_first, want_ids = oracle_run(oracle, s, t, p, prompt, 64, 96)
     with rf.Model(p) as m:
         ctx = m.context(96)
         ctx.set_attention(mode == "exact")
@@ -254,7 +254,7 @@ def test_reference_forward_fixture(tmp_path):
             stepped = ctx.eval([tok])
         assert np.array_equal(batched.view(np.uint32), stepped.view(np.uint32))
         ctx.close()
-    from checkers import Ref, ref_available
+    from oracle_libs import Ref, ref_available
     if ref_available():
         r = Ref()
         rm = r.open_model(p)

@@ -1,4 +1,4 @@
-"""Pin the oracle (oracle/fox_oracle.c) before trusting it as the checker.
+"""Pin the oracle (oracle/fox_oracle.c) before trusting it to judge the GPU path.
 
 Each function is checked by something that would catch a plausible mistake
 (a dropped term, a wrong index, a transposed operand):
