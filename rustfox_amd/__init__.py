@@ -302,6 +302,11 @@ class Gpu:
         _check(self.lib.fox_gpu_gate_up_silu(self.ctx, wg.h, wu.h, x.ptr, K, M, norm.ptr, eps,
                                              h.ptr, ff))
 
+    def rmsnorm(self, out: DeviceArray, x: DeviceArray, w: DeviceArray, n, M, eps,
+                out_stride=None, x_stride=None):
+        _check(self.lib.fox_gpu_rmsnorm(self.ctx, out.ptr, out_stride or n, x.ptr, x_stride or n,
+                                        w.ptr if w else None, n, M, eps))
+
     def argmax(self, logits: DeviceArray, n, idx: DeviceArray, pos: DeviceArray = None,
                advance=0, history: DeviceArray = None):
         _check(self.lib.fox_gpu_argmax(self.ctx, logits.ptr, n, idx.ptr, pos.ptr if pos else None,

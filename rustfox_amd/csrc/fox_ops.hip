@@ -81,6 +81,24 @@ __device__ __forceinline__ double rms_scale_d(double ss, int n, float eps)
     return 1.0 / __builtin_sqrt(ss / (double)n + (double)eps);
 }
 
+// the float scale from the tree sum tot of the squares of x[0 .. n) (one
+// thread calls it; the rare undecided case rereads x in index order)
+__device__ float rms_scale_f(double tot, const float *xt, int n, float eps)
+{
+    const double rel = (double)(n + 64) * 0x1p-52;
+    const double y_hi = rms_scale_d(tot * (1.0 - rel), n, eps) * (1.0 + 0x1p-50);
+    const double y_lo = rms_scale_d(tot * (1.0 + rel), n, eps) * (1.0 - 0x1p-50);
+    const float f_hi = (float)y_hi, f_lo = (float)y_lo;
+    if (f_hi == f_lo) return f_hi;
+    double seq = 0.0;
+    for (int i = 0; i < n; i++) seq += (double)xt[i] * (double)xt[i];
+    return (float)rms_scale_d(seq, n, eps);
+}
+
+// R > 0: n <= 256 R, and each thread holds its R values of x (and w) in
+// registers, every load issued before the first use (one memory round trip
+// instead of one per loop step).  R = 0: any n, strided loops.
+template <int R>
 __global__ __launch_bounds__(256) void rmsnorm_k(float *__restrict__ out, size_t out_stride,
                                                  const float *__restrict__ x, size_t x_stride,
                                                  const float *__restrict__ w, int n, float eps)
@@ -89,31 +107,43 @@ __global__ __launch_bounds__(256) void rmsnorm_k(float *__restrict__ out, size_t
     __shared__ float sc;
     const int t = blockIdx.x, tid = threadIdx.x;
     const float *xt = x + (size_t)t * x_stride;
+    float *ot = out + (size_t)t * out_stride;
+    constexpr int RR = R > 0 ? R : 1;
+    float xv[RR], wv[RR];
     double s = 0.0;
-    for (int i = tid; i < n; i += 256) s += (double)xt[i] * (double)xt[i];
+    if (R > 0) {
+#pragma unroll
+        for (int r = 0; r < RR; r++) {
+            const int i = tid + 256 * r, ic = i < n ? i : n - 1;
+            xv[r] = xt[ic];
+            wv[r] = w ? w[ic] : 1.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < RR; r++)
+            if (tid + 256 * r < n) s += (double)xv[r] * (double)xv[r];
+    } else {
+        for (int i = tid; i < n; i += 256) s += (double)xt[i] * (double)xt[i];
+    }
     s = wave_sum_d(s);
     if ((tid & 63) == 0) red[tid >> 6] = s;
     __syncthreads();
-    if (tid == 0) {
-        const double tot = (red[0] + red[1]) + (red[2] + red[3]);
-        const double rel = (double)(n + 64) * 0x1p-52;
-        const double y_hi = rms_scale_d(tot * (1.0 - rel), n, eps) * (1.0 + 0x1p-50);
-        const double y_lo = rms_scale_d(tot * (1.0 + rel), n, eps) * (1.0 - 0x1p-50);
-        float f_hi = (float)y_hi, f_lo = (float)y_lo;
-        if (f_hi == f_lo) {
-            sc = f_hi;
-        } else {
-            double seq = 0.0;
-            for (int i = 0; i < n; i++) seq += (double)xt[i] * (double)xt[i];
-            sc = (float)rms_scale_d(seq, n, eps);
-        }
-    }
+    if (tid == 0) sc = rms_scale_f((red[0] + red[1]) + (red[2] + red[3]), xt, n, eps);
     __syncthreads();
     const float scale = sc;
-    float *ot = out + (size_t)t * out_stride;
-    for (int i = tid; i < n; i += 256) {
-        float v = xt[i] * scale;
-        ot[i] = w ? v * w[i] : v;
+    if (R > 0) {
+#pragma unroll
+        for (int r = 0; r < RR; r++) {
+            const int i = tid + 256 * r;
+            if (i < n) {
+                const float v = xv[r] * scale;
+                ot[i] = w ? v * wv[r] : v;
+            }
+        }
+    } else {
+        for (int i = tid; i < n; i += 256) {
+            const float v = xt[i] * scale;
+            ot[i] = w ? v * w[i] : v;
+        }
     }
 }
 
@@ -125,8 +155,17 @@ extern "C" fox_gpu_status fox_gpu_rmsnorm(fox_gpu_ctx *ctx, float *out, size_t o
         return fox_fail(FOX_GPU_ERR_ARG, "rmsnorm: bad argument");
     if (M > 1 && (out_stride < n || x_stride < n))
         return fox_fail(FOX_GPU_ERR_ARG, "rmsnorm: stride < n");
-    hipLaunchKernelGGL(rmsnorm_k, dim3((unsigned)M), dim3(256), 0, ctx->stream, out,
-                       M > 1 ? out_stride : n, x, M > 1 ? x_stride : n, w, (int)n, eps);
+    const size_t r = (n + 255) / 256;
+    const void *k = r <= 2 ? (const void *)rmsnorm_k<2> : r <= 4 ? (const void *)rmsnorm_k<4>
+                  : r <= 6 ? (const void *)rmsnorm_k<6> : r <= 8 ? (const void *)rmsnorm_k<8>
+                  : r <= 10 ? (const void *)rmsnorm_k<10> : r <= 12 ? (const void *)rmsnorm_k<12>
+                  : r <= 16 ? (const void *)rmsnorm_k<16> : (const void *)rmsnorm_k<0>;
+    size_t os = M > 1 ? out_stride : n, xs = M > 1 ? x_stride : n;
+    int in = (int)n;
+    void *args[] = {(void *)&out, (void *)&os, (void *)&x, (void *)&xs, (void *)&w, (void *)&in,
+                    (void *)&eps};
+    hipError_t e = hipLaunchKernel(k, dim3((unsigned)M), dim3(256), args, 0, ctx->stream);
+    if (e != hipSuccess) return fox_hip_fail(e, "rmsnorm");
     FOX_LAUNCHED("rmsnorm");
     return FOX_GPU_OK;
 }
@@ -1240,6 +1279,7 @@ extern "C" fox_gpu_status fox_gpu_add(fox_gpu_ctx *ctx, float *dst, const float 
 // the history entry and the advanced position, and resets the counter.
 #define AM_THREADS 256
 #define AM_MAX_WG 256
+#define AM_UNROLL 8
 
 __device__ __forceinline__ void am_merge(float &best, int &bidx, float ov, int oi)
 {
@@ -1264,11 +1304,22 @@ __global__ __launch_bounds__(AM_THREADS) void argmax_k(const float *__restrict__
     const int i0 = blockIdx.x * per, i1 = min(n, i0 + per);
     float best = -INFINITY;
     int bidx = 0x7fffffff;
-    for (int i = i0 + tid; i < i1; i += AM_THREADS) {
-        const float v = x[i];
-        if (v > best) {
-            best = v;
-            bidx = i;
+    // a thread's values in index order, AM_UNROLL loads issued before the
+    // first comparison
+    for (int b0 = i0; b0 < i1; b0 += AM_THREADS * AM_UNROLL) {
+        float v[AM_UNROLL];
+#pragma unroll
+        for (int k = 0; k < AM_UNROLL; k++) {
+            const int i = b0 + tid + k * AM_THREADS;
+            v[k] = x[i < i1 ? i : i1 - 1];
+        }
+#pragma unroll
+        for (int k = 0; k < AM_UNROLL; k++) {
+            const int i = b0 + tid + k * AM_THREADS;
+            if (i < i1 && v[k] > best) {
+                best = v[k];
+                bidx = i;
+            }
         }
     }
 #pragma unroll

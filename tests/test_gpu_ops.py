@@ -4,6 +4,8 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
+EPS = 1e-6
+
 
 def _argmax_cases():
     rng = np.random.default_rng(11)
@@ -37,3 +39,30 @@ def test_argmax_follows_the_reference(gpu, oracle, name):
     want = oracle.argmax(x)
     assert int(idx.numpy()[0]) == want
     assert int(pos.numpy()[0]) == 4 and int(hist.numpy()[3]) == want
+
+
+# sizes that reach every register-held variant of the kernel (256 R >= n for
+# R = 2 .. 16) and the strided loop past 4096
+_RMS_N = [1, 7, 288, 512, 1000, 1536, 2048, 2560, 3072, 4096, 4097, 9728]
+
+
+@pytest.mark.parametrize("n", _RMS_N)
+def test_rmsnorm_bit_exact(gpu, oracle, n):
+    """src/ops.c:7-22 (double sum of squares in index order, two float
+    roundings): three rows at a padded stride, with and without weights."""
+    rng = np.random.default_rng(n)
+    M, stride = 3, n + 5
+    x = np.zeros((M, stride), np.float32)
+    x[:, :n] = rng.standard_normal((M, n)).astype(np.float32) * np.float32(3.0)
+    x[1, :n] *= np.float32(1e-3)                       # a small-norm row
+    w = (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    dx, dw = gpu.array(x), gpu.array(w)
+    for weighted in (True, False):
+        dout = gpu.array(np.full((M, stride), 7.0, np.float32))
+        gpu.rmsnorm(dout, dx, dw if weighted else None, n, M, EPS, stride, stride)
+        gpu.sync()
+        got = dout.numpy()
+        for t in range(M):
+            want = oracle.rmsnorm(x[t, :n], w if weighted else np.ones(n, np.float32), EPS)
+            assert np.array_equal(got[t, :n].view(np.uint32), want.view(np.uint32)), (t, weighted)
+            assert np.all(got[t, n:] == 7.0)           # nothing past n is written
