@@ -832,16 +832,10 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
     const bool loader = (wave & 3) != 0;     // waves on SIMD 0 do not load
     const int li = wave - 1 - (wave >> 2);
     float4 vcur[NLD], vnext[DB ? NLD : 1];
-    if (loader && li < ntile) {
-#pragma unroll
-        for (int k = 0; k < NLD; k++) {
-            const int jq = min(li * SV_QT + k * G + lq, nq_all - 1);
-            vcur[k] = v4[(size_t)jq * kvd];
-        }
-    }
 
-    // scores of the first SV_EXP_PF exp rounds, loaded now: their latency
-    // overlaps the head maxima
+    // scores of the first SV_EXP_PF exp rounds, loaded first: a wave's loads
+    // complete in order, and these are needed as soon as the maxima are
+    // known, the V tiles only after the softmax sum
     const int ex0 = li * 64 + lane;                 // loader's position in a round
     float sc[SV_EXP_PF][G];
     if (loader) {
@@ -853,23 +847,34 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
                 sc[k][gg] = srow[(size_t)gg * att_stride + (p < upto ? p : 0)];
         }
     }
-
-    // ---- head maxima (src/ops.c:26-30: a NaN first score stays the max)
-    if (wave < G) {
-        const float *tm = tmax + ((size_t)t * n_head + (size_t)kvh * G + wave) * n_tiles;
-        const int used = (upto + SC_TILE - 1) / SC_TILE;
-        float m = -INFINITY;
-        for (int i = lane; i < used; i += 64) {
-            const float v = tm[i];
-            m = v > m ? v : m;
-        }
+    if (loader && li < ntile) {
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float w = __shfl_xor(m, o);
-            m = w > m ? w : m;
+        for (int k = 0; k < NLD; k++) {
+            const int jq = min(li * SV_QT + k * G + lq, nq_all - 1);
+            vcur[k] = v4[(size_t)jq * kvd];
         }
-        const float s0 = srow[(size_t)wave * att_stride];
-        if (lane == 0) mx_s[wave] = s0 != s0 ? s0 : m;
+    }
+
+    // ---- head maxima (src/ops.c:26-30: a NaN first score stays the max),
+    // by the waves that load no V (wave 4 n takes heads n, n + 4): their
+    // tile-maximum loads are not queued behind V loads
+    if (!loader) {
+        for (int hg = wave >> 2; hg < G; hg += 4) {
+            const float *tm = tmax + ((size_t)t * n_head + (size_t)kvh * G + hg) * n_tiles;
+            const int used = (upto + SC_TILE - 1) / SC_TILE;
+            float m = -INFINITY;
+            for (int i = lane; i < used; i += 64) {
+                const float v = tm[i];
+                m = v > m ? v : m;
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const float w = __shfl_xor(m, o);
+                m = w > m ? w : m;
+            }
+            const float s0 = srow[(size_t)hg * att_stride];
+            if (lane == 0) mx_s[hg] = s0 != s0 ? s0 : m;
+        }
     }
     if (tid < SV_NP_MAX) ready[tid] = -1;
     if (tid < 32) tab[tid] = fox_exp2_tab[tid];
