@@ -138,6 +138,13 @@ void       fox_context_reset(fox_context *ctx);
  * eval or destroy (src/forward.c:411-438) */
 fox_status fox_eval(fox_context *ctx, const uint32_t *tokens, size_t n_tokens,
                     float **logits_out);
+/* EXTENSION.  The logits of every one of the n_tokens positions, row i
+ * those of token i (as fox_eval would return after tokens[0..i]), into
+ * caller-owned host memory of n_tokens * n_vocab floats: speculative
+ * verification checks all drafted positions in one pass.  RustFox computes
+ * the last position's only (src/forward.c:401-408). */
+fox_status fox_eval_all(fox_context *ctx, const uint32_t *tokens, size_t n_tokens,
+                        float *logits);
 uint32_t   fox_context_position(const fox_context *ctx);
 double     fox_context_last_eval_seconds(const fox_context *ctx);
 uint64_t   fox_context_weight_reads(const fox_context *ctx);

@@ -397,6 +397,7 @@ def host_lib() -> C.CDLL:
         "fox_context_destroy": ([vp], None),
         "fox_context_reset": ([vp], None),
         "fox_eval": ([vp, u32p, sz, C.POINTER(C.POINTER(C.c_float))], C.c_int),
+        "fox_eval_all": ([vp, u32p, sz, C.POINTER(C.c_float)], C.c_int),
         "fox_decode_greedy": ([vp, u32, sz, u32p], C.c_int),
         "fox_context_position": ([vp], u32),
         "fox_context_last_eval_seconds": ([vp], C.c_double),
@@ -501,6 +502,14 @@ class Context:
         lp = C.POINTER(C.c_float)()
         _hcheck(self.lib.fox_eval(self.ctx, t, t.size, C.byref(lp)))
         return np.ctypeslib.as_array(lp, shape=(self.model.info.n_vocab,)).copy()
+
+    def eval_all(self, tokens) -> np.ndarray:
+        """Logits of every position, one row per token."""
+        t = np.ascontiguousarray(np.atleast_1d(tokens), dtype=np.uint32)
+        out = np.empty((t.size, self.model.info.n_vocab), np.float32)
+        _hcheck(self.lib.fox_eval_all(self.ctx, t, t.size,
+                                      out.ctypes.data_as(C.POINTER(C.c_float))))
+        return out
 
     def decode_greedy(self, token: int, n_steps: int) -> np.ndarray:
         out = np.zeros(n_steps, np.uint32)

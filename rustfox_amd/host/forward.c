@@ -171,7 +171,7 @@ fox_status fox_context_create(fox_model *m, const fox_context_config *cfg, fox_c
     ALLOC(c->v, nb * c->nkv * 4)
     ALLOC(c->hb, nb * c->ff * 4)
     ALLOC(c->hb2, nb * c->ff * 4)
-    ALLOC(c->dlogits, c->vocab * 4)
+    ALLOC(c->dlogits, nb * c->vocab * 4)          /* nb rows for fox_eval_all */
     ALLOC(c->kc, (size_t)mi->n_layer * k.n_ctx * c->nkv * 4)
     ALLOC(c->vc, (size_t)mi->n_layer * FOX_GPU_V_CACHE_FLOATS(k.n_ctx, c->nkv) * 4)
     ALLOC(c->rc, (size_t)k.n_ctx * (c->hd / 2) * 4)
@@ -289,7 +289,9 @@ static fox_status project_group(fox_context *c, size_t n, const fox_gpu_tensor *
 }
 
 /* one pass over all layers for M <= FOX_GPU_MAX_TOKENS tokens already in
- * dtok, at the position held in dpos; queued on the stream, no host sync */
+ * dtok, at the position held in dpos; queued on the stream, no host sync.
+ * want_logits: 0 none, 1 the last token's (dlogits row 0), 2 every token's
+ * (dlogits rows 0 .. M-1) */
 static fox_status forward_pass(fox_context *c, size_t M, int want_logits)
 {
     const fox_model_info *mi = &c->m->info;
@@ -346,10 +348,15 @@ static fox_status forward_pass(fox_context *c, size_t M, int want_logits)
                          FOX_GPU_GEMV_ACCUMULATE), "forward: ffn_down");
     }
     if (!want_logits) return FOX_OK;
-    GPU(fox_gpu_rmsnorm(c->gpu, c->xb, c->wide, c->x + (M - 1) * c->d, c->d, c->out_norm, c->d,
-                        1, mi->rms_eps), "forward: output_norm");
-    GPU(fox_gpu_gemv(c->gpu, c->out, c->xb, c->wide, 1, c->dlogits, c->vocab, 0),
-        "forward: output");
+    {
+        /* src/forward.c:401-408 on the last row, or on every row: each row's
+         * norm and head product are independent of the others */
+        const size_t rows = want_logits == 2 ? M : 1;
+        GPU(fox_gpu_rmsnorm(c->gpu, c->xb, c->wide, c->x + (M - rows) * c->d, c->d, c->out_norm,
+                            c->d, rows, mi->rms_eps), "forward: output_norm");
+        GPU(fox_gpu_gemv(c->gpu, c->out, c->xb, c->wide, rows, c->dlogits, c->vocab, 0),
+            "forward: output");
+    }
     return FOX_OK;
 }
 
@@ -363,13 +370,14 @@ static fox_status check_tokens(const fox_context *c, const uint32_t *t, size_t n
     return FOX_OK;
 }
 
-fox_status fox_eval(fox_context *c, const uint32_t *tokens, size_t n, float **logits_out)
+/* tokens in chunks of at most n_batch (and FOX_GPU_MAX_TOKENS); all == NULL:
+ * the last token's logits into c->logits, else every token's into all */
+static fox_status eval_chunks(fox_context *c, const uint32_t *tokens, size_t n, float *all)
 {
     size_t done = 0;
     double t0;
     fox_status st;
 
-    if (!c || !tokens || n == 0) return fox_fail(FOX_ERR_ARG, "eval: nothing to evaluate");
     t0 = now_s();
     c->reads_at_start = fox_weights_reads(c->m->weights);
     while (done < n) {
@@ -384,14 +392,32 @@ fox_status fox_eval(fox_context *c, const uint32_t *tokens, size_t n, float **lo
         if ((st = check_tokens(c, tokens + done, chunk)) != FOX_OK) return st;
         GPU(fox_gpu_memcpy_h2d(c->gpu, c->dtok, tokens + done, chunk * 4), "eval: tokens");
         GPU(fox_gpu_memcpy_h2d(c->gpu, c->dpos, &c->pos, 4), "eval: position");
-        if ((st = forward_pass(c, chunk, last)) != FOX_OK) return st;
+        if ((st = forward_pass(c, chunk, all ? 2 : last)) != FOX_OK) return st;
+        if (all)
+            GPU(fox_gpu_memcpy_d2h(c->gpu, all + done * c->vocab, c->dlogits,
+                                   chunk * c->vocab * 4), "eval: logits");
         c->pos += (uint32_t)chunk;
         done += chunk;
     }
-    GPU(fox_gpu_memcpy_d2h(c->gpu, c->logits, c->dlogits, c->vocab * 4), "eval: logits");
+    if (!all) GPU(fox_gpu_memcpy_d2h(c->gpu, c->logits, c->dlogits, c->vocab * 4), "eval: logits");
     c->last_seconds = now_s() - t0;
+    return FOX_OK;
+}
+
+fox_status fox_eval(fox_context *c, const uint32_t *tokens, size_t n, float **logits_out)
+{
+    fox_status st;
+    if (!c || !tokens || n == 0) return fox_fail(FOX_ERR_ARG, "eval: nothing to evaluate");
+    if ((st = eval_chunks(c, tokens, n, NULL)) != FOX_OK) return st;
     if (logits_out) *logits_out = c->logits;
     return FOX_OK;
+}
+
+fox_status fox_eval_all(fox_context *c, const uint32_t *tokens, size_t n, float *logits)
+{
+    if (!c || !tokens || n == 0 || !logits)
+        return fox_fail(FOX_ERR_ARG, "eval_all: nothing to evaluate");
+    return eval_chunks(c, tokens, n, logits);
 }
 
 /* one greedy step: forward at dpos with the token in dtok[0], then

@@ -125,6 +125,22 @@ def test_batched_equals_stepped(tiny_models):
     assert np.array_equal(batched.view(np.uint32), stepped.view(np.uint32))
 
 
+def test_eval_all_equals_stepped(tiny_models):
+    """fox_eval_all over 7 tokens in chunks of 3 (3, 3, 1): row i is
+    bit-identical to the logits of a single-token eval after tokens 0..i
+    (each position's norm and head product are independent of the batch)."""
+    s, t, p = tiny_models["tiny-512"]
+    prompt = np.array([3, 1, 4, 1, 5, 9, 2], np.uint32)
+    with rf.Model(p) as m:
+        ctx = m.context(64, n_batch=3)
+        rows = ctx.eval_all(prompt)
+        assert ctx.position == 7 and rows.shape == (7, m.info.n_vocab)
+        ctx.reset()
+        stepped = np.stack([ctx.eval([tok]) for tok in prompt])
+        ctx.close()
+    assert np.array_equal(rows.view(np.uint32), stepped.view(np.uint32))
+
+
 def test_decode_greedy_equals_eval_argmax(tiny_models):
     """The captured-graph greedy loop is the same computation as eval +
     first argmax on the host (src/sample.c:147-153)."""
