@@ -696,7 +696,7 @@ __global__ __launch_bounds__(64) void attn_values_x(const float *__restrict__ at
 #define SV_EXR (SV_LOADERS * 64)    // positions per exp round
 #define SV_EXP_PF 3                 // exp rounds whose scores are loaded up front
 #define SV_SPIN (1 << 22)
-#define SV_IDLE_SLEEP 4             // s_sleep units (64 clocks each) between idle polls
+#define SV_IDLE_SLEEP 2             // s_sleep units (64 clocks each) between idle polls
 
 // v of lane (quad base + sel) for each lane, sel from a quad_perm control
 // word known at compile time (DPP, no LDS traffic)
