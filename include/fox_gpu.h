@@ -67,6 +67,14 @@ const char    *fox_gpu_last_error(void);
 const char    *fox_gpu_status_str(fox_gpu_status s);
 fox_gpu_status fox_gpu_device_info(fox_gpu_ctx *ctx, char *name, size_t cap,
                                    int *compute_units, uint64_t *hbm_bytes);
+/* Upper bound on the persistent grid of the fused GEMVs (fox_gpu_gemv,
+ * _gemv_rmsnorm, _qkv_rope, _gate_up_silu on ternary weights); 0, the
+ * default, means two workgroups per compute unit.  A small bound makes
+ * every workgroup walk many row tiles in turn: results are unchanged
+ * (each output row is combined by one workgroup in block order), only the
+ * speed differs.  No counterpart in RustFox: the CPU pool's thread count
+ * (src/threadpool.c:76) plays this role there. */
+fox_gpu_status fox_gpu_set_max_workgroups(fox_gpu_ctx *ctx, int n);
 
 /* ------------------------------------------------------------- memory */
 

@@ -115,7 +115,8 @@ typedef struct fox_model   fox_model;
 typedef struct fox_context fox_context;
 
 /* include/fox/fox.h:425-431.  The GPU is HIP device FOX_DEVICE (environment,
- * default 0). */
+ * default 0).  FOX_MAX_WORKGROUPS=n (environment) caps the fused GEMVs'
+ * persistent grid (fox_gpu_set_max_workgroups); results do not change. */
 fox_status fox_model_open(const char *gguf_path, fox_weights_mode mode,
                           uint64_t budget_bytes, fox_model **out);
 void       fox_model_close(fox_model *m);

@@ -54,6 +54,7 @@ def gpu_lib() -> C.CDLL:
         "fox_gpu_init": [C.c_int, C.POINTER(vp)],
         "fox_gpu_shutdown": [vp],
         "fox_gpu_device_info": [vp, C.c_char_p, sz, C.POINTER(C.c_int), C.POINTER(C.c_uint64)],
+        "fox_gpu_set_max_workgroups": [vp, C.c_int],
         "fox_gpu_malloc": [vp, sz, C.POINTER(vp)],
         "fox_gpu_free": [vp, vp],
         "fox_gpu_memcpy_h2d": [vp, vp, vp, sz],
@@ -218,6 +219,10 @@ class Gpu:
 
     def __exit__(self, *a):
         self.close()
+
+    def set_max_workgroups(self, n: int):
+        """Cap the fused GEMVs' persistent grid (0: two per compute unit)."""
+        _check(self.lib.fox_gpu_set_max_workgroups(self.ctx, n))
 
     def info(self):
         name = C.create_string_buffer(128)

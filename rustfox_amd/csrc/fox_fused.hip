@@ -750,7 +750,8 @@ template <int FMT, int IN, int EPI, int R4>
 static fox_gpu_status fused_go_r(fox_gpu_ctx *ctx, FusedArgs a, int n_work)
 {
     a.n_work = n_work;
-    const int cap = 2 * (ctx->n_cu > 0 ? ctx->n_cu : 1);
+    int cap = 2 * (ctx->n_cu > 0 ? ctx->n_cu : 1);
+    if (ctx->max_wg > 0 && ctx->max_wg < cap) cap = ctx->max_wg;
     const int grid = n_work < cap ? n_work : cap;
     a.n_per = n_work / grid;
     a.n_rem = n_work - a.n_per * grid;
@@ -903,10 +904,12 @@ extern "C" fox_gpu_status fox_gpu_qkv_rope(fox_gpu_ctx *ctx, const fox_gpu_tenso
     if (!ctx || !wq || !wk || !wv || !x || !norm_w || !q_out || !cos_t || !sin_t || !pos ||
         !k_cache || !v_cache || head_dim == 0 || n_ctx == 0)
         return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: bad argument");
-    if (wq->type != wk->type || wk->type != wv->type || wq->ne0 != wk->ne0 ||
-        wk->ne0 != wv->ne0 || wk->ne1 != wv->ne1)
-        return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: q, k, v must share type and width, k and v "
+    if (wq->ne0 != wk->ne0 || wk->ne0 != wv->ne0 || wk->ne1 != wv->ne1)
+        return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: q, k, v must share their width, k and v "
                         "their rows");
+    if (wq->type != wk->type || wk->type != wv->type)   // (a Q4_K_M-style mix: separate steps)
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "qkv_rope: q, k, v of different types take "
+                        "the separate steps");
     if (head_dim % 2 || wq->ne1 % head_dim || wk->ne1 % head_dim)
         return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: rows are not whole heads of even size");
     const size_t K = (size_t)wq->ne0;
@@ -958,8 +961,11 @@ extern "C" fox_gpu_status fox_gpu_gate_up_silu(fox_gpu_ctx *ctx, const fox_gpu_t
 {
     if (!ctx || !wg || !wu || !x || !norm_w || !h_out)
         return fox_fail(FOX_GPU_ERR_ARG, "gate_up_silu: bad argument");
-    if (wg->type != wu->type || wg->ne0 != wu->ne0 || wg->ne1 != wu->ne1)
-        return fox_fail(FOX_GPU_ERR_ARG, "gate_up_silu: gate and up must have one shape and type");
+    if (wg->ne0 != wu->ne0 || wg->ne1 != wu->ne1)
+        return fox_fail(FOX_GPU_ERR_ARG, "gate_up_silu: gate and up must have one shape");
+    if (wg->type != wu->type)
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "gate_up_silu: gate and up of different types "
+                        "take the separate steps");
     const size_t K = (size_t)wg->ne0;
     if (M > 1 && (x_stride < K || h_stride < wg->ne1))
         return fox_fail(FOX_GPU_ERR_ARG, "gate_up_silu: stride too small");

@@ -107,6 +107,13 @@ extern "C" void fox_gpu_shutdown(fox_gpu_ctx *ctx)
     delete ctx;
 }
 
+extern "C" fox_gpu_status fox_gpu_set_max_workgroups(fox_gpu_ctx *ctx, int n)
+{
+    if (!ctx || n < 0) return fox_fail(FOX_GPU_ERR_ARG, "set_max_workgroups: bad argument");
+    ctx->max_wg = n;
+    return FOX_GPU_OK;
+}
+
 extern "C" fox_gpu_status fox_gpu_device_info(fox_gpu_ctx *ctx, char *name, size_t cap,
                                               int *compute_units, uint64_t *hbm_bytes)
 {

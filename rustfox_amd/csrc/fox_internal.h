@@ -51,6 +51,9 @@ struct fox_gpu_ctx {
     int device;
     hipStream_t stream;
     int n_cu;
+    // upper bound on the persistent grid of the fused GEMV (0: two
+    // workgroups per compute unit); fox_gpu_set_max_workgroups
+    int max_wg;
     uint64_t hbm_bytes;
     char name[128];
     // activation workspace (quantised values, B operands, corrections)

@@ -67,11 +67,14 @@ fox_status fox_weights_open(const char *gguf_path, fox_weights_mode mode,
     }
     if (mode == FOX_WEIGHTS_DEVICE) {
         fox_gpu_status gs = fox_gpu_init(device_ordinal(), &w->gpu);
+        const char *mw = getenv("FOX_MAX_WORKGROUPS");
         if (gs != FOX_GPU_OK) {
             st = fox_gpu_failed(gs, "weights: no usable GPU for FOX_WEIGHTS_DEVICE");
             fox_weights_close(w);
             return st;
         }
+        /* a cap on the fused GEMVs' persistent grid (results unchanged) */
+        if (mw && *mw) fox_gpu_set_max_workgroups(w->gpu, atoi(mw));
     }
     pthread_mutex_init(&w->lock, NULL);
     *out = w;

@@ -261,36 +261,82 @@ def tensor_list(s: ModelSpec):
     return out
 
 
-def make_tensor(s: ModelSpec, index: int, name: str, ne0: int, ne1: int,
-                gtype: int) -> np.ndarray:
-    """Bytes of one tensor.  Norms are 1.0; f16 matrices ~ N(0, 0.02);
-    ternary matrices uniform trits with d ~ U(0.01, 0.05); K-quants quantise
-    N(0, 0.02) weights with the quantisers above."""
-    rng = np.random.default_rng([s.seed, index])
+# Tensors above this many elements are generated in row ranges, each range
+# from its own stream (seed, tensor index, first row), so that ranges can be
+# produced in parallel processes; smaller tensors come from one stream
+# (seed, tensor index).
+CHUNK_ELEMS = 1 << 25
+
+
+def _chunk_rows(ne0: int) -> int:
+    return max(1, (1 << 22) // ne0)
+
+
+def tensor_chunks(ne0: int, ne1: int):
+    """Row ranges [(r0, r1)] a tensor is generated in (one range when small)."""
     rows = max(ne1, 1)
+    if rows * ne0 <= CHUNK_ELEMS:
+        return [(0, rows)]
+    step = _chunk_rows(ne0)
+    return [(r0, min(rows, r0 + step)) for r0 in range(0, rows, step)]
+
+
+def _gen_rows(rng, name, ne0, nrows, gtype):
     if name.endswith("norm.weight"):
-        return np.ones(ne0, dtype=np.float32).view(np.uint8)
+        return np.ones(ne0 * nrows, dtype=np.float32).view(np.uint8)
     if gtype == F16:
-        w = rng.standard_normal((rows, ne0), dtype=np.float32) * np.float32(0.02)
+        w = rng.standard_normal((nrows, ne0), dtype=np.float32) * np.float32(0.02)
         return w.astype(np.float16).view(np.uint8).reshape(-1)
     if gtype == F32:
-        w = rng.standard_normal((rows, ne0), dtype=np.float32) * np.float32(0.02)
+        w = rng.standard_normal((nrows, ne0), dtype=np.float32) * np.float32(0.02)
         return w.view(np.uint8).reshape(-1)
     if gtype == TQ1_0:
-        return tq1_random(rng, rows * ne0 // 256).reshape(-1)
+        return tq1_random(rng, nrows * ne0 // 256).reshape(-1)
     if gtype == TQ2_0:
-        return tq2_random(rng, rows * ne0 // 256).reshape(-1)
+        return tq2_random(rng, nrows * ne0 // 256).reshape(-1)
     if gtype in (Q4_K, Q6_K):
-        out = np.empty(rows * row_bytes(gtype, ne0), dtype=np.uint8)
         rb = row_bytes(gtype, ne0)
-        step = max(1, (1 << 22) // ne0)
-        for r0 in range(0, rows, step):
-            r1 = min(rows, r0 + step)
+        out = np.empty(nrows * rb, dtype=np.uint8)
+        step = _chunk_rows(ne0)
+        for r0 in range(0, nrows, step):
+            r1 = min(nrows, r0 + step)
             w = rng.standard_normal((r1 - r0, ne0), dtype=np.float32) * np.float32(0.02)
             enc = q4k_quantize(w) if gtype == Q4_K else q6k_quantize(w)
             out[r0 * rb:r1 * rb] = enc.reshape(-1)
         return out
     raise ValueError(f"no generator for type {gtype}")
+
+
+def make_chunk(s: ModelSpec, index: int, name: str, ne0: int, ne1: int, gtype: int,
+               r0: int, r1: int) -> np.ndarray:
+    """Bytes of rows [r0, r1) of one tensor (a range of tensor_chunks)."""
+    if (r0, r1) == (0, max(ne1, 1)) and max(ne1, 1) * ne0 <= CHUNK_ELEMS:
+        rng = np.random.default_rng([s.seed, index])
+    else:
+        rng = np.random.default_rng([s.seed, index, r0])
+    return _gen_rows(rng, name, ne0, r1 - r0, gtype)
+
+
+def make_tensor(s: ModelSpec, index: int, name: str, ne0: int, ne1: int,
+                gtype: int) -> np.ndarray:
+    """Bytes of one tensor.  Norms are 1.0; f16 matrices ~ N(0, 0.02);
+    ternary matrices uniform trits with d ~ U(0.01, 0.05); K-quants quantise
+    N(0, 0.02) weights with the quantisers above."""
+    parts = [make_chunk(s, index, name, ne0, ne1, gtype, r0, r1)
+             for r0, r1 in tensor_chunks(ne0, ne1)]
+    return parts[0] if len(parts) == 1 else np.concatenate(parts)
+
+
+def _chunk_job(args):
+    return make_chunk(*args)
+
+
+def _workers() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
 
 
 # ------------------------------------------------------------------- GGUF
@@ -315,7 +361,9 @@ def _kv_str(key, v):
 
 def write_gguf(path: str, s: ModelSpec, alignment: int = 32, tensors=None) -> dict:
     """Write the model as a GGUF v3 file; returns {name: bytes ndarray} only
-    when tensors == {} is passed in to collect them (small models)."""
+    when tensors == {} is passed in to collect them.  Row ranges of large
+    tensors are generated by a pool of worker processes (the bytes do not
+    depend on the number of workers)."""
     tl = tensor_list(s)
     meta = [
         _kv_u32("general.alignment", alignment),
@@ -345,18 +393,50 @@ def write_gguf(path: str, s: ModelSpec, alignment: int = 32, tensors=None) -> di
     head = (b"GGUF" + struct.pack("<IQQ", 3, len(tl), len(meta)) + b"".join(meta)
             + b"".join(infos))
     pad = (-len(head)) % alignment
-    with open(path, "wb") as f:
-        f.write(head + b"\0" * pad)
-        pos = 0
-        for i, ((name, ne0, ne1, gt), o) in enumerate(zip(tl, offsets)):
-            if o > pos:
-                f.write(b"\0" * (o - pos))
-                pos = o
-            data = make_tensor(s, i, name, ne0, ne1, gt)
-            f.write(data.tobytes())
-            pos += data.nbytes
+    jobs = [(i, r0, r1) for i, (name, ne0, ne1, gt) in enumerate(tl)
+            for r0, r1 in tensor_chunks(ne0, ne1)]
+    nw = _workers() if sum(max(t[2], 1) * t[1] for t in tl) > 4 * CHUNK_ELEMS else 1
+    pool = None
+    if nw > 1:
+        import concurrent.futures as cf
+        import multiprocessing as mp
+        pool = cf.ProcessPoolExecutor(nw, mp_context=mp.get_context("fork"))
+    try:
+        def results():
+            if pool is None:
+                for i, r0, r1 in jobs:
+                    yield i, make_chunk(s, i, *tl[i], r0, r1)
+                return
+            window = []
+            it = iter(jobs)
+            for job in it:
+                i, r0, r1 = job
+                window.append((i, pool.submit(_chunk_job, (s, i, *tl[i], r0, r1))))
+                if len(window) >= 2 * nw:
+                    j, f = window.pop(0)
+                    yield j, f.result()
+            for j, f in window:
+                yield j, f.result()
+
+        with open(path, "wb") as f:
+            f.write(head + b"\0" * pad)
+            pos = 0
+            parts = {}
+            for i, data in results():
+                o = offsets[i]
+                if pos < o:
+                    f.write(b"\0" * (o - pos))
+                    pos = o
+                f.write(data.tobytes())
+                pos += data.nbytes
+                if tensors is not None:
+                    parts.setdefault(i, []).append(data)
             if tensors is not None:
-                tensors[name] = data
+                for i, ps in parts.items():
+                    tensors[tl[i][0]] = ps[0] if len(ps) == 1 else np.concatenate(ps)
+    finally:
+        if pool is not None:
+            pool.shutdown()
     return tensors
 
 

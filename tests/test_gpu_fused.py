@@ -144,3 +144,32 @@ def test_unsupported_cases_say_so(gpu):
         gpu.gemv_rmsnorm([t], xw, 8, gpu.array(np.ones(K, np.float32)), EPS,
                          [gpu.empty(8 * 16, np.float32)])
     assert e.value.status == 5
+
+
+def test_mixed_types_take_the_separate_steps(gpu):
+    """A Q4_K_M-style layer (Q4_K attn_q/k, Q6_K attn_v; gate and up of
+    different types) is refused by the one-launch stages with
+    FOX_GPU_ERR_UNSUPPORTED, the status on which the host runs the
+    separate steps; mismatched widths remain FOX_GPU_ERR_ARG."""
+    rng = np.random.default_rng(4)
+    K, hd, n_ctx = 512, 64, 8
+    q4 = [gpu.tensor(12, K, 128, weights(rng, 12, 128, K)) for _ in range(2)]
+    q6 = gpu.tensor(14, K, 128, weights(rng, 14, 128, K))
+    x = gpu.array(rng.standard_normal(K).astype(np.float32))
+    nw = gpu.array(np.ones(K, np.float32))
+    cs = gpu.array(np.ones(n_ctx * hd // 2, np.float32))
+    pos = gpu.array(np.zeros(1, np.uint32))
+    kc = gpu.empty(n_ctx * 128, np.float32)
+    vc = gpu.empty(n_ctx * 128, np.float32)
+    with pytest.raises(rf.FoxError) as e:
+        gpu.qkv_rope(q4[0], q4[1], q6, x, 1, nw, EPS, gpu.empty(128, np.float32), cs, cs, pos,
+                     n_ctx, kc, vc, hd)
+    assert e.value.status == 5
+    with pytest.raises(rf.FoxError) as e:
+        gpu.gate_up_silu(q4[0], q6, x, 1, nw, EPS, gpu.empty(128, np.float32))
+    assert e.value.status == 5
+    wide = gpu.tensor(34, 2 * K, 128, weights(rng, 34, 128, 2 * K))
+    narrow = gpu.tensor(34, K, 128, weights(rng, 34, 128, K))
+    with pytest.raises(rf.FoxError) as e:
+        gpu.gate_up_silu(narrow, wide, x, 1, nw, EPS, gpu.empty(128, np.float32))
+    assert e.value.status == 1
