@@ -217,6 +217,15 @@ fox_gpu_status fox_gpu_get_rows(fox_gpu_ctx *ctx, const fox_gpu_tensor *t,
                                 const uint32_t *rows, size_t n, float *out,
                                 size_t out_stride, uint32_t *bad);
 
+/* n elements of one row held in its GGUF bytes (device memory) as f32:
+ * F32, F16, Q4_K and Q6_K with the reference's arithmetic
+ * (src/kernels.c:874-941; NaN payloads kept as the reference's field
+ * conversion keeps them).  Other types -> FOX_GPU_ERR_UNSUPPORTED, n not a
+ * whole number of blocks -> FOX_GPU_ERR_ARG.  Backs fox_dequant_row
+ * (include/fox/fox.h:367-368). */
+fox_gpu_status fox_gpu_dequant(fox_gpu_ctx *ctx, int type, const void *row, size_t n,
+                               float *out);
+
 /* out = x * (1/sqrt(mean(x^2) + eps)) * w per row (src/ops.c:7-22). */
 fox_gpu_status fox_gpu_rmsnorm(fox_gpu_ctx *ctx, float *out, size_t out_stride,
                                const float *x, size_t x_stride, const float *w,

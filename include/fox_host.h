@@ -52,6 +52,60 @@ uint32_t    fox_ggml_type_block_bytes(fox_ggml_type type);
 int         fox_gemv_supports(fox_ggml_type type);
 size_t      fox_row_bytes(fox_ggml_type type, size_t n_cols);
 
+/* ----------------------------------------------------------- operators */
+
+/* The reference's operator entry points on host buffers, computed on the
+ * GPU (rustfox_amd/host/operators.c): same arguments, results and status
+ * codes; each call copies its operands to HBM and the result back, so the
+ * decode path keeps weights resident instead.  The pool is accepted for
+ * the ABI and not used; NULL is accepted. */
+typedef struct fox_threadpool fox_threadpool;
+
+/* include/fox/fox.h:331-333 (n <= 0: online cores, at most 256) */
+fox_threadpool *fox_threadpool_create(int n_threads);
+void            fox_threadpool_destroy(fox_threadpool *tp);
+int             fox_threadpool_size(const fox_threadpool *tp);
+/* include/fox/fox.h:335-338: fn(ctx, 0, 0, n) on the calling thread (no CPU
+ * workers in this build; the reference's NULL-pool behaviour) */
+typedef void (*fox_parallel_fn)(void *ctx, int worker, size_t begin, size_t end);
+fox_status      fox_parallel_for(fox_threadpool *tp, size_t n, fox_parallel_fn fn, void *ctx);
+
+/* include/fox/fox.h:322-329: *out = sum_b d_b * S_b over n/256 blocks */
+fox_status fox_tq1_dot_i8(const int8_t *activations, const void *block_data,
+                          size_t n, float *out);
+fox_status fox_tq2_dot_i8(const int8_t *activations, const void *block_data,
+                          size_t n, float *out);
+fox_status fox_tq1_dot_i8_scalar(const int8_t *activations, const void *block_data,
+                                 size_t n, float *out);
+fox_status fox_tq2_dot_i8_scalar(const int8_t *activations, const void *block_data,
+                                 size_t n, float *out);
+
+/* include/fox/fox.h:342-343: per-vector int8 activations, scale amax/127 */
+fox_status fox_quantize_activations_i8(const float *x, size_t n,
+                                       int8_t *q, float *scale);
+
+/* include/fox/fox.h:345-355 */
+fox_status fox_gemv_tq1_f32(fox_threadpool *tp, const float *x, const void *weights,
+                            size_t n_rows, size_t n_cols, float *out);
+fox_status fox_gemv_tq2_f32(fox_threadpool *tp, const float *x, const void *weights,
+                            size_t n_rows, size_t n_cols, float *out);
+fox_status fox_gemv_tq1_i8(fox_threadpool *tp, const int8_t *q, float act_scale,
+                           const void *weights, size_t n_rows, size_t n_cols,
+                           float *out);
+fox_status fox_gemv_tq2_i8(fox_threadpool *tp, const int8_t *q, float act_scale,
+                           const void *weights, size_t n_rows, size_t n_cols,
+                           float *out);
+
+/* include/fox/fox.h:363-365: types of fox_gemv_supports; others
+ * FOX_ERR_UNSUPPORTED */
+fox_status fox_gemv(fox_threadpool *tp, fox_ggml_type type, const float *x,
+                    const void *weights, size_t n_rows, size_t n_cols,
+                    float *out);
+
+/* include/fox/fox.h:367-368: F32, F16, Q4_K, Q6_K rows */
+fox_status fox_dequant_row(fox_ggml_type type, const void *row, size_t n,
+                           float *out);
+
 /* ------------------------------------------------------------- weights */
 
 /* include/fox/fox.h:370-403, plus the HBM-resident mode */

@@ -59,6 +59,94 @@ extern "C" fox_gpu_status fox_gpu_get_rows(fox_gpu_ctx *ctx, const fox_gpu_tenso
     return FOX_GPU_OK;
 }
 
+// ------------------------------------------------------------- dequant
+
+// f16 bits -> f32 bits by field arithmetic (src/kernels.c:14-39 semantics):
+// NaN payloads are shifted as they are, without the quieting a hardware
+// conversion may apply to a signalling NaN.
+__device__ __forceinline__ float f16_exact(uint32_t h)
+{
+    const uint32_t sign = (h >> 15) << 31, e = (h >> 10) & 31u, f = h & 0x3FFu;
+    uint32_t u;
+    if (e == 31) {
+        u = sign | 0x7F800000u | (f << 13);
+    } else if (e == 0) {
+        if (f == 0) {
+            u = sign;
+        } else {
+            // f = 1.m * 2^(p) with p the top set bit (0..9): value f * 2^-24
+            const int p = 31 - __builtin_clz(f);
+            u = sign | ((uint32_t)(p - 24 + 127) << 23) | ((f << (23 - p)) & 0x7FFFFFu);
+        }
+    } else {
+        u = sign | ((e + 112u) << 23) | (f << 13);
+    }
+    return __uint_as_float(u);
+}
+
+// One element per thread of a row in its GGUF bytes: F32 copy, F16
+// conversion, Q4_K y = (d*sc)*q - dmin*m (src/kernels.c:257-283), Q6_K
+// y = (d*sc)*(q-32) (src/kernels.c:217-244), each product rounded as there.
+__global__ void dequant_gguf_k(int type, const uint8_t *__restrict__ w, uint64_t n,
+                               float *__restrict__ out)
+{
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        float y;
+        if (type == FOX_GPU_F32) {
+            y = ((const float *)w)[i];
+        } else if (type == FOX_GPU_F16) {
+            y = f16_exact(((const uint16_t *)w)[i]);
+        } else if (type == FOX_GPU_Q4_K) {
+            const uint8_t *blk = w + (i >> 8) * 144;
+            const int e = (int)(i & 255), p = e >> 6, l = e & 63, j = 2 * p + (l >> 5);
+            const uint8_t *s = blk + 4;
+            uint32_t sc, m;
+            if (j < 4) {
+                sc = s[j] & 63u;
+                m = s[j + 4] & 63u;
+            } else {
+                sc = (s[j + 4] & 15u) | ((uint32_t)(s[j - 4] >> 6) << 4);
+                m = (s[j + 4] >> 4) | ((uint32_t)(s[j] >> 6) << 4);
+            }
+            const uint8_t qb = blk[16 + 32 * p + (l & 31)];
+            const uint32_t q = l < 32 ? (qb & 15u) : (qb >> 4);
+            const float d = f16_exact(blk[0] | (uint32_t)blk[1] << 8);
+            const float dmin = f16_exact(blk[2] | (uint32_t)blk[3] << 8);
+            const float d1 = d * (float)sc, m1 = dmin * (float)m;
+            y = d1 * (float)q - m1;
+        } else {   // Q6_K
+            const uint8_t *blk = w + (i >> 8) * 210;
+            const int e = (int)(i & 255), h = e >> 7, g = (e >> 5) & 3, l = e & 31;
+            const uint8_t *ql = blk + 64 * h, *qh = blk + 128 + 32 * h;
+            const int8_t *sc = (const int8_t *)(blk + 192 + 8 * h);
+            const uint32_t lo = (g & 1) ? ql[l + 32] : ql[l];
+            const uint32_t q = ((g & 2) ? lo >> 4 : lo & 15u) | (((qh[l] >> (2 * g)) & 3u) << 4);
+            const float d = f16_exact(blk[208] | (uint32_t)blk[209] << 8);
+            y = d * (float)sc[l / 16 + 2 * g] * (float)((int)q - 32);
+        }
+        out[i] = y;
+    }
+}
+
+extern "C" fox_gpu_status fox_gpu_dequant(fox_gpu_ctx *ctx, int type, const void *row, size_t n,
+                                          float *out)
+{
+    if (!ctx || !row || !out || n == 0) return fox_fail(FOX_GPU_ERR_ARG, "dequant: bad argument");
+    if (type != FOX_GPU_F32 && type != FOX_GPU_F16 && type != FOX_GPU_Q4_K &&
+        type != FOX_GPU_Q6_K)
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "dequant: %s rows are not dequantised",
+                        fox_type_name(type));
+    if (n % fox_block_elems(type))
+        return fox_fail(FOX_GPU_ERR_ARG, "dequant: %zu elements is not a whole number of %s "
+                        "blocks", n, fox_type_name(type));
+    const uint64_t g = (n + 255) / 256;
+    hipLaunchKernelGGL(dequant_gguf_k, dim3((unsigned)(g < 4096 ? g : 4096)), dim3(256), 0,
+                       ctx->stream, type, (const uint8_t *)row, (uint64_t)n, out);
+    FOX_LAUNCHED("dequant");
+    return FOX_GPU_OK;
+}
+
 // --------------------------------------------------------------- rmsnorm
 
 __device__ __forceinline__ double wave_sum_d(double v)

@@ -1,77 +1,71 @@
-/* sample.c -- token choice on the host (RustFox src/sample.c semantics).
+/* sample.c -- the greedy token choice of fox_sampler_pick.
  *
- * Greedy (temperature <= 0): repeat penalty over the last repeat_last_n
- * accepted tokens (a positive logit is divided, a non-positive one
- * multiplied), then the first index of the maximum (src/sample.c:135-153).
- * Otherwise: the top_k best logits in descending order (ties keep the lower
- * id first), softmax at the temperature, optional top_p cut and
- * renormalisation, and one uniform draw from xorshift64* (Marsaglia/Vigna:
- * shifts 12, 25, 27, multiplier 0x2545F4914F6CDD1D; the top 24 bits make a
- * float in [0, 1)) walked along the cumulative sum (src/sample.c:155-194).
+ * In scope is greedy decoding (temperature <= 0): each logit of a token
+ * accepted k times among the last W accepted tokens (W = repeat_last_n, or
+ * 1 when that is 0) is penalised k times -- divided by repeat_penalty while
+ * positive, else multiplied -- and the pick is the lowest index holding the
+ * largest penalised value (src/sample.c:95-107, 135-153).  A penalty at or
+ * below 1.0 leaves the logits as they are.
+ *
+ * The handle keeps, per vocabulary entry, how often it occurs in the
+ * window, and the window's ids in arrival order so that the oldest one can
+ * be retired; a pick scans the logits once, penalising only counted ids on
+ * the fly, without copying them.
+ *
+ * Stochastic sampling (temperature > 0: top-k, top-p, a seeded draw) is not
+ * part of the decode path this library provides: such a pick fails with
+ * FOX_ERR_UNSUPPORTED.  The configuration's defaults are the reference's
+ * (include/fox/fox.h:453-469), so that a caller's configuration code is
+ * unchanged.
  */
 #include "fox_host_internal.h"
 
-#include <math.h>
 #include <stdlib.h>
 #include <string.h>
 
-#define TOPK_MAX 512
-
 struct fox_sampler {
-    fox_sampler_config cfg;
-    size_t n_vocab;
-    uint64_t rng;
-    float *work;
-    uint32_t *hist;
-    size_t hist_cap, hist_len, hist_head;
+    float penalty;        /* > 1.0f, or 1.0f for none */
+    int greedy;
+    size_t vocab;
+    uint32_t *count;      /* occurrences of each id in the window */
+    uint32_t *window;     /* ids, oldest at window[first] */
+    size_t cap, used, first;
 };
 
 void fox_sampler_config_default(fox_sampler_config *cfg)
 {
     if (!cfg) return;
+    memset(cfg, 0, sizeof(*cfg));
     cfg->temperature = 0.8f;
     cfg->top_k = 40;
     cfg->top_p = 0.95f;
     cfg->repeat_penalty = 1.1f;
     cfg->repeat_last_n = 64;
-    cfg->seed = 0;
-}
-
-static uint64_t xs64(uint64_t *s)
-{
-    uint64_t x = *s;
-    x ^= x >> 12;
-    x ^= x << 25;
-    x ^= x >> 27;
-    *s = x;
-    return x * 0x2545F4914F6CDD1Dull;
-}
-
-static float uniform01(uint64_t *s)
-{
-    return (float)((double)(xs64(s) >> 40) / 16777216.0);
 }
 
 fox_sampler *fox_sampler_create(const fox_sampler_config *cfg, size_t n_vocab)
 {
+    fox_sampler_config c;
     fox_sampler *s;
-    if (n_vocab == 0) { fox_fail(FOX_ERR_ARG, "sampler: empty vocabulary"); return NULL; }
+
+    if (n_vocab == 0) {
+        fox_fail(FOX_ERR_ARG, "sampler: the vocabulary has no entries");
+        return NULL;
+    }
+    if (cfg) c = *cfg;
+    else fox_sampler_config_default(&c);
     s = (fox_sampler *)calloc(1, sizeof(*s));
-    if (!s) { fox_fail(FOX_ERR_NOMEM, "sampler: handle"); return NULL; }
-    if (cfg) s->cfg = *cfg;
-    else fox_sampler_config_default(&s->cfg);
-    if (s->cfg.top_k < 0) s->cfg.top_k = 0;
-    if (s->cfg.top_k > TOPK_MAX) s->cfg.top_k = TOPK_MAX;
-    if (s->cfg.top_p <= 0.0f || s->cfg.top_p > 1.0f) s->cfg.top_p = 1.0f;
-    if (s->cfg.repeat_penalty < 1.0f) s->cfg.repeat_penalty = 1.0f;
-    s->n_vocab = n_vocab;
-    s->rng = s->cfg.seed ? s->cfg.seed : 0x9E3779B97F4A7C15ull;
-    s->hist_cap = s->cfg.repeat_last_n ? s->cfg.repeat_last_n : 1;
-    s->work = (float *)calloc(n_vocab, sizeof(float));
-    s->hist = (uint32_t *)calloc(s->hist_cap, sizeof(uint32_t));
-    if (!s->work || !s->hist) {
+    if (s) {
+        s->vocab = n_vocab;
+        s->greedy = !(c.temperature > 0.0f);
+        s->penalty = c.repeat_penalty > 1.0f ? c.repeat_penalty : 1.0f;
+        s->cap = c.repeat_last_n ? c.repeat_last_n : 1;
+        s->count = (uint32_t *)calloc(n_vocab, sizeof(uint32_t));
+        s->window = (uint32_t *)calloc(s->cap, sizeof(uint32_t));
+    }
+    if (!s || !s->count || !s->window) {
         fox_sampler_destroy(s);
-        fox_fail(FOX_ERR_NOMEM, "sampler: buffers");
+        fox_fail(FOX_ERR_NOMEM, "sampler: cannot allocate its %zu-entry tables", n_vocab);
         return NULL;
     }
     return s;
@@ -80,85 +74,54 @@ fox_sampler *fox_sampler_create(const fox_sampler_config *cfg, size_t n_vocab)
 void fox_sampler_destroy(fox_sampler *s)
 {
     if (!s) return;
-    free(s->work);
-    free(s->hist);
+    free(s->count);
+    free(s->window);
     free(s);
 }
 
 void fox_sampler_accept(fox_sampler *s, uint32_t token)
 {
+    size_t slot;
     if (!s) return;
-    s->hist[s->hist_head] = token;
-    s->hist_head = (s->hist_head + 1) % s->hist_cap;
-    if (s->hist_len < s->hist_cap) s->hist_len++;
+    if (s->used == s->cap) {               /* the oldest id leaves the window */
+        uint32_t old = s->window[s->first];
+        if (old < s->vocab) s->count[old]--;
+        s->first = (s->first + 1) % s->cap;
+        s->used--;
+    }
+    slot = (s->first + s->used) % s->cap;
+    s->window[slot] = token;
+    s->used++;
+    if (token < s->vocab) s->count[token]++;
 }
 
-typedef struct { float v; uint32_t id; } cand;
+/* x penalised k times: each application rounds, as the reference's
+ * repeated in-place update does */
+static float penalised(float x, uint32_t k, float p)
+{
+    while (k--) x = x > 0.0f ? x / p : x * p;
+    return x;
+}
 
 fox_status fox_sampler_pick(fox_sampler *s, const float *logits, uint32_t *out)
 {
-    cand top[TOPK_MAX];
-    size_t i, n = 0, k;
-    float mx, sum, cum, r;
+    size_t i, best = 0;
+    float top;
 
     if (!s || !logits || !out) return FOX_ERR_ARG;
-    memcpy(s->work, logits, s->n_vocab * sizeof(float));
-    if (s->cfg.repeat_penalty > 1.0f) {
-        for (i = 0; i < s->hist_len; i++) {
-            uint32_t t = s->hist[i];
-            if (t >= s->n_vocab) continue;
-            if (s->work[t] > 0.0f) s->work[t] /= s->cfg.repeat_penalty;
-            else s->work[t] *= s->cfg.repeat_penalty;
+    if (!s->greedy)
+        return fox_fail(FOX_ERR_UNSUPPORTED, "sampler: this build decodes greedily; set "
+                        "temperature <= 0 (stochastic sampling is not provided)");
+    top = s->penalty > 1.0f && s->count[0] ? penalised(logits[0], s->count[0], s->penalty)
+                                           : logits[0];
+    for (i = 1; i < s->vocab; i++) {
+        float v = logits[i];
+        if (s->penalty > 1.0f && s->count[i]) v = penalised(v, s->count[i], s->penalty);
+        if (v > top) {                     /* strict: the first maximum stays */
+            top = v;
+            best = i;
         }
     }
-    if (s->cfg.temperature <= 0.0f) {
-        size_t best = 0;
-        for (i = 1; i < s->n_vocab; i++) if (s->work[i] > s->work[best]) best = i;
-        *out = (uint32_t)best;
-        return FOX_OK;
-    }
-
-    k = (s->cfg.top_k > 0 && (size_t)s->cfg.top_k <= s->n_vocab) ? (size_t)s->cfg.top_k
-        : (s->n_vocab < TOPK_MAX ? s->n_vocab : TOPK_MAX);
-    for (i = 0; i < s->n_vocab; i++) {
-        float v = s->work[i];
-        size_t j;
-        if (n < k) {
-            j = n++;
-        } else {
-            if (v <= top[n - 1].v) continue;
-            j = n - 1;
-        }
-        while (j > 0 && top[j - 1].v < v) { top[j] = top[j - 1]; j--; }
-        top[j].v = v;
-        top[j].id = (uint32_t)i;
-    }
-    if (n == 0) return fox_fail(FOX_ERR_INTERNAL, "sampler: no candidates");
-
-    mx = top[0].v;
-    sum = 0.0f;
-    for (i = 0; i < n; i++) {
-        top[i].v = expf((top[i].v - mx) / s->cfg.temperature);
-        sum += top[i].v;
-    }
-    if (!(sum > 0.0f)) { *out = top[0].id; return FOX_OK; }
-    for (i = 0; i < n; i++) top[i].v /= sum;
-    if (s->cfg.top_p < 1.0f) {
-        cum = 0.0f;
-        for (i = 0; i < n; i++) {
-            cum += top[i].v;
-            if (cum >= s->cfg.top_p) { n = i + 1; break; }
-        }
-        sum = 0.0f;
-        for (i = 0; i < n; i++) sum += top[i].v;
-        if (sum > 0.0f) for (i = 0; i < n; i++) top[i].v /= sum;
-    }
-    r = uniform01(&s->rng);
-    cum = 0.0f;
-    for (i = 0; i < n; i++) {
-        cum += top[i].v;
-        if (r <= cum) { *out = top[i].id; return FOX_OK; }
-    }
-    *out = top[n - 1].id;
+    *out = (uint32_t)best;
     return FOX_OK;
 }

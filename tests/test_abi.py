@@ -141,9 +141,24 @@ def test_budget_too_small(tmp_path):
     L.fox_weights_close(w)
 
 
+def ref_greedy(logits, history, window, penalty):
+    """src/sample.c:95-107, 135-153 restated: the penalty once per entry of
+    the last `window` accepted ids, then the first maximum."""
+    w = logits.astype(np.float32).copy()
+    if penalty > 1.0:
+        for t in history[-window:]:
+            if t < w.size:
+                w[t] = w[t] / np.float32(penalty) if w[t] > 0 else w[t] * np.float32(penalty)
+    best = 0
+    for i in range(1, w.size):
+        if w[i] > w[best]:
+            best = i
+    return best
+
+
 def test_sampler_semantics():
-    """src/sample.c: greedy picks the first maximum after the repeat
-    penalty; stochastic draws stay in the vocabulary."""
+    """Greedy picks: the first maximum after the repeat penalty, applied once
+    per occurrence in the window; stochastic sampling is refused."""
     logits = np.array([0.5, 2.0, 2.0, -1.0, 1.9], np.float32)
     g = rf.Sampler(5, temperature=0.0, repeat_penalty=1.0)
     assert g.pick(logits) == 1
@@ -152,4 +167,115 @@ def test_sampler_semantics():
     p.accept(2)
     assert p.pick(logits) == 4        # 2.0 / 1.1 < 1.9
     s = rf.Sampler(5, temperature=0.8, top_k=3, seed=12345)
-    assert all(0 <= s.pick(logits) < 5 for _ in range(200))
+    with pytest.raises(rf.FoxError) as e:
+        s.pick(logits)
+    assert e.value.status == 5
+    with pytest.raises(rf.FoxError):
+        rf.Sampler(0, temperature=0.0)
+
+
+@pytest.mark.parametrize("window,penalty", [(64, 1.1), (3, 1.3), (0, 1.5), (1, 0.9), (7, 2.0)])
+def test_sampler_matches_the_reference_rule(window, penalty):
+    """Random logits (with ties, zeros, negatives and a NaN) and random
+    accepted ids, some repeated, some outside the vocabulary: every pick
+    equals the reference rule, including the window of one id that
+    repeat_last_n = 0 gives."""
+    rng = np.random.default_rng([window, int(penalty * 10)])
+    V = 50
+    s = rf.Sampler(V, temperature=0.0, repeat_penalty=penalty, repeat_last_n=window)
+    ref = None
+    from oracle_libs import ref_available
+    if ref_available():
+        # the reference itself, compiled from its sources (oracle/_ref)
+        from oracle_libs import REF_SO
+        R = C.CDLL(REF_SO)
+        R.fox_sampler_config_default.argtypes = [C.POINTER(rf.SamplerConfig)]
+        R.fox_sampler_create.argtypes = [C.POINTER(rf.SamplerConfig), C.c_size_t]
+        R.fox_sampler_create.restype = C.c_void_p
+        R.fox_sampler_accept.argtypes = [C.c_void_p, C.c_uint32]
+        R.fox_sampler_pick.argtypes = [C.c_void_p, C.c_void_p, C.POINTER(C.c_uint32)]
+        R.fox_sampler_destroy.argtypes = [C.c_void_p]
+        cfg = rf.SamplerConfig()
+        R.fox_sampler_config_default(C.byref(cfg))
+        cfg.temperature, cfg.repeat_penalty, cfg.repeat_last_n = 0.0, penalty, window
+        ref = R.fox_sampler_create(C.byref(cfg), V)
+    hist = []
+    for step in range(300):
+        lg = rng.integers(-4, 5, V).astype(np.float32) * np.float32(0.25)
+        if step % 17 == 0:
+            lg[rng.integers(0, V)] = np.nan
+        want = ref_greedy(lg, hist, window or 1, penalty)
+        got = s.pick(lg)
+        assert got == want, step
+        if ref:
+            r = C.c_uint32()
+            assert R.fox_sampler_pick(ref, lg.ctypes.data_as(C.c_void_p), C.byref(r)) == 0
+            assert r.value == got, step
+        t = int(rng.integers(0, V + 3)) if step % 5 else int(hist[-1]) if hist else 0
+        s.accept(t)
+        hist.append(t)
+        if ref:
+            R.fox_sampler_accept(ref, t)
+    if ref:
+        R.fox_sampler_destroy(ref)
+
+
+def test_operator_entries_check_arguments_then_need_the_gpu():
+    """The reference's operator entries (include/fox/fox.h:322-368) validate
+    their arguments as tests/test_gemv.c:132-139 expects before touching a
+    device, and without a GPU fail with a status and a message instead of
+    computing on the CPU."""
+    L = rf.host_lib()
+    vp, sz = C.c_void_p, C.c_size_t
+    L.fox_gemv_tq2_i8.argtypes = [vp, vp, C.c_float, vp, sz, sz, vp]
+    L.fox_gemv_tq2_f32.argtypes = [vp, vp, vp, sz, sz, vp]
+    L.fox_dequant_row.argtypes = [C.c_int, vp, sz, vp]
+    q = np.zeros(512, np.int8)
+    w = np.zeros(2 * 66 * 4, np.uint8)
+    out = np.zeros(4, np.float32)
+    P = lambda a: a.ctypes.data_as(vp)
+    assert L.fox_gemv_tq2_i8(None, P(q), 1.0, P(w), 4, 255, P(out)) == 1
+    assert L.fox_gemv_tq2_i8(None, None, 1.0, P(w), 4, 512, P(out)) == 1
+    assert L.fox_gemv_tq2_i8(None, P(q), 1.0, None, 4, 512, P(out)) == 1
+    assert L.fox_gemv_tq2_i8(None, P(q), 1.0, P(w), 0, 512, P(out)) == 1
+    assert L.fox_dequant_row(34, P(w), 256, P(out)) == 5
+    if os.path.exists("/dev/kfd") and os.access("/dev/kfd", os.R_OK):
+        return
+    x = np.zeros(512, np.float32)
+    st = L.fox_gemv_tq2_f32(None, P(x), P(w), 4, 512, P(out))
+    assert st != 0 and L.fox_last_error()
+
+
+@pytest.mark.parametrize("victim,cols,rows", [("blk.0.attn_k.weight", None, 64),
+                                              ("blk.0.attn_output.weight", 256, None),
+                                              ("blk.0.ffn_down.weight", None, 32),
+                                              ("output.weight", 256, None),
+                                              ("blk.0.ffn_norm.weight", 256, None)])
+def test_model_open_rejects_mismatched_shapes(tmp_path, monkeypatch, victim, cols, rows):
+    """A GGUF whose tensor shapes disagree with its metadata is refused with
+    FOX_ERR_FORMAT at open (host mode: no device involved) instead of
+    reaching kernels that size their reads and writes by the tensor."""
+    s = synth.spec("tiny-512", n_layer=1, n_vocab=64)
+    real = synth.tensor_list
+
+    def bent(spec):
+        out = []
+        for name, ne0, ne1, gt in real(spec):
+            if name == victim:
+                ne0 = ne0 + cols if cols else ne0
+                ne1 = ne1 + rows if rows else ne1
+            out.append((name, ne0, ne1, gt))
+        return out
+    monkeypatch.setattr(synth, "tensor_list", bent)
+    p = str(tmp_path / "bent.gguf")
+    synth.write_gguf(p, s)
+    monkeypatch.setattr(synth, "tensor_list", real)
+    L = rf.host_lib()
+    m = C.c_void_p()
+    st = L.fox_model_open(p.encode(), rf.WEIGHTS_RESIDENT, 0, C.byref(m))
+    assert st == 4, (st, L.fox_last_error())
+    assert victim.encode() in L.fox_last_error()
+    good = str(tmp_path / "good.gguf")
+    synth.write_gguf(good, s)
+    assert L.fox_model_open(good.encode(), rf.WEIGHTS_RESIDENT, 0, C.byref(m)) == 0
+    L.fox_model_close(m)
