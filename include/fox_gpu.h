@@ -140,6 +140,20 @@ fox_gpu_status fox_gpu_gemv(fox_gpu_ctx *ctx, const fox_gpu_tensor *w,
                             const float *x, size_t x_stride, size_t M,
                             float *out, size_t out_stride, unsigned flags);
 
+/* fox_gpu_gemv without any allocation.  No counterpart in RustFox: it is
+ * for callers that cannot allocate device memory -- work under HIP graph
+ * capture, tight serving loops, hosts that forbid allocation after start-up.
+ * Same arguments and results as fox_gpu_gemv; where fox_gpu_gemv would grow
+ * the context's workspace (K-quant weights, ternary rows wider than the
+ * fused path takes), the activations go to a fixed 2 MiB scratch that the
+ * library holds on each GPU until the process ends (its address resolved at
+ * fox_gpu_init).  Inputs needing more scratch than that are refused with
+ * FOX_GPU_ERR_ARG.  Every call on a GPU shares its scratch, so calls that
+ * overlap in time on one GPU (two streams, two host threads) race. */
+fox_gpu_status fox_gpu_gemv_noalloc(fox_gpu_ctx *ctx, const fox_gpu_tensor *w,
+                                    const float *x, size_t x_stride, size_t M,
+                                    float *out, size_t out_stride, unsigned flags);
+
 /* Several matrices with the same K applied to one input (q/k/v, gate/up):
  * the input is quantised once.  outs[i] receives rows of ws[i]. */
 fox_gpu_status fox_gpu_gemv_multi(fox_gpu_ctx *ctx, size_t n,

@@ -71,6 +71,7 @@ def gpu_lib() -> C.CDLL:
         "fox_gpu_tensor_free": [vp, vp],
         "fox_gpu_quantize": [vp, C.c_int, vp, sz, sz, sz, vp, vp],
         "fox_gpu_gemv": [vp, vp, vp, sz, sz, vp, sz, C.c_uint],
+        "fox_gpu_gemv_noalloc": [vp, vp, vp, sz, sz, vp, sz, C.c_uint],
         "fox_gpu_gemv_multi": [vp, sz, C.POINTER(vp), vp, sz, sz, C.POINTER(vp),
                                C.POINTER(sz), C.c_uint],
         "fox_gpu_gemv_i8": [vp, vp, vp, vp, sz, vp, sz],

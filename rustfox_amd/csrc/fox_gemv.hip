@@ -637,10 +637,13 @@ static fox_gpu_status check_common(size_t n, const fox_gpu_tensor *const *ws, si
     return FOX_GPU_OK;
 }
 
-fox_gpu_status fox_gemv_launch(fox_gpu_ctx *ctx, size_t n, const fox_gpu_tensor *const *ws,
-                               const float *x, size_t x_stride, const int8_t *q,
-                               const float *scale, size_t M, float *const *outs,
-                               const size_t *out_strides, unsigned flags, int32_t *sums)
+// fixed_ws: a caller-provided workspace of fixed_cap bytes used instead of
+// the context's growable one (nullptr: the context's)
+static fox_gpu_status gemv_launch_ws(fox_gpu_ctx *ctx, size_t n, const fox_gpu_tensor *const *ws,
+                                     const float *x, size_t x_stride, const int8_t *q,
+                                     const float *scale, size_t M, float *const *outs,
+                                     const size_t *out_strides, unsigned flags, int32_t *sums,
+                                     uint8_t *fixed_ws, size_t fixed_cap)
 {
     int type;
     size_t K;
@@ -700,7 +703,16 @@ fox_gpu_status fox_gemv_launch(fox_gpu_ctx *ctx, size_t n, const fox_gpu_tensor 
     st = fox_fused_gemv(ctx, n, ws, x, x_stride, q, scale, M, outs, out_strides, flags, sums);
     if (st != FOX_GPU_ERR_UNSUPPORTED) return st;
     Ws w;
-    if ((st = carve(ctx, fmt, K, M, &w))) return st;
+    if (fixed_ws) {
+        const size_t need = act_layout(fmt, K, M, nullptr, nullptr);
+        if (need > fixed_cap)
+            return fox_fail(FOX_GPU_ERR_ARG, "gemv: %zu x %zu %s activations need %zu bytes of "
+                            "scratch; the fixed scratch holds %zu", M, K, fox_type_name(type),
+                            need, fixed_cap);
+        act_layout(fmt, K, M, fixed_ws, &w);
+    } else if ((st = carve(ctx, fmt, K, M, &w))) {
+        return st;
+    }
     if ((st = launch_prep(ctx, fmt, x, x_stride, q, scale, K, M, w, w.q, w.scale))) return st;
 
     Segs sg;
@@ -717,6 +729,37 @@ fox_gpu_status fox_gemv_launch(fox_gpu_ctx *ctx, size_t n, const fox_gpu_tensor 
     }
     sg.tile_start[n] = tiles;
     return launch_blocks(ctx, fmt, sg, tiles, (int)(K / 256), (int)M, w, flags, sums);
+}
+
+fox_gpu_status fox_gemv_launch(fox_gpu_ctx *ctx, size_t n, const fox_gpu_tensor *const *ws,
+                               const float *x, size_t x_stride, const int8_t *q,
+                               const float *scale, size_t M, float *const *outs,
+                               const size_t *out_strides, unsigned flags, int32_t *sums)
+{
+    return gemv_launch_ws(ctx, n, ws, x, x_stride, q, scale, M, outs, out_strides, flags, sums,
+                          nullptr, 0);
+}
+
+// ------------------------------------------------------ fixed scratch
+
+// The workspace of fox_gpu_gemv_noalloc: a file-scope device array, one
+// copy per GPU, alive until the process ends.  Host code never uses its
+// name as an address (that is a host-side stand-in); fox_scratch_init
+// resolves this device's copy with hipGetSymbolAddress once per context,
+// with the device current, and the kernels receive that pointer.
+static __device__ __align__(256) uint8_t scratch[FOX_NOALLOC_SCRATCH];
+
+fox_gpu_status fox_scratch_init(fox_gpu_ctx *ctx)
+{
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        ctx->scratch = nullptr;
+        return fox_fail(FOX_GPU_ERR_INTERNAL, "init: the fixed scratch of device %d has no "
+                        "address: %s", ctx->device, hipGetErrorString(e));
+    }
+    ctx->scratch = (uint8_t *)p;
+    return FOX_GPU_OK;
 }
 
 // ----------------------------------------------------------- C entries
@@ -754,6 +797,25 @@ extern "C" fox_gpu_status fox_gpu_gemv(fox_gpu_ctx *ctx, const fox_gpu_tensor *w
     size_t strides[1] = {M > 1 ? out_stride : (w ? (size_t)w->ne1 : 0)};
     return fox_gemv_launch(ctx, 1, ws, x, M > 1 ? x_stride : (w ? (size_t)w->ne0 : 0), nullptr,
                            nullptr, M, outs, strides, flags, nullptr);
+}
+
+// fox_gpu_gemv's computation, its activation workspace the fixed scratch:
+// nothing is allocated.  Calls on one device share the scratch (each
+// rewrites every byte it reads before reading it), so calls that overlap
+// in time on one device race.
+extern "C" fox_gpu_status fox_gpu_gemv_noalloc(fox_gpu_ctx *ctx, const fox_gpu_tensor *w,
+                                               const float *x, size_t x_stride, size_t M,
+                                               float *out, size_t out_stride, unsigned flags)
+{
+    if (!ctx || !x || !out) return fox_fail(FOX_GPU_ERR_ARG, "gemv_noalloc: null pointer");
+    if (!ctx->scratch)
+        return fox_fail(FOX_GPU_ERR_INTERNAL, "gemv_noalloc: the context has no fixed scratch");
+    const fox_gpu_tensor *ws[1] = {w};
+    float *outs[1] = {out};
+    size_t strides[1] = {M > 1 ? out_stride : (w ? (size_t)w->ne1 : 0)};
+    return gemv_launch_ws(ctx, 1, ws, x, M > 1 ? x_stride : (w ? (size_t)w->ne0 : 0), nullptr,
+                          nullptr, M, outs, strides, flags, nullptr, ctx->scratch,
+                          FOX_NOALLOC_SCRATCH);
 }
 
 extern "C" fox_gpu_status fox_gpu_gemv_multi(fox_gpu_ctx *ctx, size_t n,

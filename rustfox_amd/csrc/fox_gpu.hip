@@ -89,6 +89,10 @@ extern "C" fox_gpu_status fox_gpu_init(int device, fox_gpu_ctx **out)
         fox_gpu_shutdown(ctx);
         return fox_fail(FOX_GPU_ERR_NOMEM, "init: small buffer");
     }
+    if ((st = fox_scratch_init(ctx)) != FOX_GPU_OK) {   // (device `device` is current)
+        fox_gpu_shutdown(ctx);
+        return st;
+    }
     *out = ctx;
     return FOX_GPU_OK;
 }

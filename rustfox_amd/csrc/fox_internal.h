@@ -67,6 +67,8 @@ struct fox_gpu_ctx {
     // small fixed buffer (counters, cross-workgroup partials) zeroed at init;
     // its address never changes, so captured graphs may use it
     uint8_t *small;
+    // this device's copy of the fixed scratch of fox_gpu_gemv_noalloc
+    uint8_t *scratch;
 };
 #define FOX_SMALL_BYTES (64 * 1024)
 
@@ -107,6 +109,12 @@ fox_gpu_status fox_hip_fail(hipError_t e, const char *what);
 
 // ---- workspace (fox_gpu.hip)
 fox_gpu_status fox_ws_reserve(fox_gpu_ctx *ctx, size_t bytes);
+
+// ---- fixed scratch of fox_gpu_gemv_noalloc (fox_gemv.hip): resolves this
+// device's copy into ctx->scratch; called by fox_gpu_init with the device
+// current
+#define FOX_NOALLOC_SCRATCH (2u << 20)
+fox_gpu_status fox_scratch_init(fox_gpu_ctx *ctx);
 
 // ---- type helpers
 static inline size_t fox_block_bytes(int type)

@@ -1,0 +1,40 @@
+"""fox_gpu_gemv_noalloc (the entry point that allocates nothing) against
+fox_gpu_gemv, through the C ABI: bit-identical outputs on two calls in a
+row, the second with a smaller input, for weights whose GEMV uses the
+scratch (Q4_K, Q6_K, TQ1_0 wider than the fused path) and for one that
+needs none (fused TQ1_0)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import rustfox_amd as rf
+from test_gpu_gemv import weights, bits
+
+pytestmark = pytest.mark.gpu
+
+
+def noalloc(gpu, t, x, M, out, flags=0):
+    st = gpu.lib.fox_gpu_gemv_noalloc(gpu.ctx, t.h, x.ptr, t.ne0, M, out.ptr, t.ne1, flags)
+    if st:
+        raise rf.FoxError(st, gpu.lib.fox_gpu_last_error().decode())
+
+
+@pytest.mark.parametrize("tname,gtype,first,second", [
+    ("Q4_K", 12, (4096, 14336, 8), (1024, 2048, 3)),
+    ("Q6_K", 14, (14336, 4096, 8), (512, 1024, 1)),
+    ("TQ1_0", 34, (21504, 5376, 8), (17408, 300, 2)),
+    ("TQ1_0", 34, (2560, 4096, 1), (512, 64, 1)),
+])
+def test_noalloc_equals_gemv(gpu, tname, gtype, first, second):
+    rng = np.random.default_rng([gtype, first[0], 3])
+    for K, N, M in (first, second):
+        print(f"case noalloc {tname} K={K} N={N} M={M}", flush=True)
+        w = weights(rng, gtype, N, K)
+        t = gpu.tensor(gtype, K, N, w)
+        x = gpu.array(rng.standard_normal((M, K)).astype(np.float32))
+        base = rng.standard_normal((M, N)).astype(np.float32)
+        a, b = gpu.array(base), gpu.array(base)
+        gpu.gemv(t, x, M, a, flags=rf.GEMV_ACCUMULATE)
+        noalloc(gpu, t, x, M, b, rf.GEMV_ACCUMULATE)
+        assert np.array_equal(bits(a.numpy()), bits(b.numpy())), (K, N, M)
