@@ -14,8 +14,18 @@ Prints one JSON line:
              WRITE_SIZE, two runs of --gemv-only made before this process
              touches the GPU), each counter scaled by its reading for a plain
              256 MiB device copy.
-  cpu_baseline  RustFox's own threadpool CPU path (compiled from its sources
-             into oracle/_ref) decoding the same model file on this host.
+  cpu_baseline  the CPU restatement of RustFox's decode path (the oracle,
+             oracle/liboracle.so) on the same workload: the same model file,
+             the same 2048 injected cache rows, greedy steps at positions
+             2048+, its GEMVs and attention heads split over a pool of
+             threads as RustFox splits them.  Beside it: RustFox itself
+             (compiled from its sources into oracle/_ref) decoding the same
+             file at short context (its cache cannot be pre-filled), both at
+             the pool size and on one thread, and the host's CPU model, core
+             count and NUMA layout.
+  extra      the 8B-class Q4_K/Q6_K model after 4096 cached positions and the
+             27B-class TQ1_0 model after 8192 cached positions (batch-1
+             decode and the 8-token verify pass), each with its HBM GB/s.
 
 A step is one token through all 36 layers, the output head and the greedy
 pick.  Inputs are resident in HBM before the timed region starts.
@@ -52,19 +62,28 @@ def log(*a):
 
 # ------------------------------------------------------------------ decode
 
-def prefill_cache(ctx, spec, seed=11):
-    rng = np.random.default_rng([seed, 0xCAC4E])
+def kv_rows(spec, n, seed, layer):
+    rng = np.random.default_rng([seed, 0xCAC4E, layer])
     kvd = spec.n_head_kv * spec.head_dim
+    k = rng.standard_normal((n, kvd), dtype=np.float32).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal((n, kvd), dtype=np.float32).astype(np.float16).astype(np.float32)
+    return k, v
+
+
+def prefill_cache(set_kv, set_pos, spec, n, seed=11, shared=False):
+    """f16 N(0,1) rows 0..n-1 of every layer's K and V cache; shared: the
+    same rows in every layer (the larger models, where drawing
+    n_layer distinct caches would dominate the run)."""
+    kv = kv_rows(spec, n, seed, 0) if shared else None
     for layer in range(spec.n_layer):
-        k = rng.standard_normal((PREFILL, kvd), dtype=np.float32).astype(np.float16)
-        v = rng.standard_normal((PREFILL, kvd), dtype=np.float32).astype(np.float16)
-        ctx.set_kv(layer, 0, k.astype(np.float32), v.astype(np.float32))
-    ctx.set_position(PREFILL)
+        k, v = kv if shared else kv_rows(spec, n, seed, layer)
+        set_kv(layer, k, v)
+    set_pos(n)
 
 
-def time_decode(ctx, steps, warmup, exact):
+def time_decode(ctx, prefill, steps, warmup, exact):
     ctx.set_attention(exact)
-    ctx.set_position(PREFILL)
+    ctx.set_position(prefill)
     tok = 1
     if warmup:
         tok = int(ctx.decode_greedy(tok, warmup)[-1])
@@ -72,6 +91,75 @@ def time_decode(ctx, steps, warmup, exact):
     ids = ctx.decode_greedy(tok, steps)
     dt = time.perf_counter() - t0
     return dt, ids
+
+
+def token_bytes(spec, mean_pos):
+    """Algorithmic HBM bytes of one decode token: every linear weight and the
+    output head in their GGUF bytes, the norm vectors, one embedding row and
+    the K and V cache rows attention reads (f32)."""
+    b = 0
+    for name, ne0, ne1, gt in synth.tensor_list(spec):
+        rb = synth.row_bytes(gt, ne0)
+        b += rb if name == "token_embd.weight" else max(ne1, 1) * rb
+    return b + 2 * spec.n_layer * int(mean_pos) * spec.n_head_kv * spec.head_dim * 4
+
+
+def model_file(workdir, spec):
+    path = synth.path_in(workdir, spec)
+    if not os.path.exists(path):
+        t0 = time.perf_counter()
+        synth.write_gguf(path, spec)
+        log(f"bench: wrote {path} ({os.path.getsize(path) / 1e9:.2f} GB) in "
+            f"{time.perf_counter() - t0:.1f} s")
+    return path
+
+
+def extra_case(workdir, name, prefill, steps, warmup, verify):
+    """Greedy decode of one of the larger models after `prefill` cached
+    positions (and, with verify, the 8-token pass: fox_eval of 8 drafted
+    tokens, the last position's logits)."""
+    spec = synth.spec(name, n_ctx=prefill + warmup + steps + 16)
+    path = model_file(workdir, spec)
+    t0 = time.perf_counter()
+    model = rf.Model(path, mode=rf.WEIGHTS_DEVICE)
+    ctx = model.context(spec.n_ctx, n_batch=8)
+    prefill_cache(lambda l, k, v: ctx.set_kv(l, 0, k, v), ctx.set_position, spec, prefill,
+                  shared=True)
+    log(f"bench: {name} HBM load + cache prefill {time.perf_counter() - t0:.1f} s")
+    dt, ids = time_decode(ctx, prefill, steps, warmup, exact=True)
+    tok_s = steps / dt
+    gbs = token_bytes(spec, prefill + warmup + steps / 2) * tok_s / 1e9
+    out = {"workload": f"{name}-class dense decoder ({spec.n_layer} layers, d_model "
+                       f"{spec.n_embd}, {spec.n_head}/{spec.n_head_kv} heads x {spec.head_dim}, "
+                       f"ffn {spec.n_ff}, vocab {spec.n_vocab}), batch 1, greedy decode after "
+                       f"{prefill} cached positions (f16 N(0,1) rows, the same in every layer)",
+           "tok_s": round(tok_s, 2), "ms_per_token": round(dt * 1e3 / steps, 3),
+           "steps": steps, "decode_hbm_gbs": round(gbs, 1),
+           "frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4),
+           "greedy_ids_head": [int(i) for i in ids[:4]]}
+    log(f"bench: {name} decode {tok_s:.1f} tok/s, {gbs:.0f} GB/s")
+    if verify:
+        reps = 8
+        draft = np.array(ids[:8], np.uint32)
+        times = []
+        for _ in range(reps):
+            ctx.set_position(prefill)
+            t0 = time.perf_counter()
+            ctx.eval(draft)
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        gbs8 = token_bytes(spec, prefill + 4) / med / 1e9
+        out["verify8"] = {"tokens_per_pass": 8, "ms_per_pass": round(med * 1e3, 3),
+                          "tok_s": round(8 / med, 2), "weight_and_kv_gbs": round(gbs8, 1),
+                          "passes": reps,
+                          "note": "fox_eval of 8 drafted tokens at position " + str(prefill) +
+                                  ": one pass over the weights for all 8 (int8 MFMA columns), "
+                                  "last position's logits copied to the host"}
+        log(f"bench: {name} 8-token verify {8 / med:.1f} tok/s ({med * 1e3:.2f} ms per pass)")
+    ctx.close()
+    model.close()
+    os.remove(path)
+    return out
 
 
 # --------------------------------------------------------------- GEMV bench
@@ -191,35 +279,113 @@ def cpu_threads():
     return max(1, min(n, 256))
 
 
-def cpu_baseline(path, spec, budget_s):
+def host_info():
+    """CPU model, logical CPUs, sockets/cores and NUMA layout (lscpu)."""
+    info = {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k in ("Model name", "CPU(s)", "Socket(s)", "Core(s) per socket",
+                     "Thread(s) per core", "NUMA node(s)") or k.startswith("NUMA node") and "CPU" in k:
+                info[k] = v
+    except Exception as e:  # the baseline stands without it
+        info["error"] = str(e)
+    info["affinity_cpus"] = len(os.sched_getaffinity(0))
+    return info
+
+
+def timed_tokens(step, budget_s, max_tokens, min_tokens=2, warm=True):
+    """Median seconds per call of step() (after one untimed call when warm),
+    as many calls as fit the budget (between min_tokens and max_tokens)."""
+    if warm:
+        step()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < max_tokens and (len(times) < min_tokens or
+                                       time.perf_counter() - t_start < budget_s):
+        times.append(step())
+    return statistics.median(times), len(times)
+
+
+def cpu_port(path, spec, threads, budget_s, max_tokens, min_tokens=2, warm=True):
+    """The oracle (oracle/liboracle.so, the C restatement of RustFox's path)
+    decoding the same file after the same injected cache rows."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from oracle_libs import Oracle  # test infrastructure: the oracle, timed as the CPU baseline
+    om = Oracle().model(spec, synth.map_tensors(path, spec))
+    ctx = om.context(PREFILL + max_tokens + 8, n_batch=8, n_threads=threads)
+    prefill_cache(lambda l, k, v: ctx.set_kv(l, 0, k, v), ctx.set_pos, spec, PREFILL)
+    state = {"tok": 1}
+
+    def step():
+        t0 = time.perf_counter()
+        lg = ctx.eval(np.array([state["tok"]], np.uint32))
+        dt = time.perf_counter() - t0
+        state["tok"] = int(np.argmax(lg))
+        return dt
+    med, n = timed_tokens(step, budget_s, max_tokens, min_tokens, warm)
+    ctx.close()
+    return med, n
+
+
+def cpu_reference(path, threads, budget_s, max_tokens, min_tokens=2):
+    """RustFox itself (oracle/_ref, built from its sources) decoding the same
+    file from position 1 (its cache cannot be pre-filled)."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from oracle_libs import REF_FAST_SO, Ref  # test infrastructure: the reference
-    threads = cpu_threads()
     if not os.path.exists(REF_FAST_SO):
         return None
     ref = Ref(REF_FAST_SO)
     m = ref.open_model(path)
     ctx = m.context(64, n_batch=32, n_threads=threads)
-    t0 = time.perf_counter()
-    ctx.eval(np.array([1], np.uint32))        # first touch loads the weights
-    load_s = time.perf_counter() - t0
-    times = []
-    tok = 2
-    t_start = time.perf_counter()
-    while len(times) < 16 and (time.perf_counter() - t_start) < budget_s:
-        lg = ctx.eval(np.array([tok], np.uint32))
-        times.append(ctx.last_seconds())
-        tok = int(np.argmax(lg))
+    state = {"tok": 1}
+
+    def step():
+        lg = ctx.eval(np.array([state["tok"]], np.uint32))
+        state["tok"] = int(np.argmax(lg))
+        return ctx.last_seconds()
+    med, n = timed_tokens(step, budget_s, max_tokens, min_tokens)
     ctx.close()
     m.close()
-    med = statistics.median(times)
-    return {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": threads,
-            "kind": "reference",
-            "sample": (f"RustFox fox_eval (built from its sources, -O3 -march=x86-64-v3, "
-                       f"threadpool of {threads}) on the same 4B TQ1_0 GGUF, single-token "
-                       f"decode at positions 1..{len(times)} (its cache cannot be pre-filled, "
-                       f"so attention reads <= {len(times) + 1} rows instead of 2048+), median "
-                       f"of {len(times)} tokens; weight load {load_s:.1f} s excluded")}
+    return med, n
+
+
+def cpu_baseline(path, spec, budget_s):
+    threads = cpu_threads()
+    med, n = cpu_port(path, spec, threads, budget_s * 0.25, 16)
+    log(f"bench: cpu port {1 / med:.3f} tok/s on {threads} threads ({n} tokens)")
+    # one token on one thread (its pages are already in from the run above)
+    med1, n1 = cpu_port(path, spec, 1, 0.0, 1, min_tokens=1, warm=False)
+    log(f"bench: cpu port {1 / med1:.3f} tok/s on 1 thread ({n1} tokens)")
+    out = {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+           "sample": (f"the oracle (oracle/liboracle.so, the C restatement of RustFox's decode "
+                      f"path, -O2, GEMV rows and attention heads split over a pool of {threads} "
+                      f"threads as RustFox splits them) decoding the same 4B TQ1_0 GGUF after "
+                      f"the same {PREFILL} injected f16 N(0,1) cache rows: median of {n} "
+                      f"single-token steps at positions {PREFILL + 1}..{PREFILL + n} (one "
+                      f"untimed step first)"),
+           "one_thread": {"value": round(1.0 / med1, 4), "unit": "tok/s", "tokens": n1,
+                          "note": "one step at position " + str(PREFILL + 1)},
+           "host": host_info()}
+    try:
+        r = cpu_reference(path, threads, budget_s * 0.15, 16)
+        r1 = cpu_reference(path, 1, 0.0, 1, min_tokens=1) if r else None
+        if r:
+            out["reference_short_context"] = {
+                "value": round(1.0 / r[0], 3), "unit": "tok/s", "cores": threads,
+                "one_thread": round(1.0 / r1[0], 4) if r1 else None,
+                "sample": (f"RustFox's own fox_eval (built from its sources, -O3 "
+                           f"-march=x86-64-v3) on the same file, threadpool of {threads}: "
+                           f"median of {r[1]} steps at positions 2..{r[1] + 1}; its cache "
+                           f"cannot be pre-filled, so attention reads at most {r[1] + 2} "
+                           f"rows instead of {PREFILL}+")}
+            log(f"bench: cpu reference {1 / r[0]:.3f} tok/s on {threads} threads at short "
+                f"context")
+    except Exception as e:  # the port's figure stands without it
+        log(f"bench: reference timing failed: {e}")
+    return out
 
 
 # --------------------------------------------------------------------- main
@@ -229,7 +395,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--cpu-seconds", type=float, default=40.0)
+    ap.add_argument("--extra-steps", type=int, default=32,
+                    help="decode steps of the 8B- and 27B-class runs")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the 8B- and 27B-class runs")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
     ap.add_argument("--workdir", default=None)
@@ -253,26 +423,30 @@ def main():
 
     spec = synth.spec("4b", n_ctx=PREFILL + a.warmup + a.steps)
     workdir = a.workdir or tempfile.mkdtemp(prefix="foxbench-", dir="/tmp")
-    path = synth.path_in(workdir, spec)
-    t0 = time.perf_counter()
-    if not os.path.exists(path):
-        synth.write_gguf(path, spec)
-    log(f"bench: model file {path} ({os.path.getsize(path) / 1e9:.2f} GB) "
-        f"in {time.perf_counter() - t0:.1f} s")
+    path = model_file(workdir, spec)
 
     t0 = time.perf_counter()
     model = rf.Model(path, mode=rf.WEIGHTS_DEVICE)
     ctx = model.context(spec.n_ctx, n_batch=8)
-    prefill_cache(ctx, spec)
+    prefill_cache(lambda l, k, v: ctx.set_kv(l, 0, k, v), ctx.set_position, spec, PREFILL)
     log(f"bench: HBM load + cache prefill {time.perf_counter() - t0:.1f} s")
 
-    dt, ids = time_decode(ctx, a.steps, a.warmup, exact=True)
+    dt, ids = time_decode(ctx, PREFILL, a.steps, a.warmup, exact=True)
     tok_s = a.steps / dt
     log(f"bench: exact attention  {tok_s:.1f} tok/s ({dt * 1e3 / a.steps:.3f} ms/token)")
-    dt_split, ids_split = time_decode(ctx, a.steps, a.warmup, exact=False)
+    dt_split, ids_split = time_decode(ctx, PREFILL, a.steps, a.warmup, exact=False)
     log(f"bench: split attention  {a.steps / dt_split:.1f} tok/s")
     ctx.close()
     model.close()
+
+    extra = {}
+    if not a.no_extra:
+        for name, pre, verify in (("8b", 4096, False), ("27b", 8192, True)):
+            try:
+                extra[name] = extra_case(workdir, name, pre, a.extra_steps, 4, verify)
+            except Exception as e:  # the headline stands without it
+                log(f"bench: {name} run failed: {e}")
+                extra[name] = {"error": str(e)}
 
     gemv = []
     roof = None
@@ -311,9 +485,7 @@ def main():
         except OSError:
             pass
 
-    per_token_bytes = (766_402_560 + 777_912_320 + 747_520
-                       + 2 * spec.n_layer * (PREFILL + a.warmup + a.steps // 2)
-                       * spec.n_head_kv * spec.head_dim * 4)
+    per_token_bytes = token_bytes(spec, PREFILL + a.warmup + a.steps / 2)
     line = {
         "metric": "decode tok/s on 1 MI355X; quantized-GEMV HBM GB/s as % of peak",
         "value": round(tok_s, 2),
@@ -337,6 +509,8 @@ def main():
         "cpu_baseline": cpu,
         "split_attention_tok_s": round(a.steps / dt_split, 2),
         "decode_hbm_gbs": round(per_token_bytes * tok_s / 1e9, 1),
+        "decode_frac_of_hbm": round(per_token_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),
+        "extra": extra,
         "gemv": gemv,
         "greedy_ids_head": [int(i) for i in ids[:8]],
     }

@@ -734,9 +734,10 @@ static void project(or_context *c, const or_tensor *t, size_t rows, size_t cols,
                 out + i * out_stride, c->n_threads);
 }
 
-/* src/forward.c:222-257 for one head: scores, softmax, j-ordered V sum */
+/* src/forward.c:222-257 for one head: scores, softmax, j-ordered V sum;
+ * att is n_ctx floats of scratch */
 static void attend_head(or_context *c, size_t layer, size_t tok, size_t h,
-                        uint32_t seq_pos)
+                        uint32_t seq_pos, float *att)
 {
     const or_model *m = c->m;
     size_t hd = m->head_dim, kvh = h / c->gqa, j, d;
@@ -747,20 +748,39 @@ static void attend_head(or_context *c, size_t layer, size_t tok, size_t h,
     size_t upto = (size_t)seq_pos + 1;
 
     for (j = 0; j < upto; j++)
-        c->att[j] = or_dot_f32(qh, c->kc + base + j * c->nkv + kvh * hd, hd) * scale;
-    or_softmax(c->att, upto);
+        att[j] = or_dot_f32(qh, c->kc + base + j * c->nkv + kvh * hd, hd) * scale;
+    or_softmax(att, upto);
     for (d = 0; d < hd; d++) dst[d] = 0.0f;
     for (j = 0; j < upto; j++) {
         const float *vj = c->vc + base + j * c->nkv + kvh * hd;
-        for (d = 0; d < hd; d++) dst[d] += c->att[j] * vj[d];
+        for (d = 0; d < hd; d++) dst[d] += att[j] * vj[d];
     }
+}
+
+/* the heads of one token split over the pool like the reference's
+ * attention (src/forward.c:364-371): heads are independent, so the split
+ * changes no result */
+typedef struct {
+    or_context *c;
+    size_t layer, tok;
+    uint32_t seq_pos;
+} attn_job;
+
+static void attend_slice(void *p, size_t begin, size_t end)
+{
+    attn_job *j = (attn_job *)p;
+    float *att = begin == 0 ? j->c->att : (float *)malloc((size_t)j->c->n_ctx * 4);
+    size_t h;
+    if (!att) return;
+    for (h = begin; h < end; h++) attend_head(j->c, j->layer, j->tok, h, j->seq_pos, att);
+    if (att != j->c->att) free(att);
 }
 
 /* src/forward.c:295-409 */
 static int forward_batch(or_context *c, const uint32_t *tok, size_t n, int want_logits)
 {
     const or_model *m = c->m;
-    size_t d = m->n_embd, i, h;
+    size_t d = m->n_embd, i;
     uint32_t l;
     const float *w;
     size_t erow = or_row_bytes(m->token_embd.type, d);
@@ -794,9 +814,11 @@ static int forward_batch(or_context *c, const uint32_t *tok, size_t n, int want_
             memcpy(c->kc + base + (size_t)p * c->nkv, c->kb + i * c->nkv, c->nkv * 4);
             memcpy(c->vc + base + (size_t)p * c->nkv, c->vb + i * c->nkv, c->nkv * 4);
         }
-        for (i = 0; i < n; i++)
-            for (h = 0; h < m->n_head; h++)
-                attend_head(c, l, i, h, c->pos + (uint32_t)i);
+        for (i = 0; i < n; i++) {
+            attn_job job;
+            job.c = c; job.layer = l; job.tok = i; job.seq_pos = c->pos + (uint32_t)i;
+            parallel_rows(m->n_head, c->n_threads, attend_slice, &job);
+        }
 
         project(c, &L->attn_out, d, c->nq, n, c->xb, c->wide, c->xb2, c->wide);
         for (i = 0; i < n; i++) or_add(c->x + i * d, c->xb2 + i * c->wide, d);

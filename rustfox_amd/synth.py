@@ -359,11 +359,9 @@ def _kv_str(key, v):
     return struct.pack("<Q", len(k)) + k + struct.pack("<IQ", _GGUF_STR, len(b)) + b
 
 
-def write_gguf(path: str, s: ModelSpec, alignment: int = 32, tensors=None) -> dict:
-    """Write the model as a GGUF v3 file; returns {name: bytes ndarray} only
-    when tensors == {} is passed in to collect them.  Row ranges of large
-    tensors are generated by a pool of worker processes (the bytes do not
-    depend on the number of workers)."""
+def gguf_header(s: ModelSpec, alignment: int = 32):
+    """(header bytes including the padding to the data section, tensor
+    offsets from the data section's start) of the file write_gguf writes."""
     tl = tensor_list(s)
     meta = [
         _kv_u32("general.alignment", alignment),
@@ -392,7 +390,28 @@ def write_gguf(path: str, s: ModelSpec, alignment: int = 32, tensors=None) -> di
         off += nbytes
     head = (b"GGUF" + struct.pack("<IQQ", 3, len(tl), len(meta)) + b"".join(meta)
             + b"".join(infos))
-    pad = (-len(head)) % alignment
+    return head + b"\0" * ((-len(head)) % alignment), offsets
+
+
+def map_tensors(path: str, s: ModelSpec, alignment: int = 32) -> dict:
+    """{name: read-only uint8 array} over a file write_gguf wrote, memory
+    mapped (no copy)."""
+    head, offsets = gguf_header(s, alignment)
+    mm = np.memmap(path, dtype=np.uint8, mode="r")
+    out = {}
+    for (name, ne0, ne1, gt), o in zip(tensor_list(s), offsets):
+        a = len(head) + o
+        out[name] = mm[a:a + max(ne1, 1) * row_bytes(gt, ne0)]
+    return out
+
+
+def write_gguf(path: str, s: ModelSpec, alignment: int = 32, tensors=None) -> dict:
+    """Write the model as a GGUF v3 file; returns {name: bytes ndarray} only
+    when tensors == {} is passed in to collect them.  Row ranges of large
+    tensors are generated by a pool of worker processes (the bytes do not
+    depend on the number of workers)."""
+    tl = tensor_list(s)
+    head, offsets = gguf_header(s, alignment)
     jobs = [(i, r0, r1) for i, (name, ne0, ne1, gt) in enumerate(tl)
             for r0, r1 in tensor_chunks(ne0, ne1)]
     nw = _workers() if sum(max(t[2], 1) * t[1] for t in tl) > 4 * CHUNK_ELEMS else 1
@@ -408,9 +427,7 @@ def write_gguf(path: str, s: ModelSpec, alignment: int = 32, tensors=None) -> di
                     yield i, make_chunk(s, i, *tl[i], r0, r1)
                 return
             window = []
-            it = iter(jobs)
-            for job in it:
-                i, r0, r1 = job
+            for i, r0, r1 in jobs:
                 window.append((i, pool.submit(_chunk_job, (s, i, *tl[i], r0, r1))))
                 if len(window) >= 2 * nw:
                     j, f = window.pop(0)
@@ -419,7 +436,7 @@ def write_gguf(path: str, s: ModelSpec, alignment: int = 32, tensors=None) -> di
                 yield j, f.result()
 
         with open(path, "wb") as f:
-            f.write(head + b"\0" * pad)
+            f.write(head)
             pos = 0
             parts = {}
             for i, data in results():
