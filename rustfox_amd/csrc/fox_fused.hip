@@ -104,7 +104,8 @@ __device__ __forceinline__ void wave_sum_n(int (&v)[N])
     for (int i = 0; i < N; i++) v[i] = read_lane(v[i], 63);
 }
 
-#define R4_LIMIT 8              // input dwords per thread: K <= 4 * R4_LIMIT * FWG
+#define R4_LIMIT 11             // input dwords per thread: K <= 4 * R4_LIMIT * FWG
+#define R4_LIMIT_NORM 8         // with the RMSNorm weights also held: K <= 16384
 
 // Where lane dl's int8 dword (block-local elements 4 dl .. 4 dl + 3) goes in
 // a block's B operand for one token, as a byte offset from the block's
@@ -726,8 +727,13 @@ static bool fused_aligned(const void *x, size_t x_stride, size_t M, const void *
     return !((uintptr_t)x % 16) && !((uintptr_t)w % 16) && (M == 1 || x_stride % 4 == 0);
 }
 
-static fox_gpu_status fused_check(int type, size_t K, size_t M, int nslab, int *fmt)
+static fox_gpu_status fused_check(int type, size_t K, size_t M, int nslab, int *fmt,
+                                  bool norm = false)
 {
+    if (norm && K > 4 * R4_LIMIT_NORM * FWG)
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "fused gemv: K = %zu exceeds the %d values "
+                        "one workgroup holds beside the norm weights", K,
+                        4 * R4_LIMIT_NORM * FWG);
     *fmt = fmt_of(type);
     if (*fmt != FMT_TQ2)
         return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "fused gemv: %s weights use the unfused path",
@@ -767,7 +773,8 @@ static fox_gpu_status fused_go_r(fox_gpu_ctx *ctx, FusedArgs a, int n_work)
     return FOX_GPU_OK;
 }
 
-// the input registers per thread fit K: 1, 2, 3, 5 or 8 dwords
+// the input registers per thread fit K: 1, 2, 3, 5, 8 or (without the
+// norm weights beside the input) 11 dwords
 template <int FMT, int IN, int EPI>
 static fox_gpu_status fused_go(fox_gpu_ctx *ctx, const FusedArgs &a, int grid)
 {
@@ -776,7 +783,8 @@ static fox_gpu_status fused_go(fox_gpu_ctx *ctx, const FusedArgs &a, int grid)
     if (per <= 2) return fused_go_r<FMT, IN, EPI, 2>(ctx, a, grid);
     if (per <= 3) return fused_go_r<FMT, IN, EPI, 3>(ctx, a, grid);
     if (per <= 5) return fused_go_r<FMT, IN, EPI, 5>(ctx, a, grid);
-    return fused_go_r<FMT, IN, EPI, 8>(ctx, a, grid);
+    if (per <= 8 || IN == IN_NORM) return fused_go_r<FMT, IN, EPI, 8>(ctx, a, grid);
+    return fused_go_r<FMT, IN, EPI, 11>(ctx, a, grid);
 }
 
 template <int IN, int EPI>
@@ -866,7 +874,7 @@ extern "C" fox_gpu_status fox_gpu_gemv_rmsnorm(fox_gpu_ctx *ctx, size_t n,
     const size_t K = (size_t)ws[0]->ne0;
     if (M > 1 && x_stride < K) return fox_fail(FOX_GPU_ERR_ARG, "gemv_rmsnorm: input stride < K");
     int fmt;
-    fox_gpu_status st = fused_check(ws[0]->type, K, M, 1, &fmt);
+    fox_gpu_status st = fused_check(ws[0]->type, K, M, 1, &fmt, true);
     if (st) return st;
     if (!fused_aligned(x, x_stride, M, norm_w))
         return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "gemv_rmsnorm: x and norm_w must be 16-byte "
@@ -917,7 +925,7 @@ extern "C" fox_gpu_status fox_gpu_qkv_rope(fox_gpu_ctx *ctx, const fox_gpu_tenso
         return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: stride too small");
     if (n_ctx > 0x7fffffff) return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: n_ctx too large");
     int fmt;
-    fox_gpu_status st = fused_check(wq->type, K, M, 1, &fmt);
+    fox_gpu_status st = fused_check(wq->type, K, M, 1, &fmt, true);
     if (st) return st;
     if (!fused_aligned(x, x_stride, M, norm_w))
         return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "qkv_rope: x and norm_w must be 16-byte "
@@ -970,7 +978,7 @@ extern "C" fox_gpu_status fox_gpu_gate_up_silu(fox_gpu_ctx *ctx, const fox_gpu_t
     if (M > 1 && (x_stride < K || h_stride < wg->ne1))
         return fox_fail(FOX_GPU_ERR_ARG, "gate_up_silu: stride too small");
     int fmt;
-    fox_gpu_status st = fused_check(wg->type, K, M, 2, &fmt);
+    fox_gpu_status st = fused_check(wg->type, K, M, 2, &fmt, true);
     if (st) return st;
     if (!fused_aligned(x, x_stride, M, norm_w))
         return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "gate_up_silu: x and norm_w must be 16-byte "

@@ -31,8 +31,13 @@
 
 // ---------------------------------------------------- activation prep
 
-// One workgroup per token: quantise (or copy a given q), then lay the int8
-// values out as the MFMA B operand of format FMT plus per-block integer sums.
+// Workgroup (x, t) takes blocks [x AP_BLOCKS, ...) of token t: quantise (or
+// copy a given q) its slice, then lay the int8 values out as the MFMA B
+// operand of format FMT plus per-block integer sums.  The per-256 scales of
+// the K-quants depend on one block each; the per-vector scale of the ternary
+// formats depends on the whole token, so every workgroup first takes the
+// amax over all of it (a read of K floats, shared through L2).
+#define AP_BLOCKS 8
 template <int FMT>
 __global__ __launch_bounds__(512) void act_prep(const float *__restrict__ x, int x_stride,
                                                int K, int M, const int8_t *__restrict__ q_in,
@@ -42,18 +47,23 @@ __global__ __launch_bounds__(512) void act_prep(const float *__restrict__ x, int
                                                uint8_t *__restrict__ B,
                                                int32_t *__restrict__ aux)
 {
-    extern __shared__ int8_t qbuf[];
+    __shared__ int8_t qall[AP_BLOCKS * 256];
     __shared__ float red[16];
-    const int t = blockIdx.x, tid = threadIdx.x, nthr = blockDim.x;
+    const int t = blockIdx.y, tid = threadIdx.x, nthr = blockDim.x;
     const int lane = tid & 63, wave = tid >> 6, nwaves = nthr >> 6;
     const int nb = K >> 8;
     const bool per_block = (FMT == FMT_Q4K || FMT == FMT_Q6K);
+    // this workgroup's blocks and elements (a ragged tail of K belongs to the
+    // last workgroup: it is quantised, and has no block to go into)
+    const int b0 = blockIdx.x * AP_BLOCKS, b1 = min(nb, b0 + AP_BLOCKS);
+    const int e0 = b0 * 256, e1 = blockIdx.x + 1 == gridDim.x ? K : b1 * 256;
+    int8_t *qbuf = qall - e0;                      // indexed by absolute element, e0 <= i < e1
 
     if (q_in) {
-        for (int i = tid; i < K; i += nthr) qbuf[i] = q_in[(size_t)t * K + i];
+        for (int i = e0 + tid; i < e1; i += nthr) qbuf[i] = q_in[(size_t)t * K + i];
         if (scale_in && per_block) {
-            for (int b = tid; b < nb; b += nthr) scale_out[(size_t)t * nb + b] = scale_in[(size_t)t * nb + b];
-        } else if (scale_in && tid == 0) {
+            for (int b = b0 + tid; b < b1; b += nthr) scale_out[(size_t)t * nb + b] = scale_in[(size_t)t * nb + b];
+        } else if (scale_in && tid == 0 && blockIdx.x == 0) {
             scale_out[t] = scale_in[t];
         }
     } else if (!per_block) {
@@ -74,16 +84,16 @@ __global__ __launch_bounds__(512) void act_prep(const float *__restrict__ x, int
         __syncthreads();
         float amax = red[15];
         if (!(amax > 0.0f)) {
-            for (int i = tid; i < K; i += nthr) qbuf[i] = 0;
-            if (tid == 0) scale_out[t] = 0.0f;
+            for (int i = e0 + tid; i < e1; i += nthr) qbuf[i] = 0;
+            if (tid == 0 && blockIdx.x == 0) scale_out[t] = 0.0f;
         } else {
             float inv = (float)(127.0 / (double)amax);
-            for (int i = tid; i < K; i += nthr) qbuf[i] = quant_one(xt[i], inv);
-            if (tid == 0) scale_out[t] = (float)((double)amax / 127.0);
+            for (int i = e0 + tid; i < e1; i += nthr) qbuf[i] = quant_one(xt[i], inv);
+            if (tid == 0 && blockIdx.x == 0) scale_out[t] = (float)((double)amax / 127.0);
         }
     } else {
         const float *xt = x + (size_t)t * x_stride;
-        for (int b = wave; b < nb; b += nwaves) {
+        for (int b = b0 + wave; b < b1; b += nwaves) {
             float v[4], m = 0.0f;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
@@ -106,13 +116,13 @@ __global__ __launch_bounds__(512) void act_prep(const float *__restrict__ x, int
     }
     __syncthreads();
     if (q_out && !q_in)
-        for (int i = tid; i < K; i += nthr) q_out[(size_t)t * K + i] = qbuf[i];
+        for (int i = e0 + tid; i < e1; i += nthr) q_out[(size_t)t * K + i] = qbuf[i];
 
     // ---- B operand
     if (FMT == FMT_TQ2) {
-        const int items = nb * 16;  // (b, u, g)
+        const int items = (b1 - b0) * 16;  // (b, u, g)
         for (int it = tid; it < items; it += nthr) {
-            int g = it & 3, u = (it >> 2) & 3, b = it >> 4;
+            int g = it & 3, u = (it >> 2) & 3, b = b0 + (it >> 4);
             uint32_t w4[4];
 #pragma unroll
             for (int l = 0; l < 4; l++) {
@@ -128,15 +138,15 @@ __global__ __launch_bounds__(512) void act_prep(const float *__restrict__ x, int
             size_t off = ((((size_t)b * 4 + u) * 4 + g) * M + t) * 16;
             *(uint4 *)(B + off) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
         }
-        for (int b = wave; b < nb; b += nwaves) {
+        for (int b = b0 + wave; b < b1; b += nwaves) {
             const int8_t *qb = qbuf + b * 256;
             int a = wave_sum_i(qb[lane] + qb[lane + 64] + qb[lane + 128] + qb[lane + 192]);
             if (lane == 0) aux[(size_t)b * M + t] = -a;
         }
     } else if (FMT == FMT_Q4K) {
-        const int items = nb * 32;  // (b, p, g, c)
+        const int items = (b1 - b0) * 32;  // (b, p, g, c)
         for (int it = tid; it < items; it += nthr) {
-            int c = it & 1, g = (it >> 1) & 3, p = (it >> 3) & 3, b = it >> 5;
+            int c = it & 1, g = (it >> 1) & 3, p = (it >> 3) & 3, b = b0 + (it >> 5);
             const int8_t *src = qbuf + b * 256 + 64 * p + 32 * c + 8 * g;
             uint32_t lo0 = 0, lo1 = 0;
 #pragma unroll
@@ -148,16 +158,16 @@ __global__ __launch_bounds__(512) void act_prep(const float *__restrict__ x, int
             size_t off = ((((size_t)b * 4 + p) * 4 + g) * (2 * M) + 2 * t + c) * 16;
             *(uint4 *)(B + off) = v;
         }
-        for (int it = wave; it < nb * 8; it += nwaves) {
+        for (int it = b0 * 8 + wave; it < b1 * 8; it += nwaves) {
             int b = it >> 3, j = it & 7;
             int a = lane < 32 ? qbuf[b * 256 + 32 * j + lane] : 0;
             a = wave_sum_i(a);
             if (lane == 0) aux[((size_t)b * 8 + j) * M + t] = a;
         }
     } else {  // FMT_Q6K: diagonal blocks only
-        const int items = nb * 16;  // (b, v, g)
+        const int items = (b1 - b0) * 16;  // (b, v, g)
         for (int it = tid; it < items; it += nthr) {
-            int g = it & 3, v = (it >> 2) & 3, b = it >> 4;
+            int g = it & 3, v = (it >> 2) & 3, b = b0 + (it >> 4);
             int h = v >> 1, s = v & 1;
             const int8_t *src = qbuf + b * 256 + 128 * h + 32 * g + 16 * s;
             uint32_t w4[4];
@@ -171,7 +181,7 @@ __global__ __launch_bounds__(512) void act_prep(const float *__restrict__ x, int
             size_t off = ((((size_t)b * 4 + v) * 4 + g) * M + t) * 16;
             *(uint4 *)(B + off) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
         }
-        for (int it = wave; it < nb * 16; it += nwaves) {
+        for (int it = b0 * 16 + wave; it < b1 * 16; it += nwaves) {
             int b = it >> 4, v = (it >> 2) & 3, g = it & 3;
             int h = v >> 1, s = v & 1;
             int a = lane < 16 ? qbuf[b * 256 + 128 * h + 32 * g + 16 * s + lane] : 0;
@@ -565,22 +575,22 @@ static fox_gpu_status launch_prep(fox_gpu_ctx *ctx, int fmt, const float *x, siz
                                   const int8_t *q_in, const float *scale_in, size_t K,
                                   size_t M, const Ws &w, int8_t *q_out, float *scale_out)
 {
-    dim3 grid((unsigned)M), block(512);
-    size_t lds = align_up(K, 16);
-    if (lds > 65536 - 256)
-        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "gemv: K = %zu exceeds the 65536 "
-                        "activation values one workgroup stages", K);
+    // workgroups of AP_BLOCKS blocks (AP_BLOCKS * 256 values); a ragged tail
+    // of K (values beyond the last whole block) is quantised by the last
+    const size_t nwg = (K + AP_BLOCKS * 256 - 1) / (AP_BLOCKS * 256);
+    if (K > (1u << 24)) return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "gemv: K = %zu too large", K);
+    dim3 grid((unsigned)nwg, (unsigned)M), block(512);
     switch (fmt) {
     case FMT_TQ2:
-        hipLaunchKernelGGL(act_prep<FMT_TQ2>, grid, block, lds, ctx->stream, x, (int)x_stride,
+        hipLaunchKernelGGL(act_prep<FMT_TQ2>, grid, block, 0, ctx->stream, x, (int)x_stride,
                            (int)K, (int)M, q_in, scale_in, q_out, scale_out, w.B, w.aux);
         break;
     case FMT_Q4K:
-        hipLaunchKernelGGL(act_prep<FMT_Q4K>, grid, block, lds, ctx->stream, x, (int)x_stride,
+        hipLaunchKernelGGL(act_prep<FMT_Q4K>, grid, block, 0, ctx->stream, x, (int)x_stride,
                            (int)K, (int)M, q_in, scale_in, q_out, scale_out, w.B, w.aux);
         break;
     default:
-        hipLaunchKernelGGL(act_prep<FMT_Q6K>, grid, block, lds, ctx->stream, x, (int)x_stride,
+        hipLaunchKernelGGL(act_prep<FMT_Q6K>, grid, block, 0, ctx->stream, x, (int)x_stride,
                            (int)K, (int)M, q_in, scale_in, q_out, scale_out, w.B, w.aux);
         break;
     }
