@@ -114,6 +114,30 @@ fox_gpu_status fox_gpu_tensor_download(fox_gpu_ctx *ctx, const fox_gpu_tensor *t
                                        void *host, uint64_t bytes);
 void           fox_gpu_tensor_free(fox_gpu_ctx *ctx, fox_gpu_tensor *t);
 
+/* ---------------------------------------------------- streamed weights */
+
+/* The pieces of a streaming weight backend (the GPU form of RustFox's
+ * storage-streamed slots, src/weights.c:248-459, with its layer-ahead
+ * prefetch, src/forward.c:322-337): tensors allocated once and reloaded in
+ * place, pinned host staging, and a second stream (the context's copy
+ * stream) on which uploads run beside the compute stream.
+ *
+ * fox_gpu_tensor_alloc: a device tensor of the given type and shape, its
+ * contents undefined until loaded.
+ * fox_gpu_tensor_load_async: on the copy stream, copy `bytes` GGUF bytes
+ * from `host` (pinned memory from fox_gpu_host_alloc, left untouched until
+ * the copy stream has passed this call) into `dev_stage` (device memory of
+ * at least `bytes`, reused only in copy-stream order) and repack them into
+ * t's device layout.  Nothing waits: order it against compute-stream users
+ * of t with events. */
+fox_gpu_status fox_gpu_tensor_alloc(fox_gpu_ctx *ctx, int type, uint64_t ne0,
+                                    uint64_t ne1, fox_gpu_tensor **out);
+fox_gpu_status fox_gpu_tensor_load_async(fox_gpu_ctx *ctx, fox_gpu_tensor *t,
+                                         const void *host, uint64_t bytes,
+                                         void *dev_stage);
+fox_gpu_status fox_gpu_host_alloc(fox_gpu_ctx *ctx, size_t bytes, void **out);
+fox_gpu_status fox_gpu_host_free(fox_gpu_ctx *ctx, void *p);
+
 /* -------------------------------------------------------- activations */
 
 typedef enum {
@@ -320,6 +344,12 @@ fox_gpu_status fox_gpu_event_create(fox_gpu_ctx *ctx, fox_gpu_event **out);
 fox_gpu_status fox_gpu_event_record(fox_gpu_ctx *ctx, fox_gpu_event *e);
 fox_gpu_status fox_gpu_event_elapsed(fox_gpu_event *start, fox_gpu_event *stop,
                                      float *ms);
+/* Ordering between the compute stream and the copy stream: record on the
+ * copy stream; make the compute stream (on_copy = 0) or the copy stream
+ * (on_copy = 1) wait for an event; wait on the host. */
+fox_gpu_status fox_gpu_event_record_copy(fox_gpu_ctx *ctx, fox_gpu_event *e);
+fox_gpu_status fox_gpu_event_wait(fox_gpu_ctx *ctx, fox_gpu_event *e, int on_copy);
+fox_gpu_status fox_gpu_event_sync(fox_gpu_event *e);
 void           fox_gpu_event_destroy(fox_gpu_event *e);
 
 #ifdef __cplusplus

@@ -79,6 +79,11 @@ extern "C" fox_gpu_status fox_gpu_init(int device, fox_gpu_ctx **out)
         delete ctx;
         return fox_fail(FOX_GPU_ERR_INTERNAL, "init: stream creation failed");
     }
+    if (hipStreamCreateWithFlags(&ctx->copy, hipStreamNonBlocking) != hipSuccess) {
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return fox_fail(FOX_GPU_ERR_INTERNAL, "init: copy stream creation failed");
+    }
     fox_gpu_status st = fox_ws_reserve(ctx, 8u << 20);
     if (st != FOX_GPU_OK) {
         fox_gpu_shutdown(ctx);
@@ -104,6 +109,10 @@ extern "C" void fox_gpu_shutdown(fox_gpu_ctx *ctx)
     if (ctx->stream) {
         (void)hipStreamSynchronize(ctx->stream);
         (void)hipStreamDestroy(ctx->stream);
+    }
+    if (ctx->copy) {
+        (void)hipStreamSynchronize(ctx->copy);
+        (void)hipStreamDestroy(ctx->copy);
     }
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->small) (void)hipFree(ctx->small);
@@ -347,6 +356,37 @@ __global__ void tq2_to_tq1(const uint8_t *__restrict__ src, uint8_t *__restrict_
             q *= 3;
         }
         dst[i] = (uint8_t)((q * 256 + 242) / 243);
+    }
+}
+
+// TQ1_0 GGUF bytes straight into the device chunk layout of the TQ2_0
+// blocks they are held as (tq1_to_tq2 and repack_blocks in one pass): byte
+// o of chunk c is byte k of the TQ2_0 block of tile row r (chunk_source),
+// built from the trits of the TQ1_0 block.
+__global__ void repack_tq1(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                           uint64_t n_rows, uint64_t nb, uint64_t total)
+{
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t c = i / TQ2_CHUNK;
+        const int o = (int)(i - c * TQ2_CHUNK);
+        const uint64_t tile = c / nb, b = c - tile * nb;
+        int r;
+        const int k = chunk_source(FOX_GPU_TQ2_0, o, &r);
+        const uint64_t row = tile * FOX_TILE + (uint64_t)r;
+        if (row >= n_rows) {
+            dst[i] = 0;
+            continue;
+        }
+        const uint8_t *s = src + (row * nb + b) * 54;
+        if (k < 64) {
+            const int h = k >> 5, m = k & 31;
+            int v = 0;
+            for (int l = 0; l < 4; l++) v |= tq1_trit(s, h * 128 + l * 32 + m) << (2 * l);
+            dst[i] = (uint8_t)v;
+        } else {
+            dst[i] = s[52 + (k - 64)];
+        }
     }
 }
 
@@ -599,6 +639,108 @@ extern "C" void fox_gpu_tensor_free(fox_gpu_ctx *ctx, fox_gpu_tensor *t)
     delete t;
 }
 
+// ------------------------------------------------------ streamed weights
+
+static fox_gpu_status tensor_shape(int type, uint64_t ne0, uint64_t ne1, fox_gpu_tensor *t)
+{
+    const size_t be = fox_block_elems(type), bb = fox_block_bytes(type);
+    if (!be)
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "tensor: no device layout for ggml type %d",
+                        type);
+    if (ne0 == 0 || ne0 % be)
+        return fox_fail(FOX_GPU_ERR_ARG, "tensor: %llu columns is not a whole number of %s "
+                        "blocks", (unsigned long long)ne0, fox_type_name(type));
+    t->type = type;
+    t->ne0 = ne0;
+    t->ne1 = ne1 ? ne1 : 1;
+    t->gguf_bytes = t->ne1 * (ne0 / be) * bb;
+    if (fox_is_block_type(type)) {
+        t->n_tiles = (t->ne1 + FOX_TILE - 1) / FOX_TILE;
+        t->dev_bytes = t->n_tiles * (ne0 / 256) * fox_chunk_bytes(type);
+    } else {
+        const uint64_t per = FOX_FCHUNK / bb, nchunk = (ne0 + per - 1) / per;
+        t->n_tiles = (t->ne1 + FOX_FTILE - 1) / FOX_FTILE;
+        t->dev_bytes = t->n_tiles * nchunk * FOX_FTILE * FOX_FCHUNK;
+    }
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_tensor_alloc(fox_gpu_ctx *ctx, int type, uint64_t ne0,
+                                               uint64_t ne1, fox_gpu_tensor **out)
+{
+    if (!ctx || !out) return fox_fail(FOX_GPU_ERR_ARG, "tensor_alloc: bad argument");
+    *out = nullptr;
+    fox_gpu_tensor *t = new (std::nothrow) fox_gpu_tensor();
+    if (!t) return fox_fail(FOX_GPU_ERR_NOMEM, "tensor_alloc: handle");
+    fox_gpu_status st = tensor_shape(type, ne0, ne1, t);
+    if (st == FOX_GPU_OK) st = set_device(ctx);
+    if (st == FOX_GPU_OK && hipMalloc(&t->d, t->dev_bytes) != hipSuccess)
+        st = fox_fail(FOX_GPU_ERR_NOMEM, "tensor_alloc: %llu bytes of HBM",
+                      (unsigned long long)t->dev_bytes);
+    if (st) {
+        delete t;
+        return st;
+    }
+    *out = t;
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_tensor_load_async(fox_gpu_ctx *ctx, fox_gpu_tensor *t,
+                                                    const void *host, uint64_t bytes,
+                                                    void *dev_stage)
+{
+    if (!ctx || !t || !host || !dev_stage)
+        return fox_fail(FOX_GPU_ERR_ARG, "tensor_load_async: bad argument");
+    if (bytes != t->gguf_bytes)
+        return fox_fail(FOX_GPU_ERR_ARG, "tensor_load_async: %s %llux%llu is %llu bytes, %llu "
+                        "were given", fox_type_name(t->type), (unsigned long long)t->ne0,
+                        (unsigned long long)t->ne1, (unsigned long long)t->gguf_bytes,
+                        (unsigned long long)bytes);
+    FOX_HIP(hipMemcpyAsync(dev_stage, host, bytes, hipMemcpyHostToDevice, ctx->copy));
+    const uint8_t *src = (const uint8_t *)dev_stage;
+    if (!fox_is_block_type(t->type)) {
+        const uint64_t es = fox_block_bytes(t->type), n = t->dev_bytes / es;
+        if (es == 2)
+            hipLaunchKernelGGL(repack_float<uint16_t>, dim3(grid_for(n, 256)), dim3(256), 0,
+                               ctx->copy, 0, (const uint16_t *)src, (uint16_t *)t->d, t->ne1,
+                               t->ne0, n);
+        else
+            hipLaunchKernelGGL(repack_float<uint32_t>, dim3(grid_for(n, 256)), dim3(256), 0,
+                               ctx->copy, 0, (const uint32_t *)src, (uint32_t *)t->d, t->ne1,
+                               t->ne0, n);
+    } else if (t->type == FOX_GPU_TQ1_0) {
+        hipLaunchKernelGGL(repack_tq1, dim3(grid_for(t->dev_bytes, 256)), dim3(256), 0,
+                           ctx->copy, src, t->d, t->ne1, t->ne0 / 256, t->dev_bytes);
+    } else {
+        hipLaunchKernelGGL(repack_blocks, dim3(grid_for(t->dev_bytes, 256)), dim3(256), 0,
+                           ctx->copy, t->type, 0, src, t->d, t->ne1, t->ne0 / 256,
+                           (uint64_t)fox_chunk_bytes(t->type), (uint64_t)fox_block_bytes(t->type),
+                           t->dev_bytes);
+    }
+    FOX_LAUNCHED("tensor_load_async");
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_host_alloc(fox_gpu_ctx *ctx, size_t bytes, void **out)
+{
+    if (!ctx || !out || bytes == 0) return fox_fail(FOX_GPU_ERR_ARG, "host_alloc: bad argument");
+    *out = nullptr;
+    fox_gpu_status st = set_device(ctx);
+    if (st) return st;
+    if (hipHostMalloc(out, bytes, hipHostMallocDefault) != hipSuccess) {
+        *out = nullptr;
+        return fox_fail(FOX_GPU_ERR_NOMEM, "host_alloc: %zu bytes of pinned host memory", bytes);
+    }
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_host_free(fox_gpu_ctx *ctx, void *p)
+{
+    if (!ctx) return fox_fail(FOX_GPU_ERR_ARG, "host_free: null context");
+    if (p) FOX_HIP(hipHostFree(p));
+    return FOX_GPU_OK;
+}
+
 // ----------------------------------------------------------------- graphs
 
 extern "C" fox_gpu_status fox_gpu_graph_begin(fox_gpu_ctx *ctx)
@@ -668,6 +810,27 @@ extern "C" fox_gpu_status fox_gpu_event_record(fox_gpu_ctx *ctx, fox_gpu_event *
 {
     if (!ctx || !e) return fox_fail(FOX_GPU_ERR_ARG, "event_record: bad argument");
     FOX_HIP(hipEventRecord(e->ev, ctx->stream));
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_event_record_copy(fox_gpu_ctx *ctx, fox_gpu_event *e)
+{
+    if (!ctx || !e) return fox_fail(FOX_GPU_ERR_ARG, "event_record_copy: bad argument");
+    FOX_HIP(hipEventRecord(e->ev, ctx->copy));
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_event_wait(fox_gpu_ctx *ctx, fox_gpu_event *e, int on_copy)
+{
+    if (!ctx || !e) return fox_fail(FOX_GPU_ERR_ARG, "event_wait: bad argument");
+    FOX_HIP(hipStreamWaitEvent(on_copy ? ctx->copy : ctx->stream, e->ev, 0));
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_event_sync(fox_gpu_event *e)
+{
+    if (!e) return fox_fail(FOX_GPU_ERR_ARG, "event_sync: null event");
+    FOX_HIP(hipEventSynchronize(e->ev));
     return FOX_GPU_OK;
 }
 

@@ -50,6 +50,9 @@ __host__ __device__ inline uint64_t fox_float_offset(uint64_t r, uint64_t k, uin
 struct fox_gpu_ctx {
     int device;
     hipStream_t stream;
+    // second stream for weight uploads of the streaming backend (default
+    // priority, like the compute stream)
+    hipStream_t copy;
     int n_cu;
     // upper bound on the persistent grid of the fused GEMV (0: two
     // workgroups per compute unit); fox_gpu_set_max_workgroups

@@ -82,6 +82,11 @@ static const fox_gpu_tensor *dev_tensor(fox_model *m, size_t idx)
     return m->weights->dev[idx];
 }
 
+static int streaming(const fox_context *c)
+{
+    return c->m->weights->mode == FOX_WEIGHTS_STREAM;
+}
+
 void fox_context_config_default(fox_context_config *cfg, const fox_model *m)
 {
     if (!cfg) return;
@@ -108,10 +113,9 @@ void fox_context_destroy(fox_context *c)
 
 /* device f32 copy of a norm vector into `dst` (src/forward.c:167-186
  * dequantises it per use; it never changes, so it is dequantised once) */
-static fox_status norm_vector(fox_context *c, size_t idx, float *dst)
+static fox_status norm_vector(fox_context *c, const fox_gpu_tensor *t, float *dst)
 {
-    GPU(fox_gpu_get_rows(c->gpu, dev_tensor(c->m, idx), c->dzero, 1, dst, c->d, NULL),
-        "context: norm weights");
+    GPU(fox_gpu_get_rows(c->gpu, t, c->dzero, 1, dst, c->d, NULL), "context: norm weights");
     return FOX_OK;
 }
 
@@ -127,10 +131,10 @@ fox_status fox_context_create(fox_model *m, const fox_context_config *cfg, fox_c
 
     if (!m || !out) return fox_fail(FOX_ERR_ARG, "context: null argument");
     *out = NULL;
-    if (m->weights->mode != FOX_WEIGHTS_DEVICE)
+    if (m->weights->mode == FOX_WEIGHTS_RESIDENT)
         return fox_fail(FOX_ERR_UNSUPPORTED,
                         "context: rustfox_amd computes on the GPU; open the model with "
-                        "FOX_WEIGHTS_DEVICE");
+                        "FOX_WEIGHTS_DEVICE or FOX_WEIGHTS_STREAM");
     if (cfg) k = *cfg;
     else fox_context_config_default(&k, m);
     if (k.n_ctx == 0) k.n_ctx = m->info.n_ctx_train;
@@ -216,30 +220,52 @@ fox_status fox_context_create(fox_model *m, const fox_context_config *cfg, fox_c
     free(ts);
     if (st != FOX_OK) { fox_context_destroy(c); return st; }
 
-    c->embd = dev_tensor(m, m->token_embd);
-    c->out = dev_tensor(m, m->output);
+    if ((st = fox_weights_use(m->weights, m->token_embd, &c->embd)) != FOX_OK ||
+        (st = fox_weights_use(m->weights, m->output, &c->out)) != FOX_OK) {
+        fox_context_destroy(c);
+        return st;
+    }
     for (l = 0; l < mi->n_layer; l++) {
         const fox_layer_tensors *t = &m->layers[l];
         dev_layer *D = &c->L[l];
-        D->attn_q = dev_tensor(m, t->attn_q);
-        D->attn_k = dev_tensor(m, t->attn_k);
-        D->attn_v = dev_tensor(m, t->attn_v);
-        D->attn_out = dev_tensor(m, t->attn_out);
-        D->ffn_gate = dev_tensor(m, t->ffn_gate);
-        D->ffn_up = dev_tensor(m, t->ffn_up);
-        D->ffn_down = dev_tensor(m, t->ffn_down);
+        const fox_gpu_tensor *an, *fn;
         D->attn_norm = c->norms + (2 * (size_t)l) * c->d;
         D->ffn_norm = c->norms + (2 * (size_t)l + 1) * c->d;
-        if ((st = norm_vector(c, t->attn_norm, D->attn_norm)) != FOX_OK ||
-            (st = norm_vector(c, t->ffn_norm, D->ffn_norm)) != FOX_OK) {
+        if (streaming(c)) {
+            /* the layer's matrices are taken from its slot at every pass;
+             * its norm vectors are copied out once here */
+            const fox_gpu_tensor *lt[FOX_LAYER_ROLES];
+            st = fox_weights_use_layer(m->weights, l, lt);
+            an = lt[FOX_ROLE_ATTN_NORM];
+            fn = lt[FOX_ROLE_FFN_NORM];
+        } else {
+            D->attn_q = dev_tensor(m, t->attn_q);
+            D->attn_k = dev_tensor(m, t->attn_k);
+            D->attn_v = dev_tensor(m, t->attn_v);
+            D->attn_out = dev_tensor(m, t->attn_out);
+            D->ffn_gate = dev_tensor(m, t->ffn_gate);
+            D->ffn_up = dev_tensor(m, t->ffn_up);
+            D->ffn_down = dev_tensor(m, t->ffn_down);
+            an = dev_tensor(m, t->attn_norm);
+            fn = dev_tensor(m, t->ffn_norm);
+            st = FOX_OK;
+        }
+        if (st == FOX_OK) st = norm_vector(c, an, D->attn_norm);
+        if (st == FOX_OK) st = norm_vector(c, fn, D->ffn_norm);
+        if (streaming(c)) fox_weights_done_layer(m->weights, l);
+        if (st != FOX_OK) {
             fox_context_destroy(c);
             return st;
         }
     }
     c->out_norm = c->norms + 2 * (size_t)mi->n_layer * c->d;
-    if ((st = norm_vector(c, m->output_norm, c->out_norm)) != FOX_OK) {
-        fox_context_destroy(c);
-        return st;
+    {
+        const fox_gpu_tensor *on;
+        if ((st = fox_weights_use(m->weights, m->output_norm, &on)) != FOX_OK ||
+            (st = norm_vector(c, on, c->out_norm)) != FOX_OK) {
+            fox_context_destroy(c);
+            return st;
+        }
     }
     if (fox_gpu_sync(c->gpu) != FOX_GPU_OK) {
         st = fox_gpu_failed(FOX_GPU_ERR_INTERNAL, "context: setup");
@@ -303,7 +329,23 @@ static fox_status forward_pass(fox_context *c, size_t M, int want_logits)
 
     GPU(fox_gpu_get_rows(c->gpu, c->embd, c->dtok, M, c->x, c->d, NULL), "forward: embed");
     for (l = 0; l < mi->n_layer; l++) {
+        dev_layer SD;
         const dev_layer *D = &c->L[l];
+        if (streaming(c)) {
+            /* this layer from its slot (loaded now if the prefetch did not
+             * reach it); the compute stream waits for its upload */
+            const fox_gpu_tensor *lt[FOX_LAYER_ROLES];
+            if ((st = fox_weights_use_layer(c->m->weights, l, lt)) != FOX_OK) return st;
+            SD = *D;
+            SD.attn_q = lt[FOX_ROLE_ATTN_Q];
+            SD.attn_k = lt[FOX_ROLE_ATTN_K];
+            SD.attn_v = lt[FOX_ROLE_ATTN_V];
+            SD.attn_out = lt[FOX_ROLE_ATTN_OUT];
+            SD.ffn_gate = lt[FOX_ROLE_FFN_GATE];
+            SD.ffn_up = lt[FOX_ROLE_FFN_UP];
+            SD.ffn_down = lt[FOX_ROLE_FFN_DOWN];
+            D = &SD;
+        }
         const fox_gpu_tensor *qkv[3] = { D->attn_q, D->attn_k, D->attn_v };
         float *qkv_out[3] = { c->q, c->k, c->v };
         size_t qkv_str[3] = { c->nq, c->nkv, c->nkv };
@@ -346,6 +388,14 @@ static fox_status forward_pass(fox_context *c, size_t M, int want_logits)
         }
         GPU(fox_gpu_gemv(c->gpu, D->ffn_down, c->hb, c->ff, M, c->x, c->d,
                          FOX_GPU_GEMV_ACCUMULATE), "forward: ffn_down");
+        if (streaming(c)) {
+            /* the layer-ahead load (src/forward.c:333-337): the next layer,
+             * or the first one of the next pass, goes up on the copy stream
+             * while this one computes */
+            fox_weights_done_layer(c->m->weights, l);
+            if ((st = fox_weights_prefetch_layer(c->m->weights, (l + 1) % mi->n_layer)) != FOX_OK)
+                return st;
+        }
     }
     if (!want_logits) return FOX_OK;
     {
@@ -448,11 +498,12 @@ fox_status fox_decode_greedy(fox_context *c, uint32_t token, size_t n_steps, uin
     GPU(fox_gpu_memcpy_h2d(c->gpu, c->dpos, &c->pos, 4), "decode: position");
     /* the first step runs eagerly (it also sizes every workspace), the rest
      * replay one captured graph; FOX_GRAPHS=0 keeps every step eager (for
-     * profilers that cannot follow graph launches) */
+     * profilers that cannot follow graph launches), and so does streaming
+     * (each step reloads layer slots from the host) */
     if ((st = greedy_step(c)) != FOX_OK) return st;
     {
         const char *e = getenv("FOX_GRAPHS");
-        if (e && strcmp(e, "0") == 0) {
+        if ((e && strcmp(e, "0") == 0) || streaming(c)) {
             for (s = 1; s < n_steps; s++)
                 if ((st = greedy_step(c)) != FOX_OK) return st;
             GPU(fox_gpu_memcpy_d2h(c->gpu, out_ids, c->dhist + c->pos, n_steps * 4), "decode: ids");

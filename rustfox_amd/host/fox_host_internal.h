@@ -65,6 +65,23 @@ int        fox_type_layout(uint32_t type, uint32_t *block, uint32_t *bytes);
 
 /* --------------------------------------------------------------- weights */
 
+/* the tensors of one transformer layer, in this order */
+enum {
+    FOX_ROLE_ATTN_NORM, FOX_ROLE_ATTN_Q, FOX_ROLE_ATTN_K, FOX_ROLE_ATTN_V, FOX_ROLE_ATTN_OUT,
+    FOX_ROLE_FFN_NORM, FOX_ROLE_FFN_GATE, FOX_ROLE_FFN_UP, FOX_ROLE_FFN_DOWN, FOX_LAYER_ROLES
+};
+
+/* FOX_WEIGHTS_STREAM: one layer's tensors in HBM, reloaded in place */
+typedef struct {
+    int              layer;          /* layer held, -1 for none */
+    fox_gpu_tensor  *t[FOX_LAYER_ROLES];
+    fox_gpu_event   *ready;          /* copy stream: the upload of `layer` is done */
+    fox_gpu_event   *used;           /* compute stream: its last queued use is done */
+    int              used_set;
+    int              pins;           /* live leases on its tensors */
+    uint64_t         last_used;
+} fox_layer_slot;
+
 struct fox_weights {
     fox_gguf         *g;
     fox_weights_mode  mode;
@@ -77,9 +94,37 @@ struct fox_weights {
     size_t            live;
     uint64_t          held;
     uint64_t          reads;
+    /* FOX_WEIGHTS_STREAM */
+    int              *layer_of;      /* per tensor: its layer, or -1 (kept resident) */
+    int              *role_of;       /* per tensor: its FOX_ROLE_* within the layer */
+    size_t           *lt;            /* tensor index of (layer, role): lt[l * ROLES + r] */
+    uint32_t          n_layer;
+    uint64_t          layer_bytes;   /* GGUF bytes of one layer */
+    fox_layer_slot   *slots;
+    int               n_slots;
+    uint8_t          *pinned[2];     /* host staging of one layer, alternating */
+    fox_gpu_event    *staged[2];     /* copy stream: done reading pinned[i] */
+    int               staged_set[2];
+    int               next_pin;
+    void             *dev_stage;     /* device staging of one tensor's GGUF bytes */
+    uint64_t          clock, evictions;
 };
 
 const fox_tensor_desc *fox_weights_desc(const fox_weights *w, size_t idx);
+/* The device tensor of tensor idx for kernels queued next on the compute
+ * stream.  Resident tensors come from the backend's table; in
+ * FOX_WEIGHTS_STREAM a layer tensor comes from its layer's slot, the layer
+ * being loaded first if no slot holds it, and the compute stream is made to
+ * wait for that slot's upload. */
+fox_status fox_weights_use(fox_weights *w, size_t idx, const fox_gpu_tensor **out);
+/* FOX_WEIGHTS_STREAM: the nine tensors of layer l, as fox_weights_use */
+fox_status fox_weights_use_layer(fox_weights *w, uint32_t l, const fox_gpu_tensor **t);
+/* FOX_WEIGHTS_STREAM: every kernel reading layer l's slot is queued; its
+ * slot may be reloaded once the compute stream has passed this point */
+void       fox_weights_done_layer(fox_weights *w, uint32_t l);
+/* FOX_WEIGHTS_STREAM: start loading layer l into a free or least recently
+ * used slot if none holds it (the upload runs on the copy stream) */
+fox_status fox_weights_prefetch_layer(fox_weights *w, uint32_t l);
 
 /* ----------------------------------------------------------------- model */
 

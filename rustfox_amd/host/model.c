@@ -284,6 +284,11 @@ fox_status fox_model_open(const char *gguf_path, fox_weights_mode mode,
      * first evaluation */
     if (mode == FOX_WEIGHTS_DEVICE)
         for (i = 0; i < g->n_tensors && st == FOX_OK; i++) st = fox_weights_prefetch(m->weights, i);
+    /* streaming: the tensors outside the layers stay resident from the start */
+    if (mode == FOX_WEIGHTS_STREAM) {
+        const size_t keep[3] = {m->token_embd, m->output_norm, m->output};
+        for (i = 0; i < 3 && st == FOX_OK; i++) st = fox_weights_prefetch(m->weights, keep[i]);
+    }
     if (st != FOX_OK) goto fail;
     *out = m;
     return FOX_OK;

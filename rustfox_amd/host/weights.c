@@ -1,19 +1,41 @@
-/* weights.c -- the lease API (RustFox include/fox/fox.h:370-403) with two
- * backends: RESIDENT keeps host bytes (src/weights.c:461-496 semantics: a
- * tensor is read on first touch, once); DEVICE keeps each tensor in HBM as a
- * fox_gpu_tensor, read once from the file and uploaded once.  STREAM
- * (storage-streamed slots) is not part of the GPU build.
+/* weights.c -- the lease API (RustFox include/fox/fox.h:370-403) with three
+ * backends:
+ *
+ *   RESIDENT  host bytes (src/weights.c:461-496 semantics: a tensor is read
+ *             on first touch, once);
+ *   DEVICE    each tensor in HBM as a fox_gpu_tensor, read once from the file
+ *             and uploaded once;
+ *   STREAM    the GPU form of RustFox's storage-streamed slots
+ *             (src/weights.c:248-459) for models larger than the HBM the
+ *             caller grants: embeddings, the output head and other tensors
+ *             outside the layers stay resident; the layers go through a ring
+ *             of layer slots in HBM.  A layer is read from the file into
+ *             pinned host memory (two buffers, alternating) and uploaded on
+ *             the copy stream, in place into the least recently used slot
+ *             without a lease, while the compute stream works on the layer
+ *             before it (the layer-ahead prefetch of src/forward.c:322-337).
+ *             Events order the two streams: the compute stream waits for a
+ *             slot's upload, the copy stream for the compute stream's last
+ *             use of the slot it overwrites.
  *
  * Contract kept from the reference: at most FOX_WEIGHTS_MAX_LIVE_LEASES live
  * leases (src/weights.c:789-797), lease.bytes is the GGUF tensor size,
  * lease.data is borrowed until release and cleared by it (887-890), calls
- * are thread-safe under one lock, fox_weights_reads counts one read per
- * tensor, prefetch_async/_wait report FOX_ERR_UNSUPPORTED without a
- * prefetch thread (722, 750).
+ * are thread-safe under one lock, fox_weights_reads counts tensor reads from
+ * the file (one per tensor for the resident backends, again at every reload
+ * when streaming), fox_weights_evictions counts tensors whose slot was
+ * reloaded, prefetch_async/_wait report FOX_ERR_UNSUPPORTED where no
+ * asynchronous load exists (722, 750).
+ *
+ * The streaming budget is the HBM the weights may take, in GGUF bytes: the
+ * resident tensors plus as many layer slots as fit, at least two (one in
+ * use, one loading); a budget below that is refused with FOX_ERR_NOMEM.
+ * Budget 0 gives every layer a slot (nothing is reloaded).
  */
 #include "fox_host_internal.h"
 
 #include <fcntl.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 #include <unistd.h>
@@ -29,6 +51,264 @@ const fox_tensor_desc *fox_weights_desc(const fox_weights *w, size_t idx)
     return (w && idx < w->g->n_tensors) ? &w->g->tensors[idx] : NULL;
 }
 
+static const char *const ROLE_NAME[FOX_LAYER_ROLES] = {
+    "attn_norm", "attn_q", "attn_k", "attn_v", "attn_output",
+    "ffn_norm", "ffn_gate", "ffn_up", "ffn_down",
+};
+
+static fox_status read_bytes(fox_weights *w, const fox_tensor_desc *t, uint8_t *dst)
+{
+    uint64_t done = 0, at = w->g->data_offset + t->offset;
+    while (done < t->size_bytes) {
+        size_t chunk = t->size_bytes - done > (1u << 30) ? (1u << 30) : (size_t)(t->size_bytes - done);
+        ssize_t got = pread(w->fd, dst + done, chunk, (off_t)(at + done));
+        if (got <= 0) return fox_fail(FOX_ERR_IO, "weights: short read on '%s'", t->name);
+        done += (uint64_t)got;
+    }
+    return FOX_OK;
+}
+
+/* ------------------------------------------------------------ streaming */
+
+/* which layer and role each tensor plays ("blk.<l>.<role>.weight") */
+static fox_status map_layers(fox_weights *w)
+{
+    const fox_gguf *g = w->g;
+    size_t i, n = g->n_tensors;
+    uint32_t l, r;
+
+    w->layer_of = (int *)malloc((n ? n : 1) * sizeof(int));
+    w->role_of = (int *)malloc((n ? n : 1) * sizeof(int));
+    if (!w->layer_of || !w->role_of) return fox_fail(FOX_ERR_NOMEM, "weights: layer map");
+    w->n_layer = 0;
+    for (i = 0; i < n; i++) {
+        unsigned layer;
+        char role[64];
+        int used = 0;
+        w->layer_of[i] = -1;
+        w->role_of[i] = -1;
+        if (sscanf(g->tensors[i].name, "blk.%u.%63[^.].weight%n", &layer, role, &used) != 2 ||
+            used == 0 || g->tensors[i].name[used] != '\0' || layer > 1000000u)
+            continue;
+        for (r = 0; r < FOX_LAYER_ROLES; r++) {
+            if (strcmp(role, ROLE_NAME[r]) == 0) {
+                w->layer_of[i] = (int)layer;
+                w->role_of[i] = (int)r;
+                if (layer + 1 > w->n_layer) w->n_layer = layer + 1;
+                break;
+            }
+        }
+    }
+    if (w->n_layer == 0) return fox_fail(FOX_ERR_FORMAT, "weights: no layer tensors to stream");
+    w->lt = (size_t *)malloc((size_t)w->n_layer * FOX_LAYER_ROLES * sizeof(size_t));
+    if (!w->lt) return fox_fail(FOX_ERR_NOMEM, "weights: layer table");
+    for (i = 0; i < (size_t)w->n_layer * FOX_LAYER_ROLES; i++) w->lt[i] = FOX_TENSOR_ABSENT;
+    for (i = 0; i < n; i++)
+        if (w->layer_of[i] >= 0)
+            w->lt[(size_t)w->layer_of[i] * FOX_LAYER_ROLES + w->role_of[i]] = i;
+    /* every layer must have the tensors of layer 0, with its types and
+     * shapes: a slot holds any layer */
+    w->layer_bytes = 0;
+    for (l = 0; l < w->n_layer; l++) {
+        for (r = 0; r < FOX_LAYER_ROLES; r++) {
+            size_t a = w->lt[(size_t)l * FOX_LAYER_ROLES + r], b = w->lt[r];
+            const fox_tensor_desc *ta, *tb;
+            if (a == FOX_TENSOR_ABSENT || b == FOX_TENSOR_ABSENT)
+                return fox_fail(FOX_ERR_NOTFOUND, "weights: the file has no tensor "
+                                "'blk.%u.%s.weight'", a == FOX_TENSOR_ABSENT ? l : 0,
+                                ROLE_NAME[r]);
+            ta = &g->tensors[a];
+            tb = &g->tensors[b];
+            if (ta->type != tb->type || ta->n_dims != tb->n_dims || ta->ne[0] != tb->ne[0] ||
+                ta->ne[1] != tb->ne[1] || ta->size_bytes != tb->size_bytes)
+                return fox_fail(FOX_ERR_UNSUPPORTED, "weights: streaming reloads layers in "
+                                "place, and '%s' differs from layer 0's in type or shape",
+                                ta->name);
+            if (l == 0) w->layer_bytes += ta->size_bytes;
+        }
+    }
+    return FOX_OK;
+}
+
+static fox_status open_stream(fox_weights *w)
+{
+    const fox_gguf *g = w->g;
+    uint64_t outside = 0, largest = 0;
+    size_t i;
+    int s, r;
+    fox_status st;
+    fox_gpu_status gs = FOX_GPU_OK;
+
+    if ((st = map_layers(w)) != FOX_OK) return st;
+    for (i = 0; i < g->n_tensors; i++) {
+        if (w->layer_of[i] < 0) outside += g->tensors[i].size_bytes;
+        if (g->tensors[i].size_bytes > largest) largest = g->tensors[i].size_bytes;
+    }
+    if (w->budget == 0) {
+        w->n_slots = (int)w->n_layer;
+    } else {
+        uint64_t fit;
+        if (w->budget < outside + 2 * w->layer_bytes)
+            return fox_fail(FOX_ERR_NOMEM, "weights: streaming needs the %llu bytes of the "
+                            "tensors outside the layers and two %llu-byte layer slots; the "
+                            "budget is %llu", (unsigned long long)outside,
+                            (unsigned long long)w->layer_bytes, (unsigned long long)w->budget);
+        fit = (w->budget - outside) / w->layer_bytes;
+        w->n_slots = (int)(fit < w->n_layer ? fit : w->n_layer);
+    }
+    w->slots = (fox_layer_slot *)calloc((size_t)w->n_slots, sizeof(fox_layer_slot));
+    if (!w->slots) return fox_fail(FOX_ERR_NOMEM, "weights: slot table");
+    for (s = 0; s < w->n_slots; s++) w->slots[s].layer = -1;
+    for (s = 0; s < w->n_slots && gs == FOX_GPU_OK; s++) {
+        fox_layer_slot *sl = &w->slots[s];
+        for (r = 0; r < FOX_LAYER_ROLES && gs == FOX_GPU_OK; r++) {
+            const fox_tensor_desc *t = &g->tensors[w->lt[r]];
+            uint64_t rows = 1;
+            uint32_t d;
+            for (d = 1; d < t->n_dims; d++) rows *= t->ne[d];
+            gs = fox_gpu_tensor_alloc(w->gpu, (int)t->type, t->ne[0], rows, &sl->t[r]);
+        }
+        if (gs == FOX_GPU_OK) gs = fox_gpu_event_create(w->gpu, &sl->ready);
+        if (gs == FOX_GPU_OK) gs = fox_gpu_event_create(w->gpu, &sl->used);
+    }
+    for (i = 0; i < 2 && gs == FOX_GPU_OK; i++) {
+        gs = fox_gpu_host_alloc(w->gpu, (size_t)w->layer_bytes, (void **)&w->pinned[i]);
+        if (gs == FOX_GPU_OK) gs = fox_gpu_event_create(w->gpu, &w->staged[i]);
+    }
+    if (gs == FOX_GPU_OK) gs = fox_gpu_malloc(w->gpu, (size_t)largest, &w->dev_stage);
+    if (gs != FOX_GPU_OK) return fox_gpu_failed(gs, "weights: streaming buffers");
+    return FOX_OK;
+}
+
+static void close_stream(fox_weights *w)
+{
+    int s, r;
+    if (w->gpu) fox_gpu_sync(w->gpu);
+    for (s = 0; w->slots && s < w->n_slots; s++) {
+        for (r = 0; r < FOX_LAYER_ROLES; r++) fox_gpu_tensor_free(w->gpu, w->slots[s].t[r]);
+        fox_gpu_event_destroy(w->slots[s].ready);
+        fox_gpu_event_destroy(w->slots[s].used);
+    }
+    for (s = 0; s < 2; s++) {
+        if (w->gpu && w->pinned[s]) fox_gpu_host_free(w->gpu, w->pinned[s]);
+        fox_gpu_event_destroy(w->staged[s]);
+    }
+    if (w->gpu && w->dev_stage) fox_gpu_free(w->gpu, w->dev_stage);
+    free(w->slots);
+    free(w->layer_of);
+    free(w->role_of);
+    free(w->lt);
+}
+
+static fox_layer_slot *slot_of(fox_weights *w, uint32_t l)
+{
+    int s;
+    for (s = 0; s < w->n_slots; s++)
+        if (w->slots[s].layer == (int)l) return &w->slots[s];
+    return NULL;
+}
+
+/* layer l into a slot, started on the copy stream; caller holds the lock */
+static fox_status stream_in(fox_weights *w, uint32_t l, fox_layer_slot **out)
+{
+    fox_layer_slot *sl = slot_of(w, l), *victim = NULL;
+    uint8_t *pin;
+    uint64_t off = 0;
+    fox_gpu_status gs = FOX_GPU_OK;
+    fox_status st;
+    int s, r, b;
+
+    if (sl) {
+        sl->last_used = ++w->clock;
+        *out = sl;
+        return FOX_OK;
+    }
+    for (s = 0; s < w->n_slots; s++) {
+        fox_layer_slot *c = &w->slots[s];
+        if (c->pins) continue;
+        if (!victim || c->last_used < victim->last_used) victim = c;
+    }
+    if (!victim)
+        return fox_fail(FOX_ERR_NOMEM, "weights: every one of the %d layer slots holds a live "
+                        "lease", w->n_slots);
+    /* the pinned buffer of two loads ago is free once its copies are done */
+    b = w->next_pin;
+    w->next_pin ^= 1;
+    if (w->staged_set[b] && (gs = fox_gpu_event_sync(w->staged[b])) != FOX_GPU_OK)
+        return fox_gpu_failed(gs, "weights: staging");
+    pin = w->pinned[b];
+    for (r = 0; r < FOX_LAYER_ROLES; r++) {
+        const fox_tensor_desc *t = &w->g->tensors[w->lt[(size_t)l * FOX_LAYER_ROLES + r]];
+        if ((st = read_bytes(w, t, pin + off)) != FOX_OK) return st;
+        off += t->size_bytes;
+    }
+    /* the copy stream overwrites the slot after the compute stream's last
+     * queued use of its old layer */
+    if (victim->used_set) gs = fox_gpu_event_wait(w->gpu, victim->used, 1);
+    off = 0;
+    for (r = 0; r < FOX_LAYER_ROLES && gs == FOX_GPU_OK; r++) {
+        const fox_tensor_desc *t = &w->g->tensors[w->lt[(size_t)l * FOX_LAYER_ROLES + r]];
+        gs = fox_gpu_tensor_load_async(w->gpu, victim->t[r], pin + off, t->size_bytes,
+                                       w->dev_stage);
+        off += t->size_bytes;
+    }
+    if (gs == FOX_GPU_OK) gs = fox_gpu_event_record_copy(w->gpu, w->staged[b]);
+    if (gs == FOX_GPU_OK) gs = fox_gpu_event_record_copy(w->gpu, victim->ready);
+    if (victim->layer >= 0) {
+        w->evictions += FOX_LAYER_ROLES;
+        w->held -= w->layer_bytes;
+        victim->layer = -1;
+    }
+    if (gs != FOX_GPU_OK) return fox_gpu_failed(gs, "weights: layer upload");
+    w->staged_set[b] = 1;
+    victim->layer = (int)l;
+    victim->last_used = ++w->clock;
+    w->reads += FOX_LAYER_ROLES;
+    w->held += w->layer_bytes;
+    *out = victim;
+    return FOX_OK;
+}
+
+fox_status fox_weights_prefetch_layer(fox_weights *w, uint32_t l)
+{
+    fox_layer_slot *sl;
+    fox_status st;
+    if (!w || w->mode != FOX_WEIGHTS_STREAM || l >= w->n_layer) return FOX_ERR_ARG;
+    pthread_mutex_lock(&w->lock);
+    st = stream_in(w, l, &sl);
+    pthread_mutex_unlock(&w->lock);
+    return st;
+}
+
+fox_status fox_weights_use_layer(fox_weights *w, uint32_t l, const fox_gpu_tensor **t)
+{
+    fox_layer_slot *sl;
+    fox_status st;
+    int r;
+    if (!w || w->mode != FOX_WEIGHTS_STREAM || l >= w->n_layer) return FOX_ERR_ARG;
+    pthread_mutex_lock(&w->lock);
+    st = stream_in(w, l, &sl);
+    if (st == FOX_OK) {
+        fox_gpu_status gs = fox_gpu_event_wait(w->gpu, sl->ready, 0);
+        if (gs != FOX_GPU_OK) st = fox_gpu_failed(gs, "weights: layer wait");
+        for (r = 0; r < FOX_LAYER_ROLES; r++) t[r] = sl->t[r];
+    }
+    pthread_mutex_unlock(&w->lock);
+    return st;
+}
+
+void fox_weights_done_layer(fox_weights *w, uint32_t l)
+{
+    fox_layer_slot *sl;
+    if (!w || w->mode != FOX_WEIGHTS_STREAM) return;
+    pthread_mutex_lock(&w->lock);
+    sl = slot_of(w, l);
+    if (sl && fox_gpu_event_record(w->gpu, sl->used) == FOX_GPU_OK) sl->used_set = 1;
+    pthread_mutex_unlock(&w->lock);
+}
+
+/* ------------------------------------------------------------ open/close */
+
 fox_status fox_weights_open(const char *gguf_path, fox_weights_mode mode,
                             uint64_t budget_bytes, fox_weights **out)
 {
@@ -37,11 +317,7 @@ fox_status fox_weights_open(const char *gguf_path, fox_weights_mode mode,
 
     if (!gguf_path || !out) return fox_fail(FOX_ERR_ARG, "weights: null argument");
     *out = NULL;
-    if (mode == FOX_WEIGHTS_STREAM)
-        return fox_fail(FOX_ERR_UNSUPPORTED,
-                        "weights: streaming from storage is not part of the GPU build; open "
-                        "with FOX_WEIGHTS_DEVICE (HBM) or FOX_WEIGHTS_RESIDENT");
-    if (mode != FOX_WEIGHTS_RESIDENT && mode != FOX_WEIGHTS_DEVICE)
+    if (mode != FOX_WEIGHTS_RESIDENT && mode != FOX_WEIGHTS_DEVICE && mode != FOX_WEIGHTS_STREAM)
         return fox_fail(FOX_ERR_ARG, "weights: unknown mode %d", (int)mode);
 
     w = (fox_weights *)calloc(1, sizeof(*w));
@@ -51,6 +327,7 @@ fox_status fox_weights_open(const char *gguf_path, fox_weights_mode mode,
     w->fd = -1;
     st = fox_gguf_open(gguf_path, &w->g);
     if (st != FOX_OK) { free(w); return st; }
+    pthread_mutex_init(&w->lock, NULL);
     w->fd = open(gguf_path, O_RDONLY | O_CLOEXEC);
     if (w->fd < 0) {
         fox_weights_close(w);
@@ -61,22 +338,25 @@ fox_status fox_weights_open(const char *gguf_path, fox_weights_mode mode,
     else
         w->dev = (fox_gpu_tensor **)calloc(w->g->n_tensors ? w->g->n_tensors : 1,
                                            sizeof(fox_gpu_tensor *));
-    if ((mode == FOX_WEIGHTS_RESIDENT && !w->host) || (mode == FOX_WEIGHTS_DEVICE && !w->dev)) {
+    if ((mode == FOX_WEIGHTS_RESIDENT && !w->host) || (mode != FOX_WEIGHTS_RESIDENT && !w->dev)) {
         fox_weights_close(w);
         return fox_fail(FOX_ERR_NOMEM, "weights: residency table");
     }
-    if (mode == FOX_WEIGHTS_DEVICE) {
+    if (mode != FOX_WEIGHTS_RESIDENT) {
         fox_gpu_status gs = fox_gpu_init(device_ordinal(), &w->gpu);
         const char *mw = getenv("FOX_MAX_WORKGROUPS");
         if (gs != FOX_GPU_OK) {
-            st = fox_gpu_failed(gs, "weights: no usable GPU for FOX_WEIGHTS_DEVICE");
+            st = fox_gpu_failed(gs, "weights: no usable GPU for the device backends");
             fox_weights_close(w);
             return st;
         }
         /* a cap on the fused GEMVs' persistent grid (results unchanged) */
         if (mw && *mw) fox_gpu_set_max_workgroups(w->gpu, atoi(mw));
     }
-    pthread_mutex_init(&w->lock, NULL);
+    if (mode == FOX_WEIGHTS_STREAM && (st = open_stream(w)) != FOX_OK) {
+        fox_weights_close(w);
+        return st;
+    }
     *out = w;
     return FOX_OK;
 }
@@ -86,6 +366,7 @@ void fox_weights_close(fox_weights *w)
     size_t i;
     if (!w) return;
     if (w->live) fox_warn("weights: closing with %zu lease(s) still held", w->live);
+    if (w->mode == FOX_WEIGHTS_STREAM) close_stream(w);
     if (w->g) {
         for (i = 0; i < w->g->n_tensors; i++) {
             if (w->host) free(w->host[i]);
@@ -96,8 +377,8 @@ void fox_weights_close(fox_weights *w)
     free(w->dev);
     if (w->gpu) fox_gpu_shutdown(w->gpu);
     if (w->fd >= 0) close(w->fd);
-    fox_gguf_close(w->g);
     if (w->g) pthread_mutex_destroy(&w->lock);
+    fox_gguf_close(w->g);
     free(w);
 }
 
@@ -113,19 +394,12 @@ size_t fox_weights_tensor_find(const fox_weights *w, const char *name)
     return w ? fox_gguf_tensor_find(w->g, name) : FOX_TENSOR_ABSENT;
 }
 
-static fox_status read_bytes(fox_weights *w, const fox_tensor_desc *t, uint8_t *dst)
+static int streamed(const fox_weights *w, size_t idx)
 {
-    uint64_t done = 0, at = w->g->data_offset + t->offset;
-    while (done < t->size_bytes) {
-        size_t chunk = t->size_bytes - done > (1u << 30) ? (1u << 30) : (size_t)(t->size_bytes - done);
-        ssize_t got = pread(w->fd, dst + done, chunk, (off_t)(at + done));
-        if (got <= 0) return fox_fail(FOX_ERR_IO, "weights: short read on '%s'", t->name);
-        done += (uint64_t)got;
-    }
-    return FOX_OK;
+    return w->mode == FOX_WEIGHTS_STREAM && w->layer_of[idx] >= 0;
 }
 
-/* load tensor idx into its backend; caller holds the lock */
+/* load resident tensor idx into its backend; caller holds the lock */
 static fox_status load(fox_weights *w, size_t idx)
 {
     const fox_tensor_desc *t = &w->g->tensors[idx];
@@ -134,7 +408,7 @@ static fox_status load(fox_weights *w, size_t idx)
 
     if ((w->host && w->host[idx]) || (w->dev && w->dev[idx])) return FOX_OK;
     if (t->size_bytes == 0) return fox_fail(FOX_ERR_FORMAT, "weights: tensor '%s' is empty", t->name);
-    if (w->budget && w->held + t->size_bytes > w->budget)
+    if (w->mode != FOX_WEIGHTS_STREAM && w->budget && w->held + t->size_bytes > w->budget)
         return fox_fail(FOX_ERR_NOMEM,
                         "weights: tensor '%s' needs %llu bytes but only %llu of the %llu byte "
                         "budget is left", t->name, (unsigned long long)t->size_bytes,
@@ -164,9 +438,28 @@ static fox_status load(fox_weights *w, size_t idx)
     return FOX_OK;
 }
 
+fox_status fox_weights_use(fox_weights *w, size_t idx, const fox_gpu_tensor **out)
+{
+    fox_status st;
+    if (!w || !out || idx >= w->g->n_tensors || w->mode == FOX_WEIGHTS_RESIDENT)
+        return fox_fail(FOX_ERR_ARG, "weights: no device tensor %zu", idx);
+    if (streamed(w, idx)) {
+        const fox_gpu_tensor *t[FOX_LAYER_ROLES];
+        st = fox_weights_use_layer(w, (uint32_t)w->layer_of[idx], t);
+        if (st == FOX_OK) *out = t[w->role_of[idx]];
+        return st;
+    }
+    pthread_mutex_lock(&w->lock);
+    st = load(w, idx);
+    if (st == FOX_OK) *out = w->dev[idx];
+    pthread_mutex_unlock(&w->lock);
+    return st;
+}
+
 fox_status fox_weights_acquire(fox_weights *w, size_t idx, fox_weights_lease *lease)
 {
     fox_status st;
+    fox_layer_slot *sl = NULL;
     if (!w || !lease) return fox_fail(FOX_ERR_ARG, "weights: null argument");
     if (idx >= w->g->n_tensors)
         return fox_fail(FOX_ERR_NOTFOUND, "weights: no tensor at index %zu", idx);
@@ -176,13 +469,29 @@ fox_status fox_weights_acquire(fox_weights *w, size_t idx, fox_weights_lease *le
         return fox_fail(FOX_ERR_INTERNAL, "weights: %d leases already held; release before "
                         "acquiring the next one", FOX_WEIGHTS_MAX_LIVE_LEASES);
     }
-    st = load(w, idx);
+    if (streamed(w, idx)) {
+        /* the lease holds the slot: its upload is waited for here */
+        st = stream_in(w, (uint32_t)w->layer_of[idx], &sl);
+        if (st == FOX_OK) {
+            fox_gpu_status gs = fox_gpu_event_sync(sl->ready);
+            if (gs != FOX_GPU_OK) st = fox_gpu_failed(gs, "weights: layer upload");
+        }
+        if (st == FOX_OK) {
+            sl->pins++;
+            lease->data = (const void *)sl->t[w->role_of[idx]];
+            lease->slot = sl;
+        }
+    } else {
+        st = load(w, idx);
+        if (st == FOX_OK) {
+            lease->data = w->mode == FOX_WEIGHTS_RESIDENT ? (const void *)w->host[idx]
+                                                          : (const void *)w->dev[idx];
+            lease->slot = NULL;
+        }
+    }
     if (st == FOX_OK) {
-        lease->data = w->mode == FOX_WEIGHTS_RESIDENT ? (const void *)w->host[idx]
-                                                      : (const void *)w->dev[idx];
         lease->bytes = w->g->tensors[idx].size_bytes;
         lease->tensor_index = idx;
-        lease->slot = NULL;
         w->live++;
     }
     pthread_mutex_unlock(&w->lock);
@@ -198,6 +507,10 @@ void fox_weights_release(fox_weights *w, fox_weights_lease *lease)
         fox_warn("weights: release with no lease outstanding");
         return;
     }
+    if (lease->slot) {
+        fox_layer_slot *sl = (fox_layer_slot *)lease->slot;
+        if (sl->pins > 0) sl->pins--;
+    }
     w->live--;
     lease->data = NULL;
     lease->bytes = 0;
@@ -211,26 +524,46 @@ fox_status fox_weights_prefetch(fox_weights *w, size_t idx)
     if (!w) return FOX_ERR_ARG;
     if (idx >= w->g->n_tensors) return FOX_ERR_NOTFOUND;
     pthread_mutex_lock(&w->lock);
-    st = load(w, idx);
+    if (streamed(w, idx)) {
+        fox_layer_slot *sl;
+        st = stream_in(w, (uint32_t)w->layer_of[idx], &sl);
+        if (st == FOX_OK && fox_gpu_event_sync(sl->ready) != FOX_GPU_OK)
+            st = fox_fail(FOX_ERR_INTERNAL, "weights: layer upload");
+    } else {
+        st = load(w, idx);
+    }
     pthread_mutex_unlock(&w->lock);
     return st;
 }
 
+/* FOX_WEIGHTS_STREAM: start the tensor's layer upload without waiting for
+ * it; the other backends load synchronously and have nothing to start */
 fox_status fox_weights_prefetch_async(fox_weights *w, size_t idx)
 {
     if (!w) return FOX_ERR_ARG;
     if (idx >= w->g->n_tensors) return FOX_ERR_NOTFOUND;
-    return FOX_ERR_UNSUPPORTED;
+    if (!streamed(w, idx)) return FOX_ERR_UNSUPPORTED;
+    return fox_weights_prefetch_layer(w, (uint32_t)w->layer_of[idx]);
 }
 
 fox_status fox_weights_prefetch_wait(fox_weights *w, size_t idx)
 {
+    fox_layer_slot *sl;
+    fox_status st = FOX_OK;
     if (!w) return FOX_ERR_ARG;
     if (idx >= w->g->n_tensors) return FOX_ERR_NOTFOUND;
-    return FOX_ERR_UNSUPPORTED;
+    if (!streamed(w, idx)) return FOX_ERR_UNSUPPORTED;
+    pthread_mutex_lock(&w->lock);
+    sl = slot_of(w, (uint32_t)w->layer_of[idx]);
+    if (!sl) st = fox_fail(FOX_ERR_INTERNAL, "weights: no load of '%s' was started",
+                           w->g->tensors[idx].name);
+    else if (fox_gpu_event_sync(sl->ready) != FOX_GPU_OK)
+        st = fox_fail(FOX_ERR_INTERNAL, "weights: layer upload");
+    pthread_mutex_unlock(&w->lock);
+    return st;
 }
 
 size_t fox_weights_live_leases(const fox_weights *w) { return w ? w->live : 0; }
 uint64_t fox_weights_resident_bytes(const fox_weights *w) { return w ? w->held : 0; }
 uint64_t fox_weights_reads(const fox_weights *w) { return w ? w->reads : 0; }
-uint64_t fox_weights_evictions(const fox_weights *w) { (void)w; return 0; }
+uint64_t fox_weights_evictions(const fox_weights *w) { return w ? w->evictions : 0; }

@@ -284,9 +284,6 @@ def test_model_and_weights_contract(tiny_models, tmp_path):
     with pytest.raises(rf.FoxError) as e:
         rf.Model(str(tmp_path / "missing.gguf"))
     assert e.value.status == 2                       # FOX_ERR_IO
-    with pytest.raises(rf.FoxError) as e:
-        rf.Model(p, mode=rf.WEIGHTS_STREAM)
-    assert e.value.status == 5                       # no streaming backend
     with rf.Model(p, mode=rf.WEIGHTS_RESIDENT) as m:
         with pytest.raises(rf.FoxError) as e:
             m.context(32)
