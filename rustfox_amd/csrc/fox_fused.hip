@@ -541,7 +541,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
         const int nr = pick4(a.n_rows, sg);
         int orow = tl * 16 + crow;
         orow = orow < nr ? orow : nr - 1;
-        if (EPI == EPI_STORE)                               // used with ACCUMULATE only
+        if (EPI == EPI_STORE && (a.flags & FOX_GPU_GEMV_ACCUMULATE))   // (uniform)
             p0 = pick4(a.out, sg)[(size_t)ct * pick4(a.out_stride, sg) + orow];
         if (EPI == EPI_ROPE) {
             const int half = a.head_dim / 2, i = (orow % a.head_dim) >> 1;
@@ -583,8 +583,6 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     auto item_end = [&](int ti) {
         if (EPI == EPI_SUMS) return;
         __syncthreads();
-        float n0 = 0.0f, n1 = 0.0f;
-        epi_load(ti + 1, n0, n1);                           // the next item's, in flight
         int sg = 0, tl = 0;
         item(ti, csl, sg, tl);
         const int orow = tl * 16 + crow;
@@ -651,8 +649,10 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
                 }
             }
         }
-        pre0 = n0;
-        pre1 = n1;
+        // the next item's operands, loaded into the registers just read (no
+        // copy: a copy would wait here for the load); they are used at that
+        // item's end, after its blocks
+        if ((EPI == EPI_STORE || EPI == EPI_ROPE) && ti + 1 < ntl) epi_load(ti + 1, pre0, pre1);
     };
 
     // ---- blocks: integer sums, then one float term per row and token.  A
@@ -662,6 +662,9 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     const int bbytes = b_bytes_per_block_tok(FMT) * M;
     const bool lead = j < M;
     const int tok = j;
+    // a lead lane's terms: rows 4g .. 4g + 3 of token tok, row after row
+    // M * nbp floats apart, the up slab 16 M nbp floats on
+    const int rstep = M * nbp, tlane = (4 * g * M + tok) * nbp;
     if (nu == 0) {
         for (int ti = 0; ti < ntl; ti++) item_end(ti);
         return;
@@ -693,7 +696,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
                         if (grow < nrows) a.sums[((size_t)tok * nrows + grow) * nb + b] = S[q];
                     } else {
                         const float d = half_bits_to_float((hw[q >> 1] >> (16 * (q & 1))) & 0xFFFFu);
-                        terms[(ti & 1) * tstride + ((sl * 16 + row) * M + tok) * nbp + b] =
+                        terms[(ti & 1) * tstride + sl * 16 * rstep + tlane + q * rstep + b] =
                             d * (float)S[q];
                     }
                 }
