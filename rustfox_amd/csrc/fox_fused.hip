@@ -415,7 +415,9 @@ __device__ __forceinline__ T pick4(const T *v, int s)
     return r;
 }
 
-template <int FMT, int IN, int EPI, int R4>
+// MT: more than one token (the later tokens' input stages are pipelined; a
+// separate instantiation keeps the one-token kernels' registers as they are)
+template <int FMT, int IN, int EPI, int R4, bool MT>
 __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float *norm_in,
                                                  const int8_t *q_in, int nb_in, FusedArgs a)
 {
@@ -430,7 +432,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     // the units, items and weight addresses, is then scalar work)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int nb = nb_in, M = a.M, K = nb * 256;
+    const int nb = nb_in, M = MT ? a.M : 1, K = nb * 256;
     const int nslab = EPI == EPI_SILU ? 2 : 1;
     const FusedLds L = fused_lds(FMT, K, M, nslab);
     uint8_t *B = lds + L.B;
@@ -572,10 +574,16 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
         const float s = quantise_to_b<FMT, IN, R4>(a, 0, K, B, aux, dred, ured, in);
         if (tid == 0) ascale[0] = s;
     }
-    for (int t = 1; t < M; t++) {
-        load_input<IN, R4>(x_in, norm_in, q_in, a.x_stride, t, K, in);
-        const float s = quantise_to_b<FMT, IN, R4>(a, t, K, B, aux, dred, ured, in);
-        if (tid == 0) ascale[t] = s;
+    // the later tokens one ahead: token t + 1's input is in flight while
+    // token t is quantised
+    if (MT) {
+        load_input<IN, R4>(x_in, norm_in, q_in, a.x_stride, 1, K, in);
+        for (int t = 1; t < M; t++) {
+            InRegs<R4> cur = in;
+            if (t + 1 < M) load_input<IN, R4>(x_in, norm_in, q_in, a.x_stride, t + 1, K, in);
+            const float s = quantise_to_b<FMT, IN, R4>(a, t, K, B, aux, dred, ured, cur);
+            if (tid == 0) ascale[t] = s;
+        }
     }
     __syncthreads();
 
@@ -765,13 +773,18 @@ static fox_gpu_status fused_go_r(fox_gpu_ctx *ctx, FusedArgs a, int n_work)
     a.n_per = n_work / grid;
     a.n_rem = n_work - a.n_per * grid;
     const size_t lds = fused_lds(FMT, a.nb * 256, a.M, EPI == EPI_SILU ? 2 : 1).total;
+    const void *k = a.M > 1 ? (const void *)gemv_fused<FMT, IN, EPI, R4, true>
+                            : (const void *)gemv_fused<FMT, IN, EPI, R4, false>;
     if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute((const void *)gemv_fused<FMT, IN, EPI, R4>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return fox_hip_fail(e, "fused gemv: LDS size");
     }
-    hipLaunchKernelGGL((gemv_fused<FMT, IN, EPI, R4>), dim3((unsigned)grid), dim3(FWG), lds,
-                       ctx->stream, a.x, a.norm_w, a.q_in, a.nb, a);
+    if (a.M > 1)
+        hipLaunchKernelGGL((gemv_fused<FMT, IN, EPI, R4, true>), dim3((unsigned)grid), dim3(FWG),
+                           lds, ctx->stream, a.x, a.norm_w, a.q_in, a.nb, a);
+    else
+        hipLaunchKernelGGL((gemv_fused<FMT, IN, EPI, R4, false>), dim3((unsigned)grid), dim3(FWG),
+                           lds, ctx->stream, a.x, a.norm_w, a.q_in, a.nb, a);
     FOX_LAUNCHED("gemv_fused");
     return FOX_GPU_OK;
 }
@@ -786,8 +799,12 @@ static fox_gpu_status fused_go(fox_gpu_ctx *ctx, const FusedArgs &a, int grid)
     if (per <= 2) return fused_go_r<FMT, IN, EPI, 2>(ctx, a, grid);
     if (per <= 3) return fused_go_r<FMT, IN, EPI, 3>(ctx, a, grid);
     if (per <= 5) return fused_go_r<FMT, IN, EPI, 5>(ctx, a, grid);
-    if (per <= 8 || IN == IN_NORM) return fused_go_r<FMT, IN, EPI, 8>(ctx, a, grid);
-    return fused_go_r<FMT, IN, EPI, 11>(ctx, a, grid);
+    if constexpr (IN == IN_NORM) {
+        return fused_go_r<FMT, IN, EPI, 8>(ctx, a, grid);   // (fused_check: K <= 16384)
+    } else {
+        if (per <= 8) return fused_go_r<FMT, IN, EPI, 8>(ctx, a, grid);
+        return fused_go_r<FMT, IN, EPI, 11>(ctx, a, grid);
+    }
 }
 
 template <int IN, int EPI>
