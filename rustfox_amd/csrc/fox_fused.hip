@@ -1,14 +1,22 @@
-// fox_fused.hip -- one-launch GEMV stages of a decode layer for the ternary
-// formats (TQ1_0, TQ2_0; TQ1_0 tensors are held as TQ2_0 blocks of the same
-// trits): the activation input stage runs inside the GEMV.
+// fox_fused.hip -- one-launch GEMV stages of a decode layer: the activation
+// input stage runs inside the GEMV.
 //
-// Every workgroup takes the f32 input (optionally RMS-normalised first),
-// quantises it to int8 exactly as src/gemv.c:11-42 does, and lays it out in
-// LDS as the MFMA B operand; the weight loads of its waves are already in
-// flight while it does so.  The per-block integer sums, the block-order
-// float combine and the final activation-scale multiply are those of
-// gemv_blocks (fox_gemv.hip), so results are bit-identical to it and to the
-// reference.  Epilogues:
+// Ternary formats (TQ1_0, TQ2_0; TQ1_0 tensors are held as TQ2_0 blocks of
+// the same trits), 1..8 tokens: every workgroup takes the f32 input
+// (optionally RMS-normalised first), quantises it to int8 exactly as
+// src/gemv.c:11-42 does, and lays it out in LDS as the MFMA B operand; the
+// weight loads of its waves are already in flight while it does so.  The
+// per-block integer sums, the block-order float combine and the final
+// activation-scale multiply are those of gemv_blocks (fox_gemv.hip), so
+// results are bit-identical to it and to the reference.
+//
+// K-quants (Q4_K, Q6_K), one token: the input is quantised per 256-element
+// block as src/kernels.c:722-754 does, into LDS in element order with its
+// block scales and sub-block sums; each lane of a weight block takes one row
+// and one quarter of the block and forms its integer dot products with
+// v_dot4_i32_i8 (a token of one column would use 1/16 of an MFMA), then the
+// float terms of src/kernels.c:571-661 (8 per block for Q4_K, 4 for Q6_K),
+// which the ordered combine adds in the reference's order.  Epilogues:
 //   STORE  y (or out + y with FOX_GPU_GEMV_ACCUMULATE: the residual add of
 //          src/forward.c:374-377, 393-396);
 //   ROPE   segments q, k, v of one projection: RoPE on q and k
@@ -57,20 +65,31 @@ struct FusedArgs {
     float *k_cache, *v_cache;
 };
 
-// LDS carve-up (bytes), identical on host and device
+// LDS carve-up (bytes), identical on host and device.  B: the MFMA B
+// operand (ternary formats) or the int8 input in element order (K-quants,
+// one token); aux: per-block corrections (ternary) or sub-block sums
+// (K-quants: [block][8] for Q4_K, [block][4 quarters][4 groups] for Q6_K);
+// bs: the K-quants' per-block activation scales; terms: two buffers of
+// [slab][16 rows][token][ntp] float terms, ntp = terms per row (blocks times
+// terms per block) padded to a multiple of 4.
 struct FusedLds {
-    int q, B, aux, terms, y, total;
+    int B, aux, bs, terms, y, total;
 };
+
+__host__ __device__ constexpr int fused_ntp(int fmt, int nb)
+{
+    return (nb * terms_per_block(fmt) + 3) & ~3;
+}
 
 __host__ __device__ inline FusedLds fused_lds(int fmt, int K, int M, int nslab)
 {
     const int nb = K / 256;
     FusedLds L;
     int off = 0;
-    L.q = off;
-    L.B = off;     off += nb * M * b_bytes_per_block_tok(fmt);
+    L.B = off;     off += nb * M * (fmt == FMT_TQ2 ? b_bytes_per_block_tok(fmt) : 256);
     L.aux = off;   off += ((nb * M * aux_per_block_tok(fmt) * 4) + 15) & ~15;
-    L.terms = off; off += 2 * nslab * 16 * M * ((nb + 3) & ~3) * terms_per_block(fmt) * 4;
+    L.bs = off;    off += fmt == FMT_TQ2 ? 0 : ((nb * 4 + 15) & ~15);
+    L.terms = off; off += 2 * nslab * 16 * M * fused_ntp(fmt, nb) * 4;
     L.y = off;     off += nslab * 16 * M * 4;
     L.total = off;
     return L;
@@ -193,6 +212,56 @@ __device__ __forceinline__ void in_mask(int K, InRegs<R4MAX> &in)
     }
 }
 
+// RMSNorm of token t held in the input registers (src/ops.c:7-22)
+template <int R4MAX>
+__device__ __forceinline__ void rms_apply(const FusedArgs &a, int t, int K, double *dred,
+                                          InRegs<R4MAX> &in)
+{
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    float4 *xv = in.xv;
+    const float4 *wv = in.wv;
+    double ss = 0.0;
+#pragma unroll
+    for (int r = 0; r < R4MAX; r++) {
+        const double x0 = xv[r].x, x1 = xv[r].y, x2 = xv[r].z, x3 = xv[r].w;
+        ss = __builtin_fma(x0, x0, ss);
+        ss = __builtin_fma(x1, x1, ss);
+        ss = __builtin_fma(x2, x2, ss);
+        ss = __builtin_fma(x3, x3, ss);
+    }
+    ss = wave_sum_dd(ss);
+    if (lane == 0) dred[wave] = ss;
+    __syncthreads();
+    // Every wave derives the scale itself (no second barrier).  The tree sum
+    // certifies the float scale of the reference's index-order double sum
+    // (it lies within (K + 64) 2^-52 tot, and the scale is monotone in the
+    // sum): even lanes evaluate the low end of that interval, odd lanes the
+    // high end; equal floats are the reference's.
+    double tot = 0.0;
+    for (int w = 0; w < FW; w++) tot += dred[w];
+    const double rel = (double)(K + 64) * 0x1p-52;
+    const double sgn = (lane & 1) ? 1.0 : -1.0;
+    const double y = 1.0 / __builtin_sqrt(tot * (1.0 + sgn * rel) / (double)K +
+                                          (double)a.eps) * (1.0 - sgn * 0x1p-50);
+    const float f = (float)y;
+    float rs = read_lane(f, 0);
+    if (rs != read_lane(f, 1)) {
+        // undecided: the sequential sum, by every lane (wave-uniform)
+        const float *xt = a.x + (size_t)t * a.x_stride;
+        double seq = 0.0;
+        for (int i = 0; i < K; i++) seq += (double)xt[i] * (double)xt[i];
+        rs = (float)(1.0 / __builtin_sqrt(seq / (double)K + (double)a.eps));
+    }
+#pragma unroll
+    for (int r = 0; r < R4MAX; r++) {           // src/ops.c:18: x * scale * w
+        xv[r].x = xv[r].x * rs * wv[r].x;
+        xv[r].y = xv[r].y * rs * wv[r].y;
+        xv[r].z = xv[r].z * rs * wv[r].z;
+        xv[r].w = xv[r].w * rs * wv[r].w;
+    }
+}
+
 template <int FMT, int IN, int R4MAX>
 __device__ __forceinline__ float quantise_to_b(const FusedArgs &a, int t, int K, uint8_t *B, int32_t *aux,
                                                double *dred, uint32_t *ured, InRegs<R4MAX> &in)
@@ -205,49 +274,7 @@ __device__ __forceinline__ float quantise_to_b(const FusedArgs &a, int t, int K,
     float act = 0.0f;
     if (IN != IN_Q) {
         float4 *xv = in.xv;
-        if (IN == IN_NORM) {
-            const float4 *wv = in.wv;
-            double ss = 0.0;
-#pragma unroll
-            for (int r = 0; r < R4MAX; r++) {
-                const double x0 = xv[r].x, x1 = xv[r].y, x2 = xv[r].z, x3 = xv[r].w;
-                ss = __builtin_fma(x0, x0, ss);
-                ss = __builtin_fma(x1, x1, ss);
-                ss = __builtin_fma(x2, x2, ss);
-                ss = __builtin_fma(x3, x3, ss);
-            }
-            ss = wave_sum_dd(ss);
-            if (lane == 0) dred[wave] = ss;
-            __syncthreads();
-            // Every wave derives the scale itself (no second barrier).  The
-            // tree sum certifies the float scale of the reference's
-            // index-order double sum (it lies within (K + 64) 2^-52 tot, and
-            // the scale is monotone in the sum): even lanes evaluate the low
-            // end of that interval, odd lanes the high end; equal floats are
-            // the reference's.
-            double tot = 0.0;
-            for (int w = 0; w < FW; w++) tot += dred[w];
-            const double rel = (double)(K + 64) * 0x1p-52;
-            const double sgn = (lane & 1) ? 1.0 : -1.0;
-            const double y = 1.0 / __builtin_sqrt(tot * (1.0 + sgn * rel) / (double)K +
-                                                  (double)a.eps) * (1.0 - sgn * 0x1p-50);
-            const float f = (float)y;
-            float rs = read_lane(f, 0);
-            if (rs != read_lane(f, 1)) {
-                // undecided: the sequential sum, by every lane (wave-uniform)
-                const float *xt = a.x + (size_t)t * a.x_stride;
-                double seq = 0.0;
-                for (int i = 0; i < K; i++) seq += (double)xt[i] * (double)xt[i];
-                rs = (float)(1.0 / __builtin_sqrt(seq / (double)K + (double)a.eps));
-            }
-#pragma unroll
-            for (int r = 0; r < R4MAX; r++) {           // src/ops.c:18: x * scale * w
-                xv[r].x = xv[r].x * rs * wv[r].x;
-                xv[r].y = xv[r].y * rs * wv[r].y;
-                xv[r].z = xv[r].z * rs * wv[r].z;
-                xv[r].w = xv[r].w * rs * wv[r].w;
-            }
-        }
+        if (IN == IN_NORM) rms_apply<R4MAX>(a, t, K, dred, in);
         // amax (src/gemv.c:20-23) as the largest |x| bit pattern: for x >= 0
         // the integer order is the float order, and NaN lies above inf
         uint32_t mb = 0;
@@ -333,26 +360,255 @@ __device__ __forceinline__ float quantise_to_b(const FusedArgs &a, int t, int K,
     return act;
 }
 
+// N wave maxima at once (the steps of wave_reduce, interleaved); every lane
+// receives them
+template <int N>
+__device__ __forceinline__ void wave_max_n(uint32_t (&v)[N])
+{
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = max(v[i], dpp_t<0xB1, 0xF>(0u, v[i]));
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = max(v[i], dpp_t<0x4E, 0xF>(0u, v[i]));
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = max(v[i], dpp_t<0x141, 0xF>(0u, v[i]));
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = max(v[i], dpp_t<0x140, 0xF>(0u, v[i]));
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = max(v[i], dpp_t<0x142, 0xA>(0u, v[i]));
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = max(v[i], dpp_t<0x143, 0xC>(0u, v[i]));
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = read_lane(v[i], 63);
+}
+
+// K-quant input stage, one token: RMSNorm (IN_NORM), then every 256-element
+// block quantised with its own scale (src/kernels.c:722-754) into xq in
+// element order, its scale into bs and the sums of its sub-blocks (32
+// elements for Q4_K, 16 for Q6_K) into aux.  Thread tid holds input dwords
+// m = tid + FWG r, so wave w holds blocks w + FW r and a block's amax is one
+// wave maximum; the amaxes of all the wave's blocks reduce together.
+template <int FMT, int IN, int R4MAX>
+__device__ __forceinline__ void quantise_kq(const FusedArgs &a, int K, int8_t *xq, int32_t *aux,
+                                            float *bs, double *dred, InRegs<R4MAX> &in)
+{
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nb = K >> 8;
+    in_mask<IN, R4MAX>(K, in);
+    float4 *xv = in.xv;
+    if (IN == IN_NORM) rms_apply<R4MAX>(a, 0, K, dred, in);
+    // per-block amax as the largest |x| bit pattern (for x >= 0 the integer
+    // order is the float order, and NaN lies above inf)
+    uint32_t mb[R4MAX];
+#pragma unroll
+    for (int r = 0; r < R4MAX; r++) {
+        uint32_t m = __float_as_uint(xv[r].x) & 0x7fffffffu;
+        m = max(m, __float_as_uint(xv[r].y) & 0x7fffffffu);
+        m = max(m, __float_as_uint(xv[r].z) & 0x7fffffffu);
+        m = max(m, __float_as_uint(xv[r].w) & 0x7fffffffu);
+        mb[r] = m;
+    }
+    wave_max_n<R4MAX>(mb);
+    int part[R4MAX];
+#pragma unroll
+    for (int r = 0; r < R4MAX; r++) {
+        const int b = wave + FW * r;
+        const uint32_t am = mb[r];
+        uint32_t q = 0u;
+        float s = 0.0f;
+        if (am >= 0x03800000u && am < 0x7f800000u) {           // (uniform)
+            // amax in [2^-120, inf), no NaN: quant_fast applies
+            const float amax = __uint_as_float(am);
+            const float inv = fox_div(127.0f, amax);
+            q = pack_lo_bytes(quant_fast(xv[r].x, inv), quant_fast(xv[r].y, inv),
+                              quant_fast(xv[r].z, inv), quant_fast(xv[r].w, inv));
+            s = fox_div(amax, 127.0f);
+        } else if (am != 0u) {
+            // NaN, inf or a tiny amax: the float amax of the non-NaN values
+            // (src/kernels.c:734-737), then the exact quantiser
+            const float v4[4] = {xv[r].x, xv[r].y, xv[r].z, xv[r].w};
+            float m = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float av = fabsf(v4[e]);
+                if (av > m) m = av;
+            }
+            m = wave_max(m);
+            if (m > 0.0f) {
+                const float inv = fox_div(127.0f, m);
+                q = pack_lo_bytes(quant_one(v4[0], inv), quant_one(v4[1], inv),
+                                  quant_one(v4[2], inv), quant_one(v4[3], inv));
+                s = fox_div(m, 127.0f);
+            }
+        }
+        if (b < nb) {                                           // (uniform)
+            *(uint32_t *)(xq + b * 256 + 4 * lane) = q;
+            if (lane == 0) bs[b] = s;
+        }
+        part[r] = __builtin_amdgcn_sdot4((int)q, 0x01010101, 0, false);
+    }
+    // sub-block sums: quads of lanes (16 elements), then eights (32)
+#pragma unroll
+    for (int r = 0; r < R4MAX; r++) part[r] += dpp_t<0xB1, 0xF>(0, part[r]);
+#pragma unroll
+    for (int r = 0; r < R4MAX; r++) part[r] += dpp_t<0x4E, 0xF>(0, part[r]);
+    if (FMT == FMT_Q4K) {
+#pragma unroll
+        for (int r = 0; r < R4MAX; r++) part[r] += dpp_t<0x141, 0xF>(0, part[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < R4MAX; r++) {
+        const int b = wave + FW * r;
+        if (b >= nb) break;                                     // (uniform)
+        if (FMT == FMT_Q4K) {
+            if ((lane & 7) == 0) aux[b * 8 + (lane >> 3)] = part[r];
+        } else if ((lane & 3) == 0) {
+            // lane l holds elements 4l ..: half h = l >> 5, group g =
+            // (l >> 3) & 3, sixteen s = (l >> 2) & 1; stored at
+            // [block][quarter 2h + s][group g]
+            const int h = lane >> 5, g = (lane >> 3) & 3, s = (lane >> 2) & 1;
+            aux[b * 16 + (2 * h + s) * 4 + g] = part[r];
+        }
+    }
+    __syncthreads();
+}
+
 // ------------------------------------------------------------ weights
 
 // one lane's bytes of one (tile, block) chunk
+template <int FMT>
 struct RawBlk {
     uint32_t d0, d1, d2, d3;   // the lane's 16 bytes of 2-bit codes
     uint2 dd;                  // f16 scales of rows 4g .. 4g+3
 };
 
+// Q4_K lane (row r = lane & 15, part p = lane >> 4): qs[32p .. 32p + 31] of
+// its row (eight bytes from each of the lanes r + 16 g of the chunk layout)
+// and the row's d, dmin and 12 scale bytes
+template <>
+struct RawBlk<FMT_Q4K> {
+    uint2 q0, q1, q2, q3;
+    uint4 hd;
+};
+
+// Q6_K lane (row r = lane & 15, quarter v = lane >> 4 = 2 h + s): the
+// row's ql[64h + 16s ..] and ql[64h + 32 + 16s ..] (16 bytes each),
+// qh[32h + 16s ..] (16), scales 8h .. 8h + 7 and d
+template <>
+struct RawBlk<FMT_Q6K> {
+    uint4 l0, l1, h;
+    uint2 sc;
+    uint32_t d;
+};
+
 template <int FMT>
-__device__ __forceinline__ RawBlk load_raw(const uint8_t *__restrict__ ch, int lane)
+__device__ __forceinline__ RawBlk<FMT> load_raw(const uint8_t *__restrict__ ch, int lane)
 {
-    RawBlk r;
-    const int g = lane >> 4;
-    const uint4 v = *(const uint4 *)(ch + 16 * lane);
-    r.d0 = v.x;
-    r.d1 = v.y;
-    r.d2 = v.z;
-    r.d3 = v.w;
-    r.dd = *(const uint2 *)(ch + 1024 + 8 * g);
+    RawBlk<FMT> r;
+    if constexpr (FMT == FMT_TQ2) {
+        const int g = lane >> 4;
+        const uint4 v = *(const uint4 *)(ch + 16 * lane);
+        r.d0 = v.x;
+        r.d1 = v.y;
+        r.d2 = v.z;
+        r.d3 = v.w;
+        r.dd = *(const uint2 *)(ch + 1024 + 8 * g);
+    } else if constexpr (FMT == FMT_Q4K) {
+        const int row = lane & 15, p = lane >> 4;
+        const uint8_t *q = ch + 32 * row + 8 * p;   // lane r + 16 g: + 512 g
+        r.q0 = *(const uint2 *)q;
+        r.q1 = *(const uint2 *)(q + 512);
+        r.q2 = *(const uint2 *)(q + 1024);
+        r.q3 = *(const uint2 *)(q + 1536);
+        r.hd = *(const uint4 *)(ch + 2048 + 16 * row);
+    } else {
+        const int row = lane & 15, h = lane >> 5, s = (lane >> 4) & 1;
+        const uint8_t *ql = ch + 128 * row + 64 * h + 16 * s;
+        r.l0 = *(const uint4 *)ql;
+        r.l1 = *(const uint4 *)(ql + 32);
+        r.h = *(const uint4 *)(ch + 2048 + 64 * row + 32 * h + 16 * s);
+        r.sc = *(const uint2 *)(ch + 3072 + 16 * row + 8 * h);
+        r.d = *(const unsigned short *)(ch + 3328 + 2 * row);
+    }
     return r;
+}
+
+// Q4_K terms of sub-blocks 2p and 2p + 1 of one block and row
+// (src/kernels.c:585-599): xb the block's int8 input, sx its sub-block sums,
+// as its activation scale
+__device__ __forceinline__ void q4k_terms(const RawBlk<FMT_Q4K> &w, const int8_t *xb,
+                                          const int32_t *sx, float as, int p, float &t0,
+                                          float &t1)
+{
+    const uint4 *x4 = (const uint4 *)(xb + 64 * p);
+    const uint4 xa = x4[0], xb1 = x4[1], xc = x4[2], xd = x4[3];
+    // dword k of the lane holds qs[32p + 4k ..]: low nibbles with inputs
+    // 64p + 4k .., high nibbles with 64p + 32 + 4k ..
+    const uint32_t q[8] = {w.q0.x, w.q0.y, w.q1.x, w.q1.y, w.q2.x, w.q2.y, w.q3.x, w.q3.y};
+    const uint32_t xl[8] = {xa.x, xa.y, xa.z, xa.w, xb1.x, xb1.y, xb1.z, xb1.w};
+    const uint32_t xh[8] = {xc.x, xc.y, xc.z, xc.w, xd.x, xd.y, xd.z, xd.w};
+    int D0 = 0, D1 = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        D0 = __builtin_amdgcn_sdot4((int)(q[k] & 0x0F0F0F0Fu), (int)xl[k], D0, false);
+        D1 = __builtin_amdgcn_sdot4((int)((q[k] >> 4) & 0x0F0F0F0Fu), (int)xh[k], D1, false);
+    }
+    const int2 sq = *(const int2 *)(sx + 2 * p);
+    const float d = half_bits_to_float(w.hd.x & 0xFFFFu);
+    const float dmin = half_bits_to_float(w.hd.x >> 16);
+    // scale and min of sub-blocks j = 2p, 2p + 1 (src/kernels.c:246-255):
+    // bytes (j & 3) of the three scale dwords
+    const int sh = 16 * (p & 1);
+    const uint32_t S0 = w.hd.y >> sh, S1 = w.hd.z >> sh, S2 = w.hd.w >> sh;
+    int sc0, mn0, sc1, mn1;
+    if (p < 2) {
+        sc0 = S0 & 63;
+        mn0 = S1 & 63;
+        sc1 = (S0 >> 8) & 63;
+        mn1 = (S1 >> 8) & 63;
+    } else {
+        sc0 = (S2 & 0x0F) | (((S0 >> 6) & 3) << 4);
+        mn0 = ((S2 >> 4) & 0x0F) | (((S1 >> 6) & 3) << 4);
+        sc1 = ((S2 >> 8) & 0x0F) | (((S0 >> 14) & 3) << 4);
+        mn1 = ((S2 >> 12) & 0x0F) | (((S1 >> 14) & 3) << 4);
+    }
+    t0 = as * (d * (float)sc0 * (float)D0 - dmin * (float)mn0 * (float)sq.x);
+    t1 = as * (d * (float)sc1 * (float)D1 - dmin * (float)mn1 * (float)sq.y);
+}
+
+// Q6_K term of quarter v = 2h + s of one block and row: the group dot of
+// src/kernels.c:531-569 (sub = s of half h), scaled as src/kernels.c:655-657
+__device__ __forceinline__ float q6k_term(const RawBlk<FMT_Q6K> &w, const int8_t *xb,
+                                          const int32_t *sx, float as, int lane)
+{
+    const int h = lane >> 5, s = (lane >> 4) & 1;
+    const int8_t *xs = xb + 128 * h + 16 * s;
+    const int4 sg = *(const int4 *)(sx + 4 * (lane >> 4));
+    const int sgv[4] = {sg.x, sg.y, sg.z, sg.w};
+    const uint32_t L0[4] = {w.l0.x, w.l0.y, w.l0.z, w.l0.w};
+    const uint32_t L1[4] = {w.l1.x, w.l1.y, w.l1.z, w.l1.w};
+    const uint32_t H[4] = {w.h.x, w.h.y, w.h.z, w.h.w};
+    int part = 0;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        // group g: inputs 128h + 32g + 16s .., weights (ql low / high nibble
+        // of the first or second 32 bytes) | (qh bits 2g, 2g + 1) << 4
+        const uint4 x4 = *(const uint4 *)(xs + 32 * g);
+        const uint32_t xw[4] = {x4.x, x4.y, x4.z, x4.w};
+        int dot = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t src = (g & 1) ? L1[k] : L0[k];
+            const uint32_t q6 = ((src >> (4 * (g >> 1))) & 0x0F0F0F0Fu) |
+                                (((H[k] >> (2 * g)) & 0x03030303u) << 4);
+            dot = __builtin_amdgcn_sdot4((int)q6, (int)xw[k], dot, false);
+        }
+        // scale byte s + 2g of the row's scales 8h ..
+        const int sc = __builtin_amdgcn_sbfe((int)(g < 2 ? w.sc.x : w.sc.y), 8 * (s + 2 * (g & 1)), 8);
+        part += sc * (dot - 32 * sgv[g]);
+    }
+    const float d = half_bits_to_float(w.d & 0xFFFFu);
+    return as * d * (float)part;
 }
 
 // integer block sums of rows 4g .. 4g+3 for the lane's B column; returns
@@ -361,7 +617,7 @@ __device__ __forceinline__ RawBlk load_raw(const uint8_t *__restrict__ ch, int l
 // token's column (their MFMA columns are not used): with no lane-dependent
 // branch the four B reads issue together.
 template <int FMT>
-__device__ __forceinline__ void block_mfma(const RawBlk &r, const uint8_t *__restrict__ Bb,
+__device__ __forceinline__ void block_mfma(const RawBlk<FMT> &r, const uint8_t *__restrict__ Bb,
                                            int M, int lane, int corr, int S[4])
 {
     const int g = lane >> 4, j = lane & 15, jc = j < M ? j : M - 1;
@@ -427,22 +683,26 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     __shared__ uint32_t ured[FW];
     __shared__ float ascale[FOX_GPU_MAX_TOKENS];
 
-    constexpr int CHUNK = TQ2_CHUNK;
+    constexpr bool KQ = FMT != FMT_TQ2;                    // a K-quant (one token)
+    constexpr int CHUNK = FMT == FMT_TQ2 ? TQ2_CHUNK : FMT == FMT_Q4K ? Q4K_CHUNK : Q6K_CHUNK;
+    constexpr int T = terms_per_block(FMT);
     // (the wave index as a wave-uniform value: everything per wave below,
     // the units, items and weight addresses, is then scalar work)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int nb = nb_in, M = MT ? a.M : 1, K = nb * 256;
+    const int nb = nb_in, M = MT && !KQ ? a.M : 1, K = nb * 256;
     const int nslab = EPI == EPI_SILU ? 2 : 1;
     const FusedLds L = fused_lds(FMT, K, M, nslab);
     uint8_t *B = lds + L.B;
     int32_t *aux = (int32_t *)(lds + L.aux);
-    // block terms [2][nslab][16 rows][M][nbp]: a row's terms are contiguous,
-    // padded with zeros to nbp, a multiple of 4 (adding +0.0f changes no
-    // sum: the ordered sum starts at +0.0f and so is never -0.0f)
+    float *bsc = (float *)(lds + L.bs);
+    // block terms [2][nslab][16 rows][M][nbp]: a row's terms (T per block)
+    // are contiguous, padded with zeros to nbp, a multiple of 4 (adding
+    // +0.0f changes no sum: the ordered sum starts at +0.0f and so is never
+    // -0.0f)
     float *terms = (float *)(lds + L.terms);
     float *ybuf = (float *)(lds + L.y);
-    const int nbp = (nb + 3) & ~3;
+    const int nbp = fused_ntp(FMT, nb);
     const int tstride = nslab * 16 * M * nbp;              // floats per terms buffer
 
     // ---- work: items bx, bx + gridDim.x, ... (a 16-row tile of one segment,
@@ -513,10 +773,10 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     // ---- loads in the order they are used (they complete in order): the
     // input of token 0 (above), the first weight blocks, the epilogue's
     // operands
-    constexpr int PF = pf_of(R4, EPI == EPI_SILU ? 2 : 1);
+    constexpr int PF = KQ ? 4 : pf_of(R4, EPI == EPI_SILU ? 2 : 1);
     // (every wave issues PF block loads, past its last unit re-reading that
     // one, so that the input's first use waits for the input only)
-    RawBlk raw[PF];
+    RawBlk<FMT> raw[PF];
     Cur fc{0, 0, unit_ptr(0, 0)};                          // unit k (then PF) of the wave
 #pragma unroll
     for (int k = 0; k < PF; k++) {
@@ -560,17 +820,19 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     __builtin_amdgcn_sched_barrier(0);
     // the zero padding of the term rows (read after the input stage's
     // barriers)
-    if (nbp != nb) {
-        const int pad = nbp - nb;
+    if (nbp != nb * T) {
+        const int used = nb * T, pad = nbp - used;
         for (int i = tid; i < 2 * nslab * 16 * M * pad; i += FWG) {
             const int row = i / pad;
-            terms[row * nbp + nb + (i - row * pad)] = 0.0f;
+            terms[row * nbp + used + (i - row * pad)] = 0.0f;
         }
     }
 
     // ---- input stage: int8 activations straight into the B operand in LDS
     // (token 0 outside the loop: its waits then count the loads above)
-    {
+    if constexpr (KQ) {
+        quantise_kq<FMT, IN, R4>(a, K, (int8_t *)B, aux, bsc, dred, in);
+    } else {
         const float s = quantise_to_b<FMT, IN, R4>(a, 0, K, B, aux, dred, ured, in);
         if (tid == 0) ascale[0] = s;
     }
@@ -624,7 +886,9 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
             if (c + 2 < nq) add4(S2);
             if (c + 3 < nq) add4(S3);
             for (c += 4; c < nq; c++) add4(tq[c]);
-            y = acc * ascale[ct];                           // src/gemv.c:70
+            // (the ternary formats' per-vector scale: src/gemv.c:70; the
+            // K-quants' per-block scales are inside the terms)
+            y = KQ ? acc : acc * ascale[ct];
         }
         if (EPI == EPI_STORE) {
             if (owns) {
@@ -663,8 +927,9 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
         if ((EPI == EPI_STORE || EPI == EPI_ROPE) && ti + 1 < ntl) epi_load(ti + 1, pre0, pre1);
     };
 
-    // ---- blocks: integer sums, then one float term per row and token.  A
-    // wave's units run through all its items; PF blocks stay in flight.
+    // ---- blocks: integer sums, then one float term per row and token (T
+    // per row for the K-quants).  A wave's units run through all its items;
+    // PF blocks stay in flight.
     const int g = lane >> 4, j = lane & 15;
 
     const int bbytes = b_bytes_per_block_tok(FMT) * M;
@@ -684,28 +949,47 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
             const int n = n0 + k;
             if (n >= total) break;
             const int u = wave + FW * r, sl = u >= nb, b = u - sl * nb;
-            const int corr = aux[b * M + (lead ? tok : M - 1)];   // (used by lead lanes)
-            int S[4];
-            block_mfma<FMT>(raw[k], B + b * bbytes, M, lane, corr, S);
-            const RawBlk rk = raw[k];
-            if (n + PF < total) {
-                raw[k] = load_raw<FMT>(fc.p, lane);
-                if (n + PF + 1 < total) fc = cur_next(fc);
-            }
-            if (lead) {
-                const uint32_t hw[2] = {rk.dd.x, rk.dd.y};
-                int sg, tl;
-                item(ti, sl, sg, tl);
+            if constexpr (KQ) {
+                // lane (row j, part g): T / 4 terms of its row
+                const RawBlk<FMT> rk = raw[k];
+                if (n + PF < total) {
+                    raw[k] = load_raw<FMT>(fc.p, lane);
+                    if (n + PF + 1 < total) fc = cur_next(fc);
+                }
+                const int8_t *xb = (const int8_t *)B + b * 256;
+                const float as = bsc[b];
+                float *tp = terms + (ti & 1) * tstride + (sl * 16 + j) * nbp + b * T;
+                if constexpr (FMT == FMT_Q4K) {
+                    float t0, t1;
+                    q4k_terms(rk, xb, aux + b * 8, as, g, t0, t1);
+                    *(float2 *)(tp + 2 * g) = make_float2(t0, t1);
+                } else {
+                    tp[g] = q6k_term(rk, xb, aux + b * 16, as, lane);
+                }
+            } else {
+                const int corr = aux[b * M + (lead ? tok : M - 1)];   // (used by lead lanes)
+                int S[4];
+                block_mfma<FMT>(raw[k], B + b * bbytes, M, lane, corr, S);
+                const RawBlk<FMT> rk = raw[k];
+                if (n + PF < total) {
+                    raw[k] = load_raw<FMT>(fc.p, lane);
+                    if (n + PF + 1 < total) fc = cur_next(fc);
+                }
+                if (lead) {
+                    const uint32_t hw[2] = {rk.dd.x, rk.dd.y};
+                    int sg, tl;
+                    item(ti, sl, sg, tl);
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const int row = 4 * g + q;
-                    if (EPI == EPI_SUMS) {
-                        const int nrows = pick4(a.n_rows, sg), grow = tl * 16 + row;
-                        if (grow < nrows) a.sums[((size_t)tok * nrows + grow) * nb + b] = S[q];
-                    } else {
-                        const float d = half_bits_to_float((hw[q >> 1] >> (16 * (q & 1))) & 0xFFFFu);
-                        terms[(ti & 1) * tstride + sl * 16 * rstep + tlane + q * rstep + b] =
-                            d * (float)S[q];
+                    for (int q = 0; q < 4; q++) {
+                        const int row = 4 * g + q;
+                        if (EPI == EPI_SUMS) {
+                            const int nrows = pick4(a.n_rows, sg), grow = tl * 16 + row;
+                            if (grow < nrows) a.sums[((size_t)tok * nrows + grow) * nb + b] = S[q];
+                        } else {
+                            const float d = half_bits_to_float((hw[q >> 1] >> (16 * (q & 1))) & 0xFFFFu);
+                            terms[(ti & 1) * tstride + sl * 16 * rstep + tlane + q * rstep + b] =
+                                d * (float)S[q];
+                        }
                     }
                 }
             }
@@ -746,9 +1030,12 @@ static fox_gpu_status fused_check(int type, size_t K, size_t M, int nslab, int *
                         "one workgroup holds beside the norm weights", K,
                         4 * R4_LIMIT_NORM * FWG);
     *fmt = fmt_of(type);
-    if (*fmt != FMT_TQ2)
+    if (*fmt < 0)
         return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "fused gemv: %s weights use the unfused path",
                         fox_type_name(type));
+    if (*fmt != FMT_TQ2 && M != 1)
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "fused gemv: %s weights take the fused path "
+                        "for one token only", fox_type_name(type));
     if (K % 256 || K == 0) return fox_fail(FOX_GPU_ERR_ARG, "fused gemv: K %% 256 != 0");
     if (K > 4 * R4_LIMIT * FWG)
         return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "fused gemv: K = %zu exceeds the %d values "
@@ -773,14 +1060,17 @@ static fox_gpu_status fused_go_r(fox_gpu_ctx *ctx, FusedArgs a, int n_work)
     a.n_per = n_work / grid;
     a.n_rem = n_work - a.n_per * grid;
     const size_t lds = fused_lds(FMT, a.nb * 256, a.M, EPI == EPI_SILU ? 2 : 1).total;
-    const void *k = a.M > 1 ? (const void *)gemv_fused<FMT, IN, EPI, R4, true>
-                            : (const void *)gemv_fused<FMT, IN, EPI, R4, false>;
+    // (the K-quants have the one-token kernels only: fused_check)
+    constexpr bool MT_OK = FMT == FMT_TQ2;
+    const bool mt = MT_OK && a.M > 1;
+    const void *k = mt ? (const void *)gemv_fused<FMT, IN, EPI, R4, MT_OK>
+                       : (const void *)gemv_fused<FMT, IN, EPI, R4, false>;
     if (lds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return fox_hip_fail(e, "fused gemv: LDS size");
     }
-    if (a.M > 1)
-        hipLaunchKernelGGL((gemv_fused<FMT, IN, EPI, R4, true>), dim3((unsigned)grid), dim3(FWG),
+    if (mt)
+        hipLaunchKernelGGL((gemv_fused<FMT, IN, EPI, R4, MT_OK>), dim3((unsigned)grid), dim3(FWG),
                            lds, ctx->stream, a.x, a.norm_w, a.q_in, a.nb, a);
     else
         hipLaunchKernelGGL((gemv_fused<FMT, IN, EPI, R4, false>), dim3((unsigned)grid), dim3(FWG),
@@ -807,10 +1097,15 @@ static fox_gpu_status fused_go(fox_gpu_ctx *ctx, const FusedArgs &a, int grid)
     }
 }
 
+// (the K-quant kernels take f32 input and write outputs: int8 input with
+// per-block scales and the block-sum requests take the unfused path)
 template <int IN, int EPI>
 static fox_gpu_status fused_dispatch(fox_gpu_ctx *ctx, int fmt, const FusedArgs &a, int grid)
 {
-    (void)fmt;   // fused_check admits the TQ2_0 layout only
+    if constexpr (IN != IN_Q && EPI != EPI_SUMS) {
+        if (fmt == FMT_Q4K) return fused_go<FMT_Q4K, IN, EPI>(ctx, a, grid);
+        if (fmt == FMT_Q6K) return fused_go<FMT_Q6K, IN, EPI>(ctx, a, grid);
+    }
     return fused_go<FMT_TQ2, IN, EPI>(ctx, a, grid);
 }
 
@@ -841,9 +1136,10 @@ fox_gpu_status fox_fused_gemv(fox_gpu_ctx *ctx, size_t n, const fox_gpu_tensor *
 {
     int fmt;
     const size_t K = (size_t)ws[0]->ne0;
-    if (fmt_of(ws[0]->type) != FMT_TQ2)
+    const int f = fmt_of(ws[0]->type);
+    if (f < 0 || (f != FMT_TQ2 && (M != 1 || q || sums)))
         return FOX_GPU_ERR_UNSUPPORTED;
-    if (fused_lds(fmt_of(ws[0]->type), (int)K, (int)M, 1).total > FUSED_LDS_MAX ||
+    if (fused_lds(f, (int)K, (int)M, 1).total > FUSED_LDS_MAX ||
         K > 4 * R4_LIMIT * FWG || !fused_aligned(x ? (const void *)x : (const void *)q,
                                              x ? x_stride : K, M, nullptr))
         return FOX_GPU_ERR_UNSUPPORTED;

@@ -6,11 +6,9 @@
 // holds the 16 rows' bytes of that block, arranged so that lane
 // L = i + 16 g (row i of the tile, k-group g) of a wave reads only its own
 // bytes with aligned 4..16-byte loads.  Byte counts per chunk equal 16 GGUF
-// blocks (no expansion):
+// blocks (no expansion; TQ1_0 tensors are re-encoded at upload as TQ2_0
+// blocks of the same trits, 66 bytes per block instead of 54):
 //
-//   TQ1_0  864 B = QS[64 lanes][12]  lane (i,g): qs[8g..8g+7] ++ qs[32+4g..32+4g+3]
-//                  QH[64 lanes][1]   lane (i,g): qh[g]
-//                  D [16 rows][f16]
 //   TQ2_0 1056 B = QS[64 lanes][16]  lane (i,g): qs[16g..16g+15]
 //                  D [16 rows][f16]
 //   Q4_K  2304 B = QS[64 lanes][32]  lane (i,g): for p<4: qs[32p+8g..32p+8g+7]

@@ -127,15 +127,16 @@ def test_gemv_rmsnorm_nonfinite_follows_the_reference(gpu, oracle, gtype):
 
 
 def test_unsupported_cases_say_so(gpu):
-    """K-quants, and activations too wide for one workgroup, are refused with
-    FOX_GPU_ERR_UNSUPPORTED (the host then runs the separate steps)."""
+    """K-quants for more than one token, and activations too wide for one
+    workgroup, are refused with FOX_GPU_ERR_UNSUPPORTED (the host then runs
+    the separate steps)."""
     rng = np.random.default_rng(3)
     q4 = gpu.tensor(12, 512, 16, weights(rng, 12, 16, 512))
-    x = gpu.array(rng.standard_normal(512).astype(np.float32))
+    x = gpu.array(rng.standard_normal((2, 512)).astype(np.float32))
     nw = gpu.array(np.ones(512, np.float32))
-    out = gpu.empty(16, np.float32)
+    out = gpu.empty(32, np.float32)
     with pytest.raises(rf.FoxError) as e:
-        gpu.gemv_rmsnorm([q4], x, 1, nw, EPS, [out])
+        gpu.gemv_rmsnorm([q4], x, 2, nw, EPS, [out])
     assert e.value.status == 5
     K = 9728
     t = gpu.tensor(34, K, 16, weights(rng, 34, 16, K))
@@ -173,3 +174,71 @@ def test_mixed_types_take_the_separate_steps(gpu):
     with pytest.raises(rf.FoxError) as e:
         gpu.gate_up_silu(narrow, wide, x, 1, nw, EPS, gpu.empty(128, np.float32))
     assert e.value.status == 1
+
+
+@pytest.mark.parametrize("tname,gtype", [("Q4_K", 12), ("Q6_K", 14)])
+@pytest.mark.parametrize("K", [768, 4096])
+def test_kquant_one_token_stages_bit_exact(gpu, oracle, tname, gtype, K):
+    """The K-quants' one-token stages: RMSNorm, per-block quantisation
+    (src/kernels.c:722-754) and the int8 dots (src/kernels.c:571-661) in one
+    launch, with the residual add, with RoPE and the cache store, and with
+    SwiGLU; bit-identical to the oracle's separate steps."""
+    rng = np.random.default_rng([K, gtype, 61])
+    nw = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    xb = oracle.rmsnorm(x[0], nw, EPS)
+    # gemv_rmsnorm over two matrices, the first accumulating
+    Ns = [80, 45]
+    Ws = [weights(rng, gtype, N, K) for N in Ns]
+    base = [rng.standard_normal((1, N)).astype(np.float32) for N in Ns]
+    outs = [gpu.array(b) for b in base]
+    gpu.gemv_rmsnorm([gpu.tensor(gtype, K, N, w) for N, w in zip(Ns, Ws)], gpu.array(x), 1,
+                     gpu.array(nw), EPS, outs, rf.GEMV_ACCUMULATE)
+    for N, W, o, b in zip(Ns, Ws, outs, base):
+        want = b[0] + oracle.gemv(gtype, xb, W, N, K)
+        assert np.array_equal(bits(o.numpy()[0]), bits(want)), f"{tname} rmsnorm {N}"
+    # q, k, v with RoPE
+    n_head, n_kv, hd, n_ctx, pos = 4, 2, 64, 16, 9
+    kvd = n_kv * hd
+    Wq, Wk, Wv = (weights(rng, gtype, n, K) for n in (n_head * hd, kvd, kvd))
+    cos_t, sin_t = oracle.rope_tables(n_ctx, hd, 10000.0)
+    q_out = gpu.empty(n_head * hd, np.float32)
+    kc = gpu.array(np.zeros(n_ctx * kvd, np.float32))
+    vc = gpu.array(np.zeros(n_ctx * kvd, np.float32))
+    gpu.qkv_rope(gpu.tensor(gtype, K, n_head * hd, Wq), gpu.tensor(gtype, K, kvd, Wk),
+                 gpu.tensor(gtype, K, kvd, Wv), gpu.array(x), 1, gpu.array(nw), EPS, q_out,
+                 gpu.array(cos_t), gpu.array(sin_t), gpu.array(np.array([pos], np.uint32)),
+                 n_ctx, kc, vc, hd)
+    half = hd // 2
+    cr, sr = cos_t[pos * half:(pos + 1) * half], sin_t[pos * half:(pos + 1) * half]
+    want_q = oracle.rope(oracle.gemv(gtype, xb, Wq, n_head * hd, K), n_head, hd, cr, sr)
+    want_k = oracle.rope(oracle.gemv(gtype, xb, Wk, kvd, K), n_kv, hd, cr, sr)
+    want_v = oracle.gemv(gtype, xb, Wv, kvd, K)
+    vq = vc.numpy().reshape(-1, kvd, 4)
+    assert np.array_equal(bits(q_out.numpy()), bits(want_q)), f"{tname} q"
+    assert np.array_equal(bits(kc.numpy().reshape(n_ctx, kvd)[pos]), bits(want_k)), f"{tname} k"
+    assert np.array_equal(bits(vq[pos // 4, :, pos % 4]), bits(want_v)), f"{tname} v"
+    # gate / up with SwiGLU
+    ff = 300
+    Wg, Wu = weights(rng, gtype, ff, K), weights(rng, gtype, ff, K)
+    h = gpu.empty(ff, np.float32)
+    gpu.gate_up_silu(gpu.tensor(gtype, K, ff, Wg), gpu.tensor(gtype, K, ff, Wu), gpu.array(x), 1,
+                     gpu.array(nw), EPS, h)
+    want = oracle.silu_mul(oracle.gemv(gtype, xb, Wg, ff, K), oracle.gemv(gtype, xb, Wu, ff, K))
+    assert np.array_equal(bits(h.numpy()), bits(want)), f"{tname} gate/up"
+
+
+@pytest.mark.parametrize("gtype", [12, 14])
+def test_kquant_rmsnorm_nonfinite_follows_the_reference(gpu, oracle, gtype):
+    """RMSNorm then per-block quantisation on rows with NaN, inf and tiny
+    values (NaN outputs compared as NaN)."""
+    rng = np.random.default_rng(41 + gtype)
+    K, N = 512, 40
+    W = weights(rng, gtype, N, K)
+    t = gpu.tensor(gtype, K, N, W)
+    for r, xr in enumerate(nonfinite_rows(rng, K)):
+        nw = rng.uniform(0.5, 1.5, K).astype(np.float32)
+        out = gpu.array(np.zeros((1, N), np.float32))
+        gpu.gemv_rmsnorm([t], gpu.array(xr[None, :]), 1, gpu.array(nw), EPS, [out], 0)
+        want = oracle.gemv(gtype, oracle.rmsnorm(xr, nw, EPS), W, N, K)
+        assert same_or_both_nan(out.numpy()[0], want), r

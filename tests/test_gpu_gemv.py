@@ -223,15 +223,22 @@ def same_or_both_nan(a, b):
     return np.array_equal(nan, np.isnan(b)) and np.array_equal(bits(a[~nan]), bits(b[~nan]))
 
 
-@pytest.mark.parametrize("tname", ["TQ1_0", "TQ2_0"])
+@pytest.mark.parametrize("tname", ["TQ1_0", "TQ2_0", "Q4_K", "Q6_K"])
 def test_fused_gemv_nonfinite_follows_the_reference(gpu, oracle, tname):
     """The fused GEMV's in-workgroup quantiser on the same rows (NaN outputs
-    compared as NaN)."""
+    compared as NaN).  The K-quants quantise per 256-element block
+    (src/kernels.c:722-754), so their rows add an all-zero block beside a
+    normal one and a block of NaNs only (amax 0: zeros, scale 0)."""
     gtype = TYPES[tname]
     rng = np.random.default_rng(21 + gtype)
     K, N = 512, 48
     w = weights(rng, gtype, N, K)
     x = nonfinite_rows(rng, K)
+    if gtype in (12, 14):
+        z = rng.standard_normal((2, K)).astype(np.float32)
+        z[0, :256] = 0.0
+        z[1, 256:] = np.nan
+        x = np.concatenate([x, z])
     M = x.shape[0]
     t = gpu.tensor(gtype, K, N, w)
     for r in range(M):

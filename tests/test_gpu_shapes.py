@@ -206,17 +206,41 @@ def test_27b_qkv_and_gate_up_8_tokens(capped, oracle, M):
             assert not first_diff(o.numpy()[t], want), f"q/k/v rows {n} token {t}"
 
 
-@pytest.mark.parametrize("M", [1, 8])
+@pytest.mark.parametrize("M,cap", [(1, 0), (1, 3), (8, 0)])
 @pytest.mark.parametrize("tname,gtype,N,K", [("Q4_K", 12, 14336, 4096), ("Q6_K", 14, 4096, 14336),
                                              ("Q4_K", 12, 4096, 4096), ("Q6_K", 14, 1024, 4096)])
-def test_8b_kquant_shapes_bit_exact(gpu, oracle, tname, gtype, N, K, M):
+def test_8b_kquant_shapes_bit_exact(capped, oracle, tname, gtype, N, K, M, cap):
     """8B-class Q4_K_M-style matrices: ffn_gate/up (Q4_K 4096 -> 14336),
     ffn_down (Q6_K 14336 -> 4096), attn_q/o (Q4_K 4096 x 4096), attn_v (Q6_K
     4096 -> 1024), weights from the repository's quantiser
-    (src/kernels.c:571-661 int8 dots, per-256 activation scales)."""
-    print(f"case gemv 8b {tname} {N}x{K} M={M}", flush=True)
+    (src/kernels.c:571-661 int8 dots, per-256 activation scales).  One token
+    takes the fused kernel (also with its grid capped to 3 workgroups, each
+    then walking hundreds of tiles), 8 tokens the unfused path."""
+    print(f"case gemv 8b {tname} {N}x{K} M={M} cap={cap}", flush=True)
     w, x, want = case_data(oracle, gtype, N, K, M, 8)
-    out = gpu.empty((M, N), np.float32)
-    gpu.gemv(gpu.tensor(gtype, K, N, w), gpu.array(x), M, out)
+    capped.set_max_workgroups(cap)
+    out = capped.empty((M, N), np.float32)
+    capped.gemv(capped.tensor(gtype, K, N, w), capped.array(x), M, out)
     got = out.numpy()
+    assert not first_diff(got, want), first_diff(got, want)
+
+
+@pytest.mark.parametrize("cap", [0, 5])
+def test_8b_gate_up_silu_bit_exact(capped, oracle, cap):
+    """8B-class ffn_gate/ffn_up (Q4_K 4096 -> 14336, 896 tile pairs) with
+    RMSNorm and SwiGLU in one launch for one token."""
+    K, ff = 4096, 14336
+    print(f"case 8b gate/up cap={cap}", flush=True)
+    rng = np.random.default_rng([K, ff, 88])
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    Wg, Wu = weights(rng, 12, ff, K), weights(rng, 12, ff, K)
+    capped.set_max_workgroups(cap)
+    h = capped.empty(ff, np.float32)
+    capped.gate_up_silu(capped.tensor(12, K, ff, Wg), capped.tensor(12, K, ff, Wu),
+                        capped.array(x), 1, capped.array(nw), EPS, h)
+    xb = oracle.rmsnorm(x[0], nw, EPS)
+    want = oracle.silu_mul(oracle.gemv(12, xb, Wg, ff, K, n_threads=THREADS),
+                           oracle.gemv(12, xb, Wu, ff, K, n_threads=THREADS))
+    got = h.numpy()
     assert not first_diff(got, want), first_diff(got, want)
