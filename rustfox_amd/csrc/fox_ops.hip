@@ -849,36 +849,122 @@ __device__ __forceinline__ void sv_signal(int *flag, int v)
     __hip_atomic_store(flag, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// acc + x_0 + x_1 + ... over 4 * nq floats of LDS, in index order.  Eight
-// quad slots rotate: a slot is reloaded with the quad eight ahead right after
-// its four adds, so the read of a quad has seven quads of adds to complete
-// and no slot is copied (a pipelined pair of quad arrays compiles to a copy
-// of the array per step, which costs as much as the adds).
+// acc + x_0 + x_1 + ... over 4 * nq floats of LDS, in index order.  A
+// dependent add chain is bound by the wave's instruction issue, so the
+// operand reads must cost as few instructions as possible: banks of eight
+// quads alternate, the eight reads of one bank (ds_read_b128 at constant
+// offsets from one address, one wait) in flight while the other bank's 32
+// adds run.  One block of 64 quads is one asm statement (reads, waits and
+// adds, v64-v127 its banks): compiled from C, the reads of such a block are
+// hoisted and reordered across the adds, and a bank carried from one loop
+// iteration to the next is copied every iteration.  LDS reads complete in
+// order, so lgkmcnt(8) after a bank's reads means the previous bank is in.
+// (Measured on gfx950, one wave: 2.5 ns per add this way, 4 ns with a wait
+// and a read between every four adds, 1.8 ns from registers.)
+__device__ __forceinline__ float chain64_lds(float acc, const float4 *q)
+{
+    const uint32_t p = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)q;
+    asm volatile(
+        "ds_read_b128 v[64:67], %[p] offset:0\n" "ds_read_b128 v[68:71], %[p] offset:16\n" "ds_read_b128 v[72:75], %[p] offset:32\n" "ds_read_b128 v[76:79], %[p] offset:48\n"
+        "ds_read_b128 v[80:83], %[p] offset:64\n" "ds_read_b128 v[84:87], %[p] offset:80\n" "ds_read_b128 v[88:91], %[p] offset:96\n" "ds_read_b128 v[92:95], %[p] offset:112\n"
+        "ds_read_b128 v[96:99], %[p] offset:128\n" "ds_read_b128 v[100:103], %[p] offset:144\n" "ds_read_b128 v[104:107], %[p] offset:160\n" "ds_read_b128 v[108:111], %[p] offset:176\n"
+        "ds_read_b128 v[112:115], %[p] offset:192\n" "ds_read_b128 v[116:119], %[p] offset:208\n" "ds_read_b128 v[120:123], %[p] offset:224\n" "ds_read_b128 v[124:127], %[p] offset:240\n"
+        "s_waitcnt lgkmcnt(8)\n" "v_add_f32 %[acc], %[acc], v64\n" "v_add_f32 %[acc], %[acc], v65\n" "v_add_f32 %[acc], %[acc], v66\n"
+        "v_add_f32 %[acc], %[acc], v67\n" "v_add_f32 %[acc], %[acc], v68\n" "v_add_f32 %[acc], %[acc], v69\n" "v_add_f32 %[acc], %[acc], v70\n"
+        "v_add_f32 %[acc], %[acc], v71\n" "v_add_f32 %[acc], %[acc], v72\n" "v_add_f32 %[acc], %[acc], v73\n" "v_add_f32 %[acc], %[acc], v74\n"
+        "v_add_f32 %[acc], %[acc], v75\n" "v_add_f32 %[acc], %[acc], v76\n" "v_add_f32 %[acc], %[acc], v77\n" "v_add_f32 %[acc], %[acc], v78\n"
+        "v_add_f32 %[acc], %[acc], v79\n" "v_add_f32 %[acc], %[acc], v80\n" "v_add_f32 %[acc], %[acc], v81\n" "v_add_f32 %[acc], %[acc], v82\n"
+        "v_add_f32 %[acc], %[acc], v83\n" "v_add_f32 %[acc], %[acc], v84\n" "v_add_f32 %[acc], %[acc], v85\n" "v_add_f32 %[acc], %[acc], v86\n"
+        "v_add_f32 %[acc], %[acc], v87\n" "v_add_f32 %[acc], %[acc], v88\n" "v_add_f32 %[acc], %[acc], v89\n" "v_add_f32 %[acc], %[acc], v90\n"
+        "v_add_f32 %[acc], %[acc], v91\n" "v_add_f32 %[acc], %[acc], v92\n" "v_add_f32 %[acc], %[acc], v93\n" "v_add_f32 %[acc], %[acc], v94\n"
+        "v_add_f32 %[acc], %[acc], v95\n" "ds_read_b128 v[64:67], %[p] offset:256\n" "ds_read_b128 v[68:71], %[p] offset:272\n" "ds_read_b128 v[72:75], %[p] offset:288\n"
+        "ds_read_b128 v[76:79], %[p] offset:304\n" "ds_read_b128 v[80:83], %[p] offset:320\n" "ds_read_b128 v[84:87], %[p] offset:336\n" "ds_read_b128 v[88:91], %[p] offset:352\n"
+        "ds_read_b128 v[92:95], %[p] offset:368\n" "s_waitcnt lgkmcnt(8)\n" "v_add_f32 %[acc], %[acc], v96\n" "v_add_f32 %[acc], %[acc], v97\n"
+        "v_add_f32 %[acc], %[acc], v98\n" "v_add_f32 %[acc], %[acc], v99\n" "v_add_f32 %[acc], %[acc], v100\n" "v_add_f32 %[acc], %[acc], v101\n"
+        "v_add_f32 %[acc], %[acc], v102\n" "v_add_f32 %[acc], %[acc], v103\n" "v_add_f32 %[acc], %[acc], v104\n" "v_add_f32 %[acc], %[acc], v105\n"
+        "v_add_f32 %[acc], %[acc], v106\n" "v_add_f32 %[acc], %[acc], v107\n" "v_add_f32 %[acc], %[acc], v108\n" "v_add_f32 %[acc], %[acc], v109\n"
+        "v_add_f32 %[acc], %[acc], v110\n" "v_add_f32 %[acc], %[acc], v111\n" "v_add_f32 %[acc], %[acc], v112\n" "v_add_f32 %[acc], %[acc], v113\n"
+        "v_add_f32 %[acc], %[acc], v114\n" "v_add_f32 %[acc], %[acc], v115\n" "v_add_f32 %[acc], %[acc], v116\n" "v_add_f32 %[acc], %[acc], v117\n"
+        "v_add_f32 %[acc], %[acc], v118\n" "v_add_f32 %[acc], %[acc], v119\n" "v_add_f32 %[acc], %[acc], v120\n" "v_add_f32 %[acc], %[acc], v121\n"
+        "v_add_f32 %[acc], %[acc], v122\n" "v_add_f32 %[acc], %[acc], v123\n" "v_add_f32 %[acc], %[acc], v124\n" "v_add_f32 %[acc], %[acc], v125\n"
+        "v_add_f32 %[acc], %[acc], v126\n" "v_add_f32 %[acc], %[acc], v127\n" "ds_read_b128 v[96:99], %[p] offset:384\n" "ds_read_b128 v[100:103], %[p] offset:400\n"
+        "ds_read_b128 v[104:107], %[p] offset:416\n" "ds_read_b128 v[108:111], %[p] offset:432\n" "ds_read_b128 v[112:115], %[p] offset:448\n" "ds_read_b128 v[116:119], %[p] offset:464\n"
+        "ds_read_b128 v[120:123], %[p] offset:480\n" "ds_read_b128 v[124:127], %[p] offset:496\n" "s_waitcnt lgkmcnt(8)\n" "v_add_f32 %[acc], %[acc], v64\n"
+        "v_add_f32 %[acc], %[acc], v65\n" "v_add_f32 %[acc], %[acc], v66\n" "v_add_f32 %[acc], %[acc], v67\n" "v_add_f32 %[acc], %[acc], v68\n"
+        "v_add_f32 %[acc], %[acc], v69\n" "v_add_f32 %[acc], %[acc], v70\n" "v_add_f32 %[acc], %[acc], v71\n" "v_add_f32 %[acc], %[acc], v72\n"
+        "v_add_f32 %[acc], %[acc], v73\n" "v_add_f32 %[acc], %[acc], v74\n" "v_add_f32 %[acc], %[acc], v75\n" "v_add_f32 %[acc], %[acc], v76\n"
+        "v_add_f32 %[acc], %[acc], v77\n" "v_add_f32 %[acc], %[acc], v78\n" "v_add_f32 %[acc], %[acc], v79\n" "v_add_f32 %[acc], %[acc], v80\n"
+        "v_add_f32 %[acc], %[acc], v81\n" "v_add_f32 %[acc], %[acc], v82\n" "v_add_f32 %[acc], %[acc], v83\n" "v_add_f32 %[acc], %[acc], v84\n"
+        "v_add_f32 %[acc], %[acc], v85\n" "v_add_f32 %[acc], %[acc], v86\n" "v_add_f32 %[acc], %[acc], v87\n" "v_add_f32 %[acc], %[acc], v88\n"
+        "v_add_f32 %[acc], %[acc], v89\n" "v_add_f32 %[acc], %[acc], v90\n" "v_add_f32 %[acc], %[acc], v91\n" "v_add_f32 %[acc], %[acc], v92\n"
+        "v_add_f32 %[acc], %[acc], v93\n" "v_add_f32 %[acc], %[acc], v94\n" "v_add_f32 %[acc], %[acc], v95\n" "ds_read_b128 v[64:67], %[p] offset:512\n"
+        "ds_read_b128 v[68:71], %[p] offset:528\n" "ds_read_b128 v[72:75], %[p] offset:544\n" "ds_read_b128 v[76:79], %[p] offset:560\n" "ds_read_b128 v[80:83], %[p] offset:576\n"
+        "ds_read_b128 v[84:87], %[p] offset:592\n" "ds_read_b128 v[88:91], %[p] offset:608\n" "ds_read_b128 v[92:95], %[p] offset:624\n" "s_waitcnt lgkmcnt(8)\n"
+        "v_add_f32 %[acc], %[acc], v96\n" "v_add_f32 %[acc], %[acc], v97\n" "v_add_f32 %[acc], %[acc], v98\n" "v_add_f32 %[acc], %[acc], v99\n"
+        "v_add_f32 %[acc], %[acc], v100\n" "v_add_f32 %[acc], %[acc], v101\n" "v_add_f32 %[acc], %[acc], v102\n" "v_add_f32 %[acc], %[acc], v103\n"
+        "v_add_f32 %[acc], %[acc], v104\n" "v_add_f32 %[acc], %[acc], v105\n" "v_add_f32 %[acc], %[acc], v106\n" "v_add_f32 %[acc], %[acc], v107\n"
+        "v_add_f32 %[acc], %[acc], v108\n" "v_add_f32 %[acc], %[acc], v109\n" "v_add_f32 %[acc], %[acc], v110\n" "v_add_f32 %[acc], %[acc], v111\n"
+        "v_add_f32 %[acc], %[acc], v112\n" "v_add_f32 %[acc], %[acc], v113\n" "v_add_f32 %[acc], %[acc], v114\n" "v_add_f32 %[acc], %[acc], v115\n"
+        "v_add_f32 %[acc], %[acc], v116\n" "v_add_f32 %[acc], %[acc], v117\n" "v_add_f32 %[acc], %[acc], v118\n" "v_add_f32 %[acc], %[acc], v119\n"
+        "v_add_f32 %[acc], %[acc], v120\n" "v_add_f32 %[acc], %[acc], v121\n" "v_add_f32 %[acc], %[acc], v122\n" "v_add_f32 %[acc], %[acc], v123\n"
+        "v_add_f32 %[acc], %[acc], v124\n" "v_add_f32 %[acc], %[acc], v125\n" "v_add_f32 %[acc], %[acc], v126\n" "v_add_f32 %[acc], %[acc], v127\n"
+        "ds_read_b128 v[96:99], %[p] offset:640\n" "ds_read_b128 v[100:103], %[p] offset:656\n" "ds_read_b128 v[104:107], %[p] offset:672\n" "ds_read_b128 v[108:111], %[p] offset:688\n"
+        "ds_read_b128 v[112:115], %[p] offset:704\n" "ds_read_b128 v[116:119], %[p] offset:720\n" "ds_read_b128 v[120:123], %[p] offset:736\n" "ds_read_b128 v[124:127], %[p] offset:752\n"
+        "s_waitcnt lgkmcnt(8)\n" "v_add_f32 %[acc], %[acc], v64\n" "v_add_f32 %[acc], %[acc], v65\n" "v_add_f32 %[acc], %[acc], v66\n"
+        "v_add_f32 %[acc], %[acc], v67\n" "v_add_f32 %[acc], %[acc], v68\n" "v_add_f32 %[acc], %[acc], v69\n" "v_add_f32 %[acc], %[acc], v70\n"
+        "v_add_f32 %[acc], %[acc], v71\n" "v_add_f32 %[acc], %[acc], v72\n" "v_add_f32 %[acc], %[acc], v73\n" "v_add_f32 %[acc], %[acc], v74\n"
+        "v_add_f32 %[acc], %[acc], v75\n" "v_add_f32 %[acc], %[acc], v76\n" "v_add_f32 %[acc], %[acc], v77\n" "v_add_f32 %[acc], %[acc], v78\n"
+        "v_add_f32 %[acc], %[acc], v79\n" "v_add_f32 %[acc], %[acc], v80\n" "v_add_f32 %[acc], %[acc], v81\n" "v_add_f32 %[acc], %[acc], v82\n"
+        "v_add_f32 %[acc], %[acc], v83\n" "v_add_f32 %[acc], %[acc], v84\n" "v_add_f32 %[acc], %[acc], v85\n" "v_add_f32 %[acc], %[acc], v86\n"
+        "v_add_f32 %[acc], %[acc], v87\n" "v_add_f32 %[acc], %[acc], v88\n" "v_add_f32 %[acc], %[acc], v89\n" "v_add_f32 %[acc], %[acc], v90\n"
+        "v_add_f32 %[acc], %[acc], v91\n" "v_add_f32 %[acc], %[acc], v92\n" "v_add_f32 %[acc], %[acc], v93\n" "v_add_f32 %[acc], %[acc], v94\n"
+        "v_add_f32 %[acc], %[acc], v95\n" "ds_read_b128 v[64:67], %[p] offset:768\n" "ds_read_b128 v[68:71], %[p] offset:784\n" "ds_read_b128 v[72:75], %[p] offset:800\n"
+        "ds_read_b128 v[76:79], %[p] offset:816\n" "ds_read_b128 v[80:83], %[p] offset:832\n" "ds_read_b128 v[84:87], %[p] offset:848\n" "ds_read_b128 v[88:91], %[p] offset:864\n"
+        "ds_read_b128 v[92:95], %[p] offset:880\n" "s_waitcnt lgkmcnt(8)\n" "v_add_f32 %[acc], %[acc], v96\n" "v_add_f32 %[acc], %[acc], v97\n"
+        "v_add_f32 %[acc], %[acc], v98\n" "v_add_f32 %[acc], %[acc], v99\n" "v_add_f32 %[acc], %[acc], v100\n" "v_add_f32 %[acc], %[acc], v101\n"
+        "v_add_f32 %[acc], %[acc], v102\n" "v_add_f32 %[acc], %[acc], v103\n" "v_add_f32 %[acc], %[acc], v104\n" "v_add_f32 %[acc], %[acc], v105\n"
+        "v_add_f32 %[acc], %[acc], v106\n" "v_add_f32 %[acc], %[acc], v107\n" "v_add_f32 %[acc], %[acc], v108\n" "v_add_f32 %[acc], %[acc], v109\n"
+        "v_add_f32 %[acc], %[acc], v110\n" "v_add_f32 %[acc], %[acc], v111\n" "v_add_f32 %[acc], %[acc], v112\n" "v_add_f32 %[acc], %[acc], v113\n"
+        "v_add_f32 %[acc], %[acc], v114\n" "v_add_f32 %[acc], %[acc], v115\n" "v_add_f32 %[acc], %[acc], v116\n" "v_add_f32 %[acc], %[acc], v117\n"
+        "v_add_f32 %[acc], %[acc], v118\n" "v_add_f32 %[acc], %[acc], v119\n" "v_add_f32 %[acc], %[acc], v120\n" "v_add_f32 %[acc], %[acc], v121\n"
+        "v_add_f32 %[acc], %[acc], v122\n" "v_add_f32 %[acc], %[acc], v123\n" "v_add_f32 %[acc], %[acc], v124\n" "v_add_f32 %[acc], %[acc], v125\n"
+        "v_add_f32 %[acc], %[acc], v126\n" "v_add_f32 %[acc], %[acc], v127\n" "ds_read_b128 v[96:99], %[p] offset:896\n" "ds_read_b128 v[100:103], %[p] offset:912\n"
+        "ds_read_b128 v[104:107], %[p] offset:928\n" "ds_read_b128 v[108:111], %[p] offset:944\n" "ds_read_b128 v[112:115], %[p] offset:960\n" "ds_read_b128 v[116:119], %[p] offset:976\n"
+        "ds_read_b128 v[120:123], %[p] offset:992\n" "ds_read_b128 v[124:127], %[p] offset:1008\n" "s_waitcnt lgkmcnt(8)\n" "v_add_f32 %[acc], %[acc], v64\n"
+        "v_add_f32 %[acc], %[acc], v65\n" "v_add_f32 %[acc], %[acc], v66\n" "v_add_f32 %[acc], %[acc], v67\n" "v_add_f32 %[acc], %[acc], v68\n"
+        "v_add_f32 %[acc], %[acc], v69\n" "v_add_f32 %[acc], %[acc], v70\n" "v_add_f32 %[acc], %[acc], v71\n" "v_add_f32 %[acc], %[acc], v72\n"
+        "v_add_f32 %[acc], %[acc], v73\n" "v_add_f32 %[acc], %[acc], v74\n" "v_add_f32 %[acc], %[acc], v75\n" "v_add_f32 %[acc], %[acc], v76\n"
+        "v_add_f32 %[acc], %[acc], v77\n" "v_add_f32 %[acc], %[acc], v78\n" "v_add_f32 %[acc], %[acc], v79\n" "v_add_f32 %[acc], %[acc], v80\n"
+        "v_add_f32 %[acc], %[acc], v81\n" "v_add_f32 %[acc], %[acc], v82\n" "v_add_f32 %[acc], %[acc], v83\n" "v_add_f32 %[acc], %[acc], v84\n"
+        "v_add_f32 %[acc], %[acc], v85\n" "v_add_f32 %[acc], %[acc], v86\n" "v_add_f32 %[acc], %[acc], v87\n" "v_add_f32 %[acc], %[acc], v88\n"
+        "v_add_f32 %[acc], %[acc], v89\n" "v_add_f32 %[acc], %[acc], v90\n" "v_add_f32 %[acc], %[acc], v91\n" "v_add_f32 %[acc], %[acc], v92\n"
+        "v_add_f32 %[acc], %[acc], v93\n" "v_add_f32 %[acc], %[acc], v94\n" "v_add_f32 %[acc], %[acc], v95\n" "s_waitcnt lgkmcnt(0)\n"
+        "v_add_f32 %[acc], %[acc], v96\n" "v_add_f32 %[acc], %[acc], v97\n" "v_add_f32 %[acc], %[acc], v98\n" "v_add_f32 %[acc], %[acc], v99\n"
+        "v_add_f32 %[acc], %[acc], v100\n" "v_add_f32 %[acc], %[acc], v101\n" "v_add_f32 %[acc], %[acc], v102\n" "v_add_f32 %[acc], %[acc], v103\n"
+        "v_add_f32 %[acc], %[acc], v104\n" "v_add_f32 %[acc], %[acc], v105\n" "v_add_f32 %[acc], %[acc], v106\n" "v_add_f32 %[acc], %[acc], v107\n"
+        "v_add_f32 %[acc], %[acc], v108\n" "v_add_f32 %[acc], %[acc], v109\n" "v_add_f32 %[acc], %[acc], v110\n" "v_add_f32 %[acc], %[acc], v111\n"
+        "v_add_f32 %[acc], %[acc], v112\n" "v_add_f32 %[acc], %[acc], v113\n" "v_add_f32 %[acc], %[acc], v114\n" "v_add_f32 %[acc], %[acc], v115\n"
+        "v_add_f32 %[acc], %[acc], v116\n" "v_add_f32 %[acc], %[acc], v117\n" "v_add_f32 %[acc], %[acc], v118\n" "v_add_f32 %[acc], %[acc], v119\n"
+        "v_add_f32 %[acc], %[acc], v120\n" "v_add_f32 %[acc], %[acc], v121\n" "v_add_f32 %[acc], %[acc], v122\n" "v_add_f32 %[acc], %[acc], v123\n"
+        "v_add_f32 %[acc], %[acc], v124\n" "v_add_f32 %[acc], %[acc], v125\n" "v_add_f32 %[acc], %[acc], v126\n" "v_add_f32 %[acc], %[acc], v127\n"
+        : [acc] "+v"(acc)
+        : [p] "v"(p)
+        : "v64", "v65", "v66", "v67", "v68", "v69", "v70", "v71",
+          "v72", "v73", "v74", "v75", "v76", "v77", "v78", "v79",
+          "v80", "v81", "v82", "v83", "v84", "v85", "v86", "v87",
+          "v88", "v89", "v90", "v91", "v92", "v93", "v94", "v95",
+          "v96", "v97", "v98", "v99", "v100", "v101", "v102", "v103",
+          "v104", "v105", "v106", "v107", "v108", "v109", "v110", "v111",
+          "v112", "v113", "v114", "v115", "v116", "v117", "v118", "v119",
+          "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127",
+          "memory");
+    return acc;
+}
+
 __device__ __forceinline__ float chain_add_lds(float acc, const float4 *p, int nq)
 {
     int q = 0;
-    if (nq >= 16) {
-        float4 S0 = p[0], S1 = p[1], S2 = p[2], S3 = p[3];
-        float4 S4 = p[4], S5 = p[5], S6 = p[6], S7 = p[7];
-        auto add4 = [&](const float4 &v) {
-            acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
-        };
-        // (the scheduling barriers keep each reload after its slot's adds)
-        for (; q + 16 <= nq; q += 8) {
-            add4(S0); S0 = p[q + 8];  __builtin_amdgcn_sched_barrier(0);
-            add4(S1); S1 = p[q + 9];  __builtin_amdgcn_sched_barrier(0);
-            add4(S2); S2 = p[q + 10]; __builtin_amdgcn_sched_barrier(0);
-            add4(S3); S3 = p[q + 11]; __builtin_amdgcn_sched_barrier(0);
-            add4(S4); S4 = p[q + 12]; __builtin_amdgcn_sched_barrier(0);
-            add4(S5); S5 = p[q + 13]; __builtin_amdgcn_sched_barrier(0);
-            add4(S6); S6 = p[q + 14]; __builtin_amdgcn_sched_barrier(0);
-            add4(S7); S7 = p[q + 15]; __builtin_amdgcn_sched_barrier(0);
-        }
-        // the slots hold quads q .. q + 7
-        add4(S0); add4(S1); add4(S2); add4(S3);
-        add4(S4); add4(S5); add4(S6); add4(S7);
-        q += 8;
-    }
+    for (; q + 64 <= nq; q += 64) acc = chain64_lds(acc, p + q);
     for (; q < nq; q++) {
         const float4 v = p[q];
         acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
@@ -1070,6 +1156,10 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
             // waiting and the sum is replaced by NaN below)
             if (ok && f1 < i + 1 && i + 1 < ntile) ok = sv_wait_ge(&ready[stn], i + 1);
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            // tile i's reads are all in (the fence waited for them): its
+            // stage is released here, before the next reads go out (a
+            // release fence after them would wait for them)
+            sv_signal(&consumed, i + 1);
 #pragma unroll
             for (int u = 0; u < 8; u++) X[u] = Pn[u * 64 + sw[u & 3]];
             __builtin_amdgcn_sched_barrier(0);
@@ -1078,7 +1168,6 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
                 acc = acc + Y[u].x; acc = acc + Y[u].y; acc = acc + Y[u].z; acc = acc + Y[u].w;
             }
             __builtin_amdgcn_sched_barrier(0);
-            sv_signal(&consumed, i + 1);
             f1 = __builtin_amdgcn_readfirstlane(p2);
             st = stn;
         }
