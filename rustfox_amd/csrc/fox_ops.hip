@@ -783,6 +783,7 @@ __global__ __launch_bounds__(64) void attn_values_x(const float *__restrict__ at
 #define SV_STAGE (SV_QT * 64 * 16)  // bytes per product stage
 #define SV_EXR (SV_LOADERS * 64)    // positions per exp round
 #define SV_EXP_PF 3                 // exp rounds whose scores are loaded up front
+#define SV_VPF 8                    // product units of V in flight per loader
 #define SV_SPIN (1 << 22)
 #define SV_IDLE_SLEEP 2             // s_sleep units (64 clocks each) between idle polls
 
@@ -861,9 +862,15 @@ __device__ __forceinline__ void sv_signal(int *flag, int v)
 // order, so lgkmcnt(8) after a bank's reads means the previous bank is in.
 // (Measured on gfx950, one wave: 2.5 ns per add this way, 4 ns with a wait
 // and a read between every four adds, 1.8 ns from registers.)
+// the LDS address of a pointer into LDS
+__device__ __forceinline__ uint32_t lds_addr(const void *p)
+{
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
+}
+
 __device__ __forceinline__ float chain64_lds(float acc, const float4 *q)
 {
-    const uint32_t p = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)q;
+    const uint32_t p = lds_addr(q);
     asm volatile(
         "ds_read_b128 v[64:67], %[p] offset:0\n" "ds_read_b128 v[68:71], %[p] offset:16\n" "ds_read_b128 v[72:75], %[p] offset:32\n" "ds_read_b128 v[76:79], %[p] offset:48\n"
         "ds_read_b128 v[80:83], %[p] offset:64\n" "ds_read_b128 v[84:87], %[p] offset:80\n" "ds_read_b128 v[88:91], %[p] offset:96\n" "ds_read_b128 v[92:95], %[p] offset:112\n"
@@ -980,15 +987,14 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
     int np)
 {
     constexpr int DS = 64 / G;               // columns per slice
-    constexpr int NLD = SV_QT / G;           // 16-byte loads per lane per tile
-    constexpr bool DB = G > 1;               // second tile in flight
+    constexpr int NLD = SV_QT / G;           // product units per tile (G quads each)
     extern __shared__ float4 sv_lds[];
     float4 *ring = sv_lds;                                  // [np][SV_QT][64]
     float *e = (float *)(sv_lds + np * SV_QT * 64);         // [G][att_stride + 4]
     __shared__ float mx_s[G], inv_s[G];
     __shared__ int nrm_s[G];
     __shared__ uint64_t tab[32];
-    __shared__ int ready[SV_NP_MAX], consumed, a_ready, e_done;
+    __shared__ int ready[SV_NP_MAX], cnt[SV_NP_MAX], consumed, a_ready, e_done;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
     const int kvd = n_head_kv * hd;
@@ -1005,7 +1011,16 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
     const float4 *v4 = (const float4 *)vc + kvh * hd + (ld < hd ? ld : sl * DS);
     const bool loader = (wave & 3) != 0;     // waves on SIMD 0 do not load
     const int li = wave - 1 - (wave >> 2);
-    float4 vcur[NLD], vnext[DB ? NLD : 1];
+    const int nunit = ntile * NLD;
+    // V of the loader's units li + SV_LOADERS m, SV_VPF of them in flight
+    // (unit u: quads (u % NLD) G .. + G - 1 of tile u / NLD; the lane's
+    // quad is the lq-th of them)
+    auto v_of = [&](int u) -> float4 {
+        const int i = u / NLD, k = u - i * NLD;
+        const int jq = min(i * SV_QT + k * G + lq, nq_all - 1);
+        return v4[(size_t)jq * kvd];
+    };
+    float4 vq[SV_VPF];
 
     // scores of the first SV_EXP_PF exp rounds, loaded first: a wave's loads
     // complete in order, and these are needed as soon as the maxima are
@@ -1021,12 +1036,9 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
                 sc[k][gg] = srow[(size_t)gg * att_stride + (p < upto ? p : 0)];
         }
     }
-    if (loader && li < ntile) {
+    if (loader) {
 #pragma unroll
-        for (int k = 0; k < NLD; k++) {
-            const int jq = min(li * SV_QT + k * G + lq, nq_all - 1);
-            vcur[k] = v4[(size_t)jq * kvd];
-        }
+        for (int m = 0; m < SV_VPF; m++) vq[m] = v_of(min(li + m * SV_LOADERS, nunit - 1));
     }
 
     // ---- head maxima (src/ops.c:26-30: a NaN first score stays the max),
@@ -1050,7 +1062,10 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
             if (lane == 0) mx_s[hg] = s0 != s0 ? s0 : m;
         }
     }
-    if (tid < SV_NP_MAX) ready[tid] = -1;
+    if (tid < SV_NP_MAX) {
+        ready[tid] = -1;
+        cnt[tid] = 0;
+    }
     if (tid < 32) tab[tid] = fox_exp2_tab[tid];
     if (tid == 0) {
         consumed = 0;
@@ -1114,78 +1129,158 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
         sv_signal(&a_ready, 1);
 
         // ---- value sums: lane (head g, column d) adds its products in order.
-        // A tile is read as two halves of eight quads: the second half is in
-        // flight while the first is added, the next tile's first half while
-        // the second is added.
+        // Whole tiles run in one asm loop (the reasons of chain64_lds): a
+        // tile's second half (eight quads, v96-v127) is read while its first
+        // half (v64-v95) is added, then, once tile i + 1 is marked ready, the
+        // next tile's first half while the second half is added.  Tile i + 1's
+        // flag is read with the second half and tested after the first
+        // half's adds; a tile not marked by then is waited for (bounded: a
+        // timed-out wait clears ok, after which the loop runs on without
+        // waiting and the sum is replaced by NaN below).  Tile i's stage is
+        // released once all its reads are in, before the next reads go out.
+        // Ring slots are XOR-swizzled by (quad & 3) (the loaders' four quads
+        // per store fall in different banks): quad u of a stage sits at
+        // lane ^ 4 (u & 3), so four base addresses cover the sixteen quads
+        // with constant offsets.
+        static_assert(SV_QT == 16 && SV_QT * 64 * 16 == 1 << 14 && SV_SPIN == 0x400000,
+                      "the asm loop's tile size, stage size and spin limit");
         const int g = lane / DS, d = sl * DS + (lane - g * DS);
         float acc = 0.0f;
         bool ok = eok && sv_wait_ge(&ready[0], 0);
-        float4 X[8], Y[8];
-        // ring slots are XOR-swizzled by (quad & 3) so that the loaders' four
-        // quads per store fall in different banks
-        int sw[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) sw[c] = lane ^ (c << 2);
-        if (ok) {
-#pragma unroll
-            for (int u = 0; u < 8; u++) X[u] = ring[u * 64 + sw[u & 3]];
-        }
-        // whole tiles.  Tile i + 2's flag is read while tile i's first half
-        // is added and becomes a scalar only at the end of tile i, so no
-        // instruction waits for that read; the test for tile i + 1 uses the
-        // value read during tile i - 1 (a tile not yet marked then is waited
-        // for, which is rare with the stages ahead).
-        // (stage of tile i: i mod np, kept as a running index)
-        const int nwhole = nq / SV_QT;
+        const int nwhole = __builtin_amdgcn_readfirstlane(nq / SV_QT);
         int i = 0, st = 0;
-        int f1 = np > 1 ? sv_peek(&ready[1]) : -1;       // tile 1's flag
-        for (; i < nwhole; i++) {
-            const int stn = st + 1 == np ? 0 : st + 1;
-            const int st2 = stn + 1 == np ? 0 : stn + 1;
-            const float4 *P = ring + st * SV_QT * 64;
-            const float4 *Pn = ring + stn * SV_QT * 64;
-#pragma unroll
-            for (int u = 0; u < 8; u++) Y[u] = P[(8 + u) * 64 + sw[u & 3]];
-            const int p2 = sv_load(&ready[st2]);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                acc = acc + X[u].x; acc = acc + X[u].y; acc = acc + X[u].z; acc = acc + X[u].w;
-            }
-            // (no early exit: after a timed-out wait the loop runs on without
-            // waiting and the sum is replaced by NaN below)
-            if (ok && f1 < i + 1 && i + 1 < ntile) ok = sv_wait_ge(&ready[stn], i + 1);
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-            // tile i's reads are all in (the fence waited for them): its
-            // stage is released here, before the next reads go out (a
-            // release fence after them would wait for them)
-            sv_signal(&consumed, i + 1);
-#pragma unroll
-            for (int u = 0; u < 8; u++) X[u] = Pn[u * 64 + sw[u & 3]];
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                acc = acc + Y[u].x; acc = acc + Y[u].y; acc = acc + Y[u].z; acc = acc + Y[u].w;
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            f1 = __builtin_amdgcn_readfirstlane(p2);
-            st = stn;
+        if (ok && nwhole > 0) {
+            const uint32_t ra = lds_addr(ring);
+            const uint32_t l0 = ra + ((uint32_t)lane << 4), l1 = ra + ((uint32_t)(lane ^ 4) << 4);
+            const uint32_t l2 = ra + ((uint32_t)(lane ^ 8) << 4), l3 = ra + ((uint32_t)(lane ^ 12) << 4);
+            const uint32_t rb = lds_addr(ready), vc = lds_addr(&consumed);
+            const int npu = __builtin_amdgcn_readfirstlane(np);
+            int oks = 1, so, sn, sf, si1, sp;
+            uint32_t va, vv;
+            asm volatile(
+        "ds_read_b128 v[64:67], %[l0] offset:0\n"
+        "ds_read_b128 v[68:71], %[l1] offset:1024\n"
+        "ds_read_b128 v[72:75], %[l2] offset:2048\n"
+        "ds_read_b128 v[76:79], %[l3] offset:3072\n"
+        "ds_read_b128 v[80:83], %[l0] offset:4096\n"
+        "ds_read_b128 v[84:87], %[l1] offset:5120\n"
+        "ds_read_b128 v[88:91], %[l2] offset:6144\n"
+        "ds_read_b128 v[92:95], %[l3] offset:7168\n"
+        "5:\n"
+        "s_lshl_b32 %[so], %[st], 14\n"
+        "v_add_u32 v56, %[so], %[l0]\n"
+        "v_add_u32 v57, %[so], %[l1]\n"
+        "v_add_u32 v58, %[so], %[l2]\n"
+        "v_add_u32 v59, %[so], %[l3]\n"
+        "ds_read_b128 v[96:99], v56 offset:8192\n"
+        "ds_read_b128 v[100:103], v57 offset:9216\n"
+        "ds_read_b128 v[104:107], v58 offset:10240\n"
+        "ds_read_b128 v[108:111], v59 offset:11264\n"
+        "ds_read_b128 v[112:115], v56 offset:12288\n"
+        "ds_read_b128 v[116:119], v57 offset:13312\n"
+        "ds_read_b128 v[120:123], v58 offset:14336\n"
+        "ds_read_b128 v[124:127], v59 offset:15360\n"
+        "s_add_u32 %[sn], %[st], 1\n"
+        "s_cmp_eq_u32 %[sn], %[np]\n"
+        "s_cselect_b32 %[sn], 0, %[sn]\n"
+        "s_lshl_b32 %[sf], %[sn], 2\n"
+        "v_add_u32 %[va], %[sf], %[rb]\n"
+        "ds_read_b32 %[vv], %[va]\n"
+        "s_waitcnt lgkmcnt(9)\n"
+        "v_add_f32 %[acc], %[acc], v64\n" "v_add_f32 %[acc], %[acc], v65\n" "v_add_f32 %[acc], %[acc], v66\n" "v_add_f32 %[acc], %[acc], v67\n"
+        "v_add_f32 %[acc], %[acc], v68\n" "v_add_f32 %[acc], %[acc], v69\n" "v_add_f32 %[acc], %[acc], v70\n" "v_add_f32 %[acc], %[acc], v71\n"
+        "v_add_f32 %[acc], %[acc], v72\n" "v_add_f32 %[acc], %[acc], v73\n" "v_add_f32 %[acc], %[acc], v74\n" "v_add_f32 %[acc], %[acc], v75\n"
+        "v_add_f32 %[acc], %[acc], v76\n" "v_add_f32 %[acc], %[acc], v77\n" "v_add_f32 %[acc], %[acc], v78\n" "v_add_f32 %[acc], %[acc], v79\n"
+        "v_add_f32 %[acc], %[acc], v80\n" "v_add_f32 %[acc], %[acc], v81\n" "v_add_f32 %[acc], %[acc], v82\n" "v_add_f32 %[acc], %[acc], v83\n"
+        "v_add_f32 %[acc], %[acc], v84\n" "v_add_f32 %[acc], %[acc], v85\n" "v_add_f32 %[acc], %[acc], v86\n" "v_add_f32 %[acc], %[acc], v87\n"
+        "v_add_f32 %[acc], %[acc], v88\n" "v_add_f32 %[acc], %[acc], v89\n" "v_add_f32 %[acc], %[acc], v90\n" "v_add_f32 %[acc], %[acc], v91\n"
+        "v_add_f32 %[acc], %[acc], v92\n" "v_add_f32 %[acc], %[acc], v93\n" "v_add_f32 %[acc], %[acc], v94\n" "v_add_f32 %[acc], %[acc], v95\n"
+        "s_waitcnt lgkmcnt(0)\n"
+        "s_add_u32 %[si1], %[i], 1\n"
+        "v_readfirstlane_b32 %[sf], %[vv]\n"
+        "v_mov_b32 %[vv], %[si1]\n"
+        "ds_write_b32 %[vc], %[vv]\n"
+        "s_cmp_ge_u32 %[si1], %[nw]\n"
+        "s_cbranch_scc1 3f\n"
+        "s_cmp_eq_u32 %[ok], 0\n"
+        "s_cbranch_scc1 4f\n"
+        "s_cmp_ge_i32 %[sf], %[si1]\n"
+        "s_cbranch_scc1 4f\n"
+        "s_mov_b32 %[sp], 0x400000\n"
+        "1:\n"
+        "ds_read_b32 %[vv], %[va]\n"
+        "s_waitcnt lgkmcnt(0)\n"
+        "v_readfirstlane_b32 %[sf], %[vv]\n"
+        "s_cmp_ge_i32 %[sf], %[si1]\n"
+        "s_cbranch_scc1 4f\n"
+        "s_sub_u32 %[sp], %[sp], 1\n"
+        "s_cmp_eq_u32 %[sp], 0\n"
+        "s_cbranch_scc0 1b\n"
+        "s_mov_b32 %[ok], 0\n"
+        "4:\n"
+        "s_lshl_b32 %[so], %[sn], 14\n"
+        "v_add_u32 v60, %[so], %[l0]\n"
+        "v_add_u32 v61, %[so], %[l1]\n"
+        "v_add_u32 v62, %[so], %[l2]\n"
+        "v_add_u32 v63, %[so], %[l3]\n"
+        "ds_read_b128 v[64:67], v60 offset:0\n"
+        "ds_read_b128 v[68:71], v61 offset:1024\n"
+        "ds_read_b128 v[72:75], v62 offset:2048\n"
+        "ds_read_b128 v[76:79], v63 offset:3072\n"
+        "ds_read_b128 v[80:83], v60 offset:4096\n"
+        "ds_read_b128 v[84:87], v61 offset:5120\n"
+        "ds_read_b128 v[88:91], v62 offset:6144\n"
+        "ds_read_b128 v[92:95], v63 offset:7168\n"
+        "3:\n"
+        "v_add_f32 %[acc], %[acc], v96\n" "v_add_f32 %[acc], %[acc], v97\n" "v_add_f32 %[acc], %[acc], v98\n" "v_add_f32 %[acc], %[acc], v99\n"
+        "v_add_f32 %[acc], %[acc], v100\n" "v_add_f32 %[acc], %[acc], v101\n" "v_add_f32 %[acc], %[acc], v102\n" "v_add_f32 %[acc], %[acc], v103\n"
+        "v_add_f32 %[acc], %[acc], v104\n" "v_add_f32 %[acc], %[acc], v105\n" "v_add_f32 %[acc], %[acc], v106\n" "v_add_f32 %[acc], %[acc], v107\n"
+        "v_add_f32 %[acc], %[acc], v108\n" "v_add_f32 %[acc], %[acc], v109\n" "v_add_f32 %[acc], %[acc], v110\n" "v_add_f32 %[acc], %[acc], v111\n"
+        "v_add_f32 %[acc], %[acc], v112\n" "v_add_f32 %[acc], %[acc], v113\n" "v_add_f32 %[acc], %[acc], v114\n" "v_add_f32 %[acc], %[acc], v115\n"
+        "v_add_f32 %[acc], %[acc], v116\n" "v_add_f32 %[acc], %[acc], v117\n" "v_add_f32 %[acc], %[acc], v118\n" "v_add_f32 %[acc], %[acc], v119\n"
+        "v_add_f32 %[acc], %[acc], v120\n" "v_add_f32 %[acc], %[acc], v121\n" "v_add_f32 %[acc], %[acc], v122\n" "v_add_f32 %[acc], %[acc], v123\n"
+        "v_add_f32 %[acc], %[acc], v124\n" "v_add_f32 %[acc], %[acc], v125\n" "v_add_f32 %[acc], %[acc], v126\n" "v_add_f32 %[acc], %[acc], v127\n"
+        "s_mov_b32 %[st], %[sn]\n"
+        "s_mov_b32 %[i], %[si1]\n"
+        "s_cmp_lt_u32 %[i], %[nw]\n"
+        "s_cbranch_scc1 5b\n"
+        "s_waitcnt lgkmcnt(0)\n"
+                : [acc] "+v"(acc), [ok] "+s"(oks), [i] "+s"(i), [st] "+s"(st), [so] "=&s"(so),
+                  [sn] "=&s"(sn), [sf] "=&s"(sf), [si1] "=&s"(si1), [sp] "=&s"(sp), [va] "=&v"(va),
+                  [vv] "=&v"(vv)
+                : [nw] "s"(nwhole), [np] "s"(npu), [l0] "v"(l0), [l1] "v"(l1), [l2] "v"(l2),
+                  [l3] "v"(l3), [rb] "v"(rb), [vc] "v"(vc)
+                : "v56", "v57", "v58", "v59", "v60", "v61", "v62", "v63",
+                  "v64", "v65", "v66", "v67", "v68", "v69", "v70", "v71",
+                  "v72", "v73", "v74", "v75", "v76", "v77", "v78", "v79",
+                  "v80", "v81", "v82", "v83", "v84", "v85", "v86", "v87",
+                  "v88", "v89", "v90", "v91", "v92", "v93", "v94", "v95",
+                  "v96", "v97", "v98", "v99", "v100", "v101", "v102", "v103",
+                  "v104", "v105", "v106", "v107", "v108", "v109", "v110", "v111",
+                  "v112", "v113", "v114", "v115", "v116", "v117", "v118", "v119",
+                  "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127",
+                  "scc", "memory");
+            ok = oks != 0;
         }
         // the last tile, partly filled: nfull whole quads, then rem positions
         if (ok && i < ntile) {
-            const float4 *P = ring + st * SV_QT * 64;
+            ok = sv_wait_ge(&ready[st], i);
+            if (ok) {
+                const float4 *P = ring + st * SV_QT * 64;
+                float4 X[SV_QT];
 #pragma unroll
-            for (int u = 0; u < 8; u++) Y[u] = P[(8 + u) * 64 + sw[u & 3]];
-            const int nfull = nq - i * SV_QT;
+                for (int u = 0; u < SV_QT; u++) X[u] = P[u * 64 + (lane ^ ((u & 3) << 2))];
+                const int nfull = nq - i * SV_QT;
 #pragma unroll
-            for (int u = 0; u < 16; u++) {
-                const float4 v = u < 8 ? X[u & 7] : Y[u & 7];
-                if (u < nfull) {
-                    acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
-                } else if (u == nfull && rem) {
-                    acc = acc + v.x;
-                    if (rem > 1) acc = acc + v.y;
-                    if (rem > 2) acc = acc + v.z;
+                for (int u = 0; u < SV_QT; u++) {
+                    const float4 v = X[u];
+                    if (u < nfull) {
+                        acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
+                    } else if (u == nfull && rem) {
+                        acc = acc + v.x;
+                        if (rem > 1) acc = acc + v.y;
+                        if (rem > 2) acc = acc + v.z;
+                    }
                 }
             }
             sv_signal(&consumed, i + 1);
@@ -1199,7 +1294,11 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
     }
     if (!loader) return;
 
-    // ---- loaders: tile i = li, li + SV_LOADERS, ...
+    // ---- loaders: product units u = li, li + SV_LOADERS, ...  A unit is G
+    // quads of one tile for every lane (its G heads x DS columns); the
+    // NLD units of a tile come from NLD different loaders, the last of them
+    // marks the tile ready, so that the first tile is ready after one unit
+    // of work per loader.
     if (!sv_wait_ge_idle(&a_ready, 1)) return;
     // a_j = e_j * (1/sum), or e_j where the sum is not positive
     // (src/ops.c:35-38; e * 1 is e exactly): the scale per head, and that of
@@ -1212,76 +1311,64 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
     float ivm = ivg[0];
 #pragma unroll
     for (int gg = 1; gg < G; gg++) ivm = mine == gg ? ivg[gg] : ivm;
-    // weight quads read per quad of V, and quads of V per batch of reads
-    // (all of a batch's reads are issued before the first is used)
+    // weight quads read per unit (one per head, or the lane's own head's
+    // for the DPP exchange)
     constexpr int RK = DPPX ? 1 : G;
-    constexpr int KC = 8 / RK < NLD ? (8 / RK > 0 ? 8 / RK : 1) : NLD;
-    static_assert(NLD % KC == 0, "read batches cover the tile");
-    // (stage of tile i: i mod np, kept as a running index)
-    const int st_step = SV_LOADERS % np;
-    int s = li % np;
-    for (int i = li; i < ntile; i += SV_LOADERS) {
-        const int inext = i + SV_LOADERS;
-        if (DB && inext < ntile) {
+    int cons_seen = 0;                       // consumed is known to be at least this
+    for (int u0 = li; u0 < nunit; u0 += SV_VPF * SV_LOADERS) {
 #pragma unroll
-            for (int k = 0; k < NLD; k++) {
-                const int jq = min(inext * SV_QT + k * G + lq, nq_all - 1);
-                vnext[DB ? k : 0] = v4[(size_t)jq * kvd];
+        for (int m = 0; m < SV_VPF; m++) {
+            const int u = u0 + m * SV_LOADERS;
+            if (u >= nunit) break;
+            const float4 v = vq[m];
+            const int un = u + SV_VPF * SV_LOADERS;
+            if (un < nunit) vq[m] = v_of(un);
+            const int i = u / NLD, k = u - i * NLD;
+            const int qi = k * G + lq;                       // the lane's quad in the tile
+            const int jq = min(i * SV_QT + qi, nq_all - 1);
+            float4 wq[RK];
+#pragma unroll
+            for (int r = 0; r < RK; r++) wq[r] = ((const float4 *)(e + (DPPX ? mine : r) * estr))[jq];
+            // the tile's stage is free once tile i - np is consumed
+            if (i >= np && cons_seen < i - np + 1) {
+                if (!sv_wait_ge_idle(&consumed, i - np + 1)) return;
+                cons_seen = i - np + 1;
             }
-        }
-        if (i >= np && !sv_wait_ge_idle(&consumed, i - np + 1)) return;
-        float4 *P = ring + s * SV_QT * 64;
-#pragma unroll
-        for (int k0 = 0; k0 < NLD; k0 += KC) {
-            float4 wq[KC * RK];
-#pragma unroll
-            for (int kk = 0; kk < KC; kk++) {
-                const int jq = min(i * SV_QT + (k0 + kk) * G + lq, nq_all - 1);
-#pragma unroll
-                for (int r = 0; r < RK; r++)
-                    wq[kk * RK + r] = ((const float4 *)(e + (DPPX ? mine : r) * estr))[jq];
+            const int st = i % np;
+            float4 *P = ring + st * SV_QT * 64;
+            float4 am = wq[0];
+            if (DPPX) {
+                am.x = am.x * ivm; am.y = am.y * ivm; am.z = am.z * ivm; am.w = am.w * ivm;
             }
 #pragma unroll
-            for (int kk = 0; kk < KC; kk++) {
-                const int k = k0 + kk;
-                const int qi = k * G + lq;                   // quad within the tile
-                const float4 v = vcur[k];
-                float4 am = wq[kk * RK];
+            for (int gg = 0; gg < G; gg++) {
+                float4 a;
                 if (DPPX) {
-                    am.x = am.x * ivm; am.y = am.y * ivm; am.z = am.z * ivm; am.w = am.w * ivm;
+                    // quad_perm: every lane of a quad takes lane (quad base + gg)
+                    const int ctl = G == 4 ? gg * 0x55 : (gg ? 0xF5 : 0xA0);
+                    a.x = dpp_bcast(am.x, ctl);
+                    a.y = dpp_bcast(am.y, ctl);
+                    a.z = dpp_bcast(am.z, ctl);
+                    a.w = dpp_bcast(am.w, ctl);
+                } else {
+                    a = wq[DPPX ? 0 : gg];
+                    a.x = a.x * ivg[gg]; a.y = a.y * ivg[gg];
+                    a.z = a.z * ivg[gg]; a.w = a.w * ivg[gg];
                 }
-#pragma unroll
-                for (int gg = 0; gg < G; gg++) {
-                    float4 a;
-                    if (DPPX) {
-                        // quad_perm: every lane of a quad takes lane (quad base + gg)
-                        const int ctl = G == 4 ? gg * 0x55 : (gg ? 0xF5 : 0xA0);
-                        a.x = dpp_bcast(am.x, ctl);
-                        a.y = dpp_bcast(am.y, ctl);
-                        a.z = dpp_bcast(am.z, ctl);
-                        a.w = dpp_bcast(am.w, ctl);
-                    } else {
-                        a = wq[kk * RK + (DPPX ? 0 : gg)];
-                        a.x = a.x * ivg[gg]; a.y = a.y * ivg[gg];
-                        a.z = a.z * ivg[gg]; a.w = a.w * ivg[gg];
-                    }
-                    float4 p;
-                    p.x = a.x * v.x; p.y = a.y * v.y; p.z = a.z * v.z; p.w = a.w * v.w;
-                    P[qi * 64 + ((gg * DS + (lane - lq * DS)) ^ ((qi & 3) << 2))] = p;
-                }
+                float4 p;
+                p.x = a.x * v.x; p.y = a.y * v.y; p.z = a.z * v.z; p.w = a.w * v.w;
+                P[qi * 64 + ((gg * DS + (lane - lq * DS)) ^ ((qi & 3) << 2))] = p;
             }
-        }
-        sv_signal(&ready[s], i);
-        s += st_step;
-        if (s >= np) s -= np;
-        if (DB) {
-#pragma unroll
-            for (int k = 0; k < NLD; k++) vcur[k] = vnext[DB ? k : 0];
-        } else if (i + SV_LOADERS < ntile) {
-#pragma unroll
-            for (int k = 0; k < NLD; k++) {
-                const int jq = min((i + SV_LOADERS) * SV_QT + k * G + lq, nq_all - 1);
-                vcur[k] = v4[(size_t)jq * kvd];
+            // count the unit; the tile's last unit marks it ready (its
+            // writes, and through their own counts every other unit's, are
+            // complete by then)
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            int old = 0;
+            if (lane == 0) old = __hip_atomic_fetch_add(&cnt[st], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            old = __builtin_amdgcn_readfirstlane(old);
+            if (old == NLD - 1) {
+                if (lane == 0) cnt[st] = 0;          // (no unit of the stage's next tile runs before
+                sv_signal(&ready[st], i);            //  this tile is consumed)
             }
         }
     }
