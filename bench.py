@@ -511,7 +511,7 @@ def main():
         try:
             cpu = cpu_baseline(path, spec, a.cpu_seconds)
             if cpu:
-                log(f"bench: cpu reference {cpu['value']} tok/s on {cpu['cores']} threads")
+                log(f"bench: cpu baseline ({cpu['kind']}) {cpu['value']} tok/s on {cpu['cores']} threads")
         except Exception as e:  # the GPU number stands without it
             log(f"bench: cpu baseline failed: {e}")
 
