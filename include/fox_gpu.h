@@ -202,11 +202,12 @@ fox_gpu_status fox_gpu_gemv_i8(fox_gpu_ctx *ctx, const fox_gpu_tensor *w,
 fox_gpu_status fox_gpu_block_sums(fox_gpu_ctx *ctx, const fox_gpu_tensor *w,
                                   const int8_t *q, size_t M, int32_t *sums);
 
-/* One-launch stages of a decode layer (src/forward.c:318-397) for TQ1_0 and
- * TQ2_0 weights: the input stage (RMSNorm, int8 quantisation) runs inside
- * the GEMV's workgroups, results bit-identical to the separate calls.
- * Other weight types return FOX_GPU_ERR_UNSUPPORTED (use the separate
- * calls); so do activations too large for one workgroup's LDS.
+/* One-launch stages of a decode layer (src/forward.c:318-397): the input
+ * stage (RMSNorm, int8 quantisation) runs inside the GEMV's workgroups,
+ * results bit-identical to the separate calls.  TQ1_0 / TQ2_0 weights for
+ * 1 to FOX_GPU_MAX_TOKENS tokens, Q4_K / Q6_K weights for one token; other
+ * cases return FOX_GPU_ERR_UNSUPPORTED (use the separate calls), and so do
+ * activations too large for one workgroup's LDS.
  *
  * y_i = W_i rmsnorm(x, norm_w) for up to 4 matrices of one type and width
  * (flags as fox_gpu_gemv; the attn_norm / ffn_norm + project steps). */
@@ -217,7 +218,8 @@ fox_gpu_status fox_gpu_gemv_rmsnorm(fox_gpu_ctx *ctx, size_t n,
                                     const size_t *out_strides, unsigned flags);
 
 /* xb = rmsnorm(x, norm_w); q, k, v = W xb; RoPE on q and k at pos[0] + t;
- * q -> q_out, k and v -> the layer's caches (layouts as fox_gpu_rope_store). */
+ * q -> q_out, k and v -> the layer's caches (layouts as fox_gpu_rope_store).
+ * q and k share one type; v may have another (two launches then). */
 fox_gpu_status fox_gpu_qkv_rope(fox_gpu_ctx *ctx, const fox_gpu_tensor *wq,
                                 const fox_gpu_tensor *wk, const fox_gpu_tensor *wv,
                                 const float *x, size_t x_stride, size_t M,

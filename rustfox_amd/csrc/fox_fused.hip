@@ -62,6 +62,7 @@ struct FusedArgs {
     const float *rope_cos, *rope_sin;
     const uint32_t *pos;
     int head_dim, kv_dim, n_ctx;
+    int role0;                  // ROPE: the role (0 q, 1 k, 2 v) of segment 0
     float *k_cache, *v_cache;
 };
 
@@ -903,20 +904,21 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
                 a.out[0][(size_t)ct * a.out_stride[0] + orow] =
                     fox_div(gt, 1.0f + fox_expf(-gt)) * up; // src/ops.c:45-46
             }
-        } else {  // EPI_ROPE: segment 0 q, 1 k, 2 v
+        } else {  // EPI_ROPE: roles 0 q, 1 k, 2 v (segment sg has role role0 + sg)
             const float partner = lane_xor1(y);
+            const int role = sg + a.role0;
             if (owns) {
                 const bool inside = rp < (size_t)a.n_ctx;
                 float v = y;
-                if (sg < 2 && inside) {
+                if (role < 2 && inside) {
                     // src/ops.c:64-69 on the pair (row & ~1, row | 1)
                     v = (orow & 1) ? partner * pre1 + y * pre0 : y * pre0 - partner * pre1;
                 }
-                if (sg == 0) {
+                if (role == 0) {
                     a.out[0][(size_t)ct * a.out_stride[0] + orow] = v;
                 } else if (inside) {
                     const size_t kvd = (size_t)a.kv_dim;
-                    if (sg == 1) a.k_cache[rp * kvd + orow] = v;
+                    if (role == 1) a.k_cache[rp * kvd + orow] = v;
                     else a.v_cache[((rp >> 2) * kvd + orow) * 4 + (rp & 3)] = v;
                 }
             }
@@ -1231,8 +1233,8 @@ extern "C" fox_gpu_status fox_gpu_qkv_rope(fox_gpu_ctx *ctx, const fox_gpu_tenso
     if (wq->ne0 != wk->ne0 || wk->ne0 != wv->ne0 || wk->ne1 != wv->ne1)
         return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: q, k, v must share their width, k and v "
                         "their rows");
-    if (wq->type != wk->type || wk->type != wv->type)   // (a Q4_K_M-style mix: separate steps)
-        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "qkv_rope: q, k, v of different types take "
+    if (wq->type != wk->type)
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "qkv_rope: q and k of different types take "
                         "the separate steps");
     if (head_dim % 2 || wq->ne1 % head_dim || wk->ne1 % head_dim)
         return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: rows are not whole heads of even size");
@@ -1240,9 +1242,13 @@ extern "C" fox_gpu_status fox_gpu_qkv_rope(fox_gpu_ctx *ctx, const fox_gpu_tenso
     if (M > 1 && (x_stride < K || q_stride < wq->ne1))
         return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: stride too small");
     if (n_ctx > 0x7fffffff) return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: n_ctx too large");
-    int fmt;
+    // v of another type than q and k (a Q4_K_M-style mix) runs as a second
+    // launch over the same input
+    const bool split = wv->type != wq->type;
+    int fmt, fmt_v = -1;
     fox_gpu_status st = fused_check(wq->type, K, M, 1, &fmt, true);
     if (st) return st;
+    if (split && (st = fused_check(wv->type, K, M, 1, &fmt_v, true))) return st;
     if (!fused_aligned(x, x_stride, M, norm_w))
         return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "qkv_rope: x and norm_w must be 16-byte "
                         "aligned, the stride a multiple of 4");
@@ -1259,7 +1265,7 @@ extern "C" fox_gpu_status fox_gpu_qkv_rope(fox_gpu_ctx *ctx, const fox_gpu_tenso
     FusedArgs a;
     memset(&a, 0, sizeof(a));
     int tiles;
-    fused_segments(a, 3, ws, outs, strides, M, &tiles);
+    fused_segments(a, split ? 2 : 3, ws, outs, strides, M, &tiles);
     a.out_stride[0] = (int)(M > 1 ? q_stride : wq->ne1);
     a.nb = (int)(K / 256);
     a.M = (int)M;
@@ -1275,7 +1281,14 @@ extern "C" fox_gpu_status fox_gpu_qkv_rope(fox_gpu_ctx *ctx, const fox_gpu_tenso
     a.n_ctx = (int)n_ctx;
     a.k_cache = k_cache;
     a.v_cache = v_cache;
-    return fused_dispatch<IN_NORM, EPI_ROPE>(ctx, fmt, a, tiles);
+    if ((st = fused_dispatch<IN_NORM, EPI_ROPE>(ctx, fmt, a, tiles)) || !split) return st;
+    FusedArgs b = a;
+    const fox_gpu_tensor *wsv[1] = {wv};
+    float *outv[1] = {nullptr};
+    size_t strv[1] = {0};
+    fused_segments(b, 1, wsv, outv, strv, M, &tiles);
+    b.role0 = 2;
+    return fused_dispatch<IN_NORM, EPI_ROPE>(ctx, fmt_v, b, tiles);
 }
 
 extern "C" fox_gpu_status fox_gpu_gate_up_silu(fox_gpu_ctx *ctx, const fox_gpu_tensor *wg,

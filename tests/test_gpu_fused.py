@@ -148,22 +148,28 @@ def test_unsupported_cases_say_so(gpu):
 
 
 def test_mixed_types_take_the_separate_steps(gpu):
-    """A Q4_K_M-style layer (Q4_K attn_q/k, Q6_K attn_v; gate and up of
-    different types) is refused by the one-launch stages with
-    FOX_GPU_ERR_UNSUPPORTED, the status on which the host runs the
-    separate steps; mismatched widths remain FOX_GPU_ERR_ARG."""
+    """Gate and up of different types, and q and k of different types, are
+    refused by the one-launch stages with FOX_GPU_ERR_UNSUPPORTED, the
+    status on which the host runs the separate steps; so is a Q4_K_M-style
+    q/k/v (Q4_K q and k, Q6_K v) for more than one token.  Mismatched widths
+    remain FOX_GPU_ERR_ARG."""
     rng = np.random.default_rng(4)
     K, hd, n_ctx = 512, 64, 8
     q4 = [gpu.tensor(12, K, 128, weights(rng, 12, 128, K)) for _ in range(2)]
     q6 = gpu.tensor(14, K, 128, weights(rng, 14, 128, K))
     x = gpu.array(rng.standard_normal(K).astype(np.float32))
+    x2 = gpu.array(rng.standard_normal((2, K)).astype(np.float32))
     nw = gpu.array(np.ones(K, np.float32))
     cs = gpu.array(np.ones(n_ctx * hd // 2, np.float32))
     pos = gpu.array(np.zeros(1, np.uint32))
     kc = gpu.empty(n_ctx * 128, np.float32)
     vc = gpu.empty(n_ctx * 128, np.float32)
     with pytest.raises(rf.FoxError) as e:
-        gpu.qkv_rope(q4[0], q4[1], q6, x, 1, nw, EPS, gpu.empty(128, np.float32), cs, cs, pos,
+        gpu.qkv_rope(q4[0], q6, q4[1], x, 1, nw, EPS, gpu.empty(128, np.float32), cs, cs, pos,
+                     n_ctx, kc, vc, hd)
+    assert e.value.status == 5
+    with pytest.raises(rf.FoxError) as e:
+        gpu.qkv_rope(q4[0], q4[1], q6, x2, 2, nw, EPS, gpu.empty(256, np.float32), cs, cs, pos,
                      n_ctx, kc, vc, hd)
     assert e.value.status == 5
     with pytest.raises(rf.FoxError) as e:
@@ -242,3 +248,37 @@ def test_kquant_rmsnorm_nonfinite_follows_the_reference(gpu, oracle, gtype):
         gpu.gemv_rmsnorm([t], gpu.array(xr[None, :]), 1, gpu.array(nw), EPS, [out], 0)
         want = oracle.gemv(gtype, oracle.rmsnorm(xr, nw, EPS), W, N, K)
         assert same_or_both_nan(out.numpy()[0], want), r
+
+
+@pytest.mark.parametrize("K,pos", [(768, 3), (4096, 13)])
+def test_q4_k_m_qkv_rope_bit_exact(gpu, oracle, K, pos):
+    """A Q4_K_M-style q/k/v for one token: Q4_K q and k with RoPE in one
+    launch, Q6_K v into the cache in a second, both from rmsnorm(x)."""
+    n_head, n_kv, hd, n_ctx = 4, 2, 64, 16
+    kvd = n_kv * hd
+    rng = np.random.default_rng([K, pos, 62])
+    Wq, Wk = weights(rng, 12, n_head * hd, K), weights(rng, 12, kvd, K)
+    Wv = weights(rng, 14, kvd, K)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    cos_t, sin_t = oracle.rope_tables(n_ctx, hd, 10000.0)
+    q_out = gpu.empty(n_head * hd, np.float32)
+    kc = gpu.array(np.zeros(n_ctx * kvd, np.float32))
+    vc = gpu.array(np.zeros(n_ctx * kvd, np.float32))
+    gpu.qkv_rope(gpu.tensor(12, K, n_head * hd, Wq), gpu.tensor(12, K, kvd, Wk),
+                 gpu.tensor(14, K, kvd, Wv), gpu.array(x), 1, gpu.array(nw), EPS, q_out,
+                 gpu.array(cos_t), gpu.array(sin_t), gpu.array(np.array([pos], np.uint32)),
+                 n_ctx, kc, vc, hd)
+    xb = oracle.rmsnorm(x[0], nw, EPS)
+    half = hd // 2
+    cr, sr = cos_t[pos * half:(pos + 1) * half], sin_t[pos * half:(pos + 1) * half]
+    want_q = oracle.rope(oracle.gemv(12, xb, Wq, n_head * hd, K), n_head, hd, cr, sr)
+    want_k = oracle.rope(oracle.gemv(12, xb, Wk, kvd, K), n_kv, hd, cr, sr)
+    want_v = oracle.gemv(14, xb, Wv, kvd, K)
+    vq = vc.numpy().reshape(-1, kvd, 4)
+    got_k = kc.numpy().reshape(n_ctx, kvd)
+    assert np.array_equal(bits(q_out.numpy()), bits(want_q))
+    assert np.array_equal(bits(got_k[pos]), bits(want_k))
+    assert np.array_equal(bits(vq[pos // 4, :, pos % 4]), bits(want_v))
+    others = [p for p in range(n_ctx) if p != pos]
+    assert not got_k[others].any()
