@@ -860,6 +860,9 @@ __device__ __forceinline__ void sv_signal(int *flag, int v)
 // hoisted and reordered across the adds, and a bank carried from one loop
 // iteration to the next is copied every iteration.  LDS reads complete in
 // order, so lgkmcnt(8) after a bank's reads means the previous bank is in.
+// Read-write operands are early-clobber ("+&"): the asm writes them before
+// it has read every input, so no input may share their registers (an input
+// equal to acc's initial bits would otherwise be given acc's register).
 // (Measured on gfx950, one wave: 2.5 ns per add this way, 4 ns with a wait
 // and a read between every four adds, 1.8 ns from registers.)
 // the LDS address of a pointer into LDS
@@ -954,7 +957,7 @@ __device__ __forceinline__ float chain64_lds(float acc, const float4 *q)
         "v_add_f32 %[acc], %[acc], v116\n" "v_add_f32 %[acc], %[acc], v117\n" "v_add_f32 %[acc], %[acc], v118\n" "v_add_f32 %[acc], %[acc], v119\n"
         "v_add_f32 %[acc], %[acc], v120\n" "v_add_f32 %[acc], %[acc], v121\n" "v_add_f32 %[acc], %[acc], v122\n" "v_add_f32 %[acc], %[acc], v123\n"
         "v_add_f32 %[acc], %[acc], v124\n" "v_add_f32 %[acc], %[acc], v125\n" "v_add_f32 %[acc], %[acc], v126\n" "v_add_f32 %[acc], %[acc], v127\n"
-        : [acc] "+v"(acc)
+        : [acc] "+&v"(acc)
         : [p] "v"(p)
         : "v64", "v65", "v66", "v67", "v68", "v69", "v70", "v71",
           "v72", "v73", "v74", "v75", "v76", "v77", "v78", "v79",
@@ -1245,7 +1248,7 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
         "s_cmp_lt_u32 %[i], %[nw]\n"
         "s_cbranch_scc1 5b\n"
         "s_waitcnt lgkmcnt(0)\n"
-                : [acc] "+v"(acc), [ok] "+s"(oks), [i] "+s"(i), [st] "+s"(st), [so] "=&s"(so),
+                : [acc] "+&v"(acc), [ok] "+&s"(oks), [i] "+&s"(i), [st] "+&s"(st), [so] "=&s"(so),
                   [sn] "=&s"(sn), [sf] "=&s"(sf), [si1] "=&s"(si1), [sp] "=&s"(sp), [va] "=&v"(va),
                   [vv] "=&v"(vv)
                 : [nw] "s"(nwhole), [np] "s"(npu), [l0] "v"(l0), [l1] "v"(l1), [l2] "v"(l2),
