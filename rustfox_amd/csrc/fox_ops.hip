@@ -525,8 +525,10 @@ __device__ __forceinline__ void copy_to_lds16(const void *src, void *dst)
 // copy is issued at the start, and the dot products of chunk c run once that
 // chunk is in, while the later ones are still arriving (each sum stays in
 // head-dimension order, chunk after chunk).  A chunk holds 64 rows of 8
-// quads; quad j of row r sits in slot j ^ (r & 7), so that the 64 lanes'
-// reads of one quad fall in different banks.
+// quads (128 B a row); quad j of row r sits in slot j ^ ((r >> 1) & 7), so
+// that sixteen consecutive lanes' reads of one quad fall in different banks
+// (rows r and r + 1 differ in the 32-bank half, r and r + 2 .. r + 14 in the
+// slot).
 template <int NCH>
 __global__ __launch_bounds__(256) void attn_scores_x(const float *__restrict__ q,
                                                      size_t q_stride,
@@ -574,14 +576,14 @@ __global__ __launch_bounds__(256) void attn_scores_x(const float *__restrict__ q
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             const int b = 2 * wave + r, row = 8 * b + (lane >> 3);
-            const int j = (lane & 7) ^ (row & 7);
+            const int j = (lane & 7) ^ ((row >> 1) & 7);
             const int cq = min(SC_CQ * c + j, nv - 1);
             copy_to_lds16(kbase + (size_t)min(row, pn - 1) * kvd + 4 * cq,
                           kq(c) + 8 * b * SC_CQ);
         }
     }
     const bool ok = lane < pn;
-    const int row = ok ? lane : 0, sw = row & 7;
+    const int row = ok ? lane : 0, sw = (row >> 1) & 7;
     constexpr int HW = ATT_MAXG / 4;                // heads per wave at most
     float a[HW];
 #pragma unroll
