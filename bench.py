@@ -253,6 +253,45 @@ def gemv_only():
     log(f"bench: gemv-only {r['us_per_launch']} us per launch; copied {COPY_BYTES} bytes twice")
 
 
+READ_PROBE_BYTES = 1 << 30
+
+
+def read_probe():
+    """The HBM read ceiling: a 1 GiB streaming read (fox_gpu_read_probe,
+    workgroups reading contiguous chunks) with 1 to 16 16-byte loads in flight
+    per thread and 1024 to 8192 workgroups of 256 threads, beside a device
+    copy of the same size; mean of 10 timed
+    launches after 2 untimed ones, HIP events on the launching stream.  One
+    JSON line per case on stdout."""
+    gpu = rf.Gpu(0)
+    src = gpu.empty(READ_PROBE_BYTES, np.uint8)
+    dst = gpu.empty(READ_PROBE_BYTES, np.uint8)
+    src.fill(0x5a)
+    sink = gpu.array(np.zeros(1, np.uint32))
+    e0, e1 = gpu.event(), gpu.event()
+
+    def timed(run):
+        for _ in range(2):
+            run()
+        gpu.record(e0)
+        for _ in range(10):
+            run()
+        gpu.record(e1)
+        return gpu.elapsed_ms(e0, e1) / 10
+    for loads in (1, 2, 4, 8, 16):
+        for grid in (1024, 2048, 4096, 8192):
+            ms = timed(lambda: gpu.read_probe(src, READ_PROBE_BYTES, loads, grid, sink))
+            print(json.dumps({"probe": "read", "loads_in_flight": loads, "workgroups": grid,
+                              "us": round(ms * 1e3, 1),
+                              "gbs": round(READ_PROBE_BYTES / ms / 1e6, 1)}), flush=True)
+    ms = timed(lambda: gpu.copy(dst, src, READ_PROBE_BYTES))
+    print(json.dumps({"probe": "copy", "us": round(ms * 1e3, 1),
+                      "gbs_read": round(READ_PROBE_BYTES / ms / 1e6, 1),
+                      "gbs_read_plus_write": round(2 * READ_PROBE_BYTES / ms / 1e6, 1)}),
+          flush=True)
+    gpu.close()
+
+
 def pmc_run(counter, timeout):
     """Per-dispatch readings of one counter over a --gemv-only run:
     (mean of the fused GEMV's, largest of the device copy's), in KiB."""
@@ -440,6 +479,9 @@ def main():
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the roofline GEMV case and a 256 MB device copy (the runs "
                          "that rocprofv3 --pmc counts for the traffic figure)")
+    ap.add_argument("--read-probe", action="store_true",
+                    help="only the HBM read-ceiling probe (1 GiB streaming reads with 1-16 "
+                         "loads in flight per thread, and a device copy), one JSON line per case")
     a = ap.parse_args()
 
     if a.gpus != 1:
@@ -449,6 +491,9 @@ def main():
 
     if a.gemv_only:
         gemv_only()
+        return
+    if a.read_probe:
+        read_probe()
         return
     # (child processes: they run before this process initialises the GPU)
     traffic = None if (a.no_traffic or a.no_gemv) else measure_traffic()

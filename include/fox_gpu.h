@@ -88,6 +88,15 @@ fox_gpu_status fox_gpu_memcpy_d2d(fox_gpu_ctx *ctx, void *dst, const void *src, 
 fox_gpu_status fox_gpu_memset(fox_gpu_ctx *ctx, void *dst, int value, size_t n);
 fox_gpu_status fox_gpu_sync(fox_gpu_ctx *ctx);
 
+/* Diagnostic, no counterpart in RustFox: a streaming read of n bytes
+ * (n and src 16-byte aligned) by `grid` workgroups of 256 threads reading
+ * contiguous chunks of loads x 4 KB, each thread keeping `loads` (1, 2, 4, 8
+ * or 16) 16-byte loads in flight; sink
+ * (device memory, 4 bytes) is written only if the folded data hit a fixed
+ * constant.  It measures the HBM read ceiling the GEMVs are compared with. */
+fox_gpu_status fox_gpu_read_probe(fox_gpu_ctx *ctx, const void *src, size_t n, int loads,
+                                  int grid, uint32_t *sink);
+
 /* ------------------------------------------------------------ weights */
 
 /* Upload one GGUF tensor (`bytes` = its GGUF size, host pointer) into HBM.

@@ -60,6 +60,7 @@ def gpu_lib() -> C.CDLL:
         "fox_gpu_memcpy_h2d": [vp, vp, vp, sz],
         "fox_gpu_memcpy_d2h": [vp, vp, vp, sz],
         "fox_gpu_memcpy_d2d": [vp, vp, vp, sz],
+        "fox_gpu_read_probe": [vp, vp, sz, C.c_int, C.c_int, vp],
         "fox_gpu_memset": [vp, vp, C.c_int, sz],
         "fox_gpu_sync": [vp],
         "fox_gpu_tensor_upload": [vp, C.c_int, C.c_uint64, C.c_uint64, vp, C.c_uint64,
@@ -248,6 +249,11 @@ class Gpu:
     def copy(self, dst: DeviceArray, src: DeviceArray, nbytes: int):
         """Device-to-device copy on the context's stream (fox_gpu_memcpy_d2d)."""
         _check(self.lib.fox_gpu_memcpy_d2d(self.ctx, dst.ptr, src.ptr, nbytes))
+
+    def read_probe(self, src: DeviceArray, nbytes: int, loads: int, grid: int, sink: DeviceArray):
+        """Streaming read of nbytes with `loads` 16-byte loads in flight per
+        thread (fox_gpu_read_probe; a diagnostic of the HBM read ceiling)."""
+        _check(self.lib.fox_gpu_read_probe(self.ctx, src.ptr, nbytes, loads, grid, sink.ptr))
 
     # -- compute (device arrays in, device arrays out)
     def quantize(self, mode, x: DeviceArray, K, M, x_stride, q: DeviceArray, scale: DeviceArray):
