@@ -415,10 +415,13 @@ __global__ __launch_bounds__(WG) void gemv_blocks(Segs segs, int nb, int M, int 
 // tile of a large head is resident at once: with whole chunks only two
 // workgroups fit a CU and the last tiles run in a second, mostly idle
 // round.)
-#define FR 256      // rows per workgroup
+#define FR 256      // rows per tile of the layout
 
-template <typename WT, int MT>
-__global__ __launch_bounds__(FR) void gemv_float(const WT *__restrict__ W, int K, int N,
+// RW rows per workgroup (FR, or FR / 2: two workgroups per tile, each
+// reading its half of every chunk, which spreads a large head's rows more
+// evenly over the compute units)
+template <typename WT, int MT, int RW>
+__global__ __launch_bounds__(RW) void gemv_float(const WT *__restrict__ W, int K, int N,
                                                  const float *__restrict__ x, int x_stride,
                                                  int M, float *__restrict__ out,
                                                  int out_stride, unsigned flags)
@@ -427,18 +430,19 @@ __global__ __launch_bounds__(FR) void gemv_float(const WT *__restrict__ W, int K
     constexpr int RDW = FK * sizeof(WT) / 4;           // dwords of a row per step
     constexpr int RSTR = RDW + 1;                       // padded row stride
     constexpr int PPR = RDW / 4;                        // 16-byte pieces per row and step
-    constexpr int NP = FR * PPR / FR;                   // pieces per thread
-    __shared__ uint32_t wl[2][FR * RSTR];
+    constexpr int NP = PPR;                             // pieces per thread
+    __shared__ uint32_t wl[2][RW * RSTR];
     __shared__ float xs[2][MT * FK];
     if (MT == 1) M = 1;
     const int tid = threadIdx.x;
-    const int r0 = blockIdx.x * FR;
+    const int r0 = blockIdx.x * RW;
     const int nchunk = (K + FK - 1) / FK;               // steps
     const int nch128 = (K + 2 * FK - 1) / (2 * FK);     // 128-byte chunks of the layout
     // this tile's chunks, 32 KB each (rows and columns zero-padded)
-    const uint4 *tw = (const uint4 *)W + (size_t)blockIdx.x * nch128 * (FR * 2 * PPR);
+    const uint4 *tw = (const uint4 *)W + (size_t)(blockIdx.x / (FR / RW)) * nch128 * (FR * 2 * PPR) +
+                      (size_t)(blockIdx.x % (FR / RW)) * RW * 2 * PPR;
 
-    constexpr int XPT = (MT * FK + FR - 1) / FR;        // activations staged per thread
+    constexpr int XPT = (MT * FK + RW - 1) / RW;        // activations staged per thread
     uint4 R[NP];
     float xr[XPT];
     // global -> registers for chunk c (rows past N and columns past K read 0)
@@ -448,12 +452,12 @@ __global__ __launch_bounds__(FR) void gemv_float(const WT *__restrict__ W, int K
         const uint4 *cw = tw + (size_t)(c >> 1) * (FR * 2 * PPR) + (c & 1) * PPR;
 #pragma unroll
         for (int i = 0; i < NP; i++) {
-            const int pc = tid + i * FR, r = pc / PPR, part = pc - r * PPR;
+            const int pc = tid + i * RW, r = pc / PPR, part = pc - r * PPR;
             R[i] = cw[r * 2 * PPR + part];
         }
 #pragma unroll
         for (int v = 0; v < XPT; v++) {
-            const int e = tid + v * FR;
+            const int e = tid + v * RW;
             xr[v] = 0.0f;
             if (e < M * FK) {
                 const int t = e / FK, kk = e - t * FK;
@@ -464,7 +468,7 @@ __global__ __launch_bounds__(FR) void gemv_float(const WT *__restrict__ W, int K
     auto stash = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < NP; i++) {
-            const int pc = tid + i * FR, r = pc / PPR, part = pc - r * PPR;
+            const int pc = tid + i * RW, r = pc / PPR, part = pc - r * PPR;
             uint32_t *d = &wl[buf][r * RSTR + part * 4];
             d[0] = R[i].x;
             d[1] = R[i].y;
@@ -473,7 +477,7 @@ __global__ __launch_bounds__(FR) void gemv_float(const WT *__restrict__ W, int K
         }
 #pragma unroll
         for (int v = 0; v < XPT; v++) {
-            const int e = tid + v * FR;
+            const int e = tid + v * RW;
             if (e < M * FK) xs[buf][e] = xr[v];
         }
     };
@@ -680,23 +684,27 @@ static fox_gpu_status gemv_launch_ws(fox_gpu_ctx *ctx, size_t n, const fox_gpu_t
                             "gemv: %s weights take float activations", fox_type_name(type));
         for (size_t i = 0; i < n; i++) {
             const int N = (int)ws[i]->ne1;
+            // one token: half-tile workgroups (a 151936-row head is 1187 of
+            // them: 4.6 per compute unit, against 2.3 whole tiles)
+            constexpr int RH = FR / 2;
             dim3 grid((unsigned)((N + FR - 1) / FR)), block(FR);
+            dim3 grid1((unsigned)((N + RH - 1) / RH)), block1(RH);
             const _Float16 *wh = (const _Float16 *)ws[i]->d;
             const float *wf = (const float *)ws[i]->d;
             if (type == FOX_GPU_F16 && M == 1)
-                hipLaunchKernelGGL((gemv_float<_Float16, 1>), grid, block, 0, ctx->stream, wh,
+                hipLaunchKernelGGL((gemv_float<_Float16, 1, RH>), grid1, block1, 0, ctx->stream, wh,
                                    (int)K, N, x, (int)x_stride, (int)M, outs[i],
                                    (int)out_strides[i], flags);
             else if (type == FOX_GPU_F16)
-                hipLaunchKernelGGL((gemv_float<_Float16, FOX_GPU_MAX_TOKENS>), grid, block, 0,
+                hipLaunchKernelGGL((gemv_float<_Float16, FOX_GPU_MAX_TOKENS, FR>), grid, block, 0,
                                    ctx->stream, wh, (int)K, N, x, (int)x_stride, (int)M, outs[i],
                                    (int)out_strides[i], flags);
             else if (M == 1)
-                hipLaunchKernelGGL((gemv_float<float, 1>), grid, block, 0, ctx->stream, wf,
+                hipLaunchKernelGGL((gemv_float<float, 1, RH>), grid1, block1, 0, ctx->stream, wf,
                                    (int)K, N, x, (int)x_stride, (int)M, outs[i],
                                    (int)out_strides[i], flags);
             else
-                hipLaunchKernelGGL((gemv_float<float, FOX_GPU_MAX_TOKENS>), grid, block, 0,
+                hipLaunchKernelGGL((gemv_float<float, FOX_GPU_MAX_TOKENS, FR>), grid, block, 0,
                                    ctx->stream, wf, (int)K, N, x, (int)x_stride, (int)M, outs[i],
                                    (int)out_strides[i], flags);
             FOX_LAUNCHED("gemv_float");
