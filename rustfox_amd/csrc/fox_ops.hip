@@ -1138,11 +1138,13 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
         // tile's second half (eight quads, v96-v127) is read while its first
         // half (v64-v95) is added, then, once tile i + 1 is marked ready, the
         // next tile's first half while the second half is added.  Tile i + 1's
-        // flag is read with the second half and tested after the first
-        // half's adds; a tile not marked by then is waited for (bounded: a
-        // timed-out wait clears ok, after which the loop runs on without
-        // waiting and the sum is replaced by NaN below).  Tile i's stage is
-        // released once all its reads are in, before the next reads go out.
+        // flag is read a tile ahead (with tile i's first half) and tested
+        // after tile i's first half's adds; a tile not marked by then is
+        // waited for out of line (bounded: a timed-out wait clears ok, after
+        // which the loop runs on without waiting and the sum is replaced by
+        // NaN below).  Tile i's stage is released once all its reads are in,
+        // before the next reads go out; the stage's four base addresses
+        // (v56-v59) are computed once per tile.
         // Ring slots are XOR-swizzled by (quad & 3) (the loaders' four quads
         // per store fall in different banks): quad u of a stage sits at
         // lane ^ 4 (u & 3), so four base addresses cover the sixteen quads
@@ -1161,22 +1163,31 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
             const uint32_t rb = lds_addr(ready), vc = lds_addr(&consumed);
             const int npu = __builtin_amdgcn_readfirstlane(np);
             int oks = 1, so, sn, sf, si1, sp;
-            uint32_t va, vv;
+            uint32_t va, vv, vf;
             asm volatile(
-        "ds_read_b128 v[64:67], %[l0] offset:0\n"
-        "ds_read_b128 v[68:71], %[l1] offset:1024\n"
-        "ds_read_b128 v[72:75], %[l2] offset:2048\n"
-        "ds_read_b128 v[76:79], %[l3] offset:3072\n"
-        "ds_read_b128 v[80:83], %[l0] offset:4096\n"
-        "ds_read_b128 v[84:87], %[l1] offset:5120\n"
-        "ds_read_b128 v[88:91], %[l2] offset:6144\n"
-        "ds_read_b128 v[92:95], %[l3] offset:7168\n"
+        "v_mov_b32 v56, %[l0]\n"
+        "v_mov_b32 v57, %[l1]\n"
+        "v_mov_b32 v58, %[l2]\n"
+        "v_mov_b32 v59, %[l3]\n"
+        "ds_read_b128 v[64:67], v56 offset:0\n"
+        "ds_read_b128 v[68:71], v57 offset:1024\n"
+        "ds_read_b128 v[72:75], v58 offset:2048\n"
+        "ds_read_b128 v[76:79], v59 offset:3072\n"
+        "ds_read_b128 v[80:83], v56 offset:4096\n"
+        "ds_read_b128 v[84:87], v57 offset:5120\n"
+        "ds_read_b128 v[88:91], v58 offset:6144\n"
+        "ds_read_b128 v[92:95], v59 offset:7168\n"
+        "s_add_u32 %[si1], %[i], 1\n"
+        "s_cmp_ge_u32 %[si1], %[nw]\n"
+        "s_cbranch_scc1 5f\n"
+        "s_add_u32 %[sn], %[st], 1\n"
+        "s_cmp_eq_u32 %[sn], %[np]\n"
+        "s_cselect_b32 %[sn], 0, %[sn]\n"
+        "s_lshl_b32 %[sf], %[sn], 2\n"
+        "v_add_u32 %[va], %[sf], %[rb]\n"
+        "ds_read_b32 %[vf], %[va]\n"
         "5:\n"
-        "s_lshl_b32 %[so], %[st], 14\n"
-        "v_add_u32 v56, %[so], %[l0]\n"
-        "v_add_u32 v57, %[so], %[l1]\n"
-        "v_add_u32 v58, %[so], %[l2]\n"
-        "v_add_u32 v59, %[so], %[l3]\n"
+        "6:\n"
         "ds_read_b128 v[96:99], v56 offset:8192\n"
         "ds_read_b128 v[100:103], v57 offset:9216\n"
         "ds_read_b128 v[104:107], v58 offset:10240\n"
@@ -1185,13 +1196,11 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
         "ds_read_b128 v[116:119], v57 offset:13312\n"
         "ds_read_b128 v[120:123], v58 offset:14336\n"
         "ds_read_b128 v[124:127], v59 offset:15360\n"
+        "s_add_u32 %[si1], %[i], 1\n"
         "s_add_u32 %[sn], %[st], 1\n"
         "s_cmp_eq_u32 %[sn], %[np]\n"
         "s_cselect_b32 %[sn], 0, %[sn]\n"
-        "s_lshl_b32 %[sf], %[sn], 2\n"
-        "v_add_u32 %[va], %[sf], %[rb]\n"
-        "ds_read_b32 %[vv], %[va]\n"
-        "s_waitcnt lgkmcnt(9)\n"
+        "s_waitcnt lgkmcnt(8)\n"
         "v_add_f32 %[acc], %[acc], v64\n" "v_add_f32 %[acc], %[acc], v65\n" "v_add_f32 %[acc], %[acc], v66\n" "v_add_f32 %[acc], %[acc], v67\n"
         "v_add_f32 %[acc], %[acc], v68\n" "v_add_f32 %[acc], %[acc], v69\n" "v_add_f32 %[acc], %[acc], v70\n" "v_add_f32 %[acc], %[acc], v71\n"
         "v_add_f32 %[acc], %[acc], v72\n" "v_add_f32 %[acc], %[acc], v73\n" "v_add_f32 %[acc], %[acc], v74\n" "v_add_f32 %[acc], %[acc], v75\n"
@@ -1201,41 +1210,38 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
         "v_add_f32 %[acc], %[acc], v88\n" "v_add_f32 %[acc], %[acc], v89\n" "v_add_f32 %[acc], %[acc], v90\n" "v_add_f32 %[acc], %[acc], v91\n"
         "v_add_f32 %[acc], %[acc], v92\n" "v_add_f32 %[acc], %[acc], v93\n" "v_add_f32 %[acc], %[acc], v94\n" "v_add_f32 %[acc], %[acc], v95\n"
         "s_waitcnt lgkmcnt(0)\n"
-        "s_add_u32 %[si1], %[i], 1\n"
-        "v_readfirstlane_b32 %[sf], %[vv]\n"
         "v_mov_b32 %[vv], %[si1]\n"
         "ds_write_b32 %[vc], %[vv]\n"
         "s_cmp_ge_u32 %[si1], %[nw]\n"
         "s_cbranch_scc1 3f\n"
         "s_cmp_eq_u32 %[ok], 0\n"
         "s_cbranch_scc1 4f\n"
-        "s_cmp_ge_i32 %[sf], %[si1]\n"
-        "s_cbranch_scc1 4f\n"
-        "s_mov_b32 %[sp], 0x400000\n"
-        "1:\n"
-        "ds_read_b32 %[vv], %[va]\n"
-        "s_waitcnt lgkmcnt(0)\n"
-        "v_readfirstlane_b32 %[sf], %[vv]\n"
-        "s_cmp_ge_i32 %[sf], %[si1]\n"
-        "s_cbranch_scc1 4f\n"
-        "s_sub_u32 %[sp], %[sp], 1\n"
-        "s_cmp_eq_u32 %[sp], 0\n"
-        "s_cbranch_scc0 1b\n"
-        "s_mov_b32 %[ok], 0\n"
+        "v_readfirstlane_b32 %[sf], %[vf]\n"
+        "s_cmp_lt_i32 %[sf], %[si1]\n"
+        "s_cbranch_scc1 8f\n"
         "4:\n"
         "s_lshl_b32 %[so], %[sn], 14\n"
-        "v_add_u32 v60, %[so], %[l0]\n"
-        "v_add_u32 v61, %[so], %[l1]\n"
-        "v_add_u32 v62, %[so], %[l2]\n"
-        "v_add_u32 v63, %[so], %[l3]\n"
-        "ds_read_b128 v[64:67], v60 offset:0\n"
-        "ds_read_b128 v[68:71], v61 offset:1024\n"
-        "ds_read_b128 v[72:75], v62 offset:2048\n"
-        "ds_read_b128 v[76:79], v63 offset:3072\n"
-        "ds_read_b128 v[80:83], v60 offset:4096\n"
-        "ds_read_b128 v[84:87], v61 offset:5120\n"
-        "ds_read_b128 v[88:91], v62 offset:6144\n"
-        "ds_read_b128 v[92:95], v63 offset:7168\n"
+        "v_add_u32 v56, %[so], %[l0]\n"
+        "v_add_u32 v57, %[so], %[l1]\n"
+        "v_add_u32 v58, %[so], %[l2]\n"
+        "v_add_u32 v59, %[so], %[l3]\n"
+        "ds_read_b128 v[64:67], v56 offset:0\n"
+        "ds_read_b128 v[68:71], v57 offset:1024\n"
+        "ds_read_b128 v[72:75], v58 offset:2048\n"
+        "ds_read_b128 v[76:79], v59 offset:3072\n"
+        "ds_read_b128 v[80:83], v56 offset:4096\n"
+        "ds_read_b128 v[84:87], v57 offset:5120\n"
+        "ds_read_b128 v[88:91], v58 offset:6144\n"
+        "ds_read_b128 v[92:95], v59 offset:7168\n"
+        "s_add_u32 %[so], %[si1], 1\n"
+        "s_cmp_ge_u32 %[so], %[nw]\n"
+        "s_cbranch_scc1 3f\n"
+        "s_add_u32 %[sf], %[sn], 1\n"
+        "s_cmp_eq_u32 %[sf], %[np]\n"
+        "s_cselect_b32 %[sf], 0, %[sf]\n"
+        "s_lshl_b32 %[sf], %[sf], 2\n"
+        "v_add_u32 %[va], %[sf], %[rb]\n"
+        "ds_read_b32 %[vf], %[va]\n"
         "3:\n"
         "v_add_f32 %[acc], %[acc], v96\n" "v_add_f32 %[acc], %[acc], v97\n" "v_add_f32 %[acc], %[acc], v98\n" "v_add_f32 %[acc], %[acc], v99\n"
         "v_add_f32 %[acc], %[acc], v100\n" "v_add_f32 %[acc], %[acc], v101\n" "v_add_f32 %[acc], %[acc], v102\n" "v_add_f32 %[acc], %[acc], v103\n"
@@ -1248,11 +1254,28 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
         "s_mov_b32 %[st], %[sn]\n"
         "s_mov_b32 %[i], %[si1]\n"
         "s_cmp_lt_u32 %[i], %[nw]\n"
-        "s_cbranch_scc1 5b\n"
+        "s_cbranch_scc1 6b\n"
+        "s_branch 9f\n"
+        "8:\n"
+        "s_lshl_b32 %[sf], %[sn], 2\n"
+        "v_add_u32 %[va], %[sf], %[rb]\n"
+        "s_mov_b32 %[sp], 0x400000\n"
+        "1:\n"
+        "ds_read_b32 %[vf], %[va]\n"
+        "s_waitcnt lgkmcnt(0)\n"
+        "v_readfirstlane_b32 %[sf], %[vf]\n"
+        "s_cmp_ge_i32 %[sf], %[si1]\n"
+        "s_cbranch_scc1 4b\n"
+        "s_sub_u32 %[sp], %[sp], 1\n"
+        "s_cmp_eq_u32 %[sp], 0\n"
+        "s_cbranch_scc0 1b\n"
+        "s_mov_b32 %[ok], 0\n"
+        "s_branch 4b\n"
+        "9:\n"
         "s_waitcnt lgkmcnt(0)\n"
                 : [acc] "+&v"(acc), [ok] "+&s"(oks), [i] "+&s"(i), [st] "+&s"(st), [so] "=&s"(so),
                   [sn] "=&s"(sn), [sf] "=&s"(sf), [si1] "=&s"(si1), [sp] "=&s"(sp), [va] "=&v"(va),
-                  [vv] "=&v"(vv)
+                  [vv] "=&v"(vv), [vf] "=&v"(vf)
                 : [nw] "s"(nwhole), [np] "s"(npu), [l0] "v"(l0), [l1] "v"(l1), [l2] "v"(l2),
                   [l3] "v"(l3), [rb] "v"(rb), [vc] "v"(vc)
                 : "v56", "v57", "v58", "v59", "v60", "v61", "v62", "v63",
