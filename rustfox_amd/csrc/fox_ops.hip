@@ -1343,6 +1343,10 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
     // for the DPP exchange)
     constexpr int RK = DPPX ? 1 : G;
     int cons_seen = 0;                       // consumed is known to be at least this
+    // the stage of the unit's tile, i mod np, kept as a running index (a
+    // division per unit is scalar work every wave of the compute unit
+    // shares one scalar unit for, the chain wave's included)
+    int st_i = li / NLD, st = st_i % np;
     for (int u0 = li; u0 < nunit; u0 += SV_VPF * SV_LOADERS) {
 #pragma unroll
         for (int m = 0; m < SV_VPF; m++) {
@@ -1362,7 +1366,7 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
                 if (!sv_wait_ge_idle(&consumed, i - np + 1)) return;
                 cons_seen = i - np + 1;
             }
-            const int st = i % np;
+            for (st += i - st_i, st_i = i; st >= np;) st -= np;
             float4 *P = ring + st * SV_QT * 64;
             float4 am = wq[0];
             if (DPPX) {
