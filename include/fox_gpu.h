@@ -320,6 +320,17 @@ fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t out_stride
                                  size_t n_head, size_t n_head_kv, size_t head_dim,
                                  size_t M, const uint32_t *pos, size_t n_ctx, int mode);
 
+/* Weights the kernels after the next attention will read (at most 8
+ * tensors, in the order they are used, up to max_bytes in all).  The next
+ * fox_gpu_attention call, if it is exact-mode for one token, reads them on
+ * the compute units its own workgroups leave idle while the softmax and
+ * value chains run, so that the following GEMVs find them in the infinity
+ * cache; any other call drops the request.  Results are unchanged.  The
+ * whole-token decode's cross-GEMV prefetch; the reference's analogue is its
+ * layer-ahead weight prefetch (src/forward.c:322-337, src/weights.c:718-774). */
+fox_gpu_status fox_gpu_attention_prefetch(fox_gpu_ctx *ctx, size_t n,
+                                          const fox_gpu_tensor *const *ts, size_t max_bytes);
+
 /* gate = silu(gate) * up (src/ops.c:41-48) and dst += src (src/ops.c:50-54)
  * on M rows of n. */
 fox_gpu_status fox_gpu_silu_mul(fox_gpu_ctx *ctx, float *gate, const float *up,

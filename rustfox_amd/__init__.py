@@ -85,6 +85,7 @@ def gpu_lib() -> C.CDLL:
         "fox_gpu_rope_store": [vp, vp, sz, vp, sz, vp, sz, sz, sz, sz, sz, vp, vp, vp, sz,
                                vp, vp],
         "fox_gpu_attention": [vp, vp, sz, vp, sz, vp, vp, sz, sz, sz, sz, vp, sz, C.c_int],
+        "fox_gpu_attention_prefetch": [vp, sz, C.POINTER(vp), sz],
         "fox_gpu_kv_write": [vp, vp, vp, sz, sz, sz, sz, vp, vp],
         "fox_gpu_gemv_rmsnorm": [vp, sz, C.POINTER(vp), vp, sz, sz, vp, C.c_float,
                                  C.POINTER(vp), C.POINTER(sz), C.c_uint],
@@ -336,6 +337,12 @@ class Gpu:
         _check(self.lib.fox_gpu_attention(self.ctx, out.ptr, out_stride or w, q.ptr,
                                           q_stride or w, kc.ptr, vc.ptr, n_head, n_head_kv,
                                           head_dim, M, pos.ptr, n_ctx, mode))
+
+    def attention_prefetch(self, ts, max_bytes):
+        """Weights the next one-token exact attention reads ahead
+        (fox_gpu_attention_prefetch)."""
+        hs = (C.c_void_p * max(len(ts), 1))(*[t.h for t in ts])
+        _check(self.lib.fox_gpu_attention_prefetch(self.ctx, len(ts), hs, max_bytes))
 
     def event(self):
         e = C.c_void_p()

@@ -70,6 +70,11 @@ struct fox_gpu_ctx {
     uint8_t *small;
     // this device's copy of the fixed scratch of fox_gpu_gemv_noalloc
     uint8_t *scratch;
+    // weights the next one-token exact attention reads ahead
+    // (fox_gpu_attention_prefetch; cleared by every fox_gpu_attention)
+    const void *pf_p[8];
+    size_t pf_bytes[8];
+    int pf_n;
 };
 #define FOX_SMALL_BYTES (64 * 1024)
 

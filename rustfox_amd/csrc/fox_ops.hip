@@ -789,6 +789,45 @@ __global__ __launch_bounds__(64) void attn_values_x(const float *__restrict__ at
 #define SV_SPIN (1 << 22)
 #define SV_IDLE_SLEEP 2             // s_sleep units (64 clocks each) between idle polls
 
+// Weight prefetch riding on the attention launch (one token): the kernel's
+// own workgroups occupy n_head_kv x slices compute units for the length of
+// the two position-order chains, during which HBM is nearly idle.  nwg more
+// workgroups, on compute units the attention leaves free (the kernel's LDS
+// keeps one workgroup per compute unit), read the weights the next kernels
+// will read, in order, so that those kernels find them in the infinity
+// cache.  The values read are folded into a register that an empty asm
+// statement consumes: nothing is written, and results cannot change.
+#define SV_PF_REGIONS 8
+#define SV_PF_LOADS 2                // 16-byte loads in flight per thread
+#define SV_PF_WG_MAX 128
+struct SvPrefetch {
+    const uint4 *p[SV_PF_REGIONS];
+    size_t n16[SV_PF_REGIONS];       // 16-byte words of each region
+    int nreg, nwg;
+    int first;                       // blockIdx.x of the first prefetching workgroup
+};
+
+__device__ __forceinline__ void sv_prefetch_reads(const SvPrefetch &pf, int w)
+{
+    constexpr int T = SV_WAVES * 64, U = SV_PF_LOADS;
+    uint32_t acc = 0;
+    for (int r = 0; r < pf.nreg; r++) {
+        const uint4 *__restrict__ p = pf.p[r];
+        const size_t n = pf.n16[r], step = (size_t)pf.nwg * T * U;
+        for (size_t c = (size_t)w * T * U + threadIdx.x; c < n; c += step) {
+            uint4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const size_t i = c + (size_t)u * T;
+                v[u] = p[i < n ? i : n - 1];
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+        }
+    }
+    asm volatile("" ::"v"(acc));
+}
+
 // v of lane (quad base + sel) for each lane, sel from a quad_perm control
 // word known at compile time (DPP, no LDS traffic)
 __device__ __forceinline__ float dpp_bcast(float v, int ctl)
@@ -989,8 +1028,14 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
     const float *__restrict__ att, size_t att_stride, const float *__restrict__ tmax, int n_tiles,
     const float *__restrict__ vc, int n_head, int n_head_kv, int hd,
     const uint32_t *__restrict__ pos, int n_ctx, float *__restrict__ out, size_t out_stride,
-    int np)
+    int np, SvPrefetch pf)
 {
+    // the last pf.nwg workgroups of row 0 prefetch (the host adds them for
+    // one token only); they use neither LDS nor barriers
+    if (pf.nwg > 0 && (int)blockIdx.x >= pf.first) {
+        if (blockIdx.y == 0) sv_prefetch_reads(pf, (int)blockIdx.x - pf.first);
+        return;
+    }
     constexpr int DS = 64 / G;               // columns per slice
     constexpr int NLD = SV_QT / G;           // product units per tile (G quads each)
     extern __shared__ float4 sv_lds[];
@@ -1406,12 +1451,44 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
     }
 }
 
+extern "C" fox_gpu_status fox_gpu_attention_prefetch(fox_gpu_ctx *ctx, size_t n,
+                                                     const fox_gpu_tensor *const *ts,
+                                                     size_t max_bytes)
+{
+    if (!ctx) return fox_fail(FOX_GPU_ERR_ARG, "attention_prefetch: null context");
+    ctx->pf_n = 0;
+    if (n > SV_PF_REGIONS || (n && !ts))
+        return fox_fail(FOX_GPU_ERR_ARG, "attention_prefetch: at most %d tensors", SV_PF_REGIONS);
+    size_t left = max_bytes;
+    for (size_t i = 0; i < n; i++) {
+        if (!ts[i] || !ts[i]->d) return fox_fail(FOX_GPU_ERR_ARG, "attention_prefetch: null tensor");
+        if ((uintptr_t)ts[i]->d % 16) continue;
+        const size_t b = (ts[i]->dev_bytes < left ? ts[i]->dev_bytes : left) & ~(size_t)15;
+        if (b == 0) break;
+        ctx->pf_p[ctx->pf_n] = ts[i]->d;
+        ctx->pf_bytes[ctx->pf_n] = b;
+        ctx->pf_n++;
+        left -= b;
+    }
+    return FOX_GPU_OK;
+}
+
 extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t out_stride,
                                             const float *q, size_t q_stride, const float *k_cache,
                                             const float *v_cache, size_t n_head, size_t n_head_kv,
                                             size_t head_dim, size_t M, const uint32_t *pos,
                                             size_t n_ctx, int mode)
 {
+    // the pending prefetch belongs to this call, whichever path it takes
+    SvPrefetch pf = {};
+    if (ctx) {
+        pf.nreg = ctx->pf_n;
+        for (int i = 0; i < pf.nreg; i++) {
+            pf.p[i] = (const uint4 *)ctx->pf_p[i];
+            pf.n16[i] = ctx->pf_bytes[i] / 16;
+        }
+        ctx->pf_n = 0;
+    }
     if (!ctx || !out || !q || !k_cache || !v_cache || !pos || n_head == 0 || n_head_kv == 0 ||
         head_dim == 0 || M == 0 || n_ctx == 0)
         return fox_fail(FOX_GPU_ERR_ARG, "attention: bad argument");
@@ -1487,11 +1564,19 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
             if (e != hipSuccess) return fox_hip_fail(e, "attention: LDS size");
             const int sv_ds = (int)(64 / gqa);
             const unsigned nsl = (unsigned)((head_dim + sv_ds - 1) / sv_ds);
+            // prefetching workgroups: one token only, on the compute units
+            // the attention leaves free (with more than half of a compute
+            // unit's 160 KB of LDS, a workgroup has its compute unit alone)
+            const int n_attn = (int)(n_head_kv * nsl);
+            pf.first = n_attn;
+            pf.nwg = 0;
+            if (M == 1 && pf.nreg > 0 && sv_lds > 80 * 1024 && ctx->n_cu > n_attn)
+                pf.nwg = ctx->n_cu - n_attn < SV_PF_WG_MAX ? ctx->n_cu - n_attn : SV_PF_WG_MAX;
             void *args[] = {(void *)&att, (void *)&att_stride, (void *)&tmax, (void *)&n_tiles,
                             (void *)&v_cache, (void *)&ih, (void *)&ikv, (void *)&ihd,
                             (void *)&pos, (void *)&ictx, (void *)&out, (void *)&os,
-                            (void *)&np};
-            e = hipLaunchKernel(sv, dim3((unsigned)n_head_kv * nsl, (unsigned)M),
+                            (void *)&np, (void *)&pf};
+            e = hipLaunchKernel(sv, dim3((unsigned)(n_attn + pf.nwg), (unsigned)M),
                                 dim3(SV_WAVES * 64), args, sv_lds, ctx->stream);
             if (e != hipSuccess) return fox_hip_fail(e, "attention softmax+values");
             FOX_LAUNCHED("attention softmax+values");

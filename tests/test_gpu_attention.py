@@ -35,7 +35,7 @@ def reference_attention(oracle, q, K, V, n_head, n_kv, hd, pos, M, n_ctx):
     return out
 
 
-def run_gpu(gpu, q, K, V, n_head, n_kv, hd, pos, M, n_ctx, mode):
+def run_gpu(gpu, q, K, V, n_head, n_kv, hd, pos, M, n_ctx, mode, before=None):
     kvd = n_kv * hd
     kc = gpu.empty(n_ctx * kvd, np.float32)
     vc = gpu.empty((n_ctx + 3) // 4 * 4 * kvd, np.float32)
@@ -45,6 +45,8 @@ def run_gpu(gpu, q, K, V, n_head, n_kv, hd, pos, M, n_ctx, mode):
     dq = gpu.array(q)
     dpos = gpu.array(np.array([pos], np.uint32))
     out = gpu.empty(M * n_head * hd, np.float32)
+    if before:
+        before()
     gpu.attention(out, dq, kc, vc, n_head, n_kv, hd, M, dpos, n_ctx, mode)
     gpu.sync()
     return out.numpy().reshape(M, n_head * hd)
@@ -103,3 +105,44 @@ def test_nan_first_score_follows_the_reference(gpu, oracle):
     want = reference_attention(oracle, q, K, V, n_head, n_kv, hd, pos, M, n_ctx)
     assert np.isnan(want[0, :2 * hd]).all() and np.isnan(got[0, :2 * hd]).all()
     assert np.array_equal(got[0, 2 * hd:].view(np.uint32), want[0, 2 * hd:].view(np.uint32))
+
+
+@pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[5]],
+                         ids=lambda c: "h%d_kv%d_d%d_ctx%d_p%d_m%d" % c)
+def test_weight_prefetch_changes_nothing(gpu, oracle, case):
+    """fox_gpu_attention_prefetch: the next one-token exact attention reads
+    the given weights on idle compute units (a byte cap that ends inside the
+    second tensor, three tensors of which the last is never reached); for
+    several tokens the request is dropped.  The attention stays bit-identical
+    to the reference, the weights are unchanged, and a request is used once:
+    the call after it runs without one."""
+    from rustfox_amd import synth
+    n_head, n_kv, hd, n_ctx, pos, M = case
+    rng = np.random.default_rng(11 + sum(case))
+    q = (rng.standard_normal((M, n_head * hd)) * 0.3).astype(np.float32)
+    K = rng.standard_normal((n_ctx, n_kv * hd)).astype(np.float32)
+    V = rng.standard_normal((n_ctx, n_kv * hd)).astype(np.float32)
+    blobs = [synth.tq1_random(rng, r * 2560 // 256).reshape(-1) for r in (2560, 9728, 16)]
+    ts = [gpu.tensor(rf.TQ1_0, 2560, r, b) for r, b in zip((2560, 9728, 16), blobs)]
+    cap = ts[0].info()["device_bytes"] + 3 * 1000 * 1000 + 8
+    want = reference_attention(oracle, q, K, V, n_head, n_kv, hd, pos, M, n_ctx)
+    for before in (lambda: gpu.attention_prefetch(ts, cap), None):
+        got = run_gpu(gpu, q, K, V, n_head, n_kv, hd, pos, M, n_ctx, rf.ATTN_EXACT, before)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
+            f"max abs diff {np.abs(got - want).max()}"
+    for t, b in zip(ts, blobs):
+        assert np.array_equal(t.download(), b)
+        t.free()
+
+
+def test_weight_prefetch_arguments(gpu):
+    """More than eight tensors is an argument error; an empty request and a
+    zero byte cap are accepted (nothing is read)."""
+    from rustfox_amd import synth
+    rng = np.random.default_rng(3)
+    t = gpu.tensor(rf.TQ1_0, 256, 16, synth.tq1_random(rng, 16).reshape(-1))
+    with pytest.raises(rf.FoxError):
+        gpu.attention_prefetch([t] * 9, 1 << 20)
+    gpu.attention_prefetch([], 1 << 20)
+    gpu.attention_prefetch([t] * 8, 0)
+    t.free()
