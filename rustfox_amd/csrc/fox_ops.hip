@@ -519,6 +519,34 @@ __device__ __forceinline__ void copy_to_lds16(const void *src, void *dst)
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
 }
 
+// the products of one chunk (SC_CQ quads) added to acc in dimension order:
+// every read of the chunk is issued before the first add (with FULL the
+// chunk is known to be whole, and no per-quad branch splits the reads from
+// the adds)
+template <bool FULL>
+__device__ __forceinline__ float sc_chunk(float acc, const float4 *qr, const float4 *kr, int sw,
+                                          int c, int nv)
+{
+    float4 qv[SC_CQ], kv[SC_CQ];
+#pragma unroll
+    for (int j = 0; j < SC_CQ; j++) {
+        if (FULL || SC_CQ * c + j < nv) {
+            qv[j] = qr[j];
+            kv[j] = kr[j ^ sw];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < SC_CQ; j++) {
+        if (FULL || SC_CQ * c + j < nv) {
+            acc = acc + qv[j].x * kv[j].x;
+            acc = acc + qv[j].y * kv[j].y;
+            acc = acc + qv[j].z * kv[j].z;
+            acc = acc + qv[j].w * kv[j].w;
+        }
+    }
+    return acc;
+}
+
 // One workgroup per (64-position tile, kv head, token); wave w takes query
 // heads w, w + 4, ... of the kv head, one lane per position.  The tile's K
 // rows arrive in NCH chunks of 32 dimensions, copied straight into LDS: every
@@ -584,6 +612,7 @@ __global__ __launch_bounds__(256) void attn_scores_x(const float *__restrict__ q
     }
     const bool ok = lane < pn;
     const int row = ok ? lane : 0, sw = (row >> 1) & 7;
+    const bool full = nv == NCH * SC_CQ;            // (uniform) every chunk whole
     constexpr int HW = ATT_MAXG / 4;                // heads per wave at most
     float a[HW];
 #pragma unroll
@@ -602,19 +631,8 @@ __global__ __launch_bounds__(256) void attn_scores_x(const float *__restrict__ q
             const int g = wave + 4 * h;
             if (g < gqa) {
                 const float4 *qr = qq + g * nv + SC_CQ * c;
-                float acc = a[h];
-#pragma unroll
-                for (int j = 0; j < SC_CQ; j++) {
-                    if (SC_CQ * c + j < nv) {
-                        const float4 qv = qr[j];
-                        const float4 kv = kr[j ^ sw];
-                        acc = acc + qv.x * kv.x;
-                        acc = acc + qv.y * kv.y;
-                        acc = acc + qv.z * kv.z;
-                        acc = acc + qv.w * kv.w;
-                    }
-                }
-                a[h] = acc;
+                a[h] = full ? sc_chunk<true>(a[h], qr, kr, sw, c, nv)
+                            : sc_chunk<false>(a[h], qr, kr, sw, c, nv);
             }
         }
     }
