@@ -33,6 +33,7 @@ pick.  Inputs are resident in HBM before the timed region starts.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import csv
 import glob
 import json
@@ -261,7 +262,9 @@ def read_probe():
     workgroups reading contiguous chunks) with 1 to 16 16-byte loads in flight
     per thread and 1024 to 8192 workgroups of 256 threads, beside a device
     copy of the same size; mean of 10 timed
-    launches after 2 untimed ones, HIP events on the launching stream.  One
+    launches after 2 untimed ones, HIP events on the launching stream.  Then
+    single launches reading 3 to 64 MB (a decode kernel's share), and the
+    cost of an empty kernel launched back to back and as a graph node.  One
     JSON line per case on stdout."""
     gpu = rf.Gpu(0)
     src = gpu.empty(READ_PROBE_BYTES, np.uint8)
@@ -289,6 +292,51 @@ def read_probe():
                       "gbs_read": round(READ_PROBE_BYTES / ms / 1e6, 1),
                       "gbs_read_plus_write": round(2 * READ_PROBE_BYTES / ms / 1e6, 1)}),
           flush=True)
+    # one launch at the sizes of a decode step's kernels (2 loads in flight,
+    # 1024 workgroups): a new region of the buffer each launch (cold), or
+    # the same region every time (warm: the infinity cache and L2 hold it)
+    for n in (3 << 20, 15138816 // 4096 * 4096, 27 << 20, 64 << 20):
+        nreg = READ_PROBE_BYTES // n
+        for mode in ("cold", "warm"):
+            offs = [(i % nreg) * n if mode == "cold" else 0 for i in range(64)]
+            run = lambda o: rf._check(gpu.lib.fox_gpu_read_probe(gpu.ctx, src.ptr + o, n, 2,
+                                                                  1024, sink.ptr))
+            for o in offs[:4]:
+                run(o)
+            gpu.record(e0)
+            for o in offs:
+                run(o)
+            gpu.record(e1)
+            us = gpu.elapsed_ms(e0, e1) * 1e3 / len(offs)
+            print(json.dumps({"probe": "read_one_launch", "bytes": n, "mode": mode,
+                              "us": round(us, 2), "gbs": round(n / us / 1e3, 1)}), flush=True)
+    # the fixed cost of a kernel: empty launches back to back on the stream,
+    # and as the nodes of one captured graph (the decode replays one graph
+    # per token)
+    for grid in (1, 256, 1024):
+        for _ in range(50):
+            gpu.empty_probe(grid, sink)
+        gpu.record(e0)
+        for _ in range(2000):
+            gpu.empty_probe(grid, sink)
+        gpu.record(e1)
+        us_stream = gpu.elapsed_ms(e0, e1) * 1e3 / 2000
+        rf._check(gpu.lib.fox_gpu_graph_begin(gpu.ctx))
+        for _ in range(100):
+            gpu.empty_probe(grid, sink)
+        g = ctypes.c_void_p()
+        rf._check(gpu.lib.fox_gpu_graph_end(gpu.ctx, ctypes.byref(g)))
+        for _ in range(3):
+            rf._check(gpu.lib.fox_gpu_graph_launch(gpu.ctx, g))
+        gpu.record(e0)
+        for _ in range(20):
+            rf._check(gpu.lib.fox_gpu_graph_launch(gpu.ctx, g))
+        gpu.record(e1)
+        us_node = gpu.elapsed_ms(e0, e1) * 1e3 / 2000
+        gpu.lib.fox_gpu_graph_free(g)
+        print(json.dumps({"probe": "empty_kernel", "workgroups": grid,
+                          "us_per_stream_launch": round(us_stream, 2),
+                          "us_per_graph_node": round(us_node, 2)}), flush=True)
     gpu.close()
 
 
@@ -480,8 +528,10 @@ def main():
                     help="only the roofline GEMV case and a 256 MB device copy (the runs "
                          "that rocprofv3 --pmc counts for the traffic figure)")
     ap.add_argument("--read-probe", action="store_true",
-                    help="only the HBM read-ceiling probe (1 GiB streaming reads with 1-16 "
-                         "loads in flight per thread, and a device copy), one JSON line per case")
+                    help="only the HBM read-ceiling probes (1 GiB streaming reads with 1-16 "
+                         "loads in flight per thread, a device copy, single launches at "
+                         "decode-step sizes, the cost of an empty launch and graph node), "
+                         "one JSON line per case")
     a = ap.parse_args()
 
     if a.gpus != 1:

@@ -97,6 +97,12 @@ fox_gpu_status fox_gpu_sync(fox_gpu_ctx *ctx);
 fox_gpu_status fox_gpu_read_probe(fox_gpu_ctx *ctx, const void *src, size_t n, int loads,
                                   int grid, uint32_t *sink);
 
+/* Diagnostic, no counterpart in RustFox: one empty kernel of `grid`
+ * workgroups on the stream (sink, device memory, is never written).  Timed
+ * back to back, or captured in a graph, it gives the fixed cost of a launch
+ * or of a graph node, which every kernel of a decode step pays. */
+fox_gpu_status fox_gpu_empty_probe(fox_gpu_ctx *ctx, int grid, uint32_t *sink);
+
 /* ------------------------------------------------------------ weights */
 
 /* Upload one GGUF tensor (`bytes` = its GGUF size, host pointer) into HBM.

@@ -61,6 +61,7 @@ def gpu_lib() -> C.CDLL:
         "fox_gpu_memcpy_d2h": [vp, vp, vp, sz],
         "fox_gpu_memcpy_d2d": [vp, vp, vp, sz],
         "fox_gpu_read_probe": [vp, vp, sz, C.c_int, C.c_int, vp],
+        "fox_gpu_empty_probe": [vp, C.c_int, vp],
         "fox_gpu_memset": [vp, vp, C.c_int, sz],
         "fox_gpu_sync": [vp],
         "fox_gpu_tensor_upload": [vp, C.c_int, C.c_uint64, C.c_uint64, vp, C.c_uint64,
@@ -255,6 +256,10 @@ class Gpu:
         """Streaming read of nbytes with `loads` 16-byte loads in flight per
         thread (fox_gpu_read_probe; a diagnostic of the HBM read ceiling)."""
         _check(self.lib.fox_gpu_read_probe(self.ctx, src.ptr, nbytes, loads, grid, sink.ptr))
+
+    def empty_probe(self, grid: int, sink: DeviceArray):
+        """One empty kernel of `grid` workgroups (fox_gpu_empty_probe)."""
+        _check(self.lib.fox_gpu_empty_probe(self.ctx, grid, sink.ptr))
 
     # -- compute (device arrays in, device arrays out)
     def quantize(self, mode, x: DeviceArray, K, M, x_stride, q: DeviceArray, scale: DeviceArray):

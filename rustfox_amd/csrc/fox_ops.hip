@@ -1822,6 +1822,23 @@ __global__ __launch_bounds__(256) void read_probe_k(const uint4 *__restrict__ sr
     if (acc == 0x9e3779b9u) sink[0] = acc;
 }
 
+// An empty kernel: what one launch costs on the stream, or one node of a
+// graph, before any work (the store never happens: no workgroup has that
+// many threads).
+__global__ __launch_bounds__(256) void empty_probe_k(uint32_t *sink)
+{
+    if (threadIdx.x == 1u << 20) sink[0] = 1;
+}
+
+extern "C" fox_gpu_status fox_gpu_empty_probe(fox_gpu_ctx *ctx, int grid, uint32_t *sink)
+{
+    if (!ctx || !sink || grid <= 0 || grid > (1 << 20))
+        return fox_fail(FOX_GPU_ERR_ARG, "empty_probe: bad argument");
+    hipLaunchKernelGGL(empty_probe_k, dim3((unsigned)grid), dim3(256), 0, ctx->stream, sink);
+    FOX_LAUNCHED("empty_probe");
+    return FOX_GPU_OK;
+}
+
 extern "C" fox_gpu_status fox_gpu_read_probe(fox_gpu_ctx *ctx, const void *src, size_t n,
                                              int loads, int grid, uint32_t *sink)
 {
