@@ -62,6 +62,12 @@ CASES = [  # n_head, n_kv, hd, n_ctx, pos, M
     (12, 4, 64, 100, 99, 1),       # gqa 3: the three-kernel path
     (8, 2, 64, 6000, 5990, 2),     # weights leave room for few product stages (4)
     (8, 2, 64, 9000, 8990, 2),     # weights beyond the fused kernel's LDS: three-kernel path
+    # one token, scores in the same launch: several rounds of score tiles per
+    # workgroup, partial chunks, workgroups without tiles
+    (8, 8, 128, 1200, 1150, 1),    # gqa 1: two slices, 9 tiles each (3 rounds)
+    (4, 1, 64, 3000, 2999, 1),     # gqa 4, hd 64: 12 tiles per slice
+    (16, 2, 256, 500, 499, 1),     # gqa 8, hd 256: 32 slices for 8 tiles, two tiles a round
+    (6, 6, 48, 400, 399, 1),       # hd 48: the second chunk partly filled
 ]
 
 
