@@ -63,6 +63,7 @@ struct FusedArgs {
     const uint32_t *pos;
     int head_dim, kv_dim, n_ctx;
     int role0;                  // ROPE: the role (0 q, 1 k, 2 v) of segment 0
+    int q6_mask;                // FMT_KQMIX: bit s set when segment s is Q6_K (else Q4_K)
     float *k_cache, *v_cache;
 };
 
@@ -453,22 +454,33 @@ __device__ __forceinline__ void quantise_kq(const FusedArgs &a, int K, int8_t *x
     for (int r = 0; r < R4MAX; r++) part[r] += dpp_t<0xB1, 0xF>(0, part[r]);
 #pragma unroll
     for (int r = 0; r < R4MAX; r++) part[r] += dpp_t<0x4E, 0xF>(0, part[r]);
-    if (FMT == FMT_Q4K) {
+    // (both formats: the sixteen-element sums first, at aux + 8 nb, then
+    // their pairs)
+    constexpr bool S16 = FMT == FMT_Q6K || FMT == FMT_KQMIX;
+    constexpr bool S32 = FMT == FMT_Q4K || FMT == FMT_KQMIX;
+    if constexpr (S16) {
+        int32_t *a16 = aux + (FMT == FMT_KQMIX ? 8 * nb : 0);
+#pragma unroll
+        for (int r = 0; r < R4MAX; r++) {
+            const int b = wave + FW * r;
+            if (b >= nb) break;                                 // (uniform)
+            if ((lane & 3) == 0) {
+                // lane l holds elements 4l ..: half h = l >> 5, group g =
+                // (l >> 3) & 3, sixteen s = (l >> 2) & 1; stored at
+                // [block][quarter 2h + s][group g]
+                const int h = lane >> 5, g = (lane >> 3) & 3, s = (lane >> 2) & 1;
+                a16[b * 16 + (2 * h + s) * 4 + g] = part[r];
+            }
+        }
+    }
+    if constexpr (S32) {
 #pragma unroll
         for (int r = 0; r < R4MAX; r++) part[r] += dpp_t<0x141, 0xF>(0, part[r]);
-    }
 #pragma unroll
-    for (int r = 0; r < R4MAX; r++) {
-        const int b = wave + FW * r;
-        if (b >= nb) break;                                     // (uniform)
-        if (FMT == FMT_Q4K) {
+        for (int r = 0; r < R4MAX; r++) {
+            const int b = wave + FW * r;
+            if (b >= nb) break;                                 // (uniform)
             if ((lane & 7) == 0) aux[b * 8 + (lane >> 3)] = part[r];
-        } else if ((lane & 3) == 0) {
-            // lane l holds elements 4l ..: half h = l >> 5, group g =
-            // (l >> 3) & 3, sixteen s = (l >> 2) & 1; stored at
-            // [block][quarter 2h + s][group g]
-            const int h = lane >> 5, g = (lane >> 3) & 3, s = (lane >> 2) & 1;
-            aux[b * 16 + (2 * h + s) * 4 + g] = part[r];
         }
     }
     __syncthreads();
@@ -502,6 +514,45 @@ struct RawBlk<FMT_Q6K> {
     uint32_t d;
 };
 
+// either K-quant's lane bytes (FMT_KQMIX: the format is the segment's):
+// Q6_K's l0, l1, h, sc, d as a, b, c, sc, d; Q4_K's q0 .. q3 in a and b and
+// its hd in c
+template <>
+struct RawBlk<FMT_KQMIX> {
+    uint4 a, b, c;
+    uint2 sc;
+    uint32_t d;
+};
+
+__device__ __forceinline__ RawBlk<FMT_Q4K> q4k_view(const RawBlk<FMT_KQMIX> &m)
+{
+    RawBlk<FMT_Q4K> r;
+    r.q0 = make_uint2(m.a.x, m.a.y);
+    r.q1 = make_uint2(m.a.z, m.a.w);
+    r.q2 = make_uint2(m.b.x, m.b.y);
+    r.q3 = make_uint2(m.b.z, m.b.w);
+    r.hd = m.c;
+    return r;
+}
+
+__device__ __forceinline__ RawBlk<FMT_Q6K> q6k_view(const RawBlk<FMT_KQMIX> &m)
+{
+    RawBlk<FMT_Q6K> r;
+    r.l0 = m.a;
+    r.l1 = m.b;
+    r.h = m.c;
+    r.sc = m.sc;
+    r.d = m.d;
+    return r;
+}
+
+template <int FMT>
+__device__ __forceinline__ RawBlk<FMT> load_raw(const uint8_t *__restrict__ ch, int lane);
+
+// a chunk of either K-quant (q6: the segment is Q6_K)
+__device__ __forceinline__ RawBlk<FMT_KQMIX> load_raw_mix(const uint8_t *__restrict__ ch,
+                                                         int lane, bool q6);
+
 template <int FMT>
 __device__ __forceinline__ RawBlk<FMT> load_raw(const uint8_t *__restrict__ ch, int lane)
 {
@@ -532,6 +583,28 @@ __device__ __forceinline__ RawBlk<FMT> load_raw(const uint8_t *__restrict__ ch, 
         r.d = *(const unsigned short *)(ch + 3328 + 2 * row);
     }
     return r;
+}
+
+__device__ __forceinline__ RawBlk<FMT_KQMIX> load_raw_mix(const uint8_t *__restrict__ ch,
+                                                         int lane, bool q6)
+{
+    RawBlk<FMT_KQMIX> m;
+    if (q6) {                                                   // (uniform)
+        const RawBlk<FMT_Q6K> r = load_raw<FMT_Q6K>(ch, lane);
+        m.a = r.l0;
+        m.b = r.l1;
+        m.c = r.h;
+        m.sc = r.sc;
+        m.d = r.d;
+    } else {
+        const RawBlk<FMT_Q4K> r = load_raw<FMT_Q4K>(ch, lane);
+        m.a = make_uint4(r.q0.x, r.q0.y, r.q1.x, r.q1.y);
+        m.b = make_uint4(r.q2.x, r.q2.y, r.q3.x, r.q3.y);
+        m.c = r.hd;
+        m.sc = make_uint2(0u, 0u);
+        m.d = 0u;
+    }
+    return m;
 }
 
 // Q4_K terms of sub-blocks 2p and 2p + 1 of one block and row
@@ -686,6 +759,13 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
 
     constexpr bool KQ = FMT != FMT_TQ2;                    // a K-quant (one token)
     constexpr int CHUNK = FMT == FMT_TQ2 ? TQ2_CHUNK : FMT == FMT_Q4K ? Q4K_CHUNK : Q6K_CHUNK;
+    // the K-quant of segment sg (FMT_KQMIX: per segment) and its chunk bytes
+    auto seg_q6 = [&](int sg) -> bool {
+        return FMT == FMT_Q6K || (FMT == FMT_KQMIX && ((a.q6_mask >> sg) & 1));
+    };
+    auto chunk_of = [&](int sg) -> int {
+        return FMT == FMT_KQMIX ? (seg_q6(sg) ? Q6K_CHUNK : Q4K_CHUNK) : CHUNK;
+    };
     constexpr int T = terms_per_block(FMT);
     // (the wave index as a wave-uniform value: everything per wave below,
     // the units, items and weight addresses, is then scalar work)
@@ -704,6 +784,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     float *terms = (float *)(lds + L.terms);
     float *ybuf = (float *)(lds + L.y);
     const int nbp = fused_ntp(FMT, nb);
+    const int nbp6 = FMT == FMT_KQMIX ? fused_ntp(FMT_Q6K, nb) : nbp;   // (Q6_K segments' rows)
     const int tstride = nslab * 16 * M * nbp;              // floats per terms buffer
 
     // ---- work: items bx, bx + gridDim.x, ... (a 16-row tile of one segment,
@@ -738,11 +819,19 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     const int total = nu * ntl;
     // unit r (of nu) of item ti: block u = wave + FW r of the item's units
     // (clamped to the item's last one: a wave without units reads that)
-    auto unit_ptr = [&](int ti, int r) -> const uint8_t * {
+    // The wave's weight cursor: unit r of item ti, its chunk, the chunk's
+    // bytes and (FMT_KQMIX) whether its segment is Q6_K.
+    struct Cur {
+        int ti, r;
+        const uint8_t *p;
+        int ch, q6;
+    };
+    auto unit_cur = [&](int ti, int r) -> Cur {
         const int u = min(wave + FW * r, nunits - 1), sl = u >= nb, b = u - sl * nb;
         int sg, tl;
         item(ti, sl, sg, tl);
-        return pick4(a.w, sg) + ((size_t)tl * nb + b) * CHUNK;
+        const int ch = chunk_of(sg);
+        return Cur{ti, r, pick4(a.w, sg) + ((size_t)tl * nb + b) * ch, ch, (int)seg_q6(sg)};
     };
     // (item, unit) counters stepped one unit at a time (no divisions, no
     // branches)
@@ -751,37 +840,36 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
         r = wrap ? 0 : r + 1;
         ti += wrap;
     };
-    // The wave's weight cursor: unit r of item ti and its chunk.  The next
-    // unit of the same item and slab is FW chunks on; only a new item, or
-    // the step from the gate blocks to the up blocks, recomputes the
-    // address (the computation is scalar work every wave of the compute
+    // The next unit of the same item and slab is FW chunks on; only a new
+    // item, or the step from the gate blocks to the up blocks, recomputes
+    // the address (the computation is scalar work every wave of the compute
     // unit shares one scalar unit for).  Called only when a next unit
     // exists.
-    struct Cur {
-        int ti, r;
-        const uint8_t *p;
-    };
     auto cur_next = [&](Cur c) -> Cur {
         const int u = wave + FW * c.r;
         if (c.r + 1 == nu || (EPI == EPI_SILU && u < nb && u + FW >= nb)) {   // (uniform)
             int ti = c.ti, r = c.r;
             step(ti, r);
-            return Cur{ti, r, unit_ptr(ti, r)};
+            return unit_cur(ti, r);
         }
-        return Cur{c.ti, c.r + 1, c.p + FW * CHUNK};
+        return Cur{c.ti, c.r + 1, c.p + FW * (FMT == FMT_KQMIX ? c.ch : CHUNK), c.ch, c.q6};
+    };
+    auto load_unit = [&](const Cur &c) -> RawBlk<FMT> {
+        if constexpr (FMT == FMT_KQMIX) return load_raw_mix(c.p, lane, c.q6 != 0);
+        else return load_raw<FMT>(c.p, lane);
     };
 
     // ---- loads in the order they are used (they complete in order): the
     // input of token 0 (above), the first weight blocks, the epilogue's
     // operands
-    constexpr int PF = KQ ? 4 : pf_of(R4, EPI == EPI_SILU ? 2 : 1);
+    constexpr int PF = FMT == FMT_KQMIX ? 3 : KQ ? 4 : pf_of(R4, EPI == EPI_SILU ? 2 : 1);
     // (every wave issues PF block loads, past its last unit re-reading that
     // one, so that the input's first use waits for the input only)
     RawBlk<FMT> raw[PF];
-    Cur fc{0, 0, unit_ptr(0, 0)};                          // unit k (then PF) of the wave
+    Cur fc = unit_cur(0, 0);                               // unit k (then PF) of the wave
 #pragma unroll
     for (int k = 0; k < PF; k++) {
-        raw[k] = load_raw<FMT>(fc.p, lane);
+        raw[k] = load_unit(fc);
         if (k + 1 < total) fc = cur_next(fc);              // past the last unit: reload it
     }
 
@@ -866,9 +954,10 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
             // scheduling barriers keep that order), so that the reads
             // overlap the adds; with up to four chunks all reads go out at
             // once.
+            const int nbpi = FMT == FMT_KQMIX && seg_q6(sg) ? nbp6 : nbp;
             const float4 *tq = (const float4 *)(terms + (ti & 1) * tstride +
-                                                ((csl * 16 + crow) * M + ct) * nbp);
-            const int nq = nbp >> 2, last = nq - 1;
+                                                ((csl * 16 + crow) * M + ct) * nbpi);
+            const int nq = nbpi >> 2, last = nq - 1;
             float acc = 0.0f;
             auto add4 = [&](const float4 &v) {
                 acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
@@ -955,17 +1044,30 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
                 // lane (row j, part g): T / 4 terms of its row
                 const RawBlk<FMT> rk = raw[k];
                 if (n + PF < total) {
-                    raw[k] = load_raw<FMT>(fc.p, lane);
+                    raw[k] = load_unit(fc);
                     if (n + PF + 1 < total) fc = cur_next(fc);
                 }
                 const int8_t *xb = (const int8_t *)B + b * 256;
                 const float as = bsc[b];
-                float *tp = terms + (ti & 1) * tstride + (sl * 16 + j) * nbp + b * T;
-                if constexpr (FMT == FMT_Q4K) {
+                if constexpr (FMT == FMT_KQMIX) {
+                    int sg, tl;
+                    item(ti, sl, sg, tl);
+                    if (seg_q6(sg)) {                                        // (uniform)
+                        float *tp = terms + (ti & 1) * tstride + (sl * 16 + j) * nbp6 + b * 4;
+                        tp[g] = q6k_term(q6k_view(rk), xb, aux + 8 * nb + b * 16, as, lane);
+                    } else {
+                        float *tp = terms + (ti & 1) * tstride + (sl * 16 + j) * nbp + b * 8;
+                        float t0, t1;
+                        q4k_terms(q4k_view(rk), xb, aux + b * 8, as, g, t0, t1);
+                        *(float2 *)(tp + 2 * g) = make_float2(t0, t1);
+                    }
+                } else if constexpr (FMT == FMT_Q4K) {
+                    float *tp = terms + (ti & 1) * tstride + (sl * 16 + j) * nbp + b * T;
                     float t0, t1;
                     q4k_terms(rk, xb, aux + b * 8, as, g, t0, t1);
                     *(float2 *)(tp + 2 * g) = make_float2(t0, t1);
                 } else {
+                    float *tp = terms + (ti & 1) * tstride + (sl * 16 + j) * nbp + b * T;
                     tp[g] = q6k_term(rk, xb, aux + b * 16, as, lane);
                 }
             } else {
@@ -974,7 +1076,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
                 block_mfma<FMT>(raw[k], B + b * bbytes, M, lane, corr, S);
                 const RawBlk<FMT> rk = raw[k];
                 if (n + PF < total) {
-                    raw[k] = load_raw<FMT>(fc.p, lane);
+                    raw[k] = load_unit(fc);
                     if (n + PF + 1 < total) fc = cur_next(fc);
                 }
                 if (lead) {
@@ -1108,6 +1210,9 @@ static fox_gpu_status fused_dispatch(fox_gpu_ctx *ctx, int fmt, const FusedArgs 
         if (fmt == FMT_Q4K) return fused_go<FMT_Q4K, IN, EPI>(ctx, a, grid);
         if (fmt == FMT_Q6K) return fused_go<FMT_Q6K, IN, EPI>(ctx, a, grid);
     }
+    if constexpr (IN == IN_NORM && EPI == EPI_ROPE) {
+        if (fmt == FMT_KQMIX) return fused_go<FMT_KQMIX, IN, EPI>(ctx, a, grid);
+    }
     return fused_go<FMT_TQ2, IN, EPI>(ctx, a, grid);
 }
 
@@ -1233,22 +1338,32 @@ extern "C" fox_gpu_status fox_gpu_qkv_rope(fox_gpu_ctx *ctx, const fox_gpu_tenso
     if (wq->ne0 != wk->ne0 || wk->ne0 != wv->ne0 || wk->ne1 != wv->ne1)
         return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: q, k, v must share their width, k and v "
                         "their rows");
-    if (wq->type != wk->type)
-        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "qkv_rope: q and k of different types take "
-                        "the separate steps");
     if (head_dim % 2 || wq->ne1 % head_dim || wk->ne1 % head_dim)
         return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: rows are not whole heads of even size");
     const size_t K = (size_t)wq->ne0;
     if (M > 1 && (x_stride < K || q_stride < wq->ne1))
         return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: stride too small");
     if (n_ctx > 0x7fffffff) return fox_fail(FOX_GPU_ERR_ARG, "qkv_rope: n_ctx too large");
-    // v of another type than q and k (a Q4_K_M-style mix) runs as a second
-    // launch over the same input
-    const bool split = wv->type != wq->type;
-    int fmt, fmt_v = -1;
+    // Q4_K and Q6_K side by side (a Q4_K_M-style mix) run as one launch,
+    // each segment in its own format; v of another type than q and k
+    // otherwise runs as a second launch over the same input
+    int fmt, fmt_k, fmt_v = -1;
     fox_gpu_status st = fused_check(wq->type, K, M, 1, &fmt, true);
     if (st) return st;
-    if (split && (st = fused_check(wv->type, K, M, 1, &fmt_v, true))) return st;
+    if ((st = fused_check(wk->type, K, M, 1, &fmt_k, true))) return st;
+    if ((st = fused_check(wv->type, K, M, 1, &fmt_v, true))) return st;
+    auto kq = [](int f) { return f == FMT_Q4K || f == FMT_Q6K; };
+    int q6_mask = 0;
+    if (kq(fmt) && kq(fmt_k) && kq(fmt_v) && (fmt != fmt_k || fmt != fmt_v)) {
+        if (fused_lds(FMT_KQMIX, (int)K, 1, 1).total > FUSED_LDS_MAX)
+            return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "qkv_rope: K too large for one launch");
+        q6_mask = (fmt == FMT_Q6K) | (fmt_k == FMT_Q6K) << 1 | (fmt_v == FMT_Q6K) << 2;
+        fmt = fmt_v = FMT_KQMIX;
+    } else if (fmt_k != fmt) {
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "qkv_rope: q and k of different types take "
+                        "the separate steps");
+    }
+    const bool split = fmt_v != fmt;
     if (!fused_aligned(x, x_stride, M, norm_w))
         return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "qkv_rope: x and norm_w must be 16-byte "
                         "aligned, the stride a multiple of 4");
@@ -1281,6 +1396,7 @@ extern "C" fox_gpu_status fox_gpu_qkv_rope(fox_gpu_ctx *ctx, const fox_gpu_tenso
     a.n_ctx = (int)n_ctx;
     a.k_cache = k_cache;
     a.v_cache = v_cache;
+    a.q6_mask = q6_mask;
     if ((st = fused_dispatch<IN_NORM, EPI_ROPE>(ctx, fmt, a, tiles)) || !split) return st;
     FusedArgs b = a;
     const fox_gpu_tensor *wsv[1] = {wv};

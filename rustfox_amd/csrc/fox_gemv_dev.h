@@ -10,7 +10,9 @@
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 
-enum { FMT_TQ2 = 1, FMT_Q4K = 2, FMT_Q6K = 3 };
+// (FMT_KQMIX: the one-launch q/k/v of the fused path with Q4_K and Q6_K
+// segments side by side, the format chosen per segment)
+enum { FMT_TQ2 = 1, FMT_Q4K = 2, FMT_Q6K = 3, FMT_KQMIX = 4 };
 
 // the kernel format of a tensor of `type` (of its layout in HBM: TQ1_0
 // tensors are held as TQ2_0 blocks)
@@ -27,7 +29,7 @@ static inline int fmt_of(int type)
 // float terms per block and row in the ordered combine
 __host__ __device__ constexpr int terms_per_block(int fmt)
 {
-    return fmt == FMT_Q4K ? 8 : fmt == FMT_Q6K ? 4 : 1;
+    return fmt == FMT_Q4K || fmt == FMT_KQMIX ? 8 : fmt == FMT_Q6K ? 4 : 1;
 }
 
 // B-operand bytes per block and token, aux int32 per block and token
@@ -38,7 +40,7 @@ __host__ __device__ constexpr int b_bytes_per_block_tok(int fmt)
 
 __host__ __device__ constexpr int aux_per_block_tok(int fmt)
 {
-    return fmt == FMT_Q4K ? 8 : fmt == FMT_Q6K ? 16 : 1;
+    return fmt == FMT_Q4K ? 8 : fmt == FMT_Q6K ? 16 : fmt == FMT_KQMIX ? 24 : 1;
 }
 
 __device__ __forceinline__ float half_bits_to_float(unsigned h)

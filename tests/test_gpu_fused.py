@@ -148,11 +148,11 @@ def test_unsupported_cases_say_so(gpu):
 
 
 def test_mixed_types_take_the_separate_steps(gpu):
-    """Gate and up of different types, and q and k of different types, are
-    refused by the one-launch stages with FOX_GPU_ERR_UNSUPPORTED, the
-    status on which the host runs the separate steps; so is a Q4_K_M-style
-    q/k/v (Q4_K q and k, Q6_K v) for more than one token.  Mismatched widths
-    remain FOX_GPU_ERR_ARG."""
+    """Gate and up of different types, and q and k of different types other
+    than the two K-quants, are refused by the one-launch stages with
+    FOX_GPU_ERR_UNSUPPORTED, the status on which the host runs the separate
+    steps; so is a Q4_K_M-style q/k/v (Q4_K q and k, Q6_K v) for more than
+    one token.  Mismatched widths remain FOX_GPU_ERR_ARG."""
     rng = np.random.default_rng(4)
     K, hd, n_ctx = 512, 64, 8
     q4 = [gpu.tensor(12, K, 128, weights(rng, 12, 128, K)) for _ in range(2)]
@@ -164,8 +164,9 @@ def test_mixed_types_take_the_separate_steps(gpu):
     pos = gpu.array(np.zeros(1, np.uint32))
     kc = gpu.empty(n_ctx * 128, np.float32)
     vc = gpu.empty(n_ctx * 128, np.float32)
+    tq = gpu.tensor(35, K, 128, weights(rng, 35, 128, K))
     with pytest.raises(rf.FoxError) as e:
-        gpu.qkv_rope(q4[0], q6, q4[1], x, 1, nw, EPS, gpu.empty(128, np.float32), cs, cs, pos,
+        gpu.qkv_rope(tq, q4[0], q4[1], x, 1, nw, EPS, gpu.empty(128, np.float32), cs, cs, pos,
                      n_ctx, kc, vc, hd)
     assert e.value.status == 5
     with pytest.raises(rf.FoxError) as e:
@@ -251,30 +252,34 @@ def test_kquant_rmsnorm_nonfinite_follows_the_reference(gpu, oracle, gtype):
 
 
 @pytest.mark.parametrize("K,pos", [(768, 3), (4096, 13)])
-def test_q4_k_m_qkv_rope_bit_exact(gpu, oracle, K, pos):
-    """A Q4_K_M-style q/k/v for one token: Q4_K q and k with RoPE in one
-    launch, Q6_K v into the cache in a second, both from rmsnorm(x)."""
+@pytest.mark.parametrize("types", [(12, 12, 14), (12, 14, 12), (14, 14, 12), (14, 12, 14)],
+                         ids=lambda t: "-".join({12: "q4", 14: "q6"}[x] for x in t))
+def test_q4_k_m_qkv_rope_bit_exact(gpu, oracle, K, pos, types):
+    """A Q4_K_M-style q/k/v for one token (and the other mixes of the two
+    K-quants): one launch, each segment in its own format, q and k with
+    RoPE, v into the cache, all from rmsnorm(x)."""
     n_head, n_kv, hd, n_ctx = 4, 2, 64, 16
     kvd = n_kv * hd
-    rng = np.random.default_rng([K, pos, 62])
-    Wq, Wk = weights(rng, 12, n_head * hd, K), weights(rng, 12, kvd, K)
-    Wv = weights(rng, 14, kvd, K)
+    tq_, tk_, tv_ = types
+    rng = np.random.default_rng([K, pos, 62] + list(types))
+    Wq, Wk = weights(rng, tq_, n_head * hd, K), weights(rng, tk_, kvd, K)
+    Wv = weights(rng, tv_, kvd, K)
     x = rng.standard_normal((1, K)).astype(np.float32)
     nw = rng.uniform(0.5, 1.5, K).astype(np.float32)
     cos_t, sin_t = oracle.rope_tables(n_ctx, hd, 10000.0)
     q_out = gpu.empty(n_head * hd, np.float32)
     kc = gpu.array(np.zeros(n_ctx * kvd, np.float32))
     vc = gpu.array(np.zeros(n_ctx * kvd, np.float32))
-    gpu.qkv_rope(gpu.tensor(12, K, n_head * hd, Wq), gpu.tensor(12, K, kvd, Wk),
-                 gpu.tensor(14, K, kvd, Wv), gpu.array(x), 1, gpu.array(nw), EPS, q_out,
+    gpu.qkv_rope(gpu.tensor(tq_, K, n_head * hd, Wq), gpu.tensor(tk_, K, kvd, Wk),
+                 gpu.tensor(tv_, K, kvd, Wv), gpu.array(x), 1, gpu.array(nw), EPS, q_out,
                  gpu.array(cos_t), gpu.array(sin_t), gpu.array(np.array([pos], np.uint32)),
                  n_ctx, kc, vc, hd)
     xb = oracle.rmsnorm(x[0], nw, EPS)
     half = hd // 2
     cr, sr = cos_t[pos * half:(pos + 1) * half], sin_t[pos * half:(pos + 1) * half]
-    want_q = oracle.rope(oracle.gemv(12, xb, Wq, n_head * hd, K), n_head, hd, cr, sr)
-    want_k = oracle.rope(oracle.gemv(12, xb, Wk, kvd, K), n_kv, hd, cr, sr)
-    want_v = oracle.gemv(14, xb, Wv, kvd, K)
+    want_q = oracle.rope(oracle.gemv(tq_, xb, Wq, n_head * hd, K), n_head, hd, cr, sr)
+    want_k = oracle.rope(oracle.gemv(tk_, xb, Wk, kvd, K), n_kv, hd, cr, sr)
+    want_v = oracle.gemv(tv_, xb, Wv, kvd, K)
     vq = vc.numpy().reshape(-1, kvd, 4)
     got_k = kc.numpy().reshape(n_ctx, kvd)
     assert np.array_equal(bits(q_out.numpy()), bits(want_q))
