@@ -234,7 +234,9 @@ fox_gpu_status fox_gpu_gemv_rmsnorm(fox_gpu_ctx *ctx, size_t n,
 
 /* xb = rmsnorm(x, norm_w); q, k, v = W xb; RoPE on q and k at pos[0] + t;
  * q -> q_out, k and v -> the layer's caches (layouts as fox_gpu_rope_store).
- * q and k share one type; v may have another (two launches then). */
+ * One launch when q and k share one type and v has it too, or when all three
+ * are K-quants (Q4_K and Q6_K in any mix, one token); q and k of one type
+ * and v of another otherwise run as two launches. */
 fox_gpu_status fox_gpu_qkv_rope(fox_gpu_ctx *ctx, const fox_gpu_tensor *wq,
                                 const fox_gpu_tensor *wk, const fox_gpu_tensor *wv,
                                 const float *x, size_t x_stride, size_t M,
