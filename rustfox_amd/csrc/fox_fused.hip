@@ -92,7 +92,7 @@ __host__ __device__ inline FusedLds fused_lds(int fmt, int K, int M, int nslab)
     L.aux = off;   off += ((nb * M * aux_per_block_tok(fmt) * 4) + 15) & ~15;
     L.bs = off;    off += fmt == FMT_TQ2 ? 0 : ((nb * 4 + 15) & ~15);
     L.terms = off; off += 2 * nslab * 16 * M * fused_ntp(fmt, nb) * 4;
-    L.y = off;     off += nslab * 16 * M * 4;
+    L.y = off;     off += FWG * 4;
     L.total = off;
     return L;
 }
@@ -873,10 +873,17 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
         if (k + 1 < total) fc = cur_next(fc);              // past the last unit: reload it
     }
 
-    // combiner threads: (slab, token, row) of an item's outputs
-    const int nthr = nslab * 16 * M;
-    const bool comb = tid < nthr;
-    const int csl = tid / (16 * M), crem = tid - csl * 16 * M;
+    // combiner threads: (slab, token, row) of an item's outputs.  A
+    // workgroup with exactly two items ends them together: the waves from
+    // hbase on take the second item, so that its blocks follow the first
+    // item's with no barrier between, and one barrier and one combine serve
+    // both (whole waves, so that the item index stays wave-uniform).
+    const int nthr = nslab * 16 * M, hbase = (nthr + 63) & ~63;
+    const bool pair = !KQ && EPI != EPI_SUMS && ntl == 2 && hbase + nthr <= FWG;   // (uniform)
+    const int hb = pair && wave >= (hbase >> 6) ? 1 : 0;   // the wave's item of the pair
+    const int ltid = tid - hb * hbase;
+    const bool comb = ltid < nthr;
+    const int csl = ltid / (16 * M), crem = ltid - csl * 16 * M;
     const int ct = crem >> 4, crow = crem & 15;
     // the position through the scalar cache: its wait does not wait for the
     // vector loads above
@@ -904,7 +911,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     float pre0 = 0.0f, pre1 = 0.0f;
     // (the first item's old outputs or RoPE table entries: in flight during
     // the input stage)
-    if (EPI == EPI_STORE || EPI == EPI_ROPE) epi_load(0, pre0, pre1);
+    if (EPI == EPI_STORE || EPI == EPI_ROPE) epi_load(hb, pre0, pre1);
     // (nothing that uses the input may be scheduled above the weight loads)
     __builtin_amdgcn_sched_barrier(0);
     // the zero padding of the term rows (read after the input stage's
@@ -938,16 +945,19 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     }
     __syncthreads();
 
-    // ---- end of item ti: ordered combine, activation scale, epilogue
-    auto item_end = [&](int ti) {
+    // ---- end of item ti0 (with both: of items ti0 and ti0 + 1, the pair):
+    // ordered combine, activation scale, epilogue
+    auto item_end = [&](int ti0, bool both) {
         if (EPI == EPI_SUMS) return;
         __syncthreads();
+        const int ti = ti0 + hb;
+        const bool act = comb && (hb == 0 || both);
         int sg = 0, tl = 0;
         item(ti, csl, sg, tl);
         const int orow = tl * 16 + crow;
-        const bool owns = comb && orow < pick4(a.n_rows, sg);
+        const bool owns = act && orow < pick4(a.n_rows, sg);
         float y = 0.0f;
-        if (comb) {
+        if (act) {
             // The row's terms in block order, four at a time (chunk c holds
             // terms 4c .. 4c + 3).  Four chunk slots rotate, each reloaded
             // with the chunk four ahead right after its adds (the
@@ -986,10 +996,10 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
                 *o = (a.flags & FOX_GPU_GEMV_ACCUMULATE) ? pre0 + y : y;
             }
         } else if (EPI == EPI_SILU) {
-            if (comb) ybuf[tid] = y;
+            if (act) ybuf[tid] = y;
             __syncthreads();
             if (owns && csl == 0) {
-                const float gt = y, up = ybuf[16 * M + crem];
+                const float gt = y, up = ybuf[hb * hbase + 16 * M + crem];
                 a.out[0][(size_t)ct * a.out_stride[0] + orow] =
                     fox_div(gt, 1.0f + fox_expf(-gt)) * up; // src/ops.c:45-46
             }
@@ -1015,7 +1025,8 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
         // the next item's operands, loaded into the registers just read (no
         // copy: a copy would wait here for the load); they are used at that
         // item's end, after its blocks
-        if ((EPI == EPI_STORE || EPI == EPI_ROPE) && ti + 1 < ntl) epi_load(ti + 1, pre0, pre1);
+        if ((EPI == EPI_STORE || EPI == EPI_ROPE) && !pair && ti + 1 < ntl)
+            epi_load(ti + 1, pre0, pre1);
     };
 
     // ---- blocks: integer sums, then one float term per row and token (T
@@ -1029,8 +1040,13 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     // a lead lane's terms: rows 4g .. 4g + 3 of token tok, row after row
     // M * nbp floats apart, the up slab 16 M nbp floats on
     const int rstep = M * nbp, tlane = (4 * g * M + tok) * nbp;
+    // (the end of item ti; the pair's first item ends with its second)
+    auto item_done = [&](int ti) {
+        if (pair && ti == 0) return;
+        item_end(pair ? 0 : ti, pair);
+    };
     if (nu == 0) {
-        for (int ti = 0; ti < ntl; ti++) item_end(ti);
+        for (int ti = 0; ti < ntl; ti++) item_done(ti);
         return;
     }
     int ti = 0, r = 0;                                     // unit n of the wave
@@ -1097,7 +1113,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
                     }
                 }
             }
-            if (r == nu - 1) item_end(ti);
+            if (r == nu - 1) item_done(ti);
             step(ti, r);
         }
     }
