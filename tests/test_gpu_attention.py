@@ -68,6 +68,9 @@ CASES = [  # n_head, n_kv, hd, n_ctx, pos, M
     (4, 1, 64, 3000, 2999, 1),     # gqa 4, hd 64: 12 tiles per slice
     (16, 2, 256, 500, 499, 1),     # gqa 8, hd 256: 32 slices for 8 tiles, two tiles a round
     (6, 6, 48, 400, 399, 1),       # hd 48: the second chunk partly filled
+    (32, 8, 128, 2200, 2048, 1),   # 4B/8B heads past 2048 rows: 33 score tiles a kv head
+    (32, 8, 128, 4200, 4150, 1),   # 66 tiles a kv head
+    (32, 16, 128, 700, 699, 1),    # 27B heads, 16 kv heads, near the last row
 ]
 
 
