@@ -29,6 +29,7 @@
 #include "fox_math.h"
 
 #include <cstring>
+#include <type_traits>
 
 #define FW 8                    // waves per workgroup
 #define FWG (FW * 64)
@@ -381,6 +382,254 @@ __device__ __forceinline__ void wave_max_n(uint32_t (&v)[N])
     for (int i = 0; i < N; i++) v[i] = max(v[i], dpp_t<0x143, 0xC>(0u, v[i]));
 #pragma unroll
     for (int i = 0; i < N; i++) v[i] = read_lane(v[i], 63);
+}
+
+// ---- several tokens (the ternary formats, M > 1): tokens in groups of
+// TG, a group's tokens loaded together and taken through each step of
+// quantise_to_b side by side, so that a group costs the barriers of one
+// token (three) instead of three per token.  TG keeps a group's input
+// registers at 16 float4 per thread.
+__host__ __device__ constexpr int tg_of(int R4)
+{
+    return R4 <= 2 ? 2 : 1;
+}
+
+template <int R4MAX, int TG>
+struct InGrp {
+    float4 xv[TG][R4MAX];
+    float4 wv[R4MAX];                      // the RMSNorm weights (one copy for all tokens)
+    uint32_t qd[TG][R4MAX];
+};
+
+// the dwords of tokens t0 .. t0 + nt - 1 (nt <= TG; the rows past the
+// group's last token re-read it, so that the count of loads is fixed), and
+// with wv the norm weights
+template <int IN, int R4MAX, int TG>
+__device__ __forceinline__ void load_group(const float *x, const float *norm_w, const int8_t *q_in,
+                                           int x_stride, int t0, int nt, int K, bool wv,
+                                           InGrp<R4MAX, TG> &g)
+{
+    const int tid = threadIdx.x, nd = K >> 2;
+#pragma unroll
+    for (int j = 0; j < TG; j++) {
+        const int t = t0 + (j < nt ? j : nt - 1);
+        if (IN == IN_Q) {
+            const uint32_t *q4 = (const uint32_t *)(q_in + (size_t)t * K);
+#pragma unroll
+            for (int r = 0; r < R4MAX; r++) {
+                const int m = tid + r * FWG;
+                g.qd[j][r] = q4[m < nd ? m : nd - 1];
+            }
+        } else {
+            const float4 *x4 = (const float4 *)(x + (size_t)t * x_stride);
+#pragma unroll
+            for (int r = 0; r < R4MAX; r++) {
+                const int m = tid + r * FWG;
+                g.xv[j][r] = x4[m < nd ? m : nd - 1];
+            }
+        }
+    }
+    if (IN == IN_NORM && wv) {
+        const float4 *w4 = (const float4 *)norm_w;
+#pragma unroll
+        for (int r = 0; r < R4MAX; r++) {
+            const int m = tid + r * FWG;
+            g.wv[r] = w4[m < nd ? m : nd - 1];
+        }
+    }
+}
+
+// quantise_to_b for the group's tokens: the same operations per token, in
+// the same order (RMSNorm with the certified scale, amax, quantiser, B
+// operand, block corrections); dred and ured hold TG x FW partials.  Writes
+// ascale[t] and ends with a barrier.
+template <int FMT, int IN, int R4MAX, int TG>
+__device__ __forceinline__ void quantise_group(const FusedArgs &a, int t0, int nt, int K,
+                                               uint8_t *B, int32_t *aux, double *dred,
+                                               uint32_t *ured, float *ascale,
+                                               InGrp<R4MAX, TG> &g)
+{
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int M = a.M, nb = K >> 8, nd = K >> 2;
+#pragma unroll
+    for (int r = 0; r < R4MAX; r++) {
+        const bool ok = tid + r * FWG < nd;
+#pragma unroll
+        for (int j = 0; j < TG; j++) {
+            if (IN == IN_Q) g.qd[j][r] = ok ? g.qd[j][r] : 0u;
+            else g.xv[j][r] = keep4(ok, g.xv[j][r]);
+        }
+        if (IN == IN_NORM) g.wv[r] = keep4(ok, g.wv[r]);
+    }
+    float act[TG];
+#pragma unroll
+    for (int j = 0; j < TG; j++) act[j] = 0.0f;
+    if (IN == IN_NORM) {
+        // rms_apply per token, the partial sums of all tokens through one barrier
+        double ss[TG];
+#pragma unroll
+        for (int j = 0; j < TG; j++) {
+            ss[j] = 0.0;
+#pragma unroll
+            for (int r = 0; r < R4MAX; r++) {
+                const double x0 = g.xv[j][r].x, x1 = g.xv[j][r].y;
+                const double x2 = g.xv[j][r].z, x3 = g.xv[j][r].w;
+                ss[j] = __builtin_fma(x0, x0, ss[j]);
+                ss[j] = __builtin_fma(x1, x1, ss[j]);
+                ss[j] = __builtin_fma(x2, x2, ss[j]);
+                ss[j] = __builtin_fma(x3, x3, ss[j]);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < TG; j++) ss[j] = wave_sum_dd(ss[j]);
+        if (lane == 0) {
+#pragma unroll
+            for (int j = 0; j < TG; j++) dred[j * FW + wave] = ss[j];
+        }
+        __syncthreads();
+        const double rel = (double)(K + 64) * 0x1p-52;
+        const double sgn = (lane & 1) ? 1.0 : -1.0;
+#pragma unroll
+        for (int j = 0; j < TG; j++) {
+            if (j >= nt) break;                                   // (uniform)
+            double tot = 0.0;
+            for (int w = 0; w < FW; w++) tot += dred[j * FW + w];
+            const double y = 1.0 / __builtin_sqrt(tot * (1.0 + sgn * rel) / (double)K +
+                                                  (double)a.eps) * (1.0 - sgn * 0x1p-50);
+            const float f = (float)y;
+            float rs = read_lane(f, 0);
+            if (rs != read_lane(f, 1)) {
+                const float *xt = a.x + (size_t)(t0 + j) * a.x_stride;
+                double seq = 0.0;
+                for (int i = 0; i < K; i++) seq += (double)xt[i] * (double)xt[i];
+                rs = (float)(1.0 / __builtin_sqrt(seq / (double)K + (double)a.eps));
+            }
+#pragma unroll
+            for (int r = 0; r < R4MAX; r++) {
+                g.xv[j][r].x = g.xv[j][r].x * rs * g.wv[r].x;
+                g.xv[j][r].y = g.xv[j][r].y * rs * g.wv[r].y;
+                g.xv[j][r].z = g.xv[j][r].z * rs * g.wv[r].z;
+                g.xv[j][r].w = g.xv[j][r].w * rs * g.wv[r].w;
+            }
+        }
+    }
+    if (IN != IN_Q) {
+        // amax per token as the largest |x| bit pattern, all tokens' wave
+        // maxima together
+        uint32_t mb[TG];
+#pragma unroll
+        for (int j = 0; j < TG; j++) {
+            uint32_t m = 0;
+#pragma unroll
+            for (int r = 0; r < R4MAX; r++) {
+                m = max(m, __float_as_uint(g.xv[j][r].x) & 0x7fffffffu);
+                m = max(m, __float_as_uint(g.xv[j][r].y) & 0x7fffffffu);
+                m = max(m, __float_as_uint(g.xv[j][r].z) & 0x7fffffffu);
+                m = max(m, __float_as_uint(g.xv[j][r].w) & 0x7fffffffu);
+            }
+            mb[j] = m;
+        }
+        wave_max_n<TG>(mb);
+        if (lane == 0) {
+#pragma unroll
+            for (int j = 0; j < TG; j++) ured[j * FW + wave] = mb[j];
+        }
+        __syncthreads();
+        uint32_t am[TG];
+#pragma unroll
+        for (int j = 0; j < TG; j++) {
+            am[j] = 0;
+            for (int w = 0; w < FW; w++) am[j] = max(am[j], ured[j * FW + w]);
+        }
+#pragma unroll
+        for (int j = 0; j < TG; j++) {
+            if (j >= nt) break;                                   // (uniform)
+            if (am[j] >= 0x03800000u && am[j] < 0x7f800000u) {
+                const float amax = __uint_as_float(am[j]);
+                const float inv = fox_div(127.0f, amax);
+#pragma unroll
+                for (int r = 0; r < R4MAX; r++)
+                    g.qd[j][r] = pack_lo_bytes(quant_fast(g.xv[j][r].x, inv),
+                                               quant_fast(g.xv[j][r].y, inv),
+                                               quant_fast(g.xv[j][r].z, inv),
+                                               quant_fast(g.xv[j][r].w, inv));
+                act[j] = fox_div(amax, 127.0f);
+            } else if (am[j] == 0) {
+#pragma unroll
+                for (int r = 0; r < R4MAX; r++) g.qd[j][r] = 0u;
+            } else {
+                // NaN, inf or a tiny amax (uniform): the float amax of the
+                // non-NaN values, then the exact quantiser.  (Every thread
+                // has read all of the group's maxima before the first
+                // barrier here, so the slot can be reused.)
+                float m = 0.0f;
+#pragma unroll
+                for (int r = 0; r < R4MAX; r++) {
+                    const float v4[4] = {g.xv[j][r].x, g.xv[j][r].y, g.xv[j][r].z, g.xv[j][r].w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float av = fabsf(v4[e]);
+                        if (av > m) m = av;
+                    }
+                }
+                m = wave_max(m);
+                __syncthreads();
+                if (lane == 0) ured[j * FW + wave] = __float_as_uint(m);
+                __syncthreads();
+                float amax = 0.0f;
+                for (int w = 0; w < FW; w++) amax = max(amax, __uint_as_float(ured[j * FW + w]));
+                if (amax > 0.0f) {
+                    const float inv = fox_div(127.0f, amax);
+#pragma unroll
+                    for (int r = 0; r < R4MAX; r++)
+                        g.qd[j][r] = pack_lo_bytes(quant_one(g.xv[j][r].x, inv),
+                                                   quant_one(g.xv[j][r].y, inv),
+                                                   quant_one(g.xv[j][r].z, inv),
+                                                   quant_one(g.xv[j][r].w, inv));
+                    act[j] = fox_div(amax, 127.0f);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < R4MAX; r++) g.qd[j][r] = 0u;
+                }
+            }
+        }
+    }
+    // B operand and the per-block corrections of all the group's tokens
+    const int boff = b_lane_off(lane, M);
+    const int bbytes = b_bytes_per_block_tok(FMT) * M;
+    int part[TG * R4MAX];
+#pragma unroll
+    for (int j = 0; j < TG; j++) {
+#pragma unroll
+        for (int r = 0; r < R4MAX; r++) {
+            const int b = wave + FW * r;
+            if (j < nt && b < nb)                                  // (uniform)
+                *(uint32_t *)(B + b * bbytes + (t0 + j) * 16 + boff) = g.qd[j][r];
+            part[j * R4MAX + r] = __builtin_amdgcn_sdot4((int)g.qd[j][r], 0x01010101, 0, false);
+        }
+    }
+    wave_sum_n<TG * R4MAX>(part);
+    if (lane == 0) {
+#pragma unroll
+        for (int j = 0; j < TG; j++) {
+            if (j >= nt) break;
+#pragma unroll
+            for (int r = 0; r < R4MAX; r++) {
+                const int b = wave + FW * r;
+                if (b >= nb) break;
+                aux[b * M + t0 + j] = -part[j * R4MAX + r];
+            }
+        }
+    }
+    if (tid == 0) {
+#pragma unroll
+        for (int j = 0; j < TG; j++) {
+            if (j >= nt) break;
+            ascale[t0 + j] = IN == IN_Q ? (a.scale_in ? a.scale_in[t0 + j] : 0.0f) : act[j];
+        }
+    }
+    __syncthreads();
 }
 
 // K-quant input stage, one token: RMSNorm (IN_NORM), then every 256-element
@@ -753,11 +1002,12 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
 {
     extern __shared__ uint4 fused_lds4[];
     uint8_t *lds = (uint8_t *)fused_lds4;
-    __shared__ double dred[FW];
-    __shared__ uint32_t ured[FW];
+    constexpr bool KQ = FMT != FMT_TQ2;                    // a K-quant (one token)
+    constexpr int TG = MT && !KQ ? tg_of(R4) : 1;          // tokens per input group
+    __shared__ double dred[FW * TG];
+    __shared__ uint32_t ured[FW * TG];
     __shared__ float ascale[FOX_GPU_MAX_TOKENS];
 
-    constexpr bool KQ = FMT != FMT_TQ2;                    // a K-quant (one token)
     constexpr int CHUNK = FMT == FMT_TQ2 ? TQ2_CHUNK : FMT == FMT_Q4K ? Q4K_CHUNK : Q6K_CHUNK;
     // the K-quant of segment sg (FMT_KQMIX: per segment) and its chunk bytes
     auto seg_q6 = [&](int sg) -> bool {
@@ -792,10 +1042,14 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     // read with constant indices only, so that they arrive in one batch of
     // scalar loads (an argument indexed at run time is a chain of loads).
     const int bx = blockIdx.x, nwg = gridDim.x;
-    // the input of token 0 first: nothing ahead of its loads but the
-    // argument reads they need
-    InRegs<R4> in;
-    load_input<IN, R4>(x_in, norm_in, q_in, a.x_stride, 0, K, in);
+    // the input of token 0 (several tokens: of the first group) first:
+    // nothing ahead of its loads but the argument reads they need
+    using InT = std::conditional_t<MT && !KQ, InGrp<R4, TG>, InRegs<R4>>;
+    InT in;
+    if constexpr (MT && !KQ)
+        load_group<IN, R4, TG>(x_in, norm_in, q_in, a.x_stride, 0, min(M, TG), K, true, in);
+    else
+        load_input<IN, R4>(x_in, norm_in, q_in, a.x_stride, 0, K, in);
     const int ntl = a.n_per + (bx < a.n_rem);              // items of this workgroup (>= 1)
     const int ts1 = a.tile_start[1], ts2 = a.tile_start[2], ts3 = a.tile_start[3];
     // (integer arithmetic only: comparisons turned into 0/1 values and
@@ -928,20 +1182,20 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     // (token 0 outside the loop: its waits then count the loads above)
     if constexpr (KQ) {
         quantise_kq<FMT, IN, R4>(a, K, (int8_t *)B, aux, bsc, dred, in);
+    } else if constexpr (MT) {
+        // the groups in turn, the next one's input in flight while a group
+        // is quantised (the first is in flight since the start)
+        for (int t0 = 0; t0 < M; t0 += TG) {
+            InT cur = in;
+            if (t0 + TG < M)
+                load_group<IN, R4, TG>(x_in, norm_in, q_in, a.x_stride, t0 + TG,
+                                       min(M - t0 - TG, TG), K, false, in);
+            quantise_group<FMT, IN, R4, TG>(a, t0, min(M - t0, TG), K, B, aux, dred, ured,
+                                            ascale, cur);
+        }
     } else {
         const float s = quantise_to_b<FMT, IN, R4>(a, 0, K, B, aux, dred, ured, in);
         if (tid == 0) ascale[0] = s;
-    }
-    // the later tokens one ahead: token t + 1's input is in flight while
-    // token t is quantised
-    if (MT) {
-        load_input<IN, R4>(x_in, norm_in, q_in, a.x_stride, 1, K, in);
-        for (int t = 1; t < M; t++) {
-            InRegs<R4> cur = in;
-            if (t + 1 < M) load_input<IN, R4>(x_in, norm_in, q_in, a.x_stride, t + 1, K, in);
-            const float s = quantise_to_b<FMT, IN, R4>(a, t, K, B, aux, dred, ured, cur);
-            if (tid == 0) ascale[t] = s;
-        }
     }
     __syncthreads();
 
