@@ -547,12 +547,19 @@ __device__ __forceinline__ float sc_chunk(float acc, const float4 *qr, const flo
     return acc;
 }
 
-// One workgroup per (64-position tile, kv head, token); wave w takes query
-// heads w, w + 4, ... of the kv head, one lane per position.  The tile's K
-// rows arrive in NCH chunks of 32 dimensions, copied straight into LDS: every
-// copy is issued at the start, and the dot products of chunk c run once that
-// chunk is in, while the later ones are still arriving (each sum stays in
-// head-dimension order, chunk after chunk).  A chunk holds 64 rows of 8
+// tokens per scores workgroup (27B-class heads, 8192 positions, 8 tokens:
+// 241.6 us for the whole attention with one, 220.1 with two, 213.4 with
+// four, 216.3 with eight; 4B-class heads at 2048: 57.5 to 58.3 us up to four,
+// 63.9 with eight)
+#define SC_TPW 4
+// One workgroup per (64-position tile, kv head, TPW tokens); wave w
+// takes query heads w, w + 4, ... of the kv head, one lane per position.  The
+// tile's K rows arrive in NCH chunks of 32 dimensions, copied straight into
+// LDS: every copy is issued at the start, and the first token's dot products
+// of chunk c run once that chunk is in, while the later ones are still
+// arriving (each sum stays in head-dimension order, chunk after chunk).  The
+// later tokens reuse the tile (only their query heads are copied), so K is
+// read once for every TPW tokens.  A chunk holds 64 rows of 8
 // quads (128 B a row); quad j of row r sits in slot j ^ ((r >> 1) & 7), so
 // that sixteen consecutive lanes' reads of one quad fall in different banks
 // (rows r and r + 1 differ in the 32-bank half, r and r + 2 .. r + 14 in the
@@ -565,7 +572,8 @@ __global__ __launch_bounds__(256) void attn_scores_x(const float *__restrict__ q
                                                      const uint32_t *__restrict__ pos,
                                                      int n_ctx, size_t att_stride,
                                                      float *__restrict__ att,
-                                                     float *__restrict__ tmax, int n_tiles)
+                                                     float *__restrict__ tmax, int n_tiles,
+                                                     int M, int tpw)
 {
     // one array per chunk: separate objects, so that waiting for a chunk's
     // copies does not wait for the later chunks' copies
@@ -578,26 +586,35 @@ __global__ __launch_bounds__(256) void attn_scores_x(const float *__restrict__ q
         return c == 0 ? kq0 : c == 1 ? kq1 : c == 2 ? kq2 : c == 3 ? kq3
              : c == 4 ? kq4 : c == 5 ? kq5 : c == 6 ? kq6 : kq7;
     };
-    const int tile = blockIdx.x, p0 = tile * SC_TILE, kvh = blockIdx.y, t = blockIdx.z;
+    const int tile = blockIdx.x, p0 = tile * SC_TILE, kvh = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = wave_index();
     const int gqa = n_head / n_head_kv, kvd = n_head_kv * hd, nv = hd >> 2;
-    const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
-    if (p0 >= upto) return;
-    const int pn = upto - p0 < SC_TILE ? upto - p0 : SC_TILE;
+    // token t sees positions below upto(t), which grows with t: the first
+    // token that reaches this tile, and the rows the last one uses
+    auto upto_of = [&](int t) {
+        return (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
+    };
+    // this workgroup's tokens: tz .. t_end - 1
+    const int tz = (int)blockIdx.z * tpw, t_end = min(tz + tpw, M);
+    const int upto_last = upto_of(t_end - 1);
+    if (p0 >= upto_last) return;
+    int t0 = tz;
+    while (upto_of(t0) <= p0) t0++;                         // (uniform)
+    const int pn_last = upto_last - p0 < SC_TILE ? upto_last - p0 : SC_TILE;
     // the query heads: blocks of 64 quads, wave w takes blocks w, w + 4
     const int nqq = gqa * nv, nqb = (nqq + 63) >> 6;
-    const float *qbase = q + (size_t)t * q_stride + (size_t)kvh * gqa * hd;
     constexpr int QB = ATT_MAXG * ATT_MAXHD / 4 / 64 / 4;   // blocks per wave at most
-    int nq_copies = 0;
+    auto copy_q = [&](int t) {
+        const float *qbase = q + (size_t)t * q_stride + (size_t)kvh * gqa * hd;
 #pragma unroll
-    for (int k = 0; k < QB; k++) {
-        const int b = wave + 4 * k;
-        if (b < nqb) {
-            copy_to_lds16(qbase + 4 * min(64 * b + lane, nqq - 1), qq + 64 * b);
-            nq_copies++;
+        for (int k = 0; k < QB; k++) {
+            const int b = wave + 4 * k;
+            if (b < nqb) copy_to_lds16(qbase + 4 * min(64 * b + lane, nqq - 1), qq + 64 * b);
         }
-    }
+    };
+    copy_q(t0);
     // K: chunk c is 8 blocks of 8 rows; wave w copies blocks 2w and 2w + 1
+    // (the rows of the last token; an earlier token ignores those past its own)
     const float *kbase = kc + (size_t)p0 * kvd + (size_t)kvh * hd;
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
@@ -606,49 +623,64 @@ __global__ __launch_bounds__(256) void attn_scores_x(const float *__restrict__ q
             const int b = 2 * wave + r, row = 8 * b + (lane >> 3);
             const int j = (lane & 7) ^ ((row >> 1) & 7);
             const int cq = min(SC_CQ * c + j, nv - 1);
-            copy_to_lds16(kbase + (size_t)min(row, pn - 1) * kvd + 4 * cq,
+            copy_to_lds16(kbase + (size_t)min(row, pn_last - 1) * kvd + 4 * cq,
                           kq(c) + 8 * b * SC_CQ);
         }
     }
-    const bool ok = lane < pn;
-    const int row = ok ? lane : 0, sw = (row >> 1) & 7;
     const bool full = nv == NCH * SC_CQ;            // (uniform) every chunk whole
     constexpr int HW = ATT_MAXG / 4;                // heads per wave at most
-    float a[HW];
+    const float scale = fox_div(1.0f, fox_sqrtf((float)hd));
+    for (int t = t0; t < t_end; t++) {
+        const int upto = upto_of(t);
+        const int pn = upto - p0 < SC_TILE ? upto - p0 : SC_TILE;
+        const bool ok = lane < pn;
+        const int row = ok ? lane : 0, sw = (row >> 1) & 7;
+        if (t > t0) {
+            // every wave is done with the previous token's query heads
+            __syncthreads();
+            copy_q(t);
+        }
+        float a[HW];
 #pragma unroll
-    for (int h = 0; h < HW; h++) a[h] = 0.0f;
+        for (int h = 0; h < HW; h++) a[h] = 0.0f;
 #pragma unroll
-    for (int c = 0; c < NCH; c++) {
-        // this wave's copies of chunk c (and the query heads) are in once at
-        // most 2 (NCH - 1 - c) copies are pending; the barrier covers the
-        // other waves' copies
-        wait_vmcnt(2 * (NCH - 1 - c));
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-        const float4 *kr = kq(c) + row * SC_CQ;
+        for (int c = 0; c < NCH; c++) {
+            // this wave's copies of chunk c (and the query heads) are in once
+            // at most 2 (NCH - 1 - c) copies are pending (later tokens: only
+            // their query heads are pending); the barrier covers the other
+            // waves' copies
+            if (t == t0) {
+                wait_vmcnt(2 * (NCH - 1 - c));
+            } else if (c == 0) {
+                wait_vmcnt(0);
+            }
+            if (t == t0 || c == 0) {
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            }
+            const float4 *kr = kq(c) + row * SC_CQ;
+#pragma unroll
+            for (int h = 0; h < HW; h++) {
+                const int g = wave + 4 * h;
+                if (g < gqa) {
+                    const float4 *qr = qq + g * nv + SC_CQ * c;
+                    a[h] = full ? sc_chunk<true>(a[h], qr, kr, sw, c, nv)
+                                : sc_chunk<false>(a[h], qr, kr, sw, c, nv);
+                }
+            }
+        }
 #pragma unroll
         for (int h = 0; h < HW; h++) {
             const int g = wave + 4 * h;
             if (g < gqa) {
-                const float4 *qr = qq + g * nv + SC_CQ * c;
-                a[h] = full ? sc_chunk<true>(a[h], qr, kr, sw, c, nv)
-                            : sc_chunk<false>(a[h], qr, kr, sw, c, nv);
+                const float sc = a[h] * scale;
+                const int hh = kvh * gqa + g;
+                if (ok) att[((size_t)t * n_head + hh) * att_stride + p0 + lane] = sc;
+                // tile maximum, NaN never taken
+                const float m = wave_reduce((ok && sc == sc) ? sc : -INFINITY, -INFINITY,
+                                            [](float x, float y) { return y > x ? y : x; });
+                if (lane == 0) tmax[((size_t)t * n_head + hh) * n_tiles + tile] = m;
             }
-        }
-    }
-    (void)nq_copies;
-    const float scale = fox_div(1.0f, fox_sqrtf((float)hd));
-#pragma unroll
-    for (int h = 0; h < HW; h++) {
-        const int g = wave + 4 * h;
-        if (g < gqa) {
-            const float sc = a[h] * scale;
-            const int hh = kvh * gqa + g;
-            if (ok) att[((size_t)t * n_head + hh) * att_stride + p0 + lane] = sc;
-            // tile maximum, NaN never taken
-            const float m = wave_reduce((ok && sc == sc) ? sc : -INFINITY, -INFINITY,
-                                        [](float x, float y) { return y > x ? y : x; });
-            if (lane == 0) tmax[((size_t)t * n_head + hh) * n_tiles + tile] = m;
         }
     }
 }
@@ -1555,11 +1587,14 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
         }
         {
             const int ih = (int)n_head, ikv = (int)n_head_kv, ihd = (int)head_dim;
-            const int ictx = (int)n_ctx;
+            const int ictx = (int)n_ctx, iM = (int)M;
+            const int tpw = SC_TPW;
             void *args[] = {(void *)&q, (void *)&qs, (void *)&k_cache, (void *)&ih, (void *)&ikv,
                             (void *)&ihd, (void *)&pos, (void *)&ictx, (void *)&att_stride,
-                            (void *)&att, (void *)&tmax, (void *)&n_tiles};
-            hipError_t e = hipLaunchKernel(sk, dim3((unsigned)n_tiles, (unsigned)n_head_kv, (unsigned)M),
+                            (void *)&att, (void *)&tmax, (void *)&n_tiles, (void *)&iM,
+                            (void *)&tpw};
+            hipError_t e = hipLaunchKernel(sk, dim3((unsigned)n_tiles, (unsigned)n_head_kv,
+                                                    (unsigned)((M + tpw - 1) / tpw)),
                                            dim3(256), args, lds, ctx->stream);
             if (e != hipSuccess) return fox_hip_fail(e, "attention scores");
         }
