@@ -39,7 +39,12 @@ __host__ __device__ constexpr int pf_of(int R4, int epi2)
 {
     return epi2 * R4 < 4 ? 4 : epi2 * R4 > 8 ? 8 : epi2 * R4;
 }
-#define FUSED_LDS_MAX (96 * 1024)
+// LDS per workgroup: two workgroups share a compute unit up to two tokens,
+// one has it alone from three on (fused_go_r)
+__host__ __device__ constexpr int fused_lds_max(size_t M)
+{
+    return M > 2 ? 160 * 1024 : 96 * 1024;
+}
 
 enum { IN_Q = 0, IN_F32 = 1, IN_NORM = 2 };
 enum { EPI_STORE = 0, EPI_ROPE = 1, EPI_SILU = 2, EPI_SUMS = 3 };
@@ -1416,7 +1421,7 @@ static fox_gpu_status fused_check(int type, size_t K, size_t M, int nslab, int *
                         "one workgroup holds", K, 4 * R4_LIMIT * FWG);
     if (M == 0 || M > FOX_GPU_MAX_TOKENS)
         return fox_fail(FOX_GPU_ERR_ARG, "fused gemv: 1 to %d tokens", FOX_GPU_MAX_TOKENS);
-    if (fused_lds(*fmt, (int)K, (int)M, nslab).total > FUSED_LDS_MAX)
+    if (fused_lds(*fmt, (int)K, (int)M, nslab).total > fused_lds_max(M))
         return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "fused gemv: %zu x %zu activations exceed the "
                         "workgroup's LDS", M, K);
     return FOX_GPU_OK;
@@ -1519,7 +1524,7 @@ fox_gpu_status fox_fused_gemv(fox_gpu_ctx *ctx, size_t n, const fox_gpu_tensor *
     const int f = fmt_of(ws[0]->type);
     if (f < 0 || (f != FMT_TQ2 && (M != 1 || q || sums)))
         return FOX_GPU_ERR_UNSUPPORTED;
-    if (fused_lds(f, (int)K, (int)M, 1).total > FUSED_LDS_MAX ||
+    if (fused_lds(f, (int)K, (int)M, 1).total > fused_lds_max(M) ||
         K > 4 * R4_LIMIT * FWG || !fused_aligned(x ? (const void *)x : (const void *)q,
                                              x ? x_stride : K, M, nullptr))
         return FOX_GPU_ERR_UNSUPPORTED;
@@ -1628,7 +1633,7 @@ extern "C" fox_gpu_status fox_gpu_qkv_rope(fox_gpu_ctx *ctx, const fox_gpu_tenso
     auto kq = [](int f) { return f == FMT_Q4K || f == FMT_Q6K; };
     int q6_mask = 0;
     if (kq(fmt) && kq(fmt_k) && kq(fmt_v) && (fmt != fmt_k || fmt != fmt_v)) {
-        if (fused_lds(FMT_KQMIX, (int)K, 1, 1).total > FUSED_LDS_MAX)
+        if (fused_lds(FMT_KQMIX, (int)K, 1, 1).total > fused_lds_max(1))
             return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "qkv_rope: K too large for one launch");
         q6_mask = (fmt == FMT_Q6K) | (fmt_k == FMT_Q6K) << 1 | (fmt_v == FMT_Q6K) << 2;
         fmt = fmt_v = FMT_KQMIX;

@@ -21,7 +21,7 @@ def ref_norm_gemv(oracle, gtype, x, nw, W, N, K):
 
 @pytest.mark.parametrize("tname,gtype", [("TQ1_0", 34), ("TQ2_0", 35)])
 @pytest.mark.parametrize("K,M,accumulate", [(2560, 1, False), (4096, 1, True), (768, 3, False),
-                                            (512, 8, True)])
+                                            (512, 8, True), (9728, 8, False), (4096, 2, True)])
 def test_gemv_rmsnorm_bit_exact(gpu, oracle, tname, gtype, K, M, accumulate):
     rng = np.random.default_rng(K * 10 + M)
     Ns = [48, 37]
@@ -128,8 +128,9 @@ def test_gemv_rmsnorm_nonfinite_follows_the_reference(gpu, oracle, gtype):
 
 def test_unsupported_cases_say_so(gpu):
     """K-quants for more than one token, and activations too wide for one
-    workgroup, are refused with FOX_GPU_ERR_UNSUPPORTED (the host then runs
-    the separate steps)."""
+    workgroup's LDS (16384 x 8 tokens: B operand and terms above 160 KB), are
+    refused with FOX_GPU_ERR_UNSUPPORTED (the host then runs the separate
+    steps)."""
     rng = np.random.default_rng(3)
     q4 = gpu.tensor(12, 512, 16, weights(rng, 12, 16, 512))
     x = gpu.array(rng.standard_normal((2, 512)).astype(np.float32))
@@ -138,7 +139,7 @@ def test_unsupported_cases_say_so(gpu):
     with pytest.raises(rf.FoxError) as e:
         gpu.gemv_rmsnorm([q4], x, 2, nw, EPS, [out])
     assert e.value.status == 5
-    K = 9728
+    K = 16384
     t = gpu.tensor(34, K, 16, weights(rng, 34, 16, K))
     xw = gpu.array(rng.standard_normal((8, K)).astype(np.float32))
     with pytest.raises(rf.FoxError) as e:

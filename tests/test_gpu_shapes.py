@@ -16,9 +16,10 @@ Shapes: the single-op microbenchmark (TQ1_0/TQ2_0 14336 x 4096, M = 1 and
 2048+, gate/up 2560 -> 9728, ffn_down 9728 -> 2560 and attn_output 4096 ->
 2560 with the residual add), the 8B-class layer's Q4_K/Q6_K matrices
 (14336 x 4096, 4096 x 14336) and the 27B-class layer's TQ1_0 ffn_down
-(21504 -> 5376: the fused path for one token; for 8 tokens the int8 input
-no longer fits one workgroup's LDS and the unfused path runs) and its
-8-token pass at d_model 5376.
+(21504 -> 5376: the fused path for one token and for 8, where one
+workgroup per compute unit has up to 160 KB of LDS; K = 24576 is past the
+fused kernel's input registers and takes the unfused path) and its 8-token
+pass at d_model 5376.
 """
 import numpy as np
 import pytest
@@ -160,11 +161,13 @@ def test_4b_qkv_rope_bit_exact(capped, oracle, M, pos, cap):
                                         ("attn_output 4b", 2560, 4096, 1),
                                         ("attn_output 4b", 2560, 4096, 8),
                                         ("ffn_down 27b", 5376, 21504, 1),
-                                        ("ffn_down 27b", 5376, 21504, 8)])
+                                        ("ffn_down 27b", 5376, 21504, 8),
+                                        ("K past the fused limit", 1024, 24576, 8)])
 def test_residual_projections_bit_exact(capped, oracle, name, N, K, M, cap):
     """out += W x (the residual add fused into the GEMV, src/forward.c:374-377,
-    393-396).  K = 21504 with 8 tokens takes the unfused path (quantiser
-    kernel over block slices, then the block kernel)."""
+    393-396).  K = 24576 is more than the fused kernel's input registers hold
+    (22528) and takes the unfused path (quantiser kernel over block slices,
+    then the block kernel)."""
     print(f"case {name} N={N} K={K} M={M} cap={cap}", flush=True)
     rng = np.random.default_rng([N, K, M, 13])
     w = weights(rng, 34, N, K)
