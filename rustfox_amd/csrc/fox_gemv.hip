@@ -26,7 +26,12 @@
 #include <cstring>
 #include <new>
 
-#define WAVES 4
+// waves of the unfused block kernel: a wave's blocks run one after another,
+// each waiting for its loads, so more waves per tile keep more loads in
+// flight (8 tokens: TQ1_0 5376 x 21504 48.3 -> 35.7 us, 4096 x 14336 30.5 ->
+// 21.7 us, Q6_K 4096 x 14336 151 -> 93 us with 8 waves against 4; Q4_K
+// 14336 x 4096 53.4 -> 56.8 us; 16 waves were slower at 21504)
+#define WAVES 8
 #define WG (WAVES * 64)
 
 // ---------------------------------------------------- activation prep
