@@ -73,8 +73,21 @@ __global__ __launch_bounds__(512) void act_prep(const float *__restrict__ x, int
         }
     } else if (!per_block) {
         const float *xt = x + (size_t)t * x_stride;
+        // (eight reads in flight per thread: one at a time, the K / 512
+        // dependent round trips of a 21504-wide token took 14 us)
         float m = 0.0f;
-        for (int i = tid; i < K; i += nthr) {
+        int i = tid;
+        for (; i + 7 * nthr < K; i += 8 * nthr) {
+            float a[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) a[k] = xt[i + k * nthr];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const float v = fabsf(a[k]);
+                if (v > m) m = v;
+            }
+        }
+        for (; i < K; i += nthr) {
             float a = fabsf(xt[i]);
             if (a > m) m = a;
         }
