@@ -52,6 +52,7 @@ CASES = [
     ("TQ1_0", 16, 256, 1), ("TQ1_0", 37, 512, 1), ("TQ1_0", 100, 2560, 3),
     ("TQ1_0", 4096, 4096, 1), ("TQ1_0", 1024, 9728, 8), ("TQ1_0", 333, 768, 5),
     ("TQ2_0", 37, 512, 1), ("TQ2_0", 4096, 4096, 1), ("TQ2_0", 130, 1280, 8),
+    ("TQ2_0", 200, 4096, 7), ("TQ1_0", 48, 1024, 2), ("TQ2_0", 40, 5376, 6),
     ("Q4_K", 33, 768, 1), ("Q4_K", 512, 4096, 2), ("Q4_K", 64, 2048, 8),
     ("Q6_K", 29, 512, 1), ("Q6_K", 300, 4096, 3), ("Q6_K", 48, 1024, 8),
     ("F16", 50, 288, 1), ("F16", 1000, 2560, 2), ("F16", 7, 8, 1), ("F16", 257, 1000, 8),
