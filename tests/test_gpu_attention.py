@@ -71,6 +71,8 @@ CASES = [  # n_head, n_kv, hd, n_ctx, pos, M
     (32, 8, 128, 2200, 2048, 1),   # 4B/8B heads past 2048 rows: 33 score tiles a kv head
     (32, 8, 128, 4200, 4150, 1),   # 66 tiles a kv head
     (32, 16, 128, 700, 699, 1),    # 27B heads, 16 kv heads, near the last row
+    (8, 2, 128, 200, 127, 5),      # 5 tokens: a score tile first reached by the second token
+    (16, 4, 64, 300, 250, 7),      # 7 tokens: four to a score workgroup, then three
 ]
 
 
