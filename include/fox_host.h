@@ -66,7 +66,7 @@ fox_threadpool *fox_threadpool_create(int n_threads);
 void            fox_threadpool_destroy(fox_threadpool *tp);
 int             fox_threadpool_size(const fox_threadpool *tp);
 /* include/fox/fox.h:335-338: fn(ctx, 0, 0, n) on the calling thread (no CPU
- * workers in this build; the reference's NULL-pool behaviour) */
+ * workers in this library; the reference's NULL-pool behaviour) */
 typedef void (*fox_parallel_fn)(void *ctx, int worker, size_t begin, size_t end);
 fox_status      fox_parallel_for(fox_threadpool *tp, size_t n, fox_parallel_fn fn, void *ctx);
 

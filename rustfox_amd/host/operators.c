@@ -47,7 +47,7 @@ int fox_threadpool_size(const fox_threadpool *tp) { return tp ? tp->n_threads : 
 
 /* include/fox/fox.h:337-338.  A caller's own host callback runs on the
  * calling thread over the whole range, every index once (the reference's
- * NULL-pool behaviour, src/threadpool.c:157-160): this build has no CPU
+ * NULL-pool behaviour, src/threadpool.c:157-160): this library has no CPU
  * worker threads; its kernels spread work over the launch grid instead. */
 fox_status fox_parallel_for(fox_threadpool *tp, size_t n, fox_parallel_fn fn, void *ctx)
 {
@@ -187,7 +187,7 @@ static fox_status gemv_f32(fox_ggml_type type, const float *x, const void *w, si
     void *dx, *dout;
     if ((st = check_gemv(x, w, rows, cols, out)) != FOX_OK) return st;
     if (!fox_gemv_supports(type))
-        return fox_fail(FOX_ERR_UNSUPPORTED, "gemv: no device kernel for %s; this build "
+        return fox_fail(FOX_ERR_UNSUPPORTED, "gemv: no device kernel for %s; this library "
                         "handles F32, F16, Q4_K, Q6_K, TQ1_0 and TQ2_0",
                         fox_ggml_type_name(type));
     if (fox_row_bytes(type, cols) == 0) return ragged(cols, type);

@@ -110,7 +110,7 @@ fox_status fox_sampler_pick(fox_sampler *s, const float *logits, uint32_t *out)
 
     if (!s || !logits || !out) return FOX_ERR_ARG;
     if (!s->greedy)
-        return fox_fail(FOX_ERR_UNSUPPORTED, "sampler: this build decodes greedily; set "
+        return fox_fail(FOX_ERR_UNSUPPORTED, "sampler: this library decodes greedily; set "
                         "temperature <= 0 (stochastic sampling is not provided)");
     top = s->penalty > 1.0f && s->count[0] ? penalised(logits[0], s->count[0], s->penalty)
                                            : logits[0];
