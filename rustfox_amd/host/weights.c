@@ -35,6 +35,7 @@
 #include "fox_host_internal.h"
 
 #include <fcntl.h>
+#include <pthread.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -69,6 +70,83 @@ static fox_status read_bytes(fox_weights *w, const fox_tensor_desc *t, uint8_t *
 }
 
 /* ------------------------------------------------------------ streaming */
+
+/* A layer's bytes are read by up to STREAM_READERS threads: one thread moves
+ * about 10-15 GB/s out of the page cache, less than the upload to HBM
+ * takes.  The layer's tensors are one list of (file offset, destination,
+ * size) segments; thread k reads bytes [k, k + 1) x total / n of their
+ * concatenation. */
+#define STREAM_READERS 4
+#define STREAM_READ_MIN (4u << 20)      /* bytes per reader at least */
+
+typedef struct {
+    uint64_t at, size;
+    uint8_t *dst;
+} read_seg;
+
+typedef struct {
+    int fd;
+    const read_seg *seg;
+    int nseg;
+    uint64_t b0, b1;                    /* byte range of the concatenation */
+    int failed;
+} read_part;
+
+static void *read_part_run(void *arg)
+{
+    read_part *p = (read_part *)arg;
+    uint64_t base = 0;
+    int i;
+    for (i = 0; i < p->nseg && base < p->b1; base += p->seg[i].size, i++) {
+        const uint64_t s0 = base > p->b0 ? base : p->b0;
+        const uint64_t e = base + p->seg[i].size, s1 = e < p->b1 ? e : p->b1;
+        uint64_t done = 0;
+        if (s1 <= s0) continue;
+        while (done < s1 - s0) {
+            const uint64_t left = s1 - s0 - done;
+            const size_t chunk = left > (1u << 30) ? (1u << 30) : (size_t)left;
+            const uint64_t o = s0 - base + done;
+            ssize_t got = pread(p->fd, p->seg[i].dst + o, chunk, (off_t)(p->seg[i].at + o));
+            if (got <= 0) {
+                p->failed = 1;
+                return NULL;
+            }
+            done += (uint64_t)got;
+        }
+    }
+    return NULL;
+}
+
+static fox_status read_segments(fox_weights *w, const read_seg *seg, int nseg)
+{
+    uint64_t total = 0;
+    read_part part[STREAM_READERS];
+    pthread_t th[STREAM_READERS];
+    int started[STREAM_READERS] = {0};
+    int n, k, failed = 0;
+    for (k = 0; k < nseg; k++) total += seg[k].size;
+    n = (int)(total / STREAM_READ_MIN);
+    n = n < 1 ? 1 : n > STREAM_READERS ? STREAM_READERS : n;
+    for (k = 0; k < n; k++) {
+        part[k].fd = w->fd;
+        part[k].seg = seg;
+        part[k].nseg = nseg;
+        part[k].b0 = total * (uint64_t)k / (uint64_t)n;
+        part[k].b1 = total * (uint64_t)(k + 1) / (uint64_t)n;
+        part[k].failed = 0;
+    }
+    /* parts 1.. on their own threads (a part whose thread cannot start is
+     * read here), part 0 on this one */
+    for (k = 1; k < n; k++)
+        started[k] = pthread_create(&th[k], NULL, read_part_run, &part[k]) == 0;
+    read_part_run(&part[0]);
+    for (k = 1; k < n; k++) {
+        if (started[k]) pthread_join(th[k], NULL);
+        else read_part_run(&part[k]);
+    }
+    for (k = 0; k < n; k++) failed |= part[k].failed;
+    return failed ? fox_fail(FOX_ERR_IO, "weights: short read while streaming a layer") : FOX_OK;
+}
 
 /* which layer and role each tensor plays ("blk.<l>.<role>.weight") */
 static fox_status map_layers(fox_weights *w)
@@ -237,10 +315,16 @@ static fox_status stream_in(fox_weights *w, uint32_t l, fox_layer_slot **out)
     if (w->staged_set[b] && (gs = fox_gpu_event_sync(w->staged[b])) != FOX_GPU_OK)
         return fox_gpu_failed(gs, "weights: staging");
     pin = w->pinned[b];
-    for (r = 0; r < FOX_LAYER_ROLES; r++) {
-        const fox_tensor_desc *t = &w->g->tensors[w->lt[(size_t)l * FOX_LAYER_ROLES + r]];
-        if ((st = read_bytes(w, t, pin + off)) != FOX_OK) return st;
-        off += t->size_bytes;
+    {
+        read_seg seg[FOX_LAYER_ROLES];
+        for (r = 0; r < FOX_LAYER_ROLES; r++) {
+            const fox_tensor_desc *t = &w->g->tensors[w->lt[(size_t)l * FOX_LAYER_ROLES + r]];
+            seg[r].at = w->g->data_offset + t->offset;
+            seg[r].size = t->size_bytes;
+            seg[r].dst = pin + off;
+            off += t->size_bytes;
+        }
+        if ((st = read_segments(w, seg, FOX_LAYER_ROLES)) != FOX_OK) return st;
     }
     /* the copy stream overwrites the slot after the compute stream's last
      * queued use of its old layer */
