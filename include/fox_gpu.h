@@ -143,13 +143,19 @@ void           fox_gpu_tensor_free(fox_gpu_ctx *ctx, fox_gpu_tensor *t);
  * from `host` (pinned memory from fox_gpu_host_alloc, left untouched until
  * the copy stream has passed this call) into `dev_stage` (device memory of
  * at least `bytes`, reused only in copy-stream order) and repack them into
- * t's device layout.  Nothing waits: order it against compute-stream users
- * of t with events. */
+ * t's device layout; with `host` NULL the bytes are already in `dev_stage`
+ * (fox_gpu_stage_async) and only the repack runs.  Nothing waits: order it
+ * against compute-stream users of t with events.
+ * fox_gpu_stage_async: on the copy stream, copy `bytes` from pinned `host`
+ * memory to device memory `dev` (a streamed layer's tensors in one copy,
+ * then one repack each; src/weights.c:314-459 reads a layer into its slot). */
 fox_gpu_status fox_gpu_tensor_alloc(fox_gpu_ctx *ctx, int type, uint64_t ne0,
                                     uint64_t ne1, fox_gpu_tensor **out);
 fox_gpu_status fox_gpu_tensor_load_async(fox_gpu_ctx *ctx, fox_gpu_tensor *t,
                                          const void *host, uint64_t bytes,
                                          void *dev_stage);
+fox_gpu_status fox_gpu_stage_async(fox_gpu_ctx *ctx, void *dev, const void *host,
+                                   uint64_t bytes);
 fox_gpu_status fox_gpu_host_alloc(fox_gpu_ctx *ctx, size_t bytes, void **out);
 fox_gpu_status fox_gpu_host_free(fox_gpu_ctx *ctx, void *p);
 

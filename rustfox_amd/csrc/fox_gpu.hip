@@ -689,14 +689,14 @@ extern "C" fox_gpu_status fox_gpu_tensor_load_async(fox_gpu_ctx *ctx, fox_gpu_te
                                                     const void *host, uint64_t bytes,
                                                     void *dev_stage)
 {
-    if (!ctx || !t || !host || !dev_stage)
+    if (!ctx || !t || !dev_stage)
         return fox_fail(FOX_GPU_ERR_ARG, "tensor_load_async: bad argument");
     if (bytes != t->gguf_bytes)
         return fox_fail(FOX_GPU_ERR_ARG, "tensor_load_async: %s %llux%llu is %llu bytes, %llu "
                         "were given", fox_type_name(t->type), (unsigned long long)t->ne0,
                         (unsigned long long)t->ne1, (unsigned long long)t->gguf_bytes,
                         (unsigned long long)bytes);
-    FOX_HIP(hipMemcpyAsync(dev_stage, host, bytes, hipMemcpyHostToDevice, ctx->copy));
+    if (host) FOX_HIP(hipMemcpyAsync(dev_stage, host, bytes, hipMemcpyHostToDevice, ctx->copy));
     const uint8_t *src = (const uint8_t *)dev_stage;
     if (!fox_is_block_type(t->type)) {
         const uint64_t es = fox_block_bytes(t->type), n = t->dev_bytes / es;
@@ -718,6 +718,15 @@ extern "C" fox_gpu_status fox_gpu_tensor_load_async(fox_gpu_ctx *ctx, fox_gpu_te
                            t->dev_bytes);
     }
     FOX_LAUNCHED("tensor_load_async");
+    return FOX_GPU_OK;
+}
+
+extern "C" fox_gpu_status fox_gpu_stage_async(fox_gpu_ctx *ctx, void *dev, const void *host,
+                                              uint64_t bytes)
+{
+    if (!ctx || !dev || !host) return fox_fail(FOX_GPU_ERR_ARG, "stage_async: bad argument");
+    if (bytes == 0) return FOX_GPU_OK;
+    FOX_HIP(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, ctx->copy));
     return FOX_GPU_OK;
 }
 

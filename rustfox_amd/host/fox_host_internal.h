@@ -100,13 +100,16 @@ struct fox_weights {
     size_t           *lt;            /* tensor index of (layer, role): lt[l * ROLES + r] */
     uint32_t          n_layer;
     uint64_t          layer_bytes;   /* GGUF bytes of one layer */
+    uint64_t          stage_off[FOX_LAYER_ROLES]; /* a layer's tensors in the staging
+                                                     buffers (256-byte aligned) */
+    uint64_t          stage_bytes;   /* staging bytes of one layer */
     fox_layer_slot   *slots;
     int               n_slots;
     uint8_t          *pinned[2];     /* host staging of one layer, alternating */
     fox_gpu_event    *staged[2];     /* copy stream: done reading pinned[i] */
     int               staged_set[2];
     int               next_pin;
-    void             *dev_stage;     /* device staging of one tensor's GGUF bytes */
+    void             *dev_stage;     /* device staging of one layer's GGUF bytes */
     uint64_t          clock, evictions;
 };
 

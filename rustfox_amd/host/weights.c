@@ -211,7 +211,7 @@ static fox_status map_layers(fox_weights *w)
 static fox_status open_stream(fox_weights *w)
 {
     const fox_gguf *g = w->g;
-    uint64_t outside = 0, largest = 0;
+    uint64_t outside = 0;
     size_t i;
     int s, r;
     fox_status st;
@@ -220,7 +220,13 @@ static fox_status open_stream(fox_weights *w)
     if ((st = map_layers(w)) != FOX_OK) return st;
     for (i = 0; i < g->n_tensors; i++) {
         if (w->layer_of[i] < 0) outside += g->tensors[i].size_bytes;
-        if (g->tensors[i].size_bytes > largest) largest = g->tensors[i].size_bytes;
+    }
+    /* a layer's tensors at 256-byte aligned places of the staging buffers:
+     * each is repacked on the device from its own place */
+    w->stage_bytes = 0;
+    for (r = 0; r < FOX_LAYER_ROLES; r++) {
+        w->stage_off[r] = w->stage_bytes;
+        w->stage_bytes += (g->tensors[w->lt[r]].size_bytes + 255) & ~(uint64_t)255;
     }
     if (w->budget == 0) {
         w->n_slots = (int)w->n_layer;
@@ -250,10 +256,10 @@ static fox_status open_stream(fox_weights *w)
         if (gs == FOX_GPU_OK) gs = fox_gpu_event_create(w->gpu, &sl->used);
     }
     for (i = 0; i < 2 && gs == FOX_GPU_OK; i++) {
-        gs = fox_gpu_host_alloc(w->gpu, (size_t)w->layer_bytes, (void **)&w->pinned[i]);
+        gs = fox_gpu_host_alloc(w->gpu, (size_t)w->stage_bytes, (void **)&w->pinned[i]);
         if (gs == FOX_GPU_OK) gs = fox_gpu_event_create(w->gpu, &w->staged[i]);
     }
-    if (gs == FOX_GPU_OK) gs = fox_gpu_malloc(w->gpu, (size_t)largest, &w->dev_stage);
+    if (gs == FOX_GPU_OK) gs = fox_gpu_malloc(w->gpu, (size_t)w->stage_bytes, &w->dev_stage);
     if (gs != FOX_GPU_OK) return fox_gpu_failed(gs, "weights: streaming buffers");
     return FOX_OK;
 }
@@ -291,7 +297,6 @@ static fox_status stream_in(fox_weights *w, uint32_t l, fox_layer_slot **out)
 {
     fox_layer_slot *sl = slot_of(w, l), *victim = NULL;
     uint8_t *pin;
-    uint64_t off = 0;
     fox_gpu_status gs = FOX_GPU_OK;
     fox_status st;
     int s, r, b;
@@ -321,20 +326,20 @@ static fox_status stream_in(fox_weights *w, uint32_t l, fox_layer_slot **out)
             const fox_tensor_desc *t = &w->g->tensors[w->lt[(size_t)l * FOX_LAYER_ROLES + r]];
             seg[r].at = w->g->data_offset + t->offset;
             seg[r].size = t->size_bytes;
-            seg[r].dst = pin + off;
-            off += t->size_bytes;
+            seg[r].dst = pin + w->stage_off[r];
         }
         if ((st = read_segments(w, seg, FOX_LAYER_ROLES)) != FOX_OK) return st;
     }
     /* the copy stream overwrites the slot after the compute stream's last
      * queued use of its old layer */
     if (victim->used_set) gs = fox_gpu_event_wait(w->gpu, victim->used, 1);
-    off = 0;
+    /* the layer's bytes in one copy (one long transfer instead of nine),
+     * then each tensor repacked from its place in the staging buffer */
+    if (gs == FOX_GPU_OK) gs = fox_gpu_stage_async(w->gpu, w->dev_stage, pin, w->stage_bytes);
     for (r = 0; r < FOX_LAYER_ROLES && gs == FOX_GPU_OK; r++) {
         const fox_tensor_desc *t = &w->g->tensors[w->lt[(size_t)l * FOX_LAYER_ROLES + r]];
-        gs = fox_gpu_tensor_load_async(w->gpu, victim->t[r], pin + off, t->size_bytes,
-                                       w->dev_stage);
-        off += t->size_bytes;
+        gs = fox_gpu_tensor_load_async(w->gpu, victim->t[r], NULL, t->size_bytes,
+                                       (uint8_t *)w->dev_stage + w->stage_off[r]);
     }
     if (gs == FOX_GPU_OK) gs = fox_gpu_event_record_copy(w->gpu, w->staged[b]);
     if (gs == FOX_GPU_OK) gs = fox_gpu_event_record_copy(w->gpu, victim->ready);
