@@ -29,10 +29,12 @@
 // waves of the unfused block kernel: a wave's blocks run one after another,
 // each waiting for its loads, so more waves per tile keep more loads in
 // flight (8 tokens: TQ1_0 5376 x 21504 48.3 -> 35.7 us, 4096 x 14336 30.5 ->
-// 21.7 us, Q6_K 4096 x 14336 151 -> 93 us with 8 waves against 4; Q4_K
-// 14336 x 4096 53.4 -> 56.8 us; 16 waves were slower at 21504)
-#define WAVES 8
-#define WG (WAVES * 64)
+// 21.7 us, Q6_K 4096 x 14336 151 -> 93 us with 8 waves against 4; 16 waves
+// were slower at 21504).  Q4_K keeps 4 (14336 x 4096: 53.4 us, 56.8 with 8).
+__host__ __device__ constexpr int blk_waves(int fmt)
+{
+    return fmt == FMT_Q4K ? 4 : 8;
+}
 
 // ---------------------------------------------------- activation prep
 
@@ -375,11 +377,10 @@ __device__ __forceinline__ void gemv_block(const uint8_t *__restrict__ ch, int b
 }
 
 template <int FMT>
-__global__ __launch_bounds__(WG) void gemv_blocks(Segs segs, int nb, int M, int chunk_blocks,
-                                                 const uint8_t *__restrict__ B,
-                                                 const int32_t *__restrict__ aux,
-                                                 const float *__restrict__ scale,
-                                                 unsigned flags, int32_t *__restrict__ sums)
+__global__ __launch_bounds__(blk_waves(FMT) * 64) void gemv_blocks(
+    Segs segs, int nb, int M, int chunk_blocks, const uint8_t *__restrict__ B,
+    const int32_t *__restrict__ aux, const float *__restrict__ scale, unsigned flags,
+    int32_t *__restrict__ sums)
 {
     extern __shared__ float terms[];  // [chunk_blocks][T][16][M]
     constexpr int T = terms_per_block(FMT);
@@ -398,7 +399,7 @@ __global__ __launch_bounds__(WG) void gemv_blocks(Segs segs, int nb, int M, int 
 
     for (int c0 = 0; c0 < nb; c0 += chunk_blocks) {
         const int c1 = c0 + chunk_blocks < nb ? c0 + chunk_blocks : nb;
-        for (int b = c0 + wave; b < c1; b += WAVES)
+        for (int b = c0 + wave; b < c1; b += blk_waves(FMT))
             gemv_block<FMT>(wt + (size_t)b * CHUNK, b, nb, M, lane, B, aux, scale,
                             terms + (size_t)(b - c0) * T * 16 * M, sums, tile * 16, n_rows);
         if (sums) continue;
@@ -625,11 +626,12 @@ static fox_gpu_status launch_blocks(fox_gpu_ctx *ctx, int fmt, const Segs &sg, i
 {
     const int T = terms_per_block(fmt);
     int chunk_blocks = (int)(65536 / ((size_t)T * 16 * M * 4));
-    chunk_blocks = chunk_blocks / WAVES * WAVES;
-    if (chunk_blocks < WAVES) chunk_blocks = WAVES;
+    const int waves = blk_waves(fmt);
+    chunk_blocks = chunk_blocks / waves * waves;
+    if (chunk_blocks < waves) chunk_blocks = waves;
     if (chunk_blocks > nb) chunk_blocks = nb;
     size_t lds = sums ? 0 : (size_t)chunk_blocks * T * 16 * M * 4;
-    dim3 grid((unsigned)tiles), block(WG);
+    dim3 grid((unsigned)tiles), block(waves * 64);
     switch (fmt) {
     case FMT_TQ2:
         hipLaunchKernelGGL(gemv_blocks<FMT_TQ2>, grid, block, lds, ctx->stream, sg, nb, M,
