@@ -399,6 +399,16 @@ __host__ __device__ constexpr int tg_of(int R4)
     return R4 <= 2 ? 2 : 1;
 }
 
+// from three tokens on a workgroup has its compute unit alone (two waves per
+// SIMD), so a group may hold more tokens, loaded once per group instead of
+// double-buffered: up to four tokens, 8 float4 of input per thread (16, up
+// to eight tokens, spilled in the norm-input kernels and ran slower at three
+// and four tokens)
+__host__ __device__ constexpr int tg_big(int R4)
+{
+    return 8 / R4 > 4 ? 4 : 8 / R4 < 1 ? 1 : 8 / R4;
+}
+
 template <int R4MAX, int TG>
 struct InGrp {
     float4 xv[TG][R4MAX];
@@ -999,16 +1009,17 @@ __device__ __forceinline__ T pick4(const T *v, int s)
     return r;
 }
 
-// MT: more than one token (the later tokens' input stages are pipelined; a
-// separate instantiation keeps the one-token kernels' registers as they are)
-template <int FMT, int IN, int EPI, int R4, bool MT>
+// MT: 0 one token; 1 two tokens (input in pairs, the next pair in flight);
+// 2 three or more (one workgroup per compute unit, larger groups).  Separate
+// instantiations keep the one-token kernels' registers as they are.
+template <int FMT, int IN, int EPI, int R4, int MT>
 __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float *norm_in,
                                                  const int8_t *q_in, int nb_in, FusedArgs a)
 {
     extern __shared__ uint4 fused_lds4[];
     uint8_t *lds = (uint8_t *)fused_lds4;
     constexpr bool KQ = FMT != FMT_TQ2;                    // a K-quant (one token)
-    constexpr int TG = MT && !KQ ? tg_of(R4) : 1;          // tokens per input group
+    constexpr int TG = KQ ? 1 : MT == 2 ? tg_big(R4) : MT == 1 ? tg_of(R4) : 1;   // tokens per input group
     __shared__ double dred[FW * TG];
     __shared__ uint32_t ured[FW * TG];
     __shared__ float ascale[FOX_GPU_MAX_TOKENS];
@@ -1187,7 +1198,17 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     // (token 0 outside the loop: its waits then count the loads above)
     if constexpr (KQ) {
         quantise_kq<FMT, IN, R4>(a, K, (int8_t *)B, aux, bsc, dred, in);
-    } else if constexpr (MT) {
+    } else if constexpr (MT == 2) {
+        // the groups in turn (the first in flight since the start; a later
+        // group's loads go out once the group before is quantised)
+        for (int t0 = 0; t0 < M; t0 += TG) {
+            if (t0 > 0)
+                load_group<IN, R4, TG>(x_in, norm_in, q_in, a.x_stride, t0, min(M - t0, TG), K,
+                                       false, in);
+            quantise_group<FMT, IN, R4, TG>(a, t0, min(M - t0, TG), K, B, aux, dred, ured,
+                                            ascale, in);
+        }
+    } else if constexpr (MT == 1) {
         // the groups in turn, the next one's input in flight while a group
         // is quantised (the first is in flight since the start)
         for (int t0 = 0; t0 < M; t0 += TG) {
@@ -1437,25 +1458,31 @@ static fox_gpu_status fused_go_r(fox_gpu_ctx *ctx, FusedArgs a, int n_work)
 {
     // (the K-quants have the one-token kernels only: fused_check)
     constexpr bool MT_OK = FMT == FMT_TQ2;
-    const bool mt = MT_OK && a.M > 1;
+    const int mt = MT_OK ? (a.M > 2 ? 2 : a.M > 1 ? 1 : 0) : 0;
     a.n_work = n_work;
-    int cap = (mt && a.M > 2 ? 1 : 2) * (ctx->n_cu > 0 ? ctx->n_cu : 1);
+    int cap = (mt == 2 ? 1 : 2) * (ctx->n_cu > 0 ? ctx->n_cu : 1);
     if (ctx->max_wg > 0 && ctx->max_wg < cap) cap = ctx->max_wg;
     const int grid = n_work < cap ? n_work : cap;
     a.n_per = n_work / grid;
     a.n_rem = n_work - a.n_per * grid;
     const size_t lds = fused_lds(FMT, a.nb * 256, a.M, EPI == EPI_SILU ? 2 : 1).total;
-    const void *k = mt ? (const void *)gemv_fused<FMT, IN, EPI, R4, MT_OK>
-                       : (const void *)gemv_fused<FMT, IN, EPI, R4, false>;
+    // (the multi-token kernels exist for the ternary formats only)
+    constexpr int MT1 = MT_OK ? 1 : 0, MT2 = MT_OK ? 2 : 0;
+    const void *k = mt == 2 ? (const void *)gemv_fused<FMT, IN, EPI, R4, MT2>
+                  : mt == 1 ? (const void *)gemv_fused<FMT, IN, EPI, R4, MT1>
+                            : (const void *)gemv_fused<FMT, IN, EPI, R4, 0>;
     if (lds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return fox_hip_fail(e, "fused gemv: LDS size");
     }
-    if (mt)
-        hipLaunchKernelGGL((gemv_fused<FMT, IN, EPI, R4, MT_OK>), dim3((unsigned)grid), dim3(FWG),
+    if (mt == 2)
+        hipLaunchKernelGGL((gemv_fused<FMT, IN, EPI, R4, MT2>), dim3((unsigned)grid), dim3(FWG),
+                           lds, ctx->stream, a.x, a.norm_w, a.q_in, a.nb, a);
+    else if (mt == 1)
+        hipLaunchKernelGGL((gemv_fused<FMT, IN, EPI, R4, MT1>), dim3((unsigned)grid), dim3(FWG),
                            lds, ctx->stream, a.x, a.norm_w, a.q_in, a.nb, a);
     else
-        hipLaunchKernelGGL((gemv_fused<FMT, IN, EPI, R4, false>), dim3((unsigned)grid), dim3(FWG),
+        hipLaunchKernelGGL((gemv_fused<FMT, IN, EPI, R4, 0>), dim3((unsigned)grid), dim3(FWG),
                            lds, ctx->stream, a.x, a.norm_w, a.q_in, a.nb, a);
     FOX_LAUNCHED("gemv_fused");
     return FOX_GPU_OK;
