@@ -73,6 +73,11 @@ CASES = [  # n_head, n_kv, hd, n_ctx, pos, M
     (32, 16, 128, 700, 699, 1),    # 27B heads, 16 kv heads, near the last row
     (8, 2, 128, 200, 127, 5),      # 5 tokens: a score tile first reached by the second token
     (16, 4, 64, 300, 250, 7),      # 7 tokens: four to a score workgroup, then three
+    # more than one round of softmax+values workgroups over 256 compute
+    # units: the softmax sums in a launch of their own, once per head
+    (32, 8, 128, 2200, 2048, 8),   # 4B/8B heads, 8 tokens: 512 workgroups
+    (32, 16, 128, 1100, 1000, 8),  # 27B heads, 8 tokens, gqa 2: 512 workgroups
+    (32, 8, 128, 300, 295, 5),     # 5 tokens up to the cache end: 320 workgroups
 ]
 
 
@@ -102,20 +107,24 @@ def test_attention_split_within_rounding(gpu, oracle, case):
     assert err < 1e-5, err
 
 
-def test_nan_first_score_follows_the_reference(gpu, oracle):
+@pytest.mark.parametrize("case", [(4, 2, 64, 40, 39, 1), (32, 8, 128, 300, 290, 8)],
+                         ids=["one_token", "sums_launch"])
+def test_nan_first_score_follows_the_reference(gpu, oracle, case):
     """src/ops.c:26-30: a NaN score at position 0 stays the maximum, so every
     weight of that head is NaN and the sum is not normalised; a NaN later in
-    the row is skipped by the maximum.  Other heads are unaffected."""
-    n_head, n_kv, hd, n_ctx, pos, M = 4, 2, 64, 40, 39, 1
+    the row is skipped by the maximum.  Other heads are unaffected.  The
+    second case runs the softmax sums in a launch of their own."""
+    n_head, n_kv, hd, n_ctx, pos, M = case
     rng = np.random.default_rng(5)
     q = (rng.standard_normal((M, n_head * hd)) * 0.3).astype(np.float32)
     K = rng.standard_normal((n_ctx, n_kv * hd)).astype(np.float32)
     V = rng.standard_normal((n_ctx, n_kv * hd)).astype(np.float32)
-    K[0, 0] = np.nan            # kv head 0: heads 0, 1 get a NaN first score
+    K[0, 0] = np.nan            # kv head 0: its query heads get a NaN first score
     got = run_gpu(gpu, q, K, V, n_head, n_kv, hd, pos, M, n_ctx, rf.ATTN_EXACT)
     want = reference_attention(oracle, q, K, V, n_head, n_kv, hd, pos, M, n_ctx)
-    assert np.isnan(want[0, :2 * hd]).all() and np.isnan(got[0, :2 * hd]).all()
-    assert np.array_equal(got[0, 2 * hd:].view(np.uint32), want[0, 2 * hd:].view(np.uint32))
+    nh0 = (n_head // n_kv) * hd
+    assert np.isnan(want[:, :nh0]).all() and np.isnan(got[:, :nh0]).all()
+    assert np.array_equal(got[:, nh0:].view(np.uint32), want[:, nh0:].view(np.uint32))
 
 
 @pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[5]],
