@@ -21,7 +21,8 @@ def ref_norm_gemv(oracle, gtype, x, nw, W, N, K):
 
 @pytest.mark.parametrize("tname,gtype", [("TQ1_0", 34), ("TQ2_0", 35)])
 @pytest.mark.parametrize("K,M,accumulate", [(2560, 1, False), (4096, 1, True), (768, 3, False),
-                                            (512, 8, True), (9728, 8, False), (4096, 2, True)])
+                                            (512, 8, True), (9728, 8, False), (4096, 2, True),
+                                            (1536, 6, False), (1024, 7, True), (2560, 5, False)])
 def test_gemv_rmsnorm_bit_exact(gpu, oracle, tname, gtype, K, M, accumulate):
     rng = np.random.default_rng(K * 10 + M)
     Ns = [48, 37]
@@ -42,7 +43,7 @@ def test_gemv_rmsnorm_bit_exact(gpu, oracle, tname, gtype, K, M, accumulate):
 
 
 @pytest.mark.parametrize("gtype", [34, 35])
-@pytest.mark.parametrize("M,pos", [(1, 5), (3, 36), (2, 39)])
+@pytest.mark.parametrize("M,pos", [(1, 5), (3, 36), (2, 39), (5, 20), (7, 36), (8, 30)])
 def test_qkv_rope_bit_exact(gpu, oracle, gtype, M, pos):
     """q, k, v projections of rmsnorm(x), RoPE at pos + t, k and v rows into
     the caches; a token at or past n_ctx is neither rotated nor stored."""
@@ -85,7 +86,8 @@ def test_qkv_rope_bit_exact(gpu, oracle, gtype, M, pos):
 
 
 @pytest.mark.parametrize("gtype", [34, 35])
-@pytest.mark.parametrize("K,ff,M", [(2560, 700, 1), (768, 1040, 2), (512, 96, 8)])
+@pytest.mark.parametrize("K,ff,M", [(2560, 700, 1), (768, 1040, 2), (512, 96, 8), (768, 200, 5),
+                                     (2048, 64, 7), (4096, 130, 6)])
 def test_gate_up_silu_bit_exact(gpu, oracle, gtype, K, ff, M):
     rng = np.random.default_rng(K + ff + M + gtype)
     Wg, Wu = weights(rng, gtype, ff, K), weights(rng, gtype, ff, K)
