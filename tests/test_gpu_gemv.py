@@ -57,6 +57,7 @@ CASES = [
     ("Q6_K", 29, 512, 1), ("Q6_K", 300, 4096, 3), ("Q6_K", 48, 1024, 8),
     ("F16", 50, 288, 1), ("F16", 1000, 2560, 2), ("F16", 7, 8, 1), ("F16", 257, 1000, 8),
     ("F32", 9, 64, 1), ("F32", 300, 288, 4),
+    ("TQ1_0", 64, 2048, 6), ("TQ2_0", 96, 512, 7),      # input groups of four, then two or three
 ]
 
 
