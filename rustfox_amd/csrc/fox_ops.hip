@@ -825,7 +825,8 @@ __global__ __launch_bounds__(64) void attn_values_x(const float *__restrict__ at
 //     ring of LDS stages;
 //   wave 0: one lane per (head, column) adds the products in position order.
 // Stages are handed over with workgroup-scope release/acquire flags in LDS;
-// every wait is bounded (a wave that times out writes NaN and leaves).
+// every wait is bounded (a wave that times out writes NaN, sets its bit in the
+// device error word and leaves).
 #define SV_WAVES 16
 #define SV_QT 16                    // quads (4 positions) per stage
 #define SV_NP_MAX 8                 // product stages: as many as fit beside the weights
@@ -933,6 +934,13 @@ __device__ __forceinline__ bool sv_wait_ge_idle(int *flag, int v)
         __builtin_amdgcn_s_sleep(SV_IDLE_SLEEP);
     }
     return false;
+}
+
+// a timed-out wait reports itself in the device error word (read by the
+// host after the pass: fox_gpu_take_error)
+__device__ __forceinline__ void sv_error(unsigned *err, unsigned bit)
+{
+    __hip_atomic_fetch_or(err, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ void sv_signal(int *flag, int v)
@@ -1078,7 +1086,7 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
     const float *__restrict__ att, size_t att_stride, const float *__restrict__ tmax, int n_tiles,
     const float *__restrict__ vc, int n_head, int n_head_kv, int hd,
     const uint32_t *__restrict__ pos, int n_ctx, float *__restrict__ out, size_t out_stride,
-    int np, SvPrefetch pf)
+    int np, SvPrefetch pf, unsigned *err)
 {
     // the last pf.nwg workgroups of row 0 prefetch (the host adds them for
     // one token only); they use neither LDS nor barriers
@@ -1220,7 +1228,10 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
                 for (int j = p0 + 4 * nqk; j < p1; j++) sum = sum + er[j];
             }
         }
-        if (!eok) sum = __builtin_nanf("");
+        if (!eok) {
+            sum = __builtin_nanf("");
+            if (lane == 0) sv_error(err, FOX_DEV_ERR_ATTN_SUM);
+        }
         // a_j = e_j * (1/sum) is formed by the loaders (src/ops.c:35-38)
         if (lane < G) {
             nrm_s[lane] = sum > 0.0f;
@@ -1411,6 +1422,7 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
         if (!ok) {
             sv_signal(&consumed, 1 << 30);
             acc = __builtin_nanf("");
+            if (lane == 0 && eok) sv_error(err, FOX_DEV_ERR_ATTN_VALUES);
         }
         if (g < G && d < hd) out[(size_t)t * out_stride + (size_t)(kvh * G + g) * hd + d] = acc;
         return;
@@ -1422,7 +1434,10 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
     // NLD units of a tile come from NLD different loaders, the last of them
     // marks the tile ready, so that the first tile is ready after one unit
     // of work per loader.
-    if (!sv_wait_ge_idle(&a_ready, 1)) return;
+    if (!sv_wait_ge_idle(&a_ready, 1)) {
+        if (lane == 0) sv_error(err, FOX_DEV_ERR_ATTN_LOADER);
+        return;
+    }
     // a_j = e_j * (1/sum), or e_j where the sum is not positive
     // (src/ops.c:35-38; e * 1 is e exactly): the scale per head, and that of
     // the lane's own head for the DPP exchange below
@@ -1458,7 +1473,10 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
             for (int r = 0; r < RK; r++) wq[r] = ((const float4 *)(e + (DPPX ? mine : r) * estr))[jq];
             // the tile's stage is free once tile i - np is consumed
             if (i >= np && cons_seen < i - np + 1) {
-                if (!sv_wait_ge_idle(&consumed, i - np + 1)) return;
+                if (!sv_wait_ge_idle(&consumed, i - np + 1)) {
+                    if (lane == 0) sv_error(err, FOX_DEV_ERR_ATTN_LOADER);
+                    return;
+                }
                 cons_seen = i - np + 1;
             }
             for (st += i - st_i, st_i = i; st >= np;) st -= np;
@@ -1621,6 +1639,7 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
             // the attention leaves free (with more than half of a compute
             // unit's 160 KB of LDS, a workgroup has its compute unit alone)
             const int n_attn = (int)(n_head_kv * nsl);
+            unsigned *err = (unsigned *)(ctx->small + FOX_SMALL_ERR_OFF);
             pf.first = n_attn;
             pf.nwg = 0;
             if (M == 1 && pf.nreg > 0 && sv_lds > 80 * 1024 && ctx->n_cu > n_attn)
@@ -1628,7 +1647,7 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
             void *args[] = {(void *)&att, (void *)&att_stride, (void *)&tmax, (void *)&n_tiles,
                             (void *)&v_cache, (void *)&ih, (void *)&ikv, (void *)&ihd,
                             (void *)&pos, (void *)&ictx, (void *)&out, (void *)&os,
-                            (void *)&np, (void *)&pf};
+                            (void *)&np, (void *)&pf, (void *)&err};
             e = hipLaunchKernel(sv, dim3((unsigned)(n_attn + pf.nwg), (unsigned)M),
                                 dim3(SV_WAVES * 64), args, sv_lds, ctx->stream);
             if (e != hipSuccess) return fox_hip_fail(e, "attention softmax+values");
@@ -1712,10 +1731,15 @@ extern "C" fox_gpu_status fox_gpu_add(fox_gpu_ctx *ctx, float *dst, const float 
 
 // First index of the maximum, NaN never winning (src/sample.c:147-153:
 // best starts at 0 and moves only on a strict '>'; a NaN at index 0 stays).
-// Workgroups reduce contiguous ranges to (max, first index) partials; the
-// last workgroup to finish (a device-scope counter) merges them in index
-// order, applies the index-0 rule, writes the result and, for a decode loop,
-// the history entry and the advanced position, and resets the counter.
+// Two launches: argmax_part_k reduces contiguous ranges to (max, first
+// index) partials, one per workgroup; argmax_merge_k, one workgroup, merges
+// them in index order, applies the index-0 rule and writes the result and,
+// for a decode loop, the history entry and the advanced position.  The
+// partials cross a kernel boundary, as every other producer/consumer pair of
+// the decode does: a single launch whose last workgroup merged the others'
+// partials (a device-scope arrival counter, agent-scope relaxed stores and
+// loads) read a partial of the previous launch now and then, on a graph
+// replay, and picked the runner-up workgroup's maximum.
 #define AM_THREADS 256
 #define AM_MAX_WG 256
 #define AM_UNROLL 8
@@ -1728,18 +1752,28 @@ __device__ __forceinline__ void am_merge(float &best, int &bidx, float ov, int o
     }
 }
 
-__global__ __launch_bounds__(AM_THREADS) void argmax_k(const float *__restrict__ x, int n,
-                                                       int per, float *pv, int *pi,
-                                                       unsigned *counter,
-                                                       uint32_t *__restrict__ idx,
-                                                       uint32_t *__restrict__ pos,
-                                                       uint32_t advance,
-                                                       uint32_t *__restrict__ history)
+// (best, bidx) of the workgroup into thread 0's registers (NaN never taken)
+__device__ __forceinline__ void am_reduce_wg(float &best, int &bidx, float *bv, int *bi)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) am_merge(best, bidx, __shfl_xor(best, o), __shfl_xor(bidx, o));
+    if (lane == 0) {
+        bv[wave] = best;
+        bi[wave] = bidx;
+    }
+    __syncthreads();
+    if (tid == 0)
+        for (int w = 1; w < AM_THREADS / 64; w++) am_merge(best, bidx, bv[w], bi[w]);
+}
+
+__global__ __launch_bounds__(AM_THREADS) void argmax_part_k(const float *__restrict__ x, int n,
+                                                            int per, float *__restrict__ pv,
+                                                            int *__restrict__ pi)
 {
     __shared__ float bv[AM_THREADS / 64];
     __shared__ int bi[AM_THREADS / 64];
-    __shared__ int last;
-    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
+    const int tid = threadIdx.x;
     const int i0 = blockIdx.x * per, i1 = min(n, i0 + per);
     float best = -INFINITY;
     int bidx = 0x7fffffff;
@@ -1761,47 +1795,38 @@ __global__ __launch_bounds__(AM_THREADS) void argmax_k(const float *__restrict__
             }
         }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) am_merge(best, bidx, __shfl_xor(best, o), __shfl_xor(bidx, o));
-    if (lane == 0) {
-        bv[wave] = best;
-        bi[wave] = bidx;
-    }
-    __syncthreads();
+    am_reduce_wg(best, bidx, bv, bi);
     if (tid == 0) {
-        for (int w = 1; w < AM_THREADS / 64; w++) am_merge(best, bidx, bv[w], bi[w]);
-        __hip_atomic_store(&pv[blockIdx.x], best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&pi[blockIdx.x], bidx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned done = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-        last = done == gridDim.x - 1;
+        pv[blockIdx.x] = best;
+        pi[blockIdx.x] = bidx;
     }
-    __syncthreads();
-    if (!last) return;
-    best = -INFINITY;
-    bidx = 0x7fffffff;
-    for (int b = tid; b < (int)gridDim.x; b += AM_THREADS)
-        am_merge(best, bidx,
-                 __hip_atomic_load(&pv[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                 __hip_atomic_load(&pi[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) am_merge(best, bidx, __shfl_xor(best, o), __shfl_xor(bidx, o));
-    if (lane == 0) {
-        bv[wave] = best;
-        bi[wave] = bidx;
-    }
-    __syncthreads();
+}
+
+__global__ __launch_bounds__(AM_THREADS) void argmax_merge_k(const float *__restrict__ x,
+                                                             const float *__restrict__ pv,
+                                                             const int *__restrict__ pi, int nwg,
+                                                             uint32_t *__restrict__ idx,
+                                                             uint32_t *__restrict__ pos,
+                                                             uint32_t advance,
+                                                             uint32_t *__restrict__ history)
+{
+    __shared__ float bv[AM_THREADS / 64];
+    __shared__ int bi[AM_THREADS / 64];
+    const int tid = threadIdx.x;
+    float best = -INFINITY;
+    int bidx = 0x7fffffff;
+    for (int b = tid; b < nwg; b += AM_THREADS) am_merge(best, bidx, pv[b], pi[b]);
+    am_reduce_wg(best, bidx, bv, bi);
     if (tid == 0) {
-        for (int w = 1; w < AM_THREADS / 64; w++) am_merge(best, bidx, bv[w], bi[w]);
         // index 0 wins unless something is strictly greater than x[0]
         const float x0 = x[0];
         const uint32_t r = (x0 != x0 || !(best > x0)) ? 0u : (uint32_t)bidx;
         *idx = r;
         if (pos) {
-            if (history) history[*pos] = r;
-            *pos += advance;
+            const uint32_t p = *pos;
+            if (history) history[p] = r;
+            *pos = p + advance;
         }
-        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -1811,17 +1836,19 @@ extern "C" fox_gpu_status fox_gpu_argmax(fox_gpu_ctx *ctx, const float *logits, 
 {
     if (!ctx || !logits || !idx || n == 0 || n > 0x7fffffff)
         return fox_fail(FOX_GPU_ERR_ARG, "argmax: bad argument");
-    // partials and the counter live in the context's fixed small buffer
-    unsigned *counter = (unsigned *)ctx->small;
-    float *pv = (float *)(ctx->small + 256);
-    int *pi = (int *)(ctx->small + 256 + 4 * AM_MAX_WG);
+    // the partials live in the context's fixed small buffer
+    float *pv = (float *)(ctx->small + FOX_SMALL_AM_OFF);
+    int *pi = (int *)(ctx->small + FOX_SMALL_AM_OFF + 4 * AM_MAX_WG);
     size_t nwg = (n + 2047) / 2048;
     if (nwg > AM_MAX_WG) nwg = AM_MAX_WG;
     const size_t per = (n + nwg - 1) / nwg;
     nwg = (n + per - 1) / per;
-    hipLaunchKernelGGL(argmax_k, dim3((unsigned)nwg), dim3(AM_THREADS), 0, ctx->stream, logits,
-                       (int)n, (int)per, pv, pi, counter, idx, pos, advance, history);
-    FOX_LAUNCHED("argmax");
+    hipLaunchKernelGGL(argmax_part_k, dim3((unsigned)nwg), dim3(AM_THREADS), 0, ctx->stream,
+                       logits, (int)n, (int)per, pv, pi);
+    FOX_LAUNCHED("argmax partials");
+    hipLaunchKernelGGL(argmax_merge_k, dim3(1), dim3(AM_THREADS), 0, ctx->stream, logits,
+                       (const float *)pv, (const int *)pi, (int)nwg, idx, pos, advance, history);
+    FOX_LAUNCHED("argmax merge");
     return FOX_GPU_OK;
 }
 

@@ -32,13 +32,42 @@ def test_argmax_follows_the_reference(gpu, oracle, name):
     pos = gpu.array(np.array([3], np.uint32))
     hist = gpu.array(np.zeros(8, np.uint32))
     dx = gpu.array(x)
-    for _ in range(2):                                 # the counter resets itself
+    for _ in range(2):
         gpu.argmax(dx, x.size, idx)
     gpu.argmax(dx, x.size, idx, pos, 1, hist)
     gpu.sync()
     want = oracle.argmax(x)
     assert int(idx.numpy()[0]) == want
     assert int(pos.numpy()[0]) == 4 and int(hist.numpy()[3]) == want
+
+
+def test_argmax_sees_this_launchs_partials(gpu, oracle):
+    """Back-to-back argmax launches whose maxima sit in different partial
+    ranges: every result must come from its own input.  (A single launch
+    whose last workgroup merged the other workgroups' partials read a
+    partial of the previous launch now and then and returned the runner-up
+    range's maximum.)  Two inputs alternate: A has a large value in one
+    range and its maximum in another range, B the reverse, so that any
+    partial carried over from the other input changes the answer."""
+    rng = np.random.default_rng(5)
+    n = 151936
+    a = rng.standard_normal(n).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    a[77700], a[95832] = 9.0, 8.5                      # A: max at 77700, runner-up 95832
+    b[77700], b[95832] = 8.0, 8.75                     # B: max at 95832, 77700 below it
+    want = [oracle.argmax(a), oracle.argmax(b)]
+    assert want == [77700, 95832]
+    da, db = gpu.array(a), gpu.array(b)
+    steps = 64
+    idx = gpu.empty(1, np.uint32)
+    pos = gpu.array(np.array([0], np.uint32))
+    hist = gpu.array(np.zeros(steps, np.uint32))
+    for s in range(steps):
+        gpu.argmax(da if s % 2 == 0 else db, n, idx, pos, 1, hist)
+    gpu.sync()
+    got = hist.numpy()
+    assert [int(v) for v in got] == [want[s % 2] for s in range(steps)]
+    assert int(pos.numpy()[0]) == steps
 
 
 # sizes that reach every register-held variant of the kernel (256 R >= n for

@@ -300,9 +300,33 @@ def test_gemv_vs_reference(oracle, ref, gtype, N, K):
                           bits(oracle.gemv(gtype, x, w, N, K, n_threads=3)))
 
 
-@pytest.mark.parametrize("name", ["tiny-288", "tiny-512"])
-def test_forward_vs_reference(oracle, ref, name):
-    spec = synth.spec(name, n_layer=2, n_vocab=3000)
+# Grouped-query attention and a query width other than d_model, as the
+# 4B, 8B and 27B configurations have them (src/forward.c:82-83 sets the
+# group, :238 maps query head h to kv head h / gqa; head_dim comes from
+# attention.key_length, src/model.c:188-237): four query heads per kv head
+# with head_dim 128 over d_model 512 (q width 1024), the 4B/8B head layout
+# 32/8 x 128 (q width 4096, attn_output K = 4096), the 27B group of two
+# (32/16 x 64), and the 8B Q4_K/Q6_K mix with 8/2 x 128.
+_FWD = {
+    "tiny-288": ("tiny-288", {}),
+    "tiny-512": ("tiny-512", {}),
+    "gqa4-8x2x128": ("tiny-512", dict(n_head=8, n_head_kv=2, head_dim=128)),
+    "gqa4-32x8x128": ("tiny-512", dict(n_head=32, n_head_kv=8, head_dim=128)),
+    "gqa2-32x16x64": ("tiny-512", dict(n_head=32, n_head_kv=16, head_dim=64)),
+    "kquant-gqa4-8x2x128": ("tiny-512", dict(n_head=8, n_head_kv=2, head_dim=128,
+                                             linear_type=synth.Q4_K,
+                                             types={"attn_v": synth.Q6_K,
+                                                    "ffn_down": synth.Q6_K},
+                                             output_type=synth.Q6_K)),
+}
+
+
+@pytest.mark.parametrize("case", list(_FWD))
+def test_forward_vs_reference(oracle, ref, case):
+    name, over = _FWD[case]
+    spec = synth.spec(name, n_layer=2, n_vocab=3000, **over)
+    if case != name:
+        assert spec.n_head * spec.head_dim != spec.n_embd or spec.n_head != spec.n_head_kv
     with tempfile.TemporaryDirectory() as d:
         path = os.path.join(d, "m.gguf")
         tensors = {}
