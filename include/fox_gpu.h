@@ -44,9 +44,11 @@ typedef enum {
     FOX_GPU_ERR_INTERNAL
 } fox_gpu_status;
 
-/* ggml type ids (include/fox/fox.h:213-224) understood by the device path */
+/* ggml type ids (include/fox/fox.h:213-224) understood by the device path
+ * (Q4_0, Q8_0 and Q5_K by fox_gpu_dequant only) */
 enum {
-    FOX_GPU_F32 = 0, FOX_GPU_F16 = 1, FOX_GPU_Q4_K = 12, FOX_GPU_Q6_K = 14,
+    FOX_GPU_F32 = 0, FOX_GPU_F16 = 1, FOX_GPU_Q4_0 = 2, FOX_GPU_Q8_0 = 8,
+    FOX_GPU_Q4_K = 12, FOX_GPU_Q5_K = 13, FOX_GPU_Q6_K = 14,
     FOX_GPU_TQ1_0 = 34, FOX_GPU_TQ2_0 = 35
 };
 
@@ -94,21 +96,6 @@ fox_gpu_status fox_gpu_memcpy_d2h(fox_gpu_ctx *ctx, void *dst, const void *src, 
 fox_gpu_status fox_gpu_memcpy_d2d(fox_gpu_ctx *ctx, void *dst, const void *src, size_t n);
 fox_gpu_status fox_gpu_memset(fox_gpu_ctx *ctx, void *dst, int value, size_t n);
 fox_gpu_status fox_gpu_sync(fox_gpu_ctx *ctx);
-
-/* Diagnostic, no counterpart in RustFox: a streaming read of n bytes
- * (n and src 16-byte aligned) by `grid` workgroups of 256 threads reading
- * contiguous chunks of loads x 4 KB, each thread keeping `loads` (1, 2, 4, 8
- * or 16) 16-byte loads in flight; sink
- * (device memory, 4 bytes) is written only if the folded data hit a fixed
- * constant.  It measures the HBM read ceiling the GEMVs are compared with. */
-fox_gpu_status fox_gpu_read_probe(fox_gpu_ctx *ctx, const void *src, size_t n, int loads,
-                                  int grid, uint32_t *sink);
-
-/* Diagnostic, no counterpart in RustFox: one empty kernel of `grid`
- * workgroups on the stream (sink, device memory, is never written).  Timed
- * back to back, or captured in a graph, it gives the fixed cost of a launch
- * or of a graph node, which every kernel of a decode step pays. */
-fox_gpu_status fox_gpu_empty_probe(fox_gpu_ctx *ctx, int grid, uint32_t *sink);
 
 /* ------------------------------------------------------------ weights */
 
@@ -288,7 +275,7 @@ fox_gpu_status fox_gpu_get_rows(fox_gpu_ctx *ctx, const fox_gpu_tensor *t,
                                 size_t out_stride, uint32_t *bad);
 
 /* n elements of one row held in its GGUF bytes (device memory) as f32:
- * F32, F16, Q4_K and Q6_K with the reference's arithmetic
+ * F32, F16, Q8_0, Q4_0, Q4_K, Q5_K and Q6_K with the reference's arithmetic
  * (src/kernels.c:874-941; NaN payloads kept as the reference's field
  * conversion keeps them).  Other types -> FOX_GPU_ERR_UNSUPPORTED, n not a
  * whole number of blocks -> FOX_GPU_ERR_ARG.  Backs fox_dequant_row
@@ -341,16 +328,6 @@ fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t out_stride
                                  size_t n_head, size_t n_head_kv, size_t head_dim,
                                  size_t M, const uint32_t *pos, size_t n_ctx, int mode);
 
-/* Weights the kernels after the next attention will read (at most 8
- * tensors, in the order they are used, up to max_bytes in all).  The next
- * fox_gpu_attention call, if it is exact-mode for one token, reads them on
- * the compute units its own workgroups leave idle while the softmax and
- * value chains run, so that the following GEMVs find them in the infinity
- * cache; any other call drops the request.  Results are unchanged.  The
- * whole-token decode's cross-GEMV prefetch; the reference's analogue is its
- * layer-ahead weight prefetch (src/forward.c:322-337, src/weights.c:718-774). */
-fox_gpu_status fox_gpu_attention_prefetch(fox_gpu_ctx *ctx, size_t n,
-                                          const fox_gpu_tensor *const *ts, size_t max_bytes);
 
 /* gate = silu(gate) * up (src/ops.c:41-48) and dst += src (src/ops.c:50-54)
  * on M rows of n. */

@@ -39,11 +39,85 @@ const char *fox_last_error(void);
 
 #define FOX_NAME_MAX 128
 
-/* include/fox/fox.h:213-224 (the ids rustfox_amd reads) */
+/* include/fox/fox.h:213-224: the ggml type ids as GGUF files store them
+ * (the device path computes F32, F16, Q4_K, Q6_K, TQ1_0 and TQ2_0 weights) */
 typedef enum {
-    FOX_GGML_F32 = 0, FOX_GGML_F16 = 1, FOX_GGML_Q4_K = 12, FOX_GGML_Q6_K = 14,
-    FOX_GGML_TQ1_0 = 34, FOX_GGML_TQ2_0 = 35
+    FOX_GGML_F32 = 0, FOX_GGML_F16 = 1, FOX_GGML_Q4_0 = 2,
+    FOX_GGML_Q4_1 = 3, FOX_GGML_Q5_0 = 6, FOX_GGML_Q5_1 = 7,
+    FOX_GGML_Q8_0 = 8, FOX_GGML_Q2_K = 10, FOX_GGML_Q3_K = 11,
+    FOX_GGML_Q4_K = 12, FOX_GGML_Q5_K = 13, FOX_GGML_Q6_K = 14,
+    FOX_GGML_Q8_K = 15, FOX_GGML_IQ2_XXS = 16, FOX_GGML_IQ2_XS = 17,
+    FOX_GGML_IQ3_XXS = 18, FOX_GGML_IQ1_S = 19, FOX_GGML_IQ4_NL = 20,
+    FOX_GGML_IQ3_S = 21, FOX_GGML_IQ2_S = 22, FOX_GGML_IQ4_XS = 23,
+    FOX_GGML_I8 = 24, FOX_GGML_I16 = 25, FOX_GGML_I32 = 26,
+    FOX_GGML_I64 = 27, FOX_GGML_F64 = 28, FOX_GGML_IQ1_M = 29,
+    FOX_GGML_BF16 = 30, FOX_GGML_TQ1_0 = 34, FOX_GGML_TQ2_0 = 35
 } fox_ggml_type;
+
+/* include/fox/fox.h:357-358: IEEE half <-> single.  f16 -> f32 is exact
+ * (subnormals, infinities, NaN payloads kept); f32 -> f16 rounds to nearest
+ * even into the normal range, half up into the subnormal range, flushes
+ * below half the smallest subnormal to a signed zero, saturates to
+ * infinity, and turns every NaN into the quiet NaN 0x7E00 with its sign. */
+float    fox_f16_to_f32(uint16_t h);
+uint16_t fox_f32_to_f16(float f);
+
+/* --------------------------------------------------------------- gguf */
+
+/* include/fox/fox.h:204-262: the GGUF reader the model loader uses.  Same
+ * acceptance rules as RustFox src/gguf.c:348-466; metadata arrays are read
+ * into memory.  Lookups by name return SIZE_MAX when absent; a getter on an
+ * index past the table returns FOX_ERR_NOTFOUND, on a value of another type
+ * FOX_ERR_FORMAT, with a NULL handle or output FOX_ERR_ARG. */
+#define FOX_GGUF_MAX_DIMS 4
+
+typedef enum {
+    FOX_GGUF_UINT8 = 0, FOX_GGUF_INT8, FOX_GGUF_UINT16, FOX_GGUF_INT16,
+    FOX_GGUF_UINT32, FOX_GGUF_INT32, FOX_GGUF_FLOAT32, FOX_GGUF_BOOL,
+    FOX_GGUF_STRING, FOX_GGUF_ARRAY, FOX_GGUF_UINT64, FOX_GGUF_INT64,
+    FOX_GGUF_FLOAT64
+} fox_gguf_value_type;
+
+typedef struct {
+    const char   *name;
+    uint32_t      n_dims;
+    uint64_t      ne[FOX_GGUF_MAX_DIMS];
+    fox_ggml_type type;
+    uint64_t      offset;       /* from the start of the data section */
+    uint64_t      size_bytes;
+} fox_gguf_tensor;
+
+typedef struct fox_gguf fox_gguf;
+
+fox_status fox_gguf_open(const char *path, fox_gguf **out);
+void       fox_gguf_close(fox_gguf *g);
+uint32_t   fox_gguf_version(const fox_gguf *g);
+size_t     fox_gguf_metadata_count(const fox_gguf *g);
+size_t     fox_gguf_tensor_count(const fox_gguf *g);
+size_t     fox_gguf_find(const fox_gguf *g, const char *key);
+/* FOX_GGUF_ARRAY for an index past the table */
+fox_gguf_value_type fox_gguf_metadata_type(const fox_gguf *g, size_t index);
+/* 0 and FOX_GGUF_ARRAY when the value is not an array */
+size_t     fox_gguf_metadata_array_count(const fox_gguf *g, size_t index);
+fox_gguf_value_type fox_gguf_metadata_array_type(const fox_gguf *g, size_t index);
+fox_status fox_gguf_get_u32(const fox_gguf *g, size_t index, uint32_t *out);
+fox_status fox_gguf_get_bool(const fox_gguf *g, size_t index, int *out);
+fox_status fox_gguf_get_f32(const fox_gguf *g, size_t index, float *out);
+/* any integer or bool value, signed ones sign-extended */
+fox_status fox_gguf_get_uint(const fox_gguf *g, size_t index, uint64_t *out);
+fox_status fox_gguf_get_string(const fox_gguf *g, size_t index, const char **out);
+fox_status fox_gguf_get_array_string(const fox_gguf *g, size_t index,
+                                     size_t element, const char **out);
+fox_status fox_gguf_get_array_i32(const fox_gguf *g, size_t index,
+                                  size_t element, int32_t *out);
+fox_status fox_gguf_get_array_f32(const fox_gguf *g, size_t index,
+                                  size_t element, float *out);
+fox_status fox_gguf_tensor_at(const fox_gguf *g, size_t index, fox_gguf_tensor *out);
+size_t     fox_gguf_tensor_find(const fox_gguf *g, const char *name);
+/* the tensor's bytes as stored in the file; FOX_ERR_ARG if capacity is
+ * smaller than size_bytes */
+fox_status fox_gguf_read_tensor(const fox_gguf *g, size_t index,
+                                void *dst, size_t capacity);
 
 const char *fox_ggml_type_name(fox_ggml_type type);
 uint32_t    fox_ggml_type_block_size(fox_ggml_type type);
@@ -102,7 +176,8 @@ fox_status fox_gemv(fox_threadpool *tp, fox_ggml_type type, const float *x,
                     const void *weights, size_t n_rows, size_t n_cols,
                     float *out);
 
-/* include/fox/fox.h:367-368: F32, F16, Q4_K, Q6_K rows */
+/* include/fox/fox.h:367-368: F32, F16, Q8_0, Q4_0, Q4_K, Q5_K and Q6_K
+ * rows (src/kernels.c:874-941) */
 fox_status fox_dequant_row(fox_ggml_type type, const void *row, size_t n,
                            float *out);
 
@@ -131,6 +206,8 @@ typedef struct {
 fox_status fox_weights_open(const char *gguf_path, fox_weights_mode mode,
                             uint64_t budget_bytes, fox_weights **out);
 void       fox_weights_close(fox_weights *w);
+/* include/fox/fox.h:390: the parsed file behind the handle (owned by w) */
+const fox_gguf  *fox_weights_model(const fox_weights *w);
 fox_weights_mode fox_weights_get_mode(const fox_weights *w);
 size_t     fox_weights_tensor_count(const fox_weights *w);             /* EXTENSION */
 size_t     fox_weights_tensor_find(const fox_weights *w, const char *name); /* EXTENSION */

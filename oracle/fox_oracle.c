@@ -76,7 +76,8 @@ size_t or_block_elems(int type)
 {
     switch (type) {
     case OR_F32: case OR_F16: return 1;
-    case OR_Q4_K: case OR_Q6_K: case OR_TQ1_0: case OR_TQ2_0: return 256;
+    case OR_Q4_0: case OR_Q8_0: return 32;
+    case OR_Q4_K: case OR_Q5_K: case OR_Q6_K: case OR_TQ1_0: case OR_TQ2_0: return 256;
     default: return 0;
     }
 }
@@ -86,7 +87,10 @@ size_t or_block_bytes(int type)
     switch (type) {
     case OR_F32: return 4;
     case OR_F16: return 2;
+    case OR_Q4_0: return 18;
+    case OR_Q8_0: return 34;
     case OR_Q4_K: return 144;
+    case OR_Q5_K: return 176;
     case OR_Q6_K: return 210;
     case OR_TQ1_0: return 54;
     case OR_TQ2_0: return 66;
@@ -490,8 +494,9 @@ int or_gemv(int type, const float *x, const void *w, size_t rows, size_t cols,
     return OR_OK;
 }
 
-/* src/kernels.c:874-941 (path types) with the block decoders of
- * src/kernels.c:217-283 */
+/* src/kernels.c:874-941 with the block decoders of src/kernels.c:217-306
+ * (Q8_0, Q4_0: 32-element blocks, d f16 first; Q5_K: d, dmin, 12 scale
+ * bytes, qh[32], qs[128]) */
 int or_dequant_row(int type, const void *row, size_t n, float *out)
 {
     const uint8_t *w = (const uint8_t *)row;
@@ -531,6 +536,37 @@ int or_dequant_row(int type, const void *row, size_t n, float *out)
                 int nib = j & 1 ? byte >> 4 : byte & 0x0F;
                 q4k_scale_min(blk + 4, j, &sc, &mn);
                 out[b * 256 + i] = d * (float)sc * (float)nib - dmin * (float)mn;
+            }
+        }
+        return OR_OK;
+    case OR_Q8_0:
+        for (b = 0; b < n / 32; b++) {
+            const uint8_t *blk = w + b * 34;
+            float d = half_at(blk);
+            for (i = 0; i < 32; i++) out[b * 32 + i] = (float)(int8_t)blk[2 + i] * d;
+        }
+        return OR_OK;
+    case OR_Q4_0:
+        for (b = 0; b < n / 32; b++) {
+            const uint8_t *blk = w + b * 18;
+            float d = half_at(blk);
+            for (i = 0; i < 32; i++) {
+                uint8_t byte = blk[2 + i % 16];
+                int nib = i < 16 ? byte & 0x0F : byte >> 4;
+                out[b * 32 + i] = (float)(nib - 8) * d;
+            }
+        }
+        return OR_OK;
+    case OR_Q5_K:
+        for (b = 0; b < n / 256; b++) {
+            const uint8_t *blk = w + b * 176;
+            float d = half_at(blk), dmin = half_at(blk + 2);
+            for (i = 0; i < 256; i++) {
+                int grp = (int)i / 32, l = (int)i % 32, sc, mn;
+                uint8_t byte = blk[48 + 32 * (grp % 4) + l];
+                int v = (grp < 4 ? byte & 0x0F : byte >> 4) | (((blk[16 + l] >> grp) & 1) << 4);
+                q4k_scale_min(blk + 4, grp, &sc, &mn);
+                out[b * 256 + i] = d * (float)sc * (float)v - dmin * (float)mn;
             }
         }
         return OR_OK;

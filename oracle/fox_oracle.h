@@ -36,7 +36,7 @@ extern "C" {
 
 /* ggml type ids used on the path (include/fox/fox.h:213-224) */
 enum {
-    OR_F32 = 0, OR_F16 = 1, OR_Q4_K = 12, OR_Q6_K = 14,
+    OR_F32 = 0, OR_F16 = 1, OR_Q4_0 = 2, OR_Q8_0 = 8, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14,
     OR_TQ1_0 = 34, OR_TQ2_0 = 35
 };
 

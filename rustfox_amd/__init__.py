@@ -40,6 +40,24 @@ class FoxError(RuntimeError):
 _gpu = None
 
 
+PROBE_LIB = os.path.join(HERE, "lib", "librustfox_probe.so")
+_probe = None
+
+
+def probe_lib() -> C.CDLL:
+    """bench.py's diagnostics (read ceiling, launch cost): a separate
+    library, not part of the decode ABI."""
+    global _probe
+    if _probe is None:
+        gpu_lib()
+        L = C.CDLL(PROBE_LIB)
+        vp, sz = C.c_void_p, C.c_size_t
+        L.fox_gpu_read_probe.argtypes = [vp, vp, sz, C.c_int, C.c_int, vp]
+        L.fox_gpu_empty_probe.argtypes = [vp, C.c_int, vp]
+        _probe = L
+    return _probe
+
+
 def gpu_lib() -> C.CDLL:
     """Load librustfox_amd.so (raises if it has not been built)."""
     global _gpu
@@ -60,8 +78,6 @@ def gpu_lib() -> C.CDLL:
         "fox_gpu_memcpy_h2d": [vp, vp, vp, sz],
         "fox_gpu_memcpy_d2h": [vp, vp, vp, sz],
         "fox_gpu_memcpy_d2d": [vp, vp, vp, sz],
-        "fox_gpu_read_probe": [vp, vp, sz, C.c_int, C.c_int, vp],
-        "fox_gpu_empty_probe": [vp, C.c_int, vp],
         "fox_gpu_memset": [vp, vp, C.c_int, sz],
         "fox_gpu_sync": [vp],
         "fox_gpu_tensor_upload": [vp, C.c_int, C.c_uint64, C.c_uint64, vp, C.c_uint64,
@@ -86,7 +102,6 @@ def gpu_lib() -> C.CDLL:
         "fox_gpu_rope_store": [vp, vp, sz, vp, sz, vp, sz, sz, sz, sz, sz, vp, vp, vp, sz,
                                vp, vp],
         "fox_gpu_attention": [vp, vp, sz, vp, sz, vp, vp, sz, sz, sz, sz, vp, sz, C.c_int],
-        "fox_gpu_attention_prefetch": [vp, sz, C.POINTER(vp), sz],
         "fox_gpu_kv_write": [vp, vp, vp, sz, sz, sz, sz, vp, vp],
         "fox_gpu_gemv_rmsnorm": [vp, sz, C.POINTER(vp), vp, sz, sz, vp, C.c_float,
                                  C.POINTER(vp), C.POINTER(sz), C.c_uint],
@@ -255,12 +270,13 @@ class Gpu:
 
     def read_probe(self, src: DeviceArray, nbytes: int, loads: int, grid: int, sink: DeviceArray):
         """Streaming read of nbytes with `loads` 16-byte loads in flight per
-        thread (fox_gpu_read_probe; a diagnostic of the HBM read ceiling)."""
-        _check(self.lib.fox_gpu_read_probe(self.ctx, src.ptr, nbytes, loads, grid, sink.ptr))
+        thread (a diagnostic of the HBM read ceiling, from the bench-only
+        librustfox_probe.so)."""
+        _check(probe_lib().fox_gpu_read_probe(self.ctx, src.ptr, nbytes, loads, grid, sink.ptr))
 
     def empty_probe(self, grid: int, sink: DeviceArray):
-        """One empty kernel of `grid` workgroups (fox_gpu_empty_probe)."""
-        _check(self.lib.fox_gpu_empty_probe(self.ctx, grid, sink.ptr))
+        """One empty kernel of `grid` workgroups (librustfox_probe.so)."""
+        _check(probe_lib().fox_gpu_empty_probe(self.ctx, grid, sink.ptr))
 
     # -- compute (device arrays in, device arrays out)
     def quantize(self, mode, x: DeviceArray, K, M, x_stride, q: DeviceArray, scale: DeviceArray):
@@ -350,12 +366,6 @@ class Gpu:
         _check(self.lib.fox_gpu_attention(self.ctx, out.ptr, out_stride or w, q.ptr,
                                           q_stride or w, kc.ptr, vc.ptr, n_head, n_head_kv,
                                           head_dim, M, pos.ptr, n_ctx, mode))
-
-    def attention_prefetch(self, ts, max_bytes):
-        """Weights the next one-token exact attention reads ahead
-        (fox_gpu_attention_prefetch)."""
-        hs = (C.c_void_p * max(len(ts), 1))(*[t.h for t in ts])
-        _check(self.lib.fox_gpu_attention_prefetch(self.ctx, len(ts), hs, max_bytes))
 
     def event(self):
         e = C.c_void_p()

@@ -70,11 +70,6 @@ struct fox_gpu_ctx {
     uint8_t *small;
     // this device's copy of the fixed scratch of fox_gpu_gemv_noalloc
     uint8_t *scratch;
-    // weights the next one-token exact attention reads ahead
-    // (fox_gpu_attention_prefetch; cleared by every fox_gpu_attention)
-    const void *pf_p[8];
-    size_t pf_bytes[8];
-    int pf_n;
 };
 #define FOX_SMALL_BYTES (64 * 1024)
 // the small buffer's parts: the device error word (bits FOX_DEV_ERR_*, set
@@ -182,7 +177,10 @@ static inline const char *fox_type_name(int type)
     switch (type) {
     case FOX_GPU_F32: return "F32";
     case FOX_GPU_F16: return "F16";
+    case FOX_GPU_Q4_0: return "Q4_0";
+    case FOX_GPU_Q8_0: return "Q8_0";
     case FOX_GPU_Q4_K: return "Q4_K";
+    case FOX_GPU_Q5_K: return "Q5_K";
     case FOX_GPU_Q6_K: return "Q6_K";
     case FOX_GPU_TQ1_0: return "TQ1_0";
     case FOX_GPU_TQ2_0: return "TQ2_0";

@@ -85,8 +85,24 @@ __device__ __forceinline__ float f16_exact(uint32_t h)
 }
 
 // One element per thread of a row in its GGUF bytes: F32 copy, F16
-// conversion, Q4_K y = (d*sc)*q - dmin*m (src/kernels.c:257-283), Q6_K
-// y = (d*sc)*(q-32) (src/kernels.c:217-244), each product rounded as there.
+// conversion, Q8_0 y = q*d and Q4_0 y = (nibble-8)*d (src/kernels.c:896-920:
+// 32-element blocks, a block's low nibbles its first 16 elements), Q4_K
+// y = (d*sc)*q - dmin*m (src/kernels.c:257-283), Q5_K the same with a fifth
+// bit from qh (src/kernels.c:286-306: groups 0-3 take the low nibbles of
+// qs, groups 4-7 the high ones, group g's fifth bit is bit g of qh[l]),
+// Q6_K y = (d*sc)*(q-32) (src/kernels.c:217-244), each product rounded as
+// there.
+__device__ __forceinline__ void k4_scale_min(const uint8_t *s, int j, uint32_t &sc, uint32_t &m)
+{
+    if (j < 4) {
+        sc = s[j] & 63u;
+        m = s[j + 4] & 63u;
+    } else {
+        sc = (s[j + 4] & 15u) | ((uint32_t)(s[j - 4] >> 6) << 4);
+        m = (s[j + 4] >> 4) | ((uint32_t)(s[j] >> 6) << 4);
+    }
+}
+
 __global__ void dequant_gguf_k(int type, const uint8_t *__restrict__ w, uint64_t n,
                                float *__restrict__ out)
 {
@@ -97,18 +113,32 @@ __global__ void dequant_gguf_k(int type, const uint8_t *__restrict__ w, uint64_t
             y = ((const float *)w)[i];
         } else if (type == FOX_GPU_F16) {
             y = f16_exact(((const uint16_t *)w)[i]);
+        } else if (type == FOX_GPU_Q8_0) {
+            const uint8_t *blk = w + (i >> 5) * 34;
+            const float d = f16_exact(blk[0] | (uint32_t)blk[1] << 8);
+            y = (float)(int8_t)blk[2 + (i & 31)] * d;
+        } else if (type == FOX_GPU_Q4_0) {
+            const uint8_t *blk = w + (i >> 5) * 18;
+            const int e = (int)(i & 31);
+            const uint8_t qb = blk[2 + (e & 15)];
+            const int q = (int)(e < 16 ? (qb & 15u) : (qb >> 4)) - 8;
+            const float d = f16_exact(blk[0] | (uint32_t)blk[1] << 8);
+            y = (float)q * d;
+        } else if (type == FOX_GPU_Q5_K) {
+            const uint8_t *blk = w + (i >> 8) * 176;
+            const int e = (int)(i & 255), grp = e >> 5, l = e & 31;
+            uint32_t sc, m;
+            k4_scale_min(blk + 4, grp, sc, m);
+            const uint8_t qb = blk[48 + 32 * (grp & 3) + l];
+            const uint32_t q = (grp < 4 ? (qb & 15u) : (qb >> 4)) | (((blk[16 + l] >> grp) & 1u) << 4);
+            const float d = f16_exact(blk[0] | (uint32_t)blk[1] << 8);
+            const float dmin = f16_exact(blk[2] | (uint32_t)blk[3] << 8);
+            y = d * (float)sc * (float)q - dmin * (float)m;
         } else if (type == FOX_GPU_Q4_K) {
             const uint8_t *blk = w + (i >> 8) * 144;
             const int e = (int)(i & 255), p = e >> 6, l = e & 63, j = 2 * p + (l >> 5);
-            const uint8_t *s = blk + 4;
             uint32_t sc, m;
-            if (j < 4) {
-                sc = s[j] & 63u;
-                m = s[j + 4] & 63u;
-            } else {
-                sc = (s[j + 4] & 15u) | ((uint32_t)(s[j - 4] >> 6) << 4);
-                m = (s[j + 4] >> 4) | ((uint32_t)(s[j] >> 6) << 4);
-            }
+            k4_scale_min(blk + 4, j, sc, m);
             const uint8_t qb = blk[16 + 32 * p + (l & 31)];
             const uint32_t q = l < 32 ? (qb & 15u) : (qb >> 4);
             const float d = f16_exact(blk[0] | (uint32_t)blk[1] << 8);
@@ -133,11 +163,16 @@ extern "C" fox_gpu_status fox_gpu_dequant(fox_gpu_ctx *ctx, int type, const void
                                           float *out)
 {
     if (!ctx || !row || !out || n == 0) return fox_fail(FOX_GPU_ERR_ARG, "dequant: bad argument");
-    if (type != FOX_GPU_F32 && type != FOX_GPU_F16 && type != FOX_GPU_Q4_K &&
-        type != FOX_GPU_Q6_K)
+    size_t be;
+    switch (type) {
+    case FOX_GPU_F32: case FOX_GPU_F16: be = 1; break;
+    case FOX_GPU_Q8_0: case FOX_GPU_Q4_0: be = 32; break;
+    case FOX_GPU_Q4_K: case FOX_GPU_Q5_K: case FOX_GPU_Q6_K: be = 256; break;
+    default:
         return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "dequant: %s rows are not dequantised",
                         fox_type_name(type));
-    if (n % fox_block_elems(type))
+    }
+    if (n % be)
         return fox_fail(FOX_GPU_ERR_ARG, "dequant: %zu elements is not a whole number of %s "
                         "blocks", n, fox_type_name(type));
     const uint64_t g = (n + 255) / 256;
@@ -840,45 +875,6 @@ __global__ __launch_bounds__(64) void attn_values_x(const float *__restrict__ at
 #define SV_SPIN (1 << 22)
 #define SV_IDLE_SLEEP 2             // s_sleep units (64 clocks each) between idle polls
 
-// Weight prefetch riding on the attention launch (one token): the kernel's
-// own workgroups occupy n_head_kv x slices compute units for the length of
-// the two position-order chains, during which HBM is nearly idle.  nwg more
-// workgroups, on compute units the attention leaves free (the kernel's LDS
-// keeps one workgroup per compute unit), read the weights the next kernels
-// will read, in order, so that those kernels find them in the infinity
-// cache.  The values read are folded into a register that an empty asm
-// statement consumes: nothing is written, and results cannot change.
-#define SV_PF_REGIONS 8
-#define SV_PF_LOADS 2                // 16-byte loads in flight per thread
-#define SV_PF_WG_MAX 128
-struct SvPrefetch {
-    const uint4 *p[SV_PF_REGIONS];
-    size_t n16[SV_PF_REGIONS];       // 16-byte words of each region
-    int nreg, nwg;
-    int first;                       // blockIdx.x of the first prefetching workgroup
-};
-
-__device__ __forceinline__ void sv_prefetch_reads(const SvPrefetch &pf, int w)
-{
-    constexpr int T = SV_WAVES * 64, U = SV_PF_LOADS;
-    uint32_t acc = 0;
-    for (int r = 0; r < pf.nreg; r++) {
-        const uint4 *__restrict__ p = pf.p[r];
-        const size_t n = pf.n16[r], step = (size_t)pf.nwg * T * U;
-        for (size_t c = (size_t)w * T * U + threadIdx.x; c < n; c += step) {
-            uint4 v[U];
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const size_t i = c + (size_t)u * T;
-                v[u] = p[i < n ? i : n - 1];
-            }
-#pragma unroll
-            for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
-        }
-    }
-    asm volatile("" ::"v"(acc));
-}
-
 // v of lane (quad base + sel) for each lane, sel from a quad_perm control
 // word known at compile time (DPP, no LDS traffic)
 __device__ __forceinline__ float dpp_bcast(float v, int ctl)
@@ -1086,14 +1082,8 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
     const float *__restrict__ att, size_t att_stride, const float *__restrict__ tmax, int n_tiles,
     const float *__restrict__ vc, int n_head, int n_head_kv, int hd,
     const uint32_t *__restrict__ pos, int n_ctx, float *__restrict__ out, size_t out_stride,
-    int np, SvPrefetch pf, unsigned *err)
+    int np, unsigned *err)
 {
-    // the last pf.nwg workgroups of row 0 prefetch (the host adds them for
-    // one token only); they use neither LDS nor barriers
-    if (pf.nwg > 0 && (int)blockIdx.x >= pf.first) {
-        if (blockIdx.y == 0) sv_prefetch_reads(pf, (int)blockIdx.x - pf.first);
-        return;
-    }
     constexpr int DS = 64 / G;               // columns per slice
     constexpr int NLD = SV_QT / G;           // product units per tile (G quads each)
     extern __shared__ float4 sv_lds[];
@@ -1519,44 +1509,12 @@ __global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
     }
 }
 
-extern "C" fox_gpu_status fox_gpu_attention_prefetch(fox_gpu_ctx *ctx, size_t n,
-                                                     const fox_gpu_tensor *const *ts,
-                                                     size_t max_bytes)
-{
-    if (!ctx) return fox_fail(FOX_GPU_ERR_ARG, "attention_prefetch: null context");
-    ctx->pf_n = 0;
-    if (n > SV_PF_REGIONS || (n && !ts))
-        return fox_fail(FOX_GPU_ERR_ARG, "attention_prefetch: at most %d tensors", SV_PF_REGIONS);
-    size_t left = max_bytes;
-    for (size_t i = 0; i < n; i++) {
-        if (!ts[i] || !ts[i]->d) return fox_fail(FOX_GPU_ERR_ARG, "attention_prefetch: null tensor");
-        if ((uintptr_t)ts[i]->d % 16) continue;
-        const size_t b = (ts[i]->dev_bytes < left ? ts[i]->dev_bytes : left) & ~(size_t)15;
-        if (b == 0) break;
-        ctx->pf_p[ctx->pf_n] = ts[i]->d;
-        ctx->pf_bytes[ctx->pf_n] = b;
-        ctx->pf_n++;
-        left -= b;
-    }
-    return FOX_GPU_OK;
-}
-
 extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t out_stride,
                                             const float *q, size_t q_stride, const float *k_cache,
                                             const float *v_cache, size_t n_head, size_t n_head_kv,
                                             size_t head_dim, size_t M, const uint32_t *pos,
                                             size_t n_ctx, int mode)
 {
-    // the pending prefetch belongs to this call, whichever path it takes
-    SvPrefetch pf = {};
-    if (ctx) {
-        pf.nreg = ctx->pf_n;
-        for (int i = 0; i < pf.nreg; i++) {
-            pf.p[i] = (const uint4 *)ctx->pf_p[i];
-            pf.n16[i] = ctx->pf_bytes[i] / 16;
-        }
-        ctx->pf_n = 0;
-    }
     if (!ctx || !out || !q || !k_cache || !v_cache || !pos || n_head == 0 || n_head_kv == 0 ||
         head_dim == 0 || M == 0 || n_ctx == 0)
         return fox_fail(FOX_GPU_ERR_ARG, "attention: bad argument");
@@ -1635,20 +1593,13 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
             if (e != hipSuccess) return fox_hip_fail(e, "attention: LDS size");
             const int sv_ds = (int)(64 / gqa);
             const unsigned nsl = (unsigned)((head_dim + sv_ds - 1) / sv_ds);
-            // prefetching workgroups: one token only, on the compute units
-            // the attention leaves free (with more than half of a compute
-            // unit's 160 KB of LDS, a workgroup has its compute unit alone)
             const int n_attn = (int)(n_head_kv * nsl);
             unsigned *err = (unsigned *)(ctx->small + FOX_SMALL_ERR_OFF);
-            pf.first = n_attn;
-            pf.nwg = 0;
-            if (M == 1 && pf.nreg > 0 && sv_lds > 80 * 1024 && ctx->n_cu > n_attn)
-                pf.nwg = ctx->n_cu - n_attn < SV_PF_WG_MAX ? ctx->n_cu - n_attn : SV_PF_WG_MAX;
             void *args[] = {(void *)&att, (void *)&att_stride, (void *)&tmax, (void *)&n_tiles,
                             (void *)&v_cache, (void *)&ih, (void *)&ikv, (void *)&ihd,
                             (void *)&pos, (void *)&ictx, (void *)&out, (void *)&os,
-                            (void *)&np, (void *)&pf, (void *)&err};
-            e = hipLaunchKernel(sv, dim3((unsigned)(n_attn + pf.nwg), (unsigned)M),
+                            (void *)&np, (void *)&err};
+            e = hipLaunchKernel(sv, dim3((unsigned)n_attn, (unsigned)M),
                                 dim3(SV_WAVES * 64), args, sv_lds, ctx->stream);
             if (e != hipSuccess) return fox_hip_fail(e, "attention softmax+values");
             FOX_LAUNCHED("attention softmax+values");
@@ -1849,74 +1800,5 @@ extern "C" fox_gpu_status fox_gpu_argmax(fox_gpu_ctx *ctx, const float *logits, 
     hipLaunchKernelGGL(argmax_merge_k, dim3(1), dim3(AM_THREADS), 0, ctx->stream, logits,
                        (const float *)pv, (const int *)pi, (int)nwg, idx, pos, advance, history);
     FOX_LAUNCHED("argmax merge");
-    return FOX_GPU_OK;
-}
-
-// ------------------------------------------------------- read probe
-
-// Streaming read of n16 16-byte words: a workgroup reads contiguous
-// chunks of U * 4 KB (grid-stride over chunks), every thread keeping U loads
-// in flight (the U loads of a chunk are issued before any is used); the
-// ragged tail by single loads.  The loaded words are folded into one value
-// that is stored only if it equals a constant no input is expected to
-// produce, so the loads cannot be dropped and nothing is written in
-// practice.
-template <int U>
-__global__ __launch_bounds__(256) void read_probe_k(const uint4 *__restrict__ src, size_t n16,
-                                                    uint32_t *__restrict__ sink)
-{
-    constexpr size_t CH = (size_t)U * 256;             // words per chunk
-    const size_t nch = n16 / CH;
-    uint32_t acc = 0;
-    for (size_t c = blockIdx.x; c < nch; c += gridDim.x) {
-        const uint4 *p = src + c * CH + threadIdx.x;
-        uint4 v[U];
-#pragma unroll
-        for (int u = 0; u < U; u++) v[u] = p[u * 256];
-#pragma unroll
-        for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
-    }
-    for (size_t i = nch * CH + (size_t)blockIdx.x * 256 + threadIdx.x; i < n16;
-         i += (size_t)gridDim.x * 256) {
-        const uint4 v = src[i];
-        acc ^= v.x ^ v.y ^ v.z ^ v.w;
-    }
-    if (acc == 0x9e3779b9u) sink[0] = acc;
-}
-
-// An empty kernel: what one launch costs on the stream, or one node of a
-// graph, before any work (the store never happens: no workgroup has that
-// many threads).
-__global__ __launch_bounds__(256) void empty_probe_k(uint32_t *sink)
-{
-    if (threadIdx.x == 1u << 20) sink[0] = 1;
-}
-
-extern "C" fox_gpu_status fox_gpu_empty_probe(fox_gpu_ctx *ctx, int grid, uint32_t *sink)
-{
-    if (!ctx || !sink || grid <= 0 || grid > (1 << 20))
-        return fox_fail(FOX_GPU_ERR_ARG, "empty_probe: bad argument");
-    hipLaunchKernelGGL(empty_probe_k, dim3((unsigned)grid), dim3(256), 0, ctx->stream, sink);
-    FOX_LAUNCHED("empty_probe");
-    return FOX_GPU_OK;
-}
-
-extern "C" fox_gpu_status fox_gpu_read_probe(fox_gpu_ctx *ctx, const void *src, size_t n,
-                                             int loads, int grid, uint32_t *sink)
-{
-    if (!ctx || !src || !sink || n == 0 || n % 16 || (uintptr_t)src % 16 || grid <= 0 ||
-        grid > (1 << 20))
-        return fox_fail(FOX_GPU_ERR_ARG, "read_probe: bad argument");
-    const uint4 *s = (const uint4 *)src;
-    const size_t n16 = n / 16;
-    switch (loads) {
-    case 1: hipLaunchKernelGGL(read_probe_k<1>, dim3((unsigned)grid), dim3(256), 0, ctx->stream, s, n16, sink); break;
-    case 2: hipLaunchKernelGGL(read_probe_k<2>, dim3((unsigned)grid), dim3(256), 0, ctx->stream, s, n16, sink); break;
-    case 4: hipLaunchKernelGGL(read_probe_k<4>, dim3((unsigned)grid), dim3(256), 0, ctx->stream, s, n16, sink); break;
-    case 8: hipLaunchKernelGGL(read_probe_k<8>, dim3((unsigned)grid), dim3(256), 0, ctx->stream, s, n16, sink); break;
-    case 16: hipLaunchKernelGGL(read_probe_k<16>, dim3((unsigned)grid), dim3(256), 0, ctx->stream, s, n16, sink); break;
-    default: return fox_fail(FOX_GPU_ERR_ARG, "read_probe: 1, 2, 4, 8 or 16 loads in flight");
-    }
-    FOX_LAUNCHED("read_probe");
     return FOX_GPU_OK;
 }

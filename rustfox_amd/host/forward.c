@@ -48,7 +48,6 @@ struct fox_context {
     uint64_t reads_at_start;
     fox_gpu_graph *greedy;
     int attn_mode;                 /* FOX_GPU_ATTN_EXACT or FOX_GPU_ATTN_SPLIT */
-    size_t pf_bytes;               /* weights read ahead during one-token attention */
     void *allocs[32];
     int n_allocs;
 };
@@ -59,10 +58,6 @@ static double now_s(void)
     clock_gettime(CLOCK_MONOTONIC, &ts);
     return (double)ts.tv_sec + (double)ts.tv_nsec * 1e-9;
 }
-
-/* default of FOX_PREFETCH_MB: off (measured: the attention's chains slow by
- * about as much as the GEMVs after it gain) */
-#define FOX_PREFETCH_MB_DEFAULT 0
 
 #define GPU(call, what)                                       \
     do {                                                      \
@@ -164,13 +159,6 @@ fox_status fox_context_create(fox_model *m, const fox_context_config *cfg, fox_c
     {
         const char *e = getenv("FOX_ATTENTION");
         if (e && strcmp(e, "split") == 0) c->attn_mode = FOX_GPU_ATTN_SPLIT;
-    }
-    /* FOX_PREFETCH_MB: megabytes of the layer's next weights read into the
-     * infinity cache during each one-token attention (0: none) */
-    c->pf_bytes = (size_t)FOX_PREFETCH_MB_DEFAULT << 20;
-    {
-        const char *e = getenv("FOX_PREFETCH_MB");
-        if (e && *e) c->pf_bytes = (size_t)strtoul(e, NULL, 10) << 20;
     }
     nb = FOX_GPU_MAX_TOKENS;
 
@@ -381,22 +369,6 @@ static fox_status forward_pass(fox_context *c, size_t M, int want_logits)
                                    c->kc + l * kvl, c->vc + l * vl), "forward: rope");
         } else if (gs != FOX_GPU_OK) {
             return fox_gpu_failed(gs, "forward: q/k/v");
-        }
-        if (M == 1 && c->pf_bytes) {
-            /* the weights of this layer's remaining GEMVs, then (resident
-             * weights) the next layer's q/k/v, in the order they are used */
-            const fox_gpu_tensor *pt[7];
-            size_t npt = 0;
-            pt[npt++] = D->attn_out;
-            pt[npt++] = D->ffn_gate;
-            pt[npt++] = D->ffn_up;
-            pt[npt++] = D->ffn_down;
-            if (!streaming(c) && l + 1 < mi->n_layer) {
-                pt[npt++] = c->L[l + 1].attn_q;
-                pt[npt++] = c->L[l + 1].attn_k;
-                pt[npt++] = c->L[l + 1].attn_v;
-            }
-            GPU(fox_gpu_attention_prefetch(c->gpu, npt, pt, c->pf_bytes), "forward: prefetch");
         }
         GPU(fox_gpu_attention(c->gpu, c->xb, c->wide, c->q, c->nq, c->kc + l * kvl,
                               c->vc + l * vl, mi->n_head, mi->n_head_kv, c->hd, M, c->dpos,

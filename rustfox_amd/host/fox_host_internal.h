@@ -28,10 +28,14 @@ enum {
 };
 
 typedef struct {
-    char    *key;
-    uint32_t type;
-    uint64_t raw;        /* scalar bits, little endian */
-    char    *str;        /* GGUF_STRING */
+    char     *key;
+    uint32_t  type;
+    uint64_t  raw;       /* scalar bits, little endian */
+    char     *str;       /* GGUF_STRING */
+    uint32_t  atype;     /* GGUF_ARRAY: element type and count */
+    uint64_t  acount;
+    uint64_t *avals;     /* scalar elements' bits */
+    char    **astrs;     /* string elements */
 } fox_meta;
 
 typedef struct {
@@ -43,7 +47,8 @@ typedef struct {
     uint64_t size_bytes;
 } fox_tensor_desc;
 
-typedef struct {
+/* the parsed file (opaque fox_gguf of include/fox_host.h) */
+struct fox_gguf {
     uint32_t         version;
     size_t           n_meta;
     fox_meta        *meta;
@@ -52,15 +57,9 @@ typedef struct {
     uint32_t         alignment;
     uint64_t         data_offset;
     uint64_t         file_size;
-} fox_gguf;
+    char            *path;
+};
 
-fox_status fox_gguf_open(const char *path, fox_gguf **out);
-void       fox_gguf_close(fox_gguf *g);
-size_t     fox_gguf_find(const fox_gguf *g, const char *key);
-fox_status fox_gguf_get_uint(const fox_gguf *g, size_t idx, uint64_t *out);
-fox_status fox_gguf_get_f32(const fox_gguf *g, size_t idx, float *out);
-fox_status fox_gguf_get_string(const fox_gguf *g, size_t idx, const char **out);
-size_t     fox_gguf_tensor_find(const fox_gguf *g, const char *name);
 int        fox_type_layout(uint32_t type, uint32_t *block, uint32_t *bytes);
 
 /* --------------------------------------------------------------- weights */

@@ -5,7 +5,8 @@
  * dimensions, a known block layout whose block divides the element count,
  * general.alignment a power of two <= 4096 (default 32), data section
  * aligned after the tensor table, every tensor inside the file.  Array
- * metadata is skipped (nothing on the decode path reads it).
+ * metadata is read into memory (scalar elements as their bits, strings as
+ * strings) for the fox_gguf_get_array_* accessors.
  */
 #include "fox_host_internal.h"
 
@@ -27,14 +28,6 @@ static int take(rd *r, void *p, size_t n)
 {
     if ((uint64_t)n > r->size - r->pos) return 0;
     if (n && fread(p, 1, n, r->f) != n) return 0;
-    r->pos += n;
-    return 1;
-}
-
-static int skip(rd *r, uint64_t n)
-{
-    if (n > r->size - r->pos) return 0;
-    if (fseeko(r->f, (off_t)(r->pos + n), SEEK_SET) != 0) return 0;
     r->pos += n;
     return 1;
 }
@@ -68,17 +61,35 @@ static int read_str(rd *r, char **out)
     return 1;
 }
 
-static int skip_array(rd *r)
+/* an array value: element type, count, then the elements (nested arrays
+ * are refused, as RustFox src/gguf.c:128-175 refuses them) */
+static int read_array(rd *r, fox_meta *m)
 {
-    uint64_t et, count, i, n;
+    uint64_t et, count, i;
     if (!le(r, &et, 4) || et > GGUF_F64 || et == GGUF_ARRAY) return 0;
     if (!le(r, &count, 8) || count > MAX_TENSORS * 16ull) return 0;
+    m->atype = (uint32_t)et;
     if (et == GGUF_STRING) {
-        for (i = 0; i < count; i++)
-            if (!le(r, &n, 8) || n > MAX_STRING || !skip(r, n)) return 0;
+        /* each string takes at least its 8-byte length */
+        if (count > (r->size - r->pos) / 8) return 0;
+        m->astrs = (char **)calloc(count ? count : 1, sizeof(char *));
+        if (!m->astrs) return 0;
+        for (i = 0; i < count; i++) {
+            if (!read_str(r, &m->astrs[i])) return 0;
+            m->acount = i + 1;
+        }
         return 1;
     }
-    return skip(r, count * (uint64_t)scalar_size((uint32_t)et));
+    {
+        const int sz = scalar_size((uint32_t)et);
+        if (count > (r->size - r->pos) / (uint64_t)sz) return 0;
+        m->avals = (uint64_t *)malloc((count ? count : 1) * sizeof(uint64_t));
+        if (!m->avals) return 0;
+        for (i = 0; i < count; i++)
+            if (!le(r, &m->avals[i], sz)) return 0;
+        m->acount = count;
+    }
+    return 1;
 }
 
 /* block elements and bytes of each ggml type (RustFox src/gguf.c:160-195) */
@@ -103,10 +114,20 @@ void fox_gguf_close(fox_gguf *g)
 {
     size_t i;
     if (!g) return;
-    for (i = 0; i < g->n_meta; i++) { free(g->meta[i].key); free(g->meta[i].str); }
+    for (i = 0; i < g->n_meta; i++) {
+        fox_meta *m = &g->meta[i];
+        uint64_t j;
+        free(m->key);
+        free(m->str);
+        if (m->astrs)
+            for (j = 0; j < m->acount; j++) free(m->astrs[j]);
+        free(m->astrs);
+        free(m->avals);
+    }
     for (i = 0; i < g->n_tensors; i++) free(g->tensors[i].name);
     free(g->meta);
     free(g->tensors);
+    free(g->path);
     free(g);
 }
 
@@ -131,6 +152,8 @@ fox_status fox_gguf_open(const char *path, fox_gguf **out)
     if (!g) { fclose(r.f); return fox_fail(FOX_ERR_NOMEM, "gguf: header"); }
     g->file_size = r.size;
     g->alignment = 32;
+    g->path = strdup(path);
+    if (!g->path) { fclose(r.f); free(g); return fox_fail(FOX_ERR_NOMEM, "gguf: path"); }
 
     if (!take(&r, magic, 4) || memcmp(magic, "GGUF", 4) != 0) {
         st = fox_fail(FOX_ERR_FORMAT, "gguf: %s is not a GGUF file", path);
@@ -175,7 +198,7 @@ fox_status fox_gguf_open(const char *path, fox_gguf **out)
                 goto fail;
             }
         } else if (t == GGUF_ARRAY) {
-            if (!skip_array(&r)) {
+            if (!read_array(&r, m)) {
                 st = fox_fail(FOX_ERR_FORMAT, "gguf: bad array for key '%s'", m->key);
                 goto fail;
             }
@@ -254,6 +277,10 @@ fail:
     return st;
 }
 
+uint32_t fox_gguf_version(const fox_gguf *g) { return g ? g->version : 0; }
+size_t fox_gguf_metadata_count(const fox_gguf *g) { return g ? g->n_meta : 0; }
+size_t fox_gguf_tensor_count(const fox_gguf *g) { return g ? g->n_tensors : 0; }
+
 size_t fox_gguf_find(const fox_gguf *g, const char *key)
 {
     size_t i;
@@ -262,11 +289,56 @@ size_t fox_gguf_find(const fox_gguf *g, const char *key)
     return FOX_TENSOR_ABSENT;
 }
 
+/* the metadata entry idx of type `want` (any type with want < 0) */
+static fox_status meta_of(const fox_gguf *g, size_t idx, const void *out, int want,
+                          const fox_meta **m)
+{
+    if (!g || !out) return FOX_ERR_ARG;
+    if (idx >= g->n_meta) return FOX_ERR_NOTFOUND;
+    *m = &g->meta[idx];
+    if (want >= 0 && (*m)->type != (uint32_t)want) return FOX_ERR_FORMAT;
+    return FOX_OK;
+}
+
+fox_gguf_value_type fox_gguf_metadata_type(const fox_gguf *g, size_t idx)
+{
+    if (!g || idx >= g->n_meta) return FOX_GGUF_ARRAY;
+    return (fox_gguf_value_type)g->meta[idx].type;
+}
+
+size_t fox_gguf_metadata_array_count(const fox_gguf *g, size_t idx)
+{
+    if (!g || idx >= g->n_meta || g->meta[idx].type != GGUF_ARRAY) return 0;
+    return (size_t)g->meta[idx].acount;
+}
+
+fox_gguf_value_type fox_gguf_metadata_array_type(const fox_gguf *g, size_t idx)
+{
+    if (!g || idx >= g->n_meta || g->meta[idx].type != GGUF_ARRAY) return FOX_GGUF_ARRAY;
+    return (fox_gguf_value_type)g->meta[idx].atype;
+}
+
+fox_status fox_gguf_get_u32(const fox_gguf *g, size_t idx, uint32_t *out)
+{
+    const fox_meta *m;
+    fox_status st = meta_of(g, idx, out, GGUF_U32, &m);
+    if (st == FOX_OK) *out = (uint32_t)m->raw;
+    return st;
+}
+
+fox_status fox_gguf_get_bool(const fox_gguf *g, size_t idx, int *out)
+{
+    const fox_meta *m;
+    fox_status st = meta_of(g, idx, out, GGUF_BOOL, &m);
+    if (st == FOX_OK) *out = m->raw != 0;
+    return st;
+}
+
 fox_status fox_gguf_get_uint(const fox_gguf *g, size_t idx, uint64_t *out)
 {
     const fox_meta *m;
-    if (!g || idx >= g->n_meta || !out) return FOX_ERR_ARG;
-    m = &g->meta[idx];
+    fox_status st = meta_of(g, idx, out, -1, &m);
+    if (st != FOX_OK) return st;
     switch (m->type) {
     case GGUF_U8: case GGUF_U16: case GGUF_U32: case GGUF_U64: case GGUF_BOOL:
         *out = m->raw; return FOX_OK;
@@ -280,19 +352,75 @@ fox_status fox_gguf_get_uint(const fox_gguf *g, size_t idx, uint64_t *out)
 
 fox_status fox_gguf_get_f32(const fox_gguf *g, size_t idx, float *out)
 {
+    const fox_meta *m;
     uint32_t u;
-    if (!g || idx >= g->n_meta || !out) return FOX_ERR_ARG;
-    if (g->meta[idx].type != GGUF_F32) return FOX_ERR_FORMAT;
-    u = (uint32_t)g->meta[idx].raw;
+    fox_status st = meta_of(g, idx, out, GGUF_F32, &m);
+    if (st != FOX_OK) return st;
+    u = (uint32_t)m->raw;
     memcpy(out, &u, 4);
     return FOX_OK;
 }
 
 fox_status fox_gguf_get_string(const fox_gguf *g, size_t idx, const char **out)
 {
-    if (!g || idx >= g->n_meta || !out) return FOX_ERR_ARG;
-    if (g->meta[idx].type != GGUF_STRING) return FOX_ERR_FORMAT;
-    *out = g->meta[idx].str;
+    const fox_meta *m;
+    fox_status st = meta_of(g, idx, out, GGUF_STRING, &m);
+    if (st == FOX_OK) *out = m->str;
+    return st;
+}
+
+/* element `el` of an array of `want` elements */
+static fox_status elem_of(const fox_gguf *g, size_t idx, size_t el, const void *out,
+                          uint32_t want, const fox_meta **m)
+{
+    fox_status st = meta_of(g, idx, out, GGUF_ARRAY, m);
+    if (st != FOX_OK) return st;
+    if ((*m)->atype != want) return FOX_ERR_FORMAT;
+    if (el >= (*m)->acount) return FOX_ERR_NOTFOUND;
+    return FOX_OK;
+}
+
+fox_status fox_gguf_get_array_string(const fox_gguf *g, size_t idx, size_t el, const char **out)
+{
+    const fox_meta *m;
+    fox_status st = elem_of(g, idx, el, out, GGUF_STRING, &m);
+    if (st == FOX_OK) *out = m->astrs[el];
+    return st;
+}
+
+fox_status fox_gguf_get_array_i32(const fox_gguf *g, size_t idx, size_t el, int32_t *out)
+{
+    const fox_meta *m;
+    fox_status st = elem_of(g, idx, el, out, GGUF_I32, &m);
+    if (st == FOX_OK) *out = (int32_t)(uint32_t)m->avals[el];
+    return st;
+}
+
+fox_status fox_gguf_get_array_f32(const fox_gguf *g, size_t idx, size_t el, float *out)
+{
+    const fox_meta *m;
+    uint32_t u;
+    fox_status st = elem_of(g, idx, el, out, GGUF_F32, &m);
+    if (st != FOX_OK) return st;
+    u = (uint32_t)m->avals[el];
+    memcpy(out, &u, 4);
+    return FOX_OK;
+}
+
+fox_status fox_gguf_tensor_at(const fox_gguf *g, size_t idx, fox_gguf_tensor *out)
+{
+    const fox_tensor_desc *t;
+    uint32_t d;
+    if (!g || !out) return FOX_ERR_ARG;
+    if (idx >= g->n_tensors) return FOX_ERR_NOTFOUND;
+    t = &g->tensors[idx];
+    memset(out, 0, sizeof(*out));
+    out->name = t->name;
+    out->n_dims = t->n_dims;
+    for (d = 0; d < t->n_dims && d < FOX_GGUF_MAX_DIMS; d++) out->ne[d] = t->ne[d];
+    out->type = (fox_ggml_type)t->type;
+    out->offset = t->offset;
+    out->size_bytes = t->size_bytes;
     return FOX_OK;
 }
 
@@ -302,4 +430,21 @@ size_t fox_gguf_tensor_find(const fox_gguf *g, const char *name)
     if (!g || !name) return FOX_TENSOR_ABSENT;
     for (i = 0; i < g->n_tensors; i++) if (strcmp(g->tensors[i].name, name) == 0) return i;
     return FOX_TENSOR_ABSENT;
+}
+
+fox_status fox_gguf_read_tensor(const fox_gguf *g, size_t idx, void *dst, size_t capacity)
+{
+    const fox_tensor_desc *t;
+    FILE *f;
+    int ok;
+    if (!g || !dst) return FOX_ERR_ARG;
+    if (idx >= g->n_tensors) return FOX_ERR_NOTFOUND;
+    t = &g->tensors[idx];
+    if (t->size_bytes > capacity) return FOX_ERR_ARG;
+    f = fopen(g->path, "rb");
+    if (!f) return FOX_ERR_IO;
+    ok = fseeko(f, (off_t)(g->data_offset + t->offset), SEEK_SET) == 0 &&
+         fread(dst, 1, (size_t)t->size_bytes, f) == (size_t)t->size_bytes;
+    fclose(f);
+    return ok ? FOX_OK : FOX_ERR_IO;
 }

@@ -316,9 +316,10 @@ fox_status fox_dequant_row(fox_ggml_type type, const void *row, size_t n, float 
     if (rb == 0)
         return fox_fail(FOX_ERR_ARG, "dequant: %llu elements is not a whole number of %s blocks",
                         (unsigned long long)n, fox_ggml_type_name(type));
-    if (type != FOX_GGML_F32 && type != FOX_GGML_F16 && type != FOX_GGML_Q4_K &&
+    if (type != FOX_GGML_F32 && type != FOX_GGML_F16 && type != FOX_GGML_Q8_0 &&
+        type != FOX_GGML_Q4_0 && type != FOX_GGML_Q4_K && type != FOX_GGML_Q5_K &&
         type != FOX_GGML_Q6_K)
-        return fox_fail(FOX_ERR_UNSUPPORTED, "dequant: %s rows have no device decoder",
+        return fox_fail(FOX_ERR_UNSUPPORTED, "dequant: %s is not implemented yet",
                         fox_ggml_type_name(type));
     TRY(cm_begin(&m));
     TRY(cm_alloc(&m, rb, row, &dw));

@@ -471,6 +471,11 @@ void fox_weights_close(fox_weights *w)
     free(w);
 }
 
+const fox_gguf *fox_weights_model(const fox_weights *w)
+{
+    return w ? w->g : NULL;
+}
+
 fox_weights_mode fox_weights_get_mode(const fox_weights *w)
 {
     return w ? w->mode : FOX_WEIGHTS_RESIDENT;

@@ -125,44 +125,3 @@ def test_nan_first_score_follows_the_reference(gpu, oracle, case):
     nh0 = (n_head // n_kv) * hd
     assert np.isnan(want[:, :nh0]).all() and np.isnan(got[:, :nh0]).all()
     assert np.array_equal(got[:, nh0:].view(np.uint32), want[:, nh0:].view(np.uint32))
-
-
-@pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[5]],
-                         ids=lambda c: "h%d_kv%d_d%d_ctx%d_p%d_m%d" % c)
-def test_weight_prefetch_changes_nothing(gpu, oracle, case):
-    """fox_gpu_attention_prefetch: the next one-token exact attention reads
-    the given weights on idle compute units (a byte cap that ends inside the
-    second tensor, three tensors of which the last is never reached); for
-    several tokens the request is dropped.  The attention stays bit-identical
-    to the reference, the weights are unchanged, and a request is used once:
-    the call after it runs without one."""
-    from rustfox_amd import synth
-    n_head, n_kv, hd, n_ctx, pos, M = case
-    rng = np.random.default_rng(11 + sum(case))
-    q = (rng.standard_normal((M, n_head * hd)) * 0.3).astype(np.float32)
-    K = rng.standard_normal((n_ctx, n_kv * hd)).astype(np.float32)
-    V = rng.standard_normal((n_ctx, n_kv * hd)).astype(np.float32)
-    blobs = [synth.tq1_random(rng, r * 2560 // 256).reshape(-1) for r in (2560, 9728, 16)]
-    ts = [gpu.tensor(rf.TQ1_0, 2560, r, b) for r, b in zip((2560, 9728, 16), blobs)]
-    cap = ts[0].info()["device_bytes"] + 3 * 1000 * 1000 + 8
-    want = reference_attention(oracle, q, K, V, n_head, n_kv, hd, pos, M, n_ctx)
-    for before in (lambda: gpu.attention_prefetch(ts, cap), None):
-        got = run_gpu(gpu, q, K, V, n_head, n_kv, hd, pos, M, n_ctx, rf.ATTN_EXACT, before)
-        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
-            f"max abs diff {np.abs(got - want).max()}"
-    for t, b in zip(ts, blobs):
-        assert np.array_equal(t.download(), b)
-        t.free()
-
-
-def test_weight_prefetch_arguments(gpu):
-    """More than eight tensors is an argument error; an empty request and a
-    zero byte cap are accepted (nothing is read)."""
-    from rustfox_amd import synth
-    rng = np.random.default_rng(3)
-    t = gpu.tensor(rf.TQ1_0, 256, 16, synth.tq1_random(rng, 16).reshape(-1))
-    with pytest.raises(rf.FoxError):
-        gpu.attention_prefetch([t] * 9, 1 << 20)
-    gpu.attention_prefetch([], 1 << 20)
-    gpu.attention_prefetch([t] * 8, 0)
-    t.free()

@@ -163,28 +163,6 @@ def test_decode_greedy_equals_eval_argmax(tiny_models):
     assert [want[0]] + list(got) == want
 
 
-def test_weight_prefetch_decode_unchanged(tiny_models, monkeypatch):
-    """FOX_PREFETCH_MB: each one-token attention reads the layer's remaining
-    GEMV weights and the next layer's q/k/v ahead; the greedy decode (graph
-    and eager steps) is the same as without."""
-    s, t, p = tiny_models["tiny-512"]
-    prompt = synth.prompt_ids(8, s.n_vocab, seed=5)
-    runs = []
-    for mb in ("0", "64"):
-        monkeypatch.setenv("FOX_PREFETCH_MB", mb)
-        with rf.Model(p) as m:
-            ctx = m.context(64)
-            lg = ctx.eval(prompt)
-            ids = ctx.decode_greedy(int(np.argmax(lg)), 16)
-            step = ctx.eval([int(ids[-1])])
-            runs.append((lg, ids, step))
-            ctx.close()
-    (a0, b0, c0), (a1, b1, c1) = runs
-    assert np.array_equal(a0.view(np.uint32), a1.view(np.uint32))
-    assert np.array_equal(b0, b1)
-    assert np.array_equal(c0.view(np.uint32), c1.view(np.uint32))
-
-
 @pytest.mark.parametrize("mode", ["exact", "split"])
 def test_prefilled_cache_decode(tmp_path, oracle, mode):
     """A pre-filled cache (f16 N(0,1) values, as in the 4B benchmark) then

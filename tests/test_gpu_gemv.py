@@ -58,6 +58,7 @@ CASES = [
     ("F16", 50, 288, 1), ("F16", 1000, 2560, 2), ("F16", 7, 8, 1), ("F16", 257, 1000, 8),
     ("F32", 9, 64, 1), ("F32", 300, 288, 4),
     ("TQ1_0", 64, 2048, 6), ("TQ2_0", 96, 512, 7),      # input groups of four, then two or three
+    ("TQ1_0", 4096, 4096, 8), ("TQ2_0", 4096, 4096, 8),  # the 4096 x 4096 microbench, 8 stacked x
 ]
 
 

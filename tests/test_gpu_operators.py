@@ -181,13 +181,22 @@ def test_tq1_dot_known_answers(L):
 
 
 @pytest.mark.parametrize("tname,gtype,n", [("F16", 1, 65536), ("F32", 0, 1000),
-                                           ("Q4_K", 12, 4096), ("Q6_K", 14, 4096)])
+                                           ("Q4_K", 12, 4096), ("Q6_K", 14, 4096),
+                                           ("Q8_0", 8, 4096), ("Q4_0", 2, 4096),
+                                           ("Q5_K", 13, 4096)])
 def test_dequant_row_equals_the_oracle(L, oracle, tname, gtype, n):
     rng = np.random.default_rng([n, gtype])
     if gtype == 1:
         row = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.uint8)   # every f16
     elif gtype == 0:
         row = rng.standard_normal(n).astype(np.float32).view(np.uint8)
+    elif gtype in (8, 2, 13):
+        bb, offs, be = {8: (34, [0], 32), 2: (18, [0], 32), 13: (176, [0, 2], 256)}[gtype]
+        blk = rng.integers(0, 256, (n // be, bb), dtype=np.uint8)
+        for o in offs:
+            blk[:, o:o + 2] = rng.uniform(-0.1, 0.1, n // be).astype(np.float16).view(
+                np.uint8).reshape(-1, 2)
+        row = blk.reshape(-1)
     else:
         row = weights(rng, gtype, 1, n)
     out = np.empty(n, np.float32)
@@ -195,4 +204,4 @@ def test_dequant_row_equals_the_oracle(L, oracle, tname, gtype, n):
     want = oracle.dequant(gtype, row, n)
     assert np.array_equal(bits(out), bits(want)), tname
     assert L.fox_dequant_row(34, np.zeros(54, np.uint8), 256, out) == 5   # no TQ decoder
-    assert L.fox_dequant_row(12, row, 100, out) == 1                       # ragged
+    assert L.fox_dequant_row(gtype if gtype > 1 else 12, row, 100, out) == 1   # ragged

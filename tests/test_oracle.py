@@ -195,6 +195,65 @@ def test_dequant_vs_textbook(oracle):
     assert np.array_equal(bits(oracle.dequant(14, blk6, 256)), bits(want6))
 
 
+def _rand_blocks(rng, nblk, bb, half_offsets):
+    """nblk random blocks of bb bytes with finite f16 scales at the offsets."""
+    b = rng.integers(0, 256, (nblk, bb), dtype=np.uint8)
+    for o in half_offsets:
+        b[:, o:o + 2] = rng.uniform(-0.1, 0.1, nblk).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    return b
+
+
+def _k4_scale_min(s12, j):
+    """6-bit scale and min j of a K-quant 12-byte scale table (textbook:
+    j < 4 the low six bits of bytes j and j + 4; otherwise four bits from
+    byte j + 4 and the top two bits of bytes j - 4 and j)."""
+    s12 = [int(x) for x in s12]
+    if j < 4:
+        return s12[j] & 63, s12[j + 4] & 63
+    return (s12[j + 4] & 15) | ((s12[j - 4] >> 6) << 4), (s12[j + 4] >> 4) | ((s12[j] >> 6) << 4)
+
+
+def test_dequant_small_block_types_vs_textbook(oracle):
+    """Q8_0, Q4_0 (src/kernels.c:896-920) and Q5_K (src/kernels.c:286-306)
+    rows against element-wise decoders written from the block layouts, in
+    float32 with the reference's operation order."""
+    rng = np.random.default_rng(896)
+    f32 = np.float32
+    b8 = _rand_blocks(rng, 6, 34, [0])
+    want = np.concatenate([b[2:].view(np.int8).astype(f32) * b[:2].view(np.float16).astype(f32)
+                           for b in b8])
+    assert np.array_equal(bits(oracle.dequant(8, b8.reshape(-1), 192)), bits(want))
+    b4 = _rand_blocks(rng, 6, 18, [0])
+    want = []
+    for b in b4:
+        d = b[:2].view(np.float16).astype(f32)[0]
+        nib = np.concatenate([b[2:] & 15, b[2:] >> 4]).astype(np.int32) - 8
+        want.append(nib.astype(f32) * d)
+    assert np.array_equal(bits(oracle.dequant(2, b4.reshape(-1), 192)), bits(np.concatenate(want)))
+    b5 = _rand_blocks(rng, 3, 176, [0, 2])
+    want = []
+    for b in b5:
+        d, dmin = b[:4].view(np.float16).astype(f32)
+        qh, qs = b[16:48].astype(np.int32), b[48:176].astype(np.int32)
+        for grp in range(8):
+            sc, mn = _k4_scale_min(b[4:16], grp)
+            lo = qs[32 * (grp % 4):32 * (grp % 4) + 32]
+            v = (lo & 15 if grp < 4 else lo >> 4) | (((qh >> grp) & 1) << 4)
+            want.append((d * f32(sc)) * v.astype(f32) - dmin * f32(mn))
+    assert np.array_equal(bits(oracle.dequant(13, b5.reshape(-1), 768)), bits(np.concatenate(want)))
+
+
+def test_dequant_vs_reference(oracle, ref):
+    """Every row type the reference decodes, bit for bit against it."""
+    rng = np.random.default_rng(874)
+    cases = {8: (34, [0], 32), 2: (18, [0], 32), 13: (176, [0, 2], 256),
+             12: (144, [0, 2], 256), 14: (210, [208], 256)}
+    for gtype, (bb, offs, be) in cases.items():
+        row = _rand_blocks(rng, 8, bb, offs).reshape(-1)
+        n = 8 * be
+        assert np.array_equal(bits(oracle.dequant(gtype, row, n)), bits(ref.dequant(gtype, row, n)))
+
+
 def test_f16_conversions(oracle):
     """tests/test_kernels.c:199-208 known answers; every f16 bit pattern
     widens exactly (numpy's IEEE conversion)."""
