@@ -83,15 +83,27 @@ def prefill_cache(set_kv, set_pos, spec, n, seed=11, shared=False):
 
 
 def time_decode(ctx, prefill, steps, warmup, exact):
+    """Seconds of `steps` greedy steps after `warmup` untimed ones, from
+    token 1 at position `prefill`; returns (seconds, timed ids, warmup ids +
+    timed ids)."""
     ctx.set_attention(exact)
     ctx.set_position(prefill)
     tok = 1
+    first = []
     if warmup:
-        tok = int(ctx.decode_greedy(tok, warmup)[-1])
+        first = [int(i) for i in ctx.decode_greedy(tok, warmup)]
+        tok = first[-1]
     t0 = time.perf_counter()
     ids = ctx.decode_greedy(tok, steps)
     dt = time.perf_counter() - t0
-    return dt, ids
+    return dt, ids, first + [int(i) for i in ids]
+
+
+def first_logits(ctx, prefill, exact):
+    """The logits of token 1 at position `prefill` (fox_eval)."""
+    ctx.set_attention(exact)
+    ctx.set_position(prefill)
+    return ctx.eval([1]).copy()
 
 
 def token_bytes(spec, mean_pos):
@@ -127,7 +139,7 @@ def extra_case(workdir, name, prefill, steps, warmup, verify):
     prefill_cache(lambda l, k, v: ctx.set_kv(l, 0, k, v), ctx.set_position, spec, prefill,
                   shared=True)
     log(f"bench: {name} HBM load + cache prefill {time.perf_counter() - t0:.1f} s")
-    dt, ids = time_decode(ctx, prefill, steps, warmup, exact=True)
+    dt, ids, _ = time_decode(ctx, prefill, steps, warmup, exact=True)
     tok_s = steps / dt
     gbs = token_bytes(spec, prefill + warmup + steps / 2) * tok_s / 1e9
     out = {"workload": f"{name}-class dense decoder ({spec.n_layer} layers, d_model "
@@ -178,7 +190,7 @@ def stream_case(path, spec, warmup, slots=8, steps=8):
     model = rf.Model(path, mode=rf.WEIGHTS_STREAM, budget=outside + slots * layer)
     ctx = model.context(spec.n_ctx, n_batch=8)
     prefill_cache(lambda l, k, v: ctx.set_kv(l, 0, k, v), ctx.set_position, spec, PREFILL)
-    dt, ids = time_decode(ctx, PREFILL, steps, 2, exact=True)
+    dt, ids, _ = time_decode(ctx, PREFILL, steps, 2, exact=True)
     w = model.weights()
     ev = model.lib.fox_weights_evictions(w)
     ctx.close()
@@ -430,23 +442,29 @@ def timed_tokens(step, budget_s, max_tokens, min_tokens=2, warm=True):
 
 def cpu_port(path, spec, threads, budget_s, max_tokens, min_tokens=2, warm=True):
     """The oracle (oracle/liboracle.so, the C restatement of RustFox's path)
-    decoding the same file after the same injected cache rows."""
+    decoding the same file after the same injected cache rows, greedy from
+    token 1 at position PREFILL.  Returns the median step time, the number
+    of timed steps, the greedy ids of every step (the untimed first one
+    included) and the first step's logits."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from oracle_libs import Oracle  # test infrastructure: the oracle, timed as the CPU baseline
     om = Oracle().model(spec, synth.map_tensors(path, spec))
     ctx = om.context(PREFILL + max_tokens + 8, n_batch=8, n_threads=threads)
     prefill_cache(lambda l, k, v: ctx.set_kv(l, 0, k, v), ctx.set_pos, spec, PREFILL)
-    state = {"tok": 1}
+    state = {"tok": 1, "ids": [], "first": None}
 
     def step():
         t0 = time.perf_counter()
         lg = ctx.eval(np.array([state["tok"]], np.uint32))
         dt = time.perf_counter() - t0
+        if state["first"] is None:
+            state["first"] = lg.copy()
         state["tok"] = int(np.argmax(lg))
+        state["ids"].append(state["tok"])
         return dt
     med, n = timed_tokens(step, budget_s, max_tokens, min_tokens, warm)
     ctx.close()
-    return med, n
+    return med, n, state["ids"], state["first"]
 
 
 def cpu_reference(path, threads, budget_s, max_tokens, min_tokens=2):
@@ -471,12 +489,33 @@ def cpu_reference(path, threads, budget_s, max_tokens, min_tokens=2):
     return med, n
 
 
+PARITY_STEPS = 64
+
+
+def parity(gpu_ids, gpu_first, cpu_ids, cpu_first):
+    """The GPU decode against the oracle's on the same model and state:
+    greedy ids over the steps both ran, and the first step's logits."""
+    n = min(len(gpu_ids), len(cpu_ids))
+    d = np.asarray(gpu_first, np.float64) - np.asarray(cpu_first, np.float64)
+    rel = float(np.linalg.norm(d) / np.linalg.norm(np.asarray(cpu_first, np.float64)))
+    diff = [i for i in range(n) if int(gpu_ids[i]) != int(cpu_ids[i])]
+    return {"steps_compared": n, "ids_equal": not diff,
+            "first_differing_step": diff[0] if diff else None,
+            "first_logits_bit_identical": bool(np.array_equal(
+                np.asarray(gpu_first, np.float32).view(np.uint32),
+                np.asarray(cpu_first, np.float32).view(np.uint32))),
+            "rel_l2": rel}
+
+
 def cpu_baseline(path, spec, budget_s):
     threads = cpu_threads()
-    med, n = cpu_port(path, spec, threads, budget_s * 0.25, 16)
+    # the parity run: PARITY_STEPS greedy steps (the first untimed), every
+    # one's id kept; the median step time is the baseline
+    med, n, ids, first = cpu_port(path, spec, threads, 1e9, PARITY_STEPS - 1,
+                                  min_tokens=PARITY_STEPS - 1)
     log(f"bench: cpu port {1 / med:.3f} tok/s on {threads} threads ({n} tokens)")
     # one token on one thread (its pages are already in from the run above)
-    med1, n1 = cpu_port(path, spec, 1, 0.0, 1, min_tokens=1, warm=False)
+    med1, n1, _, _ = cpu_port(path, spec, 1, 0.0, 1, min_tokens=1, warm=False)
     log(f"bench: cpu port {1 / med1:.3f} tok/s on 1 thread ({n1} tokens)")
     out = {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": threads, "kind": "port",
            "sample": (f"the oracle (oracle/liboracle.so, the C restatement of RustFox's decode "
@@ -484,10 +523,12 @@ def cpu_baseline(path, spec, budget_s):
                       f"threads as RustFox splits them) decoding the same 4B TQ1_0 GGUF after "
                       f"the same {PREFILL} injected f16 N(0,1) cache rows: median of {n} "
                       f"single-token steps at positions {PREFILL + 1}..{PREFILL + n} (one "
-                      f"untimed step first)"),
+                      f"untimed step first); the same run's greedy ids and first logits are "
+                      f"the parity check of the GPU decode"),
            "one_thread": {"value": round(1.0 / med1, 4), "unit": "tok/s", "tokens": n1,
                           "note": "one step at position " + str(PREFILL + 1)},
-           "host": host_info()}
+           "host": host_info(),
+           "_parity": (ids, first)}
     try:
         r = cpu_reference(path, threads, budget_s * 0.15, 16)
         r1 = cpu_reference(path, 1, 0.0, 1, min_tokens=1) if r else None
@@ -558,11 +599,13 @@ def main():
     prefill_cache(lambda l, k, v: ctx.set_kv(l, 0, k, v), ctx.set_position, spec, PREFILL)
     log(f"bench: HBM load + cache prefill {time.perf_counter() - t0:.1f} s")
 
-    dt, ids = time_decode(ctx, PREFILL, a.steps, a.warmup, exact=True)
+    dt, ids, all_ids = time_decode(ctx, PREFILL, a.steps, a.warmup, exact=True)
     tok_s = a.steps / dt
     log(f"bench: exact attention  {tok_s:.1f} tok/s ({dt * 1e3 / a.steps:.3f} ms/token)")
-    dt_split, ids_split = time_decode(ctx, PREFILL, a.steps, a.warmup, exact=False)
+    dt_split, ids_split, all_split = time_decode(ctx, PREFILL, a.steps, a.warmup, exact=False)
     log(f"bench: split attention  {a.steps / dt_split:.1f} tok/s")
+    lg_exact = first_logits(ctx, PREFILL, True)
+    lg_split = first_logits(ctx, PREFILL, False)
     ctx.close()
     model.close()
 
@@ -602,11 +645,17 @@ def main():
                 "us_per_launch": main_case["us_per_launch"]}
 
     cpu = None
+    par = par_split = None
     if not a.no_cpu:
         try:
             cpu = cpu_baseline(path, spec, a.cpu_seconds)
             if cpu:
                 log(f"bench: cpu baseline ({cpu['kind']}) {cpu['value']} tok/s on {cpu['cores']} threads")
+                cpu_ids, cpu_first = cpu.pop("_parity")
+                par = parity(all_ids, lg_exact, cpu_ids, cpu_first)
+                par_split = parity(all_split, lg_split, cpu_ids, cpu_first)
+                log(f"bench: parity against the oracle: {par}")
+                log(f"bench: split attention against the oracle: {par_split}")
         except Exception as e:  # the GPU number stands without it
             log(f"bench: cpu baseline failed: {e}")
 
@@ -639,7 +688,10 @@ def main():
                    "attention": "exact (reference summation order)"},
         "roofline": roof,
         "cpu_baseline": cpu,
-        "split_attention_tok_s": round(a.steps / dt_split, 2),
+        "parity": par,
+        "split_attention": {"tok_s": round(a.steps / dt_split, 2), "parity": par_split,
+                            "note": "positions split over workgroups with a merge of partial "
+                                    "softmaxes (float reassociation); not the headline"},
         "decode_hbm_gbs": round(per_token_bytes * tok_s / 1e9, 1),
         "decode_frac_of_hbm": round(per_token_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4),
         "extra": extra,

@@ -512,210 +512,106 @@ __global__ void attn_merge(const float *__restrict__ part, int n_head, int hd, i
 // ---- attention in the reference's order (src/forward.c:222-257,
 // src/ops.c:24-39), bit for bit:
 //   score_j = (sum_d q_d k_jd, summed in d order) * (1 / sqrtf(hd));
-//   softmax: max, e_j = expf(score_j - max), sum in j order, e_j * (1/sum);
-//   out_d = sum in j order of a_j v_jd.
-// Each in-order sum is one lane's chain.  Three kernels: scores (a lane per
-// position, K tile in LDS) with per-tile maxima; softmax (one lane runs the
-// position-order sum from LDS); values (a lane per output column, walking
-// the interleaved V and the weights four positions per load).
+//   softmax: max (a NaN first score stays the maximum, other NaNs are
+//     skipped), e_j = expf(score_j - max), sum in j order, a_j = e_j * (1/sum)
+//     when the sum is positive;
+//   out_d = sum in j order of a_j v_jd (each product rounded, then added).
+// Each in-order sum is one lane's dependent chain.  Every hand-over inside a
+// kernel is at a workgroup barrier; between kernels, at the launch boundary.
+//   attn_qk   scores and per-64-position-tile maxima: a workgroup per (tile,
+//             kv head, up to QK_TPW tokens), the K tile and the queries in
+//             LDS, a lane per (query head, position);
+//   attn_av   one token: a workgroup per (kv head, AV_CH output chains): the
+//             head maxima, then e_j in blocks while one wave runs the softmax
+//             sums over the block before, then a_j, then the products a_j v_jd
+//             in blocks (V streamed from HBM a few blocks ahead) while the
+//             chain wave adds the block before;
+//   attn_softmax_x + attn_values_x   several tokens, or a context longer than
+//             attn_av's LDS holds: the softmax per (head, token) in place in
+//             the scores, then a lane per (head, column) walking V and the
+//             weights.
 
 #define SC_TILE 64
-#define SC_CQ 8                     // quads (4 dimensions) per chunk of a K row
+#define QK_TPW 4            // tokens per scores workgroup (the K tile is read once for them)
+#define ATT_LDS_MAX (159 * 1024)
 
-// vmcnt(n) alone (s_waitcnt fields of gfx9: vmcnt [3:0] and [15:14],
-// expcnt [6:4], lgkmcnt [11:8]; the others at their maximum)
-#define VMCNT_ONLY(n) ((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4) | (15 << 8))
-
-// s_waitcnt vmcnt(n) for n known once loops are unrolled (the instruction
-// takes an immediate)
-__device__ __forceinline__ void wait_vmcnt(int n)
+// A workgroup of 256 threads per (64-position tile, kv head, QK_TPW tokens):
+// the tile's K rows (plain loads, row stride padded by one quad against bank
+// conflicts) and one token's G query heads in LDS; item i = (query head
+// i / 64, position i % 64), so the lanes of a wave share one query head (its
+// reads are broadcasts).  Positions at or past the token's end are neither
+// computed nor written.
+template <int G>
+__global__ __launch_bounds__(256) void attn_qk(const float *__restrict__ q, size_t q_stride,
+                                               const float *__restrict__ kc, int n_head_kv,
+                                               int hd, const uint32_t *__restrict__ pos,
+                                               int n_ctx, size_t att_stride,
+                                               float *__restrict__ att, float *__restrict__ tmax,
+                                               int n_tiles, int M)
 {
-    switch (n) {
-    case 0: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(0)); break;
-    case 1: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(1)); break;
-    case 2: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(2)); break;
-    case 3: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(3)); break;
-    case 4: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(4)); break;
-    case 5: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(5)); break;
-    case 6: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(6)); break;
-    case 7: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(7)); break;
-    case 8: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(8)); break;
-    case 10: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(10)); break;
-    case 12: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(12)); break;
-    case 14: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(14)); break;
-    default: __builtin_amdgcn_s_waitcnt(VMCNT_ONLY(0)); break;
-    }
-}
-
-// global -> LDS copy of 16 bytes per lane: lane l's bytes land at dst + 16 l
-// (dst wave-uniform), counted by vmcnt like a load
-__device__ __forceinline__ void copy_to_lds16(const void *src, void *dst)
-{
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
-}
-
-// the products of one chunk (SC_CQ quads) added to acc in dimension order:
-// every read of the chunk is issued before the first add (with FULL the
-// chunk is known to be whole, and no per-quad branch splits the reads from
-// the adds)
-template <bool FULL>
-__device__ __forceinline__ float sc_chunk(float acc, const float4 *qr, const float4 *kr, int sw,
-                                          int c, int nv)
-{
-    float4 qv[SC_CQ], kv[SC_CQ];
-#pragma unroll
-    for (int j = 0; j < SC_CQ; j++) {
-        if (FULL || SC_CQ * c + j < nv) {
-            qv[j] = qr[j];
-            kv[j] = kr[j ^ sw];
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < SC_CQ; j++) {
-        if (FULL || SC_CQ * c + j < nv) {
-            acc = acc + qv[j].x * kv[j].x;
-            acc = acc + qv[j].y * kv[j].y;
-            acc = acc + qv[j].z * kv[j].z;
-            acc = acc + qv[j].w * kv[j].w;
-        }
-    }
-    return acc;
-}
-
-// tokens per scores workgroup (27B-class heads, 8192 positions, 8 tokens:
-// 241.6 us for the whole attention with one, 220.1 with two, 213.4 with
-// four, 216.3 with eight; 4B-class heads at 2048: 57.5 to 58.3 us up to four,
-// 63.9 with eight)
-#define SC_TPW 4
-// One workgroup per (64-position tile, kv head, TPW tokens); wave w
-// takes query heads w, w + 4, ... of the kv head, one lane per position.  The
-// tile's K rows arrive in NCH chunks of 32 dimensions, copied straight into
-// LDS: every copy is issued at the start, and the first token's dot products
-// of chunk c run once that chunk is in, while the later ones are still
-// arriving (each sum stays in head-dimension order, chunk after chunk).  The
-// later tokens reuse the tile (only their query heads are copied), so K is
-// read once for every TPW tokens.  A chunk holds 64 rows of 8
-// quads (128 B a row); quad j of row r sits in slot j ^ ((r >> 1) & 7), so
-// that sixteen consecutive lanes' reads of one quad fall in different banks
-// (rows r and r + 1 differ in the 32-bank half, r and r + 2 .. r + 14 in the
-// slot).
-template <int NCH>
-__global__ __launch_bounds__(256) void attn_scores_x(const float *__restrict__ q,
-                                                     size_t q_stride,
-                                                     const float *__restrict__ kc, int n_head,
-                                                     int n_head_kv, int hd,
-                                                     const uint32_t *__restrict__ pos,
-                                                     int n_ctx, size_t att_stride,
-                                                     float *__restrict__ att,
-                                                     float *__restrict__ tmax, int n_tiles,
-                                                     int M, int tpw)
-{
-    // one array per chunk: separate objects, so that waiting for a chunk's
-    // copies does not wait for the later chunks' copies
-    __shared__ float4 kq0[SC_TILE * SC_CQ], kq1[NCH > 1 ? SC_TILE * SC_CQ : 1],
-        kq2[NCH > 2 ? SC_TILE * SC_CQ : 1], kq3[NCH > 3 ? SC_TILE * SC_CQ : 1],
-        kq4[NCH > 4 ? SC_TILE * SC_CQ : 1], kq5[NCH > 5 ? SC_TILE * SC_CQ : 1],
-        kq6[NCH > 6 ? SC_TILE * SC_CQ : 1], kq7[NCH > 7 ? SC_TILE * SC_CQ : 1];
-    __shared__ float4 qq[ATT_MAXG * ATT_MAXHD / 4];             // [gqa][hd / 4]
-    auto kq = [&](int c) -> float4 * {                          // chunk c: [64 rows][8 slots]
-        return c == 0 ? kq0 : c == 1 ? kq1 : c == 2 ? kq2 : c == 3 ? kq3
-             : c == 4 ? kq4 : c == 5 ? kq5 : c == 6 ? kq6 : kq7;
-    };
+    extern __shared__ float4 qk_lds[];
+    const int hd4 = hd >> 2, ks = hd4 + 1;
+    float4 *Ks = qk_lds;                           // [SC_TILE][ks]
+    float4 *Qs = qk_lds + SC_TILE * ks;           // [G][hd4]
+    const int tid = threadIdx.x, lane = tid & 63;
     const int tile = blockIdx.x, p0 = tile * SC_TILE, kvh = blockIdx.y;
-    const int lane = threadIdx.x & 63, wave = wave_index();
-    const int gqa = n_head / n_head_kv, kvd = n_head_kv * hd, nv = hd >> 2;
-    // token t sees positions below upto(t), which grows with t: the first
-    // token that reaches this tile, and the rows the last one uses
-    auto upto_of = [&](int t) {
-        return (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
-    };
-    // this workgroup's tokens: tz .. t_end - 1
-    const int tz = (int)blockIdx.z * tpw, t_end = min(tz + tpw, M);
+    const int n_head = n_head_kv * G, kvd = n_head_kv * hd;
+    const size_t pz = pos[0];
+    auto upto_of = [&](int t) { return (int)min(pz + (size_t)t + 1, (size_t)n_ctx); };
+    const int tz = (int)blockIdx.z * QK_TPW, t_end = min(tz + QK_TPW, M);
     const int upto_last = upto_of(t_end - 1);
-    if (p0 >= upto_last) return;
-    int t0 = tz;
-    while (upto_of(t0) <= p0) t0++;                         // (uniform)
-    const int pn_last = upto_last - p0 < SC_TILE ? upto_last - p0 : SC_TILE;
-    // the query heads: blocks of 64 quads, wave w takes blocks w, w + 4
-    const int nqq = gqa * nv, nqb = (nqq + 63) >> 6;
-    constexpr int QB = ATT_MAXG * ATT_MAXHD / 4 / 64 / 4;   // blocks per wave at most
-    auto copy_q = [&](int t) {
-        const float *qbase = q + (size_t)t * q_stride + (size_t)kvh * gqa * hd;
+    if (p0 >= upto_last) return;                   // (uniform)
+    const int rows = min(SC_TILE, upto_last - p0);
+    // the K tile: float4 f of the tile is (row f / hd4, quad f % hd4); eight
+    // loads in flight per thread before they go to LDS
+    const float4 *kb = (const float4 *)(kc + (size_t)p0 * kvd + (size_t)kvh * hd);
+    const int nf = rows * hd4;
+    for (int f0 = 0; f0 < nf; f0 += 8 * 256) {
+        float4 r[8];
 #pragma unroll
-        for (int k = 0; k < QB; k++) {
-            const int b = wave + 4 * k;
-            if (b < nqb) copy_to_lds16(qbase + 4 * min(64 * b + lane, nqq - 1), qq + 64 * b);
+        for (int k = 0; k < 8; k++) {
+            const int f = min(f0 + k * 256 + tid, nf - 1);
+            r[k] = kb[(size_t)(f / hd4) * (kvd / 4) + f % hd4];
         }
-    };
-    copy_q(t0);
-    // K: chunk c is 8 blocks of 8 rows; wave w copies blocks 2w and 2w + 1
-    // (the rows of the last token; an earlier token ignores those past its own)
-    const float *kbase = kc + (size_t)p0 * kvd + (size_t)kvh * hd;
 #pragma unroll
-    for (int c = 0; c < NCH; c++) {
-#pragma unroll
-        for (int r = 0; r < 2; r++) {
-            const int b = 2 * wave + r, row = 8 * b + (lane >> 3);
-            const int j = (lane & 7) ^ ((row >> 1) & 7);
-            const int cq = min(SC_CQ * c + j, nv - 1);
-            copy_to_lds16(kbase + (size_t)min(row, pn_last - 1) * kvd + 4 * cq,
-                          kq(c) + 8 * b * SC_CQ);
+        for (int k = 0; k < 8; k++) {
+            const int f = f0 + k * 256 + tid;
+            if (f < nf) Ks[(f / hd4) * ks + f % hd4] = r[k];
         }
     }
-    const bool full = nv == NCH * SC_CQ;            // (uniform) every chunk whole
-    constexpr int HW = ATT_MAXG / 4;                // heads per wave at most
     const float scale = fox_div(1.0f, fox_sqrtf((float)hd));
+    int t0 = tz;
+    while (upto_of(t0) <= p0) t0++;                // (uniform) the first token reaching the tile
     for (int t = t0; t < t_end; t++) {
         const int upto = upto_of(t);
-        const int pn = upto - p0 < SC_TILE ? upto - p0 : SC_TILE;
-        const bool ok = lane < pn;
-        const int row = ok ? lane : 0, sw = (row >> 1) & 7;
-        if (t > t0) {
-            // every wave is done with the previous token's query heads
-            __syncthreads();
-            copy_q(t);
-        }
-        float a[HW];
+        if (t > t0) __syncthreads();              // every item of the previous token is done
+        const float4 *qb = (const float4 *)(q + (size_t)t * q_stride + (size_t)kvh * G * hd);
+        for (int f = tid; f < G * hd4; f += 256) Qs[f] = qb[f];
+        __syncthreads();
 #pragma unroll
-        for (int h = 0; h < HW; h++) a[h] = 0.0f;
-#pragma unroll
-        for (int c = 0; c < NCH; c++) {
-            // this wave's copies of chunk c (and the query heads) are in once
-            // at most 2 (NCH - 1 - c) copies are pending (later tokens: only
-            // their query heads are pending); the barrier covers the other
-            // waves' copies
-            if (t == t0) {
-                wait_vmcnt(2 * (NCH - 1 - c));
-            } else if (c == 0) {
-                wait_vmcnt(0);
-            }
-            if (t == t0 || c == 0) {
-                __builtin_amdgcn_s_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-            }
-            const float4 *kr = kq(c) + row * SC_CQ;
-#pragma unroll
-            for (int h = 0; h < HW; h++) {
-                const int g = wave + 4 * h;
-                if (g < gqa) {
-                    const float4 *qr = qq + g * nv + SC_CQ * c;
-                    a[h] = full ? sc_chunk<true>(a[h], qr, kr, sw, c, nv)
-                                : sc_chunk<false>(a[h], qr, kr, sw, c, nv);
+        for (int it = 0; it < (G * SC_TILE + 255) / 256; it++) {
+            const int item = it * 256 + tid;
+            if (G * SC_TILE % 256 != 0 && item >= G * SC_TILE) break;   // (wave-uniform)
+            const int g = item >> 6, pl = item & 63, p = p0 + pl;
+            const bool ok = p < upto;
+            float sc = -INFINITY;
+            if (ok) {
+                const float4 *kr = Ks + pl * ks, *qr = Qs + g * hd4;
+                float acc = 0.0f;
+                for (int d = 0; d < hd4; d++) {
+                    const float4 kv = kr[d], qv = qr[d];
+                    acc = acc + qv.x * kv.x;
+                    acc = acc + qv.y * kv.y;
+                    acc = acc + qv.z * kv.z;
+                    acc = acc + qv.w * kv.w;
                 }
+                sc = acc * scale;
+                att[((size_t)t * n_head + (size_t)kvh * G + g) * att_stride + p] = sc;
             }
-        }
-#pragma unroll
-        for (int h = 0; h < HW; h++) {
-            const int g = wave + 4 * h;
-            if (g < gqa) {
-                const float sc = a[h] * scale;
-                const int hh = kvh * gqa + g;
-                if (ok) att[((size_t)t * n_head + hh) * att_stride + p0 + lane] = sc;
-                // tile maximum, NaN never taken
-                const float m = wave_reduce((ok && sc == sc) ? sc : -INFINITY, -INFINITY,
-                                            [](float x, float y) { return y > x ? y : x; });
-                if (lane == 0) tmax[((size_t)t * n_head + hh) * n_tiles + tile] = m;
-            }
+            // the tile maximum, NaN never taken
+            const float m = wave_reduce((ok && sc == sc) ? sc : -INFINITY, -INFINITY,
+                                        [](float x, float y) { return y > x ? y : x; });
+            if (lane == 0) tmax[((size_t)t * n_head + (size_t)kvh * G + g) * n_tiles + tile] = m;
         }
     }
 }
@@ -845,667 +741,233 @@ __global__ __launch_bounds__(64) void attn_values_x(const float *__restrict__ at
     out[(size_t)t * out_stride + (size_t)h * hd + d] = acc;
 }
 
-// ---- fused softmax + values (exact order), one workgroup per (kv head,
-// column slice, token), 16 waves; the kv head's G query heads x 64/G columns
-// make the 64 lanes of wave 0:
-//   waves 0-3: head maxima from the per-tile maxima (the scores themselves
-//     are already on their way to the loader waves);
-//   loader waves: e_j = expf(s_j - max) into LDS for the G heads, in rounds of
-//     SV_EXR positions, each round counted when a wave completes it;
-//   wave 0: one lane per head runs the position-order sum, round by round as
-//     the rounds complete, then 1/sum;
-//   loader waves: stream the slice's V columns (each 16-byte quad loaded once,
-//     two 64-position tiles in flight per wave from the start of the kernel),
-//     multiply by the G heads' a_j and hand the products to wave 0 through a
-//     ring of LDS stages;
-//   wave 0: one lane per (head, column) adds the products in position order.
-// Stages are handed over with workgroup-scope release/acquire flags in LDS;
-// every wait is bounded (a wave that times out writes NaN, sets its bit in the
-// device error word and leaves).
-#define SV_WAVES 16
-#define SV_QT 16                    // quads (4 positions) per stage
-#define SV_NP_MAX 8                 // product stages: as many as fit beside the weights
-#define SV_NP_MIN 3
-#define SV_LOADERS 12               // waves 1-3, 5-7, 9-11, 13-15
-#define SV_LDS_MAX (159 * 1024)     // dynamic LDS of the kernel (160 KB less its static part)
-#define SV_STAGE (SV_QT * 64 * 16)  // bytes per product stage
-#define SV_EXR (SV_LOADERS * 64)    // positions per exp round
-#define SV_EXP_PF 3                 // exp rounds whose scores are loaded up front
-#define SV_VPF 8                    // product units of V in flight per loader
-#define SV_SPIN (1 << 22)
-#define SV_IDLE_SLEEP 2             // s_sleep units (64 clocks each) between idle polls
 
-// v of lane (quad base + sel) for each lane, sel from a quad_perm control
-// word known at compile time (DPP, no LDS traffic)
-__device__ __forceinline__ float dpp_bcast(float v, int ctl)
-{
-    switch (ctl) {
-    case 0x00: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x00, 0xF, 0xF, false));
-    case 0x55: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x55, 0xF, 0xF, false));
-    case 0xAA: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xAA, 0xF, 0xF, false));
-    case 0xFF: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xFF, 0xF, 0xF, false));
-    case 0xA0: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xA0, 0xF, 0xF, false));
-    default:   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xF5, 0xF, 0xF, false));
-    }
-}
+// ---- one token: softmax and values in one workgroup per (kv head, AV_CH
+// output chains), 256 threads.  The chains are (query head g, column c) for
+// the G heads of the kv head and DC = AV_CH / G columns; wave 0 runs them
+// (lane g * DC + c), waves 1-3 produce its operands.
+//   1. head maxima from the tile maxima (all waves);
+//   2. blocks of AV_EB positions: waves 1-3 write e_j = expf(s_j - max) of
+//      block k to LDS while wave 0 (lane g) adds block k - 1 to head g's
+//      softmax sum; a barrier between blocks;
+//   3. 1 / sum, and a_j = e_j * (1/sum) in place (all waves);
+//   4. blocks of AV_VB quads: waves 1-3 multiply block b's V quads (loaded
+//      AV_VD blocks ahead, from the start of the kernel) by a_j into one of two
+//      product buffers while wave 0 adds block b - 1's products to its
+//      chains; a barrier between blocks.
+// A chain lane reads its operands four at a time from LDS, the reads of
+// one group in flight while the group before is added.
+#define AV_CH 16
+#define AV_EB 768           // positions of an exp block (waves 1-3, four per lane)
+#define AV_VB 48            // quads (192 positions) of a value block
+#define AV_VD 4             // value blocks of V in flight per producer lane
+#define AV_PS (AV_VB + 1)   // quads per chain in a product buffer (one quad of padding)
 
-// Hand-over flags live in LDS and guard LDS data only, so the fences order
-// LDS accesses only: global loads a wave has in flight stay in flight.
-__device__ __forceinline__ int sv_load(int *flag)
+// acc + x_0 + ... + x_{4n-1} over float4 p[0 .. n) of LDS, in order; eight
+// quads read ahead of the adds
+__device__ __forceinline__ float chain_quads(float acc, const float4 *p, int n)
 {
-    return __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-
-// (read as a wave-uniform value: tests on it are then scalar branches and
-// the loops around them stay uniform)
-__device__ __forceinline__ int sv_peek(int *flag)
-{
-    return __builtin_amdgcn_readfirstlane(sv_load(flag));
-}
-
-// (a tight loop: waves that poll with s_sleep 1 between reads slow the
-// dependent adds of a wave on another SIMD by about a tenth; polling
-// without a sleep does not)
-__device__ __forceinline__ bool sv_wait_ge(int *flag, int v)
-{
-    for (int n = 0; n < SV_SPIN; n++) {
-        if (sv_peek(flag) >= v) {
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-            return true;
+    int i = 0;
+    if (n >= 16) {
+        float4 a[8], b[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) a[k] = p[k];
+        for (; i + 16 <= n; i += 16) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) b[k] = p[i + 8 + k];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                acc = acc + a[k].x; acc = acc + a[k].y; acc = acc + a[k].z; acc = acc + a[k].w;
+            }
+            const int nx = i + 16 + 8 <= n ? i + 16 : i;   // (the next group, if whole)
+#pragma unroll
+            for (int k = 0; k < 8; k++) a[k] = p[nx + k];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                acc = acc + b[k].x; acc = acc + b[k].y; acc = acc + b[k].z; acc = acc + b[k].w;
+            }
         }
     }
-    return false;
-}
-
-// The same for waves that are not on the chains' critical path: a read every
-// few hundred cycles, so that their polling does not queue ahead of the
-// chain wave's LDS reads
-__device__ __forceinline__ bool sv_wait_ge_idle(int *flag, int v)
-{
-    for (int n = 0; n < SV_SPIN; n++) {
-        if (sv_peek(flag) >= v) {
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-            return true;
-        }
-        __builtin_amdgcn_s_sleep(SV_IDLE_SLEEP);
-    }
-    return false;
-}
-
-// a timed-out wait reports itself in the device error word (read by the
-// host after the pass: fox_gpu_take_error)
-__device__ __forceinline__ void sv_error(unsigned *err, unsigned bit)
-{
-    __hip_atomic_fetch_or(err, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void sv_signal(int *flag, int v)
-{
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __hip_atomic_store(flag, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-
-// acc + x_0 + x_1 + ... over 4 * nq floats of LDS, in index order.  A
-// dependent add chain is bound by the wave's instruction issue, so the
-// operand reads must cost as few instructions as possible: banks of eight
-// quads alternate, the eight reads of one bank (ds_read_b128 at constant
-// offsets from one address, one wait) in flight while the other bank's 32
-// adds run.  One block of 64 quads is one asm statement (reads, waits and
-// adds, v64-v127 its banks): compiled from C, the reads of such a block are
-// hoisted and reordered across the adds, and a bank carried from one loop
-// iteration to the next is copied every iteration.  LDS reads complete in
-// order, so lgkmcnt(8) after a bank's reads means the previous bank is in.
-// Read-write operands are early-clobber ("+&"): the asm writes them before
-// it has read every input, so no input may share their registers (an input
-// equal to acc's initial bits would otherwise be given acc's register).
-// (Measured on gfx950, one wave: 2.5 ns per add this way, 4 ns with a wait
-// and a read between every four adds, 1.8 ns from registers.)
-// the LDS address of a pointer into LDS
-__device__ __forceinline__ uint32_t lds_addr(const void *p)
-{
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
-}
-
-__device__ __forceinline__ float chain64_lds(float acc, const float4 *q)
-{
-    const uint32_t p = lds_addr(q);
-    asm volatile(
-        "ds_read_b128 v[64:67], %[p] offset:0\n" "ds_read_b128 v[68:71], %[p] offset:16\n" "ds_read_b128 v[72:75], %[p] offset:32\n" "ds_read_b128 v[76:79], %[p] offset:48\n"
-        "ds_read_b128 v[80:83], %[p] offset:64\n" "ds_read_b128 v[84:87], %[p] offset:80\n" "ds_read_b128 v[88:91], %[p] offset:96\n" "ds_read_b128 v[92:95], %[p] offset:112\n"
-        "ds_read_b128 v[96:99], %[p] offset:128\n" "ds_read_b128 v[100:103], %[p] offset:144\n" "ds_read_b128 v[104:107], %[p] offset:160\n" "ds_read_b128 v[108:111], %[p] offset:176\n"
-        "ds_read_b128 v[112:115], %[p] offset:192\n" "ds_read_b128 v[116:119], %[p] offset:208\n" "ds_read_b128 v[120:123], %[p] offset:224\n" "ds_read_b128 v[124:127], %[p] offset:240\n"
-        "s_waitcnt lgkmcnt(8)\n" "v_add_f32 %[acc], %[acc], v64\n" "v_add_f32 %[acc], %[acc], v65\n" "v_add_f32 %[acc], %[acc], v66\n"
-        "v_add_f32 %[acc], %[acc], v67\n" "v_add_f32 %[acc], %[acc], v68\n" "v_add_f32 %[acc], %[acc], v69\n" "v_add_f32 %[acc], %[acc], v70\n"
-        "v_add_f32 %[acc], %[acc], v71\n" "v_add_f32 %[acc], %[acc], v72\n" "v_add_f32 %[acc], %[acc], v73\n" "v_add_f32 %[acc], %[acc], v74\n"
-        "v_add_f32 %[acc], %[acc], v75\n" "v_add_f32 %[acc], %[acc], v76\n" "v_add_f32 %[acc], %[acc], v77\n" "v_add_f32 %[acc], %[acc], v78\n"
-        "v_add_f32 %[acc], %[acc], v79\n" "v_add_f32 %[acc], %[acc], v80\n" "v_add_f32 %[acc], %[acc], v81\n" "v_add_f32 %[acc], %[acc], v82\n"
-        "v_add_f32 %[acc], %[acc], v83\n" "v_add_f32 %[acc], %[acc], v84\n" "v_add_f32 %[acc], %[acc], v85\n" "v_add_f32 %[acc], %[acc], v86\n"
-        "v_add_f32 %[acc], %[acc], v87\n" "v_add_f32 %[acc], %[acc], v88\n" "v_add_f32 %[acc], %[acc], v89\n" "v_add_f32 %[acc], %[acc], v90\n"
-        "v_add_f32 %[acc], %[acc], v91\n" "v_add_f32 %[acc], %[acc], v92\n" "v_add_f32 %[acc], %[acc], v93\n" "v_add_f32 %[acc], %[acc], v94\n"
-        "v_add_f32 %[acc], %[acc], v95\n" "ds_read_b128 v[64:67], %[p] offset:256\n" "ds_read_b128 v[68:71], %[p] offset:272\n" "ds_read_b128 v[72:75], %[p] offset:288\n"
-        "ds_read_b128 v[76:79], %[p] offset:304\n" "ds_read_b128 v[80:83], %[p] offset:320\n" "ds_read_b128 v[84:87], %[p] offset:336\n" "ds_read_b128 v[88:91], %[p] offset:352\n"
-        "ds_read_b128 v[92:95], %[p] offset:368\n" "s_waitcnt lgkmcnt(8)\n" "v_add_f32 %[acc], %[acc], v96\n" "v_add_f32 %[acc], %[acc], v97\n"
-        "v_add_f32 %[acc], %[acc], v98\n" "v_add_f32 %[acc], %[acc], v99\n" "v_add_f32 %[acc], %[acc], v100\n" "v_add_f32 %[acc], %[acc], v101\n"
-        "v_add_f32 %[acc], %[acc], v102\n" "v_add_f32 %[acc], %[acc], v103\n" "v_add_f32 %[acc], %[acc], v104\n" "v_add_f32 %[acc], %[acc], v105\n"
-        "v_add_f32 %[acc], %[acc], v106\n" "v_add_f32 %[acc], %[acc], v107\n" "v_add_f32 %[acc], %[acc], v108\n" "v_add_f32 %[acc], %[acc], v109\n"
-        "v_add_f32 %[acc], %[acc], v110\n" "v_add_f32 %[acc], %[acc], v111\n" "v_add_f32 %[acc], %[acc], v112\n" "v_add_f32 %[acc], %[acc], v113\n"
-        "v_add_f32 %[acc], %[acc], v114\n" "v_add_f32 %[acc], %[acc], v115\n" "v_add_f32 %[acc], %[acc], v116\n" "v_add_f32 %[acc], %[acc], v117\n"
-        "v_add_f32 %[acc], %[acc], v118\n" "v_add_f32 %[acc], %[acc], v119\n" "v_add_f32 %[acc], %[acc], v120\n" "v_add_f32 %[acc], %[acc], v121\n"
-        "v_add_f32 %[acc], %[acc], v122\n" "v_add_f32 %[acc], %[acc], v123\n" "v_add_f32 %[acc], %[acc], v124\n" "v_add_f32 %[acc], %[acc], v125\n"
-        "v_add_f32 %[acc], %[acc], v126\n" "v_add_f32 %[acc], %[acc], v127\n" "ds_read_b128 v[96:99], %[p] offset:384\n" "ds_read_b128 v[100:103], %[p] offset:400\n"
-        "ds_read_b128 v[104:107], %[p] offset:416\n" "ds_read_b128 v[108:111], %[p] offset:432\n" "ds_read_b128 v[112:115], %[p] offset:448\n" "ds_read_b128 v[116:119], %[p] offset:464\n"
-        "ds_read_b128 v[120:123], %[p] offset:480\n" "ds_read_b128 v[124:127], %[p] offset:496\n" "s_waitcnt lgkmcnt(8)\n" "v_add_f32 %[acc], %[acc], v64\n"
-        "v_add_f32 %[acc], %[acc], v65\n" "v_add_f32 %[acc], %[acc], v66\n" "v_add_f32 %[acc], %[acc], v67\n" "v_add_f32 %[acc], %[acc], v68\n"
-        "v_add_f32 %[acc], %[acc], v69\n" "v_add_f32 %[acc], %[acc], v70\n" "v_add_f32 %[acc], %[acc], v71\n" "v_add_f32 %[acc], %[acc], v72\n"
-        "v_add_f32 %[acc], %[acc], v73\n" "v_add_f32 %[acc], %[acc], v74\n" "v_add_f32 %[acc], %[acc], v75\n" "v_add_f32 %[acc], %[acc], v76\n"
-        "v_add_f32 %[acc], %[acc], v77\n" "v_add_f32 %[acc], %[acc], v78\n" "v_add_f32 %[acc], %[acc], v79\n" "v_add_f32 %[acc], %[acc], v80\n"
-        "v_add_f32 %[acc], %[acc], v81\n" "v_add_f32 %[acc], %[acc], v82\n" "v_add_f32 %[acc], %[acc], v83\n" "v_add_f32 %[acc], %[acc], v84\n"
-        "v_add_f32 %[acc], %[acc], v85\n" "v_add_f32 %[acc], %[acc], v86\n" "v_add_f32 %[acc], %[acc], v87\n" "v_add_f32 %[acc], %[acc], v88\n"
-        "v_add_f32 %[acc], %[acc], v89\n" "v_add_f32 %[acc], %[acc], v90\n" "v_add_f32 %[acc], %[acc], v91\n" "v_add_f32 %[acc], %[acc], v92\n"
-        "v_add_f32 %[acc], %[acc], v93\n" "v_add_f32 %[acc], %[acc], v94\n" "v_add_f32 %[acc], %[acc], v95\n" "ds_read_b128 v[64:67], %[p] offset:512\n"
-        "ds_read_b128 v[68:71], %[p] offset:528\n" "ds_read_b128 v[72:75], %[p] offset:544\n" "ds_read_b128 v[76:79], %[p] offset:560\n" "ds_read_b128 v[80:83], %[p] offset:576\n"
-        "ds_read_b128 v[84:87], %[p] offset:592\n" "ds_read_b128 v[88:91], %[p] offset:608\n" "ds_read_b128 v[92:95], %[p] offset:624\n" "s_waitcnt lgkmcnt(8)\n"
-        "v_add_f32 %[acc], %[acc], v96\n" "v_add_f32 %[acc], %[acc], v97\n" "v_add_f32 %[acc], %[acc], v98\n" "v_add_f32 %[acc], %[acc], v99\n"
-        "v_add_f32 %[acc], %[acc], v100\n" "v_add_f32 %[acc], %[acc], v101\n" "v_add_f32 %[acc], %[acc], v102\n" "v_add_f32 %[acc], %[acc], v103\n"
-        "v_add_f32 %[acc], %[acc], v104\n" "v_add_f32 %[acc], %[acc], v105\n" "v_add_f32 %[acc], %[acc], v106\n" "v_add_f32 %[acc], %[acc], v107\n"
-        "v_add_f32 %[acc], %[acc], v108\n" "v_add_f32 %[acc], %[acc], v109\n" "v_add_f32 %[acc], %[acc], v110\n" "v_add_f32 %[acc], %[acc], v111\n"
-        "v_add_f32 %[acc], %[acc], v112\n" "v_add_f32 %[acc], %[acc], v113\n" "v_add_f32 %[acc], %[acc], v114\n" "v_add_f32 %[acc], %[acc], v115\n"
-        "v_add_f32 %[acc], %[acc], v116\n" "v_add_f32 %[acc], %[acc], v117\n" "v_add_f32 %[acc], %[acc], v118\n" "v_add_f32 %[acc], %[acc], v119\n"
-        "v_add_f32 %[acc], %[acc], v120\n" "v_add_f32 %[acc], %[acc], v121\n" "v_add_f32 %[acc], %[acc], v122\n" "v_add_f32 %[acc], %[acc], v123\n"
-        "v_add_f32 %[acc], %[acc], v124\n" "v_add_f32 %[acc], %[acc], v125\n" "v_add_f32 %[acc], %[acc], v126\n" "v_add_f32 %[acc], %[acc], v127\n"
-        "ds_read_b128 v[96:99], %[p] offset:640\n" "ds_read_b128 v[100:103], %[p] offset:656\n" "ds_read_b128 v[104:107], %[p] offset:672\n" "ds_read_b128 v[108:111], %[p] offset:688\n"
-        "ds_read_b128 v[112:115], %[p] offset:704\n" "ds_read_b128 v[116:119], %[p] offset:720\n" "ds_read_b128 v[120:123], %[p] offset:736\n" "ds_read_b128 v[124:127], %[p] offset:752\n"
-        "s_waitcnt lgkmcnt(8)\n" "v_add_f32 %[acc], %[acc], v64\n" "v_add_f32 %[acc], %[acc], v65\n" "v_add_f32 %[acc], %[acc], v66\n"
-        "v_add_f32 %[acc], %[acc], v67\n" "v_add_f32 %[acc], %[acc], v68\n" "v_add_f32 %[acc], %[acc], v69\n" "v_add_f32 %[acc], %[acc], v70\n"
-        "v_add_f32 %[acc], %[acc], v71\n" "v_add_f32 %[acc], %[acc], v72\n" "v_add_f32 %[acc], %[acc], v73\n" "v_add_f32 %[acc], %[acc], v74\n"
-        "v_add_f32 %[acc], %[acc], v75\n" "v_add_f32 %[acc], %[acc], v76\n" "v_add_f32 %[acc], %[acc], v77\n" "v_add_f32 %[acc], %[acc], v78\n"
-        "v_add_f32 %[acc], %[acc], v79\n" "v_add_f32 %[acc], %[acc], v80\n" "v_add_f32 %[acc], %[acc], v81\n" "v_add_f32 %[acc], %[acc], v82\n"
-        "v_add_f32 %[acc], %[acc], v83\n" "v_add_f32 %[acc], %[acc], v84\n" "v_add_f32 %[acc], %[acc], v85\n" "v_add_f32 %[acc], %[acc], v86\n"
-        "v_add_f32 %[acc], %[acc], v87\n" "v_add_f32 %[acc], %[acc], v88\n" "v_add_f32 %[acc], %[acc], v89\n" "v_add_f32 %[acc], %[acc], v90\n"
-        "v_add_f32 %[acc], %[acc], v91\n" "v_add_f32 %[acc], %[acc], v92\n" "v_add_f32 %[acc], %[acc], v93\n" "v_add_f32 %[acc], %[acc], v94\n"
-        "v_add_f32 %[acc], %[acc], v95\n" "ds_read_b128 v[64:67], %[p] offset:768\n" "ds_read_b128 v[68:71], %[p] offset:784\n" "ds_read_b128 v[72:75], %[p] offset:800\n"
-        "ds_read_b128 v[76:79], %[p] offset:816\n" "ds_read_b128 v[80:83], %[p] offset:832\n" "ds_read_b128 v[84:87], %[p] offset:848\n" "ds_read_b128 v[88:91], %[p] offset:864\n"
-        "ds_read_b128 v[92:95], %[p] offset:880\n" "s_waitcnt lgkmcnt(8)\n" "v_add_f32 %[acc], %[acc], v96\n" "v_add_f32 %[acc], %[acc], v97\n"
-        "v_add_f32 %[acc], %[acc], v98\n" "v_add_f32 %[acc], %[acc], v99\n" "v_add_f32 %[acc], %[acc], v100\n" "v_add_f32 %[acc], %[acc], v101\n"
-        "v_add_f32 %[acc], %[acc], v102\n" "v_add_f32 %[acc], %[acc], v103\n" "v_add_f32 %[acc], %[acc], v104\n" "v_add_f32 %[acc], %[acc], v105\n"
-        "v_add_f32 %[acc], %[acc], v106\n" "v_add_f32 %[acc], %[acc], v107\n" "v_add_f32 %[acc], %[acc], v108\n" "v_add_f32 %[acc], %[acc], v109\n"
-        "v_add_f32 %[acc], %[acc], v110\n" "v_add_f32 %[acc], %[acc], v111\n" "v_add_f32 %[acc], %[acc], v112\n" "v_add_f32 %[acc], %[acc], v113\n"
-        "v_add_f32 %[acc], %[acc], v114\n" "v_add_f32 %[acc], %[acc], v115\n" "v_add_f32 %[acc], %[acc], v116\n" "v_add_f32 %[acc], %[acc], v117\n"
-        "v_add_f32 %[acc], %[acc], v118\n" "v_add_f32 %[acc], %[acc], v119\n" "v_add_f32 %[acc], %[acc], v120\n" "v_add_f32 %[acc], %[acc], v121\n"
-        "v_add_f32 %[acc], %[acc], v122\n" "v_add_f32 %[acc], %[acc], v123\n" "v_add_f32 %[acc], %[acc], v124\n" "v_add_f32 %[acc], %[acc], v125\n"
-        "v_add_f32 %[acc], %[acc], v126\n" "v_add_f32 %[acc], %[acc], v127\n" "ds_read_b128 v[96:99], %[p] offset:896\n" "ds_read_b128 v[100:103], %[p] offset:912\n"
-        "ds_read_b128 v[104:107], %[p] offset:928\n" "ds_read_b128 v[108:111], %[p] offset:944\n" "ds_read_b128 v[112:115], %[p] offset:960\n" "ds_read_b128 v[116:119], %[p] offset:976\n"
-        "ds_read_b128 v[120:123], %[p] offset:992\n" "ds_read_b128 v[124:127], %[p] offset:1008\n" "s_waitcnt lgkmcnt(8)\n" "v_add_f32 %[acc], %[acc], v64\n"
-        "v_add_f32 %[acc], %[acc], v65\n" "v_add_f32 %[acc], %[acc], v66\n" "v_add_f32 %[acc], %[acc], v67\n" "v_add_f32 %[acc], %[acc], v68\n"
-        "v_add_f32 %[acc], %[acc], v69\n" "v_add_f32 %[acc], %[acc], v70\n" "v_add_f32 %[acc], %[acc], v71\n" "v_add_f32 %[acc], %[acc], v72\n"
-        "v_add_f32 %[acc], %[acc], v73\n" "v_add_f32 %[acc], %[acc], v74\n" "v_add_f32 %[acc], %[acc], v75\n" "v_add_f32 %[acc], %[acc], v76\n"
-        "v_add_f32 %[acc], %[acc], v77\n" "v_add_f32 %[acc], %[acc], v78\n" "v_add_f32 %[acc], %[acc], v79\n" "v_add_f32 %[acc], %[acc], v80\n"
-        "v_add_f32 %[acc], %[acc], v81\n" "v_add_f32 %[acc], %[acc], v82\n" "v_add_f32 %[acc], %[acc], v83\n" "v_add_f32 %[acc], %[acc], v84\n"
-        "v_add_f32 %[acc], %[acc], v85\n" "v_add_f32 %[acc], %[acc], v86\n" "v_add_f32 %[acc], %[acc], v87\n" "v_add_f32 %[acc], %[acc], v88\n"
-        "v_add_f32 %[acc], %[acc], v89\n" "v_add_f32 %[acc], %[acc], v90\n" "v_add_f32 %[acc], %[acc], v91\n" "v_add_f32 %[acc], %[acc], v92\n"
-        "v_add_f32 %[acc], %[acc], v93\n" "v_add_f32 %[acc], %[acc], v94\n" "v_add_f32 %[acc], %[acc], v95\n" "s_waitcnt lgkmcnt(0)\n"
-        "v_add_f32 %[acc], %[acc], v96\n" "v_add_f32 %[acc], %[acc], v97\n" "v_add_f32 %[acc], %[acc], v98\n" "v_add_f32 %[acc], %[acc], v99\n"
-        "v_add_f32 %[acc], %[acc], v100\n" "v_add_f32 %[acc], %[acc], v101\n" "v_add_f32 %[acc], %[acc], v102\n" "v_add_f32 %[acc], %[acc], v103\n"
-        "v_add_f32 %[acc], %[acc], v104\n" "v_add_f32 %[acc], %[acc], v105\n" "v_add_f32 %[acc], %[acc], v106\n" "v_add_f32 %[acc], %[acc], v107\n"
-        "v_add_f32 %[acc], %[acc], v108\n" "v_add_f32 %[acc], %[acc], v109\n" "v_add_f32 %[acc], %[acc], v110\n" "v_add_f32 %[acc], %[acc], v111\n"
-        "v_add_f32 %[acc], %[acc], v112\n" "v_add_f32 %[acc], %[acc], v113\n" "v_add_f32 %[acc], %[acc], v114\n" "v_add_f32 %[acc], %[acc], v115\n"
-        "v_add_f32 %[acc], %[acc], v116\n" "v_add_f32 %[acc], %[acc], v117\n" "v_add_f32 %[acc], %[acc], v118\n" "v_add_f32 %[acc], %[acc], v119\n"
-        "v_add_f32 %[acc], %[acc], v120\n" "v_add_f32 %[acc], %[acc], v121\n" "v_add_f32 %[acc], %[acc], v122\n" "v_add_f32 %[acc], %[acc], v123\n"
-        "v_add_f32 %[acc], %[acc], v124\n" "v_add_f32 %[acc], %[acc], v125\n" "v_add_f32 %[acc], %[acc], v126\n" "v_add_f32 %[acc], %[acc], v127\n"
-        : [acc] "+&v"(acc)
-        : [p] "v"(p)
-        : "v64", "v65", "v66", "v67", "v68", "v69", "v70", "v71",
-          "v72", "v73", "v74", "v75", "v76", "v77", "v78", "v79",
-          "v80", "v81", "v82", "v83", "v84", "v85", "v86", "v87",
-          "v88", "v89", "v90", "v91", "v92", "v93", "v94", "v95",
-          "v96", "v97", "v98", "v99", "v100", "v101", "v102", "v103",
-          "v104", "v105", "v106", "v107", "v108", "v109", "v110", "v111",
-          "v112", "v113", "v114", "v115", "v116", "v117", "v118", "v119",
-          "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127",
-          "memory");
-    return acc;
-}
-
-__device__ __forceinline__ float chain_add_lds(float acc, const float4 *p, int nq)
-{
-    int q = 0;
-    for (; q + 64 <= nq; q += 64) acc = chain64_lds(acc, p + q);
-    for (; q < nq; q++) {
-        const float4 v = p[q];
+    for (; i < n; i++) {
+        const float4 v = p[i];
         acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
     }
     return acc;
 }
 
 template <int G>
-__global__ __launch_bounds__(SV_WAVES * 64) void attn_sv_x(
-    const float *__restrict__ att, size_t att_stride, const float *__restrict__ tmax, int n_tiles,
-    const float *__restrict__ vc, int n_head, int n_head_kv, int hd,
-    const uint32_t *__restrict__ pos, int n_ctx, float *__restrict__ out, size_t out_stride,
-    int np, unsigned *err)
+__global__ __launch_bounds__(256) void attn_av(const float *__restrict__ att, size_t att_stride,
+                                               const float *__restrict__ tmax, int n_tiles,
+                                               const float *__restrict__ vc, int n_head_kv,
+                                               int hd, const uint32_t *__restrict__ pos,
+                                               int n_ctx, float *__restrict__ out, int estr)
 {
-    constexpr int DS = 64 / G;               // columns per slice
-    constexpr int NLD = SV_QT / G;           // product units per tile (G quads each)
-    extern __shared__ float4 sv_lds[];
-    float4 *ring = sv_lds;                                  // [np][SV_QT][64]
-    float *e = (float *)(sv_lds + np * SV_QT * 64);         // [G][att_stride + 4]
+    constexpr int DC = AV_CH / G;                  // columns of the workgroup
+    constexpr int NPL = (DC * AV_VB + 191) / 192;  // (column, quad) pairs per producer lane
+    extern __shared__ float4 av_lds[];
+    float *e = (float *)av_lds;                    // [G][estr]: e_j, then a_j
+    float4 *prod = av_lds + G * estr / 4;          // [2][AV_CH][AV_PS]
     __shared__ float mx_s[G], inv_s[G];
     __shared__ int nrm_s[G];
     __shared__ uint64_t tab[32];
-    __shared__ int ready[SV_NP_MAX], cnt[SV_NP_MAX], consumed, a_ready, e_done;
-
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
+    const int n_cg = hd / DC;
+    const int kvh = blockIdx.x / n_cg, c0 = (blockIdx.x - kvh * n_cg) * DC;
     const int kvd = n_head_kv * hd;
-    const int n_sl = (hd + DS - 1) / DS;
-    const int kvh = blockIdx.x / n_sl, sl = blockIdx.x - kvh * n_sl, t = blockIdx.y;
-    const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
+    const int upto = (int)min((size_t)pos[0] + 1, (size_t)n_ctx);
     const int nq = upto >> 2, rem = upto & 3, nq_all = (upto + 3) >> 2;
-    const int ntile = (nq_all + SV_QT - 1) / SV_QT;
-    const int estr = (int)att_stride + 4;        // padded: heads in different banks
-    const float *srow = att + ((size_t)t * n_head + (size_t)kvh * G) * att_stride;
+    const float *srow = att + (size_t)kvh * G * att_stride;   // head g's scores at + g * att_stride
+    const bool producer = wave > 0;
+    const int L = tid - 64;                        // producer lane 0 .. 191
 
-    // loaders: lane -> (quad lq of each group of G quads, column ld)
-    const int lq = lane / DS, ld = sl * DS + (lane - lq * DS);
-    const float4 *v4 = (const float4 *)vc + kvh * hd + (ld < hd ? ld : sl * DS);
-    const bool loader = (wave & 3) != 0;     // waves on SIMD 0 do not load
-    const int li = wave - 1 - (wave >> 2);
-    const int nunit = ntile * NLD;
-    // V of the loader's units li + SV_LOADERS m, SV_VPF of them in flight
-    // (unit u: quads (u % NLD) G .. + G - 1 of tile u / NLD; the lane's
-    // quad is the lq-th of them)
-    auto v_of = [&](int u) -> float4 {
-        const int i = u / NLD, k = u - i * NLD;
-        const int jq = min(i * SV_QT + k * G + lq, nq_all - 1);
-        return v4[(size_t)jq * kvd];
+    // V of the producer's pairs (column c, quad qq) of value blocks
+    // 0 .. AV_VD - 1, requested first: they are needed last, and arrive
+    // while the softmax runs
+    const float4 *v4 = (const float4 *)vc + (size_t)kvh * hd + c0;   // quad jq, column c: v4[jq * kvd + c]
+    const int nvb = (nq_all + AV_VB - 1) / AV_VB;
+    // (vb[0] holds the next block to use; the pipeline moves down one
+    // block at a time, so that every index is known at compile time)
+    float4 vb[AV_VD][NPL];
+    auto v_load = [&](int b, float4 *dst) {
+#pragma unroll
+        for (int k = 0; k < NPL; k++) {
+            const int pi = min(L + 192 * k, DC * AV_VB - 1);
+            const int c = pi / AV_VB, jq = min(b * AV_VB + (pi - c * AV_VB), nq_all - 1);
+            dst[k] = v4[(size_t)jq * kvd + c];
+        }
     };
-    float4 vq[SV_VPF];
-
-    // scores of the first SV_EXP_PF exp rounds, loaded first: a wave's loads
-    // complete in order, and these are needed as soon as the maxima are
-    // known, the V tiles only after the softmax sum
-    const int ex0 = li * 64 + lane;                 // loader's position in a round
-    float sc[SV_EXP_PF][G];
-    if (loader) {
+    if (producer) {
 #pragma unroll
-        for (int k = 0; k < SV_EXP_PF; k++) {
-            const int p = k * SV_EXR + ex0;
-#pragma unroll
-            for (int gg = 0; gg < G; gg++)
-                sc[k][gg] = srow[(size_t)gg * att_stride + (p < upto ? p : 0)];
-        }
-    }
-    if (loader) {
-#pragma unroll
-        for (int m = 0; m < SV_VPF; m++) vq[m] = v_of(min(li + m * SV_LOADERS, nunit - 1));
+        for (int d = 0; d < AV_VD; d++) v_load(min(d, nvb - 1), vb[d]);
     }
 
-    // ---- head maxima (src/ops.c:26-30: a NaN first score stays the max),
-    // by the waves that load no V (wave 4 n takes heads n, n + 4): their
-    // tile-maximum loads are not queued behind V loads
-    if (!loader) {
-        for (int hg = wave >> 2; hg < G; hg += 4) {
-            const float *tm = tmax + ((size_t)t * n_head + (size_t)kvh * G + hg) * n_tiles;
-            const int used = (upto + SC_TILE - 1) / SC_TILE;
-            float m = -INFINITY;
-            for (int i = lane; i < used; i += 64) {
-                const float v = tm[i];
-                m = v > m ? v : m;
-            }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const float w = __shfl_xor(m, o);
-                m = w > m ? w : m;
-            }
-            const float s0 = srow[(size_t)hg * att_stride];
-            if (lane == 0) mx_s[hg] = s0 != s0 ? s0 : m;
+    // 1. head maxima (src/ops.c:26-30): wave w takes heads w, w + 4
+    for (int g = wave; g < G; g += 4) {
+        const float *tm = tmax + ((size_t)kvh * G + g) * n_tiles;
+        const int used = (upto + SC_TILE - 1) / SC_TILE;
+        float m = -INFINITY;
+        for (int i = lane; i < used; i += 64) {
+            const float v = tm[i];
+            m = v > m ? v : m;
         }
-    }
-    if (tid < SV_NP_MAX) {
-        ready[tid] = -1;
-        cnt[tid] = 0;
+        m = wave_reduce(m, -INFINITY, [](float x, float y) { return y > x ? y : x; });
+        const float s0 = srow[(size_t)g * att_stride];
+        if (lane == 0) mx_s[g] = s0 != s0 ? s0 : m;
     }
     if (tid < 32) tab[tid] = fox_exp2_tab[tid];
-    if (tid == 0) {
-        consumed = 0;
-        a_ready = 0;
-        e_done = 0;
-    }
     __syncthreads();
-    if (!loader && wave != 0) return;                // (SIMD 0 stays with wave 0)
 
-    if (loader) {
-        // ---- e_j = expf(s_j - max) (src/ops.c:31-34) in rounds of SV_EXR
-        // positions; a wave counts each round it completes
+    // 2. exp blocks and the softmax sums (lane g of wave 0)
+    const int neb = (upto + AV_EB - 1) / AV_EB;
+    float sum = 0.0f;
+    {
         float mx[G];
 #pragma unroll
-        for (int gg = 0; gg < G; gg++) mx[gg] = mx_s[gg];
-        auto exp_round = [&](int k, const float *scr) {
-            const int p = k * SV_EXR + ex0;
-            if (p < upto) {
+        for (int g = 0; g < G; g++) mx[g] = mx_s[g];
+        // the scores of a producer lane's four positions of block k
+        auto s_load = [&](int k, float4 *s) {
+            const int j = min(k * AV_EB + 4 * L, (upto - 1) & ~3);
 #pragma unroll
-                for (int gg = 0; gg < G; gg++) e[gg * estr + p] = fox_expf_t(scr[gg] - mx[gg], tab);
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-            if (lane == 0) __hip_atomic_fetch_add(&e_done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            for (int g = 0; g < G; g++) s[g] = *(const float4 *)(srow + (size_t)g * att_stride + j);
         };
+        float4 sc[G];
+        if (producer) s_load(0, sc);
+        for (int k = 0; k <= neb; k++) {
+            if (producer && k < neb) {
+                float4 cur[G];
 #pragma unroll
-        for (int k = 0; k < SV_EXP_PF; k++)
-            if (k * SV_EXR < upto) exp_round(k, sc[k]);
-        for (int k = SV_EXP_PF; k * SV_EXR < upto; k++) {
-            const int p = k * SV_EXR + ex0;
-            float s2[G];
+                for (int g = 0; g < G; g++) cur[g] = sc[g];
+                if (k + 1 < neb) s_load(k + 1, sc);
+                const int j = k * AV_EB + 4 * L;
+                if (j < upto) {
 #pragma unroll
-            for (int gg = 0; gg < G; gg++) s2[gg] = srow[(size_t)gg * att_stride + (p < upto ? p : 0)];
-            exp_round(k, s2);
-        }
-    }
-
-    if (wave == 0) {
-        // ---- softmax sums, one lane per head, position order; round k is
-        // added once every loader wave has counted it
-        float sum = 0.0f;
-        bool eok = true;
-        for (int k = 0; k * SV_EXR < upto; k++) {
-            if (!sv_wait_ge(&e_done, SV_LOADERS * (k + 1))) {
-                eok = false;
-                break;
-            }
-            const int p0 = k * SV_EXR, p1 = min(upto, p0 + SV_EXR);
-            if (lane < G) {
-                const float *er = e + lane * estr;
-                const int nqk = (p1 - p0) >> 2;
-                sum = chain_add_lds(sum, (const float4 *)(er + p0), nqk);
-                for (int j = p0 + 4 * nqk; j < p1; j++) sum = sum + er[j];
-            }
-        }
-        if (!eok) {
-            sum = __builtin_nanf("");
-            if (lane == 0) sv_error(err, FOX_DEV_ERR_ATTN_SUM);
-        }
-        // a_j = e_j * (1/sum) is formed by the loaders (src/ops.c:35-38)
-        if (lane < G) {
-            nrm_s[lane] = sum > 0.0f;
-            inv_s[lane] = sum > 0.0f ? fox_div(1.0f, sum) : 1.0f;
-        }
-        sv_signal(&a_ready, 1);
-
-        // ---- value sums: lane (head g, column d) adds its products in order.
-        // Whole tiles run in one asm loop (the reasons of chain64_lds): a
-        // tile's second half (eight quads, v96-v127) is read while its first
-        // half (v64-v95) is added, then, once tile i + 1 is marked ready, the
-        // next tile's first half while the second half is added.  Tile i + 1's
-        // flag is read a tile ahead (with tile i's first half) and tested
-        // after tile i's first half's adds; a tile not marked by then is
-        // waited for out of line (bounded: a timed-out wait clears ok, after
-        // which the loop runs on without waiting and the sum is replaced by
-        // NaN below).  Tile i's stage is released once all its reads are in,
-        // before the next reads go out; the stage's four base addresses
-        // (v56-v59) are computed once per tile.
-        // Ring slots are XOR-swizzled by (quad & 3) (the loaders' four quads
-        // per store fall in different banks): quad u of a stage sits at
-        // lane ^ 4 (u & 3), so four base addresses cover the sixteen quads
-        // with constant offsets.
-        static_assert(SV_QT == 16 && SV_QT * 64 * 16 == 1 << 14 && SV_SPIN == 0x400000,
-                      "the asm loop's tile size, stage size and spin limit");
-        const int g = lane / DS, d = sl * DS + (lane - g * DS);
-        float acc = 0.0f;
-        bool ok = eok && sv_wait_ge(&ready[0], 0);
-        const int nwhole = __builtin_amdgcn_readfirstlane(nq / SV_QT);
-        int i = 0, st = 0;
-        if (ok && nwhole > 0) {
-            const uint32_t ra = lds_addr(ring);
-            const uint32_t l0 = ra + ((uint32_t)lane << 4), l1 = ra + ((uint32_t)(lane ^ 4) << 4);
-            const uint32_t l2 = ra + ((uint32_t)(lane ^ 8) << 4), l3 = ra + ((uint32_t)(lane ^ 12) << 4);
-            const uint32_t rb = lds_addr(ready), vc = lds_addr(&consumed);
-            const int npu = __builtin_amdgcn_readfirstlane(np);
-            int oks = 1, so, sn, sf, si1, sp;
-            uint32_t va, vv, vf;
-            asm volatile(
-        "v_mov_b32 v56, %[l0]\n"
-        "v_mov_b32 v57, %[l1]\n"
-        "v_mov_b32 v58, %[l2]\n"
-        "v_mov_b32 v59, %[l3]\n"
-        "ds_read_b128 v[64:67], v56 offset:0\n"
-        "ds_read_b128 v[68:71], v57 offset:1024\n"
-        "ds_read_b128 v[72:75], v58 offset:2048\n"
-        "ds_read_b128 v[76:79], v59 offset:3072\n"
-        "ds_read_b128 v[80:83], v56 offset:4096\n"
-        "ds_read_b128 v[84:87], v57 offset:5120\n"
-        "ds_read_b128 v[88:91], v58 offset:6144\n"
-        "ds_read_b128 v[92:95], v59 offset:7168\n"
-        "s_add_u32 %[si1], %[i], 1\n"
-        "s_cmp_ge_u32 %[si1], %[nw]\n"
-        "s_cbranch_scc1 5f\n"
-        "s_add_u32 %[sn], %[st], 1\n"
-        "s_cmp_eq_u32 %[sn], %[np]\n"
-        "s_cselect_b32 %[sn], 0, %[sn]\n"
-        "s_lshl_b32 %[sf], %[sn], 2\n"
-        "v_add_u32 %[va], %[sf], %[rb]\n"
-        "ds_read_b32 %[vf], %[va]\n"
-        "5:\n"
-        "6:\n"
-        "ds_read_b128 v[96:99], v56 offset:8192\n"
-        "ds_read_b128 v[100:103], v57 offset:9216\n"
-        "ds_read_b128 v[104:107], v58 offset:10240\n"
-        "ds_read_b128 v[108:111], v59 offset:11264\n"
-        "ds_read_b128 v[112:115], v56 offset:12288\n"
-        "ds_read_b128 v[116:119], v57 offset:13312\n"
-        "ds_read_b128 v[120:123], v58 offset:14336\n"
-        "ds_read_b128 v[124:127], v59 offset:15360\n"
-        "s_add_u32 %[si1], %[i], 1\n"
-        "s_add_u32 %[sn], %[st], 1\n"
-        "s_cmp_eq_u32 %[sn], %[np]\n"
-        "s_cselect_b32 %[sn], 0, %[sn]\n"
-        "s_waitcnt lgkmcnt(8)\n"
-        "v_add_f32 %[acc], %[acc], v64\n" "v_add_f32 %[acc], %[acc], v65\n" "v_add_f32 %[acc], %[acc], v66\n" "v_add_f32 %[acc], %[acc], v67\n"
-        "v_add_f32 %[acc], %[acc], v68\n" "v_add_f32 %[acc], %[acc], v69\n" "v_add_f32 %[acc], %[acc], v70\n" "v_add_f32 %[acc], %[acc], v71\n"
-        "v_add_f32 %[acc], %[acc], v72\n" "v_add_f32 %[acc], %[acc], v73\n" "v_add_f32 %[acc], %[acc], v74\n" "v_add_f32 %[acc], %[acc], v75\n"
-        "v_add_f32 %[acc], %[acc], v76\n" "v_add_f32 %[acc], %[acc], v77\n" "v_add_f32 %[acc], %[acc], v78\n" "v_add_f32 %[acc], %[acc], v79\n"
-        "v_add_f32 %[acc], %[acc], v80\n" "v_add_f32 %[acc], %[acc], v81\n" "v_add_f32 %[acc], %[acc], v82\n" "v_add_f32 %[acc], %[acc], v83\n"
-        "v_add_f32 %[acc], %[acc], v84\n" "v_add_f32 %[acc], %[acc], v85\n" "v_add_f32 %[acc], %[acc], v86\n" "v_add_f32 %[acc], %[acc], v87\n"
-        "v_add_f32 %[acc], %[acc], v88\n" "v_add_f32 %[acc], %[acc], v89\n" "v_add_f32 %[acc], %[acc], v90\n" "v_add_f32 %[acc], %[acc], v91\n"
-        "v_add_f32 %[acc], %[acc], v92\n" "v_add_f32 %[acc], %[acc], v93\n" "v_add_f32 %[acc], %[acc], v94\n" "v_add_f32 %[acc], %[acc], v95\n"
-        "s_waitcnt lgkmcnt(0)\n"
-        "v_mov_b32 %[vv], %[si1]\n"
-        "ds_write_b32 %[vc], %[vv]\n"
-        "s_cmp_ge_u32 %[si1], %[nw]\n"
-        "s_cbranch_scc1 3f\n"
-        "s_cmp_eq_u32 %[ok], 0\n"
-        "s_cbranch_scc1 4f\n"
-        "v_readfirstlane_b32 %[sf], %[vf]\n"
-        "s_cmp_lt_i32 %[sf], %[si1]\n"
-        "s_cbranch_scc1 8f\n"
-        "4:\n"
-        "s_lshl_b32 %[so], %[sn], 14\n"
-        "v_add_u32 v56, %[so], %[l0]\n"
-        "v_add_u32 v57, %[so], %[l1]\n"
-        "v_add_u32 v58, %[so], %[l2]\n"
-        "v_add_u32 v59, %[so], %[l3]\n"
-        "ds_read_b128 v[64:67], v56 offset:0\n"
-        "ds_read_b128 v[68:71], v57 offset:1024\n"
-        "ds_read_b128 v[72:75], v58 offset:2048\n"
-        "ds_read_b128 v[76:79], v59 offset:3072\n"
-        "ds_read_b128 v[80:83], v56 offset:4096\n"
-        "ds_read_b128 v[84:87], v57 offset:5120\n"
-        "ds_read_b128 v[88:91], v58 offset:6144\n"
-        "ds_read_b128 v[92:95], v59 offset:7168\n"
-        "s_add_u32 %[so], %[si1], 1\n"
-        "s_cmp_ge_u32 %[so], %[nw]\n"
-        "s_cbranch_scc1 3f\n"
-        "s_add_u32 %[sf], %[sn], 1\n"
-        "s_cmp_eq_u32 %[sf], %[np]\n"
-        "s_cselect_b32 %[sf], 0, %[sf]\n"
-        "s_lshl_b32 %[sf], %[sf], 2\n"
-        "v_add_u32 %[va], %[sf], %[rb]\n"
-        "ds_read_b32 %[vf], %[va]\n"
-        "3:\n"
-        "v_add_f32 %[acc], %[acc], v96\n" "v_add_f32 %[acc], %[acc], v97\n" "v_add_f32 %[acc], %[acc], v98\n" "v_add_f32 %[acc], %[acc], v99\n"
-        "v_add_f32 %[acc], %[acc], v100\n" "v_add_f32 %[acc], %[acc], v101\n" "v_add_f32 %[acc], %[acc], v102\n" "v_add_f32 %[acc], %[acc], v103\n"
-        "v_add_f32 %[acc], %[acc], v104\n" "v_add_f32 %[acc], %[acc], v105\n" "v_add_f32 %[acc], %[acc], v106\n" "v_add_f32 %[acc], %[acc], v107\n"
-        "v_add_f32 %[acc], %[acc], v108\n" "v_add_f32 %[acc], %[acc], v109\n" "v_add_f32 %[acc], %[acc], v110\n" "v_add_f32 %[acc], %[acc], v111\n"
-        "v_add_f32 %[acc], %[acc], v112\n" "v_add_f32 %[acc], %[acc], v113\n" "v_add_f32 %[acc], %[acc], v114\n" "v_add_f32 %[acc], %[acc], v115\n"
-        "v_add_f32 %[acc], %[acc], v116\n" "v_add_f32 %[acc], %[acc], v117\n" "v_add_f32 %[acc], %[acc], v118\n" "v_add_f32 %[acc], %[acc], v119\n"
-        "v_add_f32 %[acc], %[acc], v120\n" "v_add_f32 %[acc], %[acc], v121\n" "v_add_f32 %[acc], %[acc], v122\n" "v_add_f32 %[acc], %[acc], v123\n"
-        "v_add_f32 %[acc], %[acc], v124\n" "v_add_f32 %[acc], %[acc], v125\n" "v_add_f32 %[acc], %[acc], v126\n" "v_add_f32 %[acc], %[acc], v127\n"
-        "s_mov_b32 %[st], %[sn]\n"
-        "s_mov_b32 %[i], %[si1]\n"
-        "s_cmp_lt_u32 %[i], %[nw]\n"
-        "s_cbranch_scc1 6b\n"
-        "s_branch 9f\n"
-        "8:\n"
-        "s_lshl_b32 %[sf], %[sn], 2\n"
-        "v_add_u32 %[va], %[sf], %[rb]\n"
-        "s_mov_b32 %[sp], 0x400000\n"
-        "1:\n"
-        "ds_read_b32 %[vf], %[va]\n"
-        "s_waitcnt lgkmcnt(0)\n"
-        "v_readfirstlane_b32 %[sf], %[vf]\n"
-        "s_cmp_ge_i32 %[sf], %[si1]\n"
-        "s_cbranch_scc1 4b\n"
-        "s_sub_u32 %[sp], %[sp], 1\n"
-        "s_cmp_eq_u32 %[sp], 0\n"
-        "s_cbranch_scc0 1b\n"
-        "s_mov_b32 %[ok], 0\n"
-        "s_branch 4b\n"
-        "9:\n"
-        "s_waitcnt lgkmcnt(0)\n"
-                : [acc] "+&v"(acc), [ok] "+&s"(oks), [i] "+&s"(i), [st] "+&s"(st), [so] "=&s"(so),
-                  [sn] "=&s"(sn), [sf] "=&s"(sf), [si1] "=&s"(si1), [sp] "=&s"(sp), [va] "=&v"(va),
-                  [vv] "=&v"(vv), [vf] "=&v"(vf)
-                : [nw] "s"(nwhole), [np] "s"(npu), [l0] "v"(l0), [l1] "v"(l1), [l2] "v"(l2),
-                  [l3] "v"(l3), [rb] "v"(rb), [vc] "v"(vc)
-                : "v56", "v57", "v58", "v59", "v60", "v61", "v62", "v63",
-                  "v64", "v65", "v66", "v67", "v68", "v69", "v70", "v71",
-                  "v72", "v73", "v74", "v75", "v76", "v77", "v78", "v79",
-                  "v80", "v81", "v82", "v83", "v84", "v85", "v86", "v87",
-                  "v88", "v89", "v90", "v91", "v92", "v93", "v94", "v95",
-                  "v96", "v97", "v98", "v99", "v100", "v101", "v102", "v103",
-                  "v104", "v105", "v106", "v107", "v108", "v109", "v110", "v111",
-                  "v112", "v113", "v114", "v115", "v116", "v117", "v118", "v119",
-                  "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127",
-                  "scc", "memory");
-            ok = oks != 0;
-        }
-        // the last tile, partly filled: nfull whole quads, then rem positions
-        if (ok && i < ntile) {
-            ok = sv_wait_ge(&ready[st], i);
-            if (ok) {
-                const float4 *P = ring + st * SV_QT * 64;
-                float4 X[SV_QT];
-#pragma unroll
-                for (int u = 0; u < SV_QT; u++) X[u] = P[u * 64 + (lane ^ ((u & 3) << 2))];
-                const int nfull = nq - i * SV_QT;
-#pragma unroll
-                for (int u = 0; u < SV_QT; u++) {
-                    const float4 v = X[u];
-                    if (u < nfull) {
-                        acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
-                    } else if (u == nfull && rem) {
-                        acc = acc + v.x;
-                        if (rem > 1) acc = acc + v.y;
-                        if (rem > 2) acc = acc + v.z;
+                    for (int g = 0; g < G; g++) {
+                        float4 r;
+                        r.x = fox_expf_t(cur[g].x - mx[g], tab);
+                        r.y = j + 1 < upto ? fox_expf_t(cur[g].y - mx[g], tab) : 0.0f;
+                        r.z = j + 2 < upto ? fox_expf_t(cur[g].z - mx[g], tab) : 0.0f;
+                        r.w = j + 3 < upto ? fox_expf_t(cur[g].w - mx[g], tab) : 0.0f;
+                        *(float4 *)(e + g * estr + j) = r;
                     }
                 }
             }
-            sv_signal(&consumed, i + 1);
+            if (wave == 0 && k > 0 && lane < G) {
+                // block k - 1, in position order
+                const int j0 = (k - 1) * AV_EB, j1 = min(upto, j0 + AV_EB);
+                const float *er = e + lane * estr;
+                const int nqk = (j1 - j0) >> 2;
+                sum = chain_quads(sum, (const float4 *)(er + j0), nqk);
+                for (int j = j0 + 4 * nqk; j < j1; j++) sum = sum + er[j];
+            }
+            __syncthreads();
         }
-        if (!ok) {
-            sv_signal(&consumed, 1 << 30);
-            acc = __builtin_nanf("");
-            if (lane == 0 && eok) sv_error(err, FOX_DEV_ERR_ATTN_VALUES);
-        }
-        if (g < G && d < hd) out[(size_t)t * out_stride + (size_t)(kvh * G + g) * hd + d] = acc;
-        return;
     }
-    if (!loader) return;
 
-    // ---- loaders: product units u = li, li + SV_LOADERS, ...  A unit is G
-    // quads of one tile for every lane (its G heads x DS columns); the
-    // NLD units of a tile come from NLD different loaders, the last of them
-    // marks the tile ready, so that the first tile is ready after one unit
-    // of work per loader.
-    if (!sv_wait_ge_idle(&a_ready, 1)) {
-        if (lane == 0) sv_error(err, FOX_DEV_ERR_ATTN_LOADER);
-        return;
+    // 3. a_j = e_j * (1/sum), or e_j where the sum is not positive
+    // (src/ops.c:35-38)
+    if (wave == 0 && lane < G) {
+        nrm_s[lane] = sum > 0.0f;
+        inv_s[lane] = sum > 0.0f ? fox_div(1.0f, sum) : 1.0f;
     }
-    // a_j = e_j * (1/sum), or e_j where the sum is not positive
-    // (src/ops.c:35-38; e * 1 is e exactly): the scale per head, and that of
-    // the lane's own head for the DPP exchange below
-    float ivg[G];
+    __syncthreads();
+    for (int i = tid; i < G * nq_all; i += 256) {
+        const int g = i / nq_all, jq = i - g * nq_all;
+        if (nrm_s[g]) {
+            float4 *a = (float4 *)(e + g * estr) + jq;
+            const float inv = inv_s[g];
+            float4 v = *a;
+            v.x = v.x * inv; v.y = v.y * inv; v.z = v.z * inv; v.w = v.w * inv;
+            *a = v;
+        }
+    }
+    __syncthreads();
+
+    // 4. value blocks: products by waves 1-3, chains by wave 0
+    const int ch = lane;                           // wave 0: chain (g, c) = (ch / DC, ch % DC)
+    float acc = 0.0f;
+    for (int b = 0; b <= nvb; b++) {
+        if (producer && b < nvb) {
+            float4 *P = prod + (b & 1) * AV_CH * AV_PS;
 #pragma unroll
-    for (int gg = 0; gg < G; gg++) ivg[gg] = nrm_s[gg] ? inv_s[gg] : 1.0f;
-    constexpr bool DPPX = G == 2 || G == 4;  // the G heads exchanged within lane quads
-    const int mine = (lane - lq * DS) % G;
-    float ivm = ivg[0];
+            for (int k = 0; k < NPL; k++) {
+                const int pi = L + 192 * k;
+                const int c = pi / AV_VB, qq = pi - c * AV_VB, jq = b * AV_VB + qq;
+                if (pi < DC * AV_VB && jq < nq_all) {
+                    const float4 v = vb[0][k];
 #pragma unroll
-    for (int gg = 1; gg < G; gg++) ivm = mine == gg ? ivg[gg] : ivm;
-    // weight quads read per unit (one per head, or the lane's own head's
-    // for the DPP exchange)
-    constexpr int RK = DPPX ? 1 : G;
-    int cons_seen = 0;                       // consumed is known to be at least this
-    // the stage of the unit's tile, i mod np, kept as a running index (a
-    // division per unit is scalar work every wave of the compute unit
-    // shares one scalar unit for, the chain wave's included)
-    int st_i = li / NLD, st = st_i % np;
-    for (int u0 = li; u0 < nunit; u0 += SV_VPF * SV_LOADERS) {
-#pragma unroll
-        for (int m = 0; m < SV_VPF; m++) {
-            const int u = u0 + m * SV_LOADERS;
-            if (u >= nunit) break;
-            const float4 v = vq[m];
-            const int un = u + SV_VPF * SV_LOADERS;
-            if (un < nunit) vq[m] = v_of(un);
-            const int i = u / NLD, k = u - i * NLD;
-            const int qi = k * G + lq;                       // the lane's quad in the tile
-            const int jq = min(i * SV_QT + qi, nq_all - 1);
-            float4 wq[RK];
-#pragma unroll
-            for (int r = 0; r < RK; r++) wq[r] = ((const float4 *)(e + (DPPX ? mine : r) * estr))[jq];
-            // the tile's stage is free once tile i - np is consumed
-            if (i >= np && cons_seen < i - np + 1) {
-                if (!sv_wait_ge_idle(&consumed, i - np + 1)) {
-                    if (lane == 0) sv_error(err, FOX_DEV_ERR_ATTN_LOADER);
-                    return;
+                    for (int g = 0; g < G; g++) {
+                        const float4 a = ((const float4 *)(e + g * estr))[jq];
+                        float4 p;
+                        p.x = a.x * v.x; p.y = a.y * v.y; p.z = a.z * v.z; p.w = a.w * v.w;
+                        P[(g * DC + c) * AV_PS + qq] = p;
+                    }
                 }
-                cons_seen = i - np + 1;
-            }
-            for (st += i - st_i, st_i = i; st >= np;) st -= np;
-            float4 *P = ring + st * SV_QT * 64;
-            float4 am = wq[0];
-            if (DPPX) {
-                am.x = am.x * ivm; am.y = am.y * ivm; am.z = am.z * ivm; am.w = am.w * ivm;
             }
 #pragma unroll
-            for (int gg = 0; gg < G; gg++) {
-                float4 a;
-                if (DPPX) {
-                    // quad_perm: every lane of a quad takes lane (quad base + gg)
-                    const int ctl = G == 4 ? gg * 0x55 : (gg ? 0xF5 : 0xA0);
-                    a.x = dpp_bcast(am.x, ctl);
-                    a.y = dpp_bcast(am.y, ctl);
-                    a.z = dpp_bcast(am.z, ctl);
-                    a.w = dpp_bcast(am.w, ctl);
-                } else {
-                    a = wq[DPPX ? 0 : gg];
-                    a.x = a.x * ivg[gg]; a.y = a.y * ivg[gg];
-                    a.z = a.z * ivg[gg]; a.w = a.w * ivg[gg];
-                }
-                float4 p;
-                p.x = a.x * v.x; p.y = a.y * v.y; p.z = a.z * v.z; p.w = a.w * v.w;
-                P[qi * 64 + ((gg * DS + (lane - lq * DS)) ^ ((qi & 3) << 2))] = p;
-            }
-            // count the unit; the tile's last unit marks it ready (its
-            // writes, and through their own counts every other unit's, are
-            // complete by then)
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-            int old = 0;
-            if (lane == 0) old = __hip_atomic_fetch_add(&cnt[st], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            old = __builtin_amdgcn_readfirstlane(old);
-            if (old == NLD - 1) {
-                if (lane == 0) cnt[st] = 0;          // (no unit of the stage's next tile runs before
-                sv_signal(&ready[st], i);            //  this tile is consumed)
+            for (int d = 0; d + 1 < AV_VD; d++)
+#pragma unroll
+                for (int k = 0; k < NPL; k++) vb[d][k] = vb[d + 1][k];
+            if (b + AV_VD < nvb) v_load(b + AV_VD, vb[AV_VD - 1]);
+        }
+        if (wave == 0 && b > 0 && ch < AV_CH) {
+            // block b - 1: whole quads of positions below upto, then the
+            // ragged quad's first rem products
+            const float4 *P = prod + ((b - 1) & 1) * AV_CH * AV_PS + ch * AV_PS;
+            const int q0 = (b - 1) * AV_VB;
+            const int nfull = min(AV_VB, nq - q0);
+            acc = chain_quads(acc, P, nfull);
+            if (b == nvb && rem) {
+                const float4 v = P[nfull];
+                acc = acc + v.x;
+                if (rem > 1) acc = acc + v.y;
+                if (rem > 2) acc = acc + v.z;
             }
         }
+        __syncthreads();
+    }
+    if (wave == 0 && ch < AV_CH) {
+        const int g = ch / DC, c = ch - g * DC;
+        out[(size_t)(kvh * G + g) * hd + c0 + c] = acc;
     }
 }
 
@@ -1546,65 +1008,52 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
         float *att = (float *)ctx->ws;
         float *tmax = (float *)(ctx->ws + att_bytes);
         const size_t gqa = n_head / n_head_kv;
-        const int nch = (int)((head_dim / 4 + SC_CQ - 1) / SC_CQ);
-        const size_t lds = 0;                                   // (static arrays)
-        const void *sk = nch == 1 ? (const void *)attn_scores_x<1>
-                       : nch == 2 ? (const void *)attn_scores_x<2>
-                       : nch == 3 ? (const void *)attn_scores_x<3>
-                       : nch == 4 ? (const void *)attn_scores_x<4>
-                       : nch == 5 ? (const void *)attn_scores_x<5>
-                       : nch == 6 ? (const void *)attn_scores_x<6>
-                       : nch == 7 ? (const void *)attn_scores_x<7>
-                                  : (const void *)attn_scores_x<8>;
-        if (lds > 64 * 1024) {
-            hipError_t e = hipFuncSetAttribute(sk, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               (int)lds);
-            if (e != hipSuccess) return fox_hip_fail(e, "attention: LDS size");
-        }
+        const int ikv = (int)n_head_kv, ihd = (int)head_dim, ictx = (int)n_ctx;
         {
-            const int ih = (int)n_head, ikv = (int)n_head_kv, ihd = (int)head_dim;
-            const int ictx = (int)n_ctx, iM = (int)M;
-            const int tpw = SC_TPW;
-            void *args[] = {(void *)&q, (void *)&qs, (void *)&k_cache, (void *)&ih, (void *)&ikv,
-                            (void *)&ihd, (void *)&pos, (void *)&ictx, (void *)&att_stride,
-                            (void *)&att, (void *)&tmax, (void *)&n_tiles, (void *)&iM,
-                            (void *)&tpw};
-            hipError_t e = hipLaunchKernel(sk, dim3((unsigned)n_tiles, (unsigned)n_head_kv,
-                                                    (unsigned)((M + tpw - 1) / tpw)),
+            // scores: the K tile (a padding quad per row) and G query heads
+            const size_t lds = ((size_t)SC_TILE * (head_dim / 4 + 1) + gqa * head_dim / 4) * 16;
+            const void *qk = gqa == 1 ? (const void *)attn_qk<1> : gqa == 2 ? (const void *)attn_qk<2>
+                           : gqa == 3 ? (const void *)attn_qk<3> : gqa == 4 ? (const void *)attn_qk<4>
+                           : gqa == 5 ? (const void *)attn_qk<5> : gqa == 6 ? (const void *)attn_qk<6>
+                           : gqa == 7 ? (const void *)attn_qk<7> : (const void *)attn_qk<8>;
+            if (lds > 64 * 1024) {
+                hipError_t e = hipFuncSetAttribute(qk, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   (int)lds);
+                if (e != hipSuccess) return fox_hip_fail(e, "attention: LDS size");
+            }
+            const int iM = (int)M;
+            void *args[] = {(void *)&q, (void *)&qs, (void *)&k_cache, (void *)&ikv, (void *)&ihd,
+                            (void *)&pos, (void *)&ictx, (void *)&att_stride, (void *)&att,
+                            (void *)&tmax, (void *)&n_tiles, (void *)&iM};
+            hipError_t e = hipLaunchKernel(qk, dim3((unsigned)n_tiles, (unsigned)n_head_kv,
+                                                    (unsigned)((M + QK_TPW - 1) / QK_TPW)),
                                            dim3(256), args, lds, ctx->stream);
             if (e != hipSuccess) return fox_hip_fail(e, "attention scores");
+            FOX_LAUNCHED("attention scores");
         }
-        FOX_LAUNCHED("attention scores");
-        const int ds = (int)(64 / gqa);
-        const int n_sl = (int)((head_dim + ds - 1) / ds);
-        const size_t e_bytes = gqa * (att_stride + 4) * sizeof(float);
-        const int ih = (int)n_head, ikv = (int)n_head_kv, ihd = (int)head_dim, ictx = (int)n_ctx;
-        const void *sv = gqa == 1 ? (const void *)attn_sv_x<1>
-                       : gqa == 2 ? (const void *)attn_sv_x<2>
-                       : gqa == 4 ? (const void *)attn_sv_x<4>
-                       : gqa == 8 ? (const void *)attn_sv_x<8> : nullptr;
-        // product stages: as many as fit beside the weights (at least SV_NP_MIN)
-        const size_t np_fit = e_bytes < SV_LDS_MAX ? (SV_LDS_MAX - e_bytes) / SV_STAGE : 0;
-        const int np = (int)(np_fit < SV_NP_MAX ? np_fit : SV_NP_MAX);
-        if (sv && np >= SV_NP_MIN) {
-            const size_t sv_lds = (size_t)np * SV_STAGE + e_bytes;
-            hipError_t e = hipFuncSetAttribute(sv, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               (int)sv_lds);
+        // one token: softmax and values in one launch, when the G heads'
+        // weights fit in LDS beside the product buffers
+        const void *av = gqa == 1 ? (const void *)attn_av<1> : gqa == 2 ? (const void *)attn_av<2>
+                       : gqa == 4 ? (const void *)attn_av<4> : gqa == 8 ? (const void *)attn_av<8>
+                                  : nullptr;
+        const int estr = (int)(((n_ctx + 31) & ~(size_t)31) + 4);   // (heads in different banks)
+        const size_t av_lds = gqa * (size_t)estr * 4 + 2 * AV_CH * AV_PS * 16;
+        const size_t dc = av ? AV_CH / gqa : 1;
+        if (M == 1 && av && av_lds <= ATT_LDS_MAX && head_dim % dc == 0) {
+            hipError_t e = hipFuncSetAttribute(av, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)av_lds);
             if (e != hipSuccess) return fox_hip_fail(e, "attention: LDS size");
-            const int sv_ds = (int)(64 / gqa);
-            const unsigned nsl = (unsigned)((head_dim + sv_ds - 1) / sv_ds);
-            const int n_attn = (int)(n_head_kv * nsl);
-            unsigned *err = (unsigned *)(ctx->small + FOX_SMALL_ERR_OFF);
             void *args[] = {(void *)&att, (void *)&att_stride, (void *)&tmax, (void *)&n_tiles,
-                            (void *)&v_cache, (void *)&ih, (void *)&ikv, (void *)&ihd,
-                            (void *)&pos, (void *)&ictx, (void *)&out, (void *)&os,
-                            (void *)&np, (void *)&err};
-            e = hipLaunchKernel(sv, dim3((unsigned)n_attn, (unsigned)M),
-                                dim3(SV_WAVES * 64), args, sv_lds, ctx->stream);
+                            (void *)&v_cache, (void *)&ikv, (void *)&ihd, (void *)&pos,
+                            (void *)&ictx, (void *)&out, (void *)&estr};
+            e = hipLaunchKernel(av, dim3((unsigned)(n_head_kv * (head_dim / dc))), dim3(256), args,
+                                av_lds, ctx->stream);
             if (e != hipSuccess) return fox_hip_fail(e, "attention softmax+values");
             FOX_LAUNCHED("attention softmax+values");
             return FOX_GPU_OK;
         }
+        const int ds = (int)(64 / gqa);
+        const int n_sl = (int)((head_dim + ds - 1) / ds);
         hipLaunchKernelGGL(attn_softmax_x, dim3((unsigned)n_head, (unsigned)M), dim3(256),
                            att_stride * sizeof(float), ctx->stream, att, att_stride, tmax,
                            n_tiles, (int)n_head, pos, (int)n_ctx);
