@@ -77,13 +77,6 @@ fox_gpu_status fox_gpu_device_info(fox_gpu_ctx *ctx, char *name, size_t cap,
  * speed differs.  No counterpart in RustFox: the CPU pool's thread count
  * (src/threadpool.c:76) plays this role there. */
 fox_gpu_status fox_gpu_set_max_workgroups(fox_gpu_ctx *ctx, int n);
-/* Wait for the stream, then read and clear the device error word: a kernel
- * whose bounded wait timed out sets a bit there (and writes NaN where its
- * result would be) instead of hanging.  *bits (optional) receives the word;
- * nonzero returns FOX_GPU_ERR_INTERNAL naming the waits.  The host library
- * calls it after every fox_eval and fox_decode_greedy and turns a failure
- * into FOX_ERR_INTERNAL.  No counterpart in RustFox (its threads join). */
-fox_gpu_status fox_gpu_take_error(fox_gpu_ctx *ctx, uint32_t *bits);
 
 /* ------------------------------------------------------------- memory */
 

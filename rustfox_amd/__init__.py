@@ -111,7 +111,6 @@ def gpu_lib() -> C.CDLL:
         "fox_gpu_silu_mul": [vp, vp, vp, sz, sz, sz],
         "fox_gpu_add": [vp, vp, vp, sz, sz, sz],
         "fox_gpu_argmax": [vp, vp, sz, vp, vp, C.c_uint32, vp],
-        "fox_gpu_take_error": [vp, C.POINTER(C.c_uint32)],
         "fox_gpu_graph_begin": [vp],
         "fox_gpu_graph_end": [vp, C.POINTER(vp)],
         "fox_gpu_graph_launch": [vp, vp],
@@ -346,13 +345,6 @@ class Gpu:
                advance=0, history: DeviceArray = None):
         _check(self.lib.fox_gpu_argmax(self.ctx, logits.ptr, n, idx.ptr, pos.ptr if pos else None,
                                        advance, history.ptr if history else None))
-
-    def take_error(self) -> int:
-        """Read and clear the device error word (0: no kernel's bounded
-        wait timed out since the last call)."""
-        bits = C.c_uint32(0)
-        self.lib.fox_gpu_take_error(self.ctx, C.byref(bits))
-        return int(bits.value)
 
     def kv_write(self, kc: DeviceArray, vc: DeviceArray, kv_dim, n_ctx, p0, k: DeviceArray,
                  v: DeviceArray, n):

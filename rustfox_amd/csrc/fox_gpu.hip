@@ -120,24 +120,6 @@ extern "C" void fox_gpu_shutdown(fox_gpu_ctx *ctx)
     delete ctx;
 }
 
-extern "C" fox_gpu_status fox_gpu_take_error(fox_gpu_ctx *ctx, uint32_t *bits)
-{
-    if (!ctx) return fox_fail(FOX_GPU_ERR_ARG, "take_error: null context");
-    uint32_t w = 0;
-    const uint32_t zero = 0;
-    uint8_t *p = ctx->small + FOX_SMALL_ERR_OFF;
-    FOX_HIP(hipStreamSynchronize(ctx->stream));
-    FOX_HIP(hipMemcpy(&w, p, 4, hipMemcpyDeviceToHost));
-    if (bits) *bits = w;
-    if (!w) return FOX_GPU_OK;
-    FOX_HIP(hipMemcpy(p, &zero, 4, hipMemcpyHostToDevice));
-    return fox_fail(FOX_GPU_ERR_INTERNAL, "a kernel's bounded wait timed out (device error bits "
-                    "0x%x:%s%s%s); the results of the pass are not valid", w,
-                    (w & FOX_DEV_ERR_ATTN_SUM) ? " attention softmax sum" : "",
-                    (w & FOX_DEV_ERR_ATTN_VALUES) ? " attention value sum" : "",
-                    (w & FOX_DEV_ERR_ATTN_LOADER) ? " attention loader" : "");
-}
-
 extern "C" fox_gpu_status fox_gpu_set_max_workgroups(fox_gpu_ctx *ctx, int n)
 {
     if (!ctx || n < 0) return fox_fail(FOX_GPU_ERR_ARG, "set_max_workgroups: bad argument");

@@ -72,14 +72,8 @@ struct fox_gpu_ctx {
     uint8_t *scratch;
 };
 #define FOX_SMALL_BYTES (64 * 1024)
-// the small buffer's parts: the device error word (bits FOX_DEV_ERR_*, set
-// by a kernel whose bounded wait timed out; read and cleared by
-// fox_gpu_take_error), then the argmax partials
-#define FOX_SMALL_ERR_OFF 0
+// the argmax partials' place in the small buffer
 #define FOX_SMALL_AM_OFF 256
-#define FOX_DEV_ERR_ATTN_SUM 1u      // exact attention: the softmax-sum hand-over
-#define FOX_DEV_ERR_ATTN_VALUES 2u   // exact attention: the value-sum hand-over
-#define FOX_DEV_ERR_ATTN_LOADER 4u   // exact attention: a loader's wait for its stage
 
 struct fox_gpu_tensor {
     int type;

@@ -562,6 +562,19 @@ __global__ __launch_bounds__(256) void attn_qk(const float *__restrict__ q, size
     const int upto_last = upto_of(t_end - 1);
     if (p0 >= upto_last) return;                   // (uniform)
     const int rows = min(SC_TILE, upto_last - p0);
+    int t0 = tz;
+    while (upto_of(t0) <= p0) t0++;                // (uniform) the first token reaching the tile
+    // the first token's queries (at most 512 quads: G <= 8, hd <= 256),
+    // requested with the K tile
+    auto q_row = [&](int t) {
+        return (const float4 *)(q + (size_t)t * q_stride + (size_t)kvh * G * hd);
+    };
+    float4 qr[2];
+    {
+        const float4 *qb = q_row(t0);
+        qr[0] = qb[min(tid, G * hd4 - 1)];
+        qr[1] = qb[min(tid + 256, G * hd4 - 1)];
+    }
     // the K tile: float4 f of the tile is (row f / hd4, quad f % hd4); eight
     // loads in flight per thread before they go to LDS
     const float4 *kb = (const float4 *)(kc + (size_t)p0 * kvd + (size_t)kvh * hd);
@@ -580,13 +593,16 @@ __global__ __launch_bounds__(256) void attn_qk(const float *__restrict__ q, size
         }
     }
     const float scale = fox_div(1.0f, fox_sqrtf((float)hd));
-    int t0 = tz;
-    while (upto_of(t0) <= p0) t0++;                // (uniform) the first token reaching the tile
     for (int t = t0; t < t_end; t++) {
         const int upto = upto_of(t);
-        if (t > t0) __syncthreads();              // every item of the previous token is done
-        const float4 *qb = (const float4 *)(q + (size_t)t * q_stride + (size_t)kvh * G * hd);
-        for (int f = tid; f < G * hd4; f += 256) Qs[f] = qb[f];
+        if (t > t0) {
+            __syncthreads();                      // every item of the previous token is done
+            const float4 *qb = q_row(t);
+            qr[0] = qb[min(tid, G * hd4 - 1)];
+            qr[1] = qb[min(tid + 256, G * hd4 - 1)];
+        }
+        if (tid < G * hd4) Qs[tid] = qr[0];
+        if (tid + 256 < G * hd4) Qs[tid + 256] = qr[1];
         __syncthreads();
 #pragma unroll
         for (int it = 0; it < (G * SC_TILE + 255) / 256; it++) {
@@ -598,7 +614,24 @@ __global__ __launch_bounds__(256) void attn_qk(const float *__restrict__ q, size
             if (ok) {
                 const float4 *kr = Ks + pl * ks, *qr = Qs + g * hd4;
                 float acc = 0.0f;
-                for (int d = 0; d < hd4; d++) {
+                int d = 0;
+                // eight quads' reads issued before their products are added
+                for (; d + 8 <= hd4; d += 8) {
+                    float4 kv[8], qv[8];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        kv[u] = kr[d + u];
+                        qv[u] = qr[d + u];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        acc = acc + qv[u].x * kv[u].x;
+                        acc = acc + qv[u].y * kv[u].y;
+                        acc = acc + qv[u].z * kv[u].z;
+                        acc = acc + qv[u].w * kv[u].w;
+                    }
+                }
+                for (; d < hd4; d++) {
                     const float4 kv = kr[d], qv = qr[d];
                     acc = acc + qv.x * kv.x;
                     acc = acc + qv.y * kv.y;
@@ -750,50 +783,188 @@ __global__ __launch_bounds__(64) void attn_values_x(const float *__restrict__ at
 //   2. blocks of AV_EB positions: waves 1-3 write e_j = expf(s_j - max) of
 //      block k to LDS while wave 0 (lane g) adds block k - 1 to head g's
 //      softmax sum; a barrier between blocks;
-//   3. 1 / sum, and a_j = e_j * (1/sum) in place (all waves);
+//   3. 1 / sum;
 //   4. blocks of AV_VB quads: waves 1-3 multiply block b's V quads (loaded
-//      AV_VD blocks ahead, from the start of the kernel) by a_j into one of two
-//      product buffers while wave 0 adds block b - 1's products to its
-//      chains; a barrier between blocks.
-// A chain lane reads its operands four at a time from LDS, the reads of
-// one group in flight while the group before is added.
+//      AV_VD blocks ahead, from the start of the kernel) by a_j = e_j * (1/sum)
+//      into one of two product buffers while wave 0 adds block b - 1's
+//      products to its chains; a barrier between blocks.
+// A chain lane reads its operands four at a time from LDS (chain_lds16).
 #define AV_CH 16
-#define AV_EB 768           // positions of an exp block (waves 1-3, four per lane)
+#define AV_EB 384           // positions of an exp block (a (head, quad) pair per producer lane for each head)
 #define AV_VB 48            // quads (192 positions) of a value block
 #define AV_VD 4             // value blocks of V in flight per producer lane
 #define AV_PS (AV_VB + 1)   // quads per chain in a product buffer (one quad of padding)
+#define AV_LDS_MIN (81 * 1024)
 
-// acc + x_0 + ... + x_{4n-1} over float4 p[0 .. n) of LDS, in order; eight
-// quads read ahead of the adds
+// acc + x_0 + ... + x_{4n-1} over float4 p[0 .. n) of LDS, in order.
+// A dependent add chain is bound by the wave's instruction issue, so its
+// operands must arrive ahead of it: in chain_lds16 two banks of eight quads
+// (v64-v95, v96-v127) alternate, one bank's reads in flight while the other
+// bank's 32 adds run (software pipelining across the loop, which the
+// compiler does not do: compiled from C, each group's reads are issued
+// after the previous group's adds and their latency is paid every time).
+// LDS returns a wave's reads in order, so lgkmcnt(8) after a bank's reads
+// means the bank before is in (earlier outstanding scalar loads only make
+// that wait stricter).  The asm ends with lgkmcnt(0).  q is the lane's own
+// address; ng >= 1 groups of 16 quads.
+__device__ __forceinline__ uint32_t lds_addr(const void *p)
+{
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
+}
+
+__device__ __forceinline__ float chain_lds16(float acc, const float4 *q, int ng)
+{
+    uint32_t p = lds_addr(q);
+    int i = ng;
+    asm volatile(
+        "ds_read_b128 v[64:67], %[p] offset:0\n"
+        "ds_read_b128 v[68:71], %[p] offset:16\n"
+        "ds_read_b128 v[72:75], %[p] offset:32\n"
+        "ds_read_b128 v[76:79], %[p] offset:48\n"
+        "ds_read_b128 v[80:83], %[p] offset:64\n"
+        "ds_read_b128 v[84:87], %[p] offset:80\n"
+        "ds_read_b128 v[88:91], %[p] offset:96\n"
+        "ds_read_b128 v[92:95], %[p] offset:112\n"
+        "1:\n"
+        "ds_read_b128 v[96:99], %[p] offset:128\n"
+        "ds_read_b128 v[100:103], %[p] offset:144\n"
+        "ds_read_b128 v[104:107], %[p] offset:160\n"
+        "ds_read_b128 v[108:111], %[p] offset:176\n"
+        "ds_read_b128 v[112:115], %[p] offset:192\n"
+        "ds_read_b128 v[116:119], %[p] offset:208\n"
+        "ds_read_b128 v[120:123], %[p] offset:224\n"
+        "ds_read_b128 v[124:127], %[p] offset:240\n"
+        "s_waitcnt lgkmcnt(8)\n"
+        "v_add_f32 %[acc], %[acc], v64\n"
+        "v_add_f32 %[acc], %[acc], v65\n"
+        "v_add_f32 %[acc], %[acc], v66\n"
+        "v_add_f32 %[acc], %[acc], v67\n"
+        "v_add_f32 %[acc], %[acc], v68\n"
+        "v_add_f32 %[acc], %[acc], v69\n"
+        "v_add_f32 %[acc], %[acc], v70\n"
+        "v_add_f32 %[acc], %[acc], v71\n"
+        "v_add_f32 %[acc], %[acc], v72\n"
+        "v_add_f32 %[acc], %[acc], v73\n"
+        "v_add_f32 %[acc], %[acc], v74\n"
+        "v_add_f32 %[acc], %[acc], v75\n"
+        "v_add_f32 %[acc], %[acc], v76\n"
+        "v_add_f32 %[acc], %[acc], v77\n"
+        "v_add_f32 %[acc], %[acc], v78\n"
+        "v_add_f32 %[acc], %[acc], v79\n"
+        "v_add_f32 %[acc], %[acc], v80\n"
+        "v_add_f32 %[acc], %[acc], v81\n"
+        "v_add_f32 %[acc], %[acc], v82\n"
+        "v_add_f32 %[acc], %[acc], v83\n"
+        "v_add_f32 %[acc], %[acc], v84\n"
+        "v_add_f32 %[acc], %[acc], v85\n"
+        "v_add_f32 %[acc], %[acc], v86\n"
+        "v_add_f32 %[acc], %[acc], v87\n"
+        "v_add_f32 %[acc], %[acc], v88\n"
+        "v_add_f32 %[acc], %[acc], v89\n"
+        "v_add_f32 %[acc], %[acc], v90\n"
+        "v_add_f32 %[acc], %[acc], v91\n"
+        "v_add_f32 %[acc], %[acc], v92\n"
+        "v_add_f32 %[acc], %[acc], v93\n"
+        "v_add_f32 %[acc], %[acc], v94\n"
+        "v_add_f32 %[acc], %[acc], v95\n"
+        "v_add_u32 %[p], 256, %[p]\n"
+        "s_sub_u32 %[i], %[i], 1\n"
+        "s_cmp_eq_u32 %[i], 0\n"
+        "s_cbranch_scc1 2f\n"
+        "ds_read_b128 v[64:67], %[p] offset:0\n"
+        "ds_read_b128 v[68:71], %[p] offset:16\n"
+        "ds_read_b128 v[72:75], %[p] offset:32\n"
+        "ds_read_b128 v[76:79], %[p] offset:48\n"
+        "ds_read_b128 v[80:83], %[p] offset:64\n"
+        "ds_read_b128 v[84:87], %[p] offset:80\n"
+        "ds_read_b128 v[88:91], %[p] offset:96\n"
+        "ds_read_b128 v[92:95], %[p] offset:112\n"
+        "s_waitcnt lgkmcnt(8)\n"
+        "v_add_f32 %[acc], %[acc], v96\n"
+        "v_add_f32 %[acc], %[acc], v97\n"
+        "v_add_f32 %[acc], %[acc], v98\n"
+        "v_add_f32 %[acc], %[acc], v99\n"
+        "v_add_f32 %[acc], %[acc], v100\n"
+        "v_add_f32 %[acc], %[acc], v101\n"
+        "v_add_f32 %[acc], %[acc], v102\n"
+        "v_add_f32 %[acc], %[acc], v103\n"
+        "v_add_f32 %[acc], %[acc], v104\n"
+        "v_add_f32 %[acc], %[acc], v105\n"
+        "v_add_f32 %[acc], %[acc], v106\n"
+        "v_add_f32 %[acc], %[acc], v107\n"
+        "v_add_f32 %[acc], %[acc], v108\n"
+        "v_add_f32 %[acc], %[acc], v109\n"
+        "v_add_f32 %[acc], %[acc], v110\n"
+        "v_add_f32 %[acc], %[acc], v111\n"
+        "v_add_f32 %[acc], %[acc], v112\n"
+        "v_add_f32 %[acc], %[acc], v113\n"
+        "v_add_f32 %[acc], %[acc], v114\n"
+        "v_add_f32 %[acc], %[acc], v115\n"
+        "v_add_f32 %[acc], %[acc], v116\n"
+        "v_add_f32 %[acc], %[acc], v117\n"
+        "v_add_f32 %[acc], %[acc], v118\n"
+        "v_add_f32 %[acc], %[acc], v119\n"
+        "v_add_f32 %[acc], %[acc], v120\n"
+        "v_add_f32 %[acc], %[acc], v121\n"
+        "v_add_f32 %[acc], %[acc], v122\n"
+        "v_add_f32 %[acc], %[acc], v123\n"
+        "v_add_f32 %[acc], %[acc], v124\n"
+        "v_add_f32 %[acc], %[acc], v125\n"
+        "v_add_f32 %[acc], %[acc], v126\n"
+        "v_add_f32 %[acc], %[acc], v127\n"
+        "s_branch 1b\n"
+        "2:\n"
+        "s_waitcnt lgkmcnt(0)\n"
+        "v_add_f32 %[acc], %[acc], v96\n"
+        "v_add_f32 %[acc], %[acc], v97\n"
+        "v_add_f32 %[acc], %[acc], v98\n"
+        "v_add_f32 %[acc], %[acc], v99\n"
+        "v_add_f32 %[acc], %[acc], v100\n"
+        "v_add_f32 %[acc], %[acc], v101\n"
+        "v_add_f32 %[acc], %[acc], v102\n"
+        "v_add_f32 %[acc], %[acc], v103\n"
+        "v_add_f32 %[acc], %[acc], v104\n"
+        "v_add_f32 %[acc], %[acc], v105\n"
+        "v_add_f32 %[acc], %[acc], v106\n"
+        "v_add_f32 %[acc], %[acc], v107\n"
+        "v_add_f32 %[acc], %[acc], v108\n"
+        "v_add_f32 %[acc], %[acc], v109\n"
+        "v_add_f32 %[acc], %[acc], v110\n"
+        "v_add_f32 %[acc], %[acc], v111\n"
+        "v_add_f32 %[acc], %[acc], v112\n"
+        "v_add_f32 %[acc], %[acc], v113\n"
+        "v_add_f32 %[acc], %[acc], v114\n"
+        "v_add_f32 %[acc], %[acc], v115\n"
+        "v_add_f32 %[acc], %[acc], v116\n"
+        "v_add_f32 %[acc], %[acc], v117\n"
+        "v_add_f32 %[acc], %[acc], v118\n"
+        "v_add_f32 %[acc], %[acc], v119\n"
+        "v_add_f32 %[acc], %[acc], v120\n"
+        "v_add_f32 %[acc], %[acc], v121\n"
+        "v_add_f32 %[acc], %[acc], v122\n"
+        "v_add_f32 %[acc], %[acc], v123\n"
+        "v_add_f32 %[acc], %[acc], v124\n"
+        "v_add_f32 %[acc], %[acc], v125\n"
+        "v_add_f32 %[acc], %[acc], v126\n"
+        "v_add_f32 %[acc], %[acc], v127\n"
+        : [acc] "+&v"(acc), [p] "+&v"(p), [i] "+&s"(i)
+        :
+        : "v64", "v65", "v66", "v67", "v68", "v69", "v70", "v71", "v72", "v73", "v74", "v75", "v76", "v77", "v78", "v79", "v80", "v81", "v82", "v83", "v84", "v85", "v86", "v87", "v88", "v89", "v90", "v91", "v92", "v93", "v94", "v95", "v96", "v97", "v98", "v99", "v100", "v101", "v102", "v103", "v104", "v105", "v106", "v107", "v108", "v109", "v110", "v111", "v112", "v113", "v114", "v115", "v116", "v117", "v118", "v119", "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127", "scc", "memory");
+    return acc;
+}
+
+// acc + x_0 + ... + x_{4n-1} over float4 p[0 .. n) of LDS, in order
 __device__ __forceinline__ float chain_quads(float acc, const float4 *p, int n)
 {
-    int i = 0;
-    if (n >= 16) {
-        float4 a[8], b[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) a[k] = p[k];
-        for (; i + 16 <= n; i += 16) {
-#pragma unroll
-            for (int k = 0; k < 8; k++) b[k] = p[i + 8 + k];
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                acc = acc + a[k].x; acc = acc + a[k].y; acc = acc + a[k].z; acc = acc + a[k].w;
-            }
-            const int nx = i + 16 + 8 <= n ? i + 16 : i;   // (the next group, if whole)
-#pragma unroll
-            for (int k = 0; k < 8; k++) a[k] = p[nx + k];
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                acc = acc + b[k].x; acc = acc + b[k].y; acc = acc + b[k].z; acc = acc + b[k].w;
-            }
-        }
-    }
-    for (; i < n; i++) {
+    const int ng = n >> 4;
+    if (ng > 0) acc = chain_lds16(acc, p, ng);
+    for (int i = ng << 4; i < n; i++) {
         const float4 v = p[i];
         acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
     }
     return acc;
 }
+
 
 template <int G>
 __global__ __launch_bounds__(256) void attn_av(const float *__restrict__ att, size_t att_stride,
@@ -808,7 +979,6 @@ __global__ __launch_bounds__(256) void attn_av(const float *__restrict__ att, si
     float *e = (float *)av_lds;                    // [G][estr]: e_j, then a_j
     float4 *prod = av_lds + G * estr / 4;          // [2][AV_CH][AV_PS]
     __shared__ float mx_s[G], inv_s[G];
-    __shared__ int nrm_s[G];
     __shared__ uint64_t tab[32];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
     const int n_cg = hd / DC;
@@ -820,13 +990,31 @@ __global__ __launch_bounds__(256) void attn_av(const float *__restrict__ att, si
     const bool producer = wave > 0;
     const int L = tid - 64;                        // producer lane 0 .. 191
 
+    // 1. head maxima (src/ops.c:26-30): wave w takes heads w, w + 4; their
+    // tile maxima (at most 256 tiles: 15360 positions) and first scores are
+    // requested before any other load, and reduced after the other loads
+    // are issued
+    constexpr int HW = (G + 3) / 4;                // heads per wave
+    const int used = (upto + SC_TILE - 1) / SC_TILE;
+    float tmv[HW][4], s0v[HW];
+#pragma unroll
+    for (int h = 0; h < HW; h++) {
+        const int g = min(wave + 4 * h, G - 1);
+        const float *tm = tmax + ((size_t)kvh * G + g) * n_tiles;
+#pragma unroll
+        for (int u = 0; u < 4; u++) tmv[h][u] = tm[min(lane + 64 * u, used - 1)];
+        s0v[h] = srow[(size_t)g * att_stride];
+    }
+
     // V of the producer's pairs (column c, quad qq) of value blocks
     // 0 .. AV_VD - 1, requested first: they are needed last, and arrive
     // while the softmax runs
     const float4 *v4 = (const float4 *)vc + (size_t)kvh * hd + c0;   // quad jq, column c: v4[jq * kvd + c]
     const int nvb = (nq_all + AV_VB - 1) / AV_VB;
-    // (vb[0] holds the next block to use; the pipeline moves down one
-    // block at a time, so that every index is known at compile time)
+    // (block b's V is in vb[b % AV_VD]; the block loop is unrolled by
+    // AV_VD, so that every index is known at compile time and each slot is
+    // reloaded in place: a load into a temporary moved into the slot would
+    // wait for the load at the move)
     float4 vb[AV_VD][NPL];
     auto v_load = [&](int b, float4 *dst) {
 #pragma unroll
@@ -840,58 +1028,67 @@ __global__ __launch_bounds__(256) void attn_av(const float *__restrict__ att, si
 #pragma unroll
         for (int d = 0; d < AV_VD; d++) v_load(min(d, nvb - 1), vb[d]);
     }
-
-    // 1. head maxima (src/ops.c:26-30): wave w takes heads w, w + 4
-    for (int g = wave; g < G; g += 4) {
-        const float *tm = tmax + ((size_t)kvh * G + g) * n_tiles;
-        const int used = (upto + SC_TILE - 1) / SC_TILE;
-        float m = -INFINITY;
-        for (int i = lane; i < used; i += 64) {
-            const float v = tm[i];
-            m = v > m ? v : m;
+    // the scores of the producer's (head, quad) pairs of exp block k: pair
+    // pi = L + 192 r is head pi / EQ, quad pi % EQ of the block
+    constexpr int EQ = AV_EB / 4;                  // quads of an exp block
+    constexpr int ER = (G * EQ + 191) / 192;       // pairs per producer lane
+    const int neb = (upto + AV_EB - 1) / AV_EB;
+    auto s_load = [&](int k, float4 *s) {
+#pragma unroll
+        for (int r = 0; r < ER; r++) {
+            const int pi = min(L + 192 * r, G * EQ - 1), g = pi / EQ;
+            const int j = min(k * AV_EB + 4 * (pi - g * EQ), (upto - 1) & ~3);
+            s[r] = *(const float4 *)(srow + (size_t)g * att_stride + j);
         }
-        m = wave_reduce(m, -INFINITY, [](float x, float y) { return y > x ? y : x; });
-        const float s0 = srow[(size_t)g * att_stride];
-        if (lane == 0) mx_s[g] = s0 != s0 ? s0 : m;
+    };
+    float4 sc[ER];
+    if (producer) s_load(0, sc);                   // (block 0's scores: with the maxima)
+#pragma unroll
+    for (int h = 0; h < HW; h++) {
+        const int g = wave + 4 * h;
+        if (g < G) {
+            float m = -INFINITY;
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (lane + 64 * u < used) m = tmv[h][u] > m ? tmv[h][u] : m;
+            m = wave_reduce(m, -INFINITY, [](float x, float y) { return y > x ? y : x; });
+            if (lane == 0) mx_s[g] = s0v[h] != s0v[h] ? s0v[h] : m;
+        }
     }
+
     if (tid < 32) tab[tid] = fox_exp2_tab[tid];
     __syncthreads();
 
     // 2. exp blocks and the softmax sums (lane g of wave 0)
-    const int neb = (upto + AV_EB - 1) / AV_EB;
     float sum = 0.0f;
-    {
-        float mx[G];
-#pragma unroll
-        for (int g = 0; g < G; g++) mx[g] = mx_s[g];
-        // the scores of a producer lane's four positions of block k
-        auto s_load = [&](int k, float4 *s) {
-            const int j = min(k * AV_EB + 4 * L, (upto - 1) & ~3);
-#pragma unroll
-            for (int g = 0; g < G; g++) s[g] = *(const float4 *)(srow + (size_t)g * att_stride + j);
-        };
-        float4 sc[G];
-        if (producer) s_load(0, sc);
+    // (the producers and wave 0 run separate loops with the same barriers,
+    // so that each loop body is straight-line code for the compiler's
+    // memory-wait bookkeeping)
+    if (producer) {
         for (int k = 0; k <= neb; k++) {
-            if (producer && k < neb) {
-                float4 cur[G];
+            float4 cur[ER];
 #pragma unroll
-                for (int g = 0; g < G; g++) cur[g] = sc[g];
-                if (k + 1 < neb) s_load(k + 1, sc);
-                const int j = k * AV_EB + 4 * L;
-                if (j < upto) {
+            for (int r = 0; r < ER; r++) cur[r] = sc[r];
+            s_load(min(k + 1, neb - 1), sc);
 #pragma unroll
-                    for (int g = 0; g < G; g++) {
-                        float4 r;
-                        r.x = fox_expf_t(cur[g].x - mx[g], tab);
-                        r.y = j + 1 < upto ? fox_expf_t(cur[g].y - mx[g], tab) : 0.0f;
-                        r.z = j + 2 < upto ? fox_expf_t(cur[g].z - mx[g], tab) : 0.0f;
-                        r.w = j + 3 < upto ? fox_expf_t(cur[g].w - mx[g], tab) : 0.0f;
-                        *(float4 *)(e + g * estr + j) = r;
-                    }
+            for (int r = 0; r < ER; r++) {
+                const int pi = L + 192 * r;
+                const int g = pi / EQ, j = k * AV_EB + 4 * (pi - g * EQ);
+                if (pi < G * EQ && k < neb && j < upto) {
+                    const float m = mx_s[g];
+                    float4 x;
+                    x.x = fox_expf_t(cur[r].x - m, tab);
+                    x.y = j + 1 < upto ? fox_expf_t(cur[r].y - m, tab) : 0.0f;
+                    x.z = j + 2 < upto ? fox_expf_t(cur[r].z - m, tab) : 0.0f;
+                    x.w = j + 3 < upto ? fox_expf_t(cur[r].w - m, tab) : 0.0f;
+                    *(float4 *)(e + g * estr + j) = x;
                 }
             }
-            if (wave == 0 && k > 0 && lane < G) {
+            __syncthreads();
+        }
+    } else {
+        for (int k = 0; k <= neb; k++) {
+            if (k > 0 && lane < G) {
                 // block k - 1, in position order
                 const int j0 = (k - 1) * AV_EB, j1 = min(upto, j0 + AV_EB);
                 const float *er = e + lane * estr;
@@ -903,55 +1100,44 @@ __global__ __launch_bounds__(256) void attn_av(const float *__restrict__ att, si
         }
     }
 
-    // 3. a_j = e_j * (1/sum), or e_j where the sum is not positive
-    // (src/ops.c:35-38)
-    if (wave == 0 && lane < G) {
-        nrm_s[lane] = sum > 0.0f;
-        inv_s[lane] = sum > 0.0f ? fox_div(1.0f, sum) : 1.0f;
-    }
+    // 3. the scale of a_j = e_j * (1/sum), or 1 where the sum is not
+    // positive (src/ops.c:35-38; e * 1 is e exactly); the producers apply it
+    // as they form the products
+    if (wave == 0 && lane < G) inv_s[lane] = sum > 0.0f ? fox_div(1.0f, sum) : 1.0f;
     __syncthreads();
-    for (int i = tid; i < G * nq_all; i += 256) {
-        const int g = i / nq_all, jq = i - g * nq_all;
-        if (nrm_s[g]) {
-            float4 *a = (float4 *)(e + g * estr) + jq;
-            const float inv = inv_s[g];
-            float4 v = *a;
-            v.x = v.x * inv; v.y = v.y * inv; v.z = v.z * inv; v.w = v.w * inv;
-            *a = v;
-        }
-    }
-    __syncthreads();
-
+    float ivg[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) ivg[g] = inv_s[g];
     // 4. value blocks: products by waves 1-3, chains by wave 0
     const int ch = lane;                           // wave 0: chain (g, c) = (ch / DC, ch % DC)
     float acc = 0.0f;
-    for (int b = 0; b <= nvb; b++) {
-        if (producer && b < nvb) {
-            float4 *P = prod + (b & 1) * AV_CH * AV_PS;
+    // the products of block b from V slot vs (then refilled with block
+    // b + AV_VD), without a branch (indices are clamped; past the last block
+    // it recomputes the last quad, into the buffer the chains are not
+    // reading), so that the V loads stay in flight across blocks
+    auto produce = [&](int b, float4 *vs) {
+        float4 *P = prod + (b & 1) * AV_CH * AV_PS;
 #pragma unroll
-            for (int k = 0; k < NPL; k++) {
-                const int pi = L + 192 * k;
-                const int c = pi / AV_VB, qq = pi - c * AV_VB, jq = b * AV_VB + qq;
-                if (pi < DC * AV_VB && jq < nq_all) {
-                    const float4 v = vb[0][k];
+        for (int k = 0; k < NPL; k++) {
+            const int pi = min(L + 192 * k, DC * AV_VB - 1);
+            const int c = pi / AV_VB, qq = pi - c * AV_VB;
+            const int jq = min(b * AV_VB + qq, nq_all - 1);
+            const float4 v = vs[k];
 #pragma unroll
-                    for (int g = 0; g < G; g++) {
-                        const float4 a = ((const float4 *)(e + g * estr))[jq];
-                        float4 p;
-                        p.x = a.x * v.x; p.y = a.y * v.y; p.z = a.z * v.z; p.w = a.w * v.w;
-                        P[(g * DC + c) * AV_PS + qq] = p;
-                    }
-                }
+            for (int g = 0; g < G; g++) {
+                float4 a = ((const float4 *)(e + g * estr))[jq];
+                a.x = a.x * ivg[g]; a.y = a.y * ivg[g]; a.z = a.z * ivg[g]; a.w = a.w * ivg[g];
+                float4 p;
+                p.x = a.x * v.x; p.y = a.y * v.y; p.z = a.z * v.z; p.w = a.w * v.w;
+                P[(g * DC + c) * AV_PS + qq] = p;
             }
-#pragma unroll
-            for (int d = 0; d + 1 < AV_VD; d++)
-#pragma unroll
-                for (int k = 0; k < NPL; k++) vb[d][k] = vb[d + 1][k];
-            if (b + AV_VD < nvb) v_load(b + AV_VD, vb[AV_VD - 1]);
         }
-        if (wave == 0 && b > 0 && ch < AV_CH) {
-            // block b - 1: whole quads of positions below upto, then the
-            // ragged quad's first rem products
+        v_load(min(b + AV_VD, nvb - 1), vs);
+    };
+    // the chains over block b - 1: whole quads of positions below upto,
+    // then the ragged quad's first rem products
+    auto chains = [&](int b) {
+        if (b > 0 && b <= nvb && ch < AV_CH) {
             const float4 *P = prod + ((b - 1) & 1) * AV_CH * AV_PS + ch * AV_PS;
             const int q0 = (b - 1) * AV_VB;
             const int nfull = min(AV_VB, nq - q0);
@@ -963,7 +1149,28 @@ __global__ __launch_bounds__(256) void attn_av(const float *__restrict__ att, si
                 if (rem > 2) acc = acc + v.z;
             }
         }
-        __syncthreads();
+    };
+    static_assert(AV_VD == 4, "the block loop is unrolled by AV_VD");
+    // (separate loops with the same barriers; steps past nvb only recompute)
+    if (producer) {
+        for (int b = 0; b <= nvb; b += AV_VD) {
+            produce(b, vb[0]);
+            __syncthreads();
+            produce(b + 1, vb[1]);
+            __syncthreads();
+            produce(b + 2, vb[2]);
+            __syncthreads();
+            produce(b + 3, vb[3]);
+            __syncthreads();
+        }
+    } else {
+        for (int b = 0; b <= nvb; b += AV_VD) {
+#pragma unroll
+            for (int d = 0; d < AV_VD; d++) {
+                chains(b + d);
+                __syncthreads();
+            }
+        }
     }
     if (wave == 0 && ch < AV_CH) {
         const int g = ch / DC, c = ch - g * DC;
@@ -1037,7 +1244,11 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
                        : gqa == 4 ? (const void *)attn_av<4> : gqa == 8 ? (const void *)attn_av<8>
                                   : nullptr;
         const int estr = (int)(((n_ctx + 31) & ~(size_t)31) + 4);   // (heads in different banks)
-        const size_t av_lds = gqa * (size_t)estr * 4 + 2 * AV_CH * AV_PS * 16;
+        // (at least AV_LDS_MIN: more than half of a compute unit's LDS, so
+        // that no two workgroups share a compute unit, whose chain waves
+        // would share SIMD 0's instruction issue)
+        size_t av_lds = gqa * (size_t)estr * 4 + 2 * AV_CH * AV_PS * 16;
+        if (av_lds < AV_LDS_MIN) av_lds = AV_LDS_MIN;
         const size_t dc = av ? AV_CH / gqa : 1;
         if (M == 1 && av && av_lds <= ATT_LDS_MAX && head_dim % dc == 0) {
             hipError_t e = hipFuncSetAttribute(av, hipFuncAttributeMaxDynamicSharedMemorySize,
