@@ -526,14 +526,15 @@ __global__ void attn_merge(const float *__restrict__ part, int n_head, int hd, i
 //             sums over the block before, then a_j, then the products a_j v_jd
 //             in blocks (V streamed from HBM a few blocks ahead) while the
 //             chain wave adds the block before;
-//   attn_softmax_x + attn_values_x   several tokens, or a context longer than
-//             attn_av's LDS holds: the softmax per (head, token) in place in
-//             the scores, then a lane per (head, column) walking V and the
-//             weights.
+//   attn_sm + attn_avm   several tokens, or a context longer than attn_av's
+//             LDS holds: the softmax per (head, token), a_j written over the
+//             scores, then the value chains of MT tokens per workgroup fed by
+//             the same block pipeline as attn_av.
 
 #define SC_TILE 64
 #define QK_TPW 4            // tokens per scores workgroup (the K tile is read once for them)
 #define ATT_LDS_MAX (159 * 1024)
+#define ATT_EXACT_MAX_CTX 32768     // attn_sm holds a head's weights in LDS
 
 // A workgroup of 256 threads per (64-position tile, kv head, QK_TPW tokens):
 // the tile's K rows (plain loads, row stride padded by one quad against bank
@@ -648,132 +649,6 @@ __global__ __launch_bounds__(256) void attn_qk(const float *__restrict__ q, size
         }
     }
 }
-
-__global__ __launch_bounds__(256) void attn_softmax_x(float *__restrict__ att,
-                                                      size_t att_stride,
-                                                      const float *__restrict__ tmax,
-                                                      int n_tiles, int n_head,
-                                                      const uint32_t *__restrict__ pos,
-                                                      int n_ctx)
-{
-    extern __shared__ float4 e4[];
-    float *e = (float *)e4;
-    __shared__ float red[4];
-    __shared__ float inv_s;
-    __shared__ int norm;
-    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-    const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
-    const int used = (upto + SC_TILE - 1) / SC_TILE;
-    float *row = att + ((size_t)t * n_head + h) * att_stride;
-    const float *tm = tmax + ((size_t)t * n_head + h) * n_tiles;
-    float m = -INFINITY;
-    for (int i = tid; i < used; i += 256) {
-        const float v = tm[i];
-        m = v > m ? v : m;
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float w = __shfl_xor(m, o);
-        m = w > m ? w : m;
-    }
-    if ((tid & 63) == 0) red[tid >> 6] = m;
-    __syncthreads();
-    // src/ops.c:26-30: max starts at x[0] and moves on a strict '>', so a
-    // NaN first score stays the maximum; otherwise NaNs are skipped
-    float mx = red[0];
-    for (int w = 1; w < 4; w++) mx = red[w] > mx ? red[w] : mx;
-    const float s0 = row[0];
-    if (s0 != s0) mx = s0;
-    for (int j = tid; j < upto; j += 256) e[j] = fox_expf(row[j] - mx);
-    __syncthreads();
-    if (tid == 0) {
-        float sum = 0.0f;
-        int j = 0;
-        for (; j + 16 <= upto; j += 16) {
-            const float4 a = *(const float4 *)(e + j), b = *(const float4 *)(e + j + 4);
-            const float4 c = *(const float4 *)(e + j + 8), d = *(const float4 *)(e + j + 12);
-            sum = sum + a.x; sum = sum + a.y; sum = sum + a.z; sum = sum + a.w;
-            sum = sum + b.x; sum = sum + b.y; sum = sum + b.z; sum = sum + b.w;
-            sum = sum + c.x; sum = sum + c.y; sum = sum + c.z; sum = sum + c.w;
-            sum = sum + d.x; sum = sum + d.y; sum = sum + d.z; sum = sum + d.w;
-        }
-        for (; j < upto; j++) sum = sum + e[j];
-        norm = sum > 0.0f;
-        inv_s = norm ? fox_div(1.0f, sum) : 1.0f;
-    }
-    __syncthreads();
-    const float inv = inv_s;
-    const int nrm = norm;
-    for (int j = tid; j < upto; j += 256) row[j] = nrm ? e[j] * inv : e[j];
-}
-
-// One wave per (kv head, column slice, token).  Lane = (query head g of the
-// kv head's group, column d); the wave covers gqa heads x (64 / gqa) columns.
-#define VX_U 8
-
-__device__ __forceinline__ float vx_quad(float acc, float4 a, float4 v)
-{
-    acc = acc + a.x * v.x;
-    acc = acc + a.y * v.y;
-    acc = acc + a.z * v.z;
-    acc = acc + a.w * v.w;
-    return acc;
-}
-
-__global__ __launch_bounds__(64) void attn_values_x(const float *__restrict__ att,
-                                                    size_t att_stride,
-                                                    const float *__restrict__ vc, int n_head,
-                                                    int n_head_kv, int hd, int ds,
-                                                    const uint32_t *__restrict__ pos,
-                                                    int n_ctx, float *__restrict__ out,
-                                                    size_t out_stride)
-{
-    const int lane = threadIdx.x, t = blockIdx.y;
-    const int gqa = n_head / n_head_kv, kvd = n_head_kv * hd;
-    const int n_sl = (hd + ds - 1) / ds;
-    const int kvh = blockIdx.x / n_sl, sl = blockIdx.x - kvh * n_sl;
-    const int g = lane / ds, d = sl * ds + (lane - g * ds);
-    if (g >= gqa || d >= hd) return;
-    const int h = kvh * gqa + g;
-    const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
-    const int nq = upto >> 2;
-    const float4 *ap = (const float4 *)(att + ((size_t)t * n_head + h) * att_stride);
-    const float4 *vp = (const float4 *)vc + (size_t)kvh * hd + d;   // quad jq at vp[jq * kvd]
-    float acc = 0.0f;
-    int jq = 0;
-    if (nq >= 2 * VX_U) {
-        float4 va[VX_U], aa[VX_U], vb[VX_U], ab[VX_U];
-#pragma unroll
-        for (int u = 0; u < VX_U; u++) {
-            va[u] = vp[(size_t)u * kvd];
-            aa[u] = ap[u];
-        }
-        for (; jq + 2 * VX_U <= nq; jq += 2 * VX_U) {
-#pragma unroll
-            for (int u = 0; u < VX_U; u++) {
-                vb[u] = vp[(size_t)(jq + VX_U + u) * kvd];
-                ab[u] = ap[jq + VX_U + u];
-            }
-#pragma unroll
-            for (int u = 0; u < VX_U; u++) acc = vx_quad(acc, aa[u], va[u]);
-#pragma unroll
-            for (int u = 0; u < VX_U; u++) {
-                // the next pair's first half, clamped inside the visible rows
-                const int k = jq + 2 * VX_U + u < nq ? jq + 2 * VX_U + u : nq - 1;
-                va[u] = vp[(size_t)k * kvd];
-                aa[u] = ap[k];
-            }
-#pragma unroll
-            for (int u = 0; u < VX_U; u++) acc = vx_quad(acc, ab[u], vb[u]);
-        }
-    }
-    for (; jq < nq; jq++) acc = vx_quad(acc, ap[jq], vp[(size_t)jq * kvd]);
-    const float *as = (const float *)(ap + nq);
-    const float *vs = (const float *)(vp + (size_t)nq * kvd);
-    for (int r = 0; r < (upto & 3); r++) acc = acc + as[r] * vs[r];
-    out[(size_t)t * out_stride + (size_t)h * hd + d] = acc;
-}
-
 
 // ---- one token: softmax and values in one workgroup per (kv head, AV_CH
 // output chains), 256 threads.  The chains are (query head g, column c) for
@@ -1178,6 +1053,241 @@ __global__ __launch_bounds__(256) void attn_av(const float *__restrict__ att, si
     }
 }
 
+// ---- several tokens, or a context longer than attn_av's LDS holds: the
+// softmax and the values in two launches.
+//   attn_sm   a workgroup per (query head, token): the maximum, then e_j in
+//             blocks of SM_EB positions by waves 1-3 while lane 0 of wave 0
+//             adds the block before, then a_j = e_j * (1/sum) written over
+//             the scores;
+//   attn_avm  a workgroup per (kv head, AV_CH / G columns, MT tokens): wave 0
+//             runs the MT x AV_CH chains (lane = token * AV_CH + head * DC +
+//             column); waves 1-3 stage block b + 1's a_j and V quads from
+//             registers (loaded AV_VD blocks ahead) into LDS and multiply block
+//             b's into one of two product buffers while wave 0 adds block
+//             b - 1; a barrier between blocks.
+#define SM_EB 768           // positions of a softmax exp block (four per producer lane)
+#define MT 4                // tokens per attn_avm workgroup
+#define MV_VB 48            // quads of an attn_avm value block
+#define MV_PS (MV_VB + 1)
+
+__global__ __launch_bounds__(256) void attn_sm(float *__restrict__ att, size_t att_stride,
+                                               const float *__restrict__ tmax, int n_tiles,
+                                               int n_head, const uint32_t *__restrict__ pos,
+                                               int n_ctx)
+{
+    extern __shared__ float4 sm_lds[];
+    float *e = (float *)sm_lds;                    // [ceil4(upto)]
+    __shared__ float mx_s, inv_s;
+    __shared__ uint64_t tab[32];
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
+    const int h = blockIdx.x, t = blockIdx.y;
+    const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
+    float *row = att + ((size_t)t * n_head + h) * att_stride;
+    const bool producer = wave > 0;
+    const int L = tid - 64;
+    const int neb = (upto + SM_EB - 1) / SM_EB;
+    auto s_load = [&](int k) {
+        return *(const float4 *)(row + min(k * SM_EB + 4 * L, (upto - 1) & ~3));
+    };
+    float4 sc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (producer) sc = s_load(0);
+    if (wave == 0) {
+        // src/ops.c:26-30: a NaN first score stays the maximum
+        const float *tm = tmax + ((size_t)t * n_head + h) * n_tiles;
+        const int used = (upto + SC_TILE - 1) / SC_TILE;
+        float m = -INFINITY;
+        for (int i = lane; i < used; i += 64) {
+            const float v = tm[i];
+            m = v > m ? v : m;
+        }
+        m = wave_reduce(m, -INFINITY, [](float x, float y) { return y > x ? y : x; });
+        const float s0 = row[0];
+        if (lane == 0) mx_s = s0 != s0 ? s0 : m;
+    }
+    if (tid < 32) tab[tid] = fox_exp2_tab[tid];
+    __syncthreads();
+    float sum = 0.0f;
+    if (producer) {
+        const float m = mx_s;
+        for (int k = 0; k <= neb; k++) {
+            const float4 cur = sc;
+            sc = s_load(min(k + 1, neb - 1));
+            const int j = k * SM_EB + 4 * L;
+            if (k < neb && j < upto) {
+                float4 x;
+                x.x = fox_expf_t(cur.x - m, tab);
+                x.y = j + 1 < upto ? fox_expf_t(cur.y - m, tab) : 0.0f;
+                x.z = j + 2 < upto ? fox_expf_t(cur.z - m, tab) : 0.0f;
+                x.w = j + 3 < upto ? fox_expf_t(cur.w - m, tab) : 0.0f;
+                *(float4 *)(e + j) = x;
+            }
+            __syncthreads();
+        }
+    } else {
+        for (int k = 0; k <= neb; k++) {
+            if (k > 0 && lane == 0) {
+                const int j0 = (k - 1) * SM_EB, j1 = min(upto, j0 + SM_EB);
+                const int nqk = (j1 - j0) >> 2;
+                sum = chain_quads(sum, (const float4 *)(e + j0), nqk);
+                for (int j = j0 + 4 * nqk; j < j1; j++) sum = sum + e[j];
+            }
+            __syncthreads();
+        }
+    }
+    // src/ops.c:35-38: a_j = e_j * (1/sum) when the sum is positive
+    if (tid == 0) inv_s = sum > 0.0f ? fox_div(1.0f, sum) : 1.0f;
+    __syncthreads();
+    const float inv = inv_s;
+    for (int jq = tid; jq < (upto + 3) >> 2; jq += 256) {
+        float4 v = ((const float4 *)e)[jq];
+        v.x = v.x * inv; v.y = v.y * inv; v.z = v.z * inv; v.w = v.w * inv;
+        ((float4 *)row)[jq] = v;
+    }
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void attn_avm(const float *__restrict__ att, size_t att_stride,
+                                                const float *__restrict__ vc, int n_head_kv,
+                                                int hd, int gq, const uint32_t *__restrict__ pos,
+                                                int n_ctx, float *__restrict__ out,
+                                                size_t out_stride, int M)
+{
+    // G: the query heads per kv head, gq, rounded up to a power of two (the
+    // rows of heads gq .. G - 1 repeat head gq - 1 and are not written)
+    constexpr int DC = AV_CH / G;                  // columns of the workgroup
+    constexpr int NR = G * MT;                     // weight rows (token, head)
+    constexpr int NA = (NR * MV_VB + 191) / 192;   // weight quads per producer lane and block
+    constexpr int NV = (DC * MV_VB + 191) / 192;   // V quads per producer lane and block
+    constexpr int NP = MT * AV_CH * MV_VB / 192;   // products per producer lane and block
+    static_assert(MT * AV_CH == 64 && MT * AV_CH * MV_VB % 192 == 0, "attn_avm lane layout");
+    // (slots and staging as native 4-vectors: a float4 struct copied into
+    // an array slot is a memcpy the compiler keeps in scratch memory)
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    __shared__ f4v A[2][NR * MV_VB], Vs[2][DC * MV_VB];
+    extern __shared__ float4 prod[];               // [2][64][MV_PS]
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
+    const int n_cg = (hd + DC - 1) / DC;           // (columns past hd: V's last column, not written)
+    const int kvh = blockIdx.x / n_cg, c0 = (blockIdx.x - kvh * n_cg) * DC;
+    const int n_head = n_head_kv * gq, kvd = n_head_kv * hd;
+    const int t0 = (int)blockIdx.y * MT, nt = min(MT, M - t0);
+    auto upto_of = [&](int tl) { return (int)min((size_t)pos[0] + (size_t)(t0 + tl) + 1, (size_t)n_ctx); };
+    const int upto_max = upto_of(nt - 1), nq_max = (upto_max + 3) >> 2;
+    const int nvb = (nq_max + MV_VB - 1) / MV_VB;
+    const bool producer = wave > 0;
+    const int L = tid - 64;
+
+    // a producer lane's loads of block b: weight quads (row r = token *
+    // G + head, quad qq) and V quads (column c, quad qq); indices clamped, so
+    // every load is inside the buffers (rows of tokens past nt and quads past
+    // a token's end are loaded and multiplied, never added)
+    struct Slot { f4v a[NA], v[NV]; };
+    auto load = [&](int b, Slot &sl) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < NA; k++) {
+            const int pa = min(L + 192 * k, NR * MV_VB - 1), r = pa / MV_VB;
+            const int tl = min(r / G, nt - 1), g = min(r - (r / G) * G, gq - 1);
+            const int jq = min(b * MV_VB + (pa - r * MV_VB), nq_max - 1);
+            sl.a[k] = ((const f4v *)(att + ((size_t)(t0 + tl) * n_head + (size_t)kvh * gq + g) *
+                                               att_stride))[jq];
+        }
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int pv = min(L + 192 * k, DC * MV_VB - 1), c = pv / MV_VB;
+            const int jq = min(b * MV_VB + (pv - c * MV_VB), nq_max - 1);
+            sl.v[k] = ((const f4v *)vc)[(size_t)jq * kvd + (size_t)kvh * hd + min(c0 + c, hd - 1)];
+        }
+    };
+    auto stage = [&](int b, const Slot &sl) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < NA; k++) {
+            const int pa = L + 192 * k;
+            if (pa < NR * MV_VB) A[b & 1][pa] = sl.a[k];
+        }
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int pv = L + 192 * k;
+            if (pv < DC * MV_VB) Vs[b & 1][pv] = sl.v[k];
+        }
+    };
+    // the products of block b from the staged quads: product pi = L + 192 k
+    // is chain pi / MV_VB (token, head, column), quad pi % MV_VB
+    auto products = [&](int b) __attribute__((always_inline)) {
+        float4 *P = prod + (b & 1) * 64 * MV_PS;
+#pragma unroll
+        for (int k = 0; k < NP; k++) {
+            const int pi = L + 192 * k, ch = pi / MV_VB, qq = pi - ch * MV_VB;
+            const int tl = ch / AV_CH, rm = ch - tl * AV_CH, g = rm / DC, c = rm - g * DC;
+            const f4v a = A[b & 1][(tl * G + g) * MV_VB + qq];
+            const f4v v = Vs[b & 1][c * MV_VB + qq];
+            float4 p;
+            p.x = a.x * v.x; p.y = a.y * v.y; p.z = a.z * v.z; p.w = a.w * v.w;
+            P[ch * MV_PS + qq] = p;
+        }
+    };
+    // wave 0: chain lane = (token tl, head g, column c); its token's whole
+    // quads of block b - 1, then its ragged quad's first rem products
+    const int tl = lane / AV_CH, rm = lane - tl * AV_CH;
+    const int my_upto = upto_of(min(tl, nt - 1)), my_nq = my_upto >> 2, my_rem = my_upto & 3;
+    const int nq_min = upto_of(0) >> 2;            // (the shortest token's whole quads)
+    float acc = 0.0f;
+    auto chains = [&](int b) __attribute__((always_inline)) {
+        // groups of 16 quads whole for every token: one wave-uniform asm
+        // chain; then the lane's own rest
+        const int q0 = (b - 1) * MV_VB;
+        const int ng = __builtin_amdgcn_readfirstlane(max(0, min(MV_VB, nq_min - q0)) >> 4);
+        if (b > 0 && b <= nvb && tl < nt) {
+            const float4 *P = prod + ((b - 1) & 1) * 64 * MV_PS + lane * MV_PS;
+            if (ng > 0) acc = chain_lds16(acc, P, ng);
+            const int nfull = min(MV_VB, my_nq - q0);
+            for (int i = ng << 4; i < nfull; i++) {
+                const float4 v = P[i];
+                acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
+            }
+            if (my_rem && nfull >= 0 && nfull < MV_VB) {
+                const float4 v = P[nfull];
+                acc = acc + v.x;
+                if (my_rem > 1) acc = acc + v.y;
+                if (my_rem > 2) acc = acc + v.z;
+            }
+        }
+    };
+    static_assert(AV_VD == 4, "the block loop is unrolled by AV_VD");
+    if (producer) {
+        // slot s holds block b with b % AV_VD == s; step b stages block b + 1
+        // and multiplies block b
+        Slot sl[AV_VD];
+#pragma unroll
+        for (int d = 0; d < AV_VD; d++) load(min(d, nvb - 1), sl[d]);
+        stage(0, sl[0]);
+        load(min(AV_VD, nvb - 1), sl[0]);
+        __syncthreads();
+        auto step = [&](int b, Slot &s1) __attribute__((always_inline)) {
+            stage(b + 1, s1);
+            load(min(b + 1 + AV_VD, nvb - 1), s1);
+            products(b);
+            __syncthreads();
+        };
+        for (int b = 0; b <= nvb; b += AV_VD) {
+            step(b, sl[1]);
+            step(b + 1, sl[2]);
+            step(b + 2, sl[3]);
+            step(b + 3, sl[0]);
+        }
+    } else {
+        __syncthreads();
+        for (int b = 0; b <= nvb; b += AV_VD) {
+#pragma unroll
+            for (int d = 0; d < AV_VD; d++) {
+                chains(b + d);
+                __syncthreads();
+            }
+        }
+        const int g = rm / DC, c = rm - g * DC;
+        if (tl < nt && g < gq && c0 + c < hd)
+            out[(size_t)(t0 + tl) * out_stride + (size_t)(kvh * gq + g) * hd + c0 + c] = acc;
+    }
+}
+
 extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t out_stride,
                                             const float *q, size_t q_stride, const float *k_cache,
                                             const float *v_cache, size_t n_head, size_t n_head_kv,
@@ -1202,10 +1312,10 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
         return fox_fail(FOX_GPU_ERR_ARG, "attention: q and the caches must be 16-byte aligned "
                         "and the q stride a multiple of 4");
     if (mode == FOX_GPU_ATTN_EXACT) {
-        if (n_ctx * sizeof(float) > 60 * 1024)
+        if (n_ctx > ATT_EXACT_MAX_CTX)
             return fox_fail(FOX_GPU_ERR_UNSUPPORTED,
                             "attention: exact mode keeps a head's %zu weights in LDS; at most "
-                            "15360 positions", n_ctx);
+                            "%d positions", n_ctx, ATT_EXACT_MAX_CTX);
         const size_t att_stride = (n_ctx + 3) & ~(size_t)3;
         const int n_tiles = (int)((n_ctx + SC_TILE - 1) / SC_TILE);
         const size_t att_bytes = M * n_head * att_stride * sizeof(float);
@@ -1250,7 +1360,7 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
         size_t av_lds = gqa * (size_t)estr * 4 + 2 * AV_CH * AV_PS * 16;
         if (av_lds < AV_LDS_MIN) av_lds = AV_LDS_MIN;
         const size_t dc = av ? AV_CH / gqa : 1;
-        if (M == 1 && av && av_lds <= ATT_LDS_MAX && head_dim % dc == 0) {
+        if (M == 1 && av && av_lds <= ATT_LDS_MAX && head_dim % dc == 0 && n_tiles <= 256) {
             hipError_t e = hipFuncSetAttribute(av, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                (int)av_lds);
             if (e != hipSuccess) return fox_hip_fail(e, "attention: LDS size");
@@ -1263,15 +1373,37 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
             FOX_LAUNCHED("attention softmax+values");
             return FOX_GPU_OK;
         }
-        const int ds = (int)(64 / gqa);
-        const int n_sl = (int)((head_dim + ds - 1) / ds);
-        hipLaunchKernelGGL(attn_softmax_x, dim3((unsigned)n_head, (unsigned)M), dim3(256),
-                           att_stride * sizeof(float), ctx->stream, att, att_stride, tmax,
-                           n_tiles, (int)n_head, pos, (int)n_ctx);
-        FOX_LAUNCHED("attention softmax");
-        hipLaunchKernelGGL(attn_values_x, dim3((unsigned)(n_head_kv * n_sl), (unsigned)M),
-                           dim3(64), 0, ctx->stream, att, att_stride, v_cache, (int)n_head,
-                           (int)n_head_kv, (int)head_dim, ds, pos, (int)n_ctx, out, os);
+        // softmax per (head, token), then the values of MT tokens per
+        // workgroup
+        const int gp = gqa == 1 ? 1 : gqa == 2 ? 2 : gqa <= 4 ? 4 : 8;
+        const size_t dcm = AV_CH / gp;
+        {
+            const size_t sm_lds = att_stride * sizeof(float);
+            if (sm_lds > 64 * 1024) {
+                hipError_t e = hipFuncSetAttribute((const void *)attn_sm,
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   (int)sm_lds);
+                if (e != hipSuccess) return fox_hip_fail(e, "attention: LDS size");
+            }
+            hipLaunchKernelGGL(attn_sm, dim3((unsigned)n_head, (unsigned)M), dim3(256), sm_lds,
+                               ctx->stream, att, att_stride, tmax, n_tiles, (int)n_head, pos,
+                               (int)n_ctx);
+            FOX_LAUNCHED("attention softmax");
+        }
+        const void *avm = gp == 1 ? (const void *)attn_avm<1> : gp == 2 ? (const void *)attn_avm<2>
+                        : gp == 4 ? (const void *)attn_avm<4> : (const void *)attn_avm<8>;
+        const size_t avm_lds = 2 * 64 * MV_PS * 16;
+        hipError_t e = hipFuncSetAttribute(avm, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)avm_lds);
+        if (e != hipSuccess) return fox_hip_fail(e, "attention: LDS size");
+        const int iM = (int)M, igq = (int)gqa;
+        void *args[] = {(void *)&att, (void *)&att_stride, (void *)&v_cache, (void *)&ikv,
+                        (void *)&ihd, (void *)&igq, (void *)&pos, (void *)&ictx, (void *)&out,
+                        (void *)&os, (void *)&iM};
+        e = hipLaunchKernel(avm, dim3((unsigned)(n_head_kv * ((head_dim + dcm - 1) / dcm)),
+                                      (unsigned)((M + MT - 1) / MT)),
+                            dim3(256), args, avm_lds, ctx->stream);
+        if (e != hipSuccess) return fox_hip_fail(e, "attention values");
         FOX_LAUNCHED("attention values");
         return FOX_GPU_OK;
     }

@@ -59,9 +59,9 @@ CASES = [  # n_head, n_kv, hd, n_ctx, pos, M
     (6, 6, 48, 77, 70, 1),         # tiny-288 heads
     (4, 1, 128, 64, 0, 1),         # a single visible row
     (16, 2, 128, 257, 200, 8),     # 8 tokens (verify batch), gqa 8
-    (12, 4, 64, 100, 99, 1),       # gqa 3: the three-kernel path
+    (12, 4, 64, 100, 99, 1),       # gqa 3: softmax and values in launches of their own
     (8, 2, 64, 6000, 5990, 2),     # weights leave room for few product stages (4)
-    (8, 2, 64, 9000, 8990, 2),     # weights beyond the fused kernel's LDS: three-kernel path
+    (8, 2, 64, 9000, 8990, 2),     # two tokens: softmax and values in launches of their own
     # one token, scores in the same launch: several rounds of score tiles per
     # workgroup, partial chunks, workgroups without tiles
     (8, 8, 128, 1200, 1150, 1),    # gqa 1: two slices, 9 tiles each (3 rounds)
@@ -73,11 +73,20 @@ CASES = [  # n_head, n_kv, hd, n_ctx, pos, M
     (32, 16, 128, 700, 699, 1),    # 27B heads, 16 kv heads, near the last row
     (8, 2, 128, 200, 127, 5),      # 5 tokens: a score tile first reached by the second token
     (16, 4, 64, 300, 250, 7),      # 7 tokens: four to a score workgroup, then three
-    # more than one round of softmax+values workgroups over 256 compute
-    # units: the softmax sums in a launch of their own, once per head
-    (32, 8, 128, 2200, 2048, 8),   # 4B/8B heads, 8 tokens: 512 workgroups
-    (32, 16, 128, 1100, 1000, 8),  # 27B heads, 8 tokens, gqa 2: 512 workgroups
-    (32, 8, 128, 300, 295, 5),     # 5 tokens up to the cache end: 320 workgroups
+    # several tokens: a softmax workgroup per (head, token), then value
+    # workgroups of four tokens whose chains end at different positions
+    (32, 8, 128, 2200, 2048, 8),   # 4B/8B heads, 8 tokens
+    (32, 16, 128, 1100, 1000, 8),  # 27B heads, 8 tokens, gqa 2
+    (32, 8, 128, 300, 295, 5),     # 5 tokens up to the cache end (the last group of one)
+    (12, 4, 64, 500, 450, 3),      # gqa 3 (heads padded to 4), 3 tokens
+    (12, 2, 64, 300, 280, 6),      # gqa 6 (heads padded to 8), 6 tokens
+    (8, 8, 64, 1000, 190, 8),      # tokens ending on both sides of a value block (192 positions)
+    (6, 6, 40, 120, 100, 2),       # hd 40: the last 16 columns of a head partly past its end
+    (4, 2, 4, 32, 20, 3),          # hd 4 (the tiny fixture's heads): 8 columns per group
+    # one token past the fused kernel's LDS: the two-launch path
+    (16, 2, 128, 16400, 16399, 1), # gqa 8, 257 score tiles
+    (8, 8, 64, 20000, 19990, 1),   # gqa 1, 20000 positions
+    (4, 1, 64, 32768, 32767, 1),   # the longest context exact mode takes
 ]
 
 
@@ -108,12 +117,12 @@ def test_attention_split_within_rounding(gpu, oracle, case):
 
 
 @pytest.mark.parametrize("case", [(4, 2, 64, 40, 39, 1), (32, 8, 128, 300, 290, 8)],
-                         ids=["one_token", "sums_launch"])
+                         ids=["one_token", "several_tokens"])
 def test_nan_first_score_follows_the_reference(gpu, oracle, case):
     """src/ops.c:26-30: a NaN score at position 0 stays the maximum, so every
     weight of that head is NaN and the sum is not normalised; a NaN later in
     the row is skipped by the maximum.  Other heads are unaffected.  The
-    second case runs the softmax sums in a launch of their own."""
+    second case runs the softmax in a launch of its own."""
     n_head, n_kv, hd, n_ctx, pos, M = case
     rng = np.random.default_rng(5)
     q = (rng.standard_normal((M, n_head * hd)) * 0.3).astype(np.float32)
@@ -125,3 +134,16 @@ def test_nan_first_score_follows_the_reference(gpu, oracle, case):
     nh0 = (n_head // n_kv) * hd
     assert np.isnan(want[:, :nh0]).all() and np.isnan(got[:, :nh0]).all()
     assert np.array_equal(got[:, nh0:].view(np.uint32), want[:, nh0:].view(np.uint32))
+
+
+def test_exact_mode_rejects_contexts_beyond_its_limit(gpu):
+    """Exact mode keeps one head's weights in LDS: a longer cache is refused
+    before anything is launched."""
+    n_head, n_kv, hd, n_ctx = 4, 1, 64, 32772
+    kc = gpu.empty(n_ctx * n_kv * hd, np.float32)
+    vc = gpu.empty(n_ctx * n_kv * hd, np.float32)
+    dq = gpu.empty(n_head * hd, np.float32)
+    dpos = gpu.array(np.array([0], np.uint32))
+    out = gpu.empty(n_head * hd, np.float32)
+    with pytest.raises(rf.FoxError):
+        gpu.attention(out, dq, kc, vc, n_head, n_kv, hd, 1, dpos, n_ctx, rf.ATTN_EXACT)
