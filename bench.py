@@ -440,17 +440,20 @@ def timed_tokens(step, budget_s, max_tokens, min_tokens=2, warm=True):
     return statistics.median(times), len(times)
 
 
-def cpu_port(path, spec, threads, budget_s, max_tokens, min_tokens=2, warm=True):
+def cpu_port(path, spec, threads, budget_s, max_tokens, min_tokens=2, warm=True,
+             prefill=PREFILL):
     """The oracle (oracle/liboracle.so, the C restatement of RustFox's path)
     decoding the same file after the same injected cache rows, greedy from
-    token 1 at position PREFILL.  Returns the median step time, the number
-    of timed steps, the greedy ids of every step (the untimed first one
-    included) and the first step's logits."""
+    token 1 at position `prefill` (0: an empty cache, as RustFox itself is
+    timed).  Returns the median step time, the number of timed steps, the
+    greedy ids of every step (the untimed first one included) and the first
+    step's logits."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from oracle_libs import Oracle  # test infrastructure: the oracle, timed as the CPU baseline
     om = Oracle().model(spec, synth.map_tensors(path, spec))
-    ctx = om.context(PREFILL + max_tokens + 8, n_batch=8, n_threads=threads)
-    prefill_cache(lambda l, k, v: ctx.set_kv(l, 0, k, v), ctx.set_pos, spec, PREFILL)
+    ctx = om.context(prefill + max_tokens + 8, n_batch=8, n_threads=threads)
+    if prefill:
+        prefill_cache(lambda l, k, v: ctx.set_kv(l, 0, k, v), ctx.set_pos, spec, prefill)
     state = {"tok": 1, "ids": [], "first": None}
 
     def step():
@@ -533,6 +536,18 @@ def cpu_baseline(path, spec, budget_s):
         r = cpu_reference(path, threads, budget_s * 0.15, 16)
         r1 = cpu_reference(path, 1, 0.0, 1, min_tokens=1) if r else None
         if r:
+            # the port at the same short context, same threads, same run:
+            # the fidelity of the port-based figure
+            ps, pn, _, _ = cpu_port(path, spec, threads, budget_s * 0.15, 16, prefill=0)
+            out["port_vs_reference"] = {
+                "port_tok_s": round(1.0 / ps, 3), "reference_tok_s": round(1.0 / r[0], 3),
+                "port_tok_s_over_reference": round(r[0] / ps, 3), "cores": threads,
+                "sample": (f"both decode the same file greedy from token 1 with an empty "
+                           f"cache on {threads} threads: medians of {pn} (port) and {r[1]} "
+                           f"(RustFox) steps at positions 2..17; RustFox's own time per "
+                           f"step, the port's around its eval call")}
+            log(f"bench: cpu port {1 / ps:.3f} tok/s vs reference {1 / r[0]:.3f} tok/s at "
+                f"short context ({r[0] / ps:.3f}x)")
             out["reference_short_context"] = {
                 "value": round(1.0 / r[0], 3), "unit": "tok/s", "cores": threads,
                 "one_thread": round(1.0 / r1[0], 4) if r1 else None,

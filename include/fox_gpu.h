@@ -77,6 +77,12 @@ fox_gpu_status fox_gpu_device_info(fox_gpu_ctx *ctx, char *name, size_t cap,
  * speed differs.  No counterpart in RustFox: the CPU pool's thread count
  * (src/threadpool.c:76) plays this role there. */
 fox_gpu_status fox_gpu_set_max_workgroups(fox_gpu_ctx *ctx, int n);
+/* Bytes of device memory the context's workspace holds now (it grows on
+ * demand and never shrinks; earlier, smaller workspaces a captured graph may
+ * still address are not counted).  No counterpart in RustFox, whose scratch
+ * is per-thread stack and heap: a diagnostic for callers that must not let
+ * a call allocate (fox_gpu_gemv_noalloc leaves it unchanged). */
+size_t         fox_gpu_workspace_bytes(const fox_gpu_ctx *ctx);
 
 /* ------------------------------------------------------------- memory */
 

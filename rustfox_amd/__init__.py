@@ -127,6 +127,8 @@ def gpu_lib() -> C.CDLL:
                                      "fox_gpu_graph_free", "fox_gpu_event_destroy") else C.c_int
     L.fox_gpu_last_error.restype = C.c_char_p
     L.fox_gpu_last_error.argtypes = []
+    L.fox_gpu_workspace_bytes.restype = C.c_size_t
+    L.fox_gpu_workspace_bytes.argtypes = [vp]
     _gpu = L
     return L
 
@@ -242,6 +244,10 @@ class Gpu:
     def set_max_workgroups(self, n: int):
         """Cap the fused GEMVs' persistent grid (0: two per compute unit)."""
         _check(self.lib.fox_gpu_set_max_workgroups(self.ctx, n))
+
+    def workspace_bytes(self) -> int:
+        """Device bytes the context's workspace holds now."""
+        return int(self.lib.fox_gpu_workspace_bytes(self.ctx))
 
     def info(self):
         name = C.create_string_buffer(128)

@@ -40,10 +40,14 @@ __host__ __device__ constexpr int pf_of(int R4, int epi2)
     return epi2 * R4 < 4 ? 4 : epi2 * R4 > 8 ? 8 : epi2 * R4;
 }
 // LDS per workgroup: two workgroups share a compute unit up to two tokens,
-// one has it alone from three on (fused_go_r)
+// one has it alone from three on (fused_go_r).  The bound is on the dynamic
+// carve-up (fused_lds); the kernel's static arrays (reduction slots of up to
+// four tokens per wave and the token scales, checked against this figure in
+// the kernel) come on top of it.
+#define FUSED_STATIC_LDS 512
 __host__ __device__ constexpr int fused_lds_max(size_t M)
 {
-    return M > 2 ? 160 * 1024 : 96 * 1024;
+    return (M > 2 ? 160 * 1024 : 96 * 1024) - FUSED_STATIC_LDS;
 }
 
 enum { IN_Q = 0, IN_F32 = 1, IN_NORM = 2 };
@@ -1023,6 +1027,8 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     __shared__ double dred[FW * TG];
     __shared__ uint32_t ured[FW * TG];
     __shared__ float ascale[FOX_GPU_MAX_TOKENS];
+    static_assert(sizeof(dred) + sizeof(ured) + sizeof(ascale) <= FUSED_STATIC_LDS,
+                  "static LDS beyond the bound fused_lds_max leaves for it");
 
     constexpr int CHUNK = FMT == FMT_TQ2 ? TQ2_CHUNK : FMT == FMT_Q4K ? Q4K_CHUNK : Q6K_CHUNK;
     // the K-quant of segment sg (FMT_KQMIX: per segment) and its chunk bytes

@@ -127,6 +127,11 @@ extern "C" fox_gpu_status fox_gpu_set_max_workgroups(fox_gpu_ctx *ctx, int n)
     return FOX_GPU_OK;
 }
 
+extern "C" size_t fox_gpu_workspace_bytes(const fox_gpu_ctx *ctx)
+{
+    return ctx ? ctx->ws_cap : 0;
+}
+
 extern "C" fox_gpu_status fox_gpu_device_info(fox_gpu_ctx *ctx, char *name, size_t cap,
                                               int *compute_units, uint64_t *hbm_bytes)
 {

@@ -88,6 +88,29 @@ def test_streamed_equals_resident(models, name):
     assert ev0 == 0 and reads0 == n_tensors
 
 
+@pytest.mark.parametrize("name", ["4b", "8b"])
+def test_streamed_equals_resident_at_benchmark_dims(tmp_path, name):
+    """Three layers of the benchmark models at their own dimensions: a 4B
+    TQ1_0 layer (21 MB) and an 8B Q4_K/Q6_K layer (123 MB) are read by
+    several reader threads over byte ranges that cross tensor boundaries,
+    and the 8B layers are repacked from the staging buffer as Q4_K and Q6_K
+    blocks.  Logits and greedy ids equal the resident backend's, with a
+    budget of two layer slots that forces evictions."""
+    s = synth.spec(name, n_layer=3, n_ctx=128)
+    p = str(tmp_path / f"{name}.gguf")
+    print(f"case stream {name}: writing the 3-layer GGUF", flush=True)
+    synth.write_gguf(p, s)
+    layer, outside = split_bytes(s)
+    prompt = synth.prompt_ids(16, s.n_vocab)
+    print(f"case stream {name}: layer {layer} B, outside {outside} B", flush=True)
+    want, want_ids, _, _ = run(p, rf.WEIGHTS_DEVICE, 0, prompt, 4)
+    got, ids, reads, ev = run(p, rf.WEIGHTS_STREAM, outside + 2 * layer, prompt, 4)
+    for k, (g, w) in enumerate(zip(got, want)):
+        assert np.array_equal(bits(g), bits(w)), f"{name} step {k}: streamed logits differ"
+    assert list(ids) == list(want_ids)
+    assert ev > 0 and reads > len(synth.tensor_list(s))
+
+
 def test_stream_budget_and_leases(models):
     s, p = models["tiny-512"]
     layer, outside = split_bytes(s)

@@ -3,9 +3,9 @@ fox_gpu_gemv, through the C ABI: bit-identical outputs on two calls in a
 row, the second with a smaller input, for weights whose GEMV uses the
 scratch (Q4_K, Q6_K; TQ1_0 with 8 tokens of 21504 values or 2 of 24576,
 more than the fused path holds) and for one that needs none (fused
-TQ1_0)."""
-import ctypes as C
-
+TQ1_0).  The no-alloc calls run first, on a fresh context, and must leave
+its workspace exactly as it was; fox_gpu_gemv runs afterwards on the same
+context for the expected outputs."""
 import numpy as np
 import pytest
 
@@ -27,15 +27,24 @@ def noalloc(gpu, t, x, M, out, flags=0):
     ("TQ1_0", 34, (21504, 5376, 8), (24576, 300, 2)),
     ("TQ1_0", 34, (2560, 4096, 1), (512, 64, 1)),
 ])
-def test_noalloc_equals_gemv(gpu, tname, gtype, first, second):
+def test_noalloc_equals_gemv(tname, gtype, first, second):
     rng = np.random.default_rng([gtype, first[0], 3])
-    for K, N, M in (first, second):
-        print(f"case noalloc {tname} K={K} N={N} M={M}", flush=True)
-        w = weights(rng, gtype, N, K)
-        t = gpu.tensor(gtype, K, N, w)
-        x = gpu.array(rng.standard_normal((M, K)).astype(np.float32))
-        base = rng.standard_normal((M, N)).astype(np.float32)
-        a, b = gpu.array(base), gpu.array(base)
-        gpu.gemv(t, x, M, a, flags=rf.GEMV_ACCUMULATE)
-        noalloc(gpu, t, x, M, b, rf.GEMV_ACCUMULATE)
-        assert np.array_equal(bits(a.numpy()), bits(b.numpy())), (K, N, M)
+    with rf.Gpu(0) as g:
+        ws0 = g.workspace_bytes()
+        cases = []
+        for K, N, M in (first, second):
+            print(f"case noalloc {tname} K={K} N={N} M={M}", flush=True)
+            w = weights(rng, gtype, N, K)
+            t = g.tensor(gtype, K, N, w)
+            x = g.array(rng.standard_normal((M, K)).astype(np.float32))
+            base = rng.standard_normal((M, N)).astype(np.float32)
+            b = g.array(base)
+            noalloc(g, t, x, M, b, rf.GEMV_ACCUMULATE)
+            assert g.workspace_bytes() == ws0, "the no-alloc call grew the workspace"
+            cases.append((t, x, M, base, b))
+        for t, x, M, base, b in cases:
+            a = g.array(base)
+            g.gemv(t, x, M, a, flags=rf.GEMV_ACCUMULATE)
+            assert np.array_equal(bits(a.numpy()), bits(b.numpy())), (t.ne0, t.ne1, M)
+            for arr in (a, b, x, t):
+                arr.free()
