@@ -521,15 +521,15 @@ __global__ void attn_merge(const float *__restrict__ part, int n_head, int hd, i
 //   attn_qk   scores and per-64-position-tile maxima: a workgroup per (tile,
 //             kv head, up to QK_TPW tokens), the K tile and the queries in
 //             LDS, a lane per (query head, position);
-//   attn_av   one token: a workgroup per (kv head, AV_CH output chains): the
-//             head maxima, then e_j in blocks while one wave runs the softmax
-//             sums over the block before, then a_j, then the products a_j v_jd
-//             in blocks (V streamed from HBM a few blocks ahead) while the
-//             chain wave adds the block before;
-//   attn_sm + attn_avm   several tokens, or a context longer than attn_av's
+//   attn_hv   one token: a workgroup per (query head, HV_CH columns): the
+//             head's maximum, then e_j in blocks while one lane runs the
+//             softmax sum over the block before, then a_j, then the products
+//             a_j v_jd in blocks (V streamed from HBM a few blocks ahead)
+//             while the chain wave adds the block before;
+//   attn_sm + attn_avm   several tokens, or a context longer than attn_hv's
 //             LDS holds: the softmax per (head, token), a_j written over the
 //             scores, then the value chains of MT tokens per workgroup fed by
-//             the same block pipeline as attn_av.
+//             the same block pipeline as attn_hv.
 
 #define SC_TILE 64
 #define QK_TPW 4            // tokens per scores workgroup (the K tile is read once for them)
@@ -650,25 +650,13 @@ __global__ __launch_bounds__(256) void attn_qk(const float *__restrict__ q, size
     }
 }
 
-// ---- one token: softmax and values in one workgroup per (kv head, AV_CH
-// output chains), 256 threads.  The chains are (query head g, column c) for
-// the G heads of the kv head and DC = AV_CH / G columns; wave 0 runs them
-// (lane g * DC + c), waves 1-3 produce its operands.
-//   1. head maxima from the tile maxima (all waves);
-//   2. blocks of AV_EB positions: waves 1-3 write e_j = expf(s_j - max) of
-//      block k to LDS while wave 0 (lane g) adds block k - 1 to head g's
-//      softmax sum; a barrier between blocks;
-//   3. 1 / sum;
-//   4. blocks of AV_VB quads: waves 1-3 multiply block b's V quads (loaded
-//      AV_VD blocks ahead, from the start of the kernel) by a_j = e_j * (1/sum)
-//      into one of two product buffers while wave 0 adds block b - 1's
-//      products to its chains; a barrier between blocks.
-// A chain lane reads its operands four at a time from LDS (chain_lds16).
+// Dependent add chains of the value and softmax sums.  AV_CH chains per
+// value workgroup of several tokens (attn_avm), AV_VD blocks of V in flight
+// per producer lane; a workgroup of the value kernels takes more than half
+// of a compute unit's LDS (AV_LDS_MIN), so that its chain wave has SIMD 0 to
+// itself.
 #define AV_CH 16
-#define AV_EB 384           // positions of an exp block (a (head, quad) pair per producer lane for each head)
-#define AV_VB 48            // quads (192 positions) of a value block
-#define AV_VD 4             // value blocks of V in flight per producer lane
-#define AV_PS (AV_VB + 1)   // quads per chain in a product buffer (one quad of padding)
+#define AV_VD 4
 #define AV_LDS_MIN (81 * 1024)
 
 // acc + x_0 + ... + x_{4n-1} over float4 p[0 .. n) of LDS, in order.
@@ -841,181 +829,191 @@ __device__ __forceinline__ float chain_quads(float acc, const float4 *p, int n)
 }
 
 
-template <int G>
-__global__ __launch_bounds__(256) void attn_av(const float *__restrict__ att, size_t att_stride,
+// ---- one token: softmax and values of one query head per workgroup, for
+// HV_CH of its columns (256 threads).  Wave 0 runs the chains: lane 0 the
+// softmax sum, then lanes 0 .. HV_CH - 1 the value sums of columns
+// c0 .. c0 + HV_CH - 1; waves 1-3 produce their operands.
+//   1. the head's maximum from its tile maxima (wave 0);
+//   2. exp blocks (HV_B0 positions, then HV_EB): waves 1-3 write e_j =
+//      expf(s_j - max) of block k to LDS while lane 0 of wave 0 adds block
+//      k - 1 to the sum; a barrier between blocks;
+//   3. 1 / sum;
+//   4. value blocks of HV_VB quads: waves 1-3 multiply block b's V quads
+//      (loaded HV_VD blocks ahead) by a_j = e_j * (1/sum) into one of two
+//      product buffers while wave 0 adds block b - 1's products to its
+//      chains; a barrier between blocks.
+// The exps of a head are computed by the hd / HV_CH workgroups of its column
+// groups only (each is a run of double-precision operations); the G query
+// heads that read the same V columns have the same blockIdx.x % 8, so that
+// they run on one XCD and V comes from its L2 once.
+#ifndef HV_CH
+#define HV_CH 16            // value chains (columns) per workgroup
+#endif
+#define HV_B0 192           // positions of the first exp block (one per producer lane)
+#define HV_EB 768           // positions of a later exp block (four per producer lane)
+#define HV_VB 96            // quads (384 positions) of a value block
+#define HV_PS (HV_VB + 1)   // quads per chain in a product buffer (one quad of padding)
+#define HV_VD 4             // value blocks of V in flight per producer lane
+#define HV_NP (HV_CH * HV_VB / 192)   // (column, quad) pairs per producer lane and block
+
+__global__ __launch_bounds__(256) void attn_hv(const float *__restrict__ att, size_t att_stride,
                                                const float *__restrict__ tmax, int n_tiles,
-                                               const float *__restrict__ vc, int n_head_kv,
-                                               int hd, const uint32_t *__restrict__ pos,
-                                               int n_ctx, float *__restrict__ out, int estr)
+                                               const float *__restrict__ vc, int n_head,
+                                               int n_head_kv, int hd,
+                                               const uint32_t *__restrict__ pos, int n_ctx,
+                                               float *__restrict__ out, int estr)
 {
-    constexpr int DC = AV_CH / G;                  // columns of the workgroup
-    constexpr int NPL = (DC * AV_VB + 191) / 192;  // (column, quad) pairs per producer lane
-    extern __shared__ float4 av_lds[];
-    float *e = (float *)av_lds;                    // [G][estr]: e_j, then a_j
-    float4 *prod = av_lds + G * estr / 4;          // [2][AV_CH][AV_PS]
-    __shared__ float mx_s[G], inv_s[G];
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    constexpr int QS = 192 / HV_CH;                // quad step of a producer lane's pairs
+    static_assert(192 % HV_CH == 0 && HV_NP * 192 == HV_CH * HV_VB && HV_VB % QS == 0,
+                  "producer lane L takes column L % HV_CH and quads L / HV_CH + QS k");
+    extern __shared__ float4 hv_lds[];
+    float *e = (float *)hv_lds;                    // [estr]: e_j
+    float4 *prod = hv_lds + estr / 4;              // [2][HV_CH][HV_PS]
+    __shared__ float mx_s, inv_s;
     __shared__ uint64_t tab[32];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
-    const int n_cg = hd / DC;
-    const int kvh = blockIdx.x / n_cg, c0 = (blockIdx.x - kvh * n_cg) * DC;
+    // workgroup -> (kv head, column group, query head of the group): u =
+    // kvh * ncg + cg keeps blockIdx.x % 8 for all G query heads
+    const int G = n_head / n_head_kv, ncg = (hd + HV_CH - 1) / HV_CH;
+    const int bx = blockIdx.x, rest = bx >> 3;
+    const int g = rest % G, u = (bx & 7) + 8 * (rest / G);
+    if (u >= n_head_kv * ncg) return;              // (uniform: the grid's padding)
+    const int kvh = u / ncg, c0 = (u - kvh * ncg) * HV_CH, h = kvh * G + g;
     const int kvd = n_head_kv * hd;
     const int upto = (int)min((size_t)pos[0] + 1, (size_t)n_ctx);
     const int nq = upto >> 2, rem = upto & 3, nq_all = (upto + 3) >> 2;
-    const float *srow = att + (size_t)kvh * G * att_stride;   // head g's scores at + g * att_stride
+    const float *srow = att + (size_t)h * att_stride;
     const bool producer = wave > 0;
     const int L = tid - 64;                        // producer lane 0 .. 191
 
-    // 1. head maxima (src/ops.c:26-30): wave w takes heads w, w + 4; their
-    // tile maxima (at most 256 tiles: 15360 positions) and first scores are
-    // requested before any other load, and reduced after the other loads
-    // are issued
-    constexpr int HW = (G + 3) / 4;                // heads per wave
-    const int used = (upto + SC_TILE - 1) / SC_TILE;
-    float tmv[HW][4], s0v[HW];
+    // the scores of the producer's positions of exp block k: block 0 is
+    // [0, HV_B0), block k >= 1 [HV_B0 + (k - 1) HV_EB, + HV_EB); lane L takes
+    // start + L + 192 i (one position in block 0, four later)
+    auto blk0 = [&](int k) { return k == 0 ? 0 : HV_B0 + (k - 1) * HV_EB; };
+    const int neb = upto <= HV_B0 ? 1 : 1 + (upto - HV_B0 + HV_EB - 1) / HV_EB;
+    const int neb2 = (neb + 1) & ~1;               // (barriers after block 0: an even number)
+    auto s_load = [&](int k, float *s) {
 #pragma unroll
-    for (int h = 0; h < HW; h++) {
-        const int g = min(wave + 4 * h, G - 1);
-        const float *tm = tmax + ((size_t)kvh * G + g) * n_tiles;
-#pragma unroll
-        for (int u = 0; u < 4; u++) tmv[h][u] = tm[min(lane + 64 * u, used - 1)];
-        s0v[h] = srow[(size_t)g * att_stride];
-    }
-
-    // V of the producer's pairs (column c, quad qq) of value blocks
-    // 0 .. AV_VD - 1, requested first: they are needed last, and arrive
-    // while the softmax runs
-    const float4 *v4 = (const float4 *)vc + (size_t)kvh * hd + c0;   // quad jq, column c: v4[jq * kvd + c]
-    const int nvb = (nq_all + AV_VB - 1) / AV_VB;
-    // (block b's V is in vb[b % AV_VD]; the block loop is unrolled by
-    // AV_VD, so that every index is known at compile time and each slot is
-    // reloaded in place: a load into a temporary moved into the slot would
-    // wait for the load at the move)
-    float4 vb[AV_VD][NPL];
-    auto v_load = [&](int b, float4 *dst) {
-#pragma unroll
-        for (int k = 0; k < NPL; k++) {
-            const int pi = min(L + 192 * k, DC * AV_VB - 1);
-            const int c = pi / AV_VB, jq = min(b * AV_VB + (pi - c * AV_VB), nq_all - 1);
-            dst[k] = v4[(size_t)jq * kvd + c];
-        }
+        for (int i = 0; i < 4; i++) s[i] = srow[min(blk0(k) + L + 192 * i, upto - 1)];
     };
-    if (producer) {
-#pragma unroll
-        for (int d = 0; d < AV_VD; d++) v_load(min(d, nvb - 1), vb[d]);
-    }
-    // the scores of the producer's (head, quad) pairs of exp block k: pair
-    // pi = L + 192 r is head pi / EQ, quad pi % EQ of the block
-    constexpr int EQ = AV_EB / 4;                  // quads of an exp block
-    constexpr int ER = (G * EQ + 191) / 192;       // pairs per producer lane
-    const int neb = (upto + AV_EB - 1) / AV_EB;
-    auto s_load = [&](int k, float4 *s) {
-#pragma unroll
-        for (int r = 0; r < ER; r++) {
-            const int pi = min(L + 192 * r, G * EQ - 1), g = pi / EQ;
-            const int j = min(k * AV_EB + 4 * (pi - g * EQ), (upto - 1) & ~3);
-            s[r] = *(const float4 *)(srow + (size_t)g * att_stride + j);
-        }
-    };
-    float4 sc[ER];
-    if (producer) s_load(0, sc);                   // (block 0's scores: with the maxima)
-#pragma unroll
-    for (int h = 0; h < HW; h++) {
-        const int g = wave + 4 * h;
-        if (g < G) {
-            float m = -INFINITY;
-#pragma unroll
-            for (int u = 0; u < 4; u++)
-                if (lane + 64 * u < used) m = tmv[h][u] > m ? tmv[h][u] : m;
-            m = wave_reduce(m, -INFINITY, [](float x, float y) { return y > x ? y : x; });
-            if (lane == 0) mx_s[g] = s0v[h] != s0v[h] ? s0v[h] : m;
-        }
-    }
+    float sc[4];
+    if (producer) s_load(0, sc);
 
+    // 1. the head's maximum (src/ops.c:26-30: a NaN first score stays)
+    if (wave == 0) {
+        const float *tm = tmax + (size_t)h * n_tiles;
+        const int used = (upto + SC_TILE - 1) / SC_TILE;
+        float m = -INFINITY;
+        for (int i = lane; i < used; i += 64) {
+            const float v = tm[i];
+            m = v > m ? v : m;
+        }
+        m = wave_reduce(m, -INFINITY, [](float x, float y) { return y > x ? y : x; });
+        const float s0 = srow[0];
+        if (lane == 0) mx_s = s0 != s0 ? s0 : m;
+    }
     if (tid < 32) tab[tid] = fox_exp2_tab[tid];
     __syncthreads();
 
-    // 2. exp blocks and the softmax sums (lane g of wave 0)
+    // V of value blocks 0 .. HV_VD - 1: producer lane L, pair k is column
+    // c0 + L % HV_CH, quad L / HV_CH + QS k of the block (a wave's loads of
+    // one k are runs of HV_CH consecutive quads).  Requested after exp blocks 0
+    // and 1's scores, so that those do not wait for them; block b's V is in
+    // vb[b % HV_VD], the block loop unrolled by HV_VD (every index known at
+    // compile time, each slot reloaded in place).
+    const f4v *v4 = (const f4v *)vc;
+    const int vcol = kvh * hd + min(c0 + L % HV_CH, hd - 1);
+    const int nvb = (nq_all + HV_VB - 1) / HV_VB;
+    f4v vb[HV_VD][HV_NP];
+    auto v_load = [&](int b, f4v *dst) {
+#pragma unroll
+        for (int k = 0; k < HV_NP; k++) {
+            const int jq = min(b * HV_VB + L / HV_CH + QS * k, nq_all - 1);
+            dst[k] = v4[(size_t)jq * kvd + vcol];
+        }
+    };
+
+    // 2. exp blocks and the softmax sum (lane 0 of wave 0)
     float sum = 0.0f;
-    // (the producers and wave 0 run separate loops with the same barriers,
-    // so that each loop body is straight-line code for the compiler's
-    // memory-wait bookkeeping)
     if (producer) {
-        for (int k = 0; k <= neb; k++) {
-            float4 cur[ER];
+        const float m = mx_s;
+        auto exps = [&](int k, const float *cur) {
+            const int j0 = blk0(k), ni = k == 0 ? 1 : 4;
 #pragma unroll
-            for (int r = 0; r < ER; r++) cur[r] = sc[r];
-            s_load(min(k + 1, neb - 1), sc);
-#pragma unroll
-            for (int r = 0; r < ER; r++) {
-                const int pi = L + 192 * r;
-                const int g = pi / EQ, j = k * AV_EB + 4 * (pi - g * EQ);
-                if (pi < G * EQ && k < neb && j < upto) {
-                    const float m = mx_s[g];
-                    float4 x;
-                    x.x = fox_expf_t(cur[r].x - m, tab);
-                    x.y = j + 1 < upto ? fox_expf_t(cur[r].y - m, tab) : 0.0f;
-                    x.z = j + 2 < upto ? fox_expf_t(cur[r].z - m, tab) : 0.0f;
-                    x.w = j + 3 < upto ? fox_expf_t(cur[r].w - m, tab) : 0.0f;
-                    *(float4 *)(e + g * estr + j) = x;
-                }
+            for (int i = 0; i < 4; i++) {
+                const int j = j0 + L + 192 * i;
+                if (i < ni && j < upto) e[j] = fox_expf_t(cur[i] - m, tab);
             }
+        };
+        // block 0 outside the loop: the V loads go out after block 1's
+        // scores.  Then two blocks per iteration, their scores in two sets
+        // of registers, each reloaded in place (a load into a temporary
+        // moved into place would wait for the load at the move).
+        float sb[4];
+        s_load(min(1, neb - 1), sb);
+#pragma unroll
+        for (int d = 0; d < HV_VD; d++) v_load(min(d, nvb - 1), vb[d]);
+        exps(0, sc);
+        __syncthreads();
+        for (int k = 1; k <= neb2; k += 2) {
+            s_load(min(k + 1, neb - 1), sc);
+            if (k < neb) exps(k, sb);
+            __syncthreads();
+            s_load(min(k + 2, neb - 1), sb);
+            if (k + 1 < neb) exps(k + 1, sc);
             __syncthreads();
         }
     } else {
-        for (int k = 0; k <= neb; k++) {
-            if (k > 0 && lane < G) {
-                // block k - 1, in position order
-                const int j0 = (k - 1) * AV_EB, j1 = min(upto, j0 + AV_EB);
-                const float *er = e + lane * estr;
+        __syncthreads();
+        for (int k = 1; k <= neb2; k++) {
+            if (lane == 0 && k <= neb) {
+                // block k - 1 in position order (its start is a multiple of 4)
+                const int j0 = blk0(k - 1), j1 = min(upto, blk0(k));
                 const int nqk = (j1 - j0) >> 2;
-                sum = chain_quads(sum, (const float4 *)(er + j0), nqk);
-                for (int j = j0 + 4 * nqk; j < j1; j++) sum = sum + er[j];
+                sum = chain_quads(sum, (const float4 *)(e + j0), nqk);
+                for (int j = j0 + 4 * nqk; j < j1; j++) sum = sum + e[j];
             }
             __syncthreads();
         }
     }
 
-    // 3. the scale of a_j = e_j * (1/sum), or 1 where the sum is not
-    // positive (src/ops.c:35-38; e * 1 is e exactly); the producers apply it
-    // as they form the products
-    if (wave == 0 && lane < G) inv_s[lane] = sum > 0.0f ? fox_div(1.0f, sum) : 1.0f;
+    // 3. a_j = e_j * (1/sum), or e_j where the sum is not positive
+    // (src/ops.c:35-38); the producers apply it as they form the products
+    if (wave == 0 && lane == 0) inv_s = sum > 0.0f ? fox_div(1.0f, sum) : 1.0f;
     __syncthreads();
-    float ivg[G];
-#pragma unroll
-    for (int g = 0; g < G; g++) ivg[g] = inv_s[g];
-    // 4. value blocks: products by waves 1-3, chains by wave 0
-    const int ch = lane;                           // wave 0: chain (g, c) = (ch / DC, ch % DC)
+    const float iv = inv_s;
+
+    // 4. value blocks: products by waves 1-3, chains by wave 0 (lane c:
+    // column c0 + c).  Indices are clamped, so steps past the last block
+    // recompute the last quads into the buffer the chains are not reading.
     float acc = 0.0f;
-    // the products of block b from V slot vs (then refilled with block
-    // b + AV_VD), without a branch (indices are clamped; past the last block
-    // it recomputes the last quad, into the buffer the chains are not
-    // reading), so that the V loads stay in flight across blocks
-    auto produce = [&](int b, float4 *vs) {
-        float4 *P = prod + (b & 1) * AV_CH * AV_PS;
+    // (all of a step's e quads are read before the first product is
+    // stored: a store to the product buffer may not be moved above a later
+    // read of e, so reads interleaved with stores would pay the LDS latency
+    // once per pair)
+    auto produce = [&](int b, f4v *vs) {
+        float4 *P = prod + (b & 1) * HV_CH * HV_PS + (L % HV_CH) * HV_PS;
+        float4 a[HV_NP];
 #pragma unroll
-        for (int k = 0; k < NPL; k++) {
-            const int pi = min(L + 192 * k, DC * AV_VB - 1);
-            const int c = pi / AV_VB, qq = pi - c * AV_VB;
-            const int jq = min(b * AV_VB + qq, nq_all - 1);
-            const float4 v = vs[k];
+        for (int k = 0; k < HV_NP; k++)
+            a[k] = ((const float4 *)e)[min(b * HV_VB + L / HV_CH + QS * k, nq_all - 1)];
 #pragma unroll
-            for (int g = 0; g < G; g++) {
-                float4 a = ((const float4 *)(e + g * estr))[jq];
-                a.x = a.x * ivg[g]; a.y = a.y * ivg[g]; a.z = a.z * ivg[g]; a.w = a.w * ivg[g];
-                float4 p;
-                p.x = a.x * v.x; p.y = a.y * v.y; p.z = a.z * v.z; p.w = a.w * v.w;
-                P[(g * DC + c) * AV_PS + qq] = p;
-            }
+        for (int k = 0; k < HV_NP; k++) {
+            const float4 ak = make_float4(a[k].x * iv, a[k].y * iv, a[k].z * iv, a[k].w * iv);
+            const f4v v = vs[k];
+            float4 p;
+            p.x = ak.x * v.x; p.y = ak.y * v.y; p.z = ak.z * v.z; p.w = ak.w * v.w;
+            P[L / HV_CH + QS * k] = p;
         }
-        v_load(min(b + AV_VD, nvb - 1), vs);
+        v_load(min(b + HV_VD, nvb - 1), vs);
     };
-    // the chains over block b - 1: whole quads of positions below upto,
-    // then the ragged quad's first rem products
+    // the chains over block b - 1: whole quads below upto, then the ragged
+    // quad's first rem products
     auto chains = [&](int b) {
-        if (b > 0 && b <= nvb && ch < AV_CH) {
-            const float4 *P = prod + ((b - 1) & 1) * AV_CH * AV_PS + ch * AV_PS;
-            const int q0 = (b - 1) * AV_VB;
-            const int nfull = min(AV_VB, nq - q0);
+        if (b > 0 && b <= nvb && lane < HV_CH) {
+            const float4 *P = prod + ((b - 1) & 1) * HV_CH * HV_PS + lane * HV_PS;
+            const int nfull = min(HV_VB, nq - (b - 1) * HV_VB);
             acc = chain_quads(acc, P, nfull);
             if (b == nvb && rem) {
                 const float4 v = P[nfull];
@@ -1025,10 +1023,9 @@ __global__ __launch_bounds__(256) void attn_av(const float *__restrict__ att, si
             }
         }
     };
-    static_assert(AV_VD == 4, "the block loop is unrolled by AV_VD");
-    // (separate loops with the same barriers; steps past nvb only recompute)
+    static_assert(HV_VD == 4, "the block loop is unrolled by HV_VD");
     if (producer) {
-        for (int b = 0; b <= nvb; b += AV_VD) {
+        for (int b = 0; b <= nvb; b += HV_VD) {
             produce(b, vb[0]);
             __syncthreads();
             produce(b + 1, vb[1]);
@@ -1039,21 +1036,18 @@ __global__ __launch_bounds__(256) void attn_av(const float *__restrict__ att, si
             __syncthreads();
         }
     } else {
-        for (int b = 0; b <= nvb; b += AV_VD) {
+        for (int b = 0; b <= nvb; b += HV_VD) {
 #pragma unroll
-            for (int d = 0; d < AV_VD; d++) {
+            for (int d = 0; d < HV_VD; d++) {
                 chains(b + d);
                 __syncthreads();
             }
         }
-    }
-    if (wave == 0 && ch < AV_CH) {
-        const int g = ch / DC, c = ch - g * DC;
-        out[(size_t)(kvh * G + g) * hd + c0 + c] = acc;
+        if (lane < HV_CH && c0 + lane < hd) out[(size_t)h * hd + c0 + lane] = acc;
     }
 }
 
-// ---- several tokens, or a context longer than attn_av's LDS holds: the
+// ---- several tokens, or a context longer than attn_hv's LDS holds: the
 // softmax and the values in two launches.
 //   attn_sm   a workgroup per (query head, token): the maximum, then e_j in
 //             blocks of SM_EB positions by waves 1-3 while lane 0 of wave 0
@@ -1211,17 +1205,31 @@ __global__ __launch_bounds__(256) void attn_avm(const float *__restrict__ att, s
     };
     // the products of block b from the staged quads: product pi = L + 192 k
     // is chain pi / MV_VB (token, head, column), quad pi % MV_VB
+    // (eight products' operands are read before the first of them is
+    // stored: a store to the product buffer may not be moved above a later
+    // read of the staging buffers, so reads interleaved with stores would
+    // pay the LDS latency once per product)
     auto products = [&](int b) __attribute__((always_inline)) {
         float4 *P = prod + (b & 1) * 64 * MV_PS;
+        static_assert(NP % 8 == 0, "products in groups of eight");
 #pragma unroll
-        for (int k = 0; k < NP; k++) {
-            const int pi = L + 192 * k, ch = pi / MV_VB, qq = pi - ch * MV_VB;
-            const int tl = ch / AV_CH, rm = ch - tl * AV_CH, g = rm / DC, c = rm - g * DC;
-            const f4v a = A[b & 1][(tl * G + g) * MV_VB + qq];
-            const f4v v = Vs[b & 1][c * MV_VB + qq];
-            float4 p;
-            p.x = a.x * v.x; p.y = a.y * v.y; p.z = a.z * v.z; p.w = a.w * v.w;
-            P[ch * MV_PS + qq] = p;
+        for (int k0 = 0; k0 < NP; k0 += 8) {
+            f4v a[8], v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int pi = L + 192 * (k0 + k), ch = pi / MV_VB, qq = pi - ch * MV_VB;
+                const int tl = ch / AV_CH, rm = ch - tl * AV_CH, g = rm / DC, c = rm - g * DC;
+                a[k] = A[b & 1][(tl * G + g) * MV_VB + qq];
+                v[k] = Vs[b & 1][c * MV_VB + qq];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int pi = L + 192 * (k0 + k), ch = pi / MV_VB, qq = pi - ch * MV_VB;
+                float4 p;
+                p.x = a[k].x * v[k].x; p.y = a[k].y * v[k].y;
+                p.z = a[k].z * v[k].z; p.w = a[k].w * v[k].w;
+                P[ch * MV_PS + qq] = p;
+            }
         }
     };
     // wave 0: chain lane = (token tl, head g, column c); its token's whole
@@ -1348,28 +1356,24 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
             if (e != hipSuccess) return fox_hip_fail(e, "attention scores");
             FOX_LAUNCHED("attention scores");
         }
-        // one token: softmax and values in one launch, when the G heads'
+        // one token: softmax and values in one launch, when the head's
         // weights fit in LDS beside the product buffers
-        const void *av = gqa == 1 ? (const void *)attn_av<1> : gqa == 2 ? (const void *)attn_av<2>
-                       : gqa == 4 ? (const void *)attn_av<4> : gqa == 8 ? (const void *)attn_av<8>
-                                  : nullptr;
-        const int estr = (int)(((n_ctx + 31) & ~(size_t)31) + 4);   // (heads in different banks)
+        const int estr = (int)((n_ctx + 31) & ~(size_t)31);
         // (at least AV_LDS_MIN: more than half of a compute unit's LDS, so
         // that no two workgroups share a compute unit, whose chain waves
         // would share SIMD 0's instruction issue)
-        size_t av_lds = gqa * (size_t)estr * 4 + 2 * AV_CH * AV_PS * 16;
-        if (av_lds < AV_LDS_MIN) av_lds = AV_LDS_MIN;
-        const size_t dc = av ? AV_CH / gqa : 1;
-        if (M == 1 && av && av_lds <= ATT_LDS_MAX && head_dim % dc == 0 && n_tiles <= 256) {
-            hipError_t e = hipFuncSetAttribute(av, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               (int)av_lds);
+        size_t hv_lds = (size_t)estr * 4 + 2 * HV_CH * HV_PS * 16;
+        if (hv_lds < AV_LDS_MIN) hv_lds = AV_LDS_MIN;
+        if (M == 1 && hv_lds <= ATT_LDS_MAX) {
+            hipError_t e = hipFuncSetAttribute((const void *)attn_hv,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)hv_lds);
             if (e != hipSuccess) return fox_hip_fail(e, "attention: LDS size");
-            void *args[] = {(void *)&att, (void *)&att_stride, (void *)&tmax, (void *)&n_tiles,
-                            (void *)&v_cache, (void *)&ikv, (void *)&ihd, (void *)&pos,
-                            (void *)&ictx, (void *)&out, (void *)&estr};
-            e = hipLaunchKernel(av, dim3((unsigned)(n_head_kv * (head_dim / dc))), dim3(256), args,
-                                av_lds, ctx->stream);
-            if (e != hipSuccess) return fox_hip_fail(e, "attention softmax+values");
+            const size_t ncg = (head_dim + HV_CH - 1) / HV_CH;
+            const size_t nwg = (n_head_kv * ncg + 7) / 8 * 8 * gqa;
+            hipLaunchKernelGGL(attn_hv, dim3((unsigned)nwg), dim3(256), hv_lds, ctx->stream, att,
+                               att_stride, tmax, n_tiles, v_cache, (int)n_head, ikv, ihd, pos,
+                               ictx, out, estr);
             FOX_LAUNCHED("attention softmax+values");
             return FOX_GPU_OK;
         }

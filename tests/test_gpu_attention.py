@@ -83,6 +83,9 @@ CASES = [  # n_head, n_kv, hd, n_ctx, pos, M
     (8, 8, 64, 1000, 190, 8),      # tokens ending on both sides of a value block (192 positions)
     (6, 6, 40, 120, 100, 2),       # hd 40: the last 16 columns of a head partly past its end
     (4, 2, 4, 32, 20, 3),          # hd 4 (the tiny fixture's heads): 8 columns per group
+    (6, 6, 40, 120, 100, 1),       # one token, hd 40: a head's last column group partly past its end
+    (4, 2, 4, 32, 20, 1),          # one token, hd 4
+    (12, 4, 64, 3000, 2500, 1),    # one token, gqa 3 past several exp blocks
     # one token past the fused kernel's LDS: the two-launch path
     (16, 2, 128, 16400, 16399, 1), # gqa 8, 257 score tiles
     (8, 8, 64, 20000, 19990, 1),   # gqa 1, 20000 positions
