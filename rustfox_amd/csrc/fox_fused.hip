@@ -33,8 +33,13 @@
 
 #define FW 8                    // waves per workgroup
 #define FWG (FW * 64)
-// weight blocks in flight per wave: one item's units (R4 blocks, 2 R4 for
-// gate/up pairs), at least 4 and at most 8
+// weight blocks in flight per wave, several tokens: one item's units (R4
+// blocks, 2 R4 for gate/up pairs), at least 4 and at most 8.  One token
+// keeps three (PF_ONE): the loads of every workgroup go out at once, so
+// fewer in flight per wave leave the input's loads less traffic to queue
+// behind (the 4B layer's four ternary GEMVs 26.3 -> 25.5 us, 14336 x 4096
+// 7.2 -> 6.8 us; two, four and six in flight were slower)
+#define PF_ONE 3
 __host__ __device__ constexpr int pf_of(int R4, int epi2)
 {
     return epi2 * R4 < 4 ? 4 : epi2 * R4 > 8 ? 8 : epi2 * R4;
@@ -1138,7 +1143,8 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     // ---- loads in the order they are used (they complete in order): the
     // input of token 0 (above), the first weight blocks, the epilogue's
     // operands
-    constexpr int PF = FMT == FMT_KQMIX ? 3 : KQ ? 4 : pf_of(R4, EPI == EPI_SILU ? 2 : 1);
+    constexpr int PF = FMT == FMT_KQMIX ? 3 : KQ ? 4 : MT ? pf_of(R4, EPI == EPI_SILU ? 2 : 1)
+                                                         : PF_ONE;
     // (every wave issues PF block loads, past its last unit re-reading that
     // one, so that the input's first use waits for the input only)
     RawBlk<FMT> raw[PF];
