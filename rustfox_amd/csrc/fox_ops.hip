@@ -538,10 +538,11 @@ __global__ void attn_merge(const float *__restrict__ part, int n_head, int hd, i
 
 // A workgroup of 256 threads per (64-position tile, kv head, QK_TPW tokens):
 // the tile's K rows (plain loads, row stride padded by one quad against bank
-// conflicts) and one token's G query heads in LDS; item i = (query head
-// i / 64, position i % 64), so the lanes of a wave share one query head (its
-// reads are broadcasts).  Positions at or past the token's end are neither
-// computed nor written.
+// conflicts) and the G query heads of QR tokens at a time in LDS, QR = 4 / G
+// for G <= 2 (so that every thread has an item), else 1; item i = (token
+// i / (64 G), query head (i / 64) % G, position i % 64), so the lanes of a
+// wave share one query (its reads are broadcasts).  Positions at or past a
+// token's end are neither computed nor written.
 template <int G>
 __global__ __launch_bounds__(256) void attn_qk(const float *__restrict__ q, size_t q_stride,
                                                const float *__restrict__ kc, int n_head_kv,
@@ -550,10 +551,12 @@ __global__ __launch_bounds__(256) void attn_qk(const float *__restrict__ q, size
                                                float *__restrict__ att, float *__restrict__ tmax,
                                                int n_tiles, int M)
 {
+    constexpr int QR = G == 1 ? 4 : G == 2 ? 2 : 1;  // tokens per round
+    constexpr int NQ = QR * G;                        // queries per round (<= 8)
     extern __shared__ float4 qk_lds[];
     const int hd4 = hd >> 2, ks = hd4 + 1;
     float4 *Ks = qk_lds;                           // [SC_TILE][ks]
-    float4 *Qs = qk_lds + SC_TILE * ks;           // [G][hd4]
+    float4 *Qs = qk_lds + SC_TILE * ks;           // [NQ][hd4]: query (token, head)
     const int tid = threadIdx.x, lane = tid & 63;
     const int tile = blockIdx.x, p0 = tile * SC_TILE, kvh = blockIdx.y;
     const int n_head = n_head_kv * G, kvd = n_head_kv * hd;
@@ -565,17 +568,18 @@ __global__ __launch_bounds__(256) void attn_qk(const float *__restrict__ q, size
     const int rows = min(SC_TILE, upto_last - p0);
     int t0 = tz;
     while (upto_of(t0) <= p0) t0++;                // (uniform) the first token reaching the tile
-    // the first token's queries (at most 512 quads: G <= 8, hd <= 256),
-    // requested with the K tile
-    auto q_row = [&](int t) {
-        return (const float4 *)(q + (size_t)t * q_stride + (size_t)kvh * G * hd);
+    // the queries of a round's tokens: quad f of the round is query f / hd4
+    // (token t + f / (G hd4), head (f / hd4) % G), dimension quad f % hd4; at
+    // most 512 quads (NQ <= 8, hd <= 256); tokens past t_end re-read the last
+    // one.  The first round's are requested with the K tile.
+    auto q_quad = [&](int t, int f) {
+        const int qi = f / hd4, tt = min(t + qi / G, t_end - 1);
+        return ((const float4 *)(q + (size_t)tt * q_stride + (size_t)kvh * G * hd))
+            [(qi % G) * hd4 + f % hd4];
     };
     float4 qr[2];
-    {
-        const float4 *qb = q_row(t0);
-        qr[0] = qb[min(tid, G * hd4 - 1)];
-        qr[1] = qb[min(tid + 256, G * hd4 - 1)];
-    }
+    qr[0] = q_quad(t0, min(tid, NQ * hd4 - 1));
+    qr[1] = q_quad(t0, min(tid + 256, NQ * hd4 - 1));
     // the K tile: float4 f of the tile is (row f / hd4, quad f % hd4); eight
     // loads in flight per thread before they go to LDS
     const float4 *kb = (const float4 *)(kc + (size_t)p0 * kvd + (size_t)kvh * hd);
@@ -594,26 +598,25 @@ __global__ __launch_bounds__(256) void attn_qk(const float *__restrict__ q, size
         }
     }
     const float scale = fox_div(1.0f, fox_sqrtf((float)hd));
-    for (int t = t0; t < t_end; t++) {
-        const int upto = upto_of(t);
+    for (int t = t0; t < t_end; t += QR) {
         if (t > t0) {
-            __syncthreads();                      // every item of the previous token is done
-            const float4 *qb = q_row(t);
-            qr[0] = qb[min(tid, G * hd4 - 1)];
-            qr[1] = qb[min(tid + 256, G * hd4 - 1)];
+            __syncthreads();                      // every item of the previous round is done
+            qr[0] = q_quad(t, min(tid, NQ * hd4 - 1));
+            qr[1] = q_quad(t, min(tid + 256, NQ * hd4 - 1));
         }
-        if (tid < G * hd4) Qs[tid] = qr[0];
-        if (tid + 256 < G * hd4) Qs[tid + 256] = qr[1];
+        if (tid < NQ * hd4) Qs[tid] = qr[0];
+        if (tid + 256 < NQ * hd4) Qs[tid + 256] = qr[1];
         __syncthreads();
 #pragma unroll
-        for (int it = 0; it < (G * SC_TILE + 255) / 256; it++) {
+        for (int it = 0; it < (NQ * SC_TILE + 255) / 256; it++) {
             const int item = it * 256 + tid;
-            if (G * SC_TILE % 256 != 0 && item >= G * SC_TILE) break;   // (wave-uniform)
-            const int g = item >> 6, pl = item & 63, p = p0 + pl;
-            const bool ok = p < upto;
+            if (NQ * SC_TILE % 256 != 0 && item >= NQ * SC_TILE) break;   // (wave-uniform)
+            const int qi = item >> 6, pl = item & 63, p = p0 + pl;
+            const int tt = t + qi / G, g = qi % G;
+            const bool ok = tt < t_end && p < upto_of(tt);
             float sc = -INFINITY;
             if (ok) {
-                const float4 *kr = Ks + pl * ks, *qr = Qs + g * hd4;
+                const float4 *kr = Ks + pl * ks, *qv4 = Qs + qi * hd4;
                 float acc = 0.0f;
                 int d = 0;
                 // eight quads' reads issued before their products are added
@@ -622,7 +625,7 @@ __global__ __launch_bounds__(256) void attn_qk(const float *__restrict__ q, size
 #pragma unroll
                     for (int u = 0; u < 8; u++) {
                         kv[u] = kr[d + u];
-                        qv[u] = qr[d + u];
+                        qv[u] = qv4[d + u];
                     }
 #pragma unroll
                     for (int u = 0; u < 8; u++) {
@@ -633,19 +636,21 @@ __global__ __launch_bounds__(256) void attn_qk(const float *__restrict__ q, size
                     }
                 }
                 for (; d < hd4; d++) {
-                    const float4 kv = kr[d], qv = qr[d];
+                    const float4 kv = kr[d], qv = qv4[d];
                     acc = acc + qv.x * kv.x;
                     acc = acc + qv.y * kv.y;
                     acc = acc + qv.z * kv.z;
                     acc = acc + qv.w * kv.w;
                 }
                 sc = acc * scale;
-                att[((size_t)t * n_head + (size_t)kvh * G + g) * att_stride + p] = sc;
+                att[((size_t)tt * n_head + (size_t)kvh * G + g) * att_stride + p] = sc;
             }
-            // the tile maximum, NaN never taken
+            // the tile maximum, NaN never taken (a wave is one query: its
+            // lanes' tokens are the same)
             const float m = wave_reduce((ok && sc == sc) ? sc : -INFINITY, -INFINITY,
                                         [](float x, float y) { return y > x ? y : x; });
-            if (lane == 0) tmax[((size_t)t * n_head + (size_t)kvh * G + g) * n_tiles + tile] = m;
+            if (lane == 0 && tt < t_end)
+                tmax[((size_t)tt * n_head + (size_t)kvh * G + g) * n_tiles + tile] = m;
         }
     }
 }
@@ -1336,7 +1341,8 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
         const int ikv = (int)n_head_kv, ihd = (int)head_dim, ictx = (int)n_ctx;
         {
             // scores: the K tile (a padding quad per row) and G query heads
-            const size_t lds = ((size_t)SC_TILE * (head_dim / 4 + 1) + gqa * head_dim / 4) * 16;
+            const size_t nq = gqa <= 2 ? 4 : gqa;          // (queries of a round: attn_qk's QR G)
+            const size_t lds = ((size_t)SC_TILE * (head_dim / 4 + 1) + nq * head_dim / 4) * 16;
             const void *qk = gqa == 1 ? (const void *)attn_qk<1> : gqa == 2 ? (const void *)attn_qk<2>
                            : gqa == 3 ? (const void *)attn_qk<3> : gqa == 4 ? (const void *)attn_qk<4>
                            : gqa == 5 ? (const void *)attn_qk<5> : gqa == 6 ? (const void *)attn_qk<6>
