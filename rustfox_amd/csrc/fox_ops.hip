@@ -543,7 +543,7 @@ __global__ void attn_merge(const float *__restrict__ part, int n_head, int hd, i
 // i / (64 G), query head (i / 64) % G, position i % 64), so the lanes of a
 // wave share one query (its reads are broadcasts).  Positions at or past a
 // token's end are neither computed nor written.
-template <int G>
+template <int G, int NCK>
 __global__ __launch_bounds__(256) void attn_qk(const float *__restrict__ q, size_t q_stride,
                                                const float *__restrict__ kc, int n_head_kv,
                                                int hd, const uint32_t *__restrict__ pos,
@@ -551,8 +551,13 @@ __global__ __launch_bounds__(256) void attn_qk(const float *__restrict__ q, size
                                                float *__restrict__ att, float *__restrict__ tmax,
                                                int n_tiles, int M)
 {
+    // NCK > 0: hd = 32 NCK, the K tile arrives in NCK chunks of 32
+    // dimensions (eight quads of every row) and the first round adds each
+    // chunk as soon as it is in LDS while the later chunks are still in
+    // flight; NCK = 0: any hd, the whole tile first
     constexpr int QR = G == 1 ? 4 : G == 2 ? 2 : 1;  // tokens per round
     constexpr int NQ = QR * G;                        // queries per round (<= 8)
+    constexpr int NIT = (NQ * SC_TILE + 255) / 256;   // items per thread
     extern __shared__ float4 qk_lds[];
     const int hd4 = hd >> 2, ks = hd4 + 1;
     float4 *Ks = qk_lds;                           // [SC_TILE][ks]
@@ -580,24 +585,67 @@ __global__ __launch_bounds__(256) void attn_qk(const float *__restrict__ q, size
     float4 qr[2];
     qr[0] = q_quad(t0, min(tid, NQ * hd4 - 1));
     qr[1] = q_quad(t0, min(tid + 256, NQ * hd4 - 1));
-    // the K tile: float4 f of the tile is (row f / hd4, quad f % hd4); eight
-    // loads in flight per thread before they go to LDS
     const float4 *kb = (const float4 *)(kc + (size_t)p0 * kvd + (size_t)kvh * hd);
-    const int nf = rows * hd4;
-    for (int f0 = 0; f0 < nf; f0 += 8 * 256) {
-        float4 r[8];
+    // NCK > 0: thread tid's quads of chunk c are idx = tid + 256 u: row
+    // idx / 8, quad 8 c + idx % 8 (a wave's load is eight 128-byte row pieces)
+    // (native 4-vectors: an array of float4 structs stays in scratch memory)
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    f4v kr[NCK > 0 ? NCK : 1][2];
+    if constexpr (NCK > 0) {
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int f = min(f0 + k * 256 + tid, nf - 1);
-            r[k] = kb[(size_t)(f / hd4) * (kvd / 4) + f % hd4];
-        }
+        for (int c = 0; c < NCK; c++)
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int f = f0 + k * 256 + tid;
-            if (f < nf) Ks[(f / hd4) * ks + f % hd4] = r[k];
+            for (int u = 0; u < 2; u++) {
+                const int idx = tid + 256 * u, row = min(idx >> 3, rows - 1);
+                kr[c][u] = ((const f4v *)kb)[(size_t)row * (kvd / 4) + 8 * c + (idx & 7)];
+            }
+    } else {
+        // the whole K tile: float4 f is (row f / hd4, quad f % hd4); eight
+        // loads in flight per thread before they go to LDS
+        const int nf = rows * hd4;
+        for (int f0 = 0; f0 < nf; f0 += 8 * 256) {
+            float4 r[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int f = min(f0 + k * 256 + tid, nf - 1);
+                r[k] = kb[(size_t)(f / hd4) * (kvd / 4) + f % hd4];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int f = f0 + k * 256 + tid;
+                if (f < nf) Ks[(f / hd4) * ks + f % hd4] = r[k];
+            }
         }
     }
     const float scale = fox_div(1.0f, fox_sqrtf((float)hd));
+    // the products of quads d0 .. d1 - 1 added to acc in dimension order,
+    // eight quads' reads issued before their adds
+    auto dots = [&](float acc, const float4 *kq, const float4 *qv4, int d0, int d1) {
+        int d = d0;
+        for (; d + 8 <= d1; d += 8) {
+            float4 kv[8], qv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                kv[u] = kq[d + u];
+                qv[u] = qv4[d + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                acc = acc + qv[u].x * kv[u].x;
+                acc = acc + qv[u].y * kv[u].y;
+                acc = acc + qv[u].z * kv[u].z;
+                acc = acc + qv[u].w * kv[u].w;
+            }
+        }
+        for (; d < d1; d++) {
+            const float4 kv = kq[d], qv = qv4[d];
+            acc = acc + qv.x * kv.x;
+            acc = acc + qv.y * kv.y;
+            acc = acc + qv.z * kv.z;
+            acc = acc + qv.w * kv.w;
+        }
+        return acc;
+    };
     for (int t = t0; t < t_end; t += QR) {
         if (t > t0) {
             __syncthreads();                      // every item of the previous round is done
@@ -606,45 +654,56 @@ __global__ __launch_bounds__(256) void attn_qk(const float *__restrict__ q, size
         }
         if (tid < NQ * hd4) Qs[tid] = qr[0];
         if (tid + 256 < NQ * hd4) Qs[tid + 256] = qr[1];
-        __syncthreads();
+        // item it of this thread: query qi = item / 64 (token tt, head g),
+        // position p
+        float acc[NIT];
 #pragma unroll
-        for (int it = 0; it < (NQ * SC_TILE + 255) / 256; it++) {
+        for (int it = 0; it < NIT; it++) acc[it] = 0.0f;
+        auto item_of = [&](int it, int &qi, int &pl, int &tt, bool &ok) {
             const int item = it * 256 + tid;
-            if (NQ * SC_TILE % 256 != 0 && item >= NQ * SC_TILE) break;   // (wave-uniform)
-            const int qi = item >> 6, pl = item & 63, p = p0 + pl;
-            const int tt = t + qi / G, g = qi % G;
-            const bool ok = tt < t_end && p < upto_of(tt);
-            float sc = -INFINITY;
-            if (ok) {
-                const float4 *kr = Ks + pl * ks, *qv4 = Qs + qi * hd4;
-                float acc = 0.0f;
-                int d = 0;
-                // eight quads' reads issued before their products are added
-                for (; d + 8 <= hd4; d += 8) {
-                    float4 kv[8], qv[8];
+            qi = item >> 6;
+            pl = item & 63;
+            tt = t + qi / G;
+            ok = item < NQ * SC_TILE && tt < t_end && p0 + pl < upto_of(tt);
+        };
+        if constexpr (NCK > 0) {
 #pragma unroll
-                    for (int u = 0; u < 8; u++) {
-                        kv[u] = kr[d + u];
-                        qv[u] = qv4[d + u];
-                    }
+            for (int c = 0; c < NCK; c++) {
+                if (t == t0) {
 #pragma unroll
-                    for (int u = 0; u < 8; u++) {
-                        acc = acc + qv[u].x * kv[u].x;
-                        acc = acc + qv[u].y * kv[u].y;
-                        acc = acc + qv[u].z * kv[u].z;
-                        acc = acc + qv[u].w * kv[u].w;
+                    for (int u = 0; u < 2; u++) {
+                        const int idx = tid + 256 * u;
+                        ((f4v *)Ks)[(idx >> 3) * ks + 8 * c + (idx & 7)] = kr[c][u];
                     }
                 }
-                for (; d < hd4; d++) {
-                    const float4 kv = kr[d], qv = qv4[d];
-                    acc = acc + qv.x * kv.x;
-                    acc = acc + qv.y * kv.y;
-                    acc = acc + qv.z * kv.z;
-                    acc = acc + qv.w * kv.w;
+                if (t == t0 || c == 0) __syncthreads();
+#pragma unroll
+                for (int it = 0; it < NIT; it++) {
+                    int qi, pl, tt;
+                    bool ok;
+                    item_of(it, qi, pl, tt, ok);
+                    if (ok) acc[it] = dots(acc[it], Ks + pl * ks, Qs + qi * hd4, 8 * c, 8 * c + 8);
                 }
-                sc = acc * scale;
-                att[((size_t)tt * n_head + (size_t)kvh * G + g) * att_stride + p] = sc;
             }
+        } else {
+            __syncthreads();
+#pragma unroll
+            for (int it = 0; it < NIT; it++) {
+                int qi, pl, tt;
+                bool ok;
+                item_of(it, qi, pl, tt, ok);
+                if (ok) acc[it] = dots(acc[it], Ks + pl * ks, Qs + qi * hd4, 0, hd4);
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < NIT; it++) {
+            int qi, pl, tt;
+            bool ok;
+            item_of(it, qi, pl, tt, ok);
+            if (it * 256 >= NQ * SC_TILE) break;  // (uniform: no items)
+            const int g = qi % G;
+            const float sc = acc[it] * scale;
+            if (ok) att[((size_t)tt * n_head + (size_t)kvh * G + g) * att_stride + p0 + pl] = sc;
             // the tile maximum, NaN never taken (a wave is one query: its
             // lanes' tokens are the same)
             const float m = wave_reduce((ok && sc == sc) ? sc : -INFINITY, -INFINITY,
@@ -1343,10 +1402,14 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
             // scores: the K tile (a padding quad per row) and G query heads
             const size_t nq = gqa <= 2 ? 4 : gqa;          // (queries of a round: attn_qk's QR G)
             const size_t lds = ((size_t)SC_TILE * (head_dim / 4 + 1) + nq * head_dim / 4) * 16;
-            const void *qk = gqa == 1 ? (const void *)attn_qk<1> : gqa == 2 ? (const void *)attn_qk<2>
-                           : gqa == 3 ? (const void *)attn_qk<3> : gqa == 4 ? (const void *)attn_qk<4>
-                           : gqa == 5 ? (const void *)attn_qk<5> : gqa == 6 ? (const void *)attn_qk<6>
-                           : gqa == 7 ? (const void *)attn_qk<7> : (const void *)attn_qk<8>;
+            // (head_dim 128: the K tile in four chunks, the first round's
+            // adds overlapping the later chunks' loads)
+            const bool ck = head_dim == 128;
+#define FOX_QK(g) (ck ? (const void *)attn_qk<g, 4> : (const void *)attn_qk<g, 0>)
+            const void *qk = gqa == 1 ? FOX_QK(1) : gqa == 2 ? FOX_QK(2) : gqa == 3 ? FOX_QK(3)
+                           : gqa == 4 ? FOX_QK(4) : gqa == 5 ? FOX_QK(5) : gqa == 6 ? FOX_QK(6)
+                           : gqa == 7 ? FOX_QK(7) : FOX_QK(8);
+#undef FOX_QK
             if (lds > 64 * 1024) {
                 hipError_t e = hipFuncSetAttribute(qk, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                    (int)lds);
