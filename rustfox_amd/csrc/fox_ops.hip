@@ -384,7 +384,6 @@ extern "C" fox_gpu_status fox_gpu_kv_write(fox_gpu_ctx *ctx, float *k_cache, flo
 
 // -------------------------------------------------------------- attention
 //
-#define ATT_SPLIT 32   // cache rows per workgroup
 #define ATT_MAXG 8     // query heads per kv head handled by one workgroup
 #define ATT_MAXHD 256
 
@@ -395,117 +394,201 @@ __device__ __forceinline__ float wave_sum_f(float v)
     return v;
 }
 
-// One workgroup per (split of ATT_SPLIT rows, kv head, token): scores of the
-// kv head's query heads against the split's keys, a local softmax (max m, sum
-// l of exp(s - m)) and the exp-weighted value sum o.  Splits past the token's
-// causal end write m = -inf, l = 0.
-__global__ __launch_bounds__(256) void attn_partial(const float *__restrict__ q, size_t q_stride,
-                                                    const float *__restrict__ kc,
-                                                    const float *__restrict__ vc, int n_head,
-                                                    int n_head_kv, int hd,
-                                                    const uint32_t *__restrict__ pos,
-                                                    int n_ctx, int n_splits,
-                                                    float *__restrict__ part)
+// ---- split mode (flash decoding): positions in splits of FD_SPLIT, each
+// split's softmax and value sum local to a workgroup, then a merge.  Sums run
+// in any order (float reassociation): results differ from the reference's in
+// their last bits.
+//   attn_fd   a workgroup per (split, kv head, token): the split's K rows, V
+//             quads and the G query heads in LDS (every thread's loads issued
+//             in one round before the first use; a wave's load is eight
+//             128-byte row pieces), scores as dot products with four partial
+//             sums, a wave per head for the split's maximum m, e = exp(s - m)
+//             and their sum l, then o = sum of e v per (head, column); writes
+//             the record (m, l, -, -, o) per (token, head, split);
+//   attn_fdm  a workgroup per (head, token), over the splits that hold the
+//             token's positions: the weights exp(m_s - M) once per split,
+//             then each column quad's weighted sum over the splits in eight
+//             split groups, divided by the weighted sum of the l_s.
+#define FD_SPLIT 32
+#define FD_MAXS 1024        // splits the merge holds (32768 positions)
+#define FD_LOADS 9          // 16-byte loads per thread: one round for G <= 8, head_dim <= 128
+
+template <int G>
+__global__ __launch_bounds__(256) void attn_fd(const float *__restrict__ q, size_t q_stride,
+                                               const float *__restrict__ kc,
+                                               const float *__restrict__ vc, int n_head_kv,
+                                               int hd, const uint32_t *__restrict__ pos,
+                                               int n_ctx, int n_splits, float *__restrict__ part)
 {
-    __shared__ float qs[ATT_MAXG * ATT_MAXHD];
-    __shared__ float sc[ATT_MAXG * ATT_SPLIT];
+    extern __shared__ float4 fd_lds[];
+    const int hd4 = hd >> 2, ks = hd4 + 1;
+    float4 *Ks = fd_lds;                           // [FD_SPLIT][ks]
+    float4 *Qs = Ks + FD_SPLIT * ks;               // [G][hd4]
+    float4 *Vs = Qs + G * hd4;                     // [FD_SPLIT / 4 quad rows][hd]
+    float *Ps = (float *)(Vs + (FD_SPLIT / 4) * hd);   // [G][FD_SPLIT]
+    __shared__ float st_m[G], st_l[G];
     const int s = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
-    const int gqa = n_head / n_head_kv, kvd = n_head_kv * hd;
-    // rows 0 .. upto-1 are visible; never past the cache
+    const int n_head = n_head_kv * G, kvd = n_head_kv * hd;
     const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
-    const int p0 = s * ATT_SPLIT;
-    const int pn = upto - p0 < ATT_SPLIT ? upto - p0 : ATT_SPLIT;
-    const size_t rec = 2 + (size_t)hd;
-    float *base = part + (((size_t)t * n_head + (size_t)kvh * gqa) * n_splits + s) * rec;
-
-    if (pn <= 0) {
-        for (int i = tid; i < gqa; i += 256) {
-            float *r = base + (size_t)i * n_splits * rec;
-            r[0] = -INFINITY;
-            r[1] = 0.0f;
-        }
-        return;
-    }
-    const float scale = fox_div(1.0f, fox_sqrtf((float)hd));
-    for (int i = tid; i < gqa * hd; i += 256)
-        qs[i] = q[(size_t)t * q_stride + (size_t)kvh * gqa * hd + i];
-    __syncthreads();
-    // scores: wave w takes rows w, w+4, ...; lanes split the head dimension
-    for (int pp = wave; pp < pn; pp += 4) {
-        const float *kr = kc + (size_t)(p0 + pp) * kvd + (size_t)kvh * hd;
-        float kv[ATT_MAXHD / 64];
+    const int p0 = s * FD_SPLIT, pn = min(FD_SPLIT, upto - p0);
+    if (pn <= 0) return;                           // (uniform) past the token's end: the merge
+                                                   // reads only the splits below it
+    const size_t rec = 4 + (size_t)hd;
+    float *base = part + (((size_t)t * n_head + (size_t)kvh * G) * n_splits + s) * rec;
+    // queries, K rows and V quads, all requested before the first is stored;
+    // a K "chunk" is eight quads of every row, a V chunk eight columns of
+    // every quad row (rows past pn re-read row pn - 1; quads past hd4 re-read
+    // the last one and are not stored)
+    const float4 *qb = (const float4 *)(q + (size_t)t * q_stride + (size_t)kvh * G * hd);
+    const float4 *kb = (const float4 *)(kc + (size_t)p0 * kvd + (size_t)kvh * hd);
+    const float4 *vb = (const float4 *)vc + (size_t)(p0 >> 2) * kvd + (size_t)kvh * hd;
+    const int nkq = FD_SPLIT * ((hd4 + 7) & ~7), nvq = (FD_SPLIT / 4) * ((hd + 7) & ~7);
+    const int rows_q = (pn + 3) >> 2;
+    // (native 4-vectors: an array of float4 structs stays in scratch memory)
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    for (int f0 = 0; f0 < nkq + nvq + G * hd4; f0 += FD_LOADS * 256) {
+        f4v r[FD_LOADS];
 #pragma unroll
-        for (int e = 0; e < ATT_MAXHD / 64; e++) {
-            int d = lane + 64 * e;
-            kv[e] = d < hd ? kr[d] : 0.0f;
-        }
-        for (int g = 0; g < gqa; g++) {
-            float a = 0.0f;
-#pragma unroll
-            for (int e = 0; e < ATT_MAXHD / 64; e++) {
-                int d = lane + 64 * e;
-                if (d < hd) a += qs[g * hd + d] * kv[e];
+        for (int k = 0; k < FD_LOADS; k++) {
+            const int f = f0 + k * 256 + tid;
+            if (f < nkq) {
+                const int row = (f >> 3) & (FD_SPLIT - 1), qd = 8 * (f / (8 * FD_SPLIT)) + (f & 7);
+                r[k] = ((const f4v *)kb)[(size_t)min(row, pn - 1) * (kvd / 4) + min(qd, hd4 - 1)];
+            } else if (f < nkq + nvq) {
+                const int g = f - nkq, row = (g >> 3) & (FD_SPLIT / 4 - 1);
+                const int col = 8 * (g / (2 * FD_SPLIT)) + (g & 7);
+                r[k] = ((const f4v *)vb)[(size_t)min(row, rows_q - 1) * kvd + min(col, hd - 1)];
+            } else {
+                r[k] = ((const f4v *)qb)[min(f - nkq - nvq, G * hd4 - 1)];
             }
-            a = wave_sum_f(a);
-            if (lane == 0) sc[g * ATT_SPLIT + pp] = a * scale;
+        }
+#pragma unroll
+        for (int k = 0; k < FD_LOADS; k++) {
+            const int f = f0 + k * 256 + tid;
+            if (f < nkq) {
+                const int row = (f >> 3) & (FD_SPLIT - 1), qd = 8 * (f / (8 * FD_SPLIT)) + (f & 7);
+                if (qd < hd4) ((f4v *)Ks)[row * ks + qd] = r[k];
+            } else if (f < nkq + nvq) {
+                const int g = f - nkq, row = (g >> 3) & (FD_SPLIT / 4 - 1);
+                const int col = 8 * (g / (2 * FD_SPLIT)) + (g & 7);
+                if (col < hd) ((f4v *)Vs)[row * hd + col] = r[k];
+            } else if (f < nkq + nvq + G * hd4) {
+                ((f4v *)Qs)[f - nkq - nvq] = r[k];
+            }
         }
     }
     __syncthreads();
-    // local softmax statistics per query head: wave w takes heads w, w+4
-    __shared__ float st_m[ATT_MAXG], st_l[ATT_MAXG];
-    for (int g = wave; g < gqa; g += 4) {
-        float v = lane < pn ? sc[g * ATT_SPLIT + lane] : -INFINITY;
-        float m = v;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-        float e = lane < pn ? fox_expf(v - m) : 0.0f;
-        if (lane < pn) sc[g * ATT_SPLIT + lane] = e;
-        float l = wave_sum_f(e);
+    // scores: item (head i / FD_SPLIT, position i % FD_SPLIT)
+    const float scale = fox_div(1.0f, fox_sqrtf((float)hd));
+    for (int i = tid; i < G * FD_SPLIT; i += 256) {
+        const int g = i / FD_SPLIT, pl = i % FD_SPLIT;
+        const float4 *kr = Ks + pl * ks, *qr = Qs + g * hd4;
+        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+        for (int d = 0; d < hd4; d++) {
+            const float4 kv = kr[d], qv = qr[d];
+            a0 += qv.x * kv.x;
+            a1 += qv.y * kv.y;
+            a2 += qv.z * kv.z;
+            a3 += qv.w * kv.w;
+        }
+        Ps[i] = pl < pn ? ((a0 + a1) + (a2 + a3)) * scale : -INFINITY;
+    }
+    __syncthreads();
+    // the split's softmax per head: wave w takes heads w, w + 4
+    for (int g = wave; g < G; g += 4) {
+        const float v = lane < FD_SPLIT ? Ps[g * FD_SPLIT + lane] : -INFINITY;
+        const float m = wave_reduce(v, -INFINITY, [](float x, float y) { return y > x ? y : x; });
+        const float e = lane < pn ? fox_expf(v - m) : 0.0f;
+        if (lane < FD_SPLIT) Ps[g * FD_SPLIT + lane] = e;
+        const float l = wave_sum_f(e);
         if (lane == 0) {
             st_m[g] = m;
             st_l[g] = l;
         }
     }
     __syncthreads();
-    // o = sum_p e_p v_p, one (head, dim) per thread
-    for (int i = tid; i < gqa * hd; i += 256) {
-        const int g = i / hd, d = i % hd;
-        const size_t c = (size_t)kvh * hd + d;
+    // o = sum of e v, item (head i / hd, column i % hd)
+    for (int i = tid; i < G * hd; i += 256) {
+        const int g = i / hd, c = i % hd;
+        const float4 *pe = (const float4 *)(Ps + g * FD_SPLIT);
         float o = 0.0f;
-        for (int pp = 0; pp < pn; pp++)
-            o += sc[g * ATT_SPLIT + pp] * vc[vq_index((size_t)(p0 + pp), c, (size_t)kvd)];
+        for (int rq = 0; rq < (pn >> 2); rq++) {
+            const float4 v = Vs[rq * hd + c], e = pe[rq];
+            o += ((e.x * v.x + e.y * v.y) + (e.z * v.z + e.w * v.w));
+        }
+        // the ragged last quad: only positions below pn (the cache rows past
+        // the token's end may hold anything, and 0 * inf is NaN)
+        if (pn & 3) {
+            const float4 v = Vs[(pn >> 2) * hd + c], e = pe[pn >> 2];
+            o += e.x * v.x;
+            if ((pn & 3) > 1) o += e.y * v.y;
+            if ((pn & 3) > 2) o += e.z * v.z;
+        }
         float *r = base + (size_t)g * n_splits * rec;
-        if (d == 0) {
+        if (c == 0) {
             r[0] = st_m[g];
             r[1] = st_l[g];
         }
-        r[2 + d] = o;
+        r[4 + c] = o;
     }
 }
 
-// Merge the splits of one (head, token): out = sum_s o_s e^{m_s - M} /
-// sum_s l_s e^{m_s - M}.
-__global__ void attn_merge(const float *__restrict__ part, int n_head, int hd, int n_splits,
-                           float *__restrict__ out, size_t out_stride)
+__global__ __launch_bounds__(256) void attn_fdm(const float *__restrict__ part,
+                                                const uint32_t *__restrict__ pos, int n_ctx,
+                                                int n_head, int hd, int n_splits,
+                                                float *__restrict__ out, size_t out_stride)
 {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    __shared__ float sw[FD_MAXS];
+    __shared__ float red[8];
+    __shared__ f4v acc[8][32];
     const int h = blockIdx.x, t = blockIdx.y;
-    const size_t rec = 2 + (size_t)hd;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
+    const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
+    const int nu = (upto + FD_SPLIT - 1) / FD_SPLIT;   // the splits attn_fd wrote
+    const size_t rec = 4 + (size_t)hd;
     const float *base = part + (((size_t)t * n_head + h) * n_splits) * rec;
     float mx = -INFINITY;
-    for (int s = 0; s < n_splits; s++) mx = fmaxf(mx, base[s * rec]);
+    for (int s = tid; s < nu; s += 256) mx = fmaxf(mx, base[(size_t)s * rec]);
+    mx = wave_reduce(mx, -INFINITY, [](float x, float y) { return fmaxf(x, y); });
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float L = 0.0f;
-    for (int s = 0; s < n_splits; s++) {
-        float m = base[s * rec];
-        if (m > -INFINITY) L += base[s * rec + 1] * fox_expf(m - mx);
+    for (int s = tid; s < nu; s += 256) {
+        const float m = base[(size_t)s * rec];
+        const float w = m > -INFINITY ? fox_expf(m - mx) : 0.0f;
+        sw[s] = w;
+        L += w * base[(size_t)s * rec + 1];
     }
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-        float o = 0.0f;
-        for (int s = 0; s < n_splits; s++) {
-            float m = base[s * rec];
-            if (m > -INFINITY) o += base[s * rec + 2 + d] * fox_expf(m - mx);
+    L = wave_sum_f(L);
+    if (lane == 0) red[4 + wave] = L;
+    __syncthreads();
+    L = (red[4] + red[5]) + (red[6] + red[7]);
+    // column quad cq of every pass, split group sg: splits sg, sg + 8, ...
+    const int sg = tid >> 5, cq = tid & 31, hd4 = hd >> 2;
+    for (int c0 = 0; c0 < hd4; c0 += 32) {
+        const int c4 = c0 + cq;
+        f4v o = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (c4 < hd4) {
+            const f4v *src = (const f4v *)(base + 4) + c4;
+#pragma unroll 4
+            for (int s = sg; s < nu; s += 8) o += sw[s] * src[(size_t)s * (rec >> 2)];
         }
-        out[(size_t)t * out_stride + (size_t)h * hd + d] = o / L;
+        acc[sg][cq] = o;
+        __syncthreads();
+        if (tid < 32 && c4 < hd4) {
+            f4v a = acc[0][cq];
+#pragma unroll
+            for (int k = 1; k < 8; k++) a += acc[k][cq];
+            float *dst = out + (size_t)t * out_stride + (size_t)h * hd + 4 * c4;
+            dst[0] = a.x / L;
+            dst[1] = a.y / L;
+            dst[2] = a.z / L;
+            dst[3] = a.w / L;
+        }
+        __syncthreads();
     }
 }
 
@@ -1481,17 +1564,34 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
         return FOX_GPU_OK;
     }
     if (mode != FOX_GPU_ATTN_SPLIT) return fox_fail(FOX_GPU_ERR_ARG, "attention: unknown mode %d", mode);
-    const int n_splits = (int)((n_ctx + ATT_SPLIT - 1) / ATT_SPLIT);
-    const size_t bytes = M * n_head * (size_t)n_splits * (2 + head_dim) * sizeof(float);
+    const int n_splits = (int)((n_ctx + FD_SPLIT - 1) / FD_SPLIT);
+    if (n_splits > FD_MAXS)
+        return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "attention: split mode takes at most %d positions",
+                        FD_MAXS * FD_SPLIT);
+    const size_t bytes = M * n_head * (size_t)n_splits * (4 + head_dim) * sizeof(float);
     fox_gpu_status st = fox_ws_reserve(ctx, bytes);
     if (st) return st;
     float *part = (float *)ctx->ws;
-    hipLaunchKernelGGL(attn_partial, dim3((unsigned)n_splits, (unsigned)n_head_kv, (unsigned)M),
-                       dim3(256), 0, ctx->stream, q, qs, k_cache, v_cache, (int)n_head,
-                       (int)n_head_kv, (int)head_dim, pos, (int)n_ctx, n_splits, part);
+    const size_t gqa = n_head / n_head_kv, hd4 = head_dim / 4;
+    const size_t lds = ((size_t)FD_SPLIT * (hd4 + 1) + gqa * hd4 + (FD_SPLIT / 4) * head_dim) * 16 +
+                       gqa * FD_SPLIT * 4;
+    const void *fd = gqa == 1 ? (const void *)attn_fd<1> : gqa == 2 ? (const void *)attn_fd<2>
+                   : gqa == 3 ? (const void *)attn_fd<3> : gqa == 4 ? (const void *)attn_fd<4>
+                   : gqa == 5 ? (const void *)attn_fd<5> : gqa == 6 ? (const void *)attn_fd<6>
+                   : gqa == 7 ? (const void *)attn_fd<7> : (const void *)attn_fd<8>;
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(fd, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return fox_hip_fail(e, "attention: LDS size");
+    }
+    const int ikv = (int)n_head_kv, ihd = (int)head_dim, ictx = (int)n_ctx;
+    void *args[] = {(void *)&q, (void *)&qs, (void *)&k_cache, (void *)&v_cache, (void *)&ikv,
+                    (void *)&ihd, (void *)&pos, (void *)&ictx, (void *)&n_splits, (void *)&part};
+    hipError_t e = hipLaunchKernel(fd, dim3((unsigned)n_splits, (unsigned)n_head_kv, (unsigned)M),
+                                   dim3(256), args, lds, ctx->stream);
+    if (e != hipSuccess) return fox_hip_fail(e, "attention partial");
     FOX_LAUNCHED("attention partial");
-    hipLaunchKernelGGL(attn_merge, dim3((unsigned)n_head, (unsigned)M), dim3(128), 0, ctx->stream,
-                       part, (int)n_head, (int)head_dim, n_splits, out, os);
+    hipLaunchKernelGGL(attn_fdm, dim3((unsigned)n_head, (unsigned)M), dim3(256), 0, ctx->stream,
+                       part, pos, ictx, (int)n_head, (int)head_dim, n_splits, out, os);
     FOX_LAUNCHED("attention merge");
     return FOX_GPU_OK;
 }
