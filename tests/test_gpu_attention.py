@@ -106,7 +106,12 @@ def test_attention_exact_is_bit_identical(gpu, oracle, case):
         f"max abs diff {np.abs(got - want).max()}"
 
 
-@pytest.mark.parametrize("case", CASES[:3], ids=lambda c: "h%d_kv%d_d%d_ctx%d_p%d_m%d" % c)
+# head_dim 256 (the largest taken) in split mode: two load rounds per workgroup,
+# two column-quad passes in the merge
+SPLIT_CASES = CASES + [(16, 2, 256, 700, 650, 2)]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: "h%d_kv%d_d%d_ctx%d_p%d_m%d" % c)
 def test_attention_split_within_rounding(gpu, oracle, case):
     n_head, n_kv, hd, n_ctx, pos, M = case
     rng = np.random.default_rng(7 + sum(case))
