@@ -398,6 +398,7 @@ __device__ __forceinline__ float wave_sum_f(float v)
 // split's softmax and value sum local to a workgroup, then a merge.  Sums run
 // in any order (float reassociation): results differ from the reference's in
 // their last bits.
+//   attn_fd128 (head_dim 128) and attn_fd (other head dims; described here)
 //   attn_fd   a workgroup per (split, kv head, token): the split's K rows, V
 //             quads and the G query heads in LDS (every thread's loads issued
 //             in one round before the first use; a wave's load is eight
@@ -406,11 +407,12 @@ __device__ __forceinline__ float wave_sum_f(float v)
 //             and their sum l, then o = sum of e v per (head, column); writes
 //             the record (m, l, -, -, o) per (token, head, split);
 //   attn_fdm  a workgroup per (head, token), over the splits that hold the
-//             token's positions: the weights exp(m_s - M) once per split,
-//             then each column quad's weighted sum over the splits in eight
-//             split groups, divided by the weighted sum of the l_s.
+//             token's positions: eight split groups, each thread loading its
+//             group's (m, l, column quad of o) for eight splits in one round
+//             and keeping a running maximum and rescaled sums; then the
+//             groups' sums weighted by exp(m_g - M), divided by their l sum.
 #define FD_SPLIT 32
-#define FD_MAXS 1024        // splits the merge holds (32768 positions)
+#define FD_MAXS 1024        // splits the merge holds (32768 positions, 65536 at head_dim 128)
 #define FD_LOADS 9          // 16-byte loads per thread: one round for G <= 8, head_dim <= 128
 
 template <int G>
@@ -499,9 +501,9 @@ __global__ __launch_bounds__(256) void attn_fd(const float *__restrict__ q, size
     for (int g = wave; g < G; g += 4) {
         const float v = lane < FD_SPLIT ? Ps[g * FD_SPLIT + lane] : -INFINITY;
         const float m = wave_reduce(v, -INFINITY, [](float x, float y) { return y > x ? y : x; });
-        const float e = lane < pn ? fox_expf(v - m) : 0.0f;
+        const float e = lane < pn ? __expf(v - m) : 0.0f;
         if (lane < FD_SPLIT) Ps[g * FD_SPLIT + lane] = e;
-        const float l = wave_sum_f(e);
+        const float l = wave_reduce(e, 0.0f, [](float x, float y) { return x + y; });
         if (lane == 0) {
             st_m[g] = m;
             st_l[g] = l;
@@ -534,59 +536,199 @@ __global__ __launch_bounds__(256) void attn_fd(const float *__restrict__ q, size
     }
 }
 
+// attn_fd for head_dim 128 in splits of FD_SPLIT_W positions, 512 threads,
+// K and V straight into registers: thread (position tid / 8, part tid % 8)
+// holds quads 4 part .. 4 part + 3 of its K row and forms the partial dots of
+// all G heads (fused multiply-adds), summed over the 8 parts by DPP; thread
+// (column tid / 4, quarter tid % 4) holds its column's 16 positions of V
+// (four quads), whose products with every head's weights are summed over
+// the quarters by DPP.  Only the queries, the scores and the weights pass
+// through LDS; a wave per head takes the split's softmax.
+#define FD_SPLIT_W 64
+template <int G>
+__global__ __launch_bounds__(512) void attn_fd128(const float *__restrict__ q, size_t q_stride,
+                                                  const float *__restrict__ kc,
+                                                  const float *__restrict__ vc, int n_head_kv,
+                                                  const uint32_t *__restrict__ pos, int n_ctx,
+                                                  int n_splits, float *__restrict__ part)
+{
+    constexpr int HD = 128, HD4 = 32, SP = FD_SPLIT_W;
+    static_assert(SP == 64 && G <= 8, "a position per 8 threads, a wave per head");
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    __shared__ f4v Qs[G * HD4];
+    __shared__ __attribute__((aligned(16))) float Ps[G][SP];   // (read as 4-vectors)
+    __shared__ float st_m[G], st_l[G];
+    const int s = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
+    const int n_head = n_head_kv * G, kvd = n_head_kv * HD;
+    const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
+    const int p0 = s * SP, pn = min(SP, upto - p0);
+    if (pn <= 0) return;                           // (uniform) past the token's end
+    // loads: K row piece, V column quads, then (G * 32 threads) a query quad
+    // (rows past pn re-read row pn - 1, quad rows past the last re-read it)
+    const int pk = tid >> 3, dp = tid & 7;
+    const f4v *kr = (const f4v *)(kc + (size_t)(p0 + min(pk, pn - 1)) * kvd + (size_t)kvh * HD) +
+                    4 * dp;
+    const int c = tid >> 2, hq = tid & 3, rows_q = (pn + 3) >> 2;
+    const f4v *vr = (const f4v *)vc + (size_t)(p0 >> 2) * kvd + (size_t)kvh * HD + c;
+    f4v kq[4], vq[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) kq[k] = kr[k];
+#pragma unroll
+    for (int k = 0; k < 4; k++) vq[k] = vr[(size_t)min(4 * hq + k, rows_q - 1) * kvd];
+    if (tid < G * HD4)
+        Qs[tid] = ((const f4v *)(q + (size_t)t * q_stride + (size_t)kvh * G * HD))[tid];
+    __syncthreads();
+    // scores: the G partial dots of this part, then the sums over the parts
+    float sc[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const f4v qq = Qs[g * HD4 + 4 * dp + k];
+            a0 = __builtin_fmaf(qq.x, kq[k].x, a0);
+            a1 = __builtin_fmaf(qq.y, kq[k].y, a1);
+            a2 = __builtin_fmaf(qq.z, kq[k].z, a2);
+            a3 = __builtin_fmaf(qq.w, kq[k].w, a3);
+        }
+        sc[g] = (a0 + a1) + (a2 + a3);
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++) sc[g] += dpp_t<0xB1, 0xF>(0.0f, sc[g]);
+#pragma unroll
+    for (int g = 0; g < G; g++) sc[g] += dpp_t<0x4E, 0xF>(0.0f, sc[g]);
+#pragma unroll
+    for (int g = 0; g < G; g++) sc[g] += dpp_t<0x141, 0xF>(0.0f, sc[g]);
+    const float scale = fox_div(1.0f, fox_sqrtf((float)HD));
+#pragma unroll
+    for (int g = 0; g < G; g++)
+        if (dp == g) Ps[g][pk] = pk < pn ? sc[g] * scale : -INFINITY;
+    __syncthreads();
+    // the split's softmax: wave g takes head g
+    if (wave < G) {
+        const float v = Ps[wave][lane];
+        const float m = wave_reduce(v, -INFINITY, [](float x, float y) { return y > x ? y : x; });
+        const float e = lane < pn ? __expf(v - m) : 0.0f;
+        Ps[wave][lane] = e;
+        const float l = wave_reduce(e, 0.0f, [](float x, float y) { return x + y; });
+        if (lane == 0) {
+            st_m[wave] = m;
+            st_l[wave] = l;
+        }
+    }
+    __syncthreads();
+    // values: the V components past pn are zeroed (cache rows past the
+    // token's end may hold anything, and 0 * inf is NaN)
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int pb = 16 * hq + 4 * k;
+        vq[k].x = pb < pn ? vq[k].x : 0.0f;
+        vq[k].y = pb + 1 < pn ? vq[k].y : 0.0f;
+        vq[k].z = pb + 2 < pn ? vq[k].z : 0.0f;
+        vq[k].w = pb + 3 < pn ? vq[k].w : 0.0f;
+    }
+    float o[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const f4v *pe = (const f4v *)&Ps[g][16 * hq];
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const f4v e = pe[k];
+            a0 = __builtin_fmaf(e.x, vq[k].x, a0);
+            a1 = __builtin_fmaf(e.y, vq[k].y, a1);
+            a0 = __builtin_fmaf(e.z, vq[k].z, a0);
+            a1 = __builtin_fmaf(e.w, vq[k].w, a1);
+        }
+        o[g] = a0 + a1;
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++) o[g] += dpp_t<0xB1, 0xF>(0.0f, o[g]);
+#pragma unroll
+    for (int g = 0; g < G; g++) o[g] += dpp_t<0x4E, 0xF>(0.0f, o[g]);
+    const size_t rec = 4 + (size_t)HD;
+    float *base = part + (((size_t)t * n_head + (size_t)kvh * G) * n_splits + s) * rec;
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        float *r = base + (size_t)g * n_splits * rec;
+        if (hq == 0) r[4 + c] = o[g];
+        if (tid == 0) {
+            r[0] = st_m[g];
+            r[1] = st_l[g];
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void attn_fdm(const float *__restrict__ part,
                                                 const uint32_t *__restrict__ pos, int n_ctx,
-                                                int n_head, int hd, int n_splits,
+                                                int n_head, int hd, int split, int n_splits,
                                                 float *__restrict__ out, size_t out_stride)
 {
     typedef float f4v __attribute__((ext_vector_type(4)));
-    __shared__ float sw[FD_MAXS];
-    __shared__ float red[8];
-    __shared__ f4v acc[8][32];
-    const int h = blockIdx.x, t = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
+    constexpr int R = 8;                       // splits a thread loads in one round
+    __shared__ float gm[8], gl[8];
+    __shared__ f4v go[8][32];
+    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
     const int upto = (int)min((size_t)pos[0] + (size_t)t + 1, (size_t)n_ctx);
-    const int nu = (upto + FD_SPLIT - 1) / FD_SPLIT;   // the splits attn_fd wrote
+    const int nu = (upto + split - 1) / split;     // the splits attn_fd wrote
     const size_t rec = 4 + (size_t)hd;
     const float *base = part + (((size_t)t * n_head + h) * n_splits) * rec;
-    float mx = -INFINITY;
-    for (int s = tid; s < nu; s += 256) mx = fmaxf(mx, base[(size_t)s * rec]);
-    mx = wave_reduce(mx, -INFINITY, [](float x, float y) { return fmaxf(x, y); });
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float L = 0.0f;
-    for (int s = tid; s < nu; s += 256) {
-        const float m = base[(size_t)s * rec];
-        const float w = m > -INFINITY ? fox_expf(m - mx) : 0.0f;
-        sw[s] = w;
-        L += w * base[(size_t)s * rec + 1];
-    }
-    L = wave_sum_f(L);
-    if (lane == 0) red[4 + wave] = L;
-    __syncthreads();
-    L = (red[4] + red[5]) + (red[6] + red[7]);
-    // column quad cq of every pass, split group sg: splits sg, sg + 8, ...
+    // split group sg takes splits sg, sg + 8, ... (a running maximum, the
+    // sums rescaled when it grows), column quad c0 + cq
     const int sg = tid >> 5, cq = tid & 31, hd4 = hd >> 2;
     for (int c0 = 0; c0 < hd4; c0 += 32) {
-        const int c4 = c0 + cq;
+        const int c4 = min(c0 + cq, hd4 - 1);          // (past the end: re-read, not stored)
+        float m = -INFINITY, l = 0.0f;
         f4v o = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (c4 < hd4) {
-            const f4v *src = (const f4v *)(base + 4) + c4;
-#pragma unroll 4
-            for (int s = sg; s < nu; s += 8) o += sw[s] * src[(size_t)s * (rec >> 2)];
-        }
-        acc[sg][cq] = o;
-        __syncthreads();
-        if (tid < 32 && c4 < hd4) {
-            f4v a = acc[0][cq];
+        for (int s0 = sg; s0 < nu; s0 += 8 * R) {
+            float ms[R], ls[R];
+            f4v os[R];
 #pragma unroll
-            for (int k = 1; k < 8; k++) a += acc[k][cq];
-            float *dst = out + (size_t)t * out_stride + (size_t)h * hd + 4 * c4;
-            dst[0] = a.x / L;
-            dst[1] = a.y / L;
-            dst[2] = a.z / L;
-            dst[3] = a.w / L;
+            for (int k = 0; k < R; k++) {
+                const float *r = base + (size_t)min(s0 + 8 * k, nu - 1) * rec;
+                ms[k] = r[0];
+                ls[k] = r[1];
+                os[k] = *(const f4v *)(r + 4 + 4 * c4);
+            }
+            float mn = m;
+#pragma unroll
+            for (int k = 0; k < R; k++)
+                if (s0 + 8 * k < nu) mn = fmaxf(mn, ms[k]);
+            const float sc = m > -INFINITY ? __expf(m - mn) : 0.0f;
+            l *= sc;
+            o *= sc;
+#pragma unroll
+            for (int k = 0; k < R; k++) {
+                const float w = s0 + 8 * k < nu && ms[k] > -INFINITY ? __expf(ms[k] - mn) : 0.0f;
+                l += w * ls[k];
+                o += w * os[k];
+            }
+            m = mn;
+        }
+        if (cq == 0) {
+            gm[sg] = m;
+            gl[sg] = l;
+        }
+        go[sg][cq] = o;
+        __syncthreads();
+        if (tid < 32 && c0 + cq < hd4) {
+            float M = gm[0];
+#pragma unroll
+            for (int g = 1; g < 8; g++) M = fmaxf(M, gm[g]);
+            float L = 0.0f;
+            f4v O = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                const float w = gm[g] > -INFINITY ? __expf(gm[g] - M) : 0.0f;
+                L += w * gl[g];
+                O += w * go[g][cq];
+            }
+            float *dst = out + (size_t)t * out_stride + (size_t)h * hd + 4 * (c0 + cq);
+            dst[0] = O.x / L;
+            dst[1] = O.y / L;
+            dst[2] = O.z / L;
+            dst[3] = O.w / L;
         }
         __syncthreads();
     }
@@ -1564,10 +1706,11 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
         return FOX_GPU_OK;
     }
     if (mode != FOX_GPU_ATTN_SPLIT) return fox_fail(FOX_GPU_ERR_ARG, "attention: unknown mode %d", mode);
-    const int n_splits = (int)((n_ctx + FD_SPLIT - 1) / FD_SPLIT);
+    const int split = head_dim == 128 ? FD_SPLIT_W : FD_SPLIT;
+    const int n_splits = (int)((n_ctx + split - 1) / split);
     if (n_splits > FD_MAXS)
         return fox_fail(FOX_GPU_ERR_UNSUPPORTED, "attention: split mode takes at most %d positions",
-                        FD_MAXS * FD_SPLIT);
+                        FD_MAXS * split);
     const size_t bytes = M * n_head * (size_t)n_splits * (4 + head_dim) * sizeof(float);
     fox_gpu_status st = fox_ws_reserve(ctx, bytes);
     if (st) return st;
@@ -1579,19 +1722,31 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
                    : gqa == 3 ? (const void *)attn_fd<3> : gqa == 4 ? (const void *)attn_fd<4>
                    : gqa == 5 ? (const void *)attn_fd<5> : gqa == 6 ? (const void *)attn_fd<6>
                    : gqa == 7 ? (const void *)attn_fd<7> : (const void *)attn_fd<8>;
-    if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute(fd, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return fox_hip_fail(e, "attention: LDS size");
-    }
     const int ikv = (int)n_head_kv, ihd = (int)head_dim, ictx = (int)n_ctx;
-    void *args[] = {(void *)&q, (void *)&qs, (void *)&k_cache, (void *)&v_cache, (void *)&ikv,
-                    (void *)&ihd, (void *)&pos, (void *)&ictx, (void *)&n_splits, (void *)&part};
-    hipError_t e = hipLaunchKernel(fd, dim3((unsigned)n_splits, (unsigned)n_head_kv, (unsigned)M),
-                                   dim3(256), args, lds, ctx->stream);
+    hipError_t e;
+    if (head_dim == 128) {
+        const void *f1 = gqa == 1 ? (const void *)attn_fd128<1> : gqa == 2 ? (const void *)attn_fd128<2>
+                       : gqa == 3 ? (const void *)attn_fd128<3> : gqa == 4 ? (const void *)attn_fd128<4>
+                       : gqa == 5 ? (const void *)attn_fd128<5> : gqa == 6 ? (const void *)attn_fd128<6>
+                       : gqa == 7 ? (const void *)attn_fd128<7> : (const void *)attn_fd128<8>;
+        void *args[] = {(void *)&q, (void *)&qs, (void *)&k_cache, (void *)&v_cache, (void *)&ikv,
+                        (void *)&pos, (void *)&ictx, (void *)&n_splits, (void *)&part};
+        e = hipLaunchKernel(f1, dim3((unsigned)n_splits, (unsigned)n_head_kv, (unsigned)M),
+                            dim3(512), args, 0, ctx->stream);
+    } else {
+        if (lds > 64 * 1024) {
+            e = hipFuncSetAttribute(fd, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return fox_hip_fail(e, "attention: LDS size");
+        }
+        void *args[] = {(void *)&q, (void *)&qs, (void *)&k_cache, (void *)&v_cache, (void *)&ikv,
+                        (void *)&ihd, (void *)&pos, (void *)&ictx, (void *)&n_splits, (void *)&part};
+        e = hipLaunchKernel(fd, dim3((unsigned)n_splits, (unsigned)n_head_kv, (unsigned)M),
+                            dim3(256), args, lds, ctx->stream);
+    }
     if (e != hipSuccess) return fox_hip_fail(e, "attention partial");
     FOX_LAUNCHED("attention partial");
     hipLaunchKernelGGL(attn_fdm, dim3((unsigned)n_head, (unsigned)M), dim3(256), 0, ctx->stream,
-                       part, pos, ictx, (int)n_head, (int)head_dim, n_splits, out, os);
+                       part, pos, ictx, (int)n_head, (int)head_dim, split, n_splits, out, os);
     FOX_LAUNCHED("attention merge");
     return FOX_GPU_OK;
 }
