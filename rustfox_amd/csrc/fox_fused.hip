@@ -55,7 +55,9 @@ __host__ __device__ constexpr int fused_lds_max(size_t M)
     return (M > 2 ? 160 * 1024 : 96 * 1024) - FUSED_STATIC_LDS;
 }
 
-enum { IN_Q = 0, IN_F32 = 1, IN_NORM = 2 };
+// IN_B: the B operand, block corrections and token scales prepared by
+// fused_prep (several tokens, f32 or RMS-normed input), copied into LDS
+enum { IN_Q = 0, IN_F32 = 1, IN_NORM = 2, IN_B = 3 };
 enum { EPI_STORE = 0, EPI_ROPE = 1, EPI_SILU = 2, EPI_SUMS = 3 };
 
 struct FusedArgs {
@@ -1073,10 +1075,25 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     // nothing ahead of its loads but the argument reads they need
     using InT = std::conditional_t<MT && !KQ, InGrp<R4, TG>, InRegs<R4>>;
     InT in;
-    if constexpr (MT && !KQ)
+    // IN_B: the prepared operand into registers ahead of the weight loads
+    // (loads complete in order); its nb M 16 + nb M / 4 words are at most
+    // 2 R4 + 1 per thread (nb <= 8 R4, M <= 8)
+    // (native 4-vectors: an array of uint4 structs stays in scratch memory)
+    typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+    constexpr int NWB = IN == IN_B ? 2 * R4 + 1 : 1;
+    u4v opw[NWB];
+    float opsc = 0.0f;
+    const int nwb = (L.terms - L.B) >> 4;
+    if constexpr (IN == IN_B) {
+        const u4v *src = (const u4v *)q_in;
+#pragma unroll
+        for (int k = 0; k < NWB; k++) opw[k] = src[min(tid + k * FWG, nwb - 1)];
+        opsc = a.scale_in[min(tid, M - 1)];
+    } else if constexpr (MT && !KQ) {
         load_group<IN, R4, TG>(x_in, norm_in, q_in, a.x_stride, 0, min(M, TG), K, true, in);
-    else
+    } else {
         load_input<IN, R4>(x_in, norm_in, q_in, a.x_stride, 0, K, in);
+    }
     const int ntl = a.n_per + (bx < a.n_rem);              // items of this workgroup (>= 1)
     const int ts1 = a.tile_start[1], ts2 = a.tile_start[2], ts3 = a.tile_start[3];
     // (integer arithmetic only: comparisons turned into 0/1 values and
@@ -1208,7 +1225,15 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
 
     // ---- input stage: int8 activations straight into the B operand in LDS
     // (token 0 outside the loop: its waits then count the loads above)
-    if constexpr (KQ) {
+    if constexpr (IN == IN_B) {
+        // fused_prep's output has the LDS carve-up of B and the corrections
+        // (one run of 16-byte words), then the token scales
+        u4v *dst = (u4v *)(lds + L.B);
+#pragma unroll
+        for (int k = 0; k < NWB; k++)
+            if (tid + k * FWG < nwb) dst[tid + k * FWG] = opw[k];
+        if (tid < M) ascale[tid] = opsc;
+    } else if constexpr (KQ) {
         quantise_kq<FMT, IN, R4>(a, K, (int8_t *)B, aux, bsc, dred, in);
     } else if constexpr (MT == 2) {
         // the groups in turn (the first in flight since the start; a later
@@ -1411,6 +1436,27 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     }
 }
 
+// Several tokens (f32 or RMS-normed input): the input stage once per launch
+// instead of once per GEMV workgroup.  Workgroup t takes token t through
+// quantise_to_b (RMSNorm, per-vector int8 quantisation of src/gemv.c:11-42,
+// B operand and per-block corrections, the operations and order of the
+// one-token kernels) into global memory laid out as the GEMV's LDS carve-up
+// for all the tokens (B at 0, corrections at `aux`), and writes its
+// activation scale; the GEMV copies the operand into LDS (IN_B).
+template <int IN, int R4>
+__global__ __launch_bounds__(FWG) void fused_prep(const float *x_in, const float *norm_in,
+                                                  int nb_in, FusedArgs a, uint8_t *B,
+                                                  int32_t *aux, float *scale)
+{
+    __shared__ double dred[FW];
+    __shared__ uint32_t ured[FW];
+    const int t = blockIdx.x, K = nb_in * 256;
+    InRegs<R4> in;
+    load_input<IN, R4>(x_in, norm_in, nullptr, a.x_stride, t, K, in);
+    const float s = quantise_to_b<FMT_TQ2, IN, R4>(a, t, K, B, aux, dred, ured, in);
+    if (threadIdx.x == 0) scale[t] = s;
+}
+
 // ------------------------------------------------------------ host
 
 // Workgroups write output rows while others still read the input, so an
@@ -1466,7 +1512,7 @@ static fox_gpu_status fused_check(int type, size_t K, size_t M, int nslab, int *
 // VALU work twice; 14336 x 4096 at 8 tokens: 16.3 -> 13.9 us, at 4 tokens
 // 11.4 -> 10.7 us, at 2 tokens 8.9 -> 9.2 us)
 template <int FMT, int IN, int EPI, int R4>
-static fox_gpu_status fused_go_r(fox_gpu_ctx *ctx, FusedArgs a, int n_work)
+static fox_gpu_status fused_go_r(fox_gpu_ctx *ctx, FusedArgs a, int n_work, uint8_t *fixed)
 {
     // (the K-quants have the one-token kernels only: fused_check)
     constexpr bool MT_OK = FMT == FMT_TQ2;
@@ -1477,19 +1523,55 @@ static fox_gpu_status fused_go_r(fox_gpu_ctx *ctx, FusedArgs a, int n_work)
     const int grid = n_work < cap ? n_work : cap;
     a.n_per = n_work / grid;
     a.n_rem = n_work - a.n_per * grid;
-    const size_t lds = fused_lds(FMT, a.nb * 256, a.M, EPI == EPI_SILU ? 2 : 1).total;
-    // (the multi-token kernels exist for the ternary formats only)
+    const FusedLds L = fused_lds(FMT, a.nb * 256, a.M, EPI == EPI_SILU ? 2 : 1);
+    const size_t lds = L.total;
+    // (the multi-token kernels exist for the ternary formats only; from
+    // three tokens on, f32 and normed input is prepared once by fused_prep
+    // and the GEMV reads it as IN_B)
     constexpr int MT1 = MT_OK ? 1 : 0, MT2 = MT_OK ? 2 : 0;
-    const void *k = mt == 2 ? (const void *)gemv_fused<FMT, IN, EPI, R4, MT2>
+    constexpr bool PREP = MT_OK && (IN == IN_F32 || IN == IN_NORM) && EPI != EPI_SUMS;
+    constexpr int IN2 = PREP ? IN_B : IN;
+    const void *k = mt == 2 ? (const void *)gemv_fused<FMT, IN2, EPI, R4, MT2>
                   : mt == 1 ? (const void *)gemv_fused<FMT, IN, EPI, R4, MT1>
                             : (const void *)gemv_fused<FMT, IN, EPI, R4, 0>;
     if (lds > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return fox_hip_fail(e, "fused gemv: LDS size");
     }
-    if (mt == 2)
-        hipLaunchKernelGGL((gemv_fused<FMT, IN, EPI, R4, MT2>), dim3((unsigned)grid), dim3(FWG),
-                           lds, ctx->stream, a.x, a.norm_w, a.q_in, a.nb, a);
+    if (mt == 2) {
+        if constexpr (PREP) {
+            // the operand (B and corrections, L.terms bytes) then the token
+            // scales, in the workspace or the caller's fixed scratch
+            const size_t opb = (size_t)(L.terms - L.B);
+            const size_t need = opb + FOX_GPU_MAX_TOKENS * sizeof(float);
+            if (opb > (size_t)(2 * R4 + 1) * FWG * 16)      // (the kernel's registers for it)
+                return fox_fail(FOX_GPU_ERR_INTERNAL, "fused gemv: %zu bytes of prepared input "
+                                "for %d input dwords per thread", opb, R4);
+            uint8_t *buf = fixed;
+            if (fixed) {
+                if (need > FOX_NOALLOC_SCRATCH)
+                    return fox_fail(FOX_GPU_ERR_ARG, "fused gemv: %zu bytes of prepared input "
+                                    "exceed the fixed scratch (%u)", need, FOX_NOALLOC_SCRATCH);
+            } else {
+                fox_gpu_status st = fox_ws_reserve(ctx, need);
+                if (st) return st;
+                buf = ctx->ws;
+            }
+            float *sc = (float *)(buf + opb);
+            hipLaunchKernelGGL((fused_prep<IN, R4>), dim3((unsigned)a.M), dim3(FWG), 0,
+                               ctx->stream, a.x, a.norm_w, a.nb, a, buf,
+                               (int32_t *)(buf + (L.aux - L.B)), sc);
+            FOX_LAUNCHED("fused_prep");
+            FusedArgs b = a;
+            b.q_in = (const int8_t *)buf;
+            b.scale_in = sc;
+            hipLaunchKernelGGL((gemv_fused<FMT, IN2, EPI, R4, MT2>), dim3((unsigned)grid),
+                               dim3(FWG), lds, ctx->stream, nullptr, nullptr, b.q_in, b.nb, b);
+        } else {
+            hipLaunchKernelGGL((gemv_fused<FMT, IN, EPI, R4, MT2>), dim3((unsigned)grid),
+                               dim3(FWG), lds, ctx->stream, a.x, a.norm_w, a.q_in, a.nb, a);
+        }
+    }
     else if (mt == 1)
         hipLaunchKernelGGL((gemv_fused<FMT, IN, EPI, R4, MT1>), dim3((unsigned)grid), dim3(FWG),
                            lds, ctx->stream, a.x, a.norm_w, a.q_in, a.nb, a);
@@ -1503,34 +1585,37 @@ static fox_gpu_status fused_go_r(fox_gpu_ctx *ctx, FusedArgs a, int n_work)
 // the input registers per thread fit K: 1, 2, 3, 5, 8 or (without the
 // norm weights beside the input) 11 dwords
 template <int FMT, int IN, int EPI>
-static fox_gpu_status fused_go(fox_gpu_ctx *ctx, const FusedArgs &a, int grid)
+static fox_gpu_status fused_go(fox_gpu_ctx *ctx, const FusedArgs &a, int grid, uint8_t *fixed)
 {
     const int per = (a.nb * 64 + FWG - 1) / FWG;
-    if (per <= 1) return fused_go_r<FMT, IN, EPI, 1>(ctx, a, grid);
-    if (per <= 2) return fused_go_r<FMT, IN, EPI, 2>(ctx, a, grid);
-    if (per <= 3) return fused_go_r<FMT, IN, EPI, 3>(ctx, a, grid);
-    if (per <= 5) return fused_go_r<FMT, IN, EPI, 5>(ctx, a, grid);
+    if (per <= 1) return fused_go_r<FMT, IN, EPI, 1>(ctx, a, grid, fixed);
+    if (per <= 2) return fused_go_r<FMT, IN, EPI, 2>(ctx, a, grid, fixed);
+    if (per <= 3) return fused_go_r<FMT, IN, EPI, 3>(ctx, a, grid, fixed);
+    if (per <= 5) return fused_go_r<FMT, IN, EPI, 5>(ctx, a, grid, fixed);
     if constexpr (IN == IN_NORM) {
-        return fused_go_r<FMT, IN, EPI, 8>(ctx, a, grid);   // (fused_check: K <= 16384)
+        return fused_go_r<FMT, IN, EPI, 8>(ctx, a, grid, fixed);   // (fused_check: K <= 16384)
     } else {
-        if (per <= 8) return fused_go_r<FMT, IN, EPI, 8>(ctx, a, grid);
-        return fused_go_r<FMT, IN, EPI, 11>(ctx, a, grid);
+        if (per <= 8) return fused_go_r<FMT, IN, EPI, 8>(ctx, a, grid, fixed);
+        return fused_go_r<FMT, IN, EPI, 11>(ctx, a, grid, fixed);
     }
 }
 
 // (the K-quant kernels take f32 input and write outputs: int8 input with
 // per-block scales and the block-sum requests take the unfused path)
+// (fixed: the caller's scratch for fused_prep's output, or null for the
+// context's workspace)
 template <int IN, int EPI>
-static fox_gpu_status fused_dispatch(fox_gpu_ctx *ctx, int fmt, const FusedArgs &a, int grid)
+static fox_gpu_status fused_dispatch(fox_gpu_ctx *ctx, int fmt, const FusedArgs &a, int grid,
+                                     uint8_t *fixed = nullptr)
 {
     if constexpr (IN != IN_Q && EPI != EPI_SUMS) {
-        if (fmt == FMT_Q4K) return fused_go<FMT_Q4K, IN, EPI>(ctx, a, grid);
-        if (fmt == FMT_Q6K) return fused_go<FMT_Q6K, IN, EPI>(ctx, a, grid);
+        if (fmt == FMT_Q4K) return fused_go<FMT_Q4K, IN, EPI>(ctx, a, grid, fixed);
+        if (fmt == FMT_Q6K) return fused_go<FMT_Q6K, IN, EPI>(ctx, a, grid, fixed);
     }
     if constexpr (IN == IN_NORM && EPI == EPI_ROPE) {
-        if (fmt == FMT_KQMIX) return fused_go<FMT_KQMIX, IN, EPI>(ctx, a, grid);
+        if (fmt == FMT_KQMIX) return fused_go<FMT_KQMIX, IN, EPI>(ctx, a, grid, fixed);
     }
-    return fused_go<FMT_TQ2, IN, EPI>(ctx, a, grid);
+    return fused_go<FMT_TQ2, IN, EPI>(ctx, a, grid, fixed);
 }
 
 static void fused_segments(FusedArgs &a, size_t n, const fox_gpu_tensor *const *ws,
@@ -1556,7 +1641,8 @@ static void fused_segments(FusedArgs &a, size_t n, const fox_gpu_tensor *const *
 fox_gpu_status fox_fused_gemv(fox_gpu_ctx *ctx, size_t n, const fox_gpu_tensor *const *ws,
                               const float *x, size_t x_stride, const int8_t *q,
                               const float *scale, size_t M, float *const *outs,
-                              const size_t *out_strides, unsigned flags, int32_t *sums)
+                              const size_t *out_strides, unsigned flags, int32_t *sums,
+                              uint8_t *fixed_ws)
 {
     int fmt;
     const size_t K = (size_t)ws[0]->ne0;
@@ -1593,7 +1679,7 @@ fox_gpu_status fox_fused_gemv(fox_gpu_ctx *ctx, size_t n, const fox_gpu_tensor *
         return fox_fail(FOX_GPU_ERR_ARG, "fused gemv: missing activations, scale or output");
     if (sums) return fused_dispatch<IN_Q, EPI_SUMS>(ctx, fmt, a, tiles);
     if (q) return fused_dispatch<IN_Q, EPI_STORE>(ctx, fmt, a, tiles);
-    return fused_dispatch<IN_F32, EPI_STORE>(ctx, fmt, a, tiles);
+    return fused_dispatch<IN_F32, EPI_STORE>(ctx, fmt, a, tiles, fixed_ws);
 }
 
 extern "C" fox_gpu_status fox_gpu_gemv_rmsnorm(fox_gpu_ctx *ctx, size_t n,

@@ -738,7 +738,8 @@ static fox_gpu_status gemv_launch_ws(fox_gpu_ctx *ctx, size_t n, const fox_gpu_t
     if (K % 256)
         return fox_fail(FOX_GPU_ERR_ARG,
                         "gemv: %zu columns is not a multiple of the 256-element block", K);
-    st = fox_fused_gemv(ctx, n, ws, x, x_stride, q, scale, M, outs, out_strides, flags, sums);
+    st = fox_fused_gemv(ctx, n, ws, x, x_stride, q, scale, M, outs, out_strides, flags, sums,
+                        fixed_ws);
     if (st != FOX_GPU_ERR_UNSUPPORTED) return st;
     Ws w;
     if (fixed_ws) {

@@ -160,8 +160,11 @@ __device__ __forceinline__ v4i load_b(const uint8_t *p, bool ok)
 
 
 // the one-launch GEMV of fox_fused.hip for the ternary formats;
-// FOX_GPU_ERR_UNSUPPORTED (no error recorded) when the unfused path applies
+// FOX_GPU_ERR_UNSUPPORTED (no error recorded) when the unfused path applies.
+// fixed_ws: scratch of FOX_NOALLOC_SCRATCH bytes for the prepared input of
+// three or more tokens, or null for the context's workspace
 fox_gpu_status fox_fused_gemv(fox_gpu_ctx *ctx, size_t n, const fox_gpu_tensor *const *ws,
                               const float *x, size_t x_stride, const int8_t *q,
                               const float *scale, size_t M, float *const *outs,
-                              const size_t *out_strides, unsigned flags, int32_t *sums);
+                              const size_t *out_strides, unsigned flags, int32_t *sums,
+                              uint8_t *fixed_ws);
