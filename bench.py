@@ -266,6 +266,34 @@ def gemv_only():
     log(f"bench: gemv-only {r['us_per_launch']} us per launch; copied {COPY_BYTES} bytes twice")
 
 
+def gemv_counters():
+    """Fixed launches for instruction counters: the TQ1_0 14336 x 4096 GEMV
+    at one and at eight tokens, and the 27B-class gate/up + SwiGLU (2 x 21504
+    x 5376) at eight tokens, six launches each on the same inputs."""
+    gpu = rf.Gpu(0)
+    rng = np.random.default_rng(3)
+
+    def tensor(N, K):
+        return gpu.tensor(rf.TQ1_0, K, N, synth.tq1_random(rng, N * K // 256).reshape(-1))
+
+    w = tensor(14336, 4096)
+    for M in (1, 8):
+        x = gpu.array(rng.standard_normal((M, 4096)).astype(np.float32))
+        out = gpu.empty((M, 14336), np.float32)
+        for _ in range(6):
+            gpu.gemv(w, x, M, out)
+    gpu.sync()
+    wg, wu = tensor(21504, 5376), tensor(21504, 5376)
+    x = gpu.array(rng.standard_normal((8, 5376)).astype(np.float32))
+    nw = gpu.array(np.ones(5376, np.float32))
+    h = gpu.empty((8, 21504), np.float32)
+    for _ in range(6):
+        gpu.gate_up_silu(wg, wu, x, 8, nw, 1e-6, h)
+    gpu.sync()
+    gpu.close()
+    log("bench: gemv-counters launches done")
+
+
 READ_PROBE_BYTES = 1 << 30
 
 
@@ -583,6 +611,10 @@ def main():
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the roofline GEMV case and a 256 MB device copy (the runs "
                          "that rocprofv3 --pmc counts for the traffic figure)")
+    ap.add_argument("--gemv-counters", action="store_true",
+                    help="only six launches each of the TQ1_0 14336 x 4096 GEMV at 1 and 8 "
+                         "tokens and the 27B-class gate/up + SwiGLU at 8 (for rocprofv3 "
+                         "instruction counters)")
     ap.add_argument("--read-probe", action="store_true",
                     help="only the HBM read-ceiling probes (1 GiB streaming reads with 1-16 "
                          "loads in flight per thread, a device copy, single launches at "
@@ -597,6 +629,9 @@ def main():
 
     if a.gemv_only:
         gemv_only()
+        return
+    if a.gemv_counters:
+        gemv_counters()
         return
     if a.read_probe:
         read_probe()
