@@ -1517,20 +1517,24 @@ static fox_gpu_status fused_go_r(fox_gpu_ctx *ctx, FusedArgs a, int n_work, uint
     // (the K-quants have the one-token kernels only: fused_check)
     constexpr bool MT_OK = FMT == FMT_TQ2;
     const int mt = MT_OK ? (a.M > 2 ? 2 : a.M > 1 ? 1 : 0) : 0;
-    a.n_work = n_work;
-    int cap = (mt == 2 ? 1 : 2) * (ctx->n_cu > 0 ? ctx->n_cu : 1);
-    if (ctx->max_wg > 0 && ctx->max_wg < cap) cap = ctx->max_wg;
-    const int grid = n_work < cap ? n_work : cap;
-    a.n_per = n_work / grid;
-    a.n_rem = n_work - a.n_per * grid;
-    const FusedLds L = fused_lds(FMT, a.nb * 256, a.M, EPI == EPI_SILU ? 2 : 1);
-    const size_t lds = L.total;
     // (the multi-token kernels exist for the ternary formats only; from
     // three tokens on, f32 and normed input is prepared once by fused_prep
     // and the GEMV reads it as IN_B)
     constexpr int MT1 = MT_OK ? 1 : 0, MT2 = MT_OK ? 2 : 0;
     constexpr bool PREP = MT_OK && (IN == IN_F32 || IN == IN_NORM) && EPI != EPI_SUMS;
     constexpr int IN2 = PREP ? IN_B : IN;
+    const FusedLds L = fused_lds(FMT, a.nb * 256, a.M, EPI == EPI_SILU ? 2 : 1);
+    const size_t lds = L.total;
+    // workgroups per compute unit: two, or one from three tokens on unless
+    // the input comes prepared and two fit the LDS and the registers (R4 <= 5:
+    // at most 128 VGPRs)
+    const int per_cu = mt == 2 ? (PREP && R4 <= 5 && lds <= 80 * 1024 ? 2 : 1) : 2;
+    a.n_work = n_work;
+    int cap = per_cu * (ctx->n_cu > 0 ? ctx->n_cu : 1);
+    if (ctx->max_wg > 0 && ctx->max_wg < cap) cap = ctx->max_wg;
+    const int grid = n_work < cap ? n_work : cap;
+    a.n_per = n_work / grid;
+    a.n_rem = n_work - a.n_per * grid;
     const void *k = mt == 2 ? (const void *)gemv_fused<FMT, IN2, EPI, R4, MT2>
                   : mt == 1 ? (const void *)gemv_fused<FMT, IN, EPI, R4, MT1>
                             : (const void *)gemv_fused<FMT, IN, EPI, R4, 0>;
