@@ -1051,7 +1051,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nb = nb_in, M = MT && !KQ ? a.M : 1, K = nb * 256;
-    const int nslab = EPI == EPI_SILU ? 2 : 1;
+    constexpr int nslab = EPI == EPI_SILU ? 2 : 1;
     const FusedLds L = fused_lds(FMT, K, M, nslab);
     uint8_t *B = lds + L.B;
     int32_t *aux = (int32_t *)(lds + L.aux);
@@ -1125,7 +1125,9 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
         int ch, q6;
     };
     auto unit_cur = [&](int ti, int r) -> Cur {
-        const int u = min(wave + FW * r, nunits - 1), sl = u >= nb, b = u - sl * nb;
+        // (one slab: sl = 0 written out, the compiler cannot see that u < nb)
+        const int u = min(wave + FW * r, nunits - 1), sl = nslab == 1 ? 0 : u >= nb;
+        const int b = u - sl * nb;
         int sg, tl;
         item(ti, sl, sg, tl);
         const int ch = chunk_of(sg);
@@ -1372,7 +1374,7 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
         for (int k = 0; k < PF; k++) {
             const int n = n0 + k;
             if (n >= total) break;
-            const int u = wave + FW * r, sl = u >= nb, b = u - sl * nb;
+            const int u = wave + FW * r, sl = nslab == 1 ? 0 : u >= nb, b = u - sl * nb;
             if constexpr (KQ) {
                 // lane (row j, part g): T / 4 terms of its row
                 const RawBlk<FMT> rk = raw[k];
