@@ -1140,9 +1140,13 @@ __device__ __forceinline__ float chain_quads(float acc, const float4 *p, int n)
 #endif
 #define HV_B0 192           // positions of the first exp block (one per producer lane)
 #define HV_EB 768           // positions of a later exp block (four per producer lane)
+#ifndef HV_VB
 #define HV_VB 96            // quads (384 positions) of a value block
+#endif
 #define HV_PS (HV_VB + 1)   // quads per chain in a product buffer (one quad of padding)
+#ifndef HV_VD
 #define HV_VD 4             // value blocks of V in flight per producer lane
+#endif
 #define HV_NP (HV_CH * HV_VB / 192)   // (column, quad) pairs per producer lane and block
 
 __global__ __launch_bounds__(256) void attn_hv(const float *__restrict__ att, size_t att_stride,
@@ -1312,17 +1316,14 @@ __global__ __launch_bounds__(256) void attn_hv(const float *__restrict__ att, si
             }
         }
     };
-    static_assert(HV_VD == 4, "the block loop is unrolled by HV_VD");
+    // (the block loop unrolled by HV_VD: block b + d's V is in vb[d])
     if (producer) {
         for (int b = 0; b <= nvb; b += HV_VD) {
-            produce(b, vb[0]);
-            __syncthreads();
-            produce(b + 1, vb[1]);
-            __syncthreads();
-            produce(b + 2, vb[2]);
-            __syncthreads();
-            produce(b + 3, vb[3]);
-            __syncthreads();
+#pragma unroll
+            for (int d = 0; d < HV_VD; d++) {
+                produce(b + d, vb[d]);
+                __syncthreads();
+            }
         }
     } else {
         for (int b = 0; b <= nvb; b += HV_VD) {
