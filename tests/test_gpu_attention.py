@@ -155,3 +155,18 @@ def test_exact_mode_rejects_contexts_beyond_its_limit(gpu):
     out = gpu.empty(n_head * hd, np.float32)
     with pytest.raises(rf.FoxError):
         gpu.attention(out, dq, kc, vc, n_head, n_kv, hd, 1, dpos, n_ctx, rf.ATTN_EXACT)
+
+
+@pytest.mark.parametrize("hd, n_ctx", [(128, 65536 + 64), (64, 32768 + 32)],
+                         ids=["hd128_65600", "hd64_32800"])
+def test_split_mode_rejects_contexts_beyond_its_limit(gpu, hd, n_ctx):
+    """The merge holds 1024 splits (64 positions each at head_dim 128, 32
+    otherwise): a longer cache is refused before anything is launched."""
+    n_head, n_kv = 4, 1
+    kc = gpu.empty(n_ctx * n_kv * hd, np.float32)
+    vc = gpu.empty((n_ctx + 3) // 4 * 4 * n_kv * hd, np.float32)
+    dq = gpu.empty(n_head * hd, np.float32)
+    dpos = gpu.array(np.array([0], np.uint32))
+    out = gpu.empty(n_head * hd, np.float32)
+    with pytest.raises(rf.FoxError):
+        gpu.attention(out, dq, kc, vc, n_head, n_kv, hd, 1, dpos, n_ctx, rf.ATTN_SPLIT)
