@@ -2,8 +2,10 @@
 fox_gpu_gemv, through the C ABI: bit-identical outputs on two calls in a
 row, the second with a smaller input, for weights whose GEMV uses the
 scratch (Q4_K, Q6_K; TQ1_0 with 8 tokens of 21504 values or 2 of 24576,
-more than the fused path holds) and for one that needs none (fused
-TQ1_0).  The no-alloc calls run first, on a fresh context, and must leave
+more than the fused path holds; fused TQ1_0 from three tokens on, whose
+input is quantised once per launch into the scratch) and for one that needs
+none (fused TQ1_0, one token).  The no-alloc calls run first, on a fresh
+context, and must leave
 its workspace exactly as it was; fox_gpu_gemv runs afterwards on the same
 context for the expected outputs."""
 import numpy as np
@@ -25,6 +27,7 @@ def noalloc(gpu, t, x, M, out, flags=0):
     ("Q4_K", 12, (4096, 14336, 8), (1024, 2048, 3)),
     ("Q6_K", 14, (14336, 4096, 8), (512, 1024, 1)),
     ("TQ1_0", 34, (21504, 5376, 8), (24576, 300, 2)),
+    ("TQ1_0", 34, (4096, 14336, 8), (2560, 640, 3)),
     ("TQ1_0", 34, (2560, 4096, 1), (512, 64, 1)),
 ])
 def test_noalloc_equals_gemv(tname, gtype, first, second):
