@@ -985,6 +985,44 @@ __device__ __forceinline__ void block_mfma(const RawBlk<FMT> &r, const uint8_t *
     for (int q = 0; q < 4; q++) S[q] = acc[q] + corr;
 }
 
+// One token, the MFMA transposed: the activations as the A operand (every
+// A row the token's, read from the same B-operand bytes) and the codes as
+// the B operand (column n = row n of the tile, the lane layout of the codes
+// is the same), so lane l receives row l % 16's integer sum in every
+// element of acc, and lanes 0-15 form one float term each instead of four
+// lanes four terms.  The chunk's codes as load_raw, and the f16 scale of the
+// lane's row l % 16.
+__device__ __forceinline__ RawBlk<FMT_TQ2> load_raw_t1(const uint8_t *__restrict__ ch, int lane)
+{
+    RawBlk<FMT_TQ2> r;
+    const uint4 v = *(const uint4 *)(ch + 16 * lane);
+    r.d0 = v.x;
+    r.d1 = v.y;
+    r.d2 = v.z;
+    r.d3 = v.w;
+    r.dd = make_uint2(*(const unsigned short *)(ch + 1024 + 2 * (lane & 15)), 0u);
+    return r;
+}
+
+__device__ __forceinline__ int block_mfma_t1(const RawBlk<FMT_TQ2> &r,
+                                             const uint8_t *__restrict__ Bb, int lane, int corr)
+{
+    const int g = lane >> 4;
+    v4i bv[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) bv[u] = *(const v4i *)(Bb + (u * 4 + g) * 16);
+    v4i acc = {0, 0, 0, 0};
+    const uint32_t dw[4] = {r.d0, r.d1, r.d2, r.d3};
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const uint32_t d = dw[u];
+        const v4i w = {(int)(d & 0x03030303u), (int)((d >> 2) & 0x03030303u),
+                       (int)((d >> 4) & 0x03030303u), (int)((d >> 6) & 0x03030303u)};
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(bv[u], w, acc, 0, 0, 0);
+    }
+    return acc[0] + corr;
+}
+
 // ------------------------------------------------------------ kernel
 
 // a wave-uniform value pinned in scalar registers: the compiler may no longer
@@ -1154,8 +1192,11 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
         }
         return Cur{c.ti, c.r + 1, c.p + FW * (FMT == FMT_KQMIX ? c.ch : CHUNK), c.ch, c.q6};
     };
+    // one token of a ternary format: the transposed block (block_mfma_t1)
+    constexpr bool T1 = FMT == FMT_TQ2 && MT == 0;
     auto load_unit = [&](const Cur &c) -> RawBlk<FMT> {
         if constexpr (FMT == FMT_KQMIX) return load_raw_mix(c.p, lane, c.q6 != 0);
+        else if constexpr (T1) return load_raw_t1(c.p, lane);
         else return load_raw<FMT>(c.p, lane);
     };
 
@@ -1404,6 +1445,24 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
                 } else {
                     float *tp = terms + (ti & 1) * tstride + (sl * 16 + j) * nbp + b * T;
                     tp[g] = q6k_term(rk, xb, aux + b * 16, as, lane);
+                }
+            } else if constexpr (T1) {
+                const int S = block_mfma_t1(raw[k], B + b * bbytes, lane, aux[b]);
+                const RawBlk<FMT> rk = raw[k];
+                if (n + PF < total) {
+                    raw[k] = load_unit(fc);
+                    if (n + PF + 1 < total) fc = cur_next(fc);
+                }
+                if (lane < 16) {                    // row lane of the tile
+                    if (EPI == EPI_SUMS) {
+                        int sg, tl;
+                        item(ti, sl, sg, tl);
+                        const int nrows = pick4(a.n_rows, sg), grow = tl * 16 + lane;
+                        if (grow < nrows) a.sums[(size_t)grow * nb + b] = S;
+                    } else {
+                        const float d = half_bits_to_float(rk.dd.x & 0xFFFFu);
+                        terms[(ti & 1) * tstride + (sl * 16 + lane) * nbp + b] = d * (float)S;
+                    }
                 }
             } else {
                 const int corr = aux[b * M + (lead ? tok : M - 1)];   // (used by lead lanes)
