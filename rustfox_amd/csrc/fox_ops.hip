@@ -1351,7 +1351,9 @@ __global__ __launch_bounds__(256) void attn_hv(const float *__restrict__ att, si
 //             b - 1; a barrier between blocks.
 #define SM_EB 768           // positions of a softmax exp block (four per producer lane)
 #define MT 4                // tokens per attn_avm workgroup
+#ifndef MV_VB
 #define MV_VB 48            // quads of an attn_avm value block
+#endif
 #define MV_PS (MV_VB + 1)
 
 __global__ __launch_bounds__(256) void attn_sm(float *__restrict__ att, size_t att_stride,
