@@ -2,13 +2,15 @@
 // input stage runs inside the GEMV.
 //
 // Ternary formats (TQ1_0, TQ2_0; TQ1_0 tensors are held as TQ2_0 blocks of
-// the same trits), 1..8 tokens: every workgroup takes the f32 input
-// (optionally RMS-normalised first), quantises it to int8 exactly as
-// src/gemv.c:11-42 does, and lays it out in LDS as the MFMA B operand; the
-// weight loads of its waves are already in flight while it does so.  The
-// per-block integer sums, the block-order float combine and the final
-// activation-scale multiply are those of gemv_blocks (fox_gemv.hip), so
-// results are bit-identical to it and to the reference.
+// the same trits), 1..8 tokens: for one or two tokens every workgroup takes
+// the f32 input (optionally RMS-normalised first), quantises it to int8
+// exactly as src/gemv.c:11-42 does, and lays it out in LDS as the MFMA B
+// operand; the weight loads of its waves are already in flight while it
+// does so.  From three tokens on fused_prep does that once per launch (one
+// workgroup per token) into workspace memory, and every GEMV workgroup copies
+// the result into LDS.  The per-block integer sums, the block-order float
+// combine and the final activation-scale multiply are those of gemv_blocks
+// (fox_gemv.hip), so results are bit-identical to it and to the reference.
 //
 // K-quants (Q4_K, Q6_K), one token: the input is quantised per 256-element
 // block as src/kernels.c:722-754 does, into LDS in element order with its
