@@ -862,25 +862,30 @@ __device__ __forceinline__ RawBlk<FMT> load_raw(const uint8_t *__restrict__ ch, 
     return r;
 }
 
+// The same seven loads for either format, only their addresses chosen by
+// the format: with a branch around the loads, the two paths leave different
+// numbers of loads in flight, and where they join the compiler waits for
+// every load (the blocks in flight included) on each unit.  A Q4_K chunk
+// reads its sc and d slots from the chunk's first bytes (unused).
 __device__ __forceinline__ RawBlk<FMT_KQMIX> load_raw_mix(const uint8_t *__restrict__ ch,
                                                          int lane, bool q6)
 {
+    const int row = lane & 15, h = lane >> 5, s = (lane >> 4) & 1;
+    const int l6 = 128 * row + 64 * h + 16 * s;                 // Q6_K ql (as load_raw)
+    const int q4 = 32 * row + 8 * (lane >> 4);                  // Q4_K qs (as load_raw)
+    const int o0 = q6 ? l6 : q4, o1 = q6 ? l6 + 8 : q4 + 512;
+    const int o2 = q6 ? l6 + 32 : q4 + 1024, o3 = q6 ? l6 + 40 : q4 + 1536;
+    const int oc = 2048 + (q6 ? 64 * row + 32 * h + 16 * s : 16 * row);
+    const int os = q6 ? 3072 + 16 * row + 8 * h : 0;
+    const int od = q6 ? 3328 + 2 * row : 0;
+    const uint2 v0 = *(const uint2 *)(ch + o0), v1 = *(const uint2 *)(ch + o1);
+    const uint2 v2 = *(const uint2 *)(ch + o2), v3 = *(const uint2 *)(ch + o3);
     RawBlk<FMT_KQMIX> m;
-    if (q6) {                                                   // (uniform)
-        const RawBlk<FMT_Q6K> r = load_raw<FMT_Q6K>(ch, lane);
-        m.a = r.l0;
-        m.b = r.l1;
-        m.c = r.h;
-        m.sc = r.sc;
-        m.d = r.d;
-    } else {
-        const RawBlk<FMT_Q4K> r = load_raw<FMT_Q4K>(ch, lane);
-        m.a = make_uint4(r.q0.x, r.q0.y, r.q1.x, r.q1.y);
-        m.b = make_uint4(r.q2.x, r.q2.y, r.q3.x, r.q3.y);
-        m.c = r.hd;
-        m.sc = make_uint2(0u, 0u);
-        m.d = 0u;
-    }
+    m.a = make_uint4(v0.x, v0.y, v1.x, v1.y);
+    m.b = make_uint4(v2.x, v2.y, v3.x, v3.y);
+    m.c = *(const uint4 *)(ch + oc);
+    m.sc = *(const uint2 *)(ch + os);
+    m.d = *(const unsigned short *)(ch + od);
     return m;
 }
 

@@ -229,6 +229,46 @@ def test_8b_kquant_shapes_bit_exact(capped, oracle, tname, gtype, N, K, M, cap):
 
 
 @pytest.mark.parametrize("cap", [0, 5])
+@pytest.mark.parametrize("v_type", [14, 12])
+def test_8b_qkv_rope_kquant_mix_bit_exact(capped, oracle, v_type, cap):
+    """8B-class q/k/v (4096 -> 4096, 1024, 1024; 32/8 heads of 128) for one
+    token at position 4096 of a 4200-row cache: Q4_K q and k with a Q6_K v
+    in one launch whose segments keep their own formats (the Q4_K_M mix),
+    and all three Q4_K.  With the grid capped each workgroup walks tiles of
+    both formats in turn."""
+    K, n_head, n_kv, hd, n_ctx, pos = 4096, 32, 8, 128, 4200, 4096
+    print(f"case qkv_rope 8b v_type={v_type} cap={cap}", flush=True)
+    rng = np.random.default_rng([K, v_type, 17])
+    Wq, Wk = weights(rng, 12, n_head * hd, K), weights(rng, 12, n_kv * hd, K)
+    Wv = weights(rng, v_type, n_kv * hd, K)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    cos_t, sin_t = oracle.rope_tables(n_ctx, hd, 5e5)
+    kvd = n_kv * hd
+    capped.set_max_workgroups(cap)
+    q_out = capped.empty(n_head * hd, np.float32)
+    kc = capped.array(np.zeros(n_ctx * kvd, np.float32))
+    vc = capped.array(np.zeros((n_ctx + 3) // 4 * 4 * kvd, np.float32))
+    capped.qkv_rope(capped.tensor(12, K, n_head * hd, Wq), capped.tensor(12, K, kvd, Wk),
+                    capped.tensor(v_type, K, kvd, Wv), capped.array(x), 1, capped.array(nw), EPS,
+                    q_out, capped.array(cos_t), capped.array(sin_t),
+                    capped.array(np.array([pos], np.uint32)), n_ctx, kc, vc, hd)
+    xb = oracle.rmsnorm(x[0], nw, EPS)
+    half = hd // 2
+    cr, sr = cos_t[pos * half:(pos + 1) * half], sin_t[pos * half:(pos + 1) * half]
+    q = oracle.rope(oracle.gemv(12, xb, Wq, n_head * hd, K, n_threads=THREADS), n_head, hd, cr, sr)
+    k = oracle.rope(oracle.gemv(12, xb, Wk, kvd, K, n_threads=THREADS), n_kv, hd, cr, sr)
+    v = oracle.gemv(v_type, xb, Wv, kvd, K, n_threads=THREADS)
+    assert not first_diff(q_out.numpy(), q), "q: " + first_diff(q_out.numpy(), q)
+    got_k = kc.numpy().reshape(n_ctx, kvd)
+    assert not first_diff(got_k[pos], k), "k: " + first_diff(got_k[pos], k)
+    vq = vc.numpy().reshape(-1, kvd, 4)
+    assert not first_diff(vq[pos // 4, :, pos % 4], v), "v: " + first_diff(vq[pos // 4, :, pos % 4], v)
+    untouched = [p for p in range(n_ctx) if p != pos]
+    assert not got_k[untouched].any()
+
+
+@pytest.mark.parametrize("cap", [0, 5])
 def test_8b_gate_up_silu_bit_exact(capped, oracle, cap):
     """8B-class ffn_gate/ffn_up (Q4_K 4096 -> 14336, 896 tile pairs) with
     RMSNorm and SwiGLU in one launch for one token."""
