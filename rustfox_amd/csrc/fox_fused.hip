@@ -41,7 +41,9 @@
 // fewer in flight per wave leave the input's loads less traffic to queue
 // behind (the 4B layer's four ternary GEMVs 26.3 -> 25.5 us, 14336 x 4096
 // 7.2 -> 6.8 us; two, four and six in flight were slower)
+#ifndef PF_ONE
 #define PF_ONE 3
+#endif
 __host__ __device__ constexpr int pf_of(int R4, int epi2)
 {
     return epi2 * R4 < 4 ? 4 : epi2 * R4 > 8 ? 8 : epi2 * R4;
@@ -1216,8 +1218,16 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
     // one, so that the input's first use waits for the input only)
     RawBlk<FMT> raw[PF];
     Cur fc = unit_cur(0, 0);                               // unit k (then PF) of the wave
+    // PF0 of them before the input stage, the rest after it.  The Q4_K
+    // kernels issue one (two for gate/up pairs) first: with every wave of
+    // every workgroup issuing four, tens of MB of weights go out ahead of
+    // the input's loads (Q4_K 4096 x 4096 6.07 -> 5.52 us, gate/up 2 x 14336
+    // x 4096 19.4 -> 18.1 us, the mixed q/k/v 10.45 -> 10.24 us).  Q6_K and
+    // the ternary kernels issue all of them first (Q6_K 4096 x 14336 14.25
+    // against 14.5 us; ternary 4B-class decode 510 against 498 tok/s).
+    constexpr int PF0 = FMT == FMT_Q4K || FMT == FMT_KQMIX ? (EPI == EPI_SILU ? 2 : 1) : PF;
 #pragma unroll
-    for (int k = 0; k < PF; k++) {
+    for (int k = 0; k < PF0; k++) {
         raw[k] = load_unit(fc);
         if (k + 1 < total) fc = cur_next(fc);              // past the last unit: reload it
     }
@@ -1311,6 +1321,11 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
         if (tid == 0) ascale[0] = s;
     }
     __syncthreads();
+#pragma unroll
+    for (int k = PF0; k < PF; k++) {
+        raw[k] = load_unit(fc);
+        if (k + 1 < total) fc = cur_next(fc);
+    }
 
     // ---- end of item ti0 (with both: of items ti0 and ti0 + 1, the pair):
     // ordered combine, activation scale, epilogue
