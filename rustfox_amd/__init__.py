@@ -54,6 +54,7 @@ def probe_lib() -> C.CDLL:
         vp, sz = C.c_void_p, C.c_size_t
         L.fox_gpu_read_probe.argtypes = [vp, vp, sz, C.c_int, C.c_int, vp]
         L.fox_gpu_empty_probe.argtypes = [vp, C.c_int, vp]
+        L.fox_gpu_sum_probe.argtypes = [vp, vp, C.c_int, C.c_float, vp]
         _probe = L
     return _probe
 
@@ -282,6 +283,13 @@ class Gpu:
     def empty_probe(self, grid: int, sink: DeviceArray):
         """One empty kernel of `grid` workgroups (librustfox_probe.so)."""
         _check(probe_lib().fox_gpu_empty_probe(self.ctx, grid, sink.ptr))
+
+    def sum_probe(self, e: DeviceArray, n: int, acc: float, out: DeviceArray):
+        """The attention kernels' whole-wave in-order softmax sum of n floats
+        from acc into out[0] and the one-add-at-a-time chain's into out[2]
+        (out[1], out[3]: their shader clocks; librustfox_probe.so, for its
+        tests)."""
+        _check(probe_lib().fox_gpu_sum_probe(self.ctx, e.ptr, n, acc, out.ptr))
 
     # -- compute (device arrays in, device arrays out)
     def quantize(self, mode, x: DeviceArray, K, M, x_stride, q: DeviceArray, scale: DeviceArray):

@@ -5,6 +5,7 @@
 #include "fox_gemv_dev.h"
 #include "fox_internal.h"
 #include "fox_math.h"
+#include "fox_sum.h"
 
 #include <cmath>
 #include <utility>
@@ -948,175 +949,21 @@ __global__ __launch_bounds__(256) void attn_qk(const float *__restrict__ q, size
 #define AV_VD 4
 #define AV_LDS_MIN (81 * 1024)
 
-// acc + x_0 + ... + x_{4n-1} over float4 p[0 .. n) of LDS, in order.
-// A dependent add chain is bound by the wave's instruction issue, so its
-// operands must arrive ahead of it: in chain_lds16 two banks of eight quads
-// (v64-v95, v96-v127) alternate, one bank's reads in flight while the other
-// bank's 32 adds run (software pipelining across the loop, which the
-// compiler does not do: compiled from C, each group's reads are issued
-// after the previous group's adds and their latency is paid every time).
-// LDS returns a wave's reads in order, so lgkmcnt(8) after a bank's reads
-// means the bank before is in (earlier outstanding scalar loads only make
-// that wait stricter).  The asm ends with lgkmcnt(0).  q is the lane's own
-// address; ng >= 1 groups of 16 quads.
-__device__ __forceinline__ uint32_t lds_addr(const void *p)
+// The softmax sum over block [j0, j1) of e (j0 a multiple of 4), by the
+// whole wave: blocks that start from position SUM_FAST_FROM on through
+// sum_in_order, earlier ones through the plain chain (there the running sum
+// still climbs a binade every few hundred elements or less, and each climb
+// is an event that costs sum_in_order as much as a run).  e must be
+// readable up to SUM_CHUNK floats past j1.
+#define SUM_FAST_FROM 2048
+__device__ __forceinline__ float softmax_sum_block(float sum, const float *e, int j0, int j1)
 {
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
+    if (j0 >= SUM_FAST_FROM) return sum_in_order(sum, e + j0, j1 - j0);
+    const int nq = (j1 - j0) >> 2;
+    sum = chain_quads(sum, (const float4 *)(e + j0), nq);
+    for (int j = j0 + 4 * nq; j < j1; j++) sum = sum + e[j];
+    return sum;
 }
-
-__device__ __forceinline__ float chain_lds16(float acc, const float4 *q, int ng)
-{
-    uint32_t p = lds_addr(q);
-    int i = ng;
-    asm volatile(
-        "ds_read_b128 v[64:67], %[p] offset:0\n"
-        "ds_read_b128 v[68:71], %[p] offset:16\n"
-        "ds_read_b128 v[72:75], %[p] offset:32\n"
-        "ds_read_b128 v[76:79], %[p] offset:48\n"
-        "ds_read_b128 v[80:83], %[p] offset:64\n"
-        "ds_read_b128 v[84:87], %[p] offset:80\n"
-        "ds_read_b128 v[88:91], %[p] offset:96\n"
-        "ds_read_b128 v[92:95], %[p] offset:112\n"
-        "1:\n"
-        "ds_read_b128 v[96:99], %[p] offset:128\n"
-        "ds_read_b128 v[100:103], %[p] offset:144\n"
-        "ds_read_b128 v[104:107], %[p] offset:160\n"
-        "ds_read_b128 v[108:111], %[p] offset:176\n"
-        "ds_read_b128 v[112:115], %[p] offset:192\n"
-        "ds_read_b128 v[116:119], %[p] offset:208\n"
-        "ds_read_b128 v[120:123], %[p] offset:224\n"
-        "ds_read_b128 v[124:127], %[p] offset:240\n"
-        "s_waitcnt lgkmcnt(8)\n"
-        "v_add_f32 %[acc], %[acc], v64\n"
-        "v_add_f32 %[acc], %[acc], v65\n"
-        "v_add_f32 %[acc], %[acc], v66\n"
-        "v_add_f32 %[acc], %[acc], v67\n"
-        "v_add_f32 %[acc], %[acc], v68\n"
-        "v_add_f32 %[acc], %[acc], v69\n"
-        "v_add_f32 %[acc], %[acc], v70\n"
-        "v_add_f32 %[acc], %[acc], v71\n"
-        "v_add_f32 %[acc], %[acc], v72\n"
-        "v_add_f32 %[acc], %[acc], v73\n"
-        "v_add_f32 %[acc], %[acc], v74\n"
-        "v_add_f32 %[acc], %[acc], v75\n"
-        "v_add_f32 %[acc], %[acc], v76\n"
-        "v_add_f32 %[acc], %[acc], v77\n"
-        "v_add_f32 %[acc], %[acc], v78\n"
-        "v_add_f32 %[acc], %[acc], v79\n"
-        "v_add_f32 %[acc], %[acc], v80\n"
-        "v_add_f32 %[acc], %[acc], v81\n"
-        "v_add_f32 %[acc], %[acc], v82\n"
-        "v_add_f32 %[acc], %[acc], v83\n"
-        "v_add_f32 %[acc], %[acc], v84\n"
-        "v_add_f32 %[acc], %[acc], v85\n"
-        "v_add_f32 %[acc], %[acc], v86\n"
-        "v_add_f32 %[acc], %[acc], v87\n"
-        "v_add_f32 %[acc], %[acc], v88\n"
-        "v_add_f32 %[acc], %[acc], v89\n"
-        "v_add_f32 %[acc], %[acc], v90\n"
-        "v_add_f32 %[acc], %[acc], v91\n"
-        "v_add_f32 %[acc], %[acc], v92\n"
-        "v_add_f32 %[acc], %[acc], v93\n"
-        "v_add_f32 %[acc], %[acc], v94\n"
-        "v_add_f32 %[acc], %[acc], v95\n"
-        "v_add_u32 %[p], 256, %[p]\n"
-        "s_sub_u32 %[i], %[i], 1\n"
-        "s_cmp_eq_u32 %[i], 0\n"
-        "s_cbranch_scc1 2f\n"
-        "ds_read_b128 v[64:67], %[p] offset:0\n"
-        "ds_read_b128 v[68:71], %[p] offset:16\n"
-        "ds_read_b128 v[72:75], %[p] offset:32\n"
-        "ds_read_b128 v[76:79], %[p] offset:48\n"
-        "ds_read_b128 v[80:83], %[p] offset:64\n"
-        "ds_read_b128 v[84:87], %[p] offset:80\n"
-        "ds_read_b128 v[88:91], %[p] offset:96\n"
-        "ds_read_b128 v[92:95], %[p] offset:112\n"
-        "s_waitcnt lgkmcnt(8)\n"
-        "v_add_f32 %[acc], %[acc], v96\n"
-        "v_add_f32 %[acc], %[acc], v97\n"
-        "v_add_f32 %[acc], %[acc], v98\n"
-        "v_add_f32 %[acc], %[acc], v99\n"
-        "v_add_f32 %[acc], %[acc], v100\n"
-        "v_add_f32 %[acc], %[acc], v101\n"
-        "v_add_f32 %[acc], %[acc], v102\n"
-        "v_add_f32 %[acc], %[acc], v103\n"
-        "v_add_f32 %[acc], %[acc], v104\n"
-        "v_add_f32 %[acc], %[acc], v105\n"
-        "v_add_f32 %[acc], %[acc], v106\n"
-        "v_add_f32 %[acc], %[acc], v107\n"
-        "v_add_f32 %[acc], %[acc], v108\n"
-        "v_add_f32 %[acc], %[acc], v109\n"
-        "v_add_f32 %[acc], %[acc], v110\n"
-        "v_add_f32 %[acc], %[acc], v111\n"
-        "v_add_f32 %[acc], %[acc], v112\n"
-        "v_add_f32 %[acc], %[acc], v113\n"
-        "v_add_f32 %[acc], %[acc], v114\n"
-        "v_add_f32 %[acc], %[acc], v115\n"
-        "v_add_f32 %[acc], %[acc], v116\n"
-        "v_add_f32 %[acc], %[acc], v117\n"
-        "v_add_f32 %[acc], %[acc], v118\n"
-        "v_add_f32 %[acc], %[acc], v119\n"
-        "v_add_f32 %[acc], %[acc], v120\n"
-        "v_add_f32 %[acc], %[acc], v121\n"
-        "v_add_f32 %[acc], %[acc], v122\n"
-        "v_add_f32 %[acc], %[acc], v123\n"
-        "v_add_f32 %[acc], %[acc], v124\n"
-        "v_add_f32 %[acc], %[acc], v125\n"
-        "v_add_f32 %[acc], %[acc], v126\n"
-        "v_add_f32 %[acc], %[acc], v127\n"
-        "s_branch 1b\n"
-        "2:\n"
-        "s_waitcnt lgkmcnt(0)\n"
-        "v_add_f32 %[acc], %[acc], v96\n"
-        "v_add_f32 %[acc], %[acc], v97\n"
-        "v_add_f32 %[acc], %[acc], v98\n"
-        "v_add_f32 %[acc], %[acc], v99\n"
-        "v_add_f32 %[acc], %[acc], v100\n"
-        "v_add_f32 %[acc], %[acc], v101\n"
-        "v_add_f32 %[acc], %[acc], v102\n"
-        "v_add_f32 %[acc], %[acc], v103\n"
-        "v_add_f32 %[acc], %[acc], v104\n"
-        "v_add_f32 %[acc], %[acc], v105\n"
-        "v_add_f32 %[acc], %[acc], v106\n"
-        "v_add_f32 %[acc], %[acc], v107\n"
-        "v_add_f32 %[acc], %[acc], v108\n"
-        "v_add_f32 %[acc], %[acc], v109\n"
-        "v_add_f32 %[acc], %[acc], v110\n"
-        "v_add_f32 %[acc], %[acc], v111\n"
-        "v_add_f32 %[acc], %[acc], v112\n"
-        "v_add_f32 %[acc], %[acc], v113\n"
-        "v_add_f32 %[acc], %[acc], v114\n"
-        "v_add_f32 %[acc], %[acc], v115\n"
-        "v_add_f32 %[acc], %[acc], v116\n"
-        "v_add_f32 %[acc], %[acc], v117\n"
-        "v_add_f32 %[acc], %[acc], v118\n"
-        "v_add_f32 %[acc], %[acc], v119\n"
-        "v_add_f32 %[acc], %[acc], v120\n"
-        "v_add_f32 %[acc], %[acc], v121\n"
-        "v_add_f32 %[acc], %[acc], v122\n"
-        "v_add_f32 %[acc], %[acc], v123\n"
-        "v_add_f32 %[acc], %[acc], v124\n"
-        "v_add_f32 %[acc], %[acc], v125\n"
-        "v_add_f32 %[acc], %[acc], v126\n"
-        "v_add_f32 %[acc], %[acc], v127\n"
-        : [acc] "+&v"(acc), [p] "+&v"(p), [i] "+&s"(i)
-        :
-        : "v64", "v65", "v66", "v67", "v68", "v69", "v70", "v71", "v72", "v73", "v74", "v75", "v76", "v77", "v78", "v79", "v80", "v81", "v82", "v83", "v84", "v85", "v86", "v87", "v88", "v89", "v90", "v91", "v92", "v93", "v94", "v95", "v96", "v97", "v98", "v99", "v100", "v101", "v102", "v103", "v104", "v105", "v106", "v107", "v108", "v109", "v110", "v111", "v112", "v113", "v114", "v115", "v116", "v117", "v118", "v119", "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127", "scc", "memory");
-    return acc;
-}
-
-// acc + x_0 + ... + x_{4n-1} over float4 p[0 .. n) of LDS, in order
-__device__ __forceinline__ float chain_quads(float acc, const float4 *p, int n)
-{
-    const int ng = n >> 4;
-    if (ng > 0) acc = chain_lds16(acc, p, ng);
-    for (int i = ng << 4; i < n; i++) {
-        const float4 v = p[i];
-        acc = acc + v.x; acc = acc + v.y; acc = acc + v.z; acc = acc + v.w;
-    }
-    return acc;
-}
-
 
 // ---- one token: softmax and values of one query head per workgroup, for
 // HV_CH of its columns (256 threads).  Wave 0 runs the chains: lane 0 the
@@ -1260,13 +1107,7 @@ __global__ __launch_bounds__(256) void attn_hv(const float *__restrict__ att, si
     } else {
         __syncthreads();
         for (int k = 1; k <= neb2; k++) {
-            if (lane == 0 && k <= neb) {
-                // block k - 1 in position order (its start is a multiple of 4)
-                const int j0 = blk0(k - 1), j1 = min(upto, blk0(k));
-                const int nqk = (j1 - j0) >> 2;
-                sum = chain_quads(sum, (const float4 *)(e + j0), nqk);
-                for (int j = j0 + 4 * nqk; j < j1; j++) sum = sum + e[j];
-            }
+            if (k <= neb) sum = softmax_sum_block(sum, e, blk0(k - 1), min(upto, blk0(k)));
             __syncthreads();
         }
     }
@@ -1411,12 +1252,8 @@ __global__ __launch_bounds__(256) void attn_sm(float *__restrict__ att, size_t a
         }
     } else {
         for (int k = 0; k <= neb; k++) {
-            if (k > 0 && lane == 0) {
-                const int j0 = (k - 1) * SM_EB, j1 = min(upto, j0 + SM_EB);
-                const int nqk = (j1 - j0) >> 2;
-                sum = chain_quads(sum, (const float4 *)(e + j0), nqk);
-                for (int j = j0 + 4 * nqk; j < j1; j++) sum = sum + e[j];
-            }
+            if (k > 0)
+                sum = softmax_sum_block(sum, e, (k - 1) * SM_EB, min(upto, k * SM_EB));
             __syncthreads();
         }
     }
@@ -1679,7 +1516,9 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
         const int gp = gqa == 1 ? 1 : gqa == 2 ? 2 : gqa <= 4 ? 4 : 8;
         const size_t dcm = AV_CH / gp;
         {
-            const size_t sm_lds = att_stride * sizeof(float);
+            // (SUM_CHUNK floats past the weights: softmax_sum_block reads
+            // whole chunks of SUM_CHUNK)
+            const size_t sm_lds = (att_stride + SUM_CHUNK) * sizeof(float);
             if (sm_lds > 64 * 1024) {
                 hipError_t e = hipFuncSetAttribute((const void *)attn_sm,
                                                    hipFuncAttributeMaxDynamicSharedMemorySize,

@@ -9,12 +9,19 @@
 //       compared with;
 //   fox_gpu_empty_probe(ctx, grid, sink)
 //       one empty kernel of `grid` workgroups: timed back to back, or
-//       captured in a graph, the fixed cost of a launch or of a graph node.
+//       captured in a graph, the fixed cost of a launch or of a graph node;
+//   fox_gpu_sum_probe(ctx, e, n, acc, out)
+//       the attention kernels' whole-wave softmax sum (sum_in_order) of n
+//       floats from acc, by one wave, into out[0], and the one-add-at-a-time
+//       chain's into out[2] (out[1], out[3]: their shader clocks): its tests
+//       compare them with the sum in order on inputs chosen to hit its
+//       events.
 //
 // sink (device memory, 4 bytes) is written only if the folded data hit a
 // fixed constant, so the loads cannot be dropped and nothing is written in
 // practice.
 #include "fox_internal.h"
+#include "fox_sum.h"
 
 // ------------------------------------------------------- read probe
 
@@ -82,5 +89,45 @@ extern "C" fox_gpu_status fox_gpu_read_probe(fox_gpu_ctx *ctx, const void *src, 
     default: return fox_fail(FOX_GPU_ERR_ARG, "read_probe: 1, 2, 4, 8 or 16 loads in flight");
     }
     FOX_LAUNCHED("read_probe");
+    return FOX_GPU_OK;
+}
+
+// ------------------------------------------------------- in-order sum
+
+#define SUM_PROBE_MAX 16384
+
+// out[0] the whole-wave sum, out[1] its shader clocks; out[2] the
+// one-add-at-a-time chain (chain_quads, then single adds), out[3] its clocks
+__global__ __launch_bounds__(64) void sum_probe_k(const float *__restrict__ e, int n, float acc,
+                                                  float *__restrict__ out)
+{
+    extern __shared__ float se[];                      // n + SUM_CHUNK floats
+    for (int i = threadIdx.x; i < n + SUM_CHUNK; i += 64) se[i] = i < n ? e[i] : 0.0f;
+    __syncthreads();
+    const uint64_t t0 = __builtin_amdgcn_s_memtime();
+    const float s = sum_in_order(acc, se, n);
+    const uint64_t t1 = __builtin_amdgcn_s_memtime();
+    float c = chain_quads(acc, (const float4 *)se, n >> 2);
+    for (int i = n & ~3; i < n; i++) c = c + se[i];
+    const uint64_t t2 = __builtin_amdgcn_s_memtime();
+    if (threadIdx.x == 0) {
+        out[0] = s;
+        out[1] = (float)(t1 - t0);
+        out[2] = c;
+        out[3] = (float)(t2 - t1);
+    }
+}
+
+extern "C" fox_gpu_status fox_gpu_sum_probe(fox_gpu_ctx *ctx, const float *e, int n, float acc,
+                                            float *out)
+{
+    if (!ctx || !out || n < 0 || n > SUM_PROBE_MAX || (n > 0 && !e))
+        return fox_fail(FOX_GPU_ERR_ARG, "sum_probe: bad argument (n at most %d)", SUM_PROBE_MAX);
+    const size_t lds = ((size_t)n + SUM_CHUNK) * sizeof(float);
+    hipError_t err = hipFuncSetAttribute((const void *)sum_probe_k,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (err != hipSuccess) return fox_hip_fail(err, "sum_probe: LDS size");
+    hipLaunchKernelGGL(sum_probe_k, dim3(1), dim3(64), lds, ctx->stream, e, n, acc, out);
+    FOX_LAUNCHED("sum_probe");
     return FOX_GPU_OK;
 }

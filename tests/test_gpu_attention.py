@@ -170,3 +170,63 @@ def test_split_mode_rejects_contexts_beyond_its_limit(gpu, hd, n_ctx):
     out = gpu.empty(n_head * hd, np.float32)
     with pytest.raises(rf.FoxError):
         gpu.attention(out, dq, kc, vc, n_head, n_kv, hd, 1, dpos, n_ctx, rf.ATTN_SPLIT)
+
+
+def _in_order(acc, e):
+    """acc + e_0 + e_1 + ..., one float32 add at a time (src/ops.c:31-33)."""
+    s = np.float32(acc)
+    with np.errstate(all="ignore"):
+        for x in e:
+            s = np.float32(s + x)
+    return s
+
+
+def _sum_inputs():
+    rng = np.random.default_rng(31)
+    cases = []
+    for n in (1, 3, 255, 256, 257, 2061, 8192):
+        for sig in (0.5, 2.0, 8.0):
+            s = rng.normal(0, sig, n)
+            cases.append((f"softmax n={n} sigma={sig}", 0.0,
+                          np.exp(s - s.max()).astype(np.float32)))
+    n = 2000
+    k, m = rng.integers(1, 8, n), rng.integers(8, 22, n)
+    cases.append(("exact ties of small multiples of powers of two", 0.0,
+                  np.ldexp(k.astype(np.float32), -m).astype(np.float32)))
+    cases.append(("ties at a sum past 2^24", 2.0 ** 24, rng.integers(0, 8, n).astype(np.float32)))
+    cases.append(("ties of halves past 2^23", 2.0 ** 23,
+                  (rng.integers(0, 8, n) * 0.5).astype(np.float32)))
+    cases.append(("thirty decades", 0.0, (10.0 ** rng.uniform(-30, 0, n)).astype(np.float32)))
+    z = rng.uniform(0, 1, n).astype(np.float32)
+    z[rng.random(n) < 0.3] = 0.0
+    z[rng.random(n) < 0.1] = np.float32(1e-40)
+    cases.append(("zeros and subnormals", 0.0, z))
+    cases.append(("a subnormal start", 1e-40, rng.uniform(0, 1e-38, n).astype(np.float32)))
+    cases.append(("negative elements", 0.25, rng.uniform(-1, 1, 600).astype(np.float32)))
+    x = rng.uniform(0, 1, 600).astype(np.float32)
+    x[300] = np.nan
+    cases.append(("a NaN element", 0.0, x))
+    x = rng.uniform(0, 1, 600).astype(np.float32)
+    x[200] = np.inf
+    cases.append(("an infinite element", 0.0, x))
+    cases.append(("no elements", 0.5, np.zeros(0, np.float32)))
+    return cases
+
+
+@pytest.mark.parametrize("name,acc,e", _sum_inputs(), ids=lambda v: v if isinstance(v, str) else "")
+def test_softmax_sum_in_order_is_the_chain(gpu, name, acc, e):
+    """The attention kernels' softmax sum, formed a wave at a time from
+    integer sums over runs that stay in one binade, equals the one add at a
+    time chain bit for bit, on inputs that hit its events: binade
+    crossings, exact ties (whose rounding depends on the sum so far), zeros,
+    subnormals, negative, infinite and NaN elements."""
+    print(f"case sum_in_order {name} n={e.size}", flush=True)
+    de = gpu.array(e if e.size else np.zeros(1, np.float32))
+    out = gpu.array(np.full(4, np.nan, np.float32))
+    gpu.sum_probe(de, int(e.size), float(acc), out)
+    gpu.sync()
+    res, want = out.numpy(), _in_order(acc, e)
+    for got, what in ((res[0], "whole-wave sum"), (res[2], "chain")):
+        assert (np.isnan(got) and np.isnan(want)) or got.view(np.uint32) == want.view(np.uint32), \
+            f"{name}, {what}: got {got!r} want {want!r}"
+    print(f"  clocks: whole-wave {res[1]:.0f}, chain {res[3]:.0f}", flush=True)
