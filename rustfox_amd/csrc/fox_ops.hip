@@ -954,8 +954,12 @@ __global__ __launch_bounds__(256) void attn_qk(const float *__restrict__ q, size
 // sum_in_order, earlier ones through the plain chain (there the running sum
 // still climbs a binade every few hundred elements or less, and each climb
 // is an event that costs sum_in_order as much as a run).  e must be
-// readable up to SUM_CHUNK floats past j1.
-#define SUM_FAST_FROM 2048
+// readable up to SUM_CHUNK floats past j1.  (4B-class decode at 2048+ rows:
+// from 512 on, the blocks from 960, 517.3 tok/s; from 1024 on 515.5; from
+// 2048 on 512.3-514.2; no block 508.8.)
+#ifndef SUM_FAST_FROM
+#define SUM_FAST_FROM 512
+#endif
 __device__ __forceinline__ float softmax_sum_block(float sum, const float *e, int j0, int j1)
 {
     if (j0 >= SUM_FAST_FROM) return sum_in_order(sum, e + j0, j1 - j0);
