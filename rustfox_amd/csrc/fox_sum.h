@@ -1,6 +1,9 @@
-// fox_sum.h -- the softmax sum of src/ops.c:31-33 (sum += e_j for j = 0, 1,
-// ..., each add rounded to nearest even, in that order) formed by a whole
-// wave a run of elements at a time instead of one dependent add per element.
+// fox_sum.h -- float sums in a fixed order for the attention kernels: the
+// one-add-at-a-time chain fed from LDS (chain_lds16, chain_quads: the value
+// sums of src/ops.c and forward.c, one chain per lane) and the softmax sum
+// of src/ops.c:31-33 (sum += e_j for j = 0, 1, ..., each add rounded to
+// nearest even, in that order) formed by a whole wave a run of elements at a
+// time (sum_in_order), with the chain's result.
 #pragma once
 
 #include "fox_gemv_dev.h"
