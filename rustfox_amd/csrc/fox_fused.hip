@@ -690,6 +690,19 @@ __device__ __forceinline__ void quantise_kq(const FusedArgs &a, int K, int8_t *x
         mb[r] = m;
     }
     wave_max_n<R4MAX>(mb);
+    // the blocks' 127/amax and amax/127 in one double division: lane r
+    // (r < R4MAX) divides for block r, lane 32 + r the other way (the same
+    // operations as per block; a double division is a long dependent
+    // sequence at the FP64 rate, two per block otherwise)
+    static_assert(R4MAX <= 32, "one lane per block in each half of the wave");
+    float dq;
+    {
+        uint32_t amr = mb[0];
+#pragma unroll
+        for (int r = 1; r < R4MAX; r++) amr = (lane & 31) == r ? mb[r] : amr;
+        const float amx = __uint_as_float(amr);
+        dq = lane < 32 ? fox_div(127.0f, amx) : fox_div(amx, 127.0f);
+    }
     int part[R4MAX];
 #pragma unroll
     for (int r = 0; r < R4MAX; r++) {
@@ -699,11 +712,10 @@ __device__ __forceinline__ void quantise_kq(const FusedArgs &a, int K, int8_t *x
         float s = 0.0f;
         if (am >= 0x03800000u && am < 0x7f800000u) {           // (uniform)
             // amax in [2^-120, inf), no NaN: quant_fast applies
-            const float amax = __uint_as_float(am);
-            const float inv = fox_div(127.0f, amax);
+            const float inv = read_lane(dq, r);                 // 127 / amax
             q = pack_lo_bytes(quant_fast(xv[r].x, inv), quant_fast(xv[r].y, inv),
                               quant_fast(xv[r].z, inv), quant_fast(xv[r].w, inv));
-            s = fox_div(amax, 127.0f);
+            s = read_lane(dq, 32 + r);                          // amax / 127
         } else if (am != 0u) {
             // NaN, inf or a tiny amax: the float amax of the non-NaN values
             // (src/kernels.c:734-737), then the exact quantiser
