@@ -975,11 +975,11 @@ __device__ __forceinline__ float softmax_sum_block(float sum, const float *e, in
 // c0 .. c0 + HV_CH - 1; waves 1-3 produce their operands.
 //   1. the head's maximum from its tile maxima (wave 0);
 //   2. exp blocks (HV_B0 positions, then HV_EB): waves 1-3 write e_j =
-//      expf(s_j - max) of block k to LDS while lane 0 of wave 0 adds block
-//      k - 1 to the sum; a barrier between blocks;
+//      expf(s_j - max) of block k to LDS while wave 0 adds block k - 1 to
+//      the sum (softmax_sum_block); a barrier between blocks;
 //   3. 1 / sum;
-//   4. value blocks of HV_VB quads: waves 1-3 multiply block b's V quads
-//      (loaded HV_VD blocks ahead) by a_j = e_j * (1/sum) into one of two
+//   4. value blocks of VB quads: waves 1-3 multiply block b's V quads
+//      (loaded VD blocks ahead) by a_j = e_j * (1/sum) into one of two
 //      product buffers while wave 0 adds block b - 1's products to its
 //      chains; a barrier between blocks.
 // The exps of a head are computed by the hd / HV_CH workgroups of its column
@@ -991,15 +991,20 @@ __device__ __forceinline__ float softmax_sum_block(float sum, const float *e, in
 #endif
 #define HV_B0 192           // positions of the first exp block (one per producer lane)
 #define HV_EB 768           // positions of a later exp block (four per producer lane)
-#ifndef HV_VB
-#define HV_VB 96            // quads (384 positions) of a value block
-#endif
-#define HV_PS (HV_VB + 1)   // quads per chain in a product buffer (one quad of padding)
-#ifndef HV_VD
-#define HV_VD 4             // value blocks of V in flight per producer lane
-#endif
-#define HV_NP (HV_CH * HV_VB / 192)   // (column, quad) pairs per producer lane and block
+// value blocks (VB quads, VD of them of V in flight per producer lane, a
+// product buffer of VB + 1 quads per chain: one quad of padding): 192 quads
+// (768 positions, half the chain restarts of 96) where a head's weights
+// leave room for their product buffers, else 96
+#define HV_VB_BIG 192
+#define HV_VD_BIG 2
+#define HV_VB 96
+#define HV_VD 4
+__host__ __device__ constexpr size_t hv_lds_bytes(int estr, int vb)
+{
+    return (size_t)estr * 4 + 2 * HV_CH * (size_t)(vb + 1) * 16;
+}
 
+template <int VB, int VD>
 __global__ __launch_bounds__(256) void attn_hv(const float *__restrict__ att, size_t att_stride,
                                                const float *__restrict__ tmax, int n_tiles,
                                                const float *__restrict__ vc, int n_head,
@@ -1008,12 +1013,14 @@ __global__ __launch_bounds__(256) void attn_hv(const float *__restrict__ att, si
                                                float *__restrict__ out, int estr)
 {
     typedef float f4v __attribute__((ext_vector_type(4)));
+    constexpr int PS = VB + 1;                     // quads per chain in a product buffer
+    constexpr int NP = HV_CH * VB / 192;           // (column, quad) pairs per producer lane and block
     constexpr int QS = 192 / HV_CH;                // quad step of a producer lane's pairs
-    static_assert(192 % HV_CH == 0 && HV_NP * 192 == HV_CH * HV_VB && HV_VB % QS == 0,
+    static_assert(192 % HV_CH == 0 && NP * 192 == HV_CH * VB && VB % QS == 0,
                   "producer lane L takes column L % HV_CH and quads L / HV_CH + QS k");
     extern __shared__ float4 hv_lds[];
     float *e = (float *)hv_lds;                    // [estr]: e_j
-    float4 *prod = hv_lds + estr / 4;              // [2][HV_CH][HV_PS]
+    float4 *prod = hv_lds + estr / 4;              // [2][HV_CH][PS]
     __shared__ float mx_s, inv_s;
     __shared__ uint64_t tab[32];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
@@ -1060,20 +1067,20 @@ __global__ __launch_bounds__(256) void attn_hv(const float *__restrict__ att, si
     if (tid < 32) tab[tid] = fox_exp2_tab[tid];
     __syncthreads();
 
-    // V of value blocks 0 .. HV_VD - 1: producer lane L, pair k is column
+    // V of value blocks 0 .. VD - 1: producer lane L, pair k is column
     // c0 + L % HV_CH, quad L / HV_CH + QS k of the block (a wave's loads of
     // one k are runs of HV_CH consecutive quads).  Requested after exp blocks 0
     // and 1's scores, so that those do not wait for them; block b's V is in
-    // vb[b % HV_VD], the block loop unrolled by HV_VD (every index known at
+    // vb[b % VD], the block loop unrolled by VD (every index known at
     // compile time, each slot reloaded in place).
     const f4v *v4 = (const f4v *)vc;
     const int vcol = kvh * hd + min(c0 + L % HV_CH, hd - 1);
-    const int nvb = (nq_all + HV_VB - 1) / HV_VB;
-    f4v vb[HV_VD][HV_NP];
+    const int nvb = (nq_all + VB - 1) / VB;
+    f4v vb[VD][NP];
     auto v_load = [&](int b, f4v *dst) {
 #pragma unroll
-        for (int k = 0; k < HV_NP; k++) {
-            const int jq = min(b * HV_VB + L / HV_CH + QS * k, nq_all - 1);
+        for (int k = 0; k < NP; k++) {
+            const int jq = min(b * VB + L / HV_CH + QS * k, nq_all - 1);
             dst[k] = v4[(size_t)jq * kvd + vcol];
         }
     };
@@ -1097,7 +1104,7 @@ __global__ __launch_bounds__(256) void attn_hv(const float *__restrict__ att, si
         float sb[4];
         s_load(min(1, neb - 1), sb);
 #pragma unroll
-        for (int d = 0; d < HV_VD; d++) v_load(min(d, nvb - 1), vb[d]);
+        for (int d = 0; d < VD; d++) v_load(min(d, nvb - 1), vb[d]);
         exps(0, sc);
         __syncthreads();
         for (int k = 1; k <= neb2; k += 2) {
@@ -1131,27 +1138,27 @@ __global__ __launch_bounds__(256) void attn_hv(const float *__restrict__ att, si
     // read of e, so reads interleaved with stores would pay the LDS latency
     // once per pair)
     auto produce = [&](int b, f4v *vs) {
-        float4 *P = prod + (b & 1) * HV_CH * HV_PS + (L % HV_CH) * HV_PS;
-        float4 a[HV_NP];
+        float4 *P = prod + (b & 1) * HV_CH * PS + (L % HV_CH) * PS;
+        float4 a[NP];
 #pragma unroll
-        for (int k = 0; k < HV_NP; k++)
-            a[k] = ((const float4 *)e)[min(b * HV_VB + L / HV_CH + QS * k, nq_all - 1)];
+        for (int k = 0; k < NP; k++)
+            a[k] = ((const float4 *)e)[min(b * VB + L / HV_CH + QS * k, nq_all - 1)];
 #pragma unroll
-        for (int k = 0; k < HV_NP; k++) {
+        for (int k = 0; k < NP; k++) {
             const float4 ak = make_float4(a[k].x * iv, a[k].y * iv, a[k].z * iv, a[k].w * iv);
             const f4v v = vs[k];
             float4 p;
             p.x = ak.x * v.x; p.y = ak.y * v.y; p.z = ak.z * v.z; p.w = ak.w * v.w;
             P[L / HV_CH + QS * k] = p;
         }
-        v_load(min(b + HV_VD, nvb - 1), vs);
+        v_load(min(b + VD, nvb - 1), vs);
     };
     // the chains over block b - 1: whole quads below upto, then the ragged
     // quad's first rem products
     auto chains = [&](int b) {
         if (b > 0 && b <= nvb && lane < HV_CH) {
-            const float4 *P = prod + ((b - 1) & 1) * HV_CH * HV_PS + lane * HV_PS;
-            const int nfull = min(HV_VB, nq - (b - 1) * HV_VB);
+            const float4 *P = prod + ((b - 1) & 1) * HV_CH * PS + lane * PS;
+            const int nfull = min(VB, nq - (b - 1) * VB);
             acc = chain_quads(acc, P, nfull);
             if (b == nvb && rem) {
                 const float4 v = P[nfull];
@@ -1161,19 +1168,19 @@ __global__ __launch_bounds__(256) void attn_hv(const float *__restrict__ att, si
             }
         }
     };
-    // (the block loop unrolled by HV_VD: block b + d's V is in vb[d])
+    // (the block loop unrolled by VD: block b + d's V is in vb[d])
     if (producer) {
-        for (int b = 0; b <= nvb; b += HV_VD) {
+        for (int b = 0; b <= nvb; b += VD) {
 #pragma unroll
-            for (int d = 0; d < HV_VD; d++) {
+            for (int d = 0; d < VD; d++) {
                 produce(b + d, vb[d]);
                 __syncthreads();
             }
         }
     } else {
-        for (int b = 0; b <= nvb; b += HV_VD) {
+        for (int b = 0; b <= nvb; b += VD) {
 #pragma unroll
-            for (int d = 0; d < HV_VD; d++) {
+            for (int d = 0; d < VD; d++) {
                 chains(b + d);
                 __syncthreads();
             }
@@ -1500,18 +1507,23 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
         // (at least AV_LDS_MIN: more than half of a compute unit's LDS, so
         // that no two workgroups share a compute unit, whose chain waves
         // would share SIMD 0's instruction issue)
-        size_t hv_lds = (size_t)estr * 4 + 2 * HV_CH * HV_PS * 16;
+        const bool big = hv_lds_bytes(estr, HV_VB_BIG) <= ATT_LDS_MAX;
+        size_t hv_lds = hv_lds_bytes(estr, big ? HV_VB_BIG : HV_VB);
         if (hv_lds < AV_LDS_MIN) hv_lds = AV_LDS_MIN;
         if (M == 1 && hv_lds <= ATT_LDS_MAX) {
-            hipError_t e = hipFuncSetAttribute((const void *)attn_hv,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+            const void *hv = big ? (const void *)attn_hv<HV_VB_BIG, HV_VD_BIG>
+                                 : (const void *)attn_hv<HV_VB, HV_VD>;
+            hipError_t e = hipFuncSetAttribute(hv, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                (int)hv_lds);
             if (e != hipSuccess) return fox_hip_fail(e, "attention: LDS size");
             const size_t ncg = (head_dim + HV_CH - 1) / HV_CH;
             const size_t nwg = (n_head_kv * ncg + 7) / 8 * 8 * gqa;
-            hipLaunchKernelGGL(attn_hv, dim3((unsigned)nwg), dim3(256), hv_lds, ctx->stream, att,
-                               att_stride, tmax, n_tiles, v_cache, (int)n_head, ikv, ihd, pos,
-                               ictx, out, estr);
+            const int in_head = (int)n_head;
+            void *args[] = {(void *)&att, (void *)&att_stride, (void *)&tmax, (void *)&n_tiles,
+                            (void *)&v_cache, (void *)&in_head, (void *)&ikv, (void *)&ihd,
+                            (void *)&pos, (void *)&ictx, (void *)&out, (void *)&estr};
+            e = hipLaunchKernel(hv, dim3((unsigned)nwg), dim3(256), args, hv_lds, ctx->stream);
+            if (e != hipSuccess) return fox_hip_fail(e, "attention softmax+values");
             FOX_LAUNCHED("attention softmax+values");
             return FOX_GPU_OK;
         }
