@@ -222,7 +222,10 @@ __device__ __forceinline__ float f4_at(const float __attribute__((ext_vector_typ
 // add, as the one-element-at-a-time chain does; the runs resume after it.  A
 // sum that is zero, subnormal, infinite or NaN, and a chunk holding a
 // negative element, take the elements one at a time the same way.  The
-// result is that chain's, bit for bit.
+// result is that chain's, bit for bit, but for a NaN sum, which is returned
+// as soon as it appears (any NaN: whatever is added after it, the chain's
+// sum stays NaN, and the softmax then uses 1 in place of 1/sum, so which NaN
+// it is never shows).
 //
 // A run of 256 elements costs about 700-900 clocks (the lane scan and the
 // scalar hand-overs are one dependent sequence), an event as much: against
@@ -253,6 +256,7 @@ __device__ __forceinline__ float sum_in_order(float acc, const float *e, int n)
                                               v[3] < 0.0f) != 0;
             fresh = false;
         }
+        if (acc != acc) return acc;                         // NaN stays NaN (see below)
         if (neg || !(acc >= 0x1p-126f && acc < INFINITY)) {
             const int d = i - c0;
             acc = uniform_f(acc + read_lane(f4_at(v, d & 3), d >> 2));
