@@ -86,6 +86,10 @@ CASES = [  # n_head, n_kv, hd, n_ctx, pos, M
     (6, 6, 40, 120, 100, 1),       # one token, hd 40: a head's last column group partly past its end
     (4, 2, 4, 32, 20, 1),          # one token, hd 4
     (12, 4, 64, 3000, 2500, 1),    # one token, gqa 3 past several exp blocks
+    # one token on either side of the largest context that takes 768-position
+    # value blocks (16,000 weights beside their product buffers)
+    (8, 2, 128, 16000, 15999, 1),  # 768-position value blocks, 21 of them, the last ragged
+    (8, 2, 128, 16032, 16031, 1),  # 384-position value blocks
     # one token past the fused kernel's LDS: the two-launch path
     (16, 2, 128, 16400, 16399, 1), # gqa 8, 257 score tiles
     (8, 8, 64, 20000, 19990, 1),   # gqa 1, 20000 positions
