@@ -1138,6 +1138,9 @@ __global__ __launch_bounds__(256) void attn_hv(const float *__restrict__ att, si
     // read of e, so reads interleaved with stores would pay the LDS latency
     // once per pair)
     auto produce = [&](int b, f4v *vs) {
+        // (the unrolled loop runs to the next multiple of VD past nvb: those
+        // steps are only their barriers)
+        if (b > nvb) return;                               // (uniform)
         float4 *P = prod + (b & 1) * HV_CH * PS + (L % HV_CH) * PS;
         float4 a[NP];
 #pragma unroll
@@ -1409,10 +1412,14 @@ __global__ __launch_bounds__(256) void attn_avm(const float *__restrict__ att, s
         stage(0, sl[0]);
         load(min(AV_VD, nvb - 1), sl[0]);
         __syncthreads();
+        // (steps past nvb, to the next multiple of AV_VD: only their
+        // barriers)
         auto step = [&](int b, Slot &s1) __attribute__((always_inline)) {
-            stage(b + 1, s1);
-            load(min(b + 1 + AV_VD, nvb - 1), s1);
-            products(b);
+            if (b <= nvb) {                                // (uniform)
+                stage(b + 1, s1);
+                load(min(b + 1 + AV_VD, nvb - 1), s1);
+                products(b);
+            }
             __syncthreads();
         };
         for (int b = 0; b <= nvb; b += AV_VD) {
@@ -1507,7 +1514,11 @@ extern "C" fox_gpu_status fox_gpu_attention(fox_gpu_ctx *ctx, float *out, size_t
         // (at least AV_LDS_MIN: more than half of a compute unit's LDS, so
         // that no two workgroups share a compute unit, whose chain waves
         // would share SIMD 0's instruction issue)
+#ifndef HV_BIG_OFF
         const bool big = hv_lds_bytes(estr, HV_VB_BIG) <= ATT_LDS_MAX;
+#else
+        const bool big = false;
+#endif
         size_t hv_lds = hv_lds_bytes(estr, big ? HV_VB_BIG : HV_VB);
         if (hv_lds < AV_LDS_MIN) hv_lds = AV_LDS_MIN;
         if (M == 1 && hv_lds <= ATT_LDS_MAX) {
