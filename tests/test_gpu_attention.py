@@ -200,6 +200,14 @@ def _sum_inputs():
     cases.append(("ties at a sum past 2^24", 2.0 ** 24, rng.integers(0, 8, n).astype(np.float32)))
     cases.append(("ties of halves past 2^23", 2.0 ** 23,
                   (rng.integers(0, 8, n) * 0.5).astype(np.float32)))
+    # e/u = k 2^(23-m) against a sum near 1: for m = 24..26 most elements
+    # are ties, several to a lane, whose rounding follows the running parity
+    for bits in (1, 6, 12):
+        k, m = rng.integers(1, 2 ** bits, 3000), rng.integers(18, 27, 3000)
+        cases.append((f"dense ties at the sum's own scale, {bits}-bit multiples", 1.0,
+                      np.ldexp(k.astype(np.float32), -m).astype(np.float32)))
+    s = rng.normal(0, 6.0, 3000)
+    cases.append(("a peaked softmax after a sum of 1", 1.0, np.exp(s - s.max()).astype(np.float32)))
     cases.append(("thirty decades", 0.0, (10.0 ** rng.uniform(-30, 0, n)).astype(np.float32)))
     z = rng.uniform(0, 1, n).astype(np.float32)
     z[rng.random(n) < 0.3] = 0.0
