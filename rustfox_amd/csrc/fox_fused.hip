@@ -1223,23 +1223,23 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
 
     // ---- loads in the order they are used (they complete in order): the
     // input of token 0 (above), the first weight blocks, the epilogue's
-    // operands
-    constexpr int PF = FMT == FMT_KQMIX ? 3 : KQ ? 4 : MT ? pf_of(R4, EPI == EPI_SILU ? 2 : 1)
-                                                         : PF_ONE;
-    // (every wave issues PF block loads, past its last unit re-reading that
-    // one, so that the input's first use waits for the input only)
+    // operands.
+    //
+    // The K-quant kernels keep one block per wave in flight: with more,
+    // tens of MB of weights queue ahead of the input's and the epilogue's
+    // loads (8B-class Q4_K/Q6_K decode at 4096 rows, alternating runs: 376.6
+    // tok/s with one, 353.3 with four (three for the mixed q/k/v), 369.5 with
+    // one but three for the mix, 366.6 with two, 322.3 with six).  The
+    // ternary kernels keep three (two or four: 4B-class decode 501.8 and
+    // 503.9 against 510.1 tok/s).
+    constexpr int PF = KQ ? 1 : MT ? pf_of(R4, EPI == EPI_SILU ? 2 : 1) : PF_ONE;
+    // (every wave issues PF block loads before the input stage, past its
+    // last unit re-reading that one, so that the input's first use waits for
+    // the input only)
     RawBlk<FMT> raw[PF];
     Cur fc = unit_cur(0, 0);                               // unit k (then PF) of the wave
-    // PF0 of them before the input stage, the rest after it.  The Q4_K
-    // kernels issue one (two for gate/up pairs) first: with every wave of
-    // every workgroup issuing four, tens of MB of weights go out ahead of
-    // the input's loads (Q4_K 4096 x 4096 6.07 -> 5.52 us, gate/up 2 x 14336
-    // x 4096 19.4 -> 18.1 us, the mixed q/k/v 10.45 -> 10.24 us).  Q6_K and
-    // the ternary kernels issue all of them first (Q6_K 4096 x 14336 14.25
-    // against 14.5 us; ternary 4B-class decode 510 against 498 tok/s).
-    constexpr int PF0 = FMT == FMT_Q4K || FMT == FMT_KQMIX ? (EPI == EPI_SILU ? 2 : 1) : PF;
 #pragma unroll
-    for (int k = 0; k < PF0; k++) {
+    for (int k = 0; k < PF; k++) {
         raw[k] = load_unit(fc);
         if (k + 1 < total) fc = cur_next(fc);              // past the last unit: reload it
     }
@@ -1333,11 +1333,6 @@ __global__ __launch_bounds__(FWG) void gemv_fused(const float *x_in, const float
         if (tid == 0) ascale[0] = s;
     }
     __syncthreads();
-#pragma unroll
-    for (int k = PF0; k < PF; k++) {
-        raw[k] = load_unit(fc);
-        if (k + 1 < total) fc = cur_next(fc);
-    }
 
     // ---- end of item ti0 (with both: of items ti0 and ti0 + 1, the pair):
     // ordered combine, activation scale, epilogue
